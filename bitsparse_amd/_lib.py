@@ -1,0 +1,172 @@
+"""ctypes binding of libbitsparse_hip.so (the C ABI in include/bitsparse_hip.h).
+
+The shared library is built in-tree next to this file by
+``bitsparse_amd.build.build_library()`` (or ``__graft_entry__.build()``).
+There is no fallback: if the library is missing or a call fails, an
+exception is raised.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+LIB_NAME = "libbitsparse_hip.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+ABI_VERSION = 1
+
+BS_OK = 0
+BS_ERR_INVALID = 1
+BS_ERR_HIP = 2
+
+# dtype codes == reference codec ids (lib_sparse/bitsparse.py:20-30)
+DT_BF16, DT_E4M3FN, DT_E5M2 = 0, 1, 2
+
+_i64 = ctypes.c_int64
+_u32 = ctypes.c_uint32
+_int = ctypes.c_int
+_vp = ctypes.c_void_p
+_f32 = ctypes.c_float
+
+# name -> argtypes (restype int unless listed in _RESTYPES)
+_SIGNATURES = {
+    "bs_last_error": [],
+    "bs_abi_version": [],
+    "bs_compress_workspace_bytes": [_i64, _i64],
+    "bs_compress": [_vp, _int, _i64, _i64, _int, _vp, _u32, _vp, _vp, _vp, _vp, _vp, _i64, _vp,
+                    _int, _vp, _vp, _int, _vp, _vp, _i64, _u32, _vp],
+    "bs_tile_pack": [_vp, _int, _i64, _i64, _vp, _vp, _vp],
+    "bs_prefix_from_counts": [_vp, _i64, _vp, _vp],
+    "bs_compact_vals": [_vp, _int, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _vp, _vp],
+    "bs_decompress": [_vp, _int, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _int, _f32,
+                      _vp, _vp],
+    "bs_relu_grad": [_vp, _i64, _i64, _vp, _vp],
+    "bs_relu2_grad": [_vp, _i64, _i64, _vp, _int, _i64, _vp, _vp, _vp, _f32, _vp, _vp],
+    "bs_amax": [_vp, _i64, _vp, _i64, _u32, _vp],
+    "bs_quantize_e4m3fn": [_vp, _i64, _vp, _vp, _vp, _i64, _u32, _vp],
+    "bs_workspace_amax_slot": [_vp, _i64],
+    "bs_workspace_fallback_counter": [_vp, _i64],
+}
+_RESTYPES = {
+    "bs_last_error": ctypes.c_char_p,
+    "bs_compress_workspace_bytes": _i64,
+    "bs_workspace_amax_slot": _vp,
+    "bs_workspace_fallback_counter": _vp,
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+class BitsparseHipError(RuntimeError):
+    """A libbitsparse_hip.so call returned an error status."""
+
+
+def exported_symbols() -> list[str]:
+    return list(_SIGNATURES)
+
+
+def load() -> ctypes.CDLL:
+    """Load the in-tree library (raises if it was not built)."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(
+                f"{LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; "
+                f"g.build()'` (hipcc --offload-arch=gfx950)")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, args in _SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = _RESTYPES.get(name, ctypes.c_int)
+        v = L.bs_abi_version()
+        if v != ABI_VERSION:
+            raise ImportError(f"{LIB_PATH} has ABI {v}, expected {ABI_VERSION}; rebuild it")
+        _lib = L
+        return L
+
+
+def check(rc: int, what: str) -> None:
+    if rc != BS_OK:
+        msg = load().bs_last_error().decode(errors="replace")
+        if rc == BS_ERR_INVALID:
+            raise ValueError(f"{what}: {msg}")
+        raise BitsparseHipError(f"{what} failed ({rc}): {msg}")
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def require_device(t: torch.Tensor, what: str) -> None:
+    """The HIP kernels run on ROCm device tensors only; there is no CPU path."""
+    if not t.is_cuda:
+        raise RuntimeError(
+            f"{what}: bitsparse_amd runs on a ROCm GPU; got a tensor on {t.device}")
+
+
+# ---------------------------------------------------------------------------
+# per-(device, stream) workspace for the single-pass compress and the amax
+# ---------------------------------------------------------------------------
+_EPOCH_LIMIT = (1 << 30) - 1
+
+
+class Workspace:
+    """Zero-initialised device scratch with an epoch counter.
+
+    Each compress / amax call takes a fresh epoch; status words written under
+    older epochs are ignored by the kernels, so the buffer never needs
+    clearing between calls.  When the epoch counter wraps the buffer is
+    zeroed again.
+    """
+
+    def __init__(self, device: torch.device):
+        self.device = device
+        self.buf = torch.zeros(0, dtype=torch.uint8, device=device)
+        self.epoch = 0
+
+    def ensure(self, nbytes: int) -> None:
+        if self.buf.numel() < nbytes:
+            # grow geometrically; a new buffer starts zeroed, epochs restart
+            size = max(nbytes, 2 * self.buf.numel(), 1 << 16)
+            self.buf = torch.zeros(size, dtype=torch.uint8, device=self.device)
+            self.epoch = 0
+
+    def next_epoch(self) -> int:
+        self.epoch += 1
+        if self.epoch > _EPOCH_LIMIT:
+            self.buf.zero_()
+            self.epoch = 1
+        return self.epoch
+
+    @property
+    def nbytes(self) -> int:
+        return self.buf.numel()
+
+    def amax_slot_ptr(self) -> int:
+        return load().bs_workspace_amax_slot(self.buf.data_ptr(), self.nbytes)
+
+    def fallback_count(self) -> int:
+        """Look-back fallbacks recorded in this workspace (synchronises)."""
+        return int(self.buf[8:12].view(torch.int32).item())
+
+
+_workspaces: dict[tuple[int, int], Workspace] = {}
+
+
+def workspace_for(device: torch.device) -> Workspace:
+    dev = device.index if device.index is not None else torch.cuda.current_device()
+    key = (dev, torch.cuda.current_stream(device).cuda_stream)
+    ws = _workspaces.get(key)
+    if ws is None:
+        ws = Workspace(torch.device("cuda", dev))
+        _workspaces[key] = ws
+    return ws

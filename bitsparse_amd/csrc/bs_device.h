@@ -1,0 +1,176 @@
+// Device-side building blocks shared by the BitSparse HIP kernels (gfx950).
+//
+// Format facts used everywhere (reference lib_sparse/src/triton_kernels.py:1-17,
+// lib_sparse/bitsparse.py:132-139):
+//   * 64x64 tiles, tile id t = tm * grid_n + tn;
+//   * a "chunk" is 8 consecutive elements of one tile row; chunk b of a tile
+//     (0..511) covers tile-flat indices 8b..8b+7, i.e. row b/8, columns
+//     8*(b%8)..+7, and owns exactly bitmask byte t*512 + b (LSB = first column);
+//   * "positive" is the strict IEEE compare x > 0 evaluated on bit patterns.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace bs {
+
+enum : int { DT_BF16 = 0, DT_E4M3FN = 1, DT_E5M2 = 2 };
+
+constexpr int kTile = 64;
+constexpr int kTileNumel = 4096;
+constexpr int kTileBytes = 512;     // bitmask bytes per tile
+constexpr int kChunksPerTile = 512; // 8-element chunks per tile
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------
+// positive tests on raw bits: x > 0 <=> bits in (0, +Inf]
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t pos_bf16(uint32_t b) { return (b - 1u) < 0x7f80u; }
+__device__ __forceinline__ uint32_t pos_e4m3(uint32_t b) { return ((b - 1u) & 0xffu) < 0x7eu; }
+__device__ __forceinline__ uint32_t pos_e5m2(uint32_t b) { return ((b - 1u) & 0xffu) < 0x7cu; }
+
+template <int DT>
+__device__ __forceinline__ uint32_t pos8(uint32_t b)
+{
+    return DT == DT_E4M3FN ? pos_e4m3(b) : pos_e5m2(b);
+}
+
+// ---------------------------------------------------------------------------
+// scalar conversions
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+// fp32 -> bf16 bits, round to nearest even, NaN kept quiet.
+__device__ __forceinline__ uint32_t f32_to_bf16(float f)
+{
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+// e4m3fn bits -> fp32 (exact). 0x7f / 0xff are NaN.
+__device__ __forceinline__ float e4m3_to_f32(uint32_t b)
+{
+    uint32_t e = (b >> 3) & 15u, m = b & 7u;
+    float v;
+    if (e == 0u) v = (float)m * 0.001953125f;                       // m * 2^-9
+    else v = __uint_as_float(((e + 120u) << 23) | (m << 20));        // 1.m * 2^(e-7)
+    if (e == 15u && m == 7u) v = __uint_as_float(0x7fc00000u);
+    return (b & 0x80u) ? -v : v;
+}
+
+// e5m2 bits -> fp32 (exact): the top byte of an IEEE half.
+__device__ __forceinline__ float e5m2_to_f32(uint32_t b)
+{
+    uint32_t e = (b >> 2) & 31u, m = b & 3u;
+    float v;
+    if (e == 0u) v = (float)m * 1.52587890625e-05f;                  // m * 2^-16
+    else if (e == 31u) v = __uint_as_float(m ? 0x7fc00000u : 0x7f800000u);
+    else v = __uint_as_float(((e + 112u) << 23) | (m << 21));
+    return (b & 0x80u) ? -v : v;
+}
+
+template <int DT>
+__device__ __forceinline__ float fp8_to_f32(uint32_t b)
+{
+    return DT == DT_E4M3FN ? e4m3_to_f32(b) : e5m2_to_f32(b);
+}
+
+// fp32 -> e4m3fn bits, round to nearest even, no saturation: |x| > 464,
+// Inf and NaN give NaN (0x7f | sign); 464 itself rounds to 448.
+__device__ __forceinline__ uint32_t f32_to_e4m3(float f)
+{
+    uint32_t u = __float_as_uint(f);
+    uint32_t sign = (u >> 24) & 0x80u;
+    uint32_t a = u & 0x7fffffffu;
+    if (a > 0x43e80000u) return sign | 0x7fu;                        // > 464.0, Inf, NaN
+    if (a < 0x3c800000u) {                                           // < 2^-6: subnormal grid 2^-9
+        float t = __builtin_rintf(__uint_as_float(a) * 512.0f);
+        return sign | (uint32_t)t;
+    }
+    a += 0x7ffffu + ((a >> 20) & 1u);                                // RNE at mantissa bit 20
+    return sign | ((((a >> 23) - 120u) << 3) | ((a >> 20) & 7u));
+}
+
+// ---------------------------------------------------------------------------
+// 8-element chunks: bitmask byte of 8 values held in registers
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t mask_bf16x8(const uint4 v)
+{
+    return pos_bf16(v.x & 0xffffu) | (pos_bf16(v.x >> 16) << 1) |
+           (pos_bf16(v.y & 0xffffu) << 2) | (pos_bf16(v.y >> 16) << 3) |
+           (pos_bf16(v.z & 0xffffu) << 4) | (pos_bf16(v.z >> 16) << 5) |
+           (pos_bf16(v.w & 0xffffu) << 6) | (pos_bf16(v.w >> 16) << 7);
+}
+
+template <int DT>
+__device__ __forceinline__ uint32_t mask_fp8x8(const uint2 v)
+{
+    uint32_t m = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) m |= pos8<DT>((v.x >> (8 * i)) & 0xffu) << i;
+#pragma unroll
+    for (int i = 0; i < 4; i++) m |= pos8<DT>((v.y >> (8 * i)) & 0xffu) << (4 + i);
+    return m;
+}
+
+__device__ __forceinline__ uint32_t get16(const uint4 v, int e)
+{
+    uint32_t w = e < 2 ? v.x : e < 4 ? v.y : e < 6 ? v.z : v.w;
+    return (e & 1) ? (w >> 16) : (w & 0xffffu);
+}
+
+__device__ __forceinline__ uint32_t get8(const uint2 v, int e)
+{
+    return ((e < 4 ? v.x : v.y) >> (8 * (e & 3))) & 0xffu;
+}
+
+// ---------------------------------------------------------------------------
+// wave / lane helpers (wave64)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }
+
+// number of set bits of `m` in lanes strictly below this lane
+__device__ __forceinline__ uint32_t popc_below(uint64_t m)
+{
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                     __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+// Exclusive prefix and total over the wave of a per-lane count in [0, 15],
+// built from four ballots (one per bit of the count).
+__device__ __forceinline__ void wave_scan_count(uint32_t c, uint32_t& excl, uint32_t& total)
+{
+    uint64_t b0 = __ballot(c & 1u), b1 = __ballot(c & 2u);
+    uint64_t b2 = __ballot(c & 4u), b3 = __ballot(c & 8u);
+    excl = popc_below(b0) + 2u * popc_below(b1) + 4u * popc_below(b2) + 8u * popc_below(b3);
+    total = (uint32_t)(__popcll(b0) + 2 * __popcll(b1) + 4 * __popcll(b2) + 8 * __popcll(b3));
+}
+
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = max(v, (uint32_t)__shfl_xor(v, o, 64));
+    return v;
+}
+
+// relaxed device-scope atomics: the status words carry their whole payload,
+// so no fence is needed around them
+__device__ __forceinline__ uint64_t ld_relaxed(const uint64_t* p)
+{
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_relaxed(uint64_t* p, uint64_t v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace bs

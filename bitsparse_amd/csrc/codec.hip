@@ -1,0 +1,1146 @@
+// BitSparse codec kernels for gfx950: single-pass compress, count/compact
+// passes of the standalone path, decompress, and the two gradient kernels.
+//
+// Work decomposition shared by all kernels: a workgroup of 256 threads
+// (4 wave64) owns a "unit" of U consecutive tiles.  For each tile, thread i
+// handles chunks i and i+256 (rows i/8 and 32+i/8), so one wave instruction
+// covers 8 full tile rows = 8 x 128 contiguous bytes of bf16.
+#include "bs_device.h"
+#include "bs_host.h"
+
+namespace bs {
+
+template <int B> struct Raw;
+template <> struct Raw<2> { using T = uint4; };   // 8 x bf16
+template <> struct Raw<1> { using T = uint2; };   // 8 x fp8
+
+constexpr int kThreads = 256;
+
+// Elements of one chunk as raw bits.
+template <int B>
+__device__ __forceinline__ uint32_t elem(const typename Raw<B>::T& v, int e)
+{
+    if constexpr (B == 2) return get16(v, e);
+    else return get8(v, e);
+}
+
+template <int B>
+__device__ __forceinline__ void set_elem(typename Raw<B>::T& v, int e, uint32_t x)
+{
+    if constexpr (B == 2) {
+        uint32_t* w = e < 2 ? &v.x : e < 4 ? &v.y : e < 6 ? &v.z : &v.w;
+        int sh = (e & 1) * 16;
+        *w = (*w & ~(0xffffu << sh)) | ((x & 0xffffu) << sh);
+    } else {
+        uint32_t* w = e < 4 ? &v.x : &v.y;
+        int sh = (e & 3) * 8;
+        *w = (*w & ~(0xffu << sh)) | ((x & 0xffu) << sh);
+    }
+}
+
+// Load chunk (row, col0..col0+7) of a row-major matrix, zeros outside [M, N].
+// VEC: N % 8 == 0 and 8-element alignment, so a chunk is all in or all out.
+template <int B, bool VEC>
+__device__ __forceinline__ typename Raw<B>::T load_chunk(const uint8_t* base, int64_t M, int64_t N,
+                                                         int64_t row, int64_t col0)
+{
+    using T = typename Raw<B>::T;
+    T v = {};
+    if (row >= M || col0 >= N) return v;
+    const uint8_t* p = base + (row * N + col0) * B;
+    if constexpr (VEC) {
+        v = *reinterpret_cast<const T*>(p);
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            if (col0 + e < N) {
+                uint32_t x = (B == 2) ? (uint32_t)reinterpret_cast<const uint16_t*>(p)[e]
+                                      : (uint32_t)p[e];
+                set_elem<B>(v, e, x);
+            }
+        }
+    }
+    return v;
+}
+
+template <int B, bool VEC>
+__device__ __forceinline__ void store_chunk(uint8_t* base, int64_t M, int64_t N, int64_t row,
+                                            int64_t col0, const typename Raw<B>::T& v)
+{
+    using T = typename Raw<B>::T;
+    if (row >= M || col0 >= N) return;
+    uint8_t* p = base + (row * N + col0) * B;
+    if constexpr (VEC) {
+        *reinterpret_cast<T*>(p) = v;
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            if (col0 + e < N) {
+                if (B == 2) reinterpret_cast<uint16_t*>(p)[e] = (uint16_t)elem<B>(v, e);
+                else p[e] = (uint8_t)elem<B>(v, e);
+            }
+        }
+    }
+}
+
+// fp32 scale of the e4m3fn quantizer from the amax slot: max(amax/448, 1e-9);
+// a NaN amax gives a NaN scale (torch's clamp keeps NaN).
+__device__ __forceinline__ float scale_from_slot(const uint64_t* slot, uint32_t epoch)
+{
+    uint64_t s = *slot;
+    float amax = ((uint32_t)(s >> 32) == epoch) ? bf16_to_f32((uint32_t)s & 0xffffu) : 0.0f;
+    float sc = amax / 448.0f;
+    return (sc < 1e-9f) ? 1e-9f : sc;
+}
+
+__device__ __forceinline__ uint2 quant_chunk(const uint4 v, float scale)
+{
+    uint2 q = {0u, 0u};
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        uint32_t b = f32_to_e4m3(bf16_to_f32(get16(v, e)) / scale);
+        if (e < 4) q.x |= b << (8 * e);
+        else q.y |= b << (8 * (e - 4));
+    }
+    return q;
+}
+
+// Chunk geometry inside tile t of a [*, N] matrix.
+__device__ __forceinline__ void chunk_pos(uint32_t t, uint32_t grid_n, int b, int64_t& row,
+                                          int64_t& col0)
+{
+    uint32_t tm = t / grid_n, tn = t - tm * grid_n;
+    row = (int64_t)tm * 64 + (b >> 3);
+    col0 = (int64_t)tn * 64 + (b & 7) * 8;
+}
+
+// ===========================================================================
+// compress
+// ===========================================================================
+enum { MODE_FUSED = 0, MODE_COUNT = 1, MODE_VALS = 2 };
+
+struct CompressArgs {
+    const uint8_t* dense;
+    int64_t M, N;
+    uint32_t grid_n;
+    uint32_t T;
+    const uint64_t* amax_slot;
+    uint32_t amax_epoch;
+    float* scale_out;
+    uint8_t* dense_q_out;
+    uint8_t* bitmask;           // written (FUSED/COUNT) or read (VALS)
+    uint32_t* prefix;           // written (FUSED/COUNT) or read (VALS)
+    uint8_t* vals;
+    int64_t vals_capacity;
+    const int64_t* offset_in;
+    int32_t align8;
+    int64_t* offset_out;
+    int64_t* start_out;
+    uint32_t tile0;             // first tile of unit 0 (VALS: also the prefix base)
+    uint32_t tend;              // one past the last tile of this launch
+    uint64_t* status;
+    uint32_t epoch;
+    int32_t* err;
+    uint32_t* fallbacks;
+};
+
+// status word: [63:34] epoch, [33:32] flag (1 aggregate, 2 inclusive), [31:0] value
+constexpr uint64_t kFlagAgg = 1, kFlagInc = 2;
+__device__ __forceinline__ uint64_t pack_status(uint32_t epoch, uint64_t flag, uint32_t v)
+{
+    return ((uint64_t)epoch << 34) | (flag << 32) | v;
+}
+
+// 20 us at the 100 MHz s_memrealtime clock: waiting longer than this for a
+// predecessor makes the waiter count that predecessor's tiles itself.
+constexpr uint64_t kLookbackPatienceTicks = 2000;
+
+template <int IN_T, bool QUANT>
+struct CompressTraits {
+    static constexpr int INB = IN_T == DT_BF16 ? 2 : 1;
+    static constexpr int OUTB = (IN_T == DT_BF16 && !QUANT) ? 2 : 1;
+    static constexpr int MASK_T = QUANT ? DT_E4M3FN : IN_T;
+};
+
+// Positive-bit byte of a loaded chunk (after quantisation when QUANT).
+template <int IN_T, bool QUANT>
+__device__ __forceinline__ uint32_t chunk_mask(const typename Raw<CompressTraits<IN_T, QUANT>::INB>::T& d,
+                                               typename Raw<CompressTraits<IN_T, QUANT>::OUTB>::T& o,
+                                               float scale)
+{
+    if constexpr (QUANT) {
+        o = quant_chunk(d, scale);
+        return mask_fp8x8<DT_E4M3FN>(o);
+    } else if constexpr (IN_T == DT_BF16) {
+        o = d;
+        return mask_bf16x8(d);
+    } else {
+        o = d;
+        return mask_fp8x8<IN_T>(d);
+    }
+}
+
+// Nonzero count of compress unit q, computed straight from the dense input
+// by one wave (look-back fallback).
+template <int IN_T, bool QUANT, bool VEC, int U>
+__device__ uint32_t unit_count_direct(const CompressArgs& a, uint32_t q, float scale, int lane)
+{
+    using TR = CompressTraits<IN_T, QUANT>;
+    uint32_t t0 = a.tile0 + q * U;
+    uint32_t nt = min((uint32_t)U, a.tend - t0);
+    uint32_t c = 0;
+    for (uint32_t k = lane; k < nt * kChunksPerTile; k += kWave) {
+        int64_t row, col0;
+        chunk_pos(t0 + (k >> 9), a.grid_n, (int)(k & 511), row, col0);
+        auto d = load_chunk<TR::INB, VEC>(a.dense, a.M, a.N, row, col0);
+        typename Raw<TR::OUTB>::T o;
+        c += __popc(chunk_mask<IN_T, QUANT>(d, o, scale));
+    }
+    return wave_sum_u32(c);
+}
+
+template <int IN_T, bool QUANT, bool VEC, int MODE, int U>
+__global__ __launch_bounds__(kThreads) void compress_kernel(CompressArgs a)
+{
+    using TR = CompressTraits<IN_T, QUANT>;
+    constexpr int INB = TR::INB, OUTB = TR::OUTB;
+    constexpr int EPS = 16 / OUTB;   // elements per 16-byte store slot
+    using RawIn = typename Raw<INB>::T;
+    using RawOut = typename Raw<OUTB>::T;
+
+    __shared__ uint32_t s_wtot[U][2][4];
+    __shared__ uint32_t s_excl;
+    __shared__ __align__(16) uint8_t s_vals[MODE == MODE_COUNT ? 16 : U * kTileNumel * OUTB + 16];
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const uint32_t u = blockIdx.x;
+    const uint32_t t0 = a.tile0 + u * U;
+    const int ntiles = (int)min((uint32_t)U, a.tend - t0);
+
+    float scale = 1.0f;
+    if constexpr (QUANT) scale = scale_from_slot(a.amax_slot, a.amax_epoch);
+
+    // ---- load every chunk of the unit first (all loads in flight together)
+    RawIn d[U][2];
+#pragma unroll
+    for (int j = 0; j < U; j++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            d[j][h] = RawIn{};
+            if (j < ntiles) {
+                int64_t row, col0;
+                chunk_pos(t0 + j, a.grid_n, h * 256 + tid, row, col0);
+                d[j][h] = load_chunk<INB, VEC>(a.dense, a.M, a.N, row, col0);
+            }
+        }
+    uint32_t vm[U][2];
+    if constexpr (MODE == MODE_VALS) {
+#pragma unroll
+        for (int j = 0; j < U; j++)
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+                vm[j][h] = j < ntiles ? a.bitmask[(size_t)(t0 + j) * kTileBytes + h * 256 + tid] : 0u;
+    }
+
+    // ---- masks, optional quantised copy, bitmask bytes
+    RawOut o[U][2];
+    uint32_t m[U][2];
+#pragma unroll
+    for (int j = 0; j < U; j++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            m[j][h] = chunk_mask<IN_T, QUANT>(d[j][h], o[j][h], scale);
+            if (j < ntiles) {
+                if constexpr (QUANT) {
+                    if (a.dense_q_out != nullptr) {
+                        int64_t row, col0;
+                        chunk_pos(t0 + j, a.grid_n, h * 256 + tid, row, col0);
+                        store_chunk<1, VEC>(a.dense_q_out, a.M, a.N, row, col0, o[j][h]);
+                    }
+                }
+                if constexpr (MODE != MODE_VALS)
+                    a.bitmask[(size_t)(t0 + j) * kTileBytes + h * 256 + tid] = (uint8_t)m[j][h];
+            }
+            if constexpr (MODE == MODE_VALS) m[j][h] = vm[j][h];
+        }
+
+    // ---- in-tile ranks: ballot scan per wave, wave totals through LDS
+    uint32_t ex[U][2];
+#pragma unroll
+    for (int j = 0; j < U; j++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            uint32_t tot;
+            wave_scan_count(__popc(m[j][h]), ex[j][h], tot);
+            if (lane == 0) s_wtot[j][h][wave] = tot;
+        }
+    __syncthreads();
+
+    uint32_t lr[U][2];   // unit-local rank of each chunk's first set element
+    uint32_t tile_base[U];
+    uint32_t unit_total = 0;
+#pragma unroll
+    for (int j = 0; j < U; j++) {
+        tile_base[j] = unit_total;
+        uint32_t h0 = 0, h0w = 0, h1w = 0, h1 = 0;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            uint32_t a0 = s_wtot[j][0][w], a1 = s_wtot[j][1][w];
+            h0 += a0;
+            h1 += a1;
+            if (w < wave) { h0w += a0; h1w += a1; }
+        }
+        lr[j][0] = unit_total + h0w + ex[j][0];
+        lr[j][1] = unit_total + h0 + h1w + ex[j][1];
+        unit_total += h0 + h1;
+    }
+
+    // ---- unit start in the value stream
+    uint32_t excl;
+    if constexpr (MODE == MODE_VALS) {
+        excl = a.prefix[t0] - a.prefix[a.tile0];
+    } else {
+        if (wave == 0) {
+            if (u == 0) {
+                excl = 0;
+                if (lane == 0) st_relaxed(&a.status[0], pack_status(a.epoch, kFlagInc, unit_total));
+            } else {
+                if (lane == 0) st_relaxed(&a.status[u], pack_status(a.epoch, kFlagAgg, unit_total));
+                // decoupled look-back over a 64-unit window per step
+                excl = 0;
+                int64_t pos = (int64_t)u - 1;
+                uint64_t since = wall_clock64();
+                while (true) {
+                    int64_t q = pos - lane;
+                    uint64_t s = q >= 0 ? ld_relaxed(&a.status[q]) : pack_status(a.epoch, kFlagInc, 0);
+                    uint32_t val = (uint32_t)s;
+                    uint32_t flag = (uint32_t)(s >> 32) & 3u;
+                    bool valid = (uint32_t)(s >> 34) == a.epoch && flag != 0u;
+                    bool inc = valid && flag == (uint32_t)kFlagInc;
+                    uint64_t notv = ~__ballot(valid);
+                    uint64_t incm = __ballot(inc);
+                    int fi = notv ? __ffsll((unsigned long long)notv) - 1 : 64;
+                    int fc = incm ? __ffsll((unsigned long long)incm) - 1 : 64;
+                    if (fc < fi) {
+                        excl += wave_sum_u32(lane <= fc ? val : 0u);
+                        break;
+                    }
+                    if (fi > 0) {
+                        excl += wave_sum_u32(lane < fi ? val : 0u);
+                        pos -= fi;
+                        since = wall_clock64();
+                        continue;
+                    }
+                    if (wall_clock64() - since > kLookbackPatienceTicks) {
+                        excl += unit_count_direct<IN_T, QUANT, VEC, U>(a, (uint32_t)pos, scale, lane);
+                        if (lane == 0 && a.fallbacks) atomicAdd(a.fallbacks, 1u);
+                        pos -= 1;
+                        since = wall_clock64();
+                        continue;
+                    }
+                    __builtin_amdgcn_s_sleep(2);
+                }
+                if (lane == 0) st_relaxed(&a.status[u], pack_status(a.epoch, kFlagInc, excl + unit_total));
+            }
+            if (lane == 0) s_excl = excl;
+        }
+        __syncthreads();
+        excl = s_excl;
+    }
+
+    int64_t start = 0;
+    if (a.offset_in) start = *a.offset_in;
+    if (a.align8) start = (start + 7) & ~(int64_t)7;
+
+    if constexpr (MODE != MODE_VALS) {
+        if (tid < ntiles) {
+            uint32_t tb = 0;
+#pragma unroll
+            for (int j = 0; j < U; j++)
+                if (j == tid) tb = tile_base[j];
+            a.prefix[t0 + tid] = excl + tb;
+        }
+        if (t0 + ntiles == a.tend && tid == 0) {
+            a.prefix[a.T] = excl + unit_total;
+            int64_t end = start + (int64_t)(excl + unit_total);
+            if (a.offset_out) *a.offset_out = end;
+            if (a.start_out) *a.start_out = start;
+            if (a.err && end > a.vals_capacity && MODE == MODE_FUSED) atomicOr(a.err, 1);
+        }
+        if constexpr (QUANT) {
+            if (u == 0 && tid == 0 && a.scale_out) *a.scale_out = scale;
+        }
+    }
+
+    if constexpr (MODE != MODE_COUNT) {
+        if (start < 0) {                             // corrupt cursor: write nothing
+            if (a.err && tid == 0) atomicOr(a.err, 2);
+            return;
+        }
+        const int64_t g0 = start + (int64_t)excl;   // first element of this unit's run
+        if (MODE == MODE_VALS && a.err && g0 + (int64_t)unit_total > a.vals_capacity && tid == 0)
+            atomicOr(a.err, 1);
+        const int p = (int)((((uintptr_t)a.vals) / OUTB + (uint64_t)g0) % EPS);
+        // stage the run in LDS at its 16-byte phase
+#pragma unroll
+        for (int j = 0; j < U; j++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                uint32_t mm = m[j][h];
+                uint32_t r = (uint32_t)p + lr[j][h];
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    if ((mm >> e) & 1u) {
+                        if constexpr (OUTB == 2)
+                            reinterpret_cast<uint16_t*>(s_vals)[r] = (uint16_t)elem<2>(o[j][h], e);
+                        else
+                            s_vals[r] = (uint8_t)elem<1>(o[j][h], e);
+                        r++;
+                    }
+                }
+            }
+        __syncthreads();
+        const int nslots = (p + (int)unit_total + EPS - 1) / EPS;
+        for (int s = tid; s < nslots; s += kThreads) {
+            const int64_t e0 = g0 - p + (int64_t)s * EPS;   // element index of slot start
+            int lo = max(0, p - s * EPS);
+            int hi = min(EPS, p + (int)unit_total - s * EPS);
+            int64_t cap_hi = a.vals_capacity - e0;
+            if (cap_hi < hi) hi = (int)max<int64_t>(cap_hi, 0);
+            if (lo == 0 && hi == EPS) {
+                *reinterpret_cast<uint4*>(a.vals + e0 * OUTB) =
+                    *reinterpret_cast<const uint4*>(s_vals + s * 16);
+            } else {
+                for (int e = lo; e < hi; e++) {
+                    if constexpr (OUTB == 2)
+                        reinterpret_cast<uint16_t*>(a.vals)[e0 + e] =
+                            reinterpret_cast<const uint16_t*>(s_vals)[s * EPS + e];
+                    else
+                        a.vals[e0 + e] = s_vals[s * EPS + e];
+                }
+            }
+        }
+    }
+}
+
+// ===========================================================================
+// tile_pack: bitmask + int32 counts (reference API shape)
+// ===========================================================================
+template <int IN_T, bool VEC>
+__global__ __launch_bounds__(kThreads) void tile_pack_kernel(const uint8_t* dense, int64_t M, int64_t N,
+                                                             uint32_t grid_n, int32_t* counts,
+                                                             uint8_t* bitmask)
+{
+    constexpr int INB = IN_T == DT_BF16 ? 2 : 1;
+    __shared__ uint32_t s_tot[4];
+    const int tid = threadIdx.x;
+    const uint32_t t = blockIdx.x;
+    uint32_t c = 0;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        int b = h * 256 + tid;
+        int64_t row, col0;
+        chunk_pos(t, grid_n, b, row, col0);
+        auto d = load_chunk<INB, VEC>(dense, M, N, row, col0);
+        typename Raw<INB>::T o;
+        uint32_t mk = chunk_mask<IN_T, false>(d, o, 1.0f);
+        bitmask[(size_t)t * kTileBytes + b] = (uint8_t)mk;
+        c += __popc(mk);
+    }
+    c = wave_sum_u32(c);
+    if ((tid & 63) == 0) s_tot[tid >> 6] = c;
+    __syncthreads();
+    if (tid == 0) counts[t] = (int32_t)(s_tot[0] + s_tot[1] + s_tot[2] + s_tot[3]);
+}
+
+// ===========================================================================
+// prefix from counts: one workgroup, 1024 threads, carries across blocks
+// ===========================================================================
+__global__ __launch_bounds__(1024) void prefix_kernel(const int32_t* counts, int64_t T, uint32_t* prefix)
+{
+    __shared__ uint32_t s_w[16];
+    __shared__ uint32_t s_carry;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    if (tid == 0) { s_carry = 0; prefix[0] = 0; }
+    __syncthreads();
+    for (int64_t base = 0; base < T; base += 1024) {
+        int64_t i = base + tid;
+        uint32_t v = i < T ? (uint32_t)counts[i] : 0u;
+        // inclusive wave scan
+        uint32_t x = v;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            uint32_t y = __shfl_up(x, o, 64);
+            if (lane >= o) x += y;
+        }
+        if (lane == 63) s_w[wave] = x;
+        __syncthreads();
+        uint32_t wb = 0, all = 0;
+        for (int w = 0; w < 16; w++) {
+            uint32_t tw = s_w[w];
+            if (w < wave) wb += tw;
+            all += tw;
+        }
+        uint32_t carry = s_carry;
+        if (i < T) prefix[i + 1] = carry + wb + x;
+        __syncthreads();
+        if (tid == 0) s_carry = carry + all;
+        __syncthreads();
+    }
+}
+
+// ===========================================================================
+// decompress / relu2-gradient value gather
+// ===========================================================================
+struct GatherArgs {
+    const uint8_t* vals;
+    int64_t vals_numel;
+    const uint8_t* bitmask;
+    const uint32_t* prefix;
+    const int64_t* vals_offset;
+    uint8_t* out;          // decompress: [rows, K] output; relu2: the gradient
+    int64_t first_m_tile;
+    uint32_t grid_n;
+    int64_t K;             // columns of out
+    int64_t rows;          // rows of out
+    uint32_t num_tiles;
+    float relu2_scale;
+    const float* scale;
+};
+
+// Stage the value run of tiles [t0, t0+ntiles) in LDS; returns its phase.
+// The run is [vo + prefix[t0], vo + prefix[t0+ntiles]).
+template <int VB>
+__device__ __forceinline__ int stage_run(const GatherArgs& a, int64_t run0, int64_t run1,
+                                         int64_t max_count, uint8_t* s_vals, int tid)
+{
+    constexpr int EPS = 16 / VB;
+    const int p = (int)((((uintptr_t)a.vals) / VB + (uint64_t)run0) % EPS);
+    // a consistent prefix gives 0 <= count <= 4096 per tile; clamp so that a
+    // corrupt one can never index past the staging buffer
+    int64_t cnt64 = run1 - run0;
+    cnt64 = cnt64 < 0 ? 0 : (cnt64 > max_count ? max_count : cnt64);
+    const int count = (int)cnt64;
+    const int nslots = (p + count + EPS - 1) / EPS;
+    for (int s = tid; s < nslots; s += kThreads) {
+        const int64_t e0 = run0 - p + (int64_t)s * EPS;
+        uint4 v = {0u, 0u, 0u, 0u};
+        if (e0 >= 0 && e0 + EPS <= a.vals_numel) {
+            v = *reinterpret_cast<const uint4*>(a.vals + e0 * VB);
+        } else {
+            for (int e = 0; e < EPS; e++) {
+                int64_t i = e0 + e;
+                if (i >= 0 && i < a.vals_numel) {
+                    if (VB == 2) {
+                        uint32_t x = reinterpret_cast<const uint16_t*>(a.vals)[i];
+                        uint32_t* w = e < 2 ? &v.x : e < 4 ? &v.y : e < 6 ? &v.z : &v.w;
+                        *w |= x << ((e & 1) * 16);
+                    } else {
+                        uint32_t x = a.vals[i];
+                        uint32_t* w = e < 4 ? &v.x : e < 8 ? &v.y : e < 12 ? &v.z : &v.w;
+                        *w |= x << ((e & 3) * 8);
+                    }
+                }
+            }
+        }
+        *reinterpret_cast<uint4*>(s_vals + s * 16) = v;
+    }
+    return p;
+}
+
+// Shared front half of decompress and relu2_grad: bitmask bytes, in-tile
+// ranks, run staging.  Fills m[][], r0[][] (LDS element index of each chunk's
+// first value) and returns after a barrier.
+template <int VB, int U>
+__device__ __forceinline__ void gather_prepare(const GatherArgs& a, uint32_t t0, int ntiles,
+                                               uint32_t (&m)[U][2], uint32_t (&r0)[U][2],
+                                               uint32_t* s_pref, uint32_t (*s_wtot)[2][4],
+                                               uint8_t* s_vals, int tid)
+{
+    const int wave = tid >> 6, lane = tid & 63;
+#pragma unroll
+    for (int j = 0; j < U; j++)
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+            m[j][h] = j < ntiles ? a.bitmask[(size_t)(t0 + j) * kTileBytes + h * 256 + tid] : 0u;
+    if (tid <= ntiles) s_pref[tid] = a.prefix[t0 + tid];
+    uint32_t ex[U][2];
+#pragma unroll
+    for (int j = 0; j < U; j++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            uint32_t tot;
+            wave_scan_count(__popc(m[j][h]), ex[j][h], tot);
+            if (lane == 0) s_wtot[j][h][wave] = tot;
+        }
+    __syncthreads();
+    const int64_t vo = a.vals_offset ? *a.vals_offset : 0;
+    const uint32_t pb = s_pref[0];
+    const int p = stage_run<VB>(a, vo + pb, vo + s_pref[ntiles], (int64_t)ntiles * kTileNumel,
+                                s_vals, tid);
+#pragma unroll
+    for (int j = 0; j < U; j++) {
+        uint32_t tb = j < ntiles ? min(s_pref[j] - pb, (uint32_t)(j * kTileNumel)) : 0u;
+        uint32_t h0 = 0, h0w = 0, h1w = 0;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            uint32_t a0 = s_wtot[j][0][w], a1 = s_wtot[j][1][w];
+            h0 += a0;
+            if (w < wave) { h0w += a0; h1w += a1; }
+        }
+        r0[j][0] = (uint32_t)p + tb + h0w + ex[j][0];
+        r0[j][1] = (uint32_t)p + tb + h0 + h1w + ex[j][1];
+    }
+    __syncthreads();
+}
+
+template <int V_T>
+__device__ __forceinline__ uint32_t lds_val(const uint8_t* s_vals, uint32_t i)
+{
+    if constexpr (V_T == DT_BF16) return reinterpret_cast<const uint16_t*>(s_vals)[i];
+    else return s_vals[i];
+}
+
+// k*v*v as bf16 bits: bf16 storage squares in bf16 ((k*v) rounded, then *v
+// rounded); fp8 storage widens to fp32 and rounds once.
+template <int V_T>
+__device__ __forceinline__ uint32_t relu2_square(uint32_t raw, float k)
+{
+    if constexpr (V_T == DT_BF16) {
+        float v = bf16_to_f32(raw);
+        float kv = bf16_to_f32(f32_to_bf16(k * v));
+        return f32_to_bf16(kv * v);
+    } else {
+        float v = fp8_to_f32<V_T>(raw);
+        return f32_to_bf16((k * v) * v);
+    }
+}
+
+template <int V_T>
+__device__ __forceinline__ float val_f32(uint32_t raw)
+{
+    if constexpr (V_T == DT_BF16) return bf16_to_f32(raw);
+    else return fp8_to_f32<V_T>(raw);
+}
+
+template <int V_T, bool SQUARE, bool HAS_SCALE, bool VEC, int U>
+__global__ __launch_bounds__(kThreads) void decompress_kernel(GatherArgs a)
+{
+    constexpr int VB = V_T == DT_BF16 ? 2 : 1;
+    constexpr int OB = SQUARE ? 2 : VB;
+    __shared__ uint32_t s_pref[U + 1];
+    __shared__ uint32_t s_wtot[U][2][4];
+    __shared__ __align__(16) uint8_t s_vals[U * kTileNumel * VB + 16];
+    const int tid = threadIdx.x;
+    const uint32_t pid0 = blockIdx.x * U;
+    const int ntiles = (int)min((uint32_t)U, a.num_tiles - pid0);
+    const uint32_t t0 = (uint32_t)a.first_m_tile * a.grid_n + pid0;
+
+    uint32_t m[U][2], r0[U][2];
+    gather_prepare<VB, U>(a, t0, ntiles, m, r0, s_pref, s_wtot, s_vals, tid);
+
+    float s2b = 1.0f;
+    if constexpr (HAS_SCALE) {
+        float s = *a.scale;
+        s2b = bf16_to_f32(f32_to_bf16(s * s));
+    }
+#pragma unroll
+    for (int j = 0; j < U; j++) {
+        if (j >= ntiles) break;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            typename Raw<OB>::T ov = {};
+            uint32_t r = r0[j][h];
+            const uint32_t mm = m[j][h];
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                uint32_t x = 0;
+                if ((mm >> e) & 1u) {
+                    x = lds_val<V_T>(s_vals, r++);
+                    if constexpr (SQUARE) x = relu2_square<V_T>(x, a.relu2_scale);
+                }
+                if constexpr (HAS_SCALE) x = f32_to_bf16(bf16_to_f32(x) * s2b);
+                set_elem<OB>(ov, e, x);
+            }
+            int64_t row, col0;
+            chunk_pos(pid0 + j, a.grid_n, h * 256 + tid, row, col0);
+            store_chunk<OB, VEC>(a.out, a.rows, a.K, row, col0, ov);
+        }
+    }
+}
+
+// grad = bit ? bf16(grad * (2k * r)) : 0, then optionally grad = bf16(grad * bf16(scale))
+template <int V_T, bool HAS_SCALE, bool VEC, int U>
+__global__ __launch_bounds__(kThreads) void relu2_grad_kernel(GatherArgs a)
+{
+    constexpr int VB = V_T == DT_BF16 ? 2 : 1;
+    __shared__ uint32_t s_pref[U + 1];
+    __shared__ uint32_t s_wtot[U][2][4];
+    __shared__ __align__(16) uint8_t s_vals[U * kTileNumel * VB + 16];
+    const int tid = threadIdx.x;
+    const uint32_t t0 = blockIdx.x * U;
+    const int ntiles = (int)min((uint32_t)U, a.num_tiles - t0);
+
+    // gradient chunks are independent of the gather: issue their loads first
+    uint4 g[U][2];
+#pragma unroll
+    for (int j = 0; j < U; j++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            g[j][h] = uint4{0u, 0u, 0u, 0u};
+            if (j < ntiles) {
+                int64_t row, col0;
+                chunk_pos(t0 + j, a.grid_n, h * 256 + tid, row, col0);
+                g[j][h] = load_chunk<2, VEC>(a.out, a.rows, a.K, row, col0);
+            }
+        }
+    uint32_t m[U][2], r0[U][2];
+    gather_prepare<VB, U>(a, t0, ntiles, m, r0, s_pref, s_wtot, s_vals, tid);
+
+    float sb = 1.0f;
+    if constexpr (HAS_SCALE) sb = bf16_to_f32(f32_to_bf16(*a.scale));
+    const float k2 = 2.0f * a.relu2_scale;
+#pragma unroll
+    for (int j = 0; j < U; j++) {
+        if (j >= ntiles) break;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            uint4 ov = {0u, 0u, 0u, 0u};
+            uint32_t r = r0[j][h];
+            const uint32_t mm = m[j][h];
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                uint32_t x = 0;
+                if ((mm >> e) & 1u) {
+                    float rv = val_f32<V_T>(lds_val<V_T>(s_vals, r++));
+                    x = f32_to_bf16(bf16_to_f32(get16(g[j][h], e)) * (k2 * rv));
+                }
+                if constexpr (HAS_SCALE) x = f32_to_bf16(bf16_to_f32(x) * sb);
+                set_elem<2>(ov, e, x);
+            }
+            int64_t row, col0;
+            chunk_pos(t0 + j, a.grid_n, h * 256 + tid, row, col0);
+            store_chunk<2, VEC>(a.out, a.rows, a.K, row, col0, ov);
+        }
+    }
+}
+
+// ===========================================================================
+// ReLU mask gradient (in place)
+// ===========================================================================
+template <bool VEC, int U>
+__global__ __launch_bounds__(kThreads) void relu_grad_kernel(uint8_t* grad, int64_t M, int64_t N,
+                                                             uint32_t grid_n, uint32_t T,
+                                                             const uint8_t* bitmask)
+{
+    const int tid = threadIdx.x;
+    const uint32_t t0 = blockIdx.x * U;
+    const int ntiles = (int)min((uint32_t)U, T - t0);
+    uint32_t m[U][2];
+#pragma unroll
+    for (int j = 0; j < U; j++)
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+            m[j][h] = j < ntiles ? bitmask[(size_t)(t0 + j) * kTileBytes + h * 256 + tid] : 0xffu;
+    uint4 g[U][2];
+#pragma unroll
+    for (int j = 0; j < U; j++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            g[j][h] = uint4{0u, 0u, 0u, 0u};
+            if (m[j][h] != 0u && m[j][h] != 0xffu) {
+                int64_t row, col0;
+                chunk_pos(t0 + j, grid_n, h * 256 + tid, row, col0);
+                g[j][h] = load_chunk<2, VEC>(grad, M, N, row, col0);
+            }
+        }
+#pragma unroll
+    for (int j = 0; j < U; j++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const uint32_t mm = m[j][h];
+            if (mm == 0xffu) continue;    // all kept: nothing to write
+            uint4 v = g[j][h];
+            // byte mask -> 16-bit lane masks (all-zero byte stores zeros)
+            uint32_t k0 = ((mm & 1u) ? 0xffffu : 0u) | ((mm & 2u) ? 0xffff0000u : 0u);
+            uint32_t k1 = ((mm & 4u) ? 0xffffu : 0u) | ((mm & 8u) ? 0xffff0000u : 0u);
+            uint32_t k2 = ((mm & 16u) ? 0xffffu : 0u) | ((mm & 32u) ? 0xffff0000u : 0u);
+            uint32_t k3 = ((mm & 64u) ? 0xffffu : 0u) | ((mm & 128u) ? 0xffff0000u : 0u);
+            v.x &= k0; v.y &= k1; v.z &= k2; v.w &= k3;
+            int64_t row, col0;
+            chunk_pos(t0 + j, grid_n, h * 256 + tid, row, col0);
+            store_chunk<2, VEC>(grad, M, N, row, col0, v);
+        }
+}
+
+// ===========================================================================
+// host launchers
+// ===========================================================================
+constexpr int kCompressU = 4;
+constexpr int kGatherU = 2;
+constexpr int kMaskU = 4;
+
+static inline bool aligned16(const void* p) { return (((uintptr_t)p) & 15u) == 0; }
+static inline bool aligned8(const void* p) { return (((uintptr_t)p) & 7u) == 0; }
+
+template <int IN_T, bool QUANT, int MODE>
+static hipError_t launch_compress_mode(const CompressArgs& a, bool vec, hipStream_t st)
+{
+    const uint32_t units = (a.tend - a.tile0 + kCompressU - 1) / kCompressU;
+    if (vec)
+        hipLaunchKernelGGL((compress_kernel<IN_T, QUANT, true, MODE, kCompressU>), dim3(units),
+                           dim3(kThreads), 0, st, a);
+    else
+        hipLaunchKernelGGL((compress_kernel<IN_T, QUANT, false, MODE, kCompressU>), dim3(units),
+                           dim3(kThreads), 0, st, a);
+    return hipGetLastError();
+}
+
+template <int MODE>
+static hipError_t launch_compress(const CompressArgs& a, int in_dtype, bool quant, bool vec,
+                                  hipStream_t st)
+{
+    if (quant) return launch_compress_mode<DT_BF16, true, MODE>(a, vec, st);
+    switch (in_dtype) {
+    case DT_BF16: return launch_compress_mode<DT_BF16, false, MODE>(a, vec, st);
+    case DT_E4M3FN: return launch_compress_mode<DT_E4M3FN, false, MODE>(a, vec, st);
+    default: return launch_compress_mode<DT_E5M2, false, MODE>(a, vec, st);
+    }
+}
+
+}  // namespace bs
+
+using namespace bs;
+
+extern "C" int64_t bs_compress_workspace_bytes(int64_t M, int64_t N)
+{
+    if (M < 0 || N < 0) return -1;
+    int64_t T = ((M + 63) / 64) * ((N + 63) / 64);
+    return kWsHeaderBytes + 8 * (T > 0 ? T : 1);
+}
+
+extern "C" const uint64_t* bs_workspace_amax_slot(const void* ws, int64_t)
+{
+    return reinterpret_cast<const uint64_t*>(reinterpret_cast<const uint8_t*>(ws) + kWsAmaxOffset);
+}
+
+extern "C" const uint32_t* bs_workspace_fallback_counter(const void* ws, int64_t)
+{
+    return reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint8_t*>(ws) + kWsFallbackOffset);
+}
+
+static int check_dense(const void* dense, int dtype, int64_t M, int64_t N, const char* what)
+{
+    if (dtype < 0 || dtype > 2) return set_error(BS_ERR_INVALID, "%s: unknown dtype code %d", what, dtype);
+    if (M < 0 || N < 0) return set_error(BS_ERR_INVALID, "%s: negative shape", what);
+    if ((M > 0 && N > 0) && dense == nullptr) return set_error(BS_ERR_INVALID, "%s: null input", what);
+    if ((uint64_t)M * (uint64_t)N >= (1ull << 32))
+        return set_error(BS_ERR_INVALID, "%s: M*N must be < 2^32 (uint32 prefix)", what);
+    int elem = dtype == DT_BF16 ? 2 : 1;
+    if (((uintptr_t)dense) % elem)
+        return set_error(BS_ERR_INVALID, "%s: input not aligned to its element size", what);
+    return BS_OK;
+}
+
+extern "C" int bs_compress(const void* dense, int in_dtype, int64_t M, int64_t N, int quantize,
+                           const uint64_t* amax_slot, uint32_t amax_epoch, float* scale_out,
+                           void* dense_q_out, uint8_t* bitmask, uint32_t* prefix, void* vals,
+                           int64_t vals_capacity, const int64_t* vals_offset_in, int align8,
+                           int64_t* vals_offset_out, int64_t* vals_start_out, int write_vals,
+                           int32_t* err_flags, void* workspace, int64_t workspace_bytes,
+                           uint32_t epoch, void* stream)
+{
+    clear_error();
+    if (int rc = check_dense(dense, in_dtype, M, N, "bs_compress")) return rc;
+    if (quantize && in_dtype != DT_BF16)
+        return set_error(BS_ERR_INVALID, "bs_compress: quantize needs bf16 input");
+    if (quantize && amax_slot == nullptr)
+        return set_error(BS_ERR_INVALID, "bs_compress: quantize needs the amax slot");
+    const int64_t T = ((M + 63) / 64) * ((N + 63) / 64);
+    if (prefix == nullptr) return set_error(BS_ERR_INVALID, "bs_compress: null prefix");
+    if (T > 0 && bitmask == nullptr) return set_error(BS_ERR_INVALID, "bs_compress: null bitmask");
+    if (write_vals && vals_capacity > 0 && vals == nullptr)
+        return set_error(BS_ERR_INVALID, "bs_compress: null vals");
+    if (vals_capacity < 0) return set_error(BS_ERR_INVALID, "bs_compress: negative capacity");
+    if (vals_offset_out != nullptr && vals_offset_out == vals_offset_in)
+        return set_error(BS_ERR_INVALID, "bs_compress: vals_offset_out aliases vals_offset_in");
+    if (epoch == 0 || epoch >= (1u << 30))
+        return set_error(BS_ERR_INVALID, "bs_compress: epoch must be in [1, 2^30)");
+    if (workspace == nullptr || workspace_bytes < bs_compress_workspace_bytes(M, N))
+        return set_error(BS_ERR_INVALID, "bs_compress: workspace too small (%lld < %lld bytes)",
+                         (long long)workspace_bytes, (long long)bs_compress_workspace_bytes(M, N));
+    const int outb = (in_dtype == DT_BF16 && !quantize) ? 2 : 1;
+    if (write_vals && ((uintptr_t)vals) % outb)
+        return set_error(BS_ERR_INVALID, "bs_compress: vals not aligned to its element size");
+    hipStream_t st = (hipStream_t)stream;
+    if (T == 0) {
+        // empty input: prefix = [0], cursor unchanged
+        hipError_t e = hipMemsetAsync(prefix, 0, 4, st);
+        if (e == hipSuccess && vals_offset_out) {
+            if (vals_offset_in) e = hipMemcpyAsync(vals_offset_out, vals_offset_in, 8, hipMemcpyDeviceToDevice, st);
+            else e = hipMemsetAsync(vals_offset_out, 0, 8, st);
+        }
+        if (e == hipSuccess && vals_start_out) {
+            if (vals_offset_in) e = hipMemcpyAsync(vals_start_out, vals_offset_in, 8, hipMemcpyDeviceToDevice, st);
+            else e = hipMemsetAsync(vals_start_out, 0, 8, st);
+        }
+        return e == hipSuccess ? BS_OK : set_error(BS_ERR_HIP, "bs_compress: %s", hipGetErrorString(e));
+    }
+    CompressArgs a{};
+    a.dense = (const uint8_t*)dense;
+    a.M = M;
+    a.N = N;
+    a.grid_n = (uint32_t)((N + 63) / 64);
+    a.T = (uint32_t)T;
+    a.amax_slot = amax_slot;
+    a.amax_epoch = amax_epoch;
+    a.scale_out = scale_out;
+    a.dense_q_out = (uint8_t*)dense_q_out;
+    a.bitmask = bitmask;
+    a.prefix = prefix;
+    a.vals = (uint8_t*)vals;
+    a.vals_capacity = vals_capacity;
+    a.offset_in = vals_offset_in;
+    a.align8 = align8;
+    a.offset_out = vals_offset_out;
+    a.start_out = vals_start_out;
+    a.tile0 = 0;
+    a.tend = (uint32_t)T;
+    a.status = reinterpret_cast<uint64_t*>((uint8_t*)workspace + kWsHeaderBytes);
+    a.epoch = epoch;
+    a.err = err_flags;
+    a.fallbacks = reinterpret_cast<uint32_t*>((uint8_t*)workspace + kWsFallbackOffset);
+    const int inb = in_dtype == DT_BF16 ? 2 : 1;
+    bool vec = (N % 8 == 0) && (((uintptr_t)dense) % (8 * inb) == 0) &&
+               (dense_q_out == nullptr || aligned8(dense_q_out));
+    hipError_t e = write_vals ? launch_compress<MODE_FUSED>(a, in_dtype, quantize != 0, vec, st)
+                              : launch_compress<MODE_COUNT>(a, in_dtype, quantize != 0, vec, st);
+    if (e != hipSuccess) return set_error(BS_ERR_HIP, "bs_compress launch: %s", hipGetErrorString(e));
+    return BS_OK;
+}
+
+extern "C" int bs_compact_vals(const void* dense, int in_dtype, int64_t M, int64_t N,
+                               const uint8_t* bitmask, const uint32_t* prefix, void* vals,
+                               int64_t vals_capacity, const int64_t* vals_offset, int64_t first_tile,
+                               int64_t num_tiles, int32_t* err_flags, void* stream)
+{
+    clear_error();
+    if (int rc = check_dense(dense, in_dtype, M, N, "bs_compact_vals")) return rc;
+    const int64_t T = ((M + 63) / 64) * ((N + 63) / 64);
+    if (first_tile < 0 || num_tiles < 0 || first_tile + num_tiles > T)
+        return set_error(BS_ERR_INVALID, "bs_compact_vals: tile range [%lld, %lld) outside [0, %lld)",
+                         (long long)first_tile, (long long)(first_tile + num_tiles), (long long)T);
+    if (num_tiles == 0) return BS_OK;
+    if (bitmask == nullptr || prefix == nullptr)
+        return set_error(BS_ERR_INVALID, "bs_compact_vals: null bitmask/prefix");
+    if (vals_capacity < 0) return set_error(BS_ERR_INVALID, "bs_compact_vals: negative capacity");
+    if (vals_capacity > 0 && vals == nullptr) return set_error(BS_ERR_INVALID, "bs_compact_vals: null vals");
+    const int eb = in_dtype == DT_BF16 ? 2 : 1;
+    if (((uintptr_t)vals) % eb) return set_error(BS_ERR_INVALID, "bs_compact_vals: vals misaligned");
+    CompressArgs a{};
+    a.dense = (const uint8_t*)dense;
+    a.M = M;
+    a.N = N;
+    a.grid_n = (uint32_t)((N + 63) / 64);
+    a.T = (uint32_t)T;
+    a.bitmask = (uint8_t*)bitmask;
+    a.prefix = (uint32_t*)prefix;
+    a.vals = (uint8_t*)vals;
+    a.vals_capacity = vals_capacity;
+    a.offset_in = vals_offset;
+    a.tile0 = (uint32_t)first_tile;
+    a.tend = (uint32_t)(first_tile + num_tiles);
+    a.err = err_flags;
+    bool vec = (N % 8 == 0) && (((uintptr_t)dense) % (8 * eb) == 0);
+    hipError_t e = launch_compress<MODE_VALS>(a, in_dtype, false, vec, (hipStream_t)stream);
+    if (e != hipSuccess) return set_error(BS_ERR_HIP, "bs_compact_vals launch: %s", hipGetErrorString(e));
+    return BS_OK;
+}
+
+extern "C" int bs_tile_pack(const void* dense, int in_dtype, int64_t M, int64_t N, int32_t* tile_counts,
+                            uint8_t* bitmask, void* stream)
+{
+    clear_error();
+    if (int rc = check_dense(dense, in_dtype, M, N, "bs_tile_pack")) return rc;
+    const int64_t T = ((M + 63) / 64) * ((N + 63) / 64);
+    if (T == 0) return BS_OK;
+    if (tile_counts == nullptr || bitmask == nullptr)
+        return set_error(BS_ERR_INVALID, "bs_tile_pack: null output");
+    const int eb = in_dtype == DT_BF16 ? 2 : 1;
+    bool vec = (N % 8 == 0) && (((uintptr_t)dense) % (8 * eb) == 0);
+    uint32_t gn = (uint32_t)((N + 63) / 64);
+    hipStream_t st = (hipStream_t)stream;
+    const uint8_t* d = (const uint8_t*)dense;
+#define BS_TP(DT, V) hipLaunchKernelGGL((tile_pack_kernel<DT, V>), dim3((uint32_t)T), dim3(kThreads), 0, st, \
+                                        d, M, N, gn, tile_counts, bitmask)
+    switch (in_dtype) {
+    case DT_BF16: if (vec) BS_TP(DT_BF16, true); else BS_TP(DT_BF16, false); break;
+    case DT_E4M3FN: if (vec) BS_TP(DT_E4M3FN, true); else BS_TP(DT_E4M3FN, false); break;
+    default: if (vec) BS_TP(DT_E5M2, true); else BS_TP(DT_E5M2, false); break;
+    }
+#undef BS_TP
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(BS_ERR_HIP, "bs_tile_pack launch: %s", hipGetErrorString(e));
+    return BS_OK;
+}
+
+extern "C" int bs_prefix_from_counts(const int32_t* tile_counts, int64_t T, uint32_t* prefix, void* stream)
+{
+    clear_error();
+    if (T < 0) return set_error(BS_ERR_INVALID, "bs_prefix_from_counts: negative T");
+    if (prefix == nullptr || (T > 0 && tile_counts == nullptr))
+        return set_error(BS_ERR_INVALID, "bs_prefix_from_counts: null pointer");
+    hipLaunchKernelGGL(prefix_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, tile_counts, T, prefix);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(BS_ERR_HIP, "bs_prefix_from_counts launch: %s", hipGetErrorString(e));
+    return BS_OK;
+}
+
+template <int V_T, bool SQ, bool SC>
+static void launch_decompress_t(const GatherArgs& a, bool vec, hipStream_t st)
+{
+    const uint32_t blocks = (a.num_tiles + kGatherU - 1) / kGatherU;
+    if (vec)
+        hipLaunchKernelGGL((decompress_kernel<V_T, SQ, SC, true, kGatherU>), dim3(blocks), dim3(kThreads), 0, st, a);
+    else
+        hipLaunchKernelGGL((decompress_kernel<V_T, SQ, SC, false, kGatherU>), dim3(blocks), dim3(kThreads), 0, st, a);
+}
+
+template <int V_T>
+static void launch_decompress_v(const GatherArgs& a, bool sq, bool sc, bool vec, hipStream_t st)
+{
+    if (!sq) launch_decompress_t<V_T, false, false>(a, vec, st);
+    else if (!sc) launch_decompress_t<V_T, true, false>(a, vec, st);
+    else launch_decompress_t<V_T, true, true>(a, vec, st);
+}
+
+static int check_gather(const void* vals, int vals_dtype, int64_t vals_numel, const uint8_t* bitmask,
+                        const uint32_t* prefix, const char* what)
+{
+    if (vals_dtype < 0 || vals_dtype > 2) return set_error(BS_ERR_INVALID, "%s: unknown dtype %d", what, vals_dtype);
+    if (vals_numel < 0) return set_error(BS_ERR_INVALID, "%s: negative vals_numel", what);
+    if (bitmask == nullptr || prefix == nullptr) return set_error(BS_ERR_INVALID, "%s: null bitmask/prefix", what);
+    if (vals_numel > 0 && vals == nullptr) return set_error(BS_ERR_INVALID, "%s: null vals", what);
+    int vb = vals_dtype == DT_BF16 ? 2 : 1;
+    if (((uintptr_t)vals) % vb) return set_error(BS_ERR_INVALID, "%s: vals misaligned", what);
+    return BS_OK;
+}
+
+extern "C" int bs_decompress(const void* vals, int vals_dtype, int64_t vals_numel, const uint8_t* bitmask,
+                             const uint32_t* prefix, const int64_t* vals_offset, void* out,
+                             int64_t first_m_tile, int64_t grid_n, int64_t K, int64_t batch_rows,
+                             int64_t num_tiles_in_batch, int square, float relu2_scale, const float* scale,
+                             void* stream)
+{
+    clear_error();
+    if (int rc = check_gather(vals, vals_dtype, vals_numel, bitmask, prefix, "bs_decompress")) return rc;
+    if (grid_n <= 0 || K < 0 || batch_rows < 0 || num_tiles_in_batch < 0 || first_m_tile < 0)
+        return set_error(BS_ERR_INVALID, "bs_decompress: bad batch geometry");
+    if (num_tiles_in_batch == 0 || K == 0 || batch_rows == 0) return BS_OK;
+    if (out == nullptr) return set_error(BS_ERR_INVALID, "bs_decompress: null output");
+    if (scale != nullptr && !square)
+        return set_error(BS_ERR_INVALID, "bs_decompress: scale is only applied with square=1");
+    if ((uint64_t)(first_m_tile * grid_n + num_tiles_in_batch) >= (1ull << 32))
+        return set_error(BS_ERR_INVALID, "bs_decompress: tile ids exceed 32 bits");
+    const int ob = square ? 2 : (vals_dtype == DT_BF16 ? 2 : 1);
+    if (((uintptr_t)out) % ob) return set_error(BS_ERR_INVALID, "bs_decompress: output misaligned");
+    GatherArgs a{};
+    a.vals = (const uint8_t*)vals;
+    a.vals_numel = vals_numel;
+    a.bitmask = bitmask;
+    a.prefix = prefix;
+    a.vals_offset = vals_offset;
+    a.out = (uint8_t*)out;
+    a.first_m_tile = first_m_tile;
+    a.grid_n = (uint32_t)grid_n;
+    a.K = K;
+    a.rows = batch_rows;
+    a.num_tiles = (uint32_t)num_tiles_in_batch;
+    a.relu2_scale = relu2_scale;
+    a.scale = scale;
+    bool vec = (K % 8 == 0) && (((uintptr_t)out) % (8 * ob) == 0);
+    hipStream_t st = (hipStream_t)stream;
+    switch (vals_dtype) {
+    case DT_BF16: launch_decompress_v<DT_BF16>(a, square, scale != nullptr, vec, st); break;
+    case DT_E4M3FN: launch_decompress_v<DT_E4M3FN>(a, square, scale != nullptr, vec, st); break;
+    default: launch_decompress_v<DT_E5M2>(a, square, scale != nullptr, vec, st); break;
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(BS_ERR_HIP, "bs_decompress launch: %s", hipGetErrorString(e));
+    return BS_OK;
+}
+
+extern "C" int bs_relu_grad(void* grad, int64_t M, int64_t N, const uint8_t* bitmask, void* stream)
+{
+    clear_error();
+    if (M < 0 || N < 0) return set_error(BS_ERR_INVALID, "bs_relu_grad: negative shape");
+    const int64_t T = ((M + 63) / 64) * ((N + 63) / 64);
+    if (T == 0) return BS_OK;
+    if (grad == nullptr || bitmask == nullptr) return set_error(BS_ERR_INVALID, "bs_relu_grad: null pointer");
+    if ((uint64_t)M * (uint64_t)N >= (1ull << 32))
+        return set_error(BS_ERR_INVALID, "bs_relu_grad: M*N must be < 2^32");
+    if (((uintptr_t)grad) & 1u) return set_error(BS_ERR_INVALID, "bs_relu_grad: grad misaligned");
+    bool vec = (N % 8 == 0) && aligned16(grad);
+    uint32_t gn = (uint32_t)((N + 63) / 64);
+    const uint32_t blocks = (uint32_t)((T + kMaskU - 1) / kMaskU);
+    hipStream_t st = (hipStream_t)stream;
+    if (vec)
+        hipLaunchKernelGGL((relu_grad_kernel<true, kMaskU>), dim3(blocks), dim3(kThreads), 0, st,
+                           (uint8_t*)grad, M, N, gn, (uint32_t)T, bitmask);
+    else
+        hipLaunchKernelGGL((relu_grad_kernel<false, kMaskU>), dim3(blocks), dim3(kThreads), 0, st,
+                           (uint8_t*)grad, M, N, gn, (uint32_t)T, bitmask);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(BS_ERR_HIP, "bs_relu_grad launch: %s", hipGetErrorString(e));
+    return BS_OK;
+}
+
+template <int V_T, bool SC>
+static void launch_relu2_t(const GatherArgs& a, bool vec, hipStream_t st)
+{
+    const uint32_t blocks = (a.num_tiles + kGatherU - 1) / kGatherU;
+    if (vec)
+        hipLaunchKernelGGL((relu2_grad_kernel<V_T, SC, true, kGatherU>), dim3(blocks), dim3(kThreads), 0, st, a);
+    else
+        hipLaunchKernelGGL((relu2_grad_kernel<V_T, SC, false, kGatherU>), dim3(blocks), dim3(kThreads), 0, st, a);
+}
+
+extern "C" int bs_relu2_grad(void* grad, int64_t M, int64_t N, const void* vals, int vals_dtype,
+                             int64_t vals_numel, const uint8_t* bitmask, const uint32_t* prefix,
+                             const int64_t* vals_offset, float relu2_scale, const float* scale, void* stream)
+{
+    clear_error();
+    if (int rc = check_gather(vals, vals_dtype, vals_numel, bitmask, prefix, "bs_relu2_grad")) return rc;
+    if (M < 0 || N < 0) return set_error(BS_ERR_INVALID, "bs_relu2_grad: negative shape");
+    const int64_t T = ((M + 63) / 64) * ((N + 63) / 64);
+    if (T == 0) return BS_OK;
+    if (grad == nullptr) return set_error(BS_ERR_INVALID, "bs_relu2_grad: null grad");
+    if ((uint64_t)M * (uint64_t)N >= (1ull << 32))
+        return set_error(BS_ERR_INVALID, "bs_relu2_grad: M*N must be < 2^32");
+    if (((uintptr_t)grad) & 1u) return set_error(BS_ERR_INVALID, "bs_relu2_grad: grad misaligned");
+    GatherArgs a{};
+    a.vals = (const uint8_t*)vals;
+    a.vals_numel = vals_numel;
+    a.bitmask = bitmask;
+    a.prefix = prefix;
+    a.vals_offset = vals_offset;
+    a.out = (uint8_t*)grad;
+    a.first_m_tile = 0;
+    a.grid_n = (uint32_t)((N + 63) / 64);
+    a.K = N;
+    a.rows = M;
+    a.num_tiles = (uint32_t)T;
+    a.relu2_scale = relu2_scale;
+    a.scale = scale;
+    bool vec = (N % 8 == 0) && aligned16(grad);
+    hipStream_t st = (hipStream_t)stream;
+    bool sc = scale != nullptr;
+    switch (vals_dtype) {
+    case DT_BF16: if (sc) launch_relu2_t<DT_BF16, true>(a, vec, st); else launch_relu2_t<DT_BF16, false>(a, vec, st); break;
+    case DT_E4M3FN: if (sc) launch_relu2_t<DT_E4M3FN, true>(a, vec, st); else launch_relu2_t<DT_E4M3FN, false>(a, vec, st); break;
+    default: if (sc) launch_relu2_t<DT_E5M2, true>(a, vec, st); else launch_relu2_t<DT_E5M2, false>(a, vec, st); break;
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(BS_ERR_HIP, "bs_relu2_grad launch: %s", hipGetErrorString(e));
+    return BS_OK;
+}

@@ -1,0 +1,126 @@
+// e4m3fn quantisation for gfx950: amax reduction and the quantize pass that
+// together replace lib_sparse/fp8.py:123-129 (to_fp8).
+//
+// scale = max(fp32(amax|x|) / 448, 1e-9); q = e4m3fn_RNE(fp32(x) / scale)
+// with one correctly rounded fp32 division per element.
+#include "bs_device.h"
+#include "bs_host.h"
+
+namespace bs {
+
+constexpr int kFp8Threads = 256;
+
+// max over |x| as bf16 magnitude bits; NaN patterns sort above Inf, so a NaN
+// anywhere wins the max and the decoded amax is NaN.
+__global__ __launch_bounds__(kFp8Threads) void amax_bf16_kernel(const uint16_t* x, int64_t n,
+                                                                uint64_t* slot, uint32_t epoch)
+{
+    __shared__ uint32_t s_w[kFp8Threads / 64];
+    const int tid = threadIdx.x;
+    uint32_t m = 0;
+    const int64_t nvec = ((((uintptr_t)x) & 15u) == 0) ? n / 8 : 0;
+    const int64_t stride = (int64_t)gridDim.x * kFp8Threads;
+    for (int64_t i = (int64_t)blockIdx.x * kFp8Threads + tid; i < nvec; i += stride) {
+        uint4 v = reinterpret_cast<const uint4*>(x)[i];
+        uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            m = max(m, w[k] & 0x7fffu);
+            m = max(m, (w[k] >> 16) & 0x7fffu);
+        }
+    }
+    for (int64_t i = nvec * 8 + (int64_t)blockIdx.x * kFp8Threads + tid; i < n; i += stride)
+        m = max(m, (uint32_t)x[i] & 0x7fffu);
+    m = wave_max_u32(m);
+    if ((tid & 63) == 0) s_w[tid >> 6] = m;
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < kFp8Threads / 64; w++) m = max(m, s_w[w]);
+        atomicMax((unsigned long long*)slot, (unsigned long long)(((uint64_t)epoch << 32) | m));
+    }
+}
+
+__device__ __forceinline__ float fp8_scale_from_slot(const uint64_t* slot, uint32_t epoch)
+{
+    uint64_t s = *slot;
+    float amax = ((uint32_t)(s >> 32) == epoch) ? bf16_to_f32((uint32_t)s & 0xffffu) : 0.0f;
+    float sc = amax / 448.0f;
+    return (sc < 1e-9f) ? 1e-9f : sc;
+}
+
+__global__ __launch_bounds__(kFp8Threads) void quantize_e4m3_kernel(const uint16_t* x, int64_t n,
+                                                                    uint8_t* q, float* scale_out,
+                                                                    const uint64_t* slot,
+                                                                    uint32_t epoch)
+{
+    const float scale = fp8_scale_from_slot(slot, epoch);
+    const int tid = threadIdx.x;
+    if (blockIdx.x == 0 && tid == 0 && scale_out) *scale_out = scale;
+    const bool vec = ((((uintptr_t)x) & 15u) == 0) && ((((uintptr_t)q) & 7u) == 0);
+    const int64_t nvec = vec ? n / 8 : 0;
+    const int64_t stride = (int64_t)gridDim.x * kFp8Threads;
+    for (int64_t i = (int64_t)blockIdx.x * kFp8Threads + tid; i < nvec; i += stride) {
+        uint4 v = reinterpret_cast<const uint4*>(x)[i];
+        uint32_t w[4] = {v.x, v.y, v.z, v.w};
+        uint32_t o[2] = {0u, 0u};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            uint32_t lo = f32_to_e4m3(bf16_to_f32(w[k] & 0xffffu) / scale);
+            uint32_t hi = f32_to_e4m3(bf16_to_f32(w[k] >> 16) / scale);
+            o[k >> 1] |= (lo | (hi << 8)) << (16 * (k & 1));
+        }
+        reinterpret_cast<uint2*>(q)[i] = uint2{o[0], o[1]};
+    }
+    for (int64_t i = nvec * 8 + (int64_t)blockIdx.x * kFp8Threads + tid; i < n; i += stride)
+        q[i] = (uint8_t)f32_to_e4m3(bf16_to_f32(x[i]) / scale);
+}
+
+static uint32_t grid_for(int64_t n)
+{
+    int64_t g = (n / 8 + kFp8Threads - 1) / kFp8Threads;
+    if (g < 1) g = 1;
+    if (g > 4096) g = 4096;
+    return (uint32_t)g;
+}
+
+}  // namespace bs
+
+using namespace bs;
+
+extern "C" int bs_amax(const void* x, int64_t n, void* workspace, int64_t workspace_bytes, uint32_t epoch,
+                       void* stream)
+{
+    clear_error();
+    if (n < 0) return set_error(BS_ERR_INVALID, "bs_amax: negative n");
+    if (workspace == nullptr || workspace_bytes < kWsHeaderBytes)
+        return set_error(BS_ERR_INVALID, "bs_amax: workspace too small");
+    if (epoch == 0 || epoch >= (1u << 30)) return set_error(BS_ERR_INVALID, "bs_amax: epoch out of range");
+    if (n > 0 && x == nullptr) return set_error(BS_ERR_INVALID, "bs_amax: null input");
+    if (((uintptr_t)x) & 1u) return set_error(BS_ERR_INVALID, "bs_amax: input misaligned");
+    if (n == 0) return BS_OK;   // slot keeps an older epoch: readers then see amax = 0
+    uint64_t* slot = reinterpret_cast<uint64_t*>((uint8_t*)workspace + kWsAmaxOffset);
+    hipLaunchKernelGGL(amax_bf16_kernel, dim3(grid_for(n)), dim3(kFp8Threads), 0, (hipStream_t)stream,
+                       (const uint16_t*)x, n, slot, epoch);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(BS_ERR_HIP, "bs_amax launch: %s", hipGetErrorString(e));
+    return BS_OK;
+}
+
+extern "C" int bs_quantize_e4m3fn(const void* x, int64_t n, void* q_out, float* scale_out,
+                                  const void* workspace, int64_t workspace_bytes, uint32_t epoch,
+                                  void* stream)
+{
+    clear_error();
+    if (n < 0) return set_error(BS_ERR_INVALID, "bs_quantize_e4m3fn: negative n");
+    if (workspace == nullptr || workspace_bytes < kWsHeaderBytes)
+        return set_error(BS_ERR_INVALID, "bs_quantize_e4m3fn: workspace too small");
+    if (n > 0 && (x == nullptr || q_out == nullptr))
+        return set_error(BS_ERR_INVALID, "bs_quantize_e4m3fn: null pointer");
+    if (((uintptr_t)x) & 1u) return set_error(BS_ERR_INVALID, "bs_quantize_e4m3fn: input misaligned");
+    const uint64_t* slot = reinterpret_cast<const uint64_t*>((const uint8_t*)workspace + kWsAmaxOffset);
+    hipLaunchKernelGGL(quantize_e4m3_kernel, dim3(grid_for(n)), dim3(kFp8Threads), 0, (hipStream_t)stream,
+                       (const uint16_t*)x, n, (uint8_t*)q_out, scale_out, slot, epoch);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(BS_ERR_HIP, "bs_quantize_e4m3fn launch: %s", hipGetErrorString(e));
+    return BS_OK;
+}

@@ -1,0 +1,163 @@
+"""Autograd MLP layers whose ReLU / ReLU^2 activation is saved compressed.
+
+Mirrors reference lib_sparse/layers.py: ``ReluLinear`` (:20-66), ``FFNRelu``
+(:69-94), ``Relu2Linear`` (:100-151), ``FFNRelu2`` (:154-177) — same
+signatures, including the reference's ``dtype`` (FFNRelu) vs
+``storage_dtype`` (FFNRelu2) keyword names.  Forward: GEMM -> ReLU (in
+place) -> [fp8 quantize] -> compress (HIP) -> GEMM.  Backward: dW from the
+compressed activation (reconstruct-into-LDS GEMM for bf16), dZ from the
+bitmask (HIP mask / ReLU^2-gradient kernels).
+"""
+from __future__ import annotations
+
+import torch
+from torch import Tensor
+from torch.autograd import Function
+
+from .bitsparse import BitsparseTensor, TensorBuffer
+from .config import RELU2_SCALE
+from .fp8 import is_fp8, matmul, to_fp8
+from .src.functions import dense_to_tilesparse, quantize_and_compress
+from .src.hip_operators import mask_with_bitmask_, relu2_grad_sparse_
+from .src.sparse_matmul import AspB, AspRelu2B
+
+
+# ------------------------------------------------------------
+# ReLU layers
+# ------------------------------------------------------------
+class ReluLinear(Function):
+    """y = relu(z) @ W.T with relu(z) saved compressed."""
+
+    @staticmethod
+    def forward(ctx, z, W, sparse_data: TensorBuffer | None = None, pack_sbit: bool = False,
+                dtype: torch.dtype = torch.bfloat16):
+        ctx.dtype = dtype
+        ctx.save_for_backward(W)
+        h = z.relu_()
+
+        if is_fp8(dtype):
+            if dtype != torch.float8_e4m3fn:
+                raise TypeError("fp8 activation storage is float8_e4m3fn")
+            h, scale, h_sparse = quantize_and_compress(h, sparse_data)
+        else:
+            scale = None
+            h_sparse = dense_to_tilesparse(h, scale, sparse_data, pack_sbit)
+
+        ctx.h_sparse = h_sparse
+        y = matmul(h, W.T, is_fp8(dtype), a_scale=scale)
+        return y
+
+    @staticmethod
+    @torch.compiler.disable
+    def backward(ctx, grad_output: Tensor):
+        W = ctx.saved_tensors[0]
+        needs_z = ctx.needs_input_grad[0]
+        h: BitsparseTensor = ctx.h_sparse
+        ctx.h_sparse = None
+
+        fp8 = is_fp8(ctx.dtype)
+        if fp8:
+            grad_output, scale = to_fp8(grad_output)
+        else:
+            grad_output, scale = grad_output, None
+
+        grad_W2 = AspB(grad_output.T, h, A_scale=scale)
+
+        if needs_z:
+            grad_h = matmul(grad_output, W, fp8=fp8, a_scale=scale)
+            grad_z = mask_with_bitmask_(grad_h, h)
+        else:
+            grad_z = None
+        return grad_z, grad_W2, None, None, None
+
+
+class FFNRelu:
+    """FFN block with ReLU activation: y = relu(x @ W1.T + b1) @ W2.T + b2."""
+
+    @staticmethod
+    def apply(x, W1, W2, b1=None, b2=None, *,
+              sparse_data: TensorBuffer | None = None, pack_sbit: bool = False,
+              dtype: torch.dtype = torch.bfloat16):
+        """x [*bs, d_in], W1 [d_ff, d_in], W2 [d_out, d_ff], b1 [d_ff], b2 [d_out]
+        -> [*bs, d_out]."""
+        bs_dims = x.shape[:-1]
+        x = x.reshape(-1, x.shape[-1])
+
+        z = matmul(x, W1.T, is_fp8(dtype))
+        if b1 is not None:
+            z = z + b1
+        y = ReluLinear.apply(z, W2, sparse_data, pack_sbit, dtype)
+
+        y = y.reshape(*bs_dims, y.shape[-1])
+        if b2 is not None:
+            y = y + b2
+        return y
+
+
+# ------------------------------------------------------------
+# ReLU^2 layers
+# ------------------------------------------------------------
+class Relu2Linear(Function):
+    """y = (k * relu(z)^2) @ W.T with r = relu(z) saved compressed."""
+
+    @staticmethod
+    def forward(ctx, z, W, sparse_data: TensorBuffer | None, pack_sbit: bool = False,
+                storage_dtype: torch.dtype = torch.bfloat16):
+        ctx.dtype = storage_dtype
+        ctx.save_for_backward(W)
+        h = z.relu_()
+
+        if is_fp8(storage_dtype):
+            if storage_dtype != torch.float8_e4m3fn:
+                raise TypeError("fp8 activation storage is float8_e4m3fn")
+            _, scale, h_sparse = quantize_and_compress(h, sparse_data)
+        else:
+            h_sparse = dense_to_tilesparse(h, None, sparse_data, pack_sbit)
+        ctx.h_sparse = h_sparse
+
+        h.square_()
+        h.mul_(RELU2_SCALE)
+        y = matmul(h, W.T, is_fp8(storage_dtype))
+        return y
+
+    @staticmethod
+    @torch.compiler.disable
+    def backward(ctx, grad_output: Tensor):
+        W = ctx.saved_tensors[0]
+        needs_z = ctx.needs_input_grad[0]
+        h: BitsparseTensor = ctx.h_sparse
+        ctx.h_sparse = None
+
+        fp8 = is_fp8(ctx.dtype)
+        if fp8:
+            grad_output, scale = to_fp8(grad_output)
+        else:
+            grad_output, scale = grad_output, None
+
+        grad_W2 = AspRelu2B(grad_output.T, h, A_scale=scale)
+
+        if needs_z:
+            grad_h = matmul(grad_output, W, fp8=fp8, a_scale=scale)
+            grad_z = relu2_grad_sparse_(grad_h, h)
+        else:
+            grad_z = None
+        return grad_z, grad_W2, None, None, None
+
+
+class FFNRelu2:
+    """FFN block with ReLU^2 activation: y = k*relu(x @ W1.T + b1)^2 @ W2.T + b2."""
+
+    @staticmethod
+    def apply(x, W1, W2, b1=None, b2=None, *,
+              sparse_data: TensorBuffer | None = None, pack_sbit: bool = False,
+              storage_dtype: torch.dtype = torch.bfloat16):
+        bs_dims = x.shape[:-1]
+        x = x.reshape(-1, x.shape[-1])
+        z = matmul(x, W1.T, is_fp8(storage_dtype))
+        if b1 is not None:
+            z = z + b1
+        y = Relu2Linear.apply(z, W2, sparse_data, pack_sbit, storage_dtype)
+        y = y.reshape(*bs_dims, y.shape[-1])
+        if b2 is not None:
+            y = y + b2
+        return y

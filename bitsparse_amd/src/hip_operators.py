@@ -1,0 +1,231 @@
+"""Launchers of the HIP codec kernels (libbitsparse_hip.so) on torch tensors.
+
+Same function names, argument meaning and in-place conventions as reference
+lib_sparse/src/triton_operators.py (:21-202); ``triton_operators`` is kept as
+an alias module of this one.  Every function enqueues on torch's current
+stream of the tensors' device and raises on CPU tensors (no CPU path).
+"""
+from __future__ import annotations
+
+import torch
+from torch import Tensor
+
+from .. import _lib
+from .._lib import check, ptr, require_device, stream_handle
+from ..bitsparse import BitsparseTensor, pack_codec
+from ..config import RELU2_SCALE
+
+_SBIT_MSG = ("pack_sbit=True (15/7-bit packed value stream) is not implemented in "
+             "bitsparse_amd yet; use raw storage (pack_sbit=False)")
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    if dtype == torch.bfloat16:
+        return _lib.DT_BF16
+    if dtype == torch.float8_e4m3fn:
+        return _lib.DT_E4M3FN
+    if dtype == torch.float8_e5m2:
+        return _lib.DT_E5M2
+    raise TypeError("BitsparseTensor supports bfloat16 and FP8 (e4m3fn/e5m2) values")
+
+
+def _contig(t: Tensor, what: str) -> Tensor:
+    if not t.is_contiguous():
+        raise ValueError(f"{what} must be contiguous (row-major)")
+    return t
+
+
+# ---------------------------------------------------------------------------
+# compress
+# ---------------------------------------------------------------------------
+def tile_pack(
+    dense: Tensor, tile_counts: Tensor, tile_bitmasks: Tensor,
+    M: int, N: int, grid_m: int, grid_n: int,
+    BLOCK_M: int, BLOCK_N: int,
+    TILE_NUMEL: int, TILE_BYTES: int,
+) -> None:
+    """Per-tile bitmask and int32 nonzero counts (in-place outputs).
+    Reference: triton_operators.py:21-33."""
+    require_device(dense, "tile_pack")
+    _contig(dense, "dense")
+    if tile_counts.dtype != torch.int32 or tile_bitmasks.dtype != torch.uint8:
+        raise TypeError("tile_pack: counts must be int32 and bitmasks uint8")
+    L = _lib.load()
+    check(L.bs_tile_pack(dense.data_ptr(), dtype_code(dense.dtype), M, N,
+                         tile_counts.data_ptr(), tile_bitmasks.data_ptr(),
+                         stream_handle(dense.device)), "bs_tile_pack")
+
+
+def prefix_from_counts(tile_counts: Tensor, tile_prefix: Tensor) -> None:
+    """prefix[0] = 0, prefix[1:] = cumsum(counts) as uint32 (reference
+    functions.py:38-40)."""
+    L = _lib.load()
+    check(L.bs_prefix_from_counts(tile_counts.data_ptr(), tile_counts.numel(),
+                                  tile_prefix.data_ptr(), stream_handle(tile_counts.device)),
+          "bs_prefix_from_counts")
+
+
+def compact_vals(
+    dense: Tensor, tile_bitmasks: Tensor, tile_prefix: Tensor,
+    vals: Tensor | None, vals_offset: Tensor | None,
+    M: int, N: int, grid_n: int, num_tiles: int,
+    BLOCK_M: int, BLOCK_N: int, TILE_NUMEL: int, pack_sbit: bool,
+) -> tuple[Tensor, Tensor]:
+    """Compact positive values into standalone (vals=None: exact-size, after
+    one host sync for nnz) or preallocated storage.
+    Reference: triton_operators.py:36-115 (raw mode)."""
+    if pack_sbit:
+        raise NotImplementedError(_SBIT_MSG)
+    require_device(dense, "compact_vals")
+    _contig(dense, "dense")
+    if vals is None:
+        nnz = int(tile_prefix[-1].item())
+        vals = torch.empty(nnz, device=dense.device, dtype=dense.dtype)
+        vals_offset = torch.zeros((), device=dense.device, dtype=torch.int64)
+    elif vals.dtype != dense.dtype:
+        raise TypeError(f"compact_vals: storage dtype {vals.dtype} differs from input {dense.dtype}")
+    L = _lib.load()
+    check(L.bs_compact_vals(dense.data_ptr(), dtype_code(dense.dtype), M, N,
+                            tile_bitmasks.data_ptr(), tile_prefix.data_ptr(),
+                            vals.data_ptr(), vals.numel(), ptr(vals_offset), 0, num_tiles,
+                            None, stream_handle(dense.device)), "bs_compact_vals")
+    return vals, vals_offset
+
+
+def compress_into(dense: Tensor, bitmask: Tensor, prefix: Tensor, vals: Tensor | None,
+                  vals_offset_in: Tensor | None, vals_offset_out: Tensor | None,
+                  err_flags: Tensor | None, write_vals: bool = True,
+                  quantize: bool = False, scale_out: Tensor | None = None,
+                  dense_q_out: Tensor | None = None, amax_epoch: int = 0) -> None:
+    """Single-pass compress (bitmask + prefix + values in one read of dense).
+
+    ``quantize``: dense is bf16 and is quantized to e4m3fn with the scale of
+    the amax computed by ``amax_into_workspace`` under ``amax_epoch``."""
+    require_device(dense, "compress")
+    _contig(dense, "dense")
+    M, N = dense.shape
+    L = _lib.load()
+    ws = _lib.workspace_for(dense.device)
+    ws.ensure(L.bs_compress_workspace_bytes(M, N))
+    epoch = ws.next_epoch()
+    cap = vals.numel() if (vals is not None and write_vals) else 0
+    check(L.bs_compress(
+        dense.data_ptr(), dtype_code(dense.dtype), M, N, int(quantize),
+        ws.amax_slot_ptr() if quantize else None, amax_epoch, ptr(scale_out), ptr(dense_q_out),
+        bitmask.data_ptr(), prefix.data_ptr(),
+        ptr(vals) if write_vals else None, cap, ptr(vals_offset_in), 0,
+        ptr(vals_offset_out), None, int(write_vals), ptr(err_flags),
+        ws.buf.data_ptr(), ws.nbytes, epoch, stream_handle(dense.device)), "bs_compress")
+
+
+def amax_into_workspace(x: Tensor) -> int:
+    """amax(|x|) of a bf16 tensor into the stream's workspace; returns the
+    epoch that tags it."""
+    require_device(x, "amax")
+    _contig(x, "x")
+    if x.dtype != torch.bfloat16:
+        raise TypeError("amax expects a bfloat16 tensor")
+    L = _lib.load()
+    ws = _lib.workspace_for(x.device)
+    ws.ensure(256)
+    epoch = ws.next_epoch()
+    check(L.bs_amax(x.data_ptr(), x.numel(), ws.buf.data_ptr(), ws.nbytes, epoch,
+                    stream_handle(x.device)), "bs_amax")
+    return epoch
+
+
+def quantize_e4m3fn(x: Tensor, amax_epoch: int) -> tuple[Tensor, Tensor]:
+    """(e4m3fn tensor, fp32 0-d scale) from the amax of ``amax_epoch``."""
+    L = _lib.load()
+    ws = _lib.workspace_for(x.device)
+    q = torch.empty(x.shape, device=x.device, dtype=torch.float8_e4m3fn)
+    scale = torch.empty((), device=x.device, dtype=torch.float32)
+    check(L.bs_quantize_e4m3fn(x.data_ptr(), x.numel(), q.data_ptr(), scale.data_ptr(),
+                               ws.buf.data_ptr(), ws.nbytes, amax_epoch,
+                               stream_handle(x.device)), "bs_quantize_e4m3fn")
+    return q, scale
+
+
+# ---------------------------------------------------------------------------
+# decompress
+# ---------------------------------------------------------------------------
+def _unpack(sparse: BitsparseTensor, output: Tensor, first_m_tile: int, grid_n: int, K: int,
+            batch_rows: int, num_tiles_in_batch: int, square: bool, scale: Tensor | None) -> Tensor:
+    if sparse.pack_sbit:
+        raise NotImplementedError(_SBIT_MSG)
+    require_device(output, "unpack")
+    _contig(output, "output")
+    want = torch.bfloat16 if square else sparse.vals.dtype
+    if output.dtype != want:
+        raise TypeError(f"unpack: output dtype {output.dtype}, expected {want}")
+    if output.numel() < batch_rows * K:
+        raise ValueError("unpack: output smaller than batch_rows x K")
+    if first_m_tile + (num_tiles_in_batch + grid_n - 1) // grid_n > sparse.grid_m:
+        raise ValueError("unpack: tile batch runs past the tile grid")
+    L = _lib.load()
+    check(L.bs_decompress(sparse.vals.data_ptr(), dtype_code(sparse.vals.dtype), sparse.vals.numel(),
+                          sparse.bitmask.data_ptr(), sparse.prefix.data_ptr(),
+                          sparse.vals_offset.data_ptr(), output.data_ptr(), first_m_tile, grid_n, K,
+                          batch_rows, num_tiles_in_batch, int(square), float(RELU2_SCALE),
+                          ptr(scale), stream_handle(output.device)), "bs_decompress")
+    return output
+
+
+def unpack_batch_(
+    sparse: BitsparseTensor, output: Tensor,
+    first_m_tile: int, grid_n: int, K: int, batch_rows: int,
+    num_tiles_in_batch: int,
+) -> Tensor:
+    """Unpack a row batch of tiles into a dense [batch_rows, K] output in the
+    stored dtype (in place).  Reference: triton_operators.py:118-138."""
+    return _unpack(sparse, output, first_m_tile, grid_n, K, batch_rows, num_tiles_in_batch,
+                   False, None)
+
+
+def unpack_relu2_batch_(
+    sparse: BitsparseTensor, output: Tensor,
+    first_m_tile: int, grid_n: int, K: int, batch_rows: int,
+    num_tiles_in_batch: int,
+) -> Tensor:
+    """Unpack stored r = relu(a) as k * r^2 into a bf16 output (in place),
+    times scale^2 for fp8 storage.  Reference: triton_operators.py:141-162."""
+    return _unpack(sparse, output, first_m_tile, grid_n, K, batch_rows, num_tiles_in_batch,
+                   True, sparse.scale)
+
+
+# ---------------------------------------------------------------------------
+# gradients
+# ---------------------------------------------------------------------------
+def _check_grad(grad: Tensor, sparse: BitsparseTensor, what: str) -> None:
+    require_device(grad, what)
+    _contig(grad, "grad")
+    if grad.dtype != torch.bfloat16:
+        raise TypeError(f"{what}: grad must be bfloat16")
+    if tuple(grad.shape) != tuple(sparse.shape):
+        raise ValueError(f"{what}: grad shape {tuple(grad.shape)} != {tuple(sparse.shape)}")
+
+
+def mask_with_bitmask_(grad: Tensor, sparse: BitsparseTensor) -> Tensor:
+    """grad <- grad * bitmask, in place.  Reference: triton_operators.py:165-175."""
+    _check_grad(grad, sparse, "mask_with_bitmask_")
+    M, N = sparse.shape
+    L = _lib.load()
+    check(L.bs_relu_grad(grad.data_ptr(), M, N, sparse.bitmask.data_ptr(),
+                         stream_handle(grad.device)), "bs_relu_grad")
+    return grad
+
+
+def relu2_grad_sparse_(grad: Tensor, sparse_z: BitsparseTensor) -> Tensor:
+    """grad <- grad * 2k*r where set, 0 elsewhere, then * scale for fp8
+    storage, in place.  Reference: triton_operators.py:178-202."""
+    if sparse_z.pack_sbit:
+        raise NotImplementedError(_SBIT_MSG)
+    _check_grad(grad, sparse_z, "relu2_grad_sparse_")
+    M, N = sparse_z.shape
+    L = _lib.load()
+    check(L.bs_relu2_grad(grad.data_ptr(), M, N, sparse_z.vals.data_ptr(),
+                          dtype_code(sparse_z.vals.dtype), sparse_z.vals.numel(),
+                          sparse_z.bitmask.data_ptr(), sparse_z.prefix.data_ptr(),
+                          sparse_z.vals_offset.data_ptr(), float(RELU2_SCALE), ptr(sparse_z.scale),
+                          stream_handle(grad.device)), "bs_relu2_grad")
+    return grad

@@ -1,0 +1,192 @@
+/*
+ * bitsparse_hip.h — C ABI of libbitsparse_hip.so, the MI355X (gfx950) kernels
+ * behind the BitSparse activation-compression path.
+ *
+ * Conventions (all entry points):
+ *   - plain C types only: device pointers as void* / typed pointers, sizes as
+ *     int64_t, the HIP stream as an opaque void* (hipStream_t; NULL = the
+ *     default stream).  No torch or C++ types cross the boundary.
+ *   - every call is asynchronous on `stream`, allocates no device memory and
+ *     returns an int status: BS_OK, or an error code with a message available
+ *     from bs_last_error() (thread local).  Argument checks happen on the
+ *     host before anything is enqueued; a failed call enqueues nothing.
+ *   - dtype codes are the reference's codec ids (lib_sparse/bitsparse.py:20-30):
+ *     0 = bf16, 1 = float8_e4m3fn, 2 = float8_e5m2.
+ *   - matrices are dense, row-major, contiguous ([rows, cols], row stride =
+ *     cols), as the reference kernels assume (triton_kernels.py:82).
+ *
+ * Compressed format (reference triton_kernels.py:1-17, bitsparse.py:132-139):
+ *   64x64 tiles, T = ceil(M/64)*ceil(N/64), tile t = tm*grid_n + tn;
+ *   bitmask  uint8[T*512]: bit (f%8) of byte t*512 + f/8 is [x > 0] for
+ *            tile-flat index f = r*64 + c;
+ *   prefix   uint32[T+1]: prefix[0] = 0, prefix[t+1] = prefix[t] + nnz(tile t);
+ *   vals     element i of tile t sits at vals[*vals_offset + prefix[t] + rank].
+ */
+#ifndef BITSPARSE_HIP_H
+#define BITSPARSE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BS_OK 0
+#define BS_ERR_INVALID 1   /* bad argument (shape, dtype, pointer, size) */
+#define BS_ERR_HIP 2       /* a HIP runtime call failed                  */
+
+#define BS_DT_BF16 0
+#define BS_DT_E4M3FN 1
+#define BS_DT_E5M2 2
+
+/* Last error message of the calling thread ("" when none). */
+const char* bs_last_error(void);
+
+/* ABI version of this library (bumped when an entry point changes). */
+int bs_abi_version(void);
+
+/*
+ * Workspace for the single-pass compress (bs_compress) and the fp8 amax
+ * (bs_amax): a status word per compress unit plus an amax slot.  It must be
+ * zero-filled once before first use; afterwards every call passes an `epoch`
+ * that differs from all epochs used with this workspace since it was last
+ * zeroed (1, 2, 3, ... up to 2^30-1).  One workspace serves one stream at a
+ * time.  Returns the byte size needed for a dense [M, N] input.
+ */
+int64_t bs_compress_workspace_bytes(int64_t M, int64_t N);
+
+/*
+ * Single-pass compress of a dense [M, N] activation: bitmask, prefix and
+ * the compacted values in one read of `dense` (decoupled look-back across
+ * compress units).
+ *   in_dtype     dtype of `dense` (0, 1, 2)
+ *   quantize     1: `dense` is bf16 and is quantized to e4m3fn on the fly
+ *                with scale = max(amax/448, 1e-9), amax taken from the amax
+ *                slot that bs_amax wrote with `amax_epoch`; the bitmask and
+ *                vals then describe the quantized values; `scale_out` (fp32,
+ *                nullable) receives the scale and `dense_q_out` (nullable,
+ *                uint8 [M, N]) the quantized dense copy.
+ *   vals         value storage (element size 2 for bf16, 1 for fp8/quantize)
+ *   vals_capacity elements available in `vals`; elements that would land at
+ *                or past it are not written and bit 0 of `*err_flags` is set
+ *   vals_offset_in  device int64 (nullable = 0): where this tensor's values
+ *                start in `vals` (the TensorBuffer cursor)
+ *   align8       1: round the start offset up to a multiple of 8
+ *   vals_offset_out device int64 (nullable): receives start + nnz, the next
+ *                cursor.  May not alias vals_offset_in.
+ *   vals_start_out device int64 (nullable): receives the (aligned) start.
+ *   write_vals   0: write only bitmask and prefix (count pass of the
+ *                standalone path, values come later from bs_compact_vals)
+ *   err_flags    device int32 (nullable), bits OR-ed in on error
+ * Replaces lib_sparse/src/functions.py:55-99 (dense_to_tilesparse), which
+ * runs triton_kernels.py:67-97 (_tile_pack_kernel), a torch.cumsum
+ * (functions.py:38-40) and triton_kernels.py:109-146 (_compact_vals_kernel).
+ */
+int bs_compress(const void* dense, int in_dtype, int64_t M, int64_t N, int quantize,
+                const uint64_t* amax_slot, uint32_t amax_epoch, float* scale_out,
+                void* dense_q_out, uint8_t* bitmask, uint32_t* prefix,
+                void* vals, int64_t vals_capacity, const int64_t* vals_offset_in,
+                int align8, int64_t* vals_offset_out, int64_t* vals_start_out,
+                int write_vals, int32_t* err_flags, void* workspace,
+                int64_t workspace_bytes, uint32_t epoch, void* stream);
+
+/*
+ * Per-tile bitmask and nonzero counts (int32[T]) of a dense [M, N] input.
+ * Replaces lib_sparse/src/triton_operators.py:21-33 (tile_pack) /
+ * triton_kernels.py:67-97 (_tile_pack_kernel).
+ */
+int bs_tile_pack(const void* dense, int in_dtype, int64_t M, int64_t N,
+                 int32_t* tile_counts, uint8_t* bitmask, void* stream);
+
+/*
+ * prefix[0] = 0, prefix[1..T] = inclusive scan of counts (uint32, wrapping).
+ * Replaces lib_sparse/src/functions.py:38-40 (torch.cumsum into prefix).
+ */
+int bs_prefix_from_counts(const int32_t* tile_counts, int64_t T, uint32_t* prefix,
+                          void* stream);
+
+/*
+ * Values of tiles [first_tile, first_tile + num_tiles) to
+ * vals[*vals_offset + prefix[t] - prefix[first_tile] + rank], using the
+ * given bitmask.  Replaces lib_sparse/src/triton_operators.py:108-115
+ * (compact_vals, raw mode) / triton_kernels.py:109-146.
+ */
+int bs_compact_vals(const void* dense, int in_dtype, int64_t M, int64_t N,
+                    const uint8_t* bitmask, const uint32_t* prefix, void* vals,
+                    int64_t vals_capacity, const int64_t* vals_offset,
+                    int64_t first_tile, int64_t num_tiles, int32_t* err_flags,
+                    void* stream);
+
+/*
+ * Decompress tiles of a row batch into a dense [batch_rows, K] output
+ * (row stride K): tile of batch tile-index p is
+ * t = (first_m_tile + p / grid_n) * grid_n + p % grid_n.
+ *   vals_dtype    stored dtype; vals_numel = elements readable in `vals`
+ *   square        0: out has the stored dtype, out = bit ? v : +0
+ *                 1: out is bf16, out = k*v*v (bf16 storage: bf16(bf16(k*v)*v);
+ *                    fp8 storage: widened to fp32, rounded once)
+ *   scale         device fp32 (nullable, only with square): then
+ *                 out = bf16(out * bf16(scale*scale)) afterwards
+ * Replaces lib_sparse/src/triton_operators.py:118-138 (unpack_batch_) and
+ * :141-162 (unpack_relu2_batch_, including its output.mul_(scale**2)) /
+ * triton_kernels.py:158-241.
+ */
+int bs_decompress(const void* vals, int vals_dtype, int64_t vals_numel,
+                  const uint8_t* bitmask, const uint32_t* prefix,
+                  const int64_t* vals_offset, void* out, int64_t first_m_tile,
+                  int64_t grid_n, int64_t K, int64_t batch_rows,
+                  int64_t num_tiles_in_batch, int square, float relu2_scale,
+                  const float* scale, void* stream);
+
+/*
+ * In place on a bf16 [M, N] gradient: grad = bit ? grad : 0.
+ * Replaces lib_sparse/src/triton_operators.py:165-175 (mask_with_bitmask_) /
+ * triton_kernels.py:251-276.
+ */
+int bs_relu_grad(void* grad, int64_t M, int64_t N, const uint8_t* bitmask, void* stream);
+
+/*
+ * In place on a bf16 [M, N] gradient:
+ *   grad = bit ? bf16(grad * (2*k*fp32(r))) : 0, r gathered from vals;
+ *   then, when `scale` is given, grad = bf16(grad * bf16(*scale)).
+ * Replaces lib_sparse/src/triton_operators.py:178-202 (relu2_grad_sparse_,
+ * including its grad.mul_(scale)) / triton_kernels.py:290-330.
+ */
+int bs_relu2_grad(void* grad, int64_t M, int64_t N, const void* vals, int vals_dtype,
+                  int64_t vals_numel, const uint8_t* bitmask, const uint32_t* prefix,
+                  const int64_t* vals_offset, float relu2_scale, const float* scale,
+                  void* stream);
+
+/*
+ * amax(|x|) of a bf16 array into the workspace's amax slot, tagged with
+ * `epoch` (NaN propagates).  Replaces the x.abs().max() of
+ * lib_sparse/fp8.py:126.
+ */
+int bs_amax(const void* x, int64_t n, void* workspace, int64_t workspace_bytes,
+            uint32_t epoch, void* stream);
+
+/*
+ * q = e4m3fn_RNE(fp32(x) / scale), scale = max(amax/448, 1e-9) with amax
+ * from the slot bs_amax wrote with `epoch`; scale_out (nullable) gets the
+ * scale.  Replaces lib_sparse/fp8.py:123-129 (to_fp8) together with bs_amax.
+ */
+int bs_quantize_e4m3fn(const void* x, int64_t n, void* q_out, float* scale_out,
+                       const void* workspace, int64_t workspace_bytes, uint32_t epoch,
+                       void* stream);
+
+/* Device pointer of the amax slot inside a workspace (for bs_compress). */
+const uint64_t* bs_workspace_amax_slot(const void* workspace, int64_t workspace_bytes);
+
+/*
+ * Diagnostics counter inside the workspace: number of look-back fallbacks
+ * (a unit counted a predecessor itself after waiting for it) since zeroing.
+ * Device pointer to a uint32.
+ */
+const uint32_t* bs_workspace_fallback_counter(const void* workspace, int64_t workspace_bytes);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BITSPARSE_HIP_H */

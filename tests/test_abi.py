@@ -1,0 +1,127 @@
+"""C ABI of libbitsparse_hip.so on the CPU: the library loads, exports every
+entry point include/bitsparse_hip.h declares, and rejects bad arguments on
+the host (before any GPU work is enqueued)."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from bitsparse_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_functions():
+    txt = open(os.path.join(ROOT, "include", "bitsparse_hip.h")).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return sorted(set(re.findall(r"\b(bs_[a-z0-9_]+)\s*\(", txt)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.load()
+    names = header_functions()
+    assert len(names) >= 14
+    for n in names:
+        assert hasattr(L, n), n
+    assert set(names) == set(_lib.exported_symbols())
+
+
+def test_abi_version_and_workspace_size():
+    L = _lib.load()
+    assert L.bs_abi_version() == _lib.ABI_VERSION
+    assert L.bs_compress_workspace_bytes(4096, 4096) == 256 + 8 * 4096
+    assert L.bs_compress_workspace_bytes(129, 131) == 256 + 8 * 9
+    assert L.bs_compress_workspace_bytes(0, 0) == 256 + 8
+
+
+def _err():
+    return _lib.load().bs_last_error().decode()
+
+
+def test_invalid_arguments_rejected_on_host():
+    L = _lib.load()
+    fake = 0x10000   # never dereferenced: validation fails first
+    # unknown dtype
+    rc = L.bs_compress(fake, 7, 64, 64, 0, None, 0, None, None, fake, fake, fake, 10, None, 0,
+                       None, None, 1, None, fake, 1 << 20, 1, None)
+    assert rc == _lib.BS_ERR_INVALID and "dtype" in _err()
+    # quantize needs bf16
+    rc = L.bs_compress(fake, 1, 64, 64, 1, fake, 1, None, None, fake, fake, fake, 10, None, 0,
+                       None, None, 1, None, fake, 1 << 20, 1, None)
+    assert rc == _lib.BS_ERR_INVALID and "bf16" in _err()
+    # workspace too small
+    rc = L.bs_compress(fake, 0, 4096, 4096, 0, None, 0, None, None, fake, fake, fake, 10, None, 0,
+                       None, None, 1, None, fake, 64, 1, None)
+    assert rc == _lib.BS_ERR_INVALID and "workspace" in _err()
+    # epoch 0 is reserved for a zeroed workspace
+    rc = L.bs_compress(fake, 0, 64, 64, 0, None, 0, None, None, fake, fake, fake, 10, None, 0,
+                       None, None, 1, None, fake, 1 << 20, 0, None)
+    assert rc == _lib.BS_ERR_INVALID and "epoch" in _err()
+    # M*N beyond the uint32 prefix
+    rc = L.bs_tile_pack(fake, 0, 1 << 20, 1 << 12, fake, fake, None)
+    assert rc == _lib.BS_ERR_INVALID and "2^32" in _err()
+    # aliasing cursors
+    rc = L.bs_compress(fake, 0, 64, 64, 0, None, 0, None, None, fake, fake, fake, 10, fake + 64, 0,
+                       fake + 64, None, 1, None, fake, 1 << 20, 1, None)
+    assert rc == _lib.BS_ERR_INVALID and "alias" in _err()
+    # tile range of compact_vals
+    rc = L.bs_compact_vals(fake, 0, 64, 64, fake, fake, fake, 10, None, 0, 2, None, None)
+    assert rc == _lib.BS_ERR_INVALID and "tile range" in _err()
+    # decompress geometry and scale misuse
+    rc = L.bs_decompress(fake, 0, 10, fake, fake, None, fake, 0, 0, 64, 64, 1, 0, 1.0, None, None)
+    assert rc == _lib.BS_ERR_INVALID
+    rc = L.bs_decompress(fake, 0, 10, fake, fake, None, fake, 0, 1, 64, 64, 1, 0, 1.0, fake, None)
+    assert rc == _lib.BS_ERR_INVALID and "square" in _err()
+    rc = L.bs_relu2_grad(fake, 64, 64, fake, 5, 10, fake, fake, None, 1.0, None, None)
+    assert rc == _lib.BS_ERR_INVALID
+    rc = L.bs_amax(fake, -1, fake, 1 << 20, 1, None)
+    assert rc == _lib.BS_ERR_INVALID
+
+
+def test_python_api_rejects_cpu_tensors_and_bad_dtypes():
+    """No CPU path: the product API refuses host tensors (loudly) and
+    unsupported dtypes with the reference's exception types."""
+    from bitsparse_amd.src.functions import dense_to_tilesparse
+    from bitsparse_amd.fp8 import to_fp8
+    with pytest.raises(TypeError):
+        dense_to_tilesparse(torch.zeros(4, 4, dtype=torch.float32), None)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        dense_to_tilesparse(torch.zeros(4, 4, dtype=torch.bfloat16), None)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        to_fp8(torch.zeros(4, 4, dtype=torch.bfloat16))
+
+
+def test_container_helpers_match_reference_definitions():
+    import numpy as np
+    from bitsparse_amd.bitsparse import BitsparseTensor, TensorBuffer, bits_per_value, pack_codec, tile_grid
+    from oracle import oracle as O
+    from tests.helpers import bits, relu_input
+    assert tile_grid(129, 131, 64, 64) == (3, 3, 9, 4096, 512)
+    assert tile_grid(16384, 16384, 64, 64)[2] == 65536
+    assert [pack_codec(d) for d in (torch.bfloat16, torch.float8_e4m3fn, torch.float8_e5m2)] == [0, 1, 2]
+    assert [bits_per_value(d) for d in (torch.bfloat16, torch.float8_e4m3fn)] == [15, 7]
+    with pytest.raises(ValueError):
+        TensorBuffer(3, device="cpu", dtype=torch.bfloat16)
+    # vram_size = nnz*vb + T*512 + 4*(T+1) (reference bitsparse.py:88-96), on
+    # a container filled from the oracle
+    x = relu_input((129, 131), 0.5, seed=0)
+    bm, pf, v = O.compress(bits(x), O.BF16)
+    sp = BitsparseTensor(torch.from_numpy(v.view(np.int16)).view(torch.bfloat16),
+                         torch.from_numpy(bm), torch.from_numpy(pf.view(np.int32)).view(torch.uint32),
+                         x.shape, torch.bfloat16, 3, 3, 64, 64)
+    assert sp.vram_size() == v.size * 2 + 9 * 512 + 4 * 10
+    assert int(sp.nnz()) == v.size == int((x.float() > 0).sum())
+    assert not sp.fp8
+    assert "BitsparseTensor" in repr(sp)
+
+
+def test_lib_sparse_alias():
+    import bitsparse_amd
+    bitsparse_amd.install_lib_sparse_alias()
+    import lib_sparse.layers as L
+    from lib_sparse.src.triton_operators import unpack_batch_
+    from lib_sparse.src.functions import dense_to_tilesparse
+    assert L.FFNRelu is bitsparse_amd.layers.FFNRelu
+    assert callable(unpack_batch_) and callable(dense_to_tilesparse)

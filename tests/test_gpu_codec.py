@@ -1,0 +1,305 @@
+"""GPU parity of the HIP codec kernels against the CPU oracle.
+
+Bar: bit-exact for bitmask, prefix, values, decompressed tiles and the
+gradient kernels; at the 16384x16384 size (beyond the oracle's budget)
+size-independent properties are checked with torch ops on the GPU.
+Everything goes through bitsparse_amd's ctypes binding of the C ABI.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests.helpers import all_fp8_patterns, bits, from_bits, preact_input, relu_input, special_bf16
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(1, 1), (64, 64), (128, 128), (129, 131), (200, 70), (5, 300), (256, 8), (320, 1024)]
+SPARSITIES = [0.0, 0.5, 0.9, 1.0]
+
+
+def _bs():
+    import bitsparse_amd.src.functions as F
+    import bitsparse_amd.src.hip_operators as H
+    from bitsparse_amd.bitsparse import TensorBuffer
+    return F, H, TensorBuffer
+
+
+def decompress(sparse):
+    _, H, _ = _bs()
+    M, N = sparse.shape
+    out = torch.empty((M, N), device=sparse.vals.device, dtype=sparse.vals.dtype)
+    return H.unpack_batch_(sparse, out, 0, sparse.grid_n, N, M, sparse.grid_m * sparse.grid_n)
+
+
+def check_sparse(sp, x_cpu, code):
+    bm, pf, v = O.compress(bits(x_cpu), code)
+    assert (bits(sp.bitmask) == bm).all(), "bitmask"
+    assert (bits(sp.prefix) == pf).all(), "prefix"
+    off = int(sp.vals_offset.reshape(-1)[0].item())
+    got = bits(sp.vals)[off:off + v.size]
+    assert (got == v).all(), "vals"
+    return bm, pf, v
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("sparsity", SPARSITIES)
+def test_compress_standalone_bf16(dev, shape, sparsity):
+    F, _, _ = _bs()
+    x = relu_input(shape, sparsity, seed=1)
+    sp = F.dense_to_tilesparse(x.to(dev), None)
+    bm, pf, v = check_sparse(sp, x, O.BF16)
+    assert sp.vals.numel() == v.size
+    d = decompress(sp)
+    assert torch.equal(d.cpu(), x)
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+def test_compress_special_values(dev, shape):
+    F, _, TB = _bs()
+    x = special_bf16(shape, seed=2)
+    sp = F.dense_to_tilesparse(x.to(dev), None)
+    bm, pf, v = check_sparse(sp, x, O.BF16)
+    buf = TB(2 * max(1, x.numel()), device=dev)
+    sp2 = F.dense_to_tilesparse(x.to(dev), None, buf)
+    check_sparse(sp2, x, O.BF16)
+    ref = O.decompress(v, O.BF16, bm, pf, *shape)
+    assert (bits(decompress(sp)) == ref).all()
+    assert (bits(decompress(sp2)) == ref).all()
+
+
+@pytest.mark.parametrize("dt,code", [(torch.float8_e4m3fn, O.E4M3FN), (torch.float8_e5m2, O.E5M2)])
+@pytest.mark.parametrize("shape", [(64, 64), (129, 131), (70, 200), (512, 384)])
+def test_compress_fp8_inputs(dev, dt, code, shape):
+    F, _, TB = _bs()
+    xb = all_fp8_patterns(shape, seed=3)
+    x = from_bits(xb, dt)
+    sp = F.dense_to_tilesparse(x.to(dev), torch.ones((), device=dev))
+    bm, pf, v = check_sparse(sp, x, code)
+    assert (bits(decompress(sp)) == O.decompress(v, code, bm, pf, *shape)).all()
+    buf = TB(x.numel() + 64, device=dev, dtype=dt)
+    sp2 = F.dense_to_tilesparse(x.to(dev), None, buf)
+    check_sparse(sp2, x, code)
+
+
+def test_shared_buffer_decompress_after_all_writes(dev):
+    """validate.py:128-139: several tensors share one TensorBuffer; every
+    tensor is decompressed only after all were written."""
+    F, _, TB = _bs()
+    xs = [relu_input(s, sp, seed=10 + i) for i, (s, sp) in
+          enumerate([(s, sp) for s in [(128, 128), (129, 131)] for sp in SPARSITIES])]
+    cap = sum(x.numel() for x in xs)
+    buf = TB(2 * cap, device=dev)
+    sps = [F.dense_to_tilesparse(x.to(dev), None, buf) for x in xs]
+    total = 0
+    for x, sp in zip(xs, sps):
+        assert sp.vals is buf.vals
+        assert int(sp.vals_offset.item()) == total
+        check_sparse(sp, x, O.BF16)
+        assert torch.equal(decompress(sp).cpu(), x)
+        total += int((x.float() > 0).sum())
+    assert int(buf.offset.item()) == total
+    assert not buf.overflowed()
+    buf.reset_buffer()
+    assert int(buf.offset.item()) == 0
+
+
+def test_buffer_overflow_is_flagged_and_contained(dev):
+    F, _, TB = _bs()
+    x = relu_input((256, 256), 0.0, seed=20)          # 65536 positives
+    buf = TB(2 * 1000, device=dev)
+    guard = torch.full((1000 + 4096,), 0x1234, dtype=torch.int16, device=dev).view(torch.bfloat16)
+    buf.vals = guard[:1000]                           # capacity 1000, guard region behind it
+    sp = F.dense_to_tilesparse(x.to(dev), None, buf)
+    torch.cuda.synchronize()
+    assert buf.overflowed()
+    assert (guard[1000:].view(torch.int16) == 0x1234).all()
+    v = O.compress(bits(x), O.BF16)[2]
+    assert (bits(guard[:1000]) == v[:1000]).all()
+
+
+def test_empty_inputs(dev):
+    F, _, TB = _bs()
+    for shape in [(0, 5), (5, 0), (0, 0)]:
+        x = torch.zeros(shape, dtype=torch.bfloat16, device=dev)
+        sp = F.dense_to_tilesparse(x, None)
+        assert sp.prefix.numel() == 1 and int(sp.prefix[0].item()) == 0
+        assert sp.vals.numel() == 0
+        buf = TB(64, device=dev)
+        sp = F.dense_to_tilesparse(x, None, buf)
+        assert int(buf.offset.item()) == 0
+
+
+def test_c1_round_trip_bit_exact(dev):
+    """4096x4096 bf16, pre-activation N(0,1) seed 0, ReLU, compress,
+    decompress; bit-exact against the oracle."""
+    F, _, TB = _bs()
+    x = torch.randn((4096, 4096), generator=torch.Generator().manual_seed(0)).to(torch.bfloat16).relu()
+    bm, pf, v = O.compress(bits(x), O.BF16)
+    buf = TB(2 * x.numel(), device=dev)
+    sp = F.dense_to_tilesparse(x.to(dev), None, buf)
+    assert (bits(sp.bitmask) == bm).all() and (bits(sp.prefix) == pf).all()
+    assert (bits(sp.vals)[:v.size] == v).all()
+    assert torch.equal(decompress(sp).cpu(), x)
+    sp2 = F.dense_to_tilesparse(x.to(dev), None)
+    assert (bits(sp2.vals) == v).all()
+
+
+def _torch_tile_bitmask(x: torch.Tensor) -> torch.Tensor:
+    """Bitmask of a [M, N] GPU tensor (M, N multiples of 64) with torch ops."""
+    M, N = x.shape
+    pos = (x.float() > 0).to(torch.uint8)
+    t = pos.reshape(M // 64, 64, N // 64, 64).permute(0, 2, 1, 3).reshape(-1, 512, 8)
+    w = (2 ** torch.arange(8, device=x.device, dtype=torch.int32)).to(torch.uint8)
+    return (t * w).sum(-1, dtype=torch.int32).to(torch.uint8).reshape(-1)
+
+
+@pytest.mark.parametrize("mu", [0.0, -2.3263])
+def test_c3_size_properties(dev, mu):
+    """configs[2] shape 16384x16384 at 50% and 99% zeros: exact round trip,
+    bitmask = torch's tile bitmask, prefix = scan of per-tile counts."""
+    F, _, TB = _bs()
+    M = N = 16384
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = (torch.randn((M, N), device=dev, generator=g) + mu).to(torch.bfloat16).relu_()
+    buf = TB(2 * M * N, device=dev)
+    sp = F.dense_to_tilesparse(x, None, buf)
+    d = decompress(sp)
+    assert torch.equal(d, x)
+    assert torch.equal(sp.bitmask, _torch_tile_bitmask(x))
+    counts = (x > 0).reshape(M // 64, 64, N // 64, 64).sum((1, 3), dtype=torch.int64).reshape(-1)
+    pref = torch.zeros(counts.numel() + 1, dtype=torch.int64, device=dev)
+    pref[1:] = counts.cumsum(0)
+    assert torch.equal(sp.prefix.to(torch.int64), pref)
+    assert int(buf.offset.item()) == int(pref[-1].item())
+    vals_ref = x.reshape(M // 64, 64, N // 64, 64).permute(0, 2, 1, 3).reshape(-1)
+    vals_ref = vals_ref[vals_ref > 0]
+    assert torch.equal(sp.vals[:vals_ref.numel()], vals_ref)
+
+
+@pytest.mark.parametrize("shape", [(129, 131), (300, 200), (448, 512)])
+def test_unpack_row_batches(dev, shape):
+    F, H, _ = _bs()
+    x = relu_input(shape, 0.5, seed=30)
+    sp = F.dense_to_tilesparse(x.to(dev), None)
+    M, N = shape
+    gn = sp.grid_n
+    bm, pf, v = O.compress(bits(x), O.BF16)
+    for first in range(sp.grid_m):
+        for nrows in (1, 2):
+            if first + nrows > sp.grid_m:
+                continue
+            rows = min(nrows * 64, M - first * 64)
+            out = torch.empty((rows, N), dtype=torch.bfloat16, device=dev)
+            H.unpack_batch_(sp, out, first, gn, N, rows, nrows * gn)
+            ref = O.unpack(v, O.BF16, bm, pf, 0, first, gn, N, rows, nrows * gn)
+            assert (bits(out) == ref).all()
+
+
+def test_relu_grad(dev):
+    F, H, _ = _bs()
+    for shape in [(129, 131), (512, 768), (64, 8)]:
+        x = special_bf16(shape, seed=40)
+        g = preact_input(shape, seed=41)
+        sp = F.dense_to_tilesparse(x.to(dev), None)
+        gd = g.to(dev)
+        out = H.mask_with_bitmask_(gd, sp)
+        assert out is gd
+        bm = O.compress(bits(x), O.BF16)[0]
+        assert (bits(out) == O.relu_grad(bits(g), bm)).all()
+
+
+@pytest.mark.parametrize("shape", [(129, 131), (256, 512), (64, 24)])
+def test_relu2_grad_bf16(dev, shape):
+    F, H, _ = _bs()
+    r = preact_input(shape, seed=50).relu()
+    g = preact_input(shape, seed=51)
+    sp = F.dense_to_tilesparse(r.to(dev), None)
+    out = H.relu2_grad_sparse_(g.to(dev), sp)
+    bm, pf, v = O.compress(bits(r), O.BF16)
+    assert (bits(out) == O.relu2_grad(bits(g), v, O.BF16, bm, pf)).all()
+
+
+@pytest.mark.parametrize("shape", [(129, 131), (256, 512)])
+def test_relu2_grad_and_square_fp8_scaled(dev, shape):
+    F, H, TB = _bs()
+    xb = all_fp8_patterns(shape, seed=52)
+    xb[(xb & 0x7F) == 0x7F] = 0x10            # NaN-free payloads
+    x = from_bits(xb, torch.float8_e4m3fn)
+    g = preact_input(shape, seed=53)
+    s = torch.tensor(0.0123, device=dev)
+    buf = TB(x.numel() + 100, device=dev, dtype=torch.float8_e4m3fn)
+    buf.offset.fill_(37)
+    sp = F.dense_to_tilesparse(x.to(dev), s, buf)
+    bm, pf, v = O.compress(xb, O.E4M3FN)
+    out = H.relu2_grad_sparse_(g.to(dev), sp)
+    assert (bits(out) == O.relu2_grad(bits(g), v, O.E4M3FN, bm, pf, scale=0.0123)).all()
+    sq = torch.empty(shape, dtype=torch.bfloat16, device=dev)
+    H.unpack_relu2_batch_(sp, sq, 0, sp.grid_n, shape[1], shape[0], sp.grid_m * sp.grid_n)
+    ref = O.decompress(v, O.E4M3FN, bm, pf, *shape, square=True)
+    ref = O.bf16_mul_scalar_tensor(ref, float(np.float32(0.0123) * np.float32(0.0123)))
+    assert (bits(sq) == ref).all()
+
+
+def test_unpack_relu2_bf16(dev):
+    F, H, _ = _bs()
+    r = relu_input((129, 131), 0.5, seed=54)
+    sp = F.dense_to_tilesparse(r.to(dev), None)
+    sq = torch.empty((129, 131), dtype=torch.bfloat16, device=dev)
+    H.unpack_relu2_batch_(sp, sq, 0, sp.grid_n, 131, 129, sp.grid_m * sp.grid_n)
+    assert torch.equal(sq.cpu(), r.square())
+
+
+def test_torch_scalar_tensor_multiply_semantics(dev):
+    """Pins the oracle's rule for bf16_tensor.mul_(fp32 0-d device tensor)
+    (triton_operators.py:160-161, :200-201) against torch on the GPU."""
+    x = preact_input((257, 129), seed=60)
+    for s in [0.0123, 1.0 / 3.0, 7.77e-5, 3.14159]:
+        st = torch.tensor(s, dtype=torch.float32, device=dev)
+        got = x.to(dev).mul_(st)
+        assert (bits(got) == O.bf16_mul_scalar_tensor(bits(x), s)).all()
+        sq = x.to(dev).mul_(st.square())
+        assert (bits(sq) == O.bf16_mul_scalar_tensor(bits(x), float(np.float32(s) * np.float32(s)))).all()
+
+
+@pytest.mark.parametrize("shape", [(1, 1), (129, 131), (1000, 4096)])
+def test_to_fp8(dev, shape):
+    from bitsparse_amd.fp8 import to_fp8
+    x = preact_input(shape, seed=70) * 5
+    q, s = to_fp8(x.to(dev))
+    qo, so = O.to_fp8(bits(x))
+    assert s.dtype == torch.float32 and float(s.item()) == so
+    assert (bits(q) == qo).all()
+    qt, st = to_fp8(x.to(dev).T)
+    assert qt.shape == x.T.shape and (bits(qt.contiguous()) == qo.T).all()
+
+
+@pytest.mark.parametrize("shape", [(129, 131), (512, 1024)])
+def test_quantize_and_compress(dev, shape):
+    F, _, TB = _bs()
+    x = preact_input(shape, seed=71).relu() * 3
+    qo, so = O.to_fp8(bits(x))
+    bm, pf, v = O.compress(qo, O.E4M3FN)
+    for buf in (None, TB(x.numel(), device=dev, dtype=torch.float8_e4m3fn)):
+        q, s, sp = F.quantize_and_compress(x.to(dev), buf)
+        assert float(s.item()) == so
+        assert (bits(q) == qo).all()
+        assert (bits(sp.bitmask) == bm).all() and (bits(sp.prefix) == pf).all()
+        assert (bits(sp.vals)[:v.size] == v).all()
+
+
+def test_tile_pack_and_compact_vals_api(dev):
+    """The reference's lower-level names keep their signatures."""
+    from bitsparse_amd.src.triton_operators import compact_vals, tile_pack
+    x = relu_input((129, 131), 0.5, seed=80)
+    xd = x.to(dev)
+    T = 3 * 3
+    counts = torch.empty(T, dtype=torch.int32, device=dev)
+    bmask = torch.empty(T * 512, dtype=torch.uint8, device=dev)
+    tile_pack(xd, counts, bmask, 129, 131, 3, 3, 64, 64, 4096, 512)
+    bm, cnt = O.tile_pack(bits(x), O.BF16)
+    assert (bits(bmask) == bm).all() and (counts.cpu().numpy() == cnt).all()
+    pf = torch.zeros(T + 1, dtype=torch.uint32, device=dev)
+    torch.cumsum(counts, 0, out=pf.view(torch.int32)[1:])
+    vals, off = compact_vals(xd, bmask, pf, None, None, 129, 131, 3, T, 64, 64, 4096, False)
+    assert (bits(vals) == O.compress(bits(x), O.BF16)[2]).all() and int(off.item()) == 0
