@@ -14,7 +14,9 @@ import threading
 import torch
 
 LIB_NAME = "libbitsparse_hip.so"
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+# BITSPARSE_HIP_LIB points at another build of the same sources (tuning sweeps)
+LIB_PATH = os.environ.get("BITSPARSE_HIP_LIB") or os.path.join(
+    os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 ABI_VERSION = 1
 
 BS_OK = 0
@@ -135,10 +137,14 @@ class Workspace:
 
     def ensure(self, nbytes: int) -> None:
         if self.buf.numel() < nbytes:
-            # grow geometrically; a new buffer starts zeroed, epochs restart
+            # grow geometrically; the old contents (amax slot, status words of
+            # earlier epochs) move along and the new tail is zero, so epochs
+            # already handed out stay meaningful
             size = max(nbytes, 2 * self.buf.numel(), 1 << 16)
-            self.buf = torch.zeros(size, dtype=torch.uint8, device=self.device)
-            self.epoch = 0
+            new = torch.zeros(size, dtype=torch.uint8, device=self.device)
+            if self.buf.numel():
+                new[:self.buf.numel()].copy_(self.buf)
+            self.buf = new
 
     def next_epoch(self) -> int:
         self.epoch += 1

@@ -27,12 +27,15 @@ def hipcc() -> str:
     return os.path.join(rocm, "bin", "hipcc")
 
 
-def build_library(verbose: bool = False) -> str:
-    """Compile every HIP source into bitsparse_amd/libbitsparse_hip.so."""
-    out = os.path.join(PKG, "libbitsparse_hip.so")
+def build_library(verbose: bool = False, out: str | None = None,
+                  defines: tuple[str, ...] = ()) -> str:
+    """Compile every HIP source into bitsparse_amd/libbitsparse_hip.so
+    (or `out`, with extra -D `defines`, for tuning builds)."""
+    out = out or os.path.join(PKG, "libbitsparse_hip.so")
     tmp = out + ".tmp"
     srcs = [os.path.join(CSRC, s) for s in SOURCES if os.path.exists(os.path.join(CSRC, s))]
-    cmd = [hipcc()] + HIPCC_FLAGS + ["-I", INCLUDE, "-I", CSRC, "-o", tmp] + srcs
+    cmd = ([hipcc()] + HIPCC_FLAGS + [f"-D{d}" for d in defines] +
+           ["-I", INCLUDE, "-I", CSRC, "-o", tmp] + srcs)
     if verbose:
         print(" ".join(cmd), file=sys.stderr)
     res = subprocess.run(cmd, capture_output=True, text=True)

@@ -16,6 +16,8 @@ template <> struct Raw<1> { using T = uint2; };   // 8 x fp8
 
 constexpr int kThreads = 256;
 
+
+
 // Elements of one chunk as raw bits.
 template <int B>
 __device__ __forceinline__ uint32_t elem(const typename Raw<B>::T& v, int e)
@@ -180,10 +182,10 @@ __device__ __forceinline__ uint32_t chunk_mask(const typename Raw<CompressTraits
     }
 }
 
-// Nonzero count of compress unit q, computed straight from the dense input
-// by one wave (look-back fallback).
+// Nonzero count of compress unit q computed straight from the dense input by
+// one wave (look-back fallback).
 template <int IN_T, bool QUANT, bool VEC, int U>
-__device__ uint32_t unit_count_direct(const CompressArgs& a, uint32_t q, float scale, int lane)
+__device__ uint32_t unit_count_wave(const CompressArgs& a, uint32_t q, float scale, int lane)
 {
     using TR = CompressTraits<IN_T, QUANT>;
     uint32_t t0 = a.tile0 + q * U;
@@ -199,18 +201,158 @@ __device__ uint32_t unit_count_direct(const CompressArgs& a, uint32_t q, float s
     return wave_sum_u32(c);
 }
 
-template <int IN_T, bool QUANT, bool VEC, int MODE, int U>
-__global__ __launch_bounds__(kThreads) void compress_kernel(CompressArgs a)
+__device__ __forceinline__ uint64_t bcast_lane0(uint64_t v)
+{
+    uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// Status of unit q as seen by this lane (units before 0 read as inclusive 0).
+__device__ __forceinline__ uint64_t status_at(const CompressArgs& a, int64_t q)
+{
+    return q >= 0 ? ld_relaxed(&a.status[q]) : pack_status(a.epoch, kFlagInc, 0);
+}
+
+// Decoupled look-back run by one wave.  The wave first polls only the
+// nearest predecessor (one word) until it is published; from then on it walks
+// back with 256-status windows (four coalesced 512-byte loads in flight per
+// round trip), adding aggregates until the nearest inclusive prefix with every
+// status before it published.  The walk speed (256 units per round trip) has
+// to exceed the rate at which units publish aggregates, or the distance to
+// the nearest inclusive prefix keeps growing.  A predecessor that stays
+// unpublished for kLookbackPatienceTicks is counted from the dense input
+// instead, so the loop ends whatever order units are scheduled in.  Returns
+// the exclusive prefix of unit u in every lane.
+#ifndef BS_LOOKBACK_WINDOWS
+#define BS_LOOKBACK_WINDOWS 1
+#endif
+#ifndef BS_LOOKBACK_WINDOW_FIRST
+#define BS_LOOKBACK_WINDOW_FIRST 1
+#endif
+constexpr int kLookbackWindows = BS_LOOKBACK_WINDOWS;   // x 64 statuses per round trip
+
+template <int IN_T, bool QUANT, bool VEC, int U>
+__device__ uint32_t wave_lookback(const CompressArgs& a, uint32_t u, float scale, int lane)
+{
+    uint32_t excl = 0;
+    int64_t pos = (int64_t)u - 1;
+    uint64_t since = wall_clock64();
+    // first round reads the window straight away; only an unpublished status
+    // at the head switches to single-word polling
+    bool head_ready = BS_LOOKBACK_WINDOW_FIRST;
+    while (true) {
+        if (!head_ready) {
+            // nearest unresolved predecessor: one lane polls one word
+            uint64_t s0 = 0;
+            if (lane == 0) s0 = status_at(a, pos);
+            s0 = bcast_lane0(s0);
+            const uint32_t f0 = (uint32_t)(s0 >> 32) & 3u;
+            if ((uint32_t)(s0 >> 34) != a.epoch || f0 == 0u) {
+                if (wall_clock64() - since > kLookbackPatienceTicks) {
+                    excl += unit_count_wave<IN_T, QUANT, VEC, U>(a, (uint32_t)pos, scale, lane);
+                    if (lane == 0 && a.fallbacks) atomicAdd(a.fallbacks, 1u);
+                    pos -= 1;
+                    if (pos < 0) break;
+                    since = wall_clock64();
+                    continue;
+                }
+                __builtin_amdgcn_s_sleep(4);
+                continue;
+            }
+            if (f0 == (uint32_t)kFlagInc) {
+                excl += (uint32_t)s0;
+                break;
+            }
+        }
+        // window of kLookbackWindows x 64 statuses behind pos, all in flight
+        uint64_t sw[kLookbackWindows];
+#pragma unroll
+        for (int w = 0; w < kLookbackWindows; w++) sw[w] = status_at(a, pos - 64 * w - lane);
+        bool done = false;
+        int consumed = 0;
+#pragma unroll
+        for (int w = 0; w < kLookbackWindows; w++) {
+            const uint64_t s = sw[w];
+            const uint32_t val = (uint32_t)s;
+            const uint32_t flag = (uint32_t)(s >> 32) & 3u;
+            const bool valid = (uint32_t)(s >> 34) == a.epoch && flag != 0u;
+            const uint64_t notv = ~__ballot(valid);
+            const uint64_t incm = __ballot(valid && flag == (uint32_t)kFlagInc);
+            const int fi = notv ? __ffsll((unsigned long long)notv) - 1 : 64;
+            const int fc = incm ? __ffsll((unsigned long long)incm) - 1 : 64;
+            if (fc < fi) {
+                excl += wave_sum_u32(lane <= fc ? val : 0u);
+                done = true;
+                break;
+            }
+            excl += wave_sum_u32(lane < fi ? val : 0u);
+            consumed += fi;
+            if (fi < 64) break;
+        }
+        if (done) break;
+        pos -= consumed;
+        // an unpublished status stopped the window: go back to polling it
+        head_ready = consumed == 64 * kLookbackWindows;
+        if (consumed > 0) since = wall_clock64();
+    }
+    return excl;
+}
+
+// 16 bytes of LDS starting at byte offset `off` (any alignment, off >= 0),
+// built from two aligned 16-byte reads and byte funnel shifts.
+__device__ __forceinline__ uint4 lds_read16_at(const uint8_t* s, int off)
+{
+    const int base = off & ~15, sh = off & 15;
+    const uint4 lo = *reinterpret_cast<const uint4*>(s + base);
+    if (sh == 0) return lo;
+    const uint4 hi = *reinterpret_cast<const uint4*>(s + base + 16);
+    const uint32_t w0 = lo.x, w1 = lo.y, w2 = lo.z, w3 = lo.w, w4 = hi.x, w5 = hi.y, w6 = hi.z,
+                   w7 = hi.w;
+    const uint32_t bs = (uint32_t)(sh & 3);
+    uint4 r;
+    switch (sh >> 2) {
+    case 0:
+        r.x = __builtin_amdgcn_alignbyte(w1, w0, bs); r.y = __builtin_amdgcn_alignbyte(w2, w1, bs);
+        r.z = __builtin_amdgcn_alignbyte(w3, w2, bs); r.w = __builtin_amdgcn_alignbyte(w4, w3, bs);
+        break;
+    case 1:
+        r.x = __builtin_amdgcn_alignbyte(w2, w1, bs); r.y = __builtin_amdgcn_alignbyte(w3, w2, bs);
+        r.z = __builtin_amdgcn_alignbyte(w4, w3, bs); r.w = __builtin_amdgcn_alignbyte(w5, w4, bs);
+        break;
+    case 2:
+        r.x = __builtin_amdgcn_alignbyte(w3, w2, bs); r.y = __builtin_amdgcn_alignbyte(w4, w3, bs);
+        r.z = __builtin_amdgcn_alignbyte(w5, w4, bs); r.w = __builtin_amdgcn_alignbyte(w6, w5, bs);
+        break;
+    default:
+        r.x = __builtin_amdgcn_alignbyte(w4, w3, bs); r.y = __builtin_amdgcn_alignbyte(w5, w4, bs);
+        r.z = __builtin_amdgcn_alignbyte(w6, w5, bs); r.w = __builtin_amdgcn_alignbyte(w7, w6, bs);
+        break;
+    }
+    return r;
+}
+
+// Fused compress of one unit (U consecutive tiles) per workgroup of NT
+// threads.  Thread i owns chunks h*NT + i (h < 512/NT) of every tile of the
+// unit; all of the unit's loads are issued before anything waits.
+template <int IN_T, bool QUANT, bool VEC, int MODE, int U, int NT>
+__global__ __launch_bounds__(NT) void compress_kernel(CompressArgs a)
 {
     using TR = CompressTraits<IN_T, QUANT>;
     constexpr int INB = TR::INB, OUTB = TR::OUTB;
-    constexpr int EPS = 16 / OUTB;   // elements per 16-byte store slot
+    constexpr int EPS = 16 / OUTB;          // elements per 16-byte store slot
+    constexpr int CH = kChunksPerTile / NT; // chunks per tile per thread
+    constexpr int NW = NT / kWave;
     using RawIn = typename Raw<INB>::T;
     using RawOut = typename Raw<OUTB>::T;
+    static_assert(CH * NT == kChunksPerTile, "NT must divide 512");
 
-    __shared__ uint32_t s_wtot[U][2][4];
-    __shared__ uint32_t s_excl;
-    __shared__ __align__(16) uint8_t s_vals[MODE == MODE_COUNT ? 16 : U * kTileNumel * OUTB + 16];
+    constexpr int NSLOT = U * CH * NW;      // per-wave partial counts, flat chunk order
+    static_assert(NSLOT <= 64, "one wave scans the per-wave counts");
+    __shared__ uint32_t s_wtot[NSLOT];
+    __shared__ uint32_t s_pre[NSLOT + 1];   // exclusive prefix of s_wtot; [NSLOT] = unit total
+    __shared__ uint32_t s_lb[1];
+    __shared__ __align__(16) uint8_t s_vals[MODE == MODE_COUNT ? 16 : U * kTileNumel * OUTB + 32];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const uint32_t u = blockIdx.x;
@@ -219,149 +361,135 @@ __global__ __launch_bounds__(kThreads) void compress_kernel(CompressArgs a)
 
     float scale = 1.0f;
     if constexpr (QUANT) scale = scale_from_slot(a.amax_slot, a.amax_epoch);
+    // the cursor is independent of everything else: fetch it first
+    int64_t start = 0;
+    if (a.offset_in) start = *a.offset_in;
+    if (a.align8) start = (start + 7) & ~(int64_t)7;
 
     // ---- load every chunk of the unit first (all loads in flight together)
-    RawIn d[U][2];
+    RawIn d[U][CH];
 #pragma unroll
     for (int j = 0; j < U; j++)
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
+        for (int h = 0; h < CH; h++) {
             d[j][h] = RawIn{};
             if (j < ntiles) {
                 int64_t row, col0;
-                chunk_pos(t0 + j, a.grid_n, h * 256 + tid, row, col0);
+                chunk_pos(t0 + j, a.grid_n, h * NT + tid, row, col0);
                 d[j][h] = load_chunk<INB, VEC>(a.dense, a.M, a.N, row, col0);
             }
         }
-    uint32_t vm[U][2];
+    uint32_t vm[U][CH];
     if constexpr (MODE == MODE_VALS) {
 #pragma unroll
         for (int j = 0; j < U; j++)
 #pragma unroll
-            for (int h = 0; h < 2; h++)
-                vm[j][h] = j < ntiles ? a.bitmask[(size_t)(t0 + j) * kTileBytes + h * 256 + tid] : 0u;
+            for (int h = 0; h < CH; h++)
+                vm[j][h] = j < ntiles ? a.bitmask[(size_t)(t0 + j) * kTileBytes + h * NT + tid] : 0u;
     }
 
     // ---- masks, optional quantised copy, bitmask bytes
-    RawOut o[U][2];
-    uint32_t m[U][2];
+    RawOut o[U][CH];
+    uint32_t m[U][CH];
 #pragma unroll
     for (int j = 0; j < U; j++)
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
+        for (int h = 0; h < CH; h++) {
             m[j][h] = chunk_mask<IN_T, QUANT>(d[j][h], o[j][h], scale);
             if (j < ntiles) {
                 if constexpr (QUANT) {
                     if (a.dense_q_out != nullptr) {
                         int64_t row, col0;
-                        chunk_pos(t0 + j, a.grid_n, h * 256 + tid, row, col0);
+                        chunk_pos(t0 + j, a.grid_n, h * NT + tid, row, col0);
                         store_chunk<1, VEC>(a.dense_q_out, a.M, a.N, row, col0, o[j][h]);
                     }
                 }
                 if constexpr (MODE != MODE_VALS)
-                    a.bitmask[(size_t)(t0 + j) * kTileBytes + h * 256 + tid] = (uint8_t)m[j][h];
+                    a.bitmask[(size_t)(t0 + j) * kTileBytes + h * NT + tid] = (uint8_t)m[j][h];
             }
             if constexpr (MODE == MODE_VALS) m[j][h] = vm[j][h];
         }
 
-    // ---- in-tile ranks: ballot scan per wave, wave totals through LDS
-    uint32_t ex[U][2];
+    // ---- ranks inside each chunk group: ballot scan per wave, totals via LDS
+    uint32_t ex[U][CH];
 #pragma unroll
     for (int j = 0; j < U; j++)
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
+        for (int h = 0; h < CH; h++) {
             uint32_t tot;
             wave_scan_count(__popc(m[j][h]), ex[j][h], tot);
-            if (lane == 0) s_wtot[j][h][wave] = tot;
+            if (lane == 0) s_wtot[(j * CH + h) * NW + wave] = tot;
         }
     __syncthreads();
-
-    uint32_t lr[U][2];   // unit-local rank of each chunk's first set element
-    uint32_t tile_base[U];
+    // wave 0 turns the per-wave counts into unit-local offsets and publishes
+    // the unit aggregate right away
     uint32_t unit_total = 0;
+    if (wave == 0) {
+        const uint32_t v = lane < NSLOT ? s_wtot[lane] : 0u;
+        uint32_t x = v;
 #pragma unroll
-    for (int j = 0; j < U; j++) {
-        tile_base[j] = unit_total;
-        uint32_t h0 = 0, h0w = 0, h1w = 0, h1 = 0;
-#pragma unroll
-        for (int w = 0; w < 4; w++) {
-            uint32_t a0 = s_wtot[j][0][w], a1 = s_wtot[j][1][w];
-            h0 += a0;
-            h1 += a1;
-            if (w < wave) { h0w += a0; h1w += a1; }
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t y = __shfl_up(x, o, 64);
+            if (lane >= o) x += y;
         }
-        lr[j][0] = unit_total + h0w + ex[j][0];
-        lr[j][1] = unit_total + h0 + h1w + ex[j][1];
-        unit_total += h0 + h1;
+        unit_total = __shfl(x, 63, 64);
+        if (lane < NSLOT) s_pre[lane] = x - v;
+        if (lane == 0) s_pre[NSLOT] = unit_total;
+        if constexpr (MODE != MODE_VALS) {
+            if (lane == 0)
+                st_relaxed(&a.status[u], pack_status(a.epoch, u == 0 ? kFlagInc : kFlagAgg, unit_total));
+        }
     }
+    __syncthreads();
+    unit_total = s_pre[NSLOT];
 
-    // ---- unit start in the value stream
+    // ---- unit start in the value stream (wave 0) while every wave stages its
+    // values in LDS at unit-local positions
+    auto stage = [&]() {
+        if constexpr (MODE != MODE_COUNT) {
+#pragma unroll
+            for (int j = 0; j < U; j++)
+#pragma unroll
+                for (int h = 0; h < CH; h++) {
+                    const uint32_t mm = m[j][h];
+                    uint32_t r = s_pre[(j * CH + h) * NW + wave] + ex[j][h];
+#pragma unroll
+                    for (int e = 0; e < 8; e++) {
+                        if ((mm >> e) & 1u) {
+                            if constexpr (OUTB == 2)
+                                reinterpret_cast<uint16_t*>(s_vals)[r] = (uint16_t)elem<2>(o[j][h], e);
+                            else
+                                s_vals[r] = (uint8_t)elem<1>(o[j][h], e);
+                            r++;
+                        }
+                    }
+                }
+        }
+    };
     uint32_t excl;
     if constexpr (MODE == MODE_VALS) {
         excl = a.prefix[t0] - a.prefix[a.tile0];
+        stage();
+        __syncthreads();
     } else {
         if (wave == 0) {
             if (u == 0) {
                 excl = 0;
-                if (lane == 0) st_relaxed(&a.status[0], pack_status(a.epoch, kFlagInc, unit_total));
             } else {
-                if (lane == 0) st_relaxed(&a.status[u], pack_status(a.epoch, kFlagAgg, unit_total));
-                // decoupled look-back over a 64-unit window per step
-                excl = 0;
-                int64_t pos = (int64_t)u - 1;
-                uint64_t since = wall_clock64();
-                while (true) {
-                    int64_t q = pos - lane;
-                    uint64_t s = q >= 0 ? ld_relaxed(&a.status[q]) : pack_status(a.epoch, kFlagInc, 0);
-                    uint32_t val = (uint32_t)s;
-                    uint32_t flag = (uint32_t)(s >> 32) & 3u;
-                    bool valid = (uint32_t)(s >> 34) == a.epoch && flag != 0u;
-                    bool inc = valid && flag == (uint32_t)kFlagInc;
-                    uint64_t notv = ~__ballot(valid);
-                    uint64_t incm = __ballot(inc);
-                    int fi = notv ? __ffsll((unsigned long long)notv) - 1 : 64;
-                    int fc = incm ? __ffsll((unsigned long long)incm) - 1 : 64;
-                    if (fc < fi) {
-                        excl += wave_sum_u32(lane <= fc ? val : 0u);
-                        break;
-                    }
-                    if (fi > 0) {
-                        excl += wave_sum_u32(lane < fi ? val : 0u);
-                        pos -= fi;
-                        since = wall_clock64();
-                        continue;
-                    }
-                    if (wall_clock64() - since > kLookbackPatienceTicks) {
-                        excl += unit_count_direct<IN_T, QUANT, VEC, U>(a, (uint32_t)pos, scale, lane);
-                        if (lane == 0 && a.fallbacks) atomicAdd(a.fallbacks, 1u);
-                        pos -= 1;
-                        since = wall_clock64();
-                        continue;
-                    }
-                    __builtin_amdgcn_s_sleep(2);
-                }
+                excl = wave_lookback<IN_T, QUANT, VEC, U>(a, u, scale, lane);
                 if (lane == 0) st_relaxed(&a.status[u], pack_status(a.epoch, kFlagInc, excl + unit_total));
             }
-            if (lane == 0) s_excl = excl;
+            if (lane == 0) s_lb[0] = excl;
         }
+        stage();
         __syncthreads();
-        excl = s_excl;
+        excl = s_lb[0];
     }
 
-    int64_t start = 0;
-    if (a.offset_in) start = *a.offset_in;
-    if (a.align8) start = (start + 7) & ~(int64_t)7;
-
     if constexpr (MODE != MODE_VALS) {
-        if (tid < ntiles) {
-            uint32_t tb = 0;
-#pragma unroll
-            for (int j = 0; j < U; j++)
-                if (j == tid) tb = tile_base[j];
-            a.prefix[t0 + tid] = excl + tb;
-        }
+        if (tid < ntiles) a.prefix[t0 + tid] = excl + s_pre[tid * CH * NW];
         if (t0 + ntiles == a.tend && tid == 0) {
-            a.prefix[a.T] = excl + unit_total;
+            a.prefix[a.tend] = excl + unit_total;
             int64_t end = start + (int64_t)(excl + unit_total);
             if (a.offset_out) *a.offset_out = end;
             if (a.start_out) *a.start_out = start;
@@ -381,42 +509,23 @@ __global__ __launch_bounds__(kThreads) void compress_kernel(CompressArgs a)
         if (MODE == MODE_VALS && a.err && g0 + (int64_t)unit_total > a.vals_capacity && tid == 0)
             atomicOr(a.err, 1);
         const int p = (int)((((uintptr_t)a.vals) / OUTB + (uint64_t)g0) % EPS);
-        // stage the run in LDS at its 16-byte phase
-#pragma unroll
-        for (int j = 0; j < U; j++)
-#pragma unroll
-            for (int h = 0; h < 2; h++) {
-                uint32_t mm = m[j][h];
-                uint32_t r = (uint32_t)p + lr[j][h];
-#pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    if ((mm >> e) & 1u) {
-                        if constexpr (OUTB == 2)
-                            reinterpret_cast<uint16_t*>(s_vals)[r] = (uint16_t)elem<2>(o[j][h], e);
-                        else
-                            s_vals[r] = (uint8_t)elem<1>(o[j][h], e);
-                        r++;
-                    }
-                }
-            }
-        __syncthreads();
         const int nslots = (p + (int)unit_total + EPS - 1) / EPS;
-        for (int s = tid; s < nslots; s += kThreads) {
+        for (int s = tid; s < nslots; s += NT) {
             const int64_t e0 = g0 - p + (int64_t)s * EPS;   // element index of slot start
-            int lo = max(0, p - s * EPS);
-            int hi = min(EPS, p + (int)unit_total - s * EPS);
-            int64_t cap_hi = a.vals_capacity - e0;
+            const int l0 = s * EPS - p;                      // staged index of slot start
+            int lo = max(0, -l0);
+            int hi = min(EPS, (int)unit_total - l0);
+            const int64_t cap_hi = a.vals_capacity - e0;
             if (cap_hi < hi) hi = (int)max<int64_t>(cap_hi, 0);
             if (lo == 0 && hi == EPS) {
-                *reinterpret_cast<uint4*>(a.vals + e0 * OUTB) =
-                    *reinterpret_cast<const uint4*>(s_vals + s * 16);
+                *reinterpret_cast<uint4*>(a.vals + e0 * OUTB) = lds_read16_at(s_vals, l0 * OUTB);
             } else {
                 for (int e = lo; e < hi; e++) {
                     if constexpr (OUTB == 2)
                         reinterpret_cast<uint16_t*>(a.vals)[e0 + e] =
-                            reinterpret_cast<const uint16_t*>(s_vals)[s * EPS + e];
+                            reinterpret_cast<const uint16_t*>(s_vals)[l0 + e];
                     else
-                        a.vals[e0 + e] = s_vals[s * EPS + e];
+                        a.vals[e0 + e] = s_vals[l0 + e];
                 }
             }
         }
@@ -776,7 +885,15 @@ __global__ __launch_bounds__(kThreads) void relu_grad_kernel(uint8_t* grad, int6
 // ===========================================================================
 // host launchers
 // ===========================================================================
-constexpr int kCompressU = 4;
+// compress unit: tiles per workgroup and workgroup size
+#ifndef BS_COMPRESS_U
+#define BS_COMPRESS_U 8
+#endif
+#ifndef BS_COMPRESS_THREADS
+#define BS_COMPRESS_THREADS 512
+#endif
+constexpr int kCompressU = BS_COMPRESS_U;
+constexpr int kCompressThreads = BS_COMPRESS_THREADS;
 constexpr int kGatherU = 2;
 constexpr int kMaskU = 4;
 
@@ -788,11 +905,11 @@ static hipError_t launch_compress_mode(const CompressArgs& a, bool vec, hipStrea
 {
     const uint32_t units = (a.tend - a.tile0 + kCompressU - 1) / kCompressU;
     if (vec)
-        hipLaunchKernelGGL((compress_kernel<IN_T, QUANT, true, MODE, kCompressU>), dim3(units),
-                           dim3(kThreads), 0, st, a);
+        hipLaunchKernelGGL((compress_kernel<IN_T, QUANT, true, MODE, kCompressU, kCompressThreads>),
+                           dim3(units), dim3(kCompressThreads), 0, st, a);
     else
-        hipLaunchKernelGGL((compress_kernel<IN_T, QUANT, false, MODE, kCompressU>), dim3(units),
-                           dim3(kThreads), 0, st, a);
+        hipLaunchKernelGGL((compress_kernel<IN_T, QUANT, false, MODE, kCompressU, kCompressThreads>),
+                           dim3(units), dim3(kCompressThreads), 0, st, a);
     return hipGetLastError();
 }
 
