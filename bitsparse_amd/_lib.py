@@ -48,12 +48,16 @@ _SIGNATURES = {
     "bs_relu2_grad": [_vp, _i64, _i64, _vp, _int, _i64, _vp, _vp, _vp, _f32, _vp, _vp],
     "bs_amax": [_vp, _i64, _vp, _i64, _u32, _vp],
     "bs_quantize_e4m3fn": [_vp, _i64, _vp, _vp, _vp, _i64, _u32, _vp],
+    "bs_gemm_compressed_b_workspace_bytes": [_i64, _i64, _i64],
+    "bs_gemm_compressed_b": [_vp, _i64, _i64, _i64, _vp, _int, _i64, _vp, _vp, _vp, _i64, _int, _f32,
+                             _vp, _vp, _vp, _i64, _vp],
     "bs_workspace_amax_slot": [_vp, _i64],
     "bs_workspace_fallback_counter": [_vp, _i64],
 }
 _RESTYPES = {
     "bs_last_error": ctypes.c_char_p,
     "bs_compress_workspace_bytes": _i64,
+    "bs_gemm_compressed_b_workspace_bytes": _i64,
     "bs_workspace_amax_slot": _vp,
     "bs_workspace_fallback_counter": _vp,
 }

@@ -1,16 +1,48 @@
-"""Host side of the reconstruct-into-LDS MFMA GEMM (C = A @ decode(B)).
+"""Host side of the reconstruct-into-LDS MFMA GEMM (``bs_gemm_compressed_b``).
 
-Placeholder until the kernel lands: ``supports`` returns False so callers
-take the decompress + library GEMM path.
+``gemm_compressed_b(A, B_sparse, square)`` computes ``A @ B`` (or
+``A @ (k * B^2)``) with B a BitsparseTensor decoded tile by tile into LDS by
+the kernel; it replaces the decompress-to-HBM + GEMM of reference
+lib_sparse/src/sparse_matmul.py:24-28 / :109-113.
 """
 from __future__ import annotations
 
+import torch
 from torch import Tensor
+
+from .. import _lib
+from .._lib import check, ptr, stream_handle
+from ..config import RELU2_SCALE
 
 
 def supports(A: Tensor, B_sparse, square: bool) -> bool:
-    return False
+    """Shapes / dtypes the kernel handles: bf16 A on the GPU; B stored as
+    bf16, or fp8 when the operand is the ReLU^2 square."""
+    if not A.is_cuda or A.dim() != 2 or A.dtype != torch.bfloat16 or B_sparse.pack_sbit:
+        return False
+    if A.shape[1] != B_sparse.shape[0]:
+        return False
+    vdt = B_sparse.vals.dtype
+    if vdt == torch.bfloat16:
+        return True
+    return square and vdt in (torch.float8_e4m3fn, torch.float8_e5m2)
 
 
 def gemm_compressed_b(A: Tensor, B_sparse, square: bool) -> Tensor:
-    raise NotImplementedError("reconstruct-into-LDS GEMM not built")
+    from .hip_operators import dtype_code
+    if not supports(A, B_sparse, square):
+        raise ValueError("gemm_compressed_b: unsupported operand combination")
+    K, N = B_sparse.shape
+    A = A.contiguous()                      # [M, K], k contiguous
+    M = A.shape[0]
+    L = _lib.load()
+    C = torch.empty((M, N), device=A.device, dtype=torch.bfloat16)
+    need = L.bs_gemm_compressed_b_workspace_bytes(M, N, K)
+    ws = torch.empty(max(need, 0), device=A.device, dtype=torch.uint8) if need > 0 else None
+    scale = B_sparse.scale if (square and B_sparse.scale is not None) else None
+    check(L.bs_gemm_compressed_b(
+        A.data_ptr(), M, K, A.stride(0), B_sparse.vals.data_ptr(), dtype_code(B_sparse.vals.dtype),
+        B_sparse.vals.numel(), B_sparse.bitmask.data_ptr(), B_sparse.prefix.data_ptr(),
+        B_sparse.vals_offset.data_ptr(), N, int(square), float(RELU2_SCALE), ptr(scale),
+        C.data_ptr(), ptr(ws), need, stream_handle(A.device)), "bs_gemm_compressed_b")
+    return C

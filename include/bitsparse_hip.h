@@ -175,6 +175,26 @@ int bs_quantize_e4m3fn(const void* x, int64_t n, void* q_out, float* scale_out,
                        const void* workspace, int64_t workspace_bytes, uint32_t epoch,
                        void* stream);
 
+/*
+ * C[M, N] (bf16, row-major, row stride N) = A[M, K] @ B[K, N], where A is bf16
+ * with k contiguous (row stride lda >= K) and B is a compressed [K, N]
+ * activation decoded tile by tile into LDS (never written to HBM dense).
+ *   square = 0: B = stored bf16 values          (AspB, bf16 storage)
+ *   square = 1: B = k*v*v as in bs_decompress   (AspRelu2B), and with
+ *               b_scale (fp8 storage) B = bf16(B * bf16(b_scale^2))
+ * fp32 MFMA accumulation; small grids split K into fp32 partial sums in
+ * `workspace` (bs_gemm_compressed_b_workspace_bytes; 0 = none needed),
+ * reduced in a fixed order.
+ * Replaces lib_sparse/src/sparse_matmul.py:24-28 (AspB) and :109-113
+ * (AspRelu2B): unpack to a dense HBM buffer, then torch.matmul.
+ */
+int64_t bs_gemm_compressed_b_workspace_bytes(int64_t M, int64_t N, int64_t K);
+int bs_gemm_compressed_b(const void* A, int64_t M, int64_t K, int64_t lda, const void* vals,
+                         int vals_dtype, int64_t vals_numel, const uint8_t* bitmask,
+                         const uint32_t* prefix, const int64_t* vals_offset, int64_t N,
+                         int square, float relu2_scale, const float* b_scale, void* C,
+                         void* workspace, int64_t workspace_bytes, void* stream);
+
 /* Device pointer of the amax slot inside a workspace (for bs_compress). */
 const uint64_t* bs_workspace_amax_slot(const void* workspace, int64_t workspace_bytes);
 

@@ -1,0 +1,79 @@
+"""Reconstruct-into-LDS MFMA GEMM (bs_gemm_compressed_b) against an fp32
+reference on the decompressed operand.  Tolerance: the kernel accumulates in
+fp32 and rounds once to bf16, so results agree with the fp32 product to about
+one bf16 ulp (2^-8 relative); the bound below is 2^-7 relative plus a small
+absolute term for near-cancelling sums."""
+import pytest
+import torch
+
+from tests.helpers import preact_input, relu_input
+
+pytestmark = pytest.mark.gpu
+
+
+def _ref(A, B_dense):
+    return A.float() @ B_dense.float()
+
+
+def _check(C, ref):
+    assert C.dtype == torch.bfloat16 and C.shape == ref.shape
+    scale = ref.abs().max().item() + 1e-6
+    torch.testing.assert_close(C.float(), ref, rtol=2 ** -7, atol=2 ** -7 * scale * 1e-2)
+
+
+@pytest.mark.parametrize("M,K,N", [(256, 64, 64), (300, 200, 130), (64, 100, 64), (768, 8192, 3072),
+                                   (1000, 512, 700), (33, 64, 1)])
+def test_gemm_bf16(dev, M, K, N):
+    from bitsparse_amd.src import dw_gemm
+    from bitsparse_amd.src.functions import dense_to_tilesparse
+    h = relu_input((K, N), 0.5, seed=1).to(dev)
+    A = preact_input((M, K), seed=2).to(dev)
+    sp = dense_to_tilesparse(h, None)
+    assert dw_gemm.supports(A, sp, square=False)
+    C = dw_gemm.gemm_compressed_b(A, sp, square=False)
+    _check(C, _ref(A, h))
+
+
+def test_gemm_transposed_a_and_buffer_offset(dev):
+    """AspB's call shape: A = dY.T (a transposed view), h in a shared buffer."""
+    from bitsparse_amd.bitsparse import TensorBuffer
+    from bitsparse_amd.src.functions import dense_to_tilesparse
+    from bitsparse_amd.src.sparse_matmul import AspB
+    dY = preact_input((512, 192), seed=3).to(dev)
+    h1 = relu_input((512, 320), 0.7, seed=4).to(dev)
+    h2 = relu_input((512, 320), 0.3, seed=5).to(dev)
+    buf = TensorBuffer(2 * 2 * 512 * 320, device=dev)
+    sp1 = dense_to_tilesparse(h1, None, buf)
+    sp2 = dense_to_tilesparse(h2, None, buf)
+    assert int(sp2.vals_offset.item()) > 0
+    for h, sp in ((h1, sp1), (h2, sp2)):
+        _check(AspB(dY.T, sp), _ref(dY.T, h))
+
+
+@pytest.mark.parametrize("storage", ["bf16", "e4m3fn"])
+def test_gemm_relu2_square(dev, storage):
+    from bitsparse_amd.src import dw_gemm
+    from bitsparse_amd.src.functions import dense_to_tilesparse, quantize_and_compress
+    from bitsparse_amd.src.hip_operators import unpack_relu2_batch_
+    K, N, M = 384, 448, 320
+    r = preact_input((K, N), seed=6).relu().to(dev)
+    A = preact_input((M, K), seed=7).to(dev)
+    if storage == "bf16":
+        sp = dense_to_tilesparse(r, None)
+    else:
+        _, _, sp = quantize_and_compress(r, None)
+    sq = torch.empty((K, N), dtype=torch.bfloat16, device=dev)
+    unpack_relu2_batch_(sp, sq, 0, sp.grid_n, N, K, sp.grid_m * sp.grid_n)
+    assert dw_gemm.supports(A, sp, square=True)
+    C = dw_gemm.gemm_compressed_b(A, sp, square=True)
+    _check(C, _ref(A, sq))
+
+
+def test_gemm_all_zero_and_dense_operands(dev):
+    from bitsparse_amd.src import dw_gemm
+    from bitsparse_amd.src.functions import dense_to_tilesparse
+    A = preact_input((256, 128), seed=8).to(dev)
+    for sparsity in (1.0, 0.0):
+        h = relu_input((128, 192), sparsity, seed=9).to(dev)
+        C = dw_gemm.gemm_compressed_b(A, dense_to_tilesparse(h, None), square=False)
+        _check(C, _ref(A, h))
