@@ -33,15 +33,17 @@ def gemm_compressed_b(A: Tensor, B_sparse, square: bool) -> Tensor:
     if not supports(A, B_sparse, square):
         raise ValueError("gemm_compressed_b: unsupported operand combination")
     K, N = B_sparse.shape
-    A = A.contiguous()                      # [M, K], k contiguous
     M = A.shape[0]
+    At = A.t()                              # [K, M]; for A = dY.T this is dY itself
+    if At.stride(1) != 1:
+        At = At.contiguous()
     L = _lib.load()
     C = torch.empty((M, N), device=A.device, dtype=torch.bfloat16)
     need = L.bs_gemm_compressed_b_workspace_bytes(M, N, K)
     ws = torch.empty(max(need, 0), device=A.device, dtype=torch.uint8) if need > 0 else None
     scale = B_sparse.scale if (square and B_sparse.scale is not None) else None
     check(L.bs_gemm_compressed_b(
-        A.data_ptr(), M, K, A.stride(0), B_sparse.vals.data_ptr(), dtype_code(B_sparse.vals.dtype),
+        At.data_ptr(), M, K, At.stride(0), B_sparse.vals.data_ptr(), dtype_code(B_sparse.vals.dtype),
         B_sparse.vals.numel(), B_sparse.bitmask.data_ptr(), B_sparse.prefix.data_ptr(),
         B_sparse.vals_offset.data_ptr(), N, int(square), float(RELU2_SCALE), ptr(scale),
         C.data_ptr(), ptr(ws), need, stream_handle(A.device)), "bs_gemm_compressed_b")

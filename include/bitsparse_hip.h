@@ -176,9 +176,10 @@ int bs_quantize_e4m3fn(const void* x, int64_t n, void* q_out, float* scale_out,
                        void* stream);
 
 /*
- * C[M, N] (bf16, row-major, row stride N) = A[M, K] @ B[K, N], where A is bf16
- * with k contiguous (row stride lda >= K) and B is a compressed [K, N]
- * activation decoded tile by tile into LDS (never written to HBM dense).
+ * C[M, N] (bf16, row-major, row stride N) = At^T @ B, where At is a dense
+ * bf16 [K, M] matrix with m contiguous (row stride ldat >= M; in the MLP
+ * backward At = dY) and B is a compressed [K, N] activation decoded tile by
+ * tile into LDS (never written to HBM dense).
  *   square = 0: B = stored bf16 values          (AspB, bf16 storage)
  *   square = 1: B = k*v*v as in bs_decompress   (AspRelu2B), and with
  *               b_scale (fp8 storage) B = bf16(B * bf16(b_scale^2))
@@ -189,7 +190,7 @@ int bs_quantize_e4m3fn(const void* x, int64_t n, void* q_out, float* scale_out,
  * (AspRelu2B): unpack to a dense HBM buffer, then torch.matmul.
  */
 int64_t bs_gemm_compressed_b_workspace_bytes(int64_t M, int64_t N, int64_t K);
-int bs_gemm_compressed_b(const void* A, int64_t M, int64_t K, int64_t lda, const void* vals,
+int bs_gemm_compressed_b(const void* At, int64_t M, int64_t K, int64_t ldat, const void* vals,
                          int vals_dtype, int64_t vals_numel, const uint8_t* bitmask,
                          const uint32_t* prefix, const int64_t* vals_offset, int64_t N,
                          int square, float relu2_scale, const float* b_scale, void* C,
