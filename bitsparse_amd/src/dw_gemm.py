@@ -22,6 +22,8 @@ def supports(A: Tensor, B_sparse, square: bool) -> bool:
         return False
     if A.shape[1] != B_sparse.shape[0]:
         return False
+    if B_sparse.vals.data_ptr() % 16 != 0:   # the kernel reads value runs as aligned 16-byte slots
+        return False
     vdt = B_sparse.vals.dtype
     if vdt == torch.bfloat16:
         return True
@@ -35,8 +37,12 @@ def gemm_compressed_b(A: Tensor, B_sparse, square: bool) -> Tensor:
     K, N = B_sparse.shape
     M = A.shape[0]
     At = A.t()                              # [K, M]; for A = dY.T this is dY itself
-    if At.stride(1) != 1:
-        At = At.contiguous()
+    if At.stride(1) != 1 or At.stride(0) % 8 != 0 or At.data_ptr() % 16 != 0:
+        # the kernel reads 8-element row chunks: rows padded to a multiple of 8
+        ld = (M + 7) // 8 * 8
+        pad = torch.zeros((K, ld), device=A.device, dtype=A.dtype)
+        pad[:, :M] = At
+        At = pad
     L = _lib.load()
     C = torch.empty((M, N), device=A.device, dtype=torch.bfloat16)
     need = L.bs_gemm_compressed_b_workspace_bytes(M, N, K)
