@@ -63,8 +63,8 @@ constexpr int kOffB = kOffA + 2 * kBK * kAP * 2;           // B_s[2][64][kBP] bf
 constexpr int kOffRun = kOffB + 2 * kBK * kBP * 2;         // run_s[2][2 tiles][kRunSlots] uint4
 constexpr int kOffBm = kOffRun + 2 * 2 * kRunSlots * 16;   // bm_s[2][2][64] uint64
 constexpr int kOffRp = kOffBm + 2 * 2 * 64 * 8;           // rp_s[2][2][64] uint32 (row prefixes)
-constexpr int kOffPre = kOffRp + 2 * 2 * 64 * 4;          // pre_s[kMaxSteps][4] uint32
-constexpr int kOffLut = kOffPre + kMaxSteps * 4 * 4;      // lut_s[256] uint4 byte-permute selectors
+constexpr int kOffMeta = kOffRp + 2 * 2 * 64 * 4;         // meta_s[2][4] int (run phases)
+constexpr int kOffLut = kOffMeta + 2 * 4 * 4;             // lut_s[256] uint4 byte-permute selectors
 constexpr int kLds = kOffLut + 256 * 16;
 // epilogue staging (after the main loop), 128 rows per consumer wave
 constexpr int kStF = 64 + 4;          // fp32 staging pitch (floats)
@@ -182,6 +182,12 @@ __device__ __forceinline__ uint2 window(const uint32_t* run32, uint32_t r)
     }
 }
 
+// compile-time register-set index
+template <int P>
+struct IC {
+    static constexpr int value = P;
+};
+
 template <int V_T, bool SQUARE, bool HAS_SCALE>
 __global__ __launch_bounds__(kThreads, 1) void gemm_cb_kernel(GemmArgs a)
 {
@@ -195,7 +201,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_cb_kernel(GemmArgs a)
     uint4* run_s = reinterpret_cast<uint4*>(lds + kOffRun);
     uint64_t* bm_s = reinterpret_cast<uint64_t*>(lds + kOffBm);
     uint32_t* rp_s = reinterpret_cast<uint32_t*>(lds + kOffRp);
-    uint32_t* pre_s = reinterpret_cast<uint32_t*>(lds + kOffPre);
+    int* meta_s = reinterpret_cast<int*>(lds + kOffMeta);
     uint4* lut_s = reinterpret_cast<uint4*>(lds + kOffLut);
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -217,14 +223,6 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_cb_kernel(GemmArgs a)
     const uint32_t kt1 = min(a.ksteps, kt0 + a.ksteps_per_split);
     const int nsteps = kt1 > kt0 ? (int)(kt1 - kt0) : 0;
 
-    // prefixes of every tile row this workgroup visits: p0, p1, p2
-    for (int s = tid; s < nsteps; s += kThreads) {
-        const size_t t = (size_t)(kt0 + s) * a.grid_n + nt0;
-        const uint32_t p0 = a.prefix[t], p1 = a.prefix[t + 1];
-        pre_s[s * 4 + 0] = p0;
-        pre_s[s * 4 + 1] = p1;
-        pre_s[s * 4 + 2] = two ? a.prefix[t + 2] : p1;
-    }
     // Byte-permute selectors per bitmask byte b.  A chunk's values are read
     // as two windows of 4 stored values: window A from the chunk's first rank
     // (elements 0-3 draw from it), window B from the rank of element 4.
@@ -259,12 +257,19 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_cb_kernel(GemmArgs a)
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
 
+    // Pipeline (both roles keep two register sets, R = 0, 1, so global loads
+    // are issued two steps before their data is stored to LDS).  At the top
+    // of iteration s: A_s/B_s[s&1] hold step s; run_s[(s+1)&1] holds run(s+1);
+    // consumer set (s+1)&1 holds A(s+1), set s&1 holds A(s+2); producer set
+    // s&1 holds run(s+2), set (s+1)&1 holds run(s+3).  Loads past the last
+    // step re-read it.  Every global read is a raw buffer load through a
+    // wave-uniform resource whose size stops at the operand's end, so
+    // out-of-range lanes read zeros without branches.
+    const int last = nsteps - 1;
+    const IC<0> R0;
+    const IC<1> R1;
     if (tid >= kProducer0) {
-        // =================== producers ===================
-        // Every global read is a raw buffer load through a per-step,
-        // wave-uniform resource whose size stops at the operand's end, so
-        // out-of-range lanes read zeros without branches and no loop-carried
-        // register is merged behind a wait.
+        // =================== producers: value runs, bitmask, decode ===================
         const int p = tid - kProducer0;                // 0..255
         const int64_t vo = a.vals_offset ? *a.vals_offset : 0;
         float s2b = 1.0f;
@@ -273,20 +278,53 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_cb_kernel(GemmArgs a)
             s2b = bf16_to_f32(f32_to_bf16(sc * sc));
         }
         const uint32_t zero_b = HAS_SCALE ? hw_bf16(0.0f * s2b) : 0u;
+        const uint32_t zero_pair = zero_b | (zero_b << 16);
         const float kr = a.relu2_scale;
+        const bool k_plain = kr >= 0.0f;           // k*0*0 is +0: expanded zeros need no fix-up
         // tile whose bitmask row `lane` this wave loads (two waves per tile)
         const int ub = __builtin_amdgcn_readfirstlane((p >> 6) & 1);
 
-        uint4 areg[8];
-        uint4 rreg[2][RUN_REGS];
-        int nsl[2] = {0, 0};                           // slots of the staged runs in rreg
-        uint64_t bmreg;
+        uint4 rreg[2][2][RUN_REGS];
+        int nsl[2][2] = {{0, 0}, {0, 0}};              // slots of the staged runs in rreg
+        int phs[2][2] = {{0, 0}, {0, 0}};              // their phases
+        uint64_t bmreg[2] = {0ull, 0ull};
 
-        // value run of tile u at step s (wave-uniform): 16-byte aligned start
-        // e0 (elements), phase = run start - e0, nslots 16-byte slots
-        auto run_geom = [&](int s, int u, int64_t& e0, int& phase, int& nslots) {
-            const uint32_t p0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)pre_s[s * 4 + u]);
-            const uint32_t p1 = (uint32_t)__builtin_amdgcn_readfirstlane((int)pre_s[s * 4 + u + 1]);
+        // prefix[t], prefix[t+1], prefix[t+2] of every step this workgroup
+        // visits, loaded once: lane l of register w holds step 64*w + l
+        // (nsteps <= kMaxSteps = 256); the loop picks them with v_readlane
+        uint32_t pq[3][kMaxSteps / 64];
+#pragma unroll
+        for (int w = 0; w < kMaxSteps / 64; w++) {
+            const int st = 64 * w + lane;
+            uint32_t v0 = 0u, v1 = 0u, v2 = 0u;
+            if (st < nsteps) {
+                const size_t t = (size_t)(kt0 + (uint32_t)st) * a.grid_n + nt0;
+                v0 = a.prefix[t];
+                v1 = a.prefix[t + 1];
+                v2 = two ? a.prefix[t + 2] : v1;
+            }
+            pq[0][w] = v0;
+            pq[1][w] = v1;
+            pq[2][w] = v2;
+        }
+        uint32_t pf[3];
+        auto load_pre = [&](int s) __attribute__((always_inline)) {
+            const int w = s >> 6, l = s & 63;
+#pragma unroll
+            for (int c = 0; c < 3; c++) {
+                const uint32_t x0 = (uint32_t)__builtin_amdgcn_readlane((int)pq[c][0], l);
+                const uint32_t x1 = (uint32_t)__builtin_amdgcn_readlane((int)pq[c][1], l);
+                const uint32_t x2 = (uint32_t)__builtin_amdgcn_readlane((int)pq[c][2], l);
+                const uint32_t x3 = (uint32_t)__builtin_amdgcn_readlane((int)pq[c][3], l);
+                pf[c] = w == 0 ? x0 : w == 1 ? x1 : w == 2 ? x2 : x3;
+            }
+        };
+        // value run of tile u of the step whose prefixes are in pf
+        // (wave-uniform): 16-byte aligned start e0 (elements), phase = run
+        // start - e0, nslots 16-byte slots
+        auto run_geom = [&](int u, int64_t& e0, int& phase, int& nslots) __attribute__((always_inline)) {
+            const uint32_t p0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)(u ? pf[1] : pf[0]));
+            const uint32_t p1 = (uint32_t)__builtin_amdgcn_readfirstlane((int)(u ? pf[2] : pf[1]));
             const int64_t run0 = vo + (int64_t)p0;
             int64_t cnt = (int64_t)p1 - (int64_t)p0;
             cnt = cnt < 0 ? 0 : (cnt > kTileNumel ? kTileNumel : cnt);
@@ -294,42 +332,22 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_cb_kernel(GemmArgs a)
             e0 = run0 - phase;
             nslots = (phase + (int)cnt + EPS - 1) / EPS;
         };
-        // dY rows of step s: chunk c = i*256 + p -> row c/32, 8 m at (c%32)*8.
-        // Rows past K lie outside the resource and read as zero; columns past M
-        // only feed C rows that are never stored.
-        auto load_a = [&](int s) {
-            const int64_t k0 = (int64_t)(kt0 + (uint32_t)s) * kBK;
-            const int64_t rows = a.K - k0 < kBK ? a.K - k0 : kBK;
-            const bs_rsrc rs = make_rsrc(a.At + k0 * a.ldat, (uint32_t)(rows * a.ldat * 2));
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const int c = i * 256 + p;
-                const uint32_t off = (uint32_t)(((c >> 5) * a.ldat + m0 + (c & 31) * 8) * 2);
-                areg[i] = load16(rs, off);
-            }
-        };
-        auto store_a = [&](int buf) {
-            uint16_t* dst = A_s + buf * (kBK * kAP);
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const int c = i * 256 + p;
-                *reinterpret_cast<uint4*>(&dst[(c >> 5) * kAP + (c & 31) * 8]) = areg[i];
-            }
-        };
         // bitmask rows and the 16-byte-aligned value runs of step s's two tiles
-        auto load_run = [&](int s) {
+        auto load_run = [&](int s, auto R) __attribute__((always_inline)) {
+            constexpr int RS = decltype(R)::value;
             const size_t t0 = (size_t)(kt0 + (uint32_t)s) * a.grid_n + nt0;
             {
                 const bs_rsrc rs = make_rsrc(a.bitmask + (t0 + ub) * kTileBytes,
                                              (ub == 0 || two) ? (uint32_t)kTileBytes : 0u);
-                bmreg = load8(rs, (uint32_t)lane * 8u);
+                bmreg[RS] = load8(rs, (uint32_t)lane * 8u);
             }
 #pragma unroll
             for (int u = 0; u < 2; u++) {
                 int64_t e0;
                 int phase, nslots;
-                run_geom(s, u, e0, phase, nslots);
-                nsl[u] = nslots;
+                run_geom(u, e0, phase, nslots);
+                nsl[RS][u] = nslots;
+                phs[RS][u] = phase;
                 const int64_t avail = a.vals_numel - e0;        // elements readable from e0
                 const bool ok = e0 >= 0 && avail > 0;
                 int64_t bytes = ok ? avail * VB : 0;
@@ -342,28 +360,30 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_cb_kernel(GemmArgs a)
                     // the slot holding the end of `vals` is read element by element
                     if ((int64_t)(sl + 1) * EPS > avail && (int64_t)sl * EPS < avail && sl < nslots)
                         v = load16_tail<VB>(rs, (uint32_t)sl * 16u);
-                    rreg[u][i] = v;
+                    rreg[RS][u][i] = v;
                 }
             }
+            load_pre(min(s + 1, last));
         };
-        auto store_run = [&](int buf) {
+        auto store_run = [&](int buf, auto R) __attribute__((always_inline)) {
+            constexpr int RS = decltype(R)::value;
 #pragma unroll
             for (int u = 0; u < 2; u++)
 #pragma unroll
                 for (int i = 0; i < RUN_REGS; i++) {
                     const int sl = i * 256 + p;
-                    if (sl < nsl[u]) run_s[(buf * 2 + u) * kRunSlots + sl] = rreg[u][i];
+                    if (sl < nsl[RS][u]) run_s[(buf * 2 + u) * kRunSlots + sl] = rreg[RS][u][i];
                 }
             if (p < 128) {                             // producer waves 0 and 1: one tile each
-                const uint32_t c = (uint32_t)__popcll(bmreg);
-                uint32_t x = c;
+                // exclusive scan of the row popcounts (0..64, 7 bits) from
+                // one ballot per bit: no LDS round trip
+                const uint32_t c = (uint32_t)__popcll(bmreg[RS]);
+                uint32_t x = 0;
 #pragma unroll
-                for (int o = 1; o < 64; o <<= 1) {
-                    const uint32_t y = __shfl_up(x, o, 64);
-                    if (lane >= o) x += y;
-                }
-                bm_s[(buf * 2 + ub) * 64 + lane] = bmreg;
-                rp_s[(buf * 2 + ub) * 64 + lane] = x - c;
+                for (int bit = 0; bit < 7; bit++) x += popc_below(__ballot(c & (1u << bit))) << bit;
+                bm_s[(buf * 2 + ub) * 64 + lane] = bmreg[RS];
+                rp_s[(buf * 2 + ub) * 64 + lane] = x;
+                if (lane < 2) meta_s[buf * 4 + lane] = phs[RS][lane];
             }
         };
         // decode step s from run/bitmask buffer rb into B_s[bb]; chunk
@@ -373,17 +393,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_cb_kernel(GemmArgs a)
         // bits).  All LDS reads of the four chunks precede the writes.
         const int du = (p >> 3) & 1, dn0 = (p & 7) * 8;
         const uint64_t below_mask = dn0 == 0 ? 0ull : (~0ull >> (64 - dn0));
-        const bool k_plain = kr >= 0.0f;           // k*0*0 is +0: expanded zeros need no fix-up
-        auto decode = [&](int s, int rb, int bb) {
-            int ph[2];
-#pragma unroll
-            for (int u = 0; u < 2; u++) {
-                int64_t e0;
-                int nslots;
-                run_geom(s, u, e0, ph[u], nslots);
-            }
+        auto decode = [&](int rb, int bb) __attribute__((always_inline)) {
             const uint32_t* run32 = reinterpret_cast<const uint32_t*>(run_s + (rb * 2 + du) * kRunSlots);
-            const uint32_t phu = (uint32_t)(du ? ph[1] : ph[0]);
+            const uint32_t phu = (uint32_t)meta_s[rb * 4 + du];
             uint64_t mrow[4];
             uint32_t rp[4];
 #pragma unroll
@@ -433,9 +445,11 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_cb_kernel(GemmArgs a)
                 if constexpr (SQUARE) {
                     if (!k_plain) {   // negative or NaN k: cleared elements must stay zero_b
 #pragma unroll
-                        for (int e = 0; e < 8; e++)
-                            if (!((byte[i] >> e) & 1u))
-                                w[e >> 1] = (w[e >> 1] & (0xffff0000u >> (16 * (e & 1)))) | (zero_b << (16 * (e & 1)));
+                        for (int d = 0; d < 4; d++) {
+                            const uint32_t keep = (((byte[i] >> (2 * d)) & 1u) ? 0x0000ffffu : 0u) |
+                                                  (((byte[i] >> (2 * d + 1)) & 1u) ? 0xffff0000u : 0u);
+                            w[d] = (w[d] & keep) | (zero_pair & ~keep);
+                        }
                     }
                 }
                 const int k = 16 * i + (p >> 4);
@@ -443,44 +457,80 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_cb_kernel(GemmArgs a)
             }
         };
 
-        // prologue: A_s[0], B_s[0] hold step 0, areg = A(1), run_s[1] = run(1),
-        // rreg = run(2).  Loads past the last step re-read the last step.
-        const int last = nsteps - 1;
         if (nsteps > 0) {
-            load_a(0);
-            load_run(0);
-            store_a(0);
-            store_run(0);
-            load_a(min(1, last));
-            load_run(min(1, last));
+            load_pre(0);
+            load_run(0, R0);
+            store_run(0, R0);
+            load_run(min(1, last), R1);
+            load_run(min(2, last), R0);
         }
         __syncthreads();
         if (nsteps > 0) {
-            decode(0, 0, 0);
-            store_run(1);
-            load_run(min(2, last));
+            decode(0, 0);
+            store_run(1, R1);
+            load_run(min(3, last), R1);
         }
         __syncthreads();
-        // iteration s: the consumers multiply step s while this prepares s+1
-        for (int s = 0; s < nsteps; s++) {
-            const int nxt = (s + 1) & 1;
-            store_a(nxt);                                   // A(s+1)
-            store_run(s & 1);                               // run(s+2)
-            load_a(min(s + 2, last));
-            load_run(min(s + 3, last));
-            if (s + 1 < nsteps) decode(s + 1, nxt, nxt);    // B(s+1)
+        // iteration s (R = register set s&1): the consumers multiply step s
+        auto iteration = [&](int s, auto R) __attribute__((always_inline)) {
+            constexpr int P = decltype(R)::value;
+            store_run(P, R);                              // run(s+2)
+            load_run(min(s + 4, last), R);
+            if (s + 1 < nsteps) decode(P ^ 1, P ^ 1);     // B(s+1)
             __syncthreads();
+        };
+        int s = 0;
+        for (; s + 1 < nsteps; s += 2) {
+            iteration(s, R0);
+            iteration(s + 1, R1);
         }
+        if (s < nsteps) iteration(s, R0);
     } else {
-        // =================== consumers ===================
+        // =================== consumers: dY tile and MFMAs ===================
+        uint4 areg[2][8];
+        // dY rows of step s: chunk c = i*256 + tid -> row c/32, 8 m at (c%32)*8.
+        // Rows past K lie outside the resource and read as zero; columns past M
+        // only feed C rows that are never stored.
+        auto load_a = [&](int s, auto R) __attribute__((always_inline)) {
+            const int64_t k0 = (int64_t)(kt0 + (uint32_t)s) * kBK;
+            const int64_t rows = a.K - k0 < kBK ? a.K - k0 : kBK;
+            const bs_rsrc rs = make_rsrc(a.At + k0 * a.ldat, (uint32_t)(rows * a.ldat * 2));
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int c = i * 256 + tid;
+                const uint32_t off = (uint32_t)(((c >> 5) * a.ldat + m0 + (c & 31) * 8) * 2);
+                areg[decltype(R)::value][i] = load16(rs, off);
+            }
+        };
+        auto store_a = [&](int buf, auto R) __attribute__((always_inline)) {
+            uint16_t* dst = A_s + buf * (kBK * kAP);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int c = i * 256 + tid;
+                *reinterpret_cast<uint4*>(&dst[(c >> 5) * kAP + (c & 31) * 8]) = areg[decltype(R)::value][i];
+            }
+        };
+        if (nsteps > 0) {
+            load_a(0, R0);
+            store_a(0, R0);
+            load_a(min(1, last), R1);
+            load_a(min(2, last), R0);
+        }
         __syncthreads();
         __syncthreads();
         const int wm = wave & 1, wn = wave >> 1;
         const int g = lane >> 4, j = lane & 15;
-        for (int s = 0; s < nsteps; s++) {
-            const int cur = s & 1;
-            const uint16_t* As = A_s + cur * (kBK * kAP);
-            const uint16_t* Bs = B_s + cur * (kBK * kBP);
+        auto iteration = [&](int s, auto R) __attribute__((always_inline)) {
+            constexpr int P = decltype(R)::value;
+            const IC<P ^ 1> Rn;
+            const uint16_t* As = A_s + P * (kBK * kAP);
+            const uint16_t* Bs = B_s + P * (kBK * kBP);
+            // A(s+1) is stored to the other buffer and A(s+3) loaded in
+            // quarters between the MFMA blocks
+            const int64_t k0n = (int64_t)(kt0 + (uint32_t)min(s + 3, last)) * kBK;
+            const int64_t rows_n = a.K - k0n < kBK ? a.K - k0n : kBK;
+            const bs_rsrc rs_n = make_rsrc(a.At + k0n * a.ldat, (uint32_t)(rows_n * a.ldat * 2));
+            uint16_t* dst_n = A_s + (P ^ 1) * (kBK * kAP);
 #pragma unroll
             for (int kk = 0; kk < 4; kk++) {
                 const int k0 = kk * 16 + 8 * (g >> 1);
@@ -494,9 +544,22 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_cb_kernel(GemmArgs a)
 #pragma unroll
                     for (int jj = 0; jj < 2; jj++)
                         acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[jj], acc[i][jj], 0, 0, 0);
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const int i = kk * 2 + h;
+                    const int c = i * 256 + tid;
+                    *reinterpret_cast<uint4*>(&dst_n[(c >> 5) * kAP + (c & 31) * 8]) = areg[P ^ 1][i];
+                    areg[P ^ 1][i] = load16(rs_n, (uint32_t)(((c >> 5) * a.ldat + m0 + (c & 31) * 8) * 2));
+                }
             }
             __syncthreads();
+        };
+        int s = 0;
+        for (; s + 1 < nsteps; s += 2) {
+            iteration(s, R0);
+            iteration(s + 1, R1);
         }
+        if (s < nsteps) iteration(s, R0);
     }
 
     // ---- epilogue: consumers stage their 128 x 64 block in LDS, then write
