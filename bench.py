@@ -8,8 +8,16 @@ TensorBuffer reset + fused single-pass compress + full decompress.
 Also reported on the same line:
   roofline      dominant kernel (compress), HIP-event timed on its stream
   kernels       per-kernel achieved GB/s for compress / decompress
+  gemm          reconstruct-into-LDS dW GEMM at the configs[1] and configs[3]
+                dW shapes: TF/s, fraction of the dense bf16 MFMA peak, and the
+                decompress + hipBLASLt path it replaces
   mlp           configs[1] GPT-2-small MLP fwd+bwd: compressed vs dense
                 activation (step and backward ms, saved-activation bytes)
+  mlp_c4        configs[3] 8B-class ReLU^2 MLP with fp8 activation storage
+  sweep         configs[2] sparsity sweep (bf16 and e4m3fn storage, skewed
+                columns)
+  stack         configs[4] 12 GPT-2-small blocks: peak activation memory and
+                fwd+bwd time, compressed vs dense storage
   cpu_baseline  the C oracle (single thread) on a bounded row sample of the
                 same workload, same unit
 
@@ -102,6 +110,71 @@ def bench_codec(M: int, N: int, mu: float, steps: int, warmup: int):
     return res
 
 
+def _timed(fn, steps: int, warmup: int) -> float:
+    """Mean ms of fn() over `steps` launches after `warmup`, HIP events."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def bench_gemm(steps: int, warmup: int):
+    """dW = dY^T @ h with h compressed, at the two MLP configs' dW shapes."""
+    import torch
+    from bitsparse_amd.src import dw_gemm
+    from bitsparse_amd.src.functions import dense_to_tilesparse, quantize_and_compress
+    from bitsparse_amd.src.hip_operators import unpack_batch_, unpack_relu2_batch_
+
+    dev = torch.device("cuda", 0)
+    out = {}
+    cases = [("configs[1] dW2", 768, 8192, 3072, 0.0, False),
+             ("configs[3] dW2", 4096, 4096, 16384, -1.2816, True)]
+    for name, M, K, N, mu, relu2_fp8 in cases:
+        g = torch.Generator(device=dev).manual_seed(0)
+        h = (torch.randn((K, N), device=dev, generator=g) + mu).to(torch.bfloat16).relu_()
+        dY = torch.randn((K, M), device=dev, generator=g).to(torch.bfloat16)
+        A = dY.T
+        if relu2_fp8:
+            _, _, sp = quantize_and_compress(h, None)
+        else:
+            sp = dense_to_tilesparse(h, None)
+        dense = torch.empty((K, N), device=dev, dtype=torch.bfloat16)
+        nt = sp.grid_m * sp.grid_n
+
+        def lds():
+            return dw_gemm.gemm_compressed_b(A, sp, square=relu2_fp8)
+
+        def ref():
+            if relu2_fp8:
+                unpack_relu2_batch_(sp, dense, 0, sp.grid_n, N, K, nt)
+            else:
+                unpack_batch_(sp, dense, 0, sp.grid_n, N, K, nt)
+            return A @ dense
+
+        t_lds = _timed(lds, steps, warmup)
+        t_ref = _timed(ref, steps, warmup)
+        flop = 2.0 * M * N * K
+        tf = flop / (t_lds * 1e9)
+        out[name] = {"M": M, "K": K, "N": N,
+                     "operand": "relu^2 (e4m3fn storage)" if relu2_fp8 else "relu (bf16 storage)",
+                     "sparsity": round(1 - int(sp.prefix[-1].item()) / (K * N), 4),
+                     "lds_gemm_ms": round(t_lds, 4), "lds_gemm_tflops": round(tf, 1),
+                     "mfma_frac_of_bf16_peak": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                     "decompress_plus_hipblaslt_ms": round(t_ref, 4)}
+        del h, dY, dense, sp
+    return out
+
+
 def bench_mlp(steps: int, warmup: int):
     """8192 x 768 -> 3072 -> 768 bf16, W ~ N(0, 0.02), x, dY ~ N(0, 1)."""
     import torch
@@ -162,6 +235,189 @@ def bench_mlp(steps: int, warmup: int):
                                      "ratio": round(stored / dense_bytes, 4)}
     out["bwd_ratio_compressed_over_dense"] = out["compressed"]["bwd_ms"] / out["dense"]["bwd_ms"]
     out["step_ratio_compressed_over_dense"] = out["compressed"]["step_ms"] / out["dense"]["step_ms"]
+    return out
+
+
+def bench_mlp_c4(steps: int, warmup: int):
+    """4096 rows, 4096 -> 16384 -> 4096, W ~ N(0, 0.02), ReLU^2,
+    pre-activation shifted (bias) so ~90% of the activation is zero, fp8
+    (e4m3fn) activation storage.  Dense comparator: the reference's fp8
+    dense-storage ReLU^2 block (r cached as e4m3fn + scale)."""
+    import torch
+    from bitsparse_amd.bitsparse import TensorBuffer
+    from bitsparse_amd.dense import DenseFFNRelu2Fp8
+    from bitsparse_amd.layers import FFNRelu2
+
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(0)
+    B, D, H = 4096, 4096, 16384
+    x = torch.randn((B, D), device=dev, generator=g).to(torch.bfloat16).requires_grad_()
+    W1 = (0.02 * torch.randn((H, D), device=dev, generator=g)).to(torch.bfloat16).requires_grad_()
+    W2 = (0.02 * torch.randn((D, H), device=dev, generator=g)).to(torch.bfloat16).requires_grad_()
+    # z = x @ W1.T has std 0.02 * sqrt(D); shift by -1.2816 std for 90% zeros
+    b1 = torch.full((H,), -1.2816 * 0.02 * D ** 0.5, device=dev, dtype=torch.bfloat16)
+    dY = torch.randn((B, D), device=dev, generator=g).to(torch.bfloat16)
+    buf = TensorBuffer(B * H, device=dev, dtype=torch.float8_e4m3fn)
+
+    def run(compressed: bool, ev=None):
+        for p in (x, W1, W2):
+            p.grad = None
+        if ev is not None:
+            ev[0].record()
+        if compressed:
+            buf.reset_buffer()
+            y = FFNRelu2.apply(x, W1, W2, b1, sparse_data=buf, storage_dtype=torch.float8_e4m3fn)
+        else:
+            y = DenseFFNRelu2Fp8.apply(x, W1, W2, b1)
+        if ev is not None:
+            ev[1].record()
+        y.backward(dY)
+        if ev is not None:
+            ev[2].record()
+
+    out = {}
+    for mode in ("dense", "compressed"):
+        comp = mode == "compressed"
+        for _ in range(warmup):
+            run(comp)
+        torch.cuda.synchronize()
+        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+        for i in range(steps):
+            run(comp, evs[i])
+        torch.cuda.synchronize()
+        out[mode] = {"step_ms": round(sum(e[0].elapsed_time(e[2]) for e in evs) / steps, 4),
+                     "fwd_ms": round(sum(e[0].elapsed_time(e[1]) for e in evs) / steps, 4),
+                     "bwd_ms": round(sum(e[1].elapsed_time(e[2]) for e in evs) / steps, 4)}
+    from bitsparse_amd.src.functions import quantize_and_compress
+    with torch.no_grad():
+        r = (x @ W1.T + b1).relu_()
+        buf.reset_buffer()
+        _, _, sp = quantize_and_compress(r, buf)
+        stored = sp.vram_size()
+        sparsity = 1 - int(sp.prefix[-1].item()) / r.numel()
+    dense_bytes = B * H        # the dense comparator caches r as e4m3fn
+    out["sparsity"] = round(sparsity, 4)
+    out["saved_activation_bytes"] = {"dense_fp8": dense_bytes, "compressed": stored,
+                                     "ratio": round(stored / dense_bytes, 4)}
+    out["bwd_ratio_compressed_over_dense"] = round(out["compressed"]["bwd_ms"] / out["dense"]["bwd_ms"], 4)
+    out["step_ratio_compressed_over_dense"] = round(out["compressed"]["step_ms"] / out["dense"]["step_ms"], 4)
+    return out
+
+
+def bench_sweep(steps: int, warmup: int):
+    """16384 x 16384, N(mu, 1) pre-activation for 50..99% zeros,
+    bf16 storage and e4m3fn storage (fused amax + quantize + compress), plus
+    a skewed case with a per-column N(0, 0.5) bias."""
+    import torch
+    from bitsparse_amd.bitsparse import TensorBuffer
+    from bitsparse_amd.src.functions import dense_to_tilesparse, quantize_and_compress
+    from bitsparse_amd.src.hip_operators import unpack_batch_
+
+    dev = torch.device("cuda", 0)
+    M = N = 16384
+    gm, gn = M // 64, N // 64
+    out = []
+    mus = [("50%", 0.0), ("75%", -0.6745), ("90%", -1.2816), ("95%", -1.6449), ("99%", -2.3263)]
+    cases = [(n, mu, st, False) for n, mu in mus for st in ("bf16", "e4m3fn")]
+    cases += [("90% skewed columns", -1.2816, "bf16", True)]
+    for name, mu, storage, skew in cases:
+        g = torch.Generator(device=dev).manual_seed(0)
+        pre = torch.randn((M, N), device=dev, generator=g) + mu
+        if skew:
+            pre += 0.5 * torch.randn((1, N), device=dev, generator=g)
+        x = pre.to(torch.bfloat16).relu_()
+        del pre
+        fp8 = storage == "e4m3fn"
+        vdt = torch.float8_e4m3fn if fp8 else torch.bfloat16
+        buf = TensorBuffer(M * N * (1 if fp8 else 2), device=dev, dtype=vdt)
+        outd = torch.empty((M, N), device=dev, dtype=vdt)
+        holder = {}
+
+        def comp():
+            buf.reset_buffer()
+            if fp8:
+                holder["sp"] = quantize_and_compress(x, buf)[2]
+            else:
+                holder["sp"] = dense_to_tilesparse(x, None, buf)
+
+        def decomp():
+            unpack_batch_(holder["sp"], outd, 0, gn, N, M, gm * gn)
+
+        tc = _timed(comp, steps, warmup)
+        td = _timed(decomp, steps, warmup)
+        sp = holder["sp"]
+        nnz = int(sp.prefix[-1].item())
+        vb = 1 if fp8 else 2
+        cb, db = codec_bytes(M, N, nnz, vb_in=2, vb=vb, vb_out=vb)
+        if fp8:
+            cb += 2 * M * N   # the amax pass reads the bf16 input once more
+        out.append({"case": name, "storage": storage, "sparsity": round(1 - nnz / (M * N), 4),
+                    "compress_ms": round(tc, 4), "decompress_ms": round(td, 4),
+                    "compress_gbs": round(cb / (tc * 1e6), 1), "decompress_gbs": round(db / (td * 1e6), 1),
+                    "roundtrip_gbs": round((cb + db) / ((tc + td) * 1e6), 1),
+                    "stored_over_dense": round(sp.vram_size() / (M * N * 2), 4)})
+        del x, buf, outd, holder
+        torch.cuda.empty_cache()
+    return out
+
+
+def bench_stack(steps: int, warmup: int):
+    """12 GPT-2-small MLP blocks (8192 x 768 -> 3072 -> 768),
+    every activation held until backward; peak memory above the parameters
+    and inputs, and fwd+bwd time, compressed vs dense storage."""
+    import torch
+    from bitsparse_amd.bitsparse import TensorBuffer
+    from bitsparse_amd.dense import DenseFFNRelu
+    from bitsparse_amd.layers import FFNRelu
+
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(0)
+    L, B, D, H = 12, 8192, 768, 3072
+    Ws = [((0.02 * torch.randn((H, D), device=dev, generator=g)).to(torch.bfloat16).requires_grad_(),
+           (0.02 * torch.randn((D, H), device=dev, generator=g)).to(torch.bfloat16).requires_grad_())
+          for _ in range(L)]
+    x0 = torch.randn((B, D), device=dev, generator=g).to(torch.bfloat16).requires_grad_()
+    dY = torch.randn((B, D), device=dev, generator=g).to(torch.bfloat16)
+    # value buffer sized to the stack's measured nonzeros (+8 per block for
+    # alignment slack), as a user would size it for their sparsity
+    with torch.no_grad():
+        h, nnz = x0, 0
+        for W1, W2 in Ws:
+            a = (h @ W1.T).relu_()
+            nnz += int((a > 0).sum().item()) + 8
+            h = h + a @ W2.T
+        del h, a
+    buf = TensorBuffer(2 * nnz, device=dev)
+    out = {}
+    for mode in ("dense", "compressed"):
+        def run():
+            for W1, W2 in Ws:
+                W1.grad = W2.grad = None
+            x0.grad = None
+            h = x0
+            if mode == "compressed":
+                buf.reset_buffer()
+            for W1, W2 in Ws:
+                if mode == "compressed":
+                    h = h + FFNRelu.apply(h, W1, W2, sparse_data=buf)
+                else:
+                    h = h + DenseFFNRelu.apply(h, W1, W2)
+            h.backward(dY)
+        for _ in range(warmup):
+            run()
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats()
+        base = torch.cuda.memory_allocated()
+        ms = _timed(run, steps, 0)
+        peak = torch.cuda.max_memory_allocated() - base
+        if mode == "compressed":
+            peak += buf.vals.numel() * buf.vals.element_size()   # allocated before `base`
+        out[mode] = {"step_ms": round(ms, 4), "peak_bytes_above_base": int(peak)}
+    out["peak_ratio_compressed_over_dense"] = round(out["compressed"]["peak_bytes_above_base"] /
+                                                    out["dense"]["peak_bytes_above_base"], 4)
+    out["note"] = ("residual stream h + block(h); the compressed peak counts its TensorBuffer "
+                   "(sized to the stack's nonzeros) in full")
+    out["buffer_bytes"] = int(2 * nnz)
     return out
 
 
@@ -228,6 +484,32 @@ def cpu_baseline_mlp(budget_s: float = 15.0):
             "reps": len(times), "threads": torch.get_num_threads(), "dtype": "bf16"}
 
 
+def cpu_baseline_mlp_c4(budget_s: float = 12.0):
+    """configs[3] dense comparator (bf16 ReLU^2 block; the host has no fp8
+    GEMM) in PyTorch on the host cores on a 64-row slice, scaled to 4096 rows."""
+    import torch
+    from bitsparse_amd.dense import DenseFFNRelu2
+    torch.set_num_threads(os.cpu_count() or 1)
+    g = torch.Generator().manual_seed(0)
+    rows, D, H = 64, 4096, 16384
+    x = torch.randn((rows, D), generator=g).to(torch.bfloat16).requires_grad_()
+    W1 = (0.02 * torch.randn((H, D), generator=g)).to(torch.bfloat16).requires_grad_()
+    W2 = (0.02 * torch.randn((D, H), generator=g)).to(torch.bfloat16).requires_grad_()
+    dY = torch.randn((rows, D), generator=g).to(torch.bfloat16)
+    times = []
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < budget_s or len(times) < 3:
+        a = time.perf_counter()
+        DenseFFNRelu2.apply(x, W1, W2).backward(dY)
+        times.append(time.perf_counter() - a)
+        x.grad = W1.grad = W2.grad = None
+    times.sort()
+    med = times[len(times) // 2]
+    return {"step_ms_full_batch_est": round(med * 1e3 * 4096 / rows, 1), "sample_rows": rows,
+            "reps": len(times), "threads": torch.get_num_threads(),
+            "dtype": "bf16 (dense ReLU^2 comparator; fp8 GEMMs are GPU-only)"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -237,6 +519,8 @@ def main() -> int:
                     help="pre-activation mean (0 -> 50%% zeros)")
     ap.add_argument("--skip-mlp", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--skip-extras", action="store_true",
+                    help="skip the GEMM, configs[3] MLP, sparsity sweep and 12-block stack sections")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a 1 GiB device copy (reference for rocprof byte counters)")
     args = ap.parse_args()
@@ -270,6 +554,17 @@ def main() -> int:
         log("mlp: configs[1] GPT-2-small block")
         mlp = bench_mlp(max(5, args.steps // 2), max(2, args.warmup // 2))
         log("mlp done")
+    gemm = mlp_c4 = sweep = stack = None
+    if not args.skip_extras:
+        log("gemm: reconstruct-into-LDS dW GEMM")
+        gemm = bench_gemm(max(5, args.steps // 2), 3)
+        log("mlp_c4: configs[3] ReLU^2 fp8 storage")
+        mlp_c4 = bench_mlp_c4(5, 2)
+        log("sweep: configs[2] sparsities")
+        sweep = bench_sweep(10, 3)
+        log("stack: configs[4] 12 blocks")
+        stack = bench_stack(3, 2)
+        log("extras done")
     cpu = None
     cpu_mlp = None
     if not args.skip_cpu:
@@ -279,6 +574,9 @@ def main() -> int:
         if not args.skip_mlp:
             cpu_mlp = cpu_baseline_mlp()
             mlp["cpu_dense_mlp"] = cpu_mlp
+        if mlp_c4 is not None:
+            log("cpu baseline: configs[3] dense ReLU^2 on host cores")
+            mlp_c4["cpu_dense_mlp"] = cpu_baseline_mlp_c4()
 
     step_ms = codec["compress_ms"] + codec["decompress_ms"]
     # HBM bytes per compress launch from the committed rocprofv3 counter runs
@@ -319,7 +617,11 @@ def main() -> int:
                     "lookback_fallbacks": codec["lookback_fallbacks"]},
         "bytes_saved": {"dense": codec["dense_bytes"], "stored": codec["stored_bytes"],
                         "saved": codec["dense_bytes"] - codec["stored_bytes"]},
+        "gemm": gemm,
         "mlp": mlp,
+        "mlp_c4": mlp_c4,
+        "sweep": sweep,
+        "stack": stack,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)

@@ -4,7 +4,9 @@ uncompressed.  They define the denominator of "compressed backward within
 
 Semantics of reference experiments/experiment.py:242-306 (``FFN``: saves
 relu(z) and masks with threshold_backward) and :322-384 (``FFNRelu2_2``:
-saves r = relu(z), rebuilds k*r^2 in backward), bf16 path.
+saves r = relu(z), rebuilds k*r^2 in backward).  ``DenseFFNRelu2Fp8`` is
+that comparator's fp8 mode (experiment.py:330-384 with an fp8 DTYPE): fp8
+GEMMs, r cached as e4m3fn + scale, k*r^2 rebuilt in bf16.
 """
 from __future__ import annotations
 
@@ -12,6 +14,7 @@ import torch
 from torch.autograd import Function
 
 from .config import RELU2_SCALE
+from .fp8 import matmul, to_fp8
 
 
 class DenseFFNRelu(Function):
@@ -59,3 +62,38 @@ class DenseFFNRelu2(Function):
         grad_x = grad_pre @ W1 if ctx.needs_input_grad[0] else None
         grad_W1 = grad_pre.T @ x
         return grad_x, grad_W1, grad_W2
+
+
+class DenseFFNRelu2Fp8(Function):
+    """fp8 mode of DenseFFNRelu2: every GEMM per-tensor fp8, r = relu(z)
+    saved as e4m3fn + scale (reference experiment.py:330-384); optional
+    first-layer bias b1 (no gradient), added before the activation."""
+
+    @staticmethod
+    def forward(ctx, x, W1, W2, b1=None):
+        z = matmul(x, W1.T, True)
+        if b1 is not None:
+            z = z + b1
+        r = z.relu_()
+        r_fp8, r_scale = to_fp8(r)
+        h = r.square()
+        h.mul_(RELU2_SCALE)
+        ctx.save_for_backward(x, W1, W2, r_fp8)
+        ctx.r_scale = r_scale
+        return matmul(h, W2.T, True)
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        x, W1, W2, r_fp8 = ctx.saved_tensors
+        g8, gs = to_fp8(grad_output)
+        r = r_fp8.to(torch.bfloat16) * ctx.r_scale
+        h = r.square().mul_(RELU2_SCALE)
+        grad_W2 = matmul(g8.T, h, True, a_scale=gs)
+        del h
+        grad_z = matmul(g8, W2, True, a_scale=gs)
+        grad_pre = grad_z * (2.0 * RELU2_SCALE * r)
+        del grad_z, r
+        p8, ps = to_fp8(grad_pre)
+        grad_x = matmul(p8, W1, True, a_scale=ps) if ctx.needs_input_grad[0] else None
+        grad_W1 = matmul(p8.T, x, True, a_scale=ps)
+        return grad_x, grad_W1, grad_W2, None
