@@ -519,6 +519,8 @@ def main() -> int:
                     help="pre-activation mean (0 -> 50%% zeros)")
     ap.add_argument("--skip-mlp", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--gemm-only", action="store_true",
+                    help="run only the LDS GEMM section and print its JSON (profiling entry point)")
     ap.add_argument("--skip-extras", action="store_true",
                     help="skip the GEMM, configs[3] MLP, sparsity sweep and 12-block stack sections")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -537,6 +539,10 @@ def main() -> int:
         return 2
     from bitsparse_amd import _lib
     _lib.load()
+
+    if args.gemm_only:
+        print(json.dumps({"gemm": bench_gemm(args.steps, args.warmup)}), flush=True)
+        return 0
 
     M = N = 16384
     log(f"codec: {M}x{N} bf16, mu={args.sparsity_mu}, steps={args.steps}, warmup={args.warmup}")

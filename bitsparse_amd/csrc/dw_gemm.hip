@@ -628,12 +628,28 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_cb_kernel(GemmArgs a)
     }
 }
 
-// C = bf16(sum over splits of part), summed in split order.
+// C = bf16(sum over splits of part), summed in split order; four elements
+// per thread with 16-byte partial reads when n % 4 == 0 (scalar tail / path
+// otherwise).
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* part, int split, int64_t n,
                                                             uint16_t* C)
 {
     const int64_t stride = (int64_t)gridDim.x * 256;
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) {
+    const int64_t n4 = (n % 4 == 0 && (((uintptr_t)part) & 15) == 0 && (((uintptr_t)C) & 7) == 0) ? n / 4 : 0;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += stride) {
+        float4 acc = reinterpret_cast<const float4*>(part)[i];
+        for (int k = 1; k < split; k++) {
+            const float4 v = reinterpret_cast<const float4*>(part + (int64_t)k * n)[i];
+            acc.x += v.x;
+            acc.y += v.y;
+            acc.z += v.z;
+            acc.w += v.w;
+        }
+        const uint32_t lo = f32_to_bf16(acc.x) | (f32_to_bf16(acc.y) << 16);
+        const uint32_t hi = f32_to_bf16(acc.z) | (f32_to_bf16(acc.w) << 16);
+        reinterpret_cast<uint2*>(C)[i] = uint2{lo, hi};
+    }
+    for (int64_t i = 4 * n4 + (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) {
         float s = 0.0f;
         for (int k = 0; k < split; k++) s += part[(int64_t)k * n + i];
         C[i] = (uint16_t)f32_to_bf16(s);
@@ -756,8 +772,9 @@ extern "C" int bs_gemm_compressed_b(const void* At, int64_t M, int64_t K, int64_
     hipError_t e = hipGetLastError();
     if (e == hipSuccess && split > 1) {
         const int64_t n = M * N;
-        int64_t nblk = (n + 255) / 256;
-        if (nblk > 4096) nblk = 4096;
+        int64_t nblk = (n / 4 + 255) / 256;
+        if (nblk > 2048) nblk = 2048;
+        if (nblk < 1) nblk = 1;
         hipLaunchKernelGGL(splitk_reduce_kernel, dim3((uint32_t)nblk), dim3(256), 0, st,
                            (const float*)workspace, split, n, (uint16_t*)C);
         e = hipGetLastError();

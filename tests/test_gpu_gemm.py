@@ -22,7 +22,7 @@ def _check(C, ref):
 
 
 @pytest.mark.parametrize("M,K,N", [(256, 64, 64), (300, 200, 130), (64, 100, 64), (768, 8192, 3072),
-                                   (1000, 512, 700), (33, 64, 1)])
+                                   (1000, 512, 700), (33, 64, 1), (255, 4096, 130)])
 def test_gemm_bf16(dev, M, K, N):
     from bitsparse_amd.src import dw_gemm
     from bitsparse_amd.src.functions import dense_to_tilesparse
