@@ -77,3 +77,29 @@ def test_gemm_all_zero_and_dense_operands(dev):
         h = relu_input((128, 192), sparsity, seed=9).to(dev)
         C = dw_gemm.gemm_compressed_b(A, dense_to_tilesparse(h, None), square=False)
         _check(C, _ref(A, h))
+
+
+@pytest.mark.parametrize("storage,square", [("bf16", False), ("bf16", True), ("e4m3fn", True)])
+def test_gemm_identity_reproduces_decoded_operand(dev, storage, square):
+    """With A = I (K = M) every output is 1.0 * b accumulated in fp32, so C
+    must equal the decompressed operand bit for bit: this pins the GEMM's
+    in-LDS decode (ranks, byte permutes, hardware bf16 / fp8 conversions,
+    ReLU^2 square and scale^2) to the decompress kernel, which the oracle
+    pins."""
+    from bitsparse_amd.src import dw_gemm
+    from bitsparse_amd.src.functions import dense_to_tilesparse, quantize_and_compress
+    from bitsparse_amd.src.hip_operators import unpack_batch_, unpack_relu2_batch_
+    K, N = 320, 448
+    r = preact_input((K, N), seed=11).relu().to(dev)
+    if storage == "bf16":
+        sp = dense_to_tilesparse(r, None)
+    else:
+        _, _, sp = quantize_and_compress(r, None)
+    ref = torch.empty((K, N), dtype=torch.bfloat16, device=dev)
+    if square:
+        unpack_relu2_batch_(sp, ref, 0, sp.grid_n, N, K, sp.grid_m * sp.grid_n)
+    else:
+        unpack_batch_(sp, ref, 0, sp.grid_n, N, K, sp.grid_m * sp.grid_n)
+    A = torch.eye(K, dtype=torch.bfloat16, device=dev)
+    C = dw_gemm.gemm_compressed_b(A, sp, square=square)
+    assert torch.equal(C.view(torch.int16), ref.view(torch.int16))

@@ -78,3 +78,25 @@ def test_ffn_relu_leading_batch_dims_and_bias(dev):
     assert y.shape == (4, 64, 128)
     y.sum().backward()
     assert x.grad.shape == x.shape and b1.grad is not None and b2.grad is not None
+
+
+def test_ffn_relu2_fp8_storage_matches_fp8_dense(dev):
+    """fp8 (e4m3fn) activation storage against the reference's fp8 dense
+    comparator (experiment.py:330-384 with an fp8 DTYPE).  Both run every GEMM
+    in per-tensor fp8; they differ only in bf16 rounding order of the ReLU^2
+    reconstruction, which can move an fp8 re-quantization by one step, so the
+    bound is fp8-sized: 2^-3 of each tensor's max."""
+    from bitsparse_amd.dense import DenseFFNRelu2Fp8
+    from bitsparse_amd.layers import FFNRelu2
+    x, W1, W2, dY = _mlp_inputs(256, 256, 512, seed=4)
+    xs, W1s, W2s = (t.to(dev).requires_grad_() for t in (x, W1, W2))
+    ys = FFNRelu2.apply(xs, W1s, W2s, storage_dtype=torch.float8_e4m3fn)
+    ys.backward(dY.to(dev))
+    xd, W1d, W2d = (t.to(dev).requires_grad_() for t in (x, W1, W2))
+    yd = DenseFFNRelu2Fp8.apply(xd, W1d, W2d)
+    yd.backward(dY.to(dev))
+    for name, a, b in (("y", ys, yd), ("dx", xs.grad, xd.grad), ("dW1", W1s.grad, W1d.grad),
+                       ("dW2", W2s.grad, W2d.grad)):
+        scale = b.abs().max().item() + 1e-6
+        err = (a.float() - b.float()).abs().max().item() / scale
+        assert err < 2 ** -3, f"{name}: {err:.3e}"
