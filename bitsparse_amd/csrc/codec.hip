@@ -214,13 +214,13 @@ __device__ __forceinline__ uint64_t status_at(const CompressArgs& a, int64_t q)
     return q >= 0 ? ld_relaxed(&a.status[q]) : pack_status(a.epoch, kFlagInc, 0);
 }
 
-// Decoupled look-back run by one wave.  The wave first polls only the
-// nearest predecessor (one word) until it is published; from then on it walks
-// back with 256-status windows (four coalesced 512-byte loads in flight per
-// round trip), adding aggregates until the nearest inclusive prefix with every
-// status before it published.  The walk speed (256 units per round trip) has
-// to exceed the rate at which units publish aggregates, or the distance to
-// the nearest inclusive prefix keeps growing.  A predecessor that stays
+// Decoupled look-back run by one wave.  It reads a window of
+// 64 x kLookbackWindows statuses behind the unit (one coalesced 512-byte load
+// per 64) and adds aggregates back to the nearest inclusive prefix; an
+// unpublished status stops the window and is then polled alone (one word)
+// until it is published.  Wider windows were measured slower (their status
+// traffic competes with the data streams), so the default is one.  A
+// predecessor that stays
 // unpublished for kLookbackPatienceTicks is counted from the dense input
 // instead, so the loop ends whatever order units are scheduled in.  Returns
 // the exclusive prefix of unit u in every lane.

@@ -177,9 +177,10 @@ int bs_quantize_e4m3fn(const void* x, int64_t n, void* q_out, float* scale_out,
 
 /*
  * C[M, N] (bf16, row-major, row stride N) = At^T @ B, where At is a dense
- * bf16 [K, M] matrix with m contiguous (row stride ldat >= M; in the MLP
- * backward At = dY) and B is a compressed [K, N] activation decoded tile by
- * tile into LDS (never written to HBM dense).
+ * bf16 [K, M] matrix with m contiguous (row stride ldat >= M, ldat % 8 == 0,
+ * ldat < 2^24, At 16-byte aligned; in the MLP backward At = dY) and B is a
+ * compressed [K, N] activation (vals 16-byte aligned) decoded tile by tile
+ * into LDS (never written to HBM dense).
  *   square = 0: B = stored bf16 values          (AspB, bf16 storage)
  *   square = 1: B = k*v*v as in bs_decompress   (AspRelu2B), and with
  *               b_scale (fp8 storage) B = bf16(B * bf16(b_scale^2))
