@@ -332,6 +332,25 @@ __device__ __forceinline__ uint4 lds_read16_at(const uint8_t* s, int off)
     return r;
 }
 
+// Stage the set elements of one chunk at consecutive positions from r0 of an
+// LDS array; cleared elements are written to `trash` instead, so every element
+// is one unconditional LDS write at an address of its own (no exec-mask
+// branches, no serial rank increment).
+template <int OUTB>
+__device__ __forceinline__ void stage_chunk(uint8_t* s, uint8_t* trash, uint32_t mm, uint32_t r0,
+                                            const typename Raw<OUTB>::T& o)
+{
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const uint32_t below = (uint32_t)__builtin_popcount(mm & ((1u << e) - 1u));
+        uint8_t* dst = ((mm >> e) & 1u) ? s + (r0 + below) * OUTB : trash;
+        if constexpr (OUTB == 2)
+            *reinterpret_cast<uint16_t*>(dst) = (uint16_t)elem<2>(o, e);
+        else
+            *dst = (uint8_t)elem<1>(o, e);
+    }
+}
+
 // Fused compress of one unit (U consecutive tiles) per workgroup of NT
 // threads.  Thread i owns chunks h*NT + i (h < 512/NT) of every tile of the
 // unit; all of the unit's loads are issued before anything waits.
@@ -353,6 +372,7 @@ __global__ __launch_bounds__(NT) void compress_kernel(CompressArgs a)
     __shared__ uint32_t s_pre[NSLOT + 1];   // exclusive prefix of s_wtot; [NSLOT] = unit total
     __shared__ uint32_t s_lb[1];
     __shared__ __align__(16) uint8_t s_vals[MODE == MODE_COUNT ? 16 : U * kTileNumel * OUTB + 32];
+    __shared__ __align__(4) uint8_t s_trash[MODE == MODE_COUNT ? 4 : NT * OUTB];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const uint32_t u = blockIdx.x;
@@ -451,18 +471,8 @@ __global__ __launch_bounds__(NT) void compress_kernel(CompressArgs a)
             for (int j = 0; j < U; j++)
 #pragma unroll
                 for (int h = 0; h < CH; h++) {
-                    const uint32_t mm = m[j][h];
-                    uint32_t r = s_pre[(j * CH + h) * NW + wave] + ex[j][h];
-#pragma unroll
-                    for (int e = 0; e < 8; e++) {
-                        if ((mm >> e) & 1u) {
-                            if constexpr (OUTB == 2)
-                                reinterpret_cast<uint16_t*>(s_vals)[r] = (uint16_t)elem<2>(o[j][h], e);
-                            else
-                                s_vals[r] = (uint8_t)elem<1>(o[j][h], e);
-                            r++;
-                        }
-                    }
+                    stage_chunk<OUTB>(s_vals, s_trash + tid * OUTB, m[j][h],
+                                      s_pre[(j * CH + h) * NW + wave] + ex[j][h], o[j][h]);
                 }
         }
     };
