@@ -95,12 +95,12 @@ __device__ __forceinline__ float scale_from_slot(const uint64_t* slot, uint32_t 
     return (sc < 1e-9f) ? 1e-9f : sc;
 }
 
-__device__ __forceinline__ uint2 quant_chunk(const uint4 v, float scale)
+__device__ __forceinline__ uint2 quant_chunk(const uint4 v, float scale, float rcp)
 {
     uint2 q = {0u, 0u};
 #pragma unroll
     for (int e = 0; e < 8; e++) {
-        uint32_t b = f32_to_e4m3(bf16_to_f32(get16(v, e)) / scale);
+        uint32_t b = div_to_e4m3(bf16_to_f32(get16(v, e)), scale, rcp);
         if (e < 4) q.x |= b << (8 * e);
         else q.y |= b << (8 * (e - 4));
     }
@@ -168,10 +168,10 @@ struct CompressTraits {
 template <int IN_T, bool QUANT>
 __device__ __forceinline__ uint32_t chunk_mask(const typename Raw<CompressTraits<IN_T, QUANT>::INB>::T& d,
                                                typename Raw<CompressTraits<IN_T, QUANT>::OUTB>::T& o,
-                                               float scale)
+                                               float scale, float rcp)
 {
     if constexpr (QUANT) {
-        o = quant_chunk(d, scale);
+        o = quant_chunk(d, scale, rcp);
         return mask_fp8x8<DT_E4M3FN>(o);
     } else if constexpr (IN_T == DT_BF16) {
         o = d;
@@ -196,7 +196,7 @@ __device__ uint32_t unit_count_wave(const CompressArgs& a, uint32_t q, float sca
         chunk_pos(t0 + (k >> 9), a.grid_n, (int)(k & 511), row, col0);
         auto d = load_chunk<TR::INB, VEC>(a.dense, a.M, a.N, row, col0);
         typename Raw<TR::OUTB>::T o;
-        c += __popc(chunk_mask<IN_T, QUANT>(d, o, scale));
+        c += __popc(chunk_mask<IN_T, QUANT>(d, o, scale, 1.0f / scale));
     }
     return wave_sum_u32(c);
 }
@@ -381,6 +381,7 @@ __global__ __launch_bounds__(NT) void compress_kernel(CompressArgs a)
 
     float scale = 1.0f;
     if constexpr (QUANT) scale = scale_from_slot(a.amax_slot, a.amax_epoch);
+    const float rcp = 1.0f / scale;
     // the cursor is independent of everything else: fetch it first
     int64_t start = 0;
     if (a.offset_in) start = *a.offset_in;
@@ -415,7 +416,7 @@ __global__ __launch_bounds__(NT) void compress_kernel(CompressArgs a)
     for (int j = 0; j < U; j++)
 #pragma unroll
         for (int h = 0; h < CH; h++) {
-            m[j][h] = chunk_mask<IN_T, QUANT>(d[j][h], o[j][h], scale);
+            m[j][h] = chunk_mask<IN_T, QUANT>(d[j][h], o[j][h], scale, rcp);
             if (j < ntiles) {
                 if constexpr (QUANT) {
                     if (a.dense_q_out != nullptr) {
@@ -562,7 +563,7 @@ __global__ __launch_bounds__(kThreads) void tile_pack_kernel(const uint8_t* dens
         chunk_pos(t, grid_n, b, row, col0);
         auto d = load_chunk<INB, VEC>(dense, M, N, row, col0);
         typename Raw<INB>::T o;
-        uint32_t mk = chunk_mask<IN_T, false>(d, o, 1.0f);
+        uint32_t mk = chunk_mask<IN_T, false>(d, o, 1.0f, 1.0f);
         bitmask[(size_t)t * kTileBytes + b] = (uint8_t)mk;
         c += __popc(mk);
     }

@@ -2,7 +2,8 @@
 // together replace lib_sparse/fp8.py:123-129 (to_fp8).
 //
 // scale = max(fp32(amax|x|) / 448, 1e-9); q = e4m3fn_RNE(fp32(x) / scale)
-// with one correctly rounded fp32 division per element.
+// with one correctly rounded fp32 division per element (computed as a
+// reciprocal product with an FMA correction, exact division near ties).
 #include "bs_device.h"
 #include "bs_host.h"
 
@@ -11,7 +12,12 @@ namespace bs {
 constexpr int kFp8Threads = 256;
 
 // max over |x| as bf16 magnitude bits; NaN patterns sort above Inf, so a NaN
-// anywhere wins the max and the decoded amax is NaN.
+// anywhere wins the max and the decoded amax is NaN.  Each thread keeps four
+// independent 16-byte loads in flight per pass; the grid is a few workgroups
+// per CU, so the per-workgroup device-scope atomicMax on the one slot (the
+// only serialised step) stays at a few hundred.
+constexpr int kAmaxUnroll = 4;
+
 __global__ __launch_bounds__(kFp8Threads) void amax_bf16_kernel(const uint16_t* x, int64_t n,
                                                                 uint64_t* slot, uint32_t epoch)
 {
@@ -20,17 +26,33 @@ __global__ __launch_bounds__(kFp8Threads) void amax_bf16_kernel(const uint16_t* 
     uint32_t m = 0;
     const int64_t nvec = ((((uintptr_t)x) & 15u) == 0) ? n / 8 : 0;
     const int64_t stride = (int64_t)gridDim.x * kFp8Threads;
-    for (int64_t i = (int64_t)blockIdx.x * kFp8Threads + tid; i < nvec; i += stride) {
-        uint4 v = reinterpret_cast<const uint4*>(x)[i];
-        uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    const uint4* xv = reinterpret_cast<const uint4*>(x);
+    int64_t i = (int64_t)blockIdx.x * kFp8Threads + tid;
+    for (; i + (kAmaxUnroll - 1) * stride < nvec; i += kAmaxUnroll * stride) {
+        uint4 v[kAmaxUnroll];
+#pragma unroll
+        for (int u = 0; u < kAmaxUnroll; u++) v[u] = xv[i + u * stride];
+#pragma unroll
+        for (int u = 0; u < kAmaxUnroll; u++) {
+            const uint32_t w[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                m = max(m, w[k] & 0x7fffu);
+                m = max(m, (w[k] >> 16) & 0x7fffu);
+            }
+        }
+    }
+    for (; i < nvec; i += stride) {
+        const uint4 v = xv[i];
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
         for (int k = 0; k < 4; k++) {
             m = max(m, w[k] & 0x7fffu);
             m = max(m, (w[k] >> 16) & 0x7fffu);
         }
     }
-    for (int64_t i = nvec * 8 + (int64_t)blockIdx.x * kFp8Threads + tid; i < n; i += stride)
-        m = max(m, (uint32_t)x[i] & 0x7fffu);
+    for (int64_t j = nvec * 8 + (int64_t)blockIdx.x * kFp8Threads + tid; j < n; j += stride)
+        m = max(m, (uint32_t)x[j] & 0x7fffu);
     m = wave_max_u32(m);
     if ((tid & 63) == 0) s_w[tid >> 6] = m;
     __syncthreads();
@@ -54,6 +76,7 @@ __global__ __launch_bounds__(kFp8Threads) void quantize_e4m3_kernel(const uint16
                                                                     uint32_t epoch)
 {
     const float scale = fp8_scale_from_slot(slot, epoch);
+    const float rcp = 1.0f / scale;
     const int tid = threadIdx.x;
     if (blockIdx.x == 0 && tid == 0 && scale_out) *scale_out = scale;
     const bool vec = ((((uintptr_t)x) & 15u) == 0) && ((((uintptr_t)q) & 7u) == 0);
@@ -65,14 +88,14 @@ __global__ __launch_bounds__(kFp8Threads) void quantize_e4m3_kernel(const uint16
         uint32_t o[2] = {0u, 0u};
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            uint32_t lo = f32_to_e4m3(bf16_to_f32(w[k] & 0xffffu) / scale);
-            uint32_t hi = f32_to_e4m3(bf16_to_f32(w[k] >> 16) / scale);
+            uint32_t lo = div_to_e4m3(bf16_to_f32(w[k] & 0xffffu), scale, rcp);
+            uint32_t hi = div_to_e4m3(bf16_to_f32(w[k] >> 16), scale, rcp);
             o[k >> 1] |= (lo | (hi << 8)) << (16 * (k & 1));
         }
         reinterpret_cast<uint2*>(q)[i] = uint2{o[0], o[1]};
     }
     for (int64_t i = nvec * 8 + (int64_t)blockIdx.x * kFp8Threads + tid; i < n; i += stride)
-        q[i] = (uint8_t)f32_to_e4m3(bf16_to_f32(x[i]) / scale);
+        q[i] = (uint8_t)div_to_e4m3(bf16_to_f32(x[i]), scale, rcp);
 }
 
 static uint32_t grid_for(int64_t n)
@@ -99,7 +122,13 @@ extern "C" int bs_amax(const void* x, int64_t n, void* workspace, int64_t worksp
     if (((uintptr_t)x) & 1u) return set_error(BS_ERR_INVALID, "bs_amax: input misaligned");
     if (n == 0) return BS_OK;   // slot keeps an older epoch: readers then see amax = 0
     uint64_t* slot = reinterpret_cast<uint64_t*>((uint8_t*)workspace + kWsAmaxOffset);
-    hipLaunchKernelGGL(amax_bf16_kernel, dim3(grid_for(n)), dim3(kFp8Threads), 0, (hipStream_t)stream,
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+        cus = 256;
+    uint32_t grid = grid_for(n);
+    if (grid > (uint32_t)(2 * cus)) grid = (uint32_t)(2 * cus);
+    hipLaunchKernelGGL(amax_bf16_kernel, dim3(grid), dim3(kFp8Threads), 0, (hipStream_t)stream,
                        (const uint16_t*)x, n, slot, epoch);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(BS_ERR_HIP, "bs_amax launch: %s", hipGetErrorString(e));

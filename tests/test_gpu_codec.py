@@ -303,3 +303,36 @@ def test_tile_pack_and_compact_vals_api(dev):
     torch.cumsum(counts, 0, out=pf.view(torch.int32)[1:])
     vals, off = compact_vals(xd, bmask, pf, None, None, 129, 131, 3, T, 64, 64, 4096, False)
     assert (bits(vals) == O.compress(bits(x), O.BF16)[2]).all() and int(off.item()) == 0
+
+
+def _all_finite_bf16_upto(amax_bits):
+    """Every finite bf16 pattern with magnitude <= the given one, both signs."""
+    mags = np.arange(0, amax_bits + 1, dtype=np.uint16)
+    return np.concatenate([mags, mags | np.uint16(0x8000)])
+
+
+@pytest.mark.parametrize("amax", [448.0, 1.0, 3.0e38, 1e-30, 6.5, 0.0173, 1234.5, 2.0 ** -20] +
+                         [float(v) for v in np.random.default_rng(5).lognormal(0.0, 6.0, 16)])
+def test_to_fp8_all_bf16_patterns(dev, amax):
+    """Every finite bf16 input at a given amax (scale = amax / 448) against the
+    oracle's division and RNE rounding: pins the reciprocal/FMA quotient and the
+    hardware e4m3 conversion of the quantizer."""
+    from bitsparse_amd.fp8 import to_fp8
+    a_bits = int(np.array([amax], dtype=np.float32).view(np.uint32)[0] >> 16)
+    a_bits = min(a_bits, 0x7f7f)
+    x_bits = _all_finite_bf16_upto(a_bits)
+    x = torch.from_numpy(x_bits.view(np.int16).copy()).view(torch.bfloat16).reshape(-1, 2)
+    q, s = to_fp8(x.to(dev))
+    qo, so = O.to_fp8(bits(x))
+    assert float(s.item()) == so
+    assert (bits(q) == qo).all()
+
+
+def test_to_fp8_nan_input(dev):
+    from bitsparse_amd.fp8 import to_fp8
+    x = preact_input((64, 64), seed=72)
+    x[3, 5] = float("nan")
+    q, s = to_fp8(x.to(dev))
+    qo, so = O.to_fp8(bits(x))
+    assert np.isnan(float(s.item())) and np.isnan(so)
+    assert (bits(q) == qo).all()
