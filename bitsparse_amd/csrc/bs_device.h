@@ -175,6 +175,13 @@ __device__ __forceinline__ void wave_scan_count(uint32_t c, uint32_t& excl, uint
     total = (uint32_t)(__popcll(b0) + 2 * __popcll(b1) + 4 * __popcll(b2) + 8 * __popcll(b3));
 }
 
+// Wave total of a per-lane count in [0, 15] (four ballots, scalar result).
+__device__ __forceinline__ uint32_t wave_sum_count(uint32_t c)
+{
+    return (uint32_t)(__popcll(__ballot(c & 1u)) + 2 * __popcll(__ballot(c & 2u)) +
+                      4 * __popcll(__ballot(c & 4u)) + 8 * __popcll(__ballot(c & 8u)));
+}
+
 __device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v)
 {
 #pragma unroll

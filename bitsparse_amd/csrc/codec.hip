@@ -8,6 +8,10 @@
 #include "bs_device.h"
 #include "bs_host.h"
 
+#include <algorithm>
+#include <map>
+#include <mutex>
+
 namespace bs {
 
 template <int B> struct Raw;
@@ -141,6 +145,7 @@ struct CompressArgs {
     uint32_t tile0;             // first tile of unit 0 (VALS: also the prefix base)
     uint32_t tend;              // one past the last tile of this launch
     uint64_t* status;
+    uint64_t* gstat;            // one status word per group of kGroupUnits units
     uint32_t epoch;
     int32_t* err;
     uint32_t* fallbacks;
@@ -182,6 +187,50 @@ __device__ __forceinline__ uint32_t chunk_mask(const typename Raw<CompressTraits
     }
 }
 
+// Inclusive wave64 prefix sum (row shifts inside 16-lane rows, then the row
+// broadcasts of lanes 15 and 31).
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x)
+{
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xf, 0xf, false);   // row_shr:1
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xf, 0xf, false);   // row_shr:2
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xf, 0xf, false);   // row_shr:4
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xf, 0xf, false);   // row_shr:8
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x142, 0xa, 0xf, false);   // row_bcast:15
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x143, 0xc, 0xf, false);   // row_bcast:31
+    return x;
+}
+
+// Positive-bit byte of 8 bf16 values with packed 16-bit arithmetic:
+// x > 0  <=>  (bits - 1) mod 2^16 < 0x7f80.
+__device__ __forceinline__ uint32_t mask_bf16x8_pk(const uint4 v)
+{
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    uint32_t q[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const u16x2 h = __builtin_bit_cast(u16x2, w[i]);
+        const u16x2 t = h - (u16x2)(1);
+        const u16x2 s = __builtin_elementwise_sub_sat((u16x2)(0x7f80), t);
+        q[i] = __builtin_bit_cast(uint32_t, __builtin_elementwise_min(s, (u16x2)(1)));   // bits 0, 16
+    }
+    const uint32_t x = q[0] | (q[1] << 2) | (q[2] << 4) | (q[3] << 6);
+    return (x & 0x55u) | ((x >> 15) & 0xaau);
+}
+
+template <int IN_T, bool QUANT>
+__device__ __forceinline__ uint32_t stream_chunk_mask(const typename Raw<CompressTraits<IN_T, QUANT>::INB>::T& d,
+                                                      typename Raw<CompressTraits<IN_T, QUANT>::OUTB>::T& o,
+                                                      float scale, float rcp)
+{
+    if constexpr (IN_T == DT_BF16 && !QUANT) {
+        o = d;
+        return mask_bf16x8_pk(d);
+    } else {
+        return chunk_mask<IN_T, QUANT>(d, o, scale, rcp);
+    }
+}
+
 // Nonzero count of compress unit q computed straight from the dense input by
 // one wave (look-back fallback).
 template <int IN_T, bool QUANT, bool VEC, int U>
@@ -195,10 +244,18 @@ __device__ uint32_t unit_count_wave(const CompressArgs& a, uint32_t q, float sca
         int64_t row, col0;
         chunk_pos(t0 + (k >> 9), a.grid_n, (int)(k & 511), row, col0);
         auto d = load_chunk<TR::INB, VEC>(a.dense, a.M, a.N, row, col0);
-        typename Raw<TR::OUTB>::T o;
-        c += __popc(chunk_mask<IN_T, QUANT>(d, o, scale, 1.0f / scale));
+        if constexpr (IN_T == DT_BF16 && !QUANT) {
+            // count only (no mask byte): few live registers on this rare path
+            const uint32_t w[4] = {d.x, d.y, d.z, d.w};
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                c += pos_bf16(w[i] & 0xffffu) + pos_bf16(w[i] >> 16);
+        } else {
+            typename Raw<TR::OUTB>::T o;
+            c += __popc(stream_chunk_mask<IN_T, QUANT>(d, o, scale, 1.0f / scale));
+        }
     }
-    return wave_sum_u32(c);
+    return (uint32_t)__builtin_amdgcn_readlane((int)wave_incl_scan(c), 63);
 }
 
 __device__ __forceinline__ uint64_t bcast_lane0(uint64_t v)
@@ -232,7 +289,7 @@ __device__ __forceinline__ uint64_t status_at(const CompressArgs& a, int64_t q)
 #endif
 constexpr int kLookbackWindows = BS_LOOKBACK_WINDOWS;   // x 64 statuses per round trip
 
-template <int IN_T, bool QUANT, bool VEC, int U>
+template <int IN_T, bool QUANT, bool VEC, int U, bool FALLBACK = true>
 __device__ uint32_t wave_lookback(const CompressArgs& a, uint32_t u, float scale, int lane)
 {
     uint32_t excl = 0;
@@ -249,7 +306,7 @@ __device__ uint32_t wave_lookback(const CompressArgs& a, uint32_t u, float scale
             s0 = bcast_lane0(s0);
             const uint32_t f0 = (uint32_t)(s0 >> 32) & 3u;
             if ((uint32_t)(s0 >> 34) != a.epoch || f0 == 0u) {
-                if (wall_clock64() - since > kLookbackPatienceTicks) {
+                if (FALLBACK && wall_clock64() - since > kLookbackPatienceTicks) {
                     excl += unit_count_wave<IN_T, QUANT, VEC, U>(a, (uint32_t)pos, scale, lane);
                     if (lane == 0 && a.fallbacks) atomicAdd(a.fallbacks, 1u);
                     pos -= 1;
@@ -295,6 +352,99 @@ __device__ uint32_t wave_lookback(const CompressArgs& a, uint32_t u, float scale
         // an unpublished status stopped the window: go back to polling it
         head_ready = consumed == 64 * kLookbackWindows;
         if (consumed > 0) since = wall_clock64();
+    }
+    return excl;
+}
+
+// Two-level decoupled look-back of the streaming kernel, run by one wave.
+// Units form groups of kGroupUnits; besides its unit status word, the last
+// unit of a group publishes a group status word: the group aggregate when its
+// own walk passes the group start seeing aggregates only, then the group's
+// inclusive prefix once it has resolved.  A walk adds whole groups (64 group
+// words per read) wherever a group word is out and falls back to that
+// group's unit words otherwise, so a unit resolves in a few reads however far
+// the nearest inclusive prefix is.  Only unit words are ever waited for; a
+// unit that stays unpublished for kLookbackPatienceTicks is counted from the
+// dense input instead.  Returns the exclusive prefix of unit u in every lane.
+constexpr int kGroupUnits = 64;
+
+__device__ __forceinline__ uint32_t wave_total(uint32_t v)
+{
+    return (uint32_t)__builtin_amdgcn_readlane((int)wave_incl_scan(v), 63);
+}
+
+template <int IN_T, bool QUANT, bool VEC, int U>
+__device__ uint32_t wave_lookback_grouped(const CompressArgs& a, uint32_t u, uint32_t unit_total,
+                                          float scale, int lane)
+{
+    uint32_t excl = 0;
+    int64_t pos = (int64_t)u - 1;           // next unit still to be added
+    const int64_t my_lo = (int64_t)u & ~(int64_t)(kGroupUnits - 1);
+    const bool group_last = ((u + 1) & (kGroupUnits - 1)) == 0;
+    bool units_only = false;                // the group word at pos was not out
+    uint64_t since = wall_clock64();
+    while (pos >= 0) {
+        const int64_t lo = pos & ~(int64_t)(kGroupUnits - 1);
+        if (!units_only && pos == lo + kGroupUnits - 1) {
+            const int64_t gq = (pos / kGroupUnits) - lane;
+            const uint64_t s = gq >= 0 ? ld_relaxed(&a.gstat[gq]) : pack_status(a.epoch, kFlagInc, 0);
+            const uint32_t val = (uint32_t)s, flag = (uint32_t)(s >> 32) & 3u;
+            const bool valid = (uint32_t)(s >> 34) == a.epoch && flag != 0u;
+            const uint64_t notv = ~__ballot(valid);
+            const uint64_t incm = __ballot(valid && flag == (uint32_t)kFlagInc);
+            const int fi = notv ? __ffsll((unsigned long long)notv) - 1 : 64;
+            const int fc = incm ? __ffsll((unsigned long long)incm) - 1 : 64;
+            if (fc < fi) return excl + wave_total(lane <= fc ? val : 0u);
+            excl += wave_total(lane < fi ? val : 0u);
+            pos -= (int64_t)fi * kGroupUnits;
+            units_only = fi < 64;
+            if (fi > 0) since = wall_clock64();
+            continue;
+        }
+        units_only = false;
+        const int n = (int)(pos - lo) + 1;  // units pos, pos-1, ..., lo
+        const uint64_t s = lane < n ? ld_relaxed(&a.status[pos - lane]) : 0ull;
+        const uint32_t val = (uint32_t)s, flag = (uint32_t)(s >> 32) & 3u;
+        const bool valid = lane < n && (uint32_t)(s >> 34) == a.epoch && flag != 0u;
+        const uint64_t inwin = n == 64 ? ~0ull : ((1ull << n) - 1ull);
+        const uint64_t notv = ~__ballot(valid) & inwin;
+        const uint64_t incm = __ballot(valid && flag == (uint32_t)kFlagInc);
+        const int fi = notv ? __ffsll((unsigned long long)notv) - 1 : n;
+        const int fc = incm ? __ffsll((unsigned long long)incm) - 1 : 64;
+        if (fc < fi) return excl + wave_total(lane <= fc ? val : 0u);
+        excl += wave_total(lane < fi ? val : 0u);
+        pos -= fi;
+        if (fi > 0) since = wall_clock64();
+        if (fi == n) {
+            // the group start passed with aggregates only: publish the group's
+            // aggregate if this unit closes it
+            if (group_last && lo == my_lo && lane == 0)
+                st_relaxed(&a.gstat[u / kGroupUnits], pack_status(a.epoch, kFlagAgg, excl + unit_total));
+            continue;
+        }
+        // unit pos is not out yet: poll it alone (patience counts from here)
+        since = wall_clock64();
+        while (true) {
+            uint64_t s0 = 0;
+            if (lane == 0) s0 = ld_relaxed(&a.status[pos]);
+            s0 = bcast_lane0(s0);
+            const uint32_t f0 = (uint32_t)(s0 >> 32) & 3u;
+            if ((uint32_t)(s0 >> 34) == a.epoch && f0 != 0u) {
+                if (f0 == (uint32_t)kFlagInc) return excl + (uint32_t)s0;
+                excl += (uint32_t)s0;
+                break;
+            }
+            if (wall_clock64() - since > kLookbackPatienceTicks) {
+                excl += unit_count_wave<IN_T, QUANT, VEC, U>(a, (uint32_t)pos, scale, lane);
+                if (lane == 0 && a.fallbacks) atomicAdd(a.fallbacks, 1u);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(4);
+        }
+        pos -= 1;
+        since = wall_clock64();
+        if (pos == lo - 1 && group_last && lo == my_lo && lane == 0)
+            st_relaxed(&a.gstat[u / kGroupUnits], pack_status(a.epoch, kFlagAgg, excl + unit_total));
     }
     return excl;
 }
@@ -537,6 +687,304 @@ __global__ __launch_bounds__(NT) void compress_kernel(CompressArgs a)
                             reinterpret_cast<const uint16_t*>(s_vals)[l0 + e];
                     else
                         a.vals[e0 + e] = s_vals[l0 + e];
+                }
+            }
+        }
+    }
+}
+
+// ===========================================================================
+// streaming compress (bs_compress FUSED / COUNT)
+//
+// One wave per tile, U tiles (one look-back unit) per workgroup, persistent
+// workgroups that take units from a ticket counter.  Lane l owns chunks
+// 64k + l (k < 8) of its tile: rows 8k + l/8, columns 8(l%8)..+7, so every
+// load instruction covers 8 whole tile rows and the tile's value run is
+// produced in eight in-order rounds of 64 chunks.  The loaded chunks stay in
+// registers while wave 0 runs the look-back; afterwards each wave streams its
+// run through a private LDS ring:
+//   * a chunk is compacted in registers (v_perm with selectors from a
+//     256-entry table indexed by the mask byte) and its 8 elements are written
+//     at the chunk's run position in descending element order: the elements
+//     past the chunk's count land on the positions of the following chunks,
+//     which later (lower-index) writes of those chunks overwrite, so no
+//     element needs an address or a predicate of its own;
+//   * ring slot 0 always holds the output's pending 16-byte slot (the one the
+//     next element falls in); every slot a round completes is stored with one
+//     16-byte write, then the new pending slot is copied back to ring slot 0;
+//   * the partial slots at the two ends of the run, shared with the
+//     neighbouring runs, get element stores.
+// ===========================================================================
+constexpr int kRingElems = 576;     // >= 15 (pending) + 512 (one round) + 8 (overrun)
+
+#ifndef BS_STREAM_WAVES_PER_EU
+#define BS_STREAM_WAVES_PER_EU 8
+#endif
+
+__device__ __forceinline__ void opaque(uint4& v)
+{
+    asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w));
+}
+__device__ __forceinline__ void opaque(uint2& v) { asm volatile("" : "+v"(v.x), "+v"(v.y)); }
+
+// Compaction selectors of mask byte m: the set elements move to the front.
+// bf16 (OUTB 2): output dword j = perm(D1, D0, s[j]) | perm(D3, D2, s[4 + j]);
+// fp8 (OUTB 1): output dword j = perm(D1, D0, s[j]), j < 2.
+template <int OUTB>
+__device__ __forceinline__ void compaction_selectors(uint32_t m, uint32_t* s)
+{
+    constexpr int NS = OUTB == 2 ? 8 : 2;
+#pragma unroll
+    for (int i = 0; i < NS; i++) s[i] = 0x0c0c0c0cu;   // 0x0c selects a zero byte
+    uint32_t q = 0;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        if ((m >> e) & 1u) {
+            if constexpr (OUTB == 2) {
+                const uint32_t ee = (uint32_t)(e & 3);
+                const uint32_t pair = (2u * ee) | ((2u * ee + 1u) << 8);
+                const uint32_t sh = (q & 1u) * 16u;
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    if ((uint32_t)j == (q >> 1)) {
+                        uint32_t& w = s[(e < 4 ? 0 : 4) + j];
+                        w = (w & ~(0xffffu << sh)) | (pair << sh);
+                    }
+            } else {
+                const uint32_t sh = (q & 3u) * 8u;
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+                    if ((uint32_t)j == (q >> 2)) s[j] = (s[j] & ~(0xffu << sh)) | ((uint32_t)e << sh);
+            }
+            q++;
+        }
+    }
+}
+
+// Write the 8 elements of a compacted chunk at consecutive positions from p,
+// last element first (see the kernel comment for why the order matters).
+template <int OUTB>
+__device__ __forceinline__ void write_compacted(uint8_t* p, const typename Raw<OUTB>::T& c)
+{
+    if constexpr (OUTB == 2) {
+        const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+        for (int i = 7; i >= 0; i--) {
+            *reinterpret_cast<uint16_t*>(p + 2 * i) = (uint16_t)(w[i >> 1] >> (16 * (i & 1)));
+            asm volatile("" ::: "memory");
+        }
+    } else {
+        const uint32_t w[2] = {c.x, c.y};
+#pragma unroll
+        for (int i = 7; i >= 0; i--) {
+            p[i] = (uint8_t)(w[i >> 2] >> (8 * (i & 3)));
+            asm volatile("" ::: "memory");
+        }
+    }
+}
+
+template <int OUTB>
+__device__ __forceinline__ void ring_elem_store(uint8_t* vals, int64_t gi, const uint8_t* ring, int idx)
+{
+    if constexpr (OUTB == 2)
+        reinterpret_cast<uint16_t*>(vals)[gi] = reinterpret_cast<const uint16_t*>(ring)[idx];
+    else
+        vals[gi] = ring[idx];
+}
+
+template <int IN_T, bool QUANT, bool VEC, bool WRITE_VALS, int U>
+__global__ __launch_bounds__(64 * U) __attribute__((amdgpu_waves_per_eu(QUANT ? 6 : BS_STREAM_WAVES_PER_EU)))
+void compress_stream_kernel(CompressArgs a)
+{
+    using TR = CompressTraits<IN_T, QUANT>;
+    constexpr int INB = TR::INB, OUTB = TR::OUTB;
+    constexpr int EPS = 16 / OUTB;          // elements per 16-byte slot
+    constexpr int NSEL = OUTB == 2 ? 8 : 2; // selector dwords per mask byte
+    using RawIn = typename Raw<INB>::T;
+    using RawOut = typename Raw<OUTB>::T;
+    static_assert(U >= 1 && U <= 16, "one wave per tile, at most 16 waves");
+
+    __shared__ uint32_t s_cnt[U];
+    __shared__ uint32_t s_toff[U];          // tile offsets inside the unit's run
+    __shared__ uint32_t s_excl[1];
+    __shared__ __align__(16) uint8_t s_ring[WRITE_VALS ? U * kRingElems * OUTB : 16];
+    __shared__ __align__(16) uint32_t s_sel[WRITE_VALS ? 256 * NSEL : 4];
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    if constexpr (WRITE_VALS) {
+        if (tid < 256) {
+            uint32_t sel[NSEL];
+            compaction_selectors<OUTB>((uint32_t)tid, sel);
+#pragma unroll
+            for (int i = 0; i < NSEL; i += 2)
+                *reinterpret_cast<uint2*>(&s_sel[tid * NSEL + i]) = make_uint2(sel[i], sel[i + 1]);
+        }
+    }
+    float scale = 1.0f;
+    if constexpr (QUANT) scale = scale_from_slot(a.amax_slot, a.amax_epoch);
+    const float rcp = 1.0f / scale;
+    int64_t start = 0;
+    if (a.offset_in) start = *a.offset_in;
+    if (a.align8) start = (start + 7) & ~(int64_t)7;
+    __syncthreads();
+
+    {
+        const uint32_t u = blockIdx.x;
+
+        const uint32_t t0 = a.tile0 + u * U;
+        const int ntiles = (int)min((uint32_t)U, a.tend - t0);
+        const bool tile_ok = wave < ntiles;     // wave-uniform
+        const uint32_t t = t0 + (uint32_t)wave;
+
+        // ---- loads: all eight chunks of the lane in flight together.  Waves
+        // past the last tile read the last tile again; with VEC, rows and
+        // columns past the matrix read a clamped in-range address.  Either way
+        // the chunk's mask byte is forced to 0, so no load is conditional (a
+        // conditional load makes the compiler wait for it before the next).
+        const uint32_t tc = tile_ok ? t : a.tend - 1;
+        const uint32_t tm = tc / a.grid_n, tn = tc - tm * a.grid_n;
+        const int64_t row0 = (int64_t)tm * 64 + (lane >> 3);
+        const int64_t col0 = (int64_t)tn * 64 + (lane & 7) * 8;
+        RawIn d[8];
+        // chunk k is inside the matrix iff 8k < rows_in (rows_in <= 0: none)
+        const int64_t rows_in = (tile_ok && col0 < a.N) ? a.M - row0 : 0;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int64_t row = row0 + 8 * k;
+            if constexpr (VEC) {
+                const int64_t rc = min(row, a.M - 1), cc = min(col0, a.N - 8);
+                d[k] = *reinterpret_cast<const RawIn*>(a.dense + (rc * a.N + cc) * INB);
+            } else {
+                d[k] = tile_ok ? load_chunk<INB, false>(a.dense, a.M, a.N, row, col0) : RawIn{};
+            }
+        }
+
+        // ---- masks, bitmask bytes, round totals
+        RawOut o[8];
+        uint32_t mp[2] = {0u, 0u};              // the eight mask bytes, four per register
+        uint32_t P[9];                          // wave-uniform run offset of each round
+        P[0] = 0;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const uint32_t m = stream_chunk_mask<IN_T, QUANT>(d[k], o[k], scale, rcp) & (8 * k < rows_in ? 0xffu : 0u);
+            mp[k >> 2] |= m << (8 * (k & 3));
+            if (tile_ok) {
+                if constexpr (QUANT) {
+                    if (a.dense_q_out != nullptr)
+                        store_chunk<1, VEC>(a.dense_q_out, a.M, a.N, row0 + 8 * k, col0, o[k]);
+                }
+                a.bitmask[(size_t)t * kTileBytes + 64 * k + lane] = (uint8_t)m;
+            }
+            P[k + 1] = P[k] + wave_sum_count(__popc(m));
+        }
+        if (lane == 0) s_cnt[wave] = P[8];
+        __syncthreads();
+
+        // ---- unit total, aggregate, look-back, prefix entries (wave 0)
+        if (wave == 0) {
+            const uint32_t v = lane < U ? s_cnt[lane] : 0u;
+            uint32_t x = v;
+#pragma unroll
+            for (int off = 1; off < U; off <<= 1) {
+                const uint32_t y = __shfl_up(x, off, 64);
+                if (lane >= off) x += y;
+            }
+            const uint32_t unit_total = __shfl(x, U - 1, 64);
+            if (lane < U) s_toff[lane] = x - v;
+            if (lane == 0)
+                st_relaxed(&a.status[u], pack_status(a.epoch, u == 0 ? kFlagInc : kFlagAgg, unit_total));
+            uint32_t excl = 0;
+            if (u != 0) {
+                excl = wave_lookback_grouped<IN_T, QUANT, VEC, U>(a, u, unit_total, scale, lane);
+                if (lane == 0) st_relaxed(&a.status[u], pack_status(a.epoch, kFlagInc, excl + unit_total));
+            }
+            if (lane == 0 && ((u + 1) & (kGroupUnits - 1)) == 0)
+                st_relaxed(&a.gstat[u / kGroupUnits], pack_status(a.epoch, kFlagInc, excl + unit_total));
+            if (lane == 0) s_excl[0] = excl;
+            if (lane < ntiles) a.prefix[t0 + lane] = excl + (x - v);
+            if (lane == 0 && t0 + ntiles == a.tend) {
+                a.prefix[a.tend] = excl + unit_total;
+                const int64_t end = start + (int64_t)(excl + unit_total);
+                if (a.offset_out) *a.offset_out = end;
+                if (a.start_out) *a.start_out = start;
+                if (a.err && end > a.vals_capacity && WRITE_VALS) atomicOr(a.err, 1);
+                if (start < 0 && a.err && WRITE_VALS) atomicOr(a.err, 2);
+            }
+            if constexpr (QUANT) {
+                if (u == 0 && lane == 0 && a.scale_out) *a.scale_out = scale;
+            }
+        }
+        if constexpr (WRITE_VALS) {
+            __syncthreads();
+            if (tile_ok && start >= 0) {
+                const int64_t g = start + (int64_t)__builtin_amdgcn_readfirstlane(s_excl[0]) +
+                                  (int64_t)__builtin_amdgcn_readfirstlane(s_toff[wave]);
+                const int cnt = (int)P[8];
+                const int a0 = (int)((((uintptr_t)a.vals) + (uint64_t)g * OUTB) & 15u) / OUTB;
+                const int64_t room = a.vals_capacity - g;
+                const int endr = (int)max<int64_t>(0, min<int64_t>((int64_t)cnt, room));
+                uint8_t* const slot_base = a.vals + (g - a0) * OUTB;      // 16-byte aligned
+                uint8_t* const ring = s_ring + wave * (kRingElems * OUTB);
+                const int j_lo = a0 ? 1 : 0;                              // first whole slot
+                const int j_hi = (a0 + endr) / EPS;                       // one past the last whole slot
+                const int front_n = a0 ? min(endr, EPS - a0) : 0;         // leading partial slot
+                const int back_s = max(j_hi, j_lo) * EPS - a0;            // trailing partial slot
+                bool front_done = front_n == 0;
+                bool back_done = back_s >= endr;
+                int pend = 0;                   // output slot held in ring slot 0
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    if (front_done && back_done && max(pend, j_lo) >= j_hi) break;
+                    // one round at a time: nothing of round k is computed early
+                    asm volatile("" : "+v"(mp[0]), "+v"(mp[1]) : : "memory");
+                    const uint32_t m = (mp[k >> 2] >> (8 * (k & 3))) & 0xffu;
+                    const uint32_t c = (uint32_t)__popc(m);
+                    const uint32_t ex = wave_incl_scan(c) - c;
+                    const int rb = a0 + (int)P[k] - pend * EPS;           // ring index of the round's first element
+                    RawOut cv;
+                    if constexpr (OUTB == 2) {
+                        const uint4 s0 = *reinterpret_cast<const uint4*>(&s_sel[m * NSEL]);
+                        const uint4 s1 = *reinterpret_cast<const uint4*>(&s_sel[m * NSEL + 4]);
+                        const uint4 v = o[k];
+                        cv.x = __builtin_amdgcn_perm(v.y, v.x, s0.x) | __builtin_amdgcn_perm(v.w, v.z, s1.x);
+                        cv.y = __builtin_amdgcn_perm(v.y, v.x, s0.y) | __builtin_amdgcn_perm(v.w, v.z, s1.y);
+                        cv.z = __builtin_amdgcn_perm(v.y, v.x, s0.z) | __builtin_amdgcn_perm(v.w, v.z, s1.z);
+                        cv.w = __builtin_amdgcn_perm(v.y, v.x, s0.w) | __builtin_amdgcn_perm(v.w, v.z, s1.w);
+                    } else {
+                        const uint2 s0 = *reinterpret_cast<const uint2*>(&s_sel[m * NSEL]);
+                        const uint2 v = o[k];
+                        cv.x = __builtin_amdgcn_perm(v.y, v.x, s0.x);
+                        cv.y = __builtin_amdgcn_perm(v.y, v.x, s0.y);
+                    }
+                    if (c != 0u) write_compacted<OUTB>(ring + (rb + (int)ex) * OUTB, cv);
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                    __builtin_amdgcn_wave_barrier();
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                    const int done = (int)P[k + 1];
+                    const int npend = (a0 + done) / EPS;
+                    if (!front_done && done >= front_n) {
+                        front_done = true;          // pend is still 0 here
+                        if (lane < front_n) ring_elem_store<OUTB>(a.vals, g + lane, ring, a0 + lane);
+                    }
+                    const int jh = min(j_hi, npend);
+                    for (int j = max(pend, j_lo) + lane; j < jh; j += 64)
+                        *reinterpret_cast<uint4*>(slot_base + (int64_t)j * 16) =
+                            *reinterpret_cast<const uint4*>(ring + (j - pend) * 16);
+                    if (!back_done && done >= endr) {
+                        back_done = true;
+                        const int r = back_s + lane;
+                        if (lane < EPS && r < endr)
+                            ring_elem_store<OUTB>(a.vals, g + r, ring, a0 + r - pend * EPS);
+                    }
+                    if (npend > pend) {
+                        if (lane == 0)
+                            *reinterpret_cast<uint4*>(ring) =
+                                *reinterpret_cast<const uint4*>(ring + (npend - pend) * 16);
+                        pend = npend;
+                    }
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                    __builtin_amdgcn_wave_barrier();
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
                 }
             }
         }
@@ -911,9 +1359,28 @@ constexpr int kMaskU = 4;
 static inline bool aligned16(const void* p) { return (((uintptr_t)p) & 15u) == 0; }
 static inline bool aligned8(const void* p) { return (((uintptr_t)p) & 7u) == 0; }
 
+#ifndef BS_COMPRESS_STREAM
+#define BS_COMPRESS_STREAM 1
+#endif
+
+#ifndef BS_STREAM_U
+#define BS_STREAM_U 8
+#endif
+constexpr int kStreamU = BS_STREAM_U;
+
 template <int IN_T, bool QUANT, int MODE>
 static hipError_t launch_compress_mode(const CompressArgs& a, bool vec, hipStream_t st)
 {
+    if constexpr (BS_COMPRESS_STREAM && MODE != MODE_VALS) {
+        constexpr bool WV = MODE == MODE_FUSED;
+        const uint32_t sunits = (a.tend - a.tile0 + kStreamU - 1) / kStreamU;
+        auto launch = [&](auto kern) -> hipError_t {
+            hipLaunchKernelGGL(kern, dim3(sunits), dim3(64 * kStreamU), 0, st, a);
+            return hipGetLastError();
+        };
+        return vec ? launch(compress_stream_kernel<IN_T, QUANT, true, WV, kStreamU>)
+                   : launch(compress_stream_kernel<IN_T, QUANT, false, WV, kStreamU>);
+    }
     const uint32_t units = (a.tend - a.tile0 + kCompressU - 1) / kCompressU;
     if (vec)
         hipLaunchKernelGGL((compress_kernel<IN_T, QUANT, true, MODE, kCompressU, kCompressThreads>),
@@ -944,7 +1411,9 @@ extern "C" int64_t bs_compress_workspace_bytes(int64_t M, int64_t N)
 {
     if (M < 0 || N < 0) return -1;
     int64_t T = ((M + 63) / 64) * ((N + 63) / 64);
-    return kWsHeaderBytes + 8 * (T > 0 ? T : 1);
+    // status words: one per tile covers the units and the unit groups of the
+    // streaming kernel (T/8 + T/512 words) and the units of the others
+    return kWsHeaderBytes + 8 * (T + 2);
 }
 
 extern "C" const uint64_t* bs_workspace_amax_slot(const void* ws, int64_t)
@@ -1038,6 +1507,7 @@ extern "C" int bs_compress(const void* dense, int in_dtype, int64_t M, int64_t N
     a.epoch = epoch;
     a.err = err_flags;
     a.fallbacks = reinterpret_cast<uint32_t*>((uint8_t*)workspace + kWsFallbackOffset);
+    a.gstat = a.status + (T + kStreamU - 1) / kStreamU;
     const int inb = in_dtype == DT_BF16 ? 2 : 1;
     bool vec = (N % 8 == 0) && (((uintptr_t)dense) % (8 * inb) == 0) &&
                (dense_q_out == nullptr || aligned8(dense_q_out));
