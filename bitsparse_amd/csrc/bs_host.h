@@ -11,11 +11,9 @@ namespace bs {
 // Workspace layout: [0, 256) header, then one uint64 status word per tile.
 //   header +0  : uint64 amax slot ((epoch << 32) | bf16 magnitude bits)
 //   header +8  : uint32 look-back fallback counter
-//   header +16 : uint32 unit ticket counter of the streaming compress (0 between launches)
 constexpr int64_t kWsHeaderBytes = 256;
 constexpr int64_t kWsAmaxOffset = 0;
 constexpr int64_t kWsFallbackOffset = 8;
-constexpr int64_t kWsTicketOffset = 16;
 
 // Records a formatted message for bs_last_error() and returns `code`.
 int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));

@@ -1,16 +1,16 @@
-// BitSparse codec kernels for gfx950: single-pass compress, count/compact
-// passes of the standalone path, decompress, and the two gradient kernels.
+// BitSparse codec kernels for gfx950: single-pass compress (and the count /
+// values passes of the standalone path), decompress, and the two gradient
+// kernels.
 //
-// Work decomposition shared by all kernels: a workgroup of 256 threads
-// (4 wave64) owns a "unit" of U consecutive tiles.  For each tile, thread i
-// handles chunks i and i+256 (rows i/8 and 32+i/8), so one wave instruction
-// covers 8 full tile rows = 8 x 128 contiguous bytes of bf16.
+// Compress runs one wave per tile (lane l owns chunks 64k + l, k < 8) and a
+// look-back unit of 8 tiles per workgroup.  The gather kernels (decompress,
+// gradients) use a workgroup of 256 threads (4 wave64) per "unit" of U
+// consecutive tiles: for each tile, thread i handles chunks i and i+256 (rows
+// i/8 and 32+i/8), so one wave instruction covers 8 full tile rows = 8 x 128
+// contiguous bytes of bf16.
 #include "bs_device.h"
 #include "bs_host.h"
 
-#include <algorithm>
-#include <map>
-#include <mutex>
 
 namespace bs {
 
@@ -158,9 +158,11 @@ __device__ __forceinline__ uint64_t pack_status(uint32_t epoch, uint64_t flag, u
     return ((uint64_t)epoch << 34) | (flag << 32) | v;
 }
 
-// 20 us at the 100 MHz s_memrealtime clock: waiting longer than this for a
-// predecessor makes the waiter count that predecessor's tiles itself.
-constexpr uint64_t kLookbackPatienceTicks = 2000;
+// 200 us at the 100 MHz s_memrealtime clock: waiting longer than this for a
+// predecessor makes the waiter count that predecessor's tiles itself (a
+// safety net: in-order workgroup dispatch never needs it, and normal waits
+// behind slow predecessors stay well below it).
+constexpr uint64_t kLookbackPatienceTicks = 20000;
 
 template <int IN_T, bool QUANT>
 struct CompressTraits {
@@ -265,97 +267,6 @@ __device__ __forceinline__ uint64_t bcast_lane0(uint64_t v)
     return ((uint64_t)hi << 32) | lo;
 }
 
-// Status of unit q as seen by this lane (units before 0 read as inclusive 0).
-__device__ __forceinline__ uint64_t status_at(const CompressArgs& a, int64_t q)
-{
-    return q >= 0 ? ld_relaxed(&a.status[q]) : pack_status(a.epoch, kFlagInc, 0);
-}
-
-// Decoupled look-back run by one wave.  It reads a window of
-// 64 x kLookbackWindows statuses behind the unit (one coalesced 512-byte load
-// per 64) and adds aggregates back to the nearest inclusive prefix; an
-// unpublished status stops the window and is then polled alone (one word)
-// until it is published.  Wider windows were measured slower (their status
-// traffic competes with the data streams), so the default is one.  A
-// predecessor that stays
-// unpublished for kLookbackPatienceTicks is counted from the dense input
-// instead, so the loop ends whatever order units are scheduled in.  Returns
-// the exclusive prefix of unit u in every lane.
-#ifndef BS_LOOKBACK_WINDOWS
-#define BS_LOOKBACK_WINDOWS 1
-#endif
-#ifndef BS_LOOKBACK_WINDOW_FIRST
-#define BS_LOOKBACK_WINDOW_FIRST 1
-#endif
-constexpr int kLookbackWindows = BS_LOOKBACK_WINDOWS;   // x 64 statuses per round trip
-
-template <int IN_T, bool QUANT, bool VEC, int U, bool FALLBACK = true>
-__device__ uint32_t wave_lookback(const CompressArgs& a, uint32_t u, float scale, int lane)
-{
-    uint32_t excl = 0;
-    int64_t pos = (int64_t)u - 1;
-    uint64_t since = wall_clock64();
-    // first round reads the window straight away; only an unpublished status
-    // at the head switches to single-word polling
-    bool head_ready = BS_LOOKBACK_WINDOW_FIRST;
-    while (true) {
-        if (!head_ready) {
-            // nearest unresolved predecessor: one lane polls one word
-            uint64_t s0 = 0;
-            if (lane == 0) s0 = status_at(a, pos);
-            s0 = bcast_lane0(s0);
-            const uint32_t f0 = (uint32_t)(s0 >> 32) & 3u;
-            if ((uint32_t)(s0 >> 34) != a.epoch || f0 == 0u) {
-                if (FALLBACK && wall_clock64() - since > kLookbackPatienceTicks) {
-                    excl += unit_count_wave<IN_T, QUANT, VEC, U>(a, (uint32_t)pos, scale, lane);
-                    if (lane == 0 && a.fallbacks) atomicAdd(a.fallbacks, 1u);
-                    pos -= 1;
-                    if (pos < 0) break;
-                    since = wall_clock64();
-                    continue;
-                }
-                __builtin_amdgcn_s_sleep(4);
-                continue;
-            }
-            if (f0 == (uint32_t)kFlagInc) {
-                excl += (uint32_t)s0;
-                break;
-            }
-        }
-        // window of kLookbackWindows x 64 statuses behind pos, all in flight
-        uint64_t sw[kLookbackWindows];
-#pragma unroll
-        for (int w = 0; w < kLookbackWindows; w++) sw[w] = status_at(a, pos - 64 * w - lane);
-        bool done = false;
-        int consumed = 0;
-#pragma unroll
-        for (int w = 0; w < kLookbackWindows; w++) {
-            const uint64_t s = sw[w];
-            const uint32_t val = (uint32_t)s;
-            const uint32_t flag = (uint32_t)(s >> 32) & 3u;
-            const bool valid = (uint32_t)(s >> 34) == a.epoch && flag != 0u;
-            const uint64_t notv = ~__ballot(valid);
-            const uint64_t incm = __ballot(valid && flag == (uint32_t)kFlagInc);
-            const int fi = notv ? __ffsll((unsigned long long)notv) - 1 : 64;
-            const int fc = incm ? __ffsll((unsigned long long)incm) - 1 : 64;
-            if (fc < fi) {
-                excl += wave_sum_u32(lane <= fc ? val : 0u);
-                done = true;
-                break;
-            }
-            excl += wave_sum_u32(lane < fi ? val : 0u);
-            consumed += fi;
-            if (fi < 64) break;
-        }
-        if (done) break;
-        pos -= consumed;
-        // an unpublished status stopped the window: go back to polling it
-        head_ready = consumed == 64 * kLookbackWindows;
-        if (consumed > 0) since = wall_clock64();
-    }
-    return excl;
-}
-
 // Two-level decoupled look-back of the streaming kernel, run by one wave.
 // Units form groups of kGroupUnits; besides its unit status word, the last
 // unit of a group publishes a group status word: the group aggregate when its
@@ -447,250 +358,6 @@ __device__ uint32_t wave_lookback_grouped(const CompressArgs& a, uint32_t u, uin
             st_relaxed(&a.gstat[u / kGroupUnits], pack_status(a.epoch, kFlagAgg, excl + unit_total));
     }
     return excl;
-}
-
-// 16 bytes of LDS starting at byte offset `off` (any alignment, off >= 0),
-// built from two aligned 16-byte reads and byte funnel shifts.
-__device__ __forceinline__ uint4 lds_read16_at(const uint8_t* s, int off)
-{
-    const int base = off & ~15, sh = off & 15;
-    const uint4 lo = *reinterpret_cast<const uint4*>(s + base);
-    if (sh == 0) return lo;
-    const uint4 hi = *reinterpret_cast<const uint4*>(s + base + 16);
-    const uint32_t w0 = lo.x, w1 = lo.y, w2 = lo.z, w3 = lo.w, w4 = hi.x, w5 = hi.y, w6 = hi.z,
-                   w7 = hi.w;
-    const uint32_t bs = (uint32_t)(sh & 3);
-    uint4 r;
-    switch (sh >> 2) {
-    case 0:
-        r.x = __builtin_amdgcn_alignbyte(w1, w0, bs); r.y = __builtin_amdgcn_alignbyte(w2, w1, bs);
-        r.z = __builtin_amdgcn_alignbyte(w3, w2, bs); r.w = __builtin_amdgcn_alignbyte(w4, w3, bs);
-        break;
-    case 1:
-        r.x = __builtin_amdgcn_alignbyte(w2, w1, bs); r.y = __builtin_amdgcn_alignbyte(w3, w2, bs);
-        r.z = __builtin_amdgcn_alignbyte(w4, w3, bs); r.w = __builtin_amdgcn_alignbyte(w5, w4, bs);
-        break;
-    case 2:
-        r.x = __builtin_amdgcn_alignbyte(w3, w2, bs); r.y = __builtin_amdgcn_alignbyte(w4, w3, bs);
-        r.z = __builtin_amdgcn_alignbyte(w5, w4, bs); r.w = __builtin_amdgcn_alignbyte(w6, w5, bs);
-        break;
-    default:
-        r.x = __builtin_amdgcn_alignbyte(w4, w3, bs); r.y = __builtin_amdgcn_alignbyte(w5, w4, bs);
-        r.z = __builtin_amdgcn_alignbyte(w6, w5, bs); r.w = __builtin_amdgcn_alignbyte(w7, w6, bs);
-        break;
-    }
-    return r;
-}
-
-// Stage the set elements of one chunk at consecutive positions from r0 of an
-// LDS array; cleared elements are written to `trash` instead, so every element
-// is one unconditional LDS write at an address of its own (no exec-mask
-// branches, no serial rank increment).
-template <int OUTB>
-__device__ __forceinline__ void stage_chunk(uint8_t* s, uint8_t* trash, uint32_t mm, uint32_t r0,
-                                            const typename Raw<OUTB>::T& o)
-{
-#pragma unroll
-    for (int e = 0; e < 8; e++) {
-        const uint32_t below = (uint32_t)__builtin_popcount(mm & ((1u << e) - 1u));
-        uint8_t* dst = ((mm >> e) & 1u) ? s + (r0 + below) * OUTB : trash;
-        if constexpr (OUTB == 2)
-            *reinterpret_cast<uint16_t*>(dst) = (uint16_t)elem<2>(o, e);
-        else
-            *dst = (uint8_t)elem<1>(o, e);
-    }
-}
-
-// Fused compress of one unit (U consecutive tiles) per workgroup of NT
-// threads.  Thread i owns chunks h*NT + i (h < 512/NT) of every tile of the
-// unit; all of the unit's loads are issued before anything waits.
-template <int IN_T, bool QUANT, bool VEC, int MODE, int U, int NT>
-__global__ __launch_bounds__(NT) void compress_kernel(CompressArgs a)
-{
-    using TR = CompressTraits<IN_T, QUANT>;
-    constexpr int INB = TR::INB, OUTB = TR::OUTB;
-    constexpr int EPS = 16 / OUTB;          // elements per 16-byte store slot
-    constexpr int CH = kChunksPerTile / NT; // chunks per tile per thread
-    constexpr int NW = NT / kWave;
-    using RawIn = typename Raw<INB>::T;
-    using RawOut = typename Raw<OUTB>::T;
-    static_assert(CH * NT == kChunksPerTile, "NT must divide 512");
-
-    constexpr int NSLOT = U * CH * NW;      // per-wave partial counts, flat chunk order
-    static_assert(NSLOT <= 64, "one wave scans the per-wave counts");
-    __shared__ uint32_t s_wtot[NSLOT];
-    __shared__ uint32_t s_pre[NSLOT + 1];   // exclusive prefix of s_wtot; [NSLOT] = unit total
-    __shared__ uint32_t s_lb[1];
-    __shared__ __align__(16) uint8_t s_vals[MODE == MODE_COUNT ? 16 : U * kTileNumel * OUTB + 32];
-    __shared__ __align__(4) uint8_t s_trash[MODE == MODE_COUNT ? 4 : NT * OUTB];
-
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const uint32_t u = blockIdx.x;
-    const uint32_t t0 = a.tile0 + u * U;
-    const int ntiles = (int)min((uint32_t)U, a.tend - t0);
-
-    float scale = 1.0f;
-    if constexpr (QUANT) scale = scale_from_slot(a.amax_slot, a.amax_epoch);
-    const float rcp = 1.0f / scale;
-    // the cursor is independent of everything else: fetch it first
-    int64_t start = 0;
-    if (a.offset_in) start = *a.offset_in;
-    if (a.align8) start = (start + 7) & ~(int64_t)7;
-
-    // ---- load every chunk of the unit first (all loads in flight together)
-    RawIn d[U][CH];
-#pragma unroll
-    for (int j = 0; j < U; j++)
-#pragma unroll
-        for (int h = 0; h < CH; h++) {
-            d[j][h] = RawIn{};
-            if (j < ntiles) {
-                int64_t row, col0;
-                chunk_pos(t0 + j, a.grid_n, h * NT + tid, row, col0);
-                d[j][h] = load_chunk<INB, VEC>(a.dense, a.M, a.N, row, col0);
-            }
-        }
-    uint32_t vm[U][CH];
-    if constexpr (MODE == MODE_VALS) {
-#pragma unroll
-        for (int j = 0; j < U; j++)
-#pragma unroll
-            for (int h = 0; h < CH; h++)
-                vm[j][h] = j < ntiles ? a.bitmask[(size_t)(t0 + j) * kTileBytes + h * NT + tid] : 0u;
-    }
-
-    // ---- masks, optional quantised copy, bitmask bytes
-    RawOut o[U][CH];
-    uint32_t m[U][CH];
-#pragma unroll
-    for (int j = 0; j < U; j++)
-#pragma unroll
-        for (int h = 0; h < CH; h++) {
-            m[j][h] = chunk_mask<IN_T, QUANT>(d[j][h], o[j][h], scale, rcp);
-            if (j < ntiles) {
-                if constexpr (QUANT) {
-                    if (a.dense_q_out != nullptr) {
-                        int64_t row, col0;
-                        chunk_pos(t0 + j, a.grid_n, h * NT + tid, row, col0);
-                        store_chunk<1, VEC>(a.dense_q_out, a.M, a.N, row, col0, o[j][h]);
-                    }
-                }
-                if constexpr (MODE != MODE_VALS)
-                    a.bitmask[(size_t)(t0 + j) * kTileBytes + h * NT + tid] = (uint8_t)m[j][h];
-            }
-            if constexpr (MODE == MODE_VALS) m[j][h] = vm[j][h];
-        }
-
-    // ---- ranks inside each chunk group: ballot scan per wave, totals via LDS
-    uint32_t ex[U][CH];
-#pragma unroll
-    for (int j = 0; j < U; j++)
-#pragma unroll
-        for (int h = 0; h < CH; h++) {
-            uint32_t tot;
-            wave_scan_count(__popc(m[j][h]), ex[j][h], tot);
-            if (lane == 0) s_wtot[(j * CH + h) * NW + wave] = tot;
-        }
-    __syncthreads();
-    // wave 0 turns the per-wave counts into unit-local offsets and publishes
-    // the unit aggregate right away
-    uint32_t unit_total = 0;
-    if (wave == 0) {
-        const uint32_t v = lane < NSLOT ? s_wtot[lane] : 0u;
-        uint32_t x = v;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const uint32_t y = __shfl_up(x, o, 64);
-            if (lane >= o) x += y;
-        }
-        unit_total = __shfl(x, 63, 64);
-        if (lane < NSLOT) s_pre[lane] = x - v;
-        if (lane == 0) s_pre[NSLOT] = unit_total;
-        if constexpr (MODE != MODE_VALS) {
-            if (lane == 0)
-                st_relaxed(&a.status[u], pack_status(a.epoch, u == 0 ? kFlagInc : kFlagAgg, unit_total));
-        }
-    }
-    __syncthreads();
-    unit_total = s_pre[NSLOT];
-
-    // ---- unit start in the value stream (wave 0) while every wave stages its
-    // values in LDS at unit-local positions
-    auto stage = [&]() {
-        if constexpr (MODE != MODE_COUNT) {
-#pragma unroll
-            for (int j = 0; j < U; j++)
-#pragma unroll
-                for (int h = 0; h < CH; h++) {
-                    stage_chunk<OUTB>(s_vals, s_trash + tid * OUTB, m[j][h],
-                                      s_pre[(j * CH + h) * NW + wave] + ex[j][h], o[j][h]);
-                }
-        }
-    };
-    uint32_t excl;
-    if constexpr (MODE == MODE_VALS) {
-        excl = a.prefix[t0] - a.prefix[a.tile0];
-        stage();
-        __syncthreads();
-    } else {
-        if (wave == 0) {
-            if (u == 0) {
-                excl = 0;
-            } else {
-                excl = wave_lookback<IN_T, QUANT, VEC, U>(a, u, scale, lane);
-                if (lane == 0) st_relaxed(&a.status[u], pack_status(a.epoch, kFlagInc, excl + unit_total));
-            }
-            if (lane == 0) s_lb[0] = excl;
-        }
-        stage();
-        __syncthreads();
-        excl = s_lb[0];
-    }
-
-    if constexpr (MODE != MODE_VALS) {
-        if (tid < ntiles) a.prefix[t0 + tid] = excl + s_pre[tid * CH * NW];
-        if (t0 + ntiles == a.tend && tid == 0) {
-            a.prefix[a.tend] = excl + unit_total;
-            int64_t end = start + (int64_t)(excl + unit_total);
-            if (a.offset_out) *a.offset_out = end;
-            if (a.start_out) *a.start_out = start;
-            if (a.err && end > a.vals_capacity && MODE == MODE_FUSED) atomicOr(a.err, 1);
-        }
-        if constexpr (QUANT) {
-            if (u == 0 && tid == 0 && a.scale_out) *a.scale_out = scale;
-        }
-    }
-
-    if constexpr (MODE != MODE_COUNT) {
-        if (start < 0) {                             // corrupt cursor: write nothing
-            if (a.err && tid == 0) atomicOr(a.err, 2);
-            return;
-        }
-        const int64_t g0 = start + (int64_t)excl;   // first element of this unit's run
-        if (MODE == MODE_VALS && a.err && g0 + (int64_t)unit_total > a.vals_capacity && tid == 0)
-            atomicOr(a.err, 1);
-        const int p = (int)((((uintptr_t)a.vals) / OUTB + (uint64_t)g0) % EPS);
-        const int nslots = (p + (int)unit_total + EPS - 1) / EPS;
-        for (int s = tid; s < nslots; s += NT) {
-            const int64_t e0 = g0 - p + (int64_t)s * EPS;   // element index of slot start
-            const int l0 = s * EPS - p;                      // staged index of slot start
-            int lo = max(0, -l0);
-            int hi = min(EPS, (int)unit_total - l0);
-            const int64_t cap_hi = a.vals_capacity - e0;
-            if (cap_hi < hi) hi = (int)max<int64_t>(cap_hi, 0);
-            if (lo == 0 && hi == EPS) {
-                *reinterpret_cast<uint4*>(a.vals + e0 * OUTB) = lds_read16_at(s_vals, l0 * OUTB);
-            } else {
-                for (int e = lo; e < hi; e++) {
-                    if constexpr (OUTB == 2)
-                        reinterpret_cast<uint16_t*>(a.vals)[e0 + e] =
-                            reinterpret_cast<const uint16_t*>(s_vals)[l0 + e];
-                    else
-                        a.vals[e0 + e] = s_vals[l0 + e];
-                }
-            }
-        }
-    }
 }
 
 // ===========================================================================
@@ -792,10 +459,12 @@ __device__ __forceinline__ void ring_elem_store(uint8_t* vals, int64_t gi, const
         vals[gi] = ring[idx];
 }
 
-template <int IN_T, bool QUANT, bool VEC, bool WRITE_VALS, int U>
+template <int IN_T, bool QUANT, bool VEC, int MODE, int U>
 __global__ __launch_bounds__(64 * U) __attribute__((amdgpu_waves_per_eu(QUANT ? 6 : BS_STREAM_WAVES_PER_EU)))
 void compress_stream_kernel(CompressArgs a)
 {
+    static_assert(!(QUANT && MODE == MODE_VALS), "the values pass copies stored values");
+    constexpr bool WRITE_VALS = MODE != MODE_COUNT;
     using TR = CompressTraits<IN_T, QUANT>;
     constexpr int INB = TR::INB, OUTB = TR::OUTB;
     constexpr int EPS = 16 / OUTB;          // elements per 16-byte slot
@@ -846,6 +515,7 @@ void compress_stream_kernel(CompressArgs a)
         const int64_t row0 = (int64_t)tm * 64 + (lane >> 3);
         const int64_t col0 = (int64_t)tn * 64 + (lane & 7) * 8;
         RawIn d[8];
+        uint32_t vm[8];                         // MODE_VALS: the given bitmask bytes
         // chunk k is inside the matrix iff 8k < rows_in (rows_in <= 0: none)
         const int64_t rows_in = (tile_ok && col0 < a.N) ? a.M - row0 : 0;
 #pragma unroll
@@ -857,6 +527,7 @@ void compress_stream_kernel(CompressArgs a)
             } else {
                 d[k] = tile_ok ? load_chunk<INB, false>(a.dense, a.M, a.N, row, col0) : RawIn{};
             }
+            if constexpr (MODE == MODE_VALS) vm[k] = a.bitmask[(size_t)tc * kTileBytes + 64 * k + lane];
         }
 
         // ---- masks, bitmask bytes, round totals
@@ -866,22 +537,30 @@ void compress_stream_kernel(CompressArgs a)
         P[0] = 0;
 #pragma unroll
         for (int k = 0; k < 8; k++) {
-            const uint32_t m = stream_chunk_mask<IN_T, QUANT>(d[k], o[k], scale, rcp) & (8 * k < rows_in ? 0xffu : 0u);
-            mp[k >> 2] |= m << (8 * (k & 3));
-            if (tile_ok) {
-                if constexpr (QUANT) {
-                    if (a.dense_q_out != nullptr)
-                        store_chunk<1, VEC>(a.dense_q_out, a.M, a.N, row0 + 8 * k, col0, o[k]);
+            uint32_t m;
+            if constexpr (MODE == MODE_VALS) {
+                o[k] = d[k];
+                m = tile_ok ? vm[k] & 0xffu : 0u;
+            } else {
+                m = stream_chunk_mask<IN_T, QUANT>(d[k], o[k], scale, rcp) & (8 * k < rows_in ? 0xffu : 0u);
+                if (tile_ok) {
+                    if constexpr (QUANT) {
+                        if (a.dense_q_out != nullptr)
+                            store_chunk<1, VEC>(a.dense_q_out, a.M, a.N, row0 + 8 * k, col0, o[k]);
+                    }
+                    a.bitmask[(size_t)t * kTileBytes + 64 * k + lane] = (uint8_t)m;
                 }
-                a.bitmask[(size_t)t * kTileBytes + 64 * k + lane] = (uint8_t)m;
             }
+            mp[k >> 2] |= m << (8 * (k & 3));
             P[k + 1] = P[k] + wave_sum_count(__popc(m));
         }
-        if (lane == 0) s_cnt[wave] = P[8];
-        __syncthreads();
+        if constexpr (MODE != MODE_VALS) {
+            if (lane == 0) s_cnt[wave] = P[8];
+            __syncthreads();
+        }
 
         // ---- unit total, aggregate, look-back, prefix entries (wave 0)
-        if (wave == 0) {
+        if (MODE != MODE_VALS && wave == 0) {
             const uint32_t v = lane < U ? s_cnt[lane] : 0u;
             uint32_t x = v;
 #pragma unroll
@@ -915,11 +594,20 @@ void compress_stream_kernel(CompressArgs a)
             }
         }
         if constexpr (WRITE_VALS) {
-            __syncthreads();
+            if constexpr (MODE == MODE_VALS) {
+                if (start < 0 && tid == 0 && a.err) atomicOr(a.err, 2);
+            } else {
+                __syncthreads();
+            }
             if (tile_ok && start >= 0) {
-                const int64_t g = start + (int64_t)__builtin_amdgcn_readfirstlane(s_excl[0]) +
-                                  (int64_t)__builtin_amdgcn_readfirstlane(s_toff[wave]);
+                int64_t g;
+                if constexpr (MODE == MODE_VALS)
+                    g = start + (int64_t)(a.prefix[t] - a.prefix[a.tile0]);
+                else
+                    g = start + (int64_t)__builtin_amdgcn_readfirstlane(s_excl[0]) +
+                        (int64_t)__builtin_amdgcn_readfirstlane(s_toff[wave]);
                 const int cnt = (int)P[8];
+                if (MODE == MODE_VALS && a.err && lane == 0 && g + cnt > a.vals_capacity) atomicOr(a.err, 1);
                 const int a0 = (int)((((uintptr_t)a.vals) + (uint64_t)g * OUTB) & 15u) / OUTB;
                 const int64_t room = a.vals_capacity - g;
                 const int endr = (int)max<int64_t>(0, min<int64_t>((int64_t)cnt, room));
@@ -1345,23 +1033,12 @@ __global__ __launch_bounds__(kThreads) void relu_grad_kernel(uint8_t* grad, int6
 // host launchers
 // ===========================================================================
 // compress unit: tiles per workgroup and workgroup size
-#ifndef BS_COMPRESS_U
-#define BS_COMPRESS_U 8
-#endif
-#ifndef BS_COMPRESS_THREADS
-#define BS_COMPRESS_THREADS 512
-#endif
-constexpr int kCompressU = BS_COMPRESS_U;
-constexpr int kCompressThreads = BS_COMPRESS_THREADS;
 constexpr int kGatherU = 2;
 constexpr int kMaskU = 4;
 
 static inline bool aligned16(const void* p) { return (((uintptr_t)p) & 15u) == 0; }
 static inline bool aligned8(const void* p) { return (((uintptr_t)p) & 7u) == 0; }
 
-#ifndef BS_COMPRESS_STREAM
-#define BS_COMPRESS_STREAM 1
-#endif
 
 #ifndef BS_STREAM_U
 #define BS_STREAM_U 8
@@ -1371,23 +1048,13 @@ constexpr int kStreamU = BS_STREAM_U;
 template <int IN_T, bool QUANT, int MODE>
 static hipError_t launch_compress_mode(const CompressArgs& a, bool vec, hipStream_t st)
 {
-    if constexpr (BS_COMPRESS_STREAM && MODE != MODE_VALS) {
-        constexpr bool WV = MODE == MODE_FUSED;
-        const uint32_t sunits = (a.tend - a.tile0 + kStreamU - 1) / kStreamU;
-        auto launch = [&](auto kern) -> hipError_t {
-            hipLaunchKernelGGL(kern, dim3(sunits), dim3(64 * kStreamU), 0, st, a);
-            return hipGetLastError();
-        };
-        return vec ? launch(compress_stream_kernel<IN_T, QUANT, true, WV, kStreamU>)
-                   : launch(compress_stream_kernel<IN_T, QUANT, false, WV, kStreamU>);
-    }
-    const uint32_t units = (a.tend - a.tile0 + kCompressU - 1) / kCompressU;
+    const uint32_t units = (a.tend - a.tile0 + kStreamU - 1) / kStreamU;
     if (vec)
-        hipLaunchKernelGGL((compress_kernel<IN_T, QUANT, true, MODE, kCompressU, kCompressThreads>),
-                           dim3(units), dim3(kCompressThreads), 0, st, a);
+        hipLaunchKernelGGL((compress_stream_kernel<IN_T, QUANT, true, MODE, kStreamU>), dim3(units),
+                           dim3(64 * kStreamU), 0, st, a);
     else
-        hipLaunchKernelGGL((compress_kernel<IN_T, QUANT, false, MODE, kCompressU, kCompressThreads>),
-                           dim3(units), dim3(kCompressThreads), 0, st, a);
+        hipLaunchKernelGGL((compress_stream_kernel<IN_T, QUANT, false, MODE, kStreamU>), dim3(units),
+                           dim3(64 * kStreamU), 0, st, a);
     return hipGetLastError();
 }
 
@@ -1395,7 +1062,9 @@ template <int MODE>
 static hipError_t launch_compress(const CompressArgs& a, int in_dtype, bool quant, bool vec,
                                   hipStream_t st)
 {
-    if (quant) return launch_compress_mode<DT_BF16, true, MODE>(a, vec, st);
+    if constexpr (MODE != MODE_VALS) {
+        if (quant) return launch_compress_mode<DT_BF16, true, MODE>(a, vec, st);
+    }
     switch (in_dtype) {
     case DT_BF16: return launch_compress_mode<DT_BF16, false, MODE>(a, vec, st);
     case DT_E4M3FN: return launch_compress_mode<DT_E4M3FN, false, MODE>(a, vec, st);
