@@ -613,7 +613,7 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(codec["compress_gbs"], 2),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(codec["compress_gbs"] / HBM_PEAK_GBS, 4),
-                     "traffic": traffic, "kernel": "compress_kernel (fused single pass)",
+                     "traffic": traffic, "kernel": "compress_stream_kernel (fused single pass)",
                      "bytes_per_launch": codec["compress_bytes"],
                      "avg_launch_ms": round(codec["compress_ms"], 5)},
         "kernels": {"compress_gbs": round(codec["compress_gbs"], 2),
