@@ -306,8 +306,9 @@ def bench_mlp_c4(steps: int, warmup: int):
 
 def bench_sweep(steps: int, warmup: int):
     """16384 x 16384, N(mu, 1) pre-activation for 50..99% zeros,
-    bf16 storage and e4m3fn storage (fused amax + quantize + compress), plus
-    a skewed case with a per-column N(0, 0.5) bias."""
+    bf16 storage and e4m3fn storage (fused amax + quantize + compress), a
+    skewed case with a per-column N(0, 0.5) bias, and the packed 15/7-bit
+    value stream (pack_sbit) at 50% and 90%."""
     import torch
     from bitsparse_amd.bitsparse import TensorBuffer
     from bitsparse_amd.src.functions import dense_to_tilesparse, quantize_and_compress
@@ -318,9 +319,10 @@ def bench_sweep(steps: int, warmup: int):
     gm, gn = M // 64, N // 64
     out = []
     mus = [("50%", 0.0), ("75%", -0.6745), ("90%", -1.2816), ("95%", -1.6449), ("99%", -2.3263)]
-    cases = [(n, mu, st, False) for n, mu in mus for st in ("bf16", "e4m3fn")]
-    cases += [("90% skewed columns", -1.2816, "bf16", True)]
-    for name, mu, storage, skew in cases:
+    cases = [(n, mu, st, False, False) for n, mu in mus for st in ("bf16", "e4m3fn")]
+    cases += [("90% skewed columns", -1.2816, "bf16", True, False)]
+    cases += [(n, mu, st, False, True) for n, mu in mus[:3:2] for st in ("bf16", "e4m3fn")]
+    for name, mu, storage, skew, pack in cases:
         g = torch.Generator(device=dev).manual_seed(0)
         pre = torch.randn((M, N), device=dev, generator=g) + mu
         if skew:
@@ -329,16 +331,16 @@ def bench_sweep(steps: int, warmup: int):
         del pre
         fp8 = storage == "e4m3fn"
         vdt = torch.float8_e4m3fn if fp8 else torch.bfloat16
-        buf = TensorBuffer(M * N * (1 if fp8 else 2), device=dev, dtype=vdt)
+        buf = TensorBuffer(M * N * (1 if fp8 else 2), device=dev, dtype=vdt, pack_sbit=pack)
         outd = torch.empty((M, N), device=dev, dtype=vdt)
         holder = {}
 
         def comp():
             buf.reset_buffer()
             if fp8:
-                holder["sp"] = quantize_and_compress(x, buf)[2]
+                holder["sp"] = quantize_and_compress(x, buf, pack_sbit=pack)[2]
             else:
-                holder["sp"] = dense_to_tilesparse(x, None, buf)
+                holder["sp"] = dense_to_tilesparse(x, None, buf, pack_sbit=pack)
 
         def decomp():
             unpack_batch_(holder["sp"], outd, 0, gn, N, M, gm * gn)
@@ -349,9 +351,13 @@ def bench_sweep(steps: int, warmup: int):
         nnz = int(sp.prefix[-1].item())
         vb = 1 if fp8 else 2
         cb, db = codec_bytes(M, N, nnz, vb_in=2, vb=vb, vb_out=vb)
+        if pack:   # algorithmic value bytes of the stream: nnz * b / 8
+            dv = nnz * vb - (nnz * (7 if fp8 else 15) + 7) // 8
+            cb, db = cb - dv, db - dv
         if fp8:
             cb += 2 * M * N   # the amax pass reads the bf16 input once more
-        out.append({"case": name, "storage": storage, "sparsity": round(1 - nnz / (M * N), 4),
+        out.append({"case": name, "storage": storage + (" pack_sbit" if pack else ""),
+                    "sparsity": round(1 - nnz / (M * N), 4),
                     "compress_ms": round(tc, 4), "decompress_ms": round(td, 4),
                     "compress_gbs": round(cb / (tc * 1e6), 1), "decompress_gbs": round(db / (td * 1e6), 1),
                     "roundtrip_gbs": round((cb + db) / ((tc + td) * 1e6), 1),

@@ -11,6 +11,8 @@
 #include "bs_device.h"
 #include "bs_host.h"
 
+#include <algorithm>
+
 
 namespace bs {
 
@@ -680,6 +682,58 @@ void compress_stream_kernel(CompressArgs a)
 }
 
 // ===========================================================================
+// bitstream packing (pack_sbit storage)
+//
+// Value i of a packed stream occupies stream bits [i*PB, (i+1)*PB), LSB first
+// (byte i*PB/8 holds the low bits); the payload is the low PB bits of the
+// stored value (15 for bf16, 7 for fp8: the sign bit of a ReLU value is 0).
+// The kernel packs raw[0, count) to stream indices [start, start + count):
+// one thread per output dword, each gathering the <= 3 (bf16) / <= 6 (fp8)
+// values that overlap it.  Dwords shared with bits outside the run keep those
+// bits (atomicAnd of the run's bit mask complement, then atomicOr of the
+// run's bits: concurrent writers of disjoint bits commute).
+// ===========================================================================
+template <int VB, int PB>
+__global__ __launch_bounds__(256) void pack_bits_kernel(const uint8_t* raw, const uint32_t* count_ptr,
+                                                        int64_t count_max, uint32_t* out, int64_t out_words,
+                                                        const int64_t* start_ptr, int32_t* err)
+{
+    const int64_t start = start_ptr ? *start_ptr : 0;
+    int64_t count = count_max;
+    if (count_ptr) count = min((int64_t)*count_ptr, count_max);
+    if (start < 0) {
+        if (err && blockIdx.x == 0 && threadIdx.x == 0) atomicOr(err, 2);
+        return;
+    }
+    const int64_t S = start * PB, E = (start + count) * PB;   // stream bits of the run
+    const int64_t D0 = S >> 5, D1 = (E + 31) >> 5;            // output dwords it touches
+    for (int64_t D = D0 + (int64_t)blockIdx.x * 256 + threadIdx.x; D < D1; D += (int64_t)gridDim.x * 256) {
+        if (D >= out_words) {                                  // past the storage: drop, flag
+            if (err) atomicOr(err, 1);
+            break;
+        }
+        const int64_t lo = max(D * 32, S), hi = min(D * 32 + 32, E);
+        const int64_t v0 = (lo - S) / PB, v1 = (hi - 1 - S) / PB;
+        uint64_t acc = 0;
+        for (int64_t v = v0; v <= v1; v++) {
+            const uint32_t x = (VB == 2 ? (uint32_t)reinterpret_cast<const uint16_t*>(raw)[v] : (uint32_t)raw[v]) &
+                               ((1u << PB) - 1u);
+            const int64_t pos = S + v * PB - D * 32;           // > -PB
+            acc |= pos >= 0 ? ((uint64_t)x << pos) : ((uint64_t)x >> (-pos));
+        }
+        const uint32_t word = (uint32_t)acc;
+        const uint32_t lb = (uint32_t)(lo - D * 32), hb = (uint32_t)(hi - D * 32);   // 0 <= lb < hb <= 32
+        const uint32_t mask = (hb == 32u ? 0xffffffffu : ((1u << hb) - 1u)) & ~((1u << lb) - 1u);
+        if (mask == 0xffffffffu) {
+            out[D] = word;
+        } else {
+            atomicAnd(&out[D], ~mask);
+            atomicOr(&out[D], word & mask);
+        }
+    }
+}
+
+// ===========================================================================
 // tile_pack: bitmask + int32 counts (reference API shape)
 // ===========================================================================
 template <int IN_T, bool VEC>
@@ -804,14 +858,47 @@ __device__ __forceinline__ int stage_run(const GatherArgs& a, int64_t run0, int6
     return p;
 }
 
+// Packed variant: stage the stream bytes holding bits [run0*PB, run1*PB) of
+// a PB-bit value stream (vals_numel = stream bytes) from a 16-byte aligned
+// byte, plus one more 16-byte slot so two-dword reads never leave the staged
+// data.  Returns the bit position of value run0 inside the staged bytes.
+template <int PB>
+__device__ __forceinline__ int stage_run_packed(const GatherArgs& a, int64_t run0, int64_t run1,
+                                                int64_t max_count, uint8_t* s_vals, int tid)
+{
+    int64_t cnt64 = run1 - run0;
+    cnt64 = cnt64 < 0 ? 0 : (cnt64 > max_count ? max_count : cnt64);
+    const int64_t bit0 = run0 * PB;
+    const int64_t sb = (bit0 >> 3) & ~(int64_t)15;                 // first staged byte
+    const int64_t eb = (bit0 + cnt64 * PB + 7) >> 3;               // one past the last needed byte
+    const int nslots = (int)((eb - sb + 15) >> 4) + 1;
+    for (int s = tid; s < nslots; s += kThreads) {
+        const int64_t b0 = sb + (int64_t)s * 16;
+        uint4 v = {0u, 0u, 0u, 0u};
+        if (b0 >= 0 && b0 + 16 <= a.vals_numel) {
+            v = *reinterpret_cast<const uint4*>(a.vals + b0);
+        } else {
+            for (int e = 0; e < 16; e++) {
+                const int64_t i = b0 + e;
+                if (i >= 0 && i < a.vals_numel) {
+                    uint32_t* w = e < 4 ? &v.x : e < 8 ? &v.y : e < 12 ? &v.z : &v.w;
+                    *w |= (uint32_t)a.vals[i] << ((e & 3) * 8);
+                }
+            }
+        }
+        *reinterpret_cast<uint4*>(s_vals + s * 16) = v;
+    }
+    return (int)(bit0 - sb * 8);
+}
+
 // Shared front half of decompress and relu2_grad: bitmask bytes, in-tile
 // ranks, run staging.  Fills m[][], r0[][] (LDS element index of each chunk's
 // first value) and returns after a barrier.
-template <int VB, int U>
-__device__ __forceinline__ void gather_prepare(const GatherArgs& a, uint32_t t0, int ntiles,
-                                               uint32_t (&m)[U][2], uint32_t (&r0)[U][2],
-                                               uint32_t* s_pref, uint32_t (*s_wtot)[2][4],
-                                               uint8_t* s_vals, int tid)
+template <int VB, int PB, int U>
+__device__ __forceinline__ int gather_prepare(const GatherArgs& a, uint32_t t0, int ntiles,
+                                              uint32_t (&m)[U][2], uint32_t (&r0)[U][2],
+                                              uint32_t* s_pref, uint32_t (*s_wtot)[2][4],
+                                              uint8_t* s_vals, int tid)
 {
     const int wave = tid >> 6, lane = tid & 63;
 #pragma unroll
@@ -832,8 +919,12 @@ __device__ __forceinline__ void gather_prepare(const GatherArgs& a, uint32_t t0,
     __syncthreads();
     const int64_t vo = a.vals_offset ? *a.vals_offset : 0;
     const uint32_t pb = s_pref[0];
-    const int p = stage_run<VB>(a, vo + pb, vo + s_pref[ntiles], (int64_t)ntiles * kTileNumel,
-                                s_vals, tid);
+    int p = 0, bitbase = 0;
+    if constexpr (PB > 0)
+        bitbase = stage_run_packed<PB>(a, vo + pb, vo + s_pref[ntiles], (int64_t)ntiles * kTileNumel,
+                                       s_vals, tid);
+    else
+        p = stage_run<VB>(a, vo + pb, vo + s_pref[ntiles], (int64_t)ntiles * kTileNumel, s_vals, tid);
 #pragma unroll
     for (int j = 0; j < U; j++) {
         uint32_t tb = j < ntiles ? min(s_pref[j] - pb, (uint32_t)(j * kTileNumel)) : 0u;
@@ -848,13 +939,23 @@ __device__ __forceinline__ void gather_prepare(const GatherArgs& a, uint32_t t0,
         r0[j][1] = (uint32_t)p + tb + h0 + h1w + ex[j][1];
     }
     __syncthreads();
+    return bitbase;
 }
 
-template <int V_T>
-__device__ __forceinline__ uint32_t lds_val(const uint8_t* s_vals, uint32_t i)
+// Stored bits of the i-th staged value.  Packed (PB > 0): bits
+// [bitbase + i*PB, +PB) of the staged stream, from two aligned dword reads.
+template <int V_T, int PB>
+__device__ __forceinline__ uint32_t lds_val(const uint8_t* s_vals, uint32_t i, int bitbase)
 {
-    if constexpr (V_T == DT_BF16) return reinterpret_cast<const uint16_t*>(s_vals)[i];
-    else return s_vals[i];
+    if constexpr (PB > 0) {
+        const uint32_t bit = (uint32_t)bitbase + i * PB;
+        const uint32_t* w = reinterpret_cast<const uint32_t*>(s_vals) + (bit >> 5);
+        return __builtin_amdgcn_alignbit(w[1], w[0], bit & 31u) & ((1u << PB) - 1u);
+    } else if constexpr (V_T == DT_BF16) {
+        return reinterpret_cast<const uint16_t*>(s_vals)[i];
+    } else {
+        return s_vals[i];
+    }
 }
 
 // k*v*v as bf16 bits: bf16 storage squares in bf16 ((k*v) rounded, then *v
@@ -879,21 +980,24 @@ __device__ __forceinline__ float val_f32(uint32_t raw)
     else return fp8_to_f32<V_T>(raw);
 }
 
-template <int V_T, bool SQUARE, bool HAS_SCALE, bool VEC, int U>
+template <int V_T, bool SQUARE, bool HAS_SCALE, bool VEC, int U, bool PACKED>
 __global__ __launch_bounds__(kThreads) void decompress_kernel(GatherArgs a)
 {
     constexpr int VB = V_T == DT_BF16 ? 2 : 1;
+    constexpr int PB = PACKED ? (V_T == DT_BF16 ? 15 : 7) : 0;
     constexpr int OB = SQUARE ? 2 : VB;
     __shared__ uint32_t s_pref[U + 1];
     __shared__ uint32_t s_wtot[U][2][4];
-    __shared__ __align__(16) uint8_t s_vals[U * kTileNumel * VB + 16];
+    // raw run: 16-byte phase + the run; packed run: 16-byte phase, the run
+    // (PB/8 < VB bytes per value) and a guard slot
+    __shared__ __align__(16) uint8_t s_vals[U * kTileNumel * VB + 32];
     const int tid = threadIdx.x;
     const uint32_t pid0 = blockIdx.x * U;
     const int ntiles = (int)min((uint32_t)U, a.num_tiles - pid0);
     const uint32_t t0 = (uint32_t)a.first_m_tile * a.grid_n + pid0;
 
     uint32_t m[U][2], r0[U][2];
-    gather_prepare<VB, U>(a, t0, ntiles, m, r0, s_pref, s_wtot, s_vals, tid);
+    const int bitbase = gather_prepare<VB, PB, U>(a, t0, ntiles, m, r0, s_pref, s_wtot, s_vals, tid);
 
     float s2b = 1.0f;
     if constexpr (HAS_SCALE) {
@@ -912,7 +1016,7 @@ __global__ __launch_bounds__(kThreads) void decompress_kernel(GatherArgs a)
             for (int e = 0; e < 8; e++) {
                 uint32_t x = 0;
                 if ((mm >> e) & 1u) {
-                    x = lds_val<V_T>(s_vals, r++);
+                    x = lds_val<V_T, PB>(s_vals, r++, bitbase);
                     if constexpr (SQUARE) x = relu2_square<V_T>(x, a.relu2_scale);
                 }
                 if constexpr (HAS_SCALE) x = f32_to_bf16(bf16_to_f32(x) * s2b);
@@ -926,13 +1030,14 @@ __global__ __launch_bounds__(kThreads) void decompress_kernel(GatherArgs a)
 }
 
 // grad = bit ? bf16(grad * (2k * r)) : 0, then optionally grad = bf16(grad * bf16(scale))
-template <int V_T, bool HAS_SCALE, bool VEC, int U>
+template <int V_T, bool HAS_SCALE, bool VEC, int U, bool PACKED>
 __global__ __launch_bounds__(kThreads) void relu2_grad_kernel(GatherArgs a)
 {
     constexpr int VB = V_T == DT_BF16 ? 2 : 1;
+    constexpr int PB = PACKED ? (V_T == DT_BF16 ? 15 : 7) : 0;
     __shared__ uint32_t s_pref[U + 1];
     __shared__ uint32_t s_wtot[U][2][4];
-    __shared__ __align__(16) uint8_t s_vals[U * kTileNumel * VB + 16];
+    __shared__ __align__(16) uint8_t s_vals[U * kTileNumel * VB + 32];
     const int tid = threadIdx.x;
     const uint32_t t0 = blockIdx.x * U;
     const int ntiles = (int)min((uint32_t)U, a.num_tiles - t0);
@@ -951,7 +1056,7 @@ __global__ __launch_bounds__(kThreads) void relu2_grad_kernel(GatherArgs a)
             }
         }
     uint32_t m[U][2], r0[U][2];
-    gather_prepare<VB, U>(a, t0, ntiles, m, r0, s_pref, s_wtot, s_vals, tid);
+    const int bitbase = gather_prepare<VB, PB, U>(a, t0, ntiles, m, r0, s_pref, s_wtot, s_vals, tid);
 
     float sb = 1.0f;
     if constexpr (HAS_SCALE) sb = bf16_to_f32(f32_to_bf16(*a.scale));
@@ -968,7 +1073,7 @@ __global__ __launch_bounds__(kThreads) void relu2_grad_kernel(GatherArgs a)
             for (int e = 0; e < 8; e++) {
                 uint32_t x = 0;
                 if ((mm >> e) & 1u) {
-                    float rv = val_f32<V_T>(lds_val<V_T>(s_vals, r++));
+                    float rv = val_f32<V_T>(lds_val<V_T, PB>(s_vals, r++, bitbase));
                     x = f32_to_bf16(bf16_to_f32(get16(g[j][h], e)) * (k2 * rv));
                 }
                 if constexpr (HAS_SCALE) x = f32_to_bf16(bf16_to_f32(x) * sb);
@@ -1263,44 +1368,44 @@ extern "C" int bs_prefix_from_counts(const int32_t* tile_counts, int64_t T, uint
     return BS_OK;
 }
 
-template <int V_T, bool SQ, bool SC>
+template <int V_T, bool SQ, bool SC, bool PK>
 static void launch_decompress_t(const GatherArgs& a, bool vec, hipStream_t st)
 {
     const uint32_t blocks = (a.num_tiles + kGatherU - 1) / kGatherU;
     if (vec)
-        hipLaunchKernelGGL((decompress_kernel<V_T, SQ, SC, true, kGatherU>), dim3(blocks), dim3(kThreads), 0, st, a);
+        hipLaunchKernelGGL((decompress_kernel<V_T, SQ, SC, true, kGatherU, PK>), dim3(blocks), dim3(kThreads), 0, st, a);
     else
-        hipLaunchKernelGGL((decompress_kernel<V_T, SQ, SC, false, kGatherU>), dim3(blocks), dim3(kThreads), 0, st, a);
+        hipLaunchKernelGGL((decompress_kernel<V_T, SQ, SC, false, kGatherU, PK>), dim3(blocks), dim3(kThreads), 0, st, a);
 }
 
-template <int V_T>
+template <int V_T, bool PK>
 static void launch_decompress_v(const GatherArgs& a, bool sq, bool sc, bool vec, hipStream_t st)
 {
-    if (!sq) launch_decompress_t<V_T, false, false>(a, vec, st);
-    else if (!sc) launch_decompress_t<V_T, true, false>(a, vec, st);
-    else launch_decompress_t<V_T, true, true>(a, vec, st);
+    if (!sq) launch_decompress_t<V_T, false, false, PK>(a, vec, st);
+    else if (!sc) launch_decompress_t<V_T, true, false, PK>(a, vec, st);
+    else launch_decompress_t<V_T, true, true, PK>(a, vec, st);
 }
 
 static int check_gather(const void* vals, int vals_dtype, int64_t vals_numel, const uint8_t* bitmask,
-                        const uint32_t* prefix, const char* what)
+                        const uint32_t* prefix, const char* what, bool packed = false)
 {
     if (vals_dtype < 0 || vals_dtype > 2) return set_error(BS_ERR_INVALID, "%s: unknown dtype %d", what, vals_dtype);
     if (vals_numel < 0) return set_error(BS_ERR_INVALID, "%s: negative vals_numel", what);
     if (bitmask == nullptr || prefix == nullptr) return set_error(BS_ERR_INVALID, "%s: null bitmask/prefix", what);
     if (vals_numel > 0 && vals == nullptr) return set_error(BS_ERR_INVALID, "%s: null vals", what);
-    int vb = vals_dtype == DT_BF16 ? 2 : 1;
+    int vb = (vals_dtype == DT_BF16 && !packed) ? 2 : 1;
     if (((uintptr_t)vals) % vb) return set_error(BS_ERR_INVALID, "%s: vals misaligned", what);
     return BS_OK;
 }
 
-extern "C" int bs_decompress(const void* vals, int vals_dtype, int64_t vals_numel, const uint8_t* bitmask,
-                             const uint32_t* prefix, const int64_t* vals_offset, void* out,
-                             int64_t first_m_tile, int64_t grid_n, int64_t K, int64_t batch_rows,
-                             int64_t num_tiles_in_batch, int square, float relu2_scale, const float* scale,
-                             void* stream)
+static int decompress_impl(const void* vals, int vals_dtype, int64_t vals_numel, const uint8_t* bitmask,
+                           const uint32_t* prefix, const int64_t* vals_offset, void* out,
+                           int64_t first_m_tile, int64_t grid_n, int64_t K, int64_t batch_rows,
+                           int64_t num_tiles_in_batch, int square, float relu2_scale, const float* scale,
+                           void* stream, bool packed)
 {
     clear_error();
-    if (int rc = check_gather(vals, vals_dtype, vals_numel, bitmask, prefix, "bs_decompress")) return rc;
+    if (int rc = check_gather(vals, vals_dtype, vals_numel, bitmask, prefix, "bs_decompress", packed)) return rc;
     if (grid_n <= 0 || K < 0 || batch_rows < 0 || num_tiles_in_batch < 0 || first_m_tile < 0)
         return set_error(BS_ERR_INVALID, "bs_decompress: bad batch geometry");
     if (num_tiles_in_batch == 0 || K == 0 || batch_rows == 0) return BS_OK;
@@ -1327,14 +1432,46 @@ extern "C" int bs_decompress(const void* vals, int vals_dtype, int64_t vals_nume
     a.scale = scale;
     bool vec = (K % 8 == 0) && (((uintptr_t)out) % (8 * ob) == 0);
     hipStream_t st = (hipStream_t)stream;
+    const bool sc = scale != nullptr;
     switch (vals_dtype) {
-    case DT_BF16: launch_decompress_v<DT_BF16>(a, square, scale != nullptr, vec, st); break;
-    case DT_E4M3FN: launch_decompress_v<DT_E4M3FN>(a, square, scale != nullptr, vec, st); break;
-    default: launch_decompress_v<DT_E5M2>(a, square, scale != nullptr, vec, st); break;
+    case DT_BF16:
+        if (packed) launch_decompress_v<DT_BF16, true>(a, square, sc, vec, st);
+        else launch_decompress_v<DT_BF16, false>(a, square, sc, vec, st);
+        break;
+    case DT_E4M3FN:
+        if (packed) launch_decompress_v<DT_E4M3FN, true>(a, square, sc, vec, st);
+        else launch_decompress_v<DT_E4M3FN, false>(a, square, sc, vec, st);
+        break;
+    default:
+        if (packed) launch_decompress_v<DT_E5M2, true>(a, square, sc, vec, st);
+        else launch_decompress_v<DT_E5M2, false>(a, square, sc, vec, st);
+        break;
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(BS_ERR_HIP, "bs_decompress launch: %s", hipGetErrorString(e));
     return BS_OK;
+}
+
+extern "C" int bs_decompress(const void* vals, int vals_dtype, int64_t vals_numel, const uint8_t* bitmask,
+                             const uint32_t* prefix, const int64_t* vals_offset, void* out,
+                             int64_t first_m_tile, int64_t grid_n, int64_t K, int64_t batch_rows,
+                             int64_t num_tiles_in_batch, int square, float relu2_scale, const float* scale,
+                             void* stream)
+{
+    return decompress_impl(vals, vals_dtype, vals_numel, bitmask, prefix, vals_offset, out, first_m_tile,
+                           grid_n, K, batch_rows, num_tiles_in_batch, square, relu2_scale, scale, stream, false);
+}
+
+extern "C" int bs_decompress_packed(const void* stream_bytes, int vals_dtype, int64_t stream_nbytes,
+                                    const uint8_t* bitmask, const uint32_t* prefix,
+                                    const int64_t* vals_offset, void* out, int64_t first_m_tile,
+                                    int64_t grid_n, int64_t K, int64_t batch_rows,
+                                    int64_t num_tiles_in_batch, int square, float relu2_scale,
+                                    const float* scale, void* stream)
+{
+    return decompress_impl(stream_bytes, vals_dtype, stream_nbytes, bitmask, prefix, vals_offset, out,
+                           first_m_tile, grid_n, K, batch_rows, num_tiles_in_batch, square, relu2_scale,
+                           scale, stream, true);
 }
 
 extern "C" int bs_relu_grad(void* grad, int64_t M, int64_t N, const uint8_t* bitmask, void* stream)
@@ -1362,22 +1499,30 @@ extern "C" int bs_relu_grad(void* grad, int64_t M, int64_t N, const uint8_t* bit
     return BS_OK;
 }
 
-template <int V_T, bool SC>
+template <int V_T, bool SC, bool PK>
 static void launch_relu2_t(const GatherArgs& a, bool vec, hipStream_t st)
 {
     const uint32_t blocks = (a.num_tiles + kGatherU - 1) / kGatherU;
     if (vec)
-        hipLaunchKernelGGL((relu2_grad_kernel<V_T, SC, true, kGatherU>), dim3(blocks), dim3(kThreads), 0, st, a);
+        hipLaunchKernelGGL((relu2_grad_kernel<V_T, SC, true, kGatherU, PK>), dim3(blocks), dim3(kThreads), 0, st, a);
     else
-        hipLaunchKernelGGL((relu2_grad_kernel<V_T, SC, false, kGatherU>), dim3(blocks), dim3(kThreads), 0, st, a);
+        hipLaunchKernelGGL((relu2_grad_kernel<V_T, SC, false, kGatherU, PK>), dim3(blocks), dim3(kThreads), 0, st, a);
 }
 
-extern "C" int bs_relu2_grad(void* grad, int64_t M, int64_t N, const void* vals, int vals_dtype,
-                             int64_t vals_numel, const uint8_t* bitmask, const uint32_t* prefix,
-                             const int64_t* vals_offset, float relu2_scale, const float* scale, void* stream)
+template <int V_T, bool PK>
+static void launch_relu2_v(const GatherArgs& a, bool sc, bool vec, hipStream_t st)
+{
+    if (sc) launch_relu2_t<V_T, true, PK>(a, vec, st);
+    else launch_relu2_t<V_T, false, PK>(a, vec, st);
+}
+
+static int relu2_grad_impl(void* grad, int64_t M, int64_t N, const void* vals, int vals_dtype,
+                           int64_t vals_numel, const uint8_t* bitmask, const uint32_t* prefix,
+                           const int64_t* vals_offset, float relu2_scale, const float* scale, void* stream,
+                           bool packed)
 {
     clear_error();
-    if (int rc = check_gather(vals, vals_dtype, vals_numel, bitmask, prefix, "bs_relu2_grad")) return rc;
+    if (int rc = check_gather(vals, vals_dtype, vals_numel, bitmask, prefix, "bs_relu2_grad", packed)) return rc;
     if (M < 0 || N < 0) return set_error(BS_ERR_INVALID, "bs_relu2_grad: negative shape");
     const int64_t T = ((M + 63) / 64) * ((N + 63) / 64);
     if (T == 0) return BS_OK;
@@ -1401,13 +1546,70 @@ extern "C" int bs_relu2_grad(void* grad, int64_t M, int64_t N, const void* vals,
     a.scale = scale;
     bool vec = (N % 8 == 0) && aligned16(grad);
     hipStream_t st = (hipStream_t)stream;
-    bool sc = scale != nullptr;
+    const bool sc = scale != nullptr;
     switch (vals_dtype) {
-    case DT_BF16: if (sc) launch_relu2_t<DT_BF16, true>(a, vec, st); else launch_relu2_t<DT_BF16, false>(a, vec, st); break;
-    case DT_E4M3FN: if (sc) launch_relu2_t<DT_E4M3FN, true>(a, vec, st); else launch_relu2_t<DT_E4M3FN, false>(a, vec, st); break;
-    default: if (sc) launch_relu2_t<DT_E5M2, true>(a, vec, st); else launch_relu2_t<DT_E5M2, false>(a, vec, st); break;
+    case DT_BF16:
+        if (packed) launch_relu2_v<DT_BF16, true>(a, sc, vec, st);
+        else launch_relu2_v<DT_BF16, false>(a, sc, vec, st);
+        break;
+    case DT_E4M3FN:
+        if (packed) launch_relu2_v<DT_E4M3FN, true>(a, sc, vec, st);
+        else launch_relu2_v<DT_E4M3FN, false>(a, sc, vec, st);
+        break;
+    default:
+        if (packed) launch_relu2_v<DT_E5M2, true>(a, sc, vec, st);
+        else launch_relu2_v<DT_E5M2, false>(a, sc, vec, st);
+        break;
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(BS_ERR_HIP, "bs_relu2_grad launch: %s", hipGetErrorString(e));
+    return BS_OK;
+}
+
+extern "C" int bs_relu2_grad(void* grad, int64_t M, int64_t N, const void* vals, int vals_dtype,
+                             int64_t vals_numel, const uint8_t* bitmask, const uint32_t* prefix,
+                             const int64_t* vals_offset, float relu2_scale, const float* scale, void* stream)
+{
+    return relu2_grad_impl(grad, M, N, vals, vals_dtype, vals_numel, bitmask, prefix, vals_offset,
+                           relu2_scale, scale, stream, false);
+}
+
+extern "C" int bs_relu2_grad_packed(void* grad, int64_t M, int64_t N, const void* stream_bytes,
+                                    int vals_dtype, int64_t stream_nbytes, const uint8_t* bitmask,
+                                    const uint32_t* prefix, const int64_t* vals_offset, float relu2_scale,
+                                    const float* scale, void* stream)
+{
+    return relu2_grad_impl(grad, M, N, stream_bytes, vals_dtype, stream_nbytes, bitmask, prefix, vals_offset,
+                           relu2_scale, scale, stream, true);
+}
+
+extern "C" int bs_pack_bits(const void* raw, int vals_dtype, const uint32_t* count_ptr, int64_t count_max,
+                            void* stream_bytes, int64_t stream_nbytes, const int64_t* start_index,
+                            int32_t* err_flags, void* stream)
+{
+    clear_error();
+    if (vals_dtype < 0 || vals_dtype > 2) return set_error(BS_ERR_INVALID, "bs_pack_bits: unknown dtype %d", vals_dtype);
+    if (count_max < 0 || stream_nbytes < 0) return set_error(BS_ERR_INVALID, "bs_pack_bits: negative size");
+    if (count_max == 0) return BS_OK;
+    if (raw == nullptr || stream_bytes == nullptr) return set_error(BS_ERR_INVALID, "bs_pack_bits: null pointer");
+    const int vb = vals_dtype == DT_BF16 ? 2 : 1, pb = vals_dtype == DT_BF16 ? 15 : 7;
+    if (((uintptr_t)raw) % vb) return set_error(BS_ERR_INVALID, "bs_pack_bits: raw values misaligned");
+    if (((uintptr_t)stream_bytes) & 3u) return set_error(BS_ERR_INVALID, "bs_pack_bits: stream not 4-byte aligned");
+    if (count_max > (int64_t)1 << 40) return set_error(BS_ERR_INVALID, "bs_pack_bits: count too large");
+    // dwords a run of count_max values can touch, whatever its start
+    const int64_t words = (count_max * pb + 62) / 32 + 1;
+    const uint32_t blocks = (uint32_t)std::min<int64_t>((words + 255) / 256, 65535);
+    hipStream_t st = (hipStream_t)stream;
+    const uint8_t* r = (const uint8_t*)raw;
+    uint32_t* o = (uint32_t*)stream_bytes;
+    const int64_t ow = stream_nbytes / 4;
+    if (vals_dtype == DT_BF16)
+        hipLaunchKernelGGL((pack_bits_kernel<2, 15>), dim3(blocks), dim3(256), 0, st, r, count_ptr, count_max, o, ow,
+                           start_index, err_flags);
+    else
+        hipLaunchKernelGGL((pack_bits_kernel<1, 7>), dim3(blocks), dim3(256), 0, st, r, count_ptr, count_max, o, ow,
+                           start_index, err_flags);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(BS_ERR_HIP, "bs_pack_bits launch: %s", hipGetErrorString(e));
     return BS_OK;
 }

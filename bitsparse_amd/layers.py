@@ -38,7 +38,7 @@ class ReluLinear(Function):
         if is_fp8(dtype):
             if dtype != torch.float8_e4m3fn:
                 raise TypeError("fp8 activation storage is float8_e4m3fn")
-            h, scale, h_sparse = quantize_and_compress(h, sparse_data)
+            h, scale, h_sparse = quantize_and_compress(h, sparse_data, pack_sbit)
         else:
             scale = None
             h_sparse = dense_to_tilesparse(h, scale, sparse_data, pack_sbit)
@@ -110,7 +110,7 @@ class Relu2Linear(Function):
         if is_fp8(storage_dtype):
             if storage_dtype != torch.float8_e4m3fn:
                 raise TypeError("fp8 activation storage is float8_e4m3fn")
-            _, scale, h_sparse = quantize_and_compress(h, sparse_data)
+            _, scale, h_sparse = quantize_and_compress(h, sparse_data, pack_sbit)
         else:
             h_sparse = dense_to_tilesparse(h, None, sparse_data, pack_sbit)
         ctx.h_sparse = h_sparse

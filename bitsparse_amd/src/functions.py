@@ -9,6 +9,11 @@ Mirrors reference lib_sparse/src/functions.py:23-99.  Two execution paths:
   host reads nnz (one sync, as the reference does at
   triton_operators.py:50), allocates exactly nnz values, and a compact pass
   fills them.
+
+With ``pack_sbit`` the values are compacted into a raw staging buffer and
+packed into the 15/7-bit stream (``bitpacking.pack_bits``); a TensorBuffer
+cursor is first rounded up to a multiple of 8 values (functions.py:78-81),
+so activations never share stream bytes.
 """
 from __future__ import annotations
 
@@ -18,6 +23,7 @@ import torch
 from torch import Tensor
 
 from . import hip_operators as ops
+from .bitpacking import pack_bits
 from ..bitsparse import BitsparseTensor, TensorBuffer, tile_grid
 from ..config import BLOCK_M, BLOCK_N
 from ..fp8 import is_fp8
@@ -63,8 +69,6 @@ def dense_to_tilesparse(
     ``scale`` is carried as metadata (fp8 storage); values are stored bit for
     bit in ``dense``'s dtype.  Reference: functions.py:55-99.
     """
-    if pack_sbit:
-        raise NotImplementedError(ops._SBIT_MSG)
     _check_input(dense)
     ops.require_device(dense, "dense_to_tilesparse")
     dense = dense.contiguous()
@@ -80,8 +84,9 @@ def dense_to_tilesparse(
                                grid_m, grid_n, BLOCK_M, BLOCK_N, scale=scale,
                                vals_offset=vals_offset, pack_sbit=pack_sbit)
 
-    if sparse_data.pack_sbit:
-        raise NotImplementedError(ops._SBIT_MSG)
+    _check_buffer(sparse_data, dense.dtype, pack_sbit)
+    if pack_sbit:
+        return _compress_packed_into_buffer(dense, scale, sparse_data)
     if sparse_data.vals.dtype != dense.dtype:
         raise TypeError(f"TensorBuffer stores {sparse_data.vals.dtype} but the input is {dense.dtype}")
     bitmask = torch.empty(num_tiles * TILE_BYTES, device=dense.device, dtype=torch.uint8)
@@ -96,8 +101,36 @@ def dense_to_tilesparse(
                            vals_offset=vals_offset, pack_sbit=pack_sbit)
 
 
+def _check_buffer(buf: TensorBuffer, dtype: torch.dtype, pack_sbit: bool) -> None:
+    if bool(buf.pack_sbit) != bool(pack_sbit):
+        raise ValueError(f"TensorBuffer(pack_sbit={buf.pack_sbit}) used with pack_sbit={pack_sbit}")
+    if pack_sbit and buf.dtype != dtype:
+        raise TypeError(f"packed TensorBuffer holds {buf.dtype} values but the input is {dtype}")
+
+
+def _compress_packed_into_buffer(dense: Tensor, scale: Tensor | None, buf: TensorBuffer,
+                                 **quant) -> BitsparseTensor:
+    """Fused compress into a raw staging buffer, then pack at the 8-aligned
+    cursor; no host synchronisation.  ``quant`` forwards the quantise options
+    of ``compress_into`` (the staging then holds e4m3fn values)."""
+    M, N = dense.shape
+    grid_m, grid_n, num_tiles, TILE_NUMEL, TILE_BYTES = tile_grid(M, N, BLOCK_M, BLOCK_N)
+    stored = torch.float8_e4m3fn if quant.get("quantize") else dense.dtype
+    bitmask = torch.empty(num_tiles * TILE_BYTES, device=dense.device, dtype=torch.uint8)
+    prefix = torch.empty(num_tiles + 1, device=dense.device, dtype=torch.uint32)
+    staging = torch.empty(max(M * N, 1), device=dense.device, dtype=stored)
+    nnz = torch.empty(1, device=dense.device, dtype=torch.int64)
+    ops.compress_into(dense, bitmask, prefix, staging, None, nnz, None, write_vals=True, **quant)
+    vals_offset = (buf.offset + 7) // 8 * 8
+    pack_bits(staging, buf.vals, vals_offset, M * N, prefix[num_tiles:num_tiles + 1], buf.err_flags)
+    buf.offset = vals_offset + nnz
+    return BitsparseTensor(buf.vals, bitmask, prefix, dense.shape, stored,
+                           grid_m, grid_n, BLOCK_M, BLOCK_N, scale=scale,
+                           vals_offset=vals_offset, pack_sbit=True)
+
+
 def quantize_and_compress(
-    dense: Tensor, sparse_data: TensorBuffer | None = None,
+    dense: Tensor, sparse_data: TensorBuffer | None = None, pack_sbit: bool = False,
 ) -> tuple[Tensor, Tensor, BitsparseTensor]:
     """bf16 [M, N] -> (e4m3fn dense, fp32 scale, BitsparseTensor of the e4m3fn
     values) with one amax pass and one fused quantize+compress pass.
@@ -120,9 +153,15 @@ def quantize_and_compress(
         ops.compress_into(dense, bitmask, prefix, None, None, None, None, write_vals=False,
                           quantize=True, scale_out=scale, dense_q_out=q, amax_epoch=amax_epoch)
         vals, vals_offset = ops.compact_vals(q, bitmask, prefix, None, None, M, N, grid_n,
-                                             num_tiles, BLOCK_M, BLOCK_N, TILE_NUMEL, False)
+                                             num_tiles, BLOCK_M, BLOCK_N, TILE_NUMEL, pack_sbit)
         sp = BitsparseTensor(vals, bitmask, prefix, q.shape, q.dtype, grid_m, grid_n,
-                             BLOCK_M, BLOCK_N, scale=scale, vals_offset=vals_offset)
+                             BLOCK_M, BLOCK_N, scale=scale, vals_offset=vals_offset,
+                             pack_sbit=pack_sbit)
+        return q, scale, sp
+    _check_buffer(sparse_data, torch.float8_e4m3fn, pack_sbit)
+    if pack_sbit:
+        sp = _compress_packed_into_buffer(dense, scale, sparse_data, quantize=True, scale_out=scale,
+                                          dense_q_out=q, amax_epoch=amax_epoch)
         return q, scale, sp
     if sparse_data.vals.dtype != torch.float8_e4m3fn:
         raise TypeError(f"TensorBuffer stores {sparse_data.vals.dtype}, need float8_e4m3fn")

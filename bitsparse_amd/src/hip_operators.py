@@ -12,11 +12,9 @@ from torch import Tensor
 
 from .. import _lib
 from .._lib import check, ptr, require_device, stream_handle
-from ..bitsparse import BitsparseTensor, pack_codec
+from ..bitsparse import BitsparseTensor, bits_per_value, pack_codec
 from ..config import RELU2_SCALE
-
-_SBIT_MSG = ("pack_sbit=True (15/7-bit packed value stream) is not implemented in "
-             "bitsparse_amd yet; use raw storage (pack_sbit=False)")
+from .bitpacking import pack_bits, packed_storage_nbytes
 
 
 def dtype_code(dtype: torch.dtype) -> int:
@@ -72,12 +70,15 @@ def compact_vals(
     BLOCK_M: int, BLOCK_N: int, TILE_NUMEL: int, pack_sbit: bool,
 ) -> tuple[Tensor, Tensor]:
     """Compact positive values into standalone (vals=None: exact-size, after
-    one host sync for nnz) or preallocated storage.
-    Reference: triton_operators.py:36-115 (raw mode)."""
-    if pack_sbit:
-        raise NotImplementedError(_SBIT_MSG)
+    one host sync for nnz) or preallocated storage.  ``pack_sbit``: ``vals``
+    is the uint8 packed stream; the values are compacted into a raw staging
+    buffer and packed at ``vals_offset`` (a value index).
+    Reference: triton_operators.py:36-115."""
     require_device(dense, "compact_vals")
     _contig(dense, "dense")
+    if pack_sbit:
+        return _compact_vals_packed(dense, tile_bitmasks, tile_prefix, vals, vals_offset, M, N,
+                                    num_tiles)
     if vals is None:
         nnz = int(tile_prefix[-1].item())
         vals = torch.empty(nnz, device=dense.device, dtype=dense.dtype)
@@ -89,6 +90,31 @@ def compact_vals(
                             tile_bitmasks.data_ptr(), tile_prefix.data_ptr(),
                             vals.data_ptr(), vals.numel(), ptr(vals_offset), 0, num_tiles,
                             None, stream_handle(dense.device)), "bs_compact_vals")
+    return vals, vals_offset
+
+
+def _compact_vals_packed(dense: Tensor, tile_bitmasks: Tensor, tile_prefix: Tensor,
+                         vals: Tensor | None, vals_offset: Tensor | None,
+                         M: int, N: int, num_tiles: int) -> tuple[Tensor, Tensor]:
+    bits = bits_per_value(dense.dtype)
+    if vals is None:
+        nnz = int(tile_prefix[-1].item())
+        vals = torch.empty(packed_storage_nbytes(nnz, bits), device=dense.device, dtype=torch.uint8)
+        vals_offset = torch.zeros((), device=dense.device, dtype=torch.int64)
+        staging = torch.empty(max(nnz, 1), device=dense.device, dtype=dense.dtype)
+        count, count_t = nnz, None
+    else:
+        if vals.dtype != torch.uint8:
+            raise TypeError("compact_vals(pack_sbit=True): storage must be the uint8 packed stream")
+        # values of tiles [0, num_tiles) are prefix[num_tiles] - prefix[0] <= M*N
+        staging = torch.empty(max(M * N, 1), device=dense.device, dtype=dense.dtype)
+        count, count_t = M * N, tile_prefix[num_tiles:num_tiles + 1]
+    L = _lib.load()
+    check(L.bs_compact_vals(dense.data_ptr(), dtype_code(dense.dtype), M, N,
+                            tile_bitmasks.data_ptr(), tile_prefix.data_ptr(),
+                            staging.data_ptr(), staging.numel(), None, 0, num_tiles,
+                            None, stream_handle(dense.device)), "bs_compact_vals")
+    pack_bits(staging, vals, vals_offset, count, count_t)
     return vals, vals_offset
 
 
@@ -151,11 +177,10 @@ def quantize_e4m3fn(x: Tensor, amax_epoch: int) -> tuple[Tensor, Tensor]:
 # ---------------------------------------------------------------------------
 def _unpack(sparse: BitsparseTensor, output: Tensor, first_m_tile: int, grid_n: int, K: int,
             batch_rows: int, num_tiles_in_batch: int, square: bool, scale: Tensor | None) -> Tensor:
-    if sparse.pack_sbit:
-        raise NotImplementedError(_SBIT_MSG)
     require_device(output, "unpack")
     _contig(output, "output")
-    want = torch.bfloat16 if square else sparse.vals.dtype
+    stored = sparse.dtype if sparse.pack_sbit else sparse.vals.dtype
+    want = torch.bfloat16 if square else stored
     if output.dtype != want:
         raise TypeError(f"unpack: output dtype {output.dtype}, expected {want}")
     if output.numel() < batch_rows * K:
@@ -163,11 +188,12 @@ def _unpack(sparse: BitsparseTensor, output: Tensor, first_m_tile: int, grid_n: 
     if first_m_tile + (num_tiles_in_batch + grid_n - 1) // grid_n > sparse.grid_m:
         raise ValueError("unpack: tile batch runs past the tile grid")
     L = _lib.load()
-    check(L.bs_decompress(sparse.vals.data_ptr(), dtype_code(sparse.vals.dtype), sparse.vals.numel(),
-                          sparse.bitmask.data_ptr(), sparse.prefix.data_ptr(),
-                          sparse.vals_offset.data_ptr(), output.data_ptr(), first_m_tile, grid_n, K,
-                          batch_rows, num_tiles_in_batch, int(square), float(RELU2_SCALE),
-                          ptr(scale), stream_handle(output.device)), "bs_decompress")
+    fn = L.bs_decompress_packed if sparse.pack_sbit else L.bs_decompress
+    check(fn(sparse.vals.data_ptr(), dtype_code(stored), sparse.vals.numel(),
+             sparse.bitmask.data_ptr(), sparse.prefix.data_ptr(),
+             sparse.vals_offset.data_ptr(), output.data_ptr(), first_m_tile, grid_n, K,
+             batch_rows, num_tiles_in_batch, int(square), float(RELU2_SCALE),
+             ptr(scale), stream_handle(output.device)), "bs_decompress")
     return output
 
 
@@ -218,14 +244,13 @@ def mask_with_bitmask_(grad: Tensor, sparse: BitsparseTensor) -> Tensor:
 def relu2_grad_sparse_(grad: Tensor, sparse_z: BitsparseTensor) -> Tensor:
     """grad <- grad * 2k*r where set, 0 elsewhere, then * scale for fp8
     storage, in place.  Reference: triton_operators.py:178-202."""
-    if sparse_z.pack_sbit:
-        raise NotImplementedError(_SBIT_MSG)
     _check_grad(grad, sparse_z, "relu2_grad_sparse_")
     M, N = sparse_z.shape
     L = _lib.load()
-    check(L.bs_relu2_grad(grad.data_ptr(), M, N, sparse_z.vals.data_ptr(),
-                          dtype_code(sparse_z.vals.dtype), sparse_z.vals.numel(),
-                          sparse_z.bitmask.data_ptr(), sparse_z.prefix.data_ptr(),
-                          sparse_z.vals_offset.data_ptr(), float(RELU2_SCALE), ptr(sparse_z.scale),
-                          stream_handle(grad.device)), "bs_relu2_grad")
+    stored = sparse_z.dtype if sparse_z.pack_sbit else sparse_z.vals.dtype
+    fn = L.bs_relu2_grad_packed if sparse_z.pack_sbit else L.bs_relu2_grad
+    check(fn(grad.data_ptr(), M, N, sparse_z.vals.data_ptr(), dtype_code(stored),
+             sparse_z.vals.numel(), sparse_z.bitmask.data_ptr(), sparse_z.prefix.data_ptr(),
+             sparse_z.vals_offset.data_ptr(), float(RELU2_SCALE), ptr(sparse_z.scale),
+             stream_handle(grad.device)), "bs_relu2_grad")
     return grad

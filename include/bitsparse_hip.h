@@ -197,6 +197,46 @@ int bs_gemm_compressed_b(const void* At, int64_t M, int64_t K, int64_t ldat, con
                          int square, float relu2_scale, const float* b_scale, void* C,
                          void* workspace, int64_t workspace_bytes, void* stream);
 
+/*
+ * Packed value stream (pack_sbit storage, reference lib_sparse/src/bitpacking.py).
+ * Value i of a stream occupies stream bits [i*PB, (i+1)*PB), least significant
+ * bit first (byte i*PB/8 holds the low bits); PB = 15 for bf16 and 7 for fp8
+ * codes, the low PB bits of the stored value (a ReLU value's sign bit is 0).
+ * Storage is a byte array; readers may touch the 4 bytes after the payload
+ * (the reference's guard word, bitpacking.py:32-34).
+ */
+
+/*
+ * Pack raw values raw[0, count) (vals_dtype elements, the compacted output of
+ * bs_compress / bs_compact_vals) into stream indices [*start_index,
+ * *start_index + count) of `stream_bytes` (4-byte aligned, stream_nbytes
+ * bytes).  count = min(*count_ptr, count_max) when count_ptr (device uint32,
+ * e.g. prefix + T) is given, else count_max.  Stream bits outside the run
+ * keep their values; words past stream_nbytes are not written and bit 0 of
+ * *err_flags is set; a negative *start_index sets bit 1.
+ * Replaces lib_sparse/src/bitpacking.py:58-117 (_pack_kernel) as launched by
+ * triton_operators.py:61-105.
+ */
+int bs_pack_bits(const void* raw, int vals_dtype, const uint32_t* count_ptr, int64_t count_max,
+                 void* stream_bytes, int64_t stream_nbytes, const int64_t* start_index,
+                 int32_t* err_flags, void* stream);
+
+/*
+ * bs_decompress / bs_relu2_grad reading the values from a packed stream of
+ * stream_nbytes bytes; *vals_offset is a value index into the stream.
+ * Replace the pack_sbit branches of triton_kernels.py:186-187 and :320-321
+ * (load_packed_at_indices, bitpacking.py:37-55).
+ */
+int bs_decompress_packed(const void* stream_bytes, int vals_dtype, int64_t stream_nbytes,
+                         const uint8_t* bitmask, const uint32_t* prefix, const int64_t* vals_offset,
+                         void* out, int64_t first_m_tile, int64_t grid_n, int64_t K,
+                         int64_t batch_rows, int64_t num_tiles_in_batch, int square,
+                         float relu2_scale, const float* scale, void* stream);
+int bs_relu2_grad_packed(void* grad, int64_t M, int64_t N, const void* stream_bytes, int vals_dtype,
+                         int64_t stream_nbytes, const uint8_t* bitmask, const uint32_t* prefix,
+                         const int64_t* vals_offset, float relu2_scale, const float* scale,
+                         void* stream);
+
 /* Device pointer of the amax slot inside a workspace (for bs_compress). */
 const uint64_t* bs_workspace_amax_slot(const void* workspace, int64_t workspace_bytes);
 

@@ -351,3 +351,51 @@ int64_t or_compress(const void* dense, int dtype, int64_t M, int64_t N,
     or_compact(dense, dtype, M, N, bitmask, prefix, vals, vals_offset, 0, T);
     return (int64_t)prefix[T];
 }
+
+/* ------------------------------------------------------------------------ */
+/* packed value stream (pack_sbit)                                          */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * Pack raw[0, n) (bf16 uint16 or fp8 uint8 bit patterns, low `bits` bits
+ * each) into the byte stream at value index `start`: one output byte at a
+ * time, its bits gathered from the (at most two) values overlapping it, bytes
+ * shared with bits outside the run merged with their old content.  Follows
+ * reference lib_sparse/src/bitpacking.py:58-117 (_pack_kernel: relative_bit,
+ * value0 >> bit_offsets | value1 << (bits - bit_offsets), valid_lo/valid_hi
+ * merge).
+ */
+void or_pack_bits(const void* raw, int vdtype, int64_t n, int bits, uint8_t* stream, int64_t start)
+{
+    if (n <= 0) return;
+    int64_t start_bit = start * bits, end_bit = start_bit + n * bits;
+    int64_t first_byte = start_bit / 8, end_byte = (end_bit + 7) / 8;
+    for (int64_t ob = first_byte; ob < end_byte; ob++) {
+        int64_t relative_bit = ob * 8 - start_bit;
+        int64_t source_bit = relative_bit > 0 ? relative_bit : 0;
+        int64_t idx = source_bit / bits, off = source_bit % bits;
+        uint32_t v0 = 0, v1 = 0;
+        if (idx < n) v0 = vdtype == OR_BF16 ? ((const uint16_t*)raw)[idx] : ((const uint8_t*)raw)[idx];
+        if (idx + 1 < n) v1 = vdtype == OR_BF16 ? ((const uint16_t*)raw)[idx + 1] : ((const uint8_t*)raw)[idx + 1];
+        uint32_t mask = (1u << bits) - 1u;
+        v0 &= mask;
+        v1 &= mask;
+        uint32_t packed = (v0 >> off) | (v1 << (bits - off));
+        packed = (packed << (relative_bit < 0 ? -relative_bit : 0)) & 0xffu;
+        int64_t lo = start_bit - ob * 8, hi = end_bit - ob * 8;
+        lo = lo < 0 ? 0 : (lo > 8 ? 8 : lo);
+        hi = hi < 0 ? 0 : (hi > 8 ? 8 : hi);
+        uint32_t valid = ((1u << hi) - 1u) & ~((1u << lo) - 1u);
+        stream[ob] = (uint8_t)((stream[ob] & ~valid) | (packed & valid));
+    }
+}
+
+/* Value `idx` of a packed stream: two little-endian uint16 words, shifted
+ * and masked (reference bitpacking.py:37-55, load_packed_at_indices). */
+uint32_t or_unpack_bits_at(const uint8_t* stream, int bits, int64_t idx)
+{
+    int64_t word = (idx * bits) / 16, shift = (idx * bits) % 16;
+    uint32_t w0 = (uint32_t)stream[2 * word] | ((uint32_t)stream[2 * word + 1] << 8);
+    uint32_t w1 = (uint32_t)stream[2 * word + 2] | ((uint32_t)stream[2 * word + 3] << 8);
+    return ((w0 | (w1 << 16)) >> shift) & ((1u << bits) - 1u);
+}

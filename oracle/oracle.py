@@ -77,6 +77,8 @@ def lib():
                 "or_relu_grad": (None, [_ptr, _i64, _i64, _ptr]),
                 "or_relu2_grad": (None, [_ptr, _i64, _i64, _ptr, _int, _ptr, _ptr, _i64, _f32, _ptr]),
                 "or_compress": (_i64, [_ptr, _int, _i64, _i64, _ptr, _ptr, _ptr, _ptr, _i64]),
+                "or_pack_bits": (None, [_ptr, _int, _i64, _int, _ptr, _i64]),
+                "or_unpack_bits_at": (ctypes.c_uint32, [_ptr, _int, _i64]),
             }
             for name, (res, args) in sigs.items():
                 fn = getattr(L, name)
@@ -187,6 +189,31 @@ def relu2_grad(grad: np.ndarray, vals: np.ndarray, vdtype: int, bitmask: np.ndar
     return g
 
 
+def bits_per_value(dtype: int) -> int:
+    """Stored bits per value of the packed stream (reference bitsparse.py:15-23)."""
+    return 15 if dtype == BF16 else 7
+
+
+def pack_bits(raw: np.ndarray, dtype: int, stream: np.ndarray, start: int = 0) -> np.ndarray:
+    """C restatement of the stream packer: raw values into ``stream`` (uint8,
+    modified in place) at value index ``start``."""
+    _check_bits(raw, dtype)
+    raw = np.ascontiguousarray(raw)
+    assert stream.dtype == np.uint8 and stream.flags["C_CONTIGUOUS"]
+    assert (start + raw.size) * bits_per_value(dtype) <= stream.size * 8
+    lib().or_pack_bits(_p(raw), dtype, raw.size, bits_per_value(dtype), _p(stream), start)
+    return stream
+
+
+def unpack_bits(stream: np.ndarray, dtype: int, idx) -> np.ndarray:
+    """Values at indices ``idx`` of a packed stream (C restatement of the
+    reference's uint16-word decode; needs the guard word after the payload)."""
+    bits = bits_per_value(dtype)
+    out = np.array([lib().or_unpack_bits_at(_p(stream), bits, int(i)) for i in np.ravel(idx)],
+                   dtype=np.uint16 if dtype == BF16 else np.uint8)
+    return out
+
+
 def amax_bf16(x: np.ndarray) -> float:
     x = np.ascontiguousarray(x, dtype=np.uint16)
     return float(lib().or_amax_bf16(_p(x), x.size))
@@ -287,3 +314,27 @@ def np_bitmask_to_dense_mask(bitmask: np.ndarray, M: int, N: int) -> np.ndarray:
     gm, gn, T = tile_grid(M, N)
     bits = np.unpackbits(bitmask.reshape(T, TILE_BYTES), axis=1, bitorder="little").astype(bool)
     return np.ascontiguousarray(_from_tiles(bits, M, N))
+
+
+def np_pack_bits(raw: np.ndarray, dtype: int, stream: np.ndarray, start: int = 0) -> np.ndarray:
+    """numpy restatement of the stream packer: each value's low b bits as a
+    little-endian bit vector, concatenated, written at bit start*b (bits of
+    ``stream`` outside the run are kept)."""
+    b = bits_per_value(dtype)
+    n = raw.size
+    if n == 0:
+        return stream
+    vals = raw.astype(np.uint32) & ((1 << b) - 1)
+    vbits = ((vals[:, None] >> np.arange(b, dtype=np.uint32)[None, :]) & 1).astype(np.uint8).reshape(-1)
+    sbits = np.unpackbits(stream, bitorder="little")
+    sbits[start * b:(start + n) * b] = vbits
+    stream[:] = np.packbits(sbits, bitorder="little")
+    return stream
+
+
+def np_unpack_bits(stream: np.ndarray, dtype: int, start: int, n: int) -> np.ndarray:
+    """numpy inverse of ``np_pack_bits``: n values from value index ``start``."""
+    b = bits_per_value(dtype)
+    sbits = np.unpackbits(stream, bitorder="little")[start * b:(start + n) * b].reshape(n, b)
+    v = (sbits.astype(np.uint32) << np.arange(b, dtype=np.uint32)[None, :]).sum(axis=1)
+    return v.astype(np.uint16 if dtype == BF16 else np.uint8)

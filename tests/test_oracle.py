@@ -261,3 +261,77 @@ def test_to_fp8_definition():
     n = x.clone()
     n[3, 3] = float("nan")
     assert np.isnan(O.amax_bf16(bits(n)))
+
+
+# ---------------------------------------------------------------------------
+# packed value stream (pack_sbit)
+# ---------------------------------------------------------------------------
+def test_pack_bits_hand_examples():
+    """Worked by hand from the format (value i at stream bits [i*b, (i+1)*b),
+    LSB first): bf16 1.0 = 0x3f80 and 2.0 = 0x4000 -> 0x3f80 | 0x4000 << 15 =
+    0x20003f80; e4m3fn 1.0 = 0x38 and 2.0 = 0x40 -> 0x38 | 0x40 << 7 = 0x2038."""
+    s = np.zeros(8, np.uint8)
+    O.pack_bits(np.array([0x3F80, 0x4000], np.uint16), O.BF16, s)
+    assert s[:4].tobytes() == bytes([0x80, 0x3F, 0x00, 0x20]) and not s[4:].any()
+    s = np.zeros(8, np.uint8)
+    O.pack_bits(np.array([0x38, 0x40], np.uint8), O.E4M3FN, s)
+    assert s[:2].tobytes() == bytes([0x38, 0x20]) and not s[2:].any()
+    # a value starting at stream bit 15 (start = 1, bf16): 0x7fff << 15
+    s = np.zeros(8, np.uint8)
+    O.pack_bits(np.array([0x7FFF], np.uint16), O.BF16, s, start=1)
+    assert int.from_bytes(s[:4].tobytes(), "little") == 0x7FFF << 15
+
+
+def _brute_pack(raw, b, nbytes, start, init):
+    acc = int.from_bytes(init.tobytes(), "little")
+    for i, v in enumerate(raw.tolist()):
+        for k in range(b):
+            bit = (start + i) * b + k
+            acc = (acc & ~(1 << bit)) | (((v >> k) & 1) << bit)
+    return np.frombuffer(acc.to_bytes(nbytes, "little"), np.uint8)
+
+
+@pytest.mark.parametrize("code", [O.BF16, O.E4M3FN, O.E5M2])
+@pytest.mark.parametrize("start", [0, 1, 3, 7, 8, 13, 67])
+def test_pack_bits_brute_force_and_numpy(code, start):
+    """C packer == bit-by-bit Python-int packer == numpy bit-vector packer on
+    random values (sign bit set too: only the low b bits are stored), with
+    the stream pre-filled with random bytes that must survive outside the run."""
+    rng = np.random.default_rng(start + 10 * code)
+    b = O.bits_per_value(code)
+    dt = np.uint16 if code == O.BF16 else np.uint8
+    n = 37
+    raw = rng.integers(0, np.iinfo(dt).max + 1, n).astype(dt)
+    nbytes = ((start + n) * b + 7) // 8 + 6
+    init = rng.integers(0, 256, nbytes).astype(np.uint8)
+    c = O.pack_bits(raw, code, init.copy(), start)
+    brute = _brute_pack(raw & ((1 << b) - 1), b, nbytes, start, init)
+    npv = O.np_pack_bits(raw, code, init.copy(), start)
+    assert (c == brute).all()
+    assert (npv == brute).all()
+
+
+@pytest.mark.parametrize("code", [O.BF16, O.E4M3FN])
+def test_unpack_bits_inverts_pack(code):
+    """The reference's uint16-word decode (bitpacking.py:37-55) and the numpy
+    bit-vector decode both return the low b bits of every packed value."""
+    rng = np.random.default_rng(code)
+    b = O.bits_per_value(code)
+    dt = np.uint16 if code == O.BF16 else np.uint8
+    n, start = 500, 16
+    raw = rng.integers(0, np.iinfo(dt).max + 1, n).astype(dt)
+    s = np.zeros(((start + n) * b + 7) // 8 + 8, np.uint8)
+    O.pack_bits(raw, code, s, start)
+    want = raw & ((1 << b) - 1)
+    assert (O.unpack_bits(s, code, np.arange(start, start + n)) == want).all()
+    assert (O.np_unpack_bits(s, code, start, n) == want).all()
+
+
+def test_pack_bits_eight_value_groups_are_byte_aligned():
+    """Eight values are exactly 15 (bf16) / 7 (fp8) bytes, so runs starting at
+    multiples of 8 values share no stream byte (reference functions.py:78-81)."""
+    for code, b in ((O.BF16, 15), (O.E4M3FN, 7)):
+        dt = np.uint16 if code == O.BF16 else np.uint8
+        s = np.zeros(64, np.uint8)
+        O.pack_bits(np.full(8, (1 << b) - 1, dt), code, s, 8)
+        assert not s[:b].any() and (s[b:2 * b] == 0xFF).all() and not s[2 * b:].any()
