@@ -39,6 +39,9 @@ _SIGNATURES = {
     "bs_compress_workspace_bytes": [_i64, _i64],
     "bs_compress": [_vp, _int, _i64, _i64, _int, _vp, _u32, _vp, _vp, _vp, _vp, _vp, _i64, _vp,
                     _int, _vp, _vp, _int, _vp, _vp, _i64, _u32, _vp],
+    "bs_compress_relu": [_vp, _int, _i64, _i64, _int, _vp, _u32, _vp, _vp, _vp, _vp, _vp, _i64, _vp,
+                         _int, _vp, _vp, _int, _vp, _vp, _i64, _u32, _vp, _vp],
+    "bs_amax_relu": [_vp, _i64, _vp, _i64, _u32, _vp],
     "bs_tile_pack": [_vp, _int, _i64, _i64, _vp, _vp, _vp],
     "bs_prefix_from_counts": [_vp, _i64, _vp, _vp],
     "bs_compact_vals": [_vp, _int, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _vp, _vp],

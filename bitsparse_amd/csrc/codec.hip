@@ -146,6 +146,8 @@ struct CompressArgs {
     int64_t* start_out;
     uint32_t tile0;             // first tile of unit 0 (VALS: also the prefix base)
     uint32_t tend;              // one past the last tile of this launch
+    int32_t relu;               // 1: `dense` is a pre-activation, compress relu(dense)
+    uint8_t* relu_out;          // nullable (may alias dense): receives relu(dense)
     uint64_t* status;
     uint64_t* gstat;            // one status word per group of kGroupUnits units
     uint32_t epoch;
@@ -232,6 +234,38 @@ __device__ __forceinline__ uint32_t stream_chunk_mask(const typename Raw<Compres
         return mask_bf16x8_pk(d);
     } else {
         return chunk_mask<IN_T, QUANT>(d, o, scale, rcp);
+    }
+}
+
+// relu(x) of a loaded chunk with the semantics of torch's GPU relu: x <= 0
+// becomes +0 (so -0 does too), NaN and positives keep their bits (bit
+// patterns: bf16 [0x8000, 0xff80], e4m3fn [0x80, 0xfe], e5m2 [0x80, 0xfc] are
+// the non-positive non-NaN values besides +0).
+template <int DT>
+__device__ __forceinline__ typename Raw<DT == DT_BF16 ? 2 : 1>::T relu_chunk(typename Raw<DT == DT_BF16 ? 2 : 1>::T v)
+{
+    if constexpr (DT == DT_BF16) {
+        uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t lo = w[i] & 0xffffu, hi = w[i] >> 16;
+            w[i] = ((lo - 0x8000u) < 0x7f81u ? 0u : lo) | (((hi - 0x8000u) < 0x7f81u ? 0u : hi) << 16);
+        }
+        return uint4{w[0], w[1], w[2], w[3]};
+    } else {
+        constexpr uint32_t span = DT == DT_E4M3FN ? 0x7fu : 0x7du;   // zeroed: [0x80, 0x80 + span)
+        uint32_t w[2] = {v.x, v.y};
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            uint32_t r = 0;
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const uint32_t x = (w[i] >> (8 * b)) & 0xffu;
+                r |= ((x - 0x80u) < span ? 0u : x) << (8 * b);
+            }
+            w[i] = r;
+        }
+        return uint2{w[0], w[1]};
     }
 }
 
@@ -531,6 +565,12 @@ void compress_stream_kernel(CompressArgs a)
             }
             if constexpr (MODE == MODE_VALS) vm[k] = a.bitmask[(size_t)tc * kTileBytes + 64 * k + lane];
         }
+        if constexpr (MODE != MODE_VALS) {
+            if (a.relu) {
+#pragma unroll
+                for (int k = 0; k < 8; k++) d[k] = relu_chunk<IN_T>(d[k]);
+            }
+        }
 
         // ---- masks, bitmask bytes, round totals
         RawOut o[8];
@@ -546,6 +586,8 @@ void compress_stream_kernel(CompressArgs a)
             } else {
                 m = stream_chunk_mask<IN_T, QUANT>(d[k], o[k], scale, rcp) & (8 * k < rows_in ? 0xffu : 0u);
                 if (tile_ok) {
+                    if (a.relu_out != nullptr)
+                        store_chunk<INB, VEC>(a.relu_out, a.M, a.N, row0 + 8 * k, col0, d[k]);
                     if constexpr (QUANT) {
                         if (a.dense_q_out != nullptr)
                             store_chunk<1, VEC>(a.dense_q_out, a.M, a.N, row0 + 8 * k, col0, o[k]);
@@ -1213,15 +1255,19 @@ static int check_dense(const void* dense, int dtype, int64_t M, int64_t N, const
     return BS_OK;
 }
 
-extern "C" int bs_compress(const void* dense, int in_dtype, int64_t M, int64_t N, int quantize,
-                           const uint64_t* amax_slot, uint32_t amax_epoch, float* scale_out,
-                           void* dense_q_out, uint8_t* bitmask, uint32_t* prefix, void* vals,
-                           int64_t vals_capacity, const int64_t* vals_offset_in, int align8,
-                           int64_t* vals_offset_out, int64_t* vals_start_out, int write_vals,
-                           int32_t* err_flags, void* workspace, int64_t workspace_bytes,
-                           uint32_t epoch, void* stream)
+static int compress_impl(const void* dense, int in_dtype, int64_t M, int64_t N, int quantize,
+                         const uint64_t* amax_slot, uint32_t amax_epoch, float* scale_out,
+                         void* dense_q_out, uint8_t* bitmask, uint32_t* prefix, void* vals,
+                         int64_t vals_capacity, const int64_t* vals_offset_in, int align8,
+                         int64_t* vals_offset_out, int64_t* vals_start_out, int write_vals,
+                         int32_t* err_flags, void* workspace, int64_t workspace_bytes,
+                         uint32_t epoch, void* stream, bool relu, void* relu_out)
 {
     clear_error();
+    if (relu_out != nullptr && !relu)
+        return set_error(BS_ERR_INVALID, "bs_compress: relu_out without relu");
+    if (relu_out != nullptr && (((uintptr_t)relu_out) % (in_dtype == DT_BF16 ? 2 : 1)))
+        return set_error(BS_ERR_INVALID, "bs_compress_relu: relu_out misaligned");
     if (int rc = check_dense(dense, in_dtype, M, N, "bs_compress")) return rc;
     if (quantize && in_dtype != DT_BF16)
         return set_error(BS_ERR_INVALID, "bs_compress: quantize needs bf16 input");
@@ -1277,6 +1323,8 @@ extern "C" int bs_compress(const void* dense, int in_dtype, int64_t M, int64_t N
     a.start_out = vals_start_out;
     a.tile0 = 0;
     a.tend = (uint32_t)T;
+    a.relu = relu ? 1 : 0;
+    a.relu_out = (uint8_t*)relu_out;
     a.status = reinterpret_cast<uint64_t*>((uint8_t*)workspace + kWsHeaderBytes);
     a.epoch = epoch;
     a.err = err_flags;
@@ -1284,11 +1332,40 @@ extern "C" int bs_compress(const void* dense, int in_dtype, int64_t M, int64_t N
     a.gstat = a.status + (T + kStreamU - 1) / kStreamU;
     const int inb = in_dtype == DT_BF16 ? 2 : 1;
     bool vec = (N % 8 == 0) && (((uintptr_t)dense) % (8 * inb) == 0) &&
-               (dense_q_out == nullptr || aligned8(dense_q_out));
+               (dense_q_out == nullptr || aligned8(dense_q_out)) &&
+               (relu_out == nullptr || ((uintptr_t)relu_out) % (8 * inb) == 0);
     hipError_t e = write_vals ? launch_compress<MODE_FUSED>(a, in_dtype, quantize != 0, vec, st)
                               : launch_compress<MODE_COUNT>(a, in_dtype, quantize != 0, vec, st);
     if (e != hipSuccess) return set_error(BS_ERR_HIP, "bs_compress launch: %s", hipGetErrorString(e));
     return BS_OK;
+}
+
+extern "C" int bs_compress(const void* dense, int in_dtype, int64_t M, int64_t N, int quantize,
+                           const uint64_t* amax_slot, uint32_t amax_epoch, float* scale_out,
+                           void* dense_q_out, uint8_t* bitmask, uint32_t* prefix, void* vals,
+                           int64_t vals_capacity, const int64_t* vals_offset_in, int align8,
+                           int64_t* vals_offset_out, int64_t* vals_start_out, int write_vals,
+                           int32_t* err_flags, void* workspace, int64_t workspace_bytes,
+                           uint32_t epoch, void* stream)
+{
+    return compress_impl(dense, in_dtype, M, N, quantize, amax_slot, amax_epoch, scale_out, dense_q_out,
+                         bitmask, prefix, vals, vals_capacity, vals_offset_in, align8, vals_offset_out,
+                         vals_start_out, write_vals, err_flags, workspace, workspace_bytes, epoch, stream,
+                         false, nullptr);
+}
+
+extern "C" int bs_compress_relu(const void* preact, int in_dtype, int64_t M, int64_t N, int quantize,
+                                const uint64_t* amax_slot, uint32_t amax_epoch, float* scale_out,
+                                void* dense_q_out, uint8_t* bitmask, uint32_t* prefix, void* vals,
+                                int64_t vals_capacity, const int64_t* vals_offset_in, int align8,
+                                int64_t* vals_offset_out, int64_t* vals_start_out, int write_vals,
+                                int32_t* err_flags, void* workspace, int64_t workspace_bytes,
+                                uint32_t epoch, void* relu_out, void* stream)
+{
+    return compress_impl(preact, in_dtype, M, N, quantize, amax_slot, amax_epoch, scale_out, dense_q_out,
+                         bitmask, prefix, vals, vals_capacity, vals_offset_in, align8, vals_offset_out,
+                         vals_start_out, write_vals, err_flags, workspace, workspace_bytes, epoch, stream,
+                         true, relu_out);
 }
 
 extern "C" int bs_compact_vals(const void* dense, int in_dtype, int64_t M, int64_t N,

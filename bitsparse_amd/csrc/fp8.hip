@@ -18,6 +18,16 @@ constexpr int kFp8Threads = 256;
 // only serialised step) stays at a few hundred.
 constexpr int kAmaxUnroll = 4;
 
+// RELU: amax of relu(x) (x <= 0 counts as 0; NaN is kept by relu, so it still wins).
+template <bool RELU>
+__device__ __forceinline__ uint32_t mag_bits(uint32_t b)
+{
+    const uint32_t m = b & 0x7fffu;
+    if constexpr (RELU) return ((b & 0x8000u) && m <= 0x7f80u) ? 0u : m;
+    else return m;
+}
+
+template <bool RELU>
 __global__ __launch_bounds__(kFp8Threads) void amax_bf16_kernel(const uint16_t* x, int64_t n,
                                                                 uint64_t* slot, uint32_t epoch)
 {
@@ -37,8 +47,8 @@ __global__ __launch_bounds__(kFp8Threads) void amax_bf16_kernel(const uint16_t* 
             const uint32_t w[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
 #pragma unroll
             for (int k = 0; k < 4; k++) {
-                m = max(m, w[k] & 0x7fffu);
-                m = max(m, (w[k] >> 16) & 0x7fffu);
+                m = max(m, mag_bits<RELU>(w[k] & 0xffffu));
+                m = max(m, mag_bits<RELU>(w[k] >> 16));
             }
         }
     }
@@ -47,12 +57,12 @@ __global__ __launch_bounds__(kFp8Threads) void amax_bf16_kernel(const uint16_t* 
         const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            m = max(m, w[k] & 0x7fffu);
-            m = max(m, (w[k] >> 16) & 0x7fffu);
+            m = max(m, mag_bits<RELU>(w[k] & 0xffffu));
+            m = max(m, mag_bits<RELU>(w[k] >> 16));
         }
     }
     for (int64_t j = nvec * 8 + (int64_t)blockIdx.x * kFp8Threads + tid; j < n; j += stride)
-        m = max(m, (uint32_t)x[j] & 0x7fffu);
+        m = max(m, mag_bits<RELU>((uint32_t)x[j]));
     m = wave_max_u32(m);
     if ((tid & 63) == 0) s_w[tid >> 6] = m;
     __syncthreads();
@@ -110,8 +120,8 @@ static uint32_t grid_for(int64_t n)
 
 using namespace bs;
 
-extern "C" int bs_amax(const void* x, int64_t n, void* workspace, int64_t workspace_bytes, uint32_t epoch,
-                       void* stream)
+static int amax_impl(const void* x, int64_t n, void* workspace, int64_t workspace_bytes, uint32_t epoch,
+                     void* stream, bool relu)
 {
     clear_error();
     if (n < 0) return set_error(BS_ERR_INVALID, "bs_amax: negative n");
@@ -128,11 +138,27 @@ extern "C" int bs_amax(const void* x, int64_t n, void* workspace, int64_t worksp
         cus = 256;
     uint32_t grid = grid_for(n);
     if (grid > (uint32_t)(2 * cus)) grid = (uint32_t)(2 * cus);
-    hipLaunchKernelGGL(amax_bf16_kernel, dim3(grid), dim3(kFp8Threads), 0, (hipStream_t)stream,
-                       (const uint16_t*)x, n, slot, epoch);
+    if (relu)
+        hipLaunchKernelGGL(amax_bf16_kernel<true>, dim3(grid), dim3(kFp8Threads), 0, (hipStream_t)stream,
+                           (const uint16_t*)x, n, slot, epoch);
+    else
+        hipLaunchKernelGGL(amax_bf16_kernel<false>, dim3(grid), dim3(kFp8Threads), 0, (hipStream_t)stream,
+                           (const uint16_t*)x, n, slot, epoch);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(BS_ERR_HIP, "bs_amax launch: %s", hipGetErrorString(e));
     return BS_OK;
+}
+
+extern "C" int bs_amax(const void* x, int64_t n, void* workspace, int64_t workspace_bytes, uint32_t epoch,
+                       void* stream)
+{
+    return amax_impl(x, n, workspace, workspace_bytes, epoch, stream, false);
+}
+
+extern "C" int bs_amax_relu(const void* preact, int64_t n, void* workspace, int64_t workspace_bytes,
+                            uint32_t epoch, void* stream)
+{
+    return amax_impl(preact, n, workspace, workspace_bytes, epoch, stream, true);
 }
 
 extern "C" int bs_quantize_e4m3fn(const void* x, int64_t n, void* q_out, float* scale_out,

@@ -17,7 +17,7 @@ from torch.autograd import Function
 from .bitsparse import BitsparseTensor, TensorBuffer
 from .config import RELU2_SCALE
 from .fp8 import is_fp8, matmul, to_fp8
-from .src.functions import dense_to_tilesparse, quantize_and_compress
+from .src.functions import relu_and_compress, relu_quantize_and_compress
 from .src.hip_operators import mask_with_bitmask_, relu2_grad_sparse_
 from .src.sparse_matmul import AspB, AspRelu2B
 
@@ -33,15 +33,14 @@ class ReluLinear(Function):
                 dtype: torch.dtype = torch.bfloat16):
         ctx.dtype = dtype
         ctx.save_for_backward(W)
-        h = z.relu_()
-
+        # h = z.relu_() fused into the compress pass (z is still updated in place)
         if is_fp8(dtype):
             if dtype != torch.float8_e4m3fn:
                 raise TypeError("fp8 activation storage is float8_e4m3fn")
-            h, scale, h_sparse = quantize_and_compress(h, sparse_data, pack_sbit)
+            h, scale, h_sparse = relu_quantize_and_compress(z, sparse_data, pack_sbit)
         else:
             scale = None
-            h_sparse = dense_to_tilesparse(h, scale, sparse_data, pack_sbit)
+            h, h_sparse = relu_and_compress(z, sparse_data, pack_sbit)
 
         ctx.h_sparse = h_sparse
         y = matmul(h, W.T, is_fp8(dtype), a_scale=scale)
@@ -105,14 +104,14 @@ class Relu2Linear(Function):
                 storage_dtype: torch.dtype = torch.bfloat16):
         ctx.dtype = storage_dtype
         ctx.save_for_backward(W)
-        h = z.relu_()
-
+        # h = z.relu_() fused into the compress pass (z is still updated in place)
         if is_fp8(storage_dtype):
             if storage_dtype != torch.float8_e4m3fn:
                 raise TypeError("fp8 activation storage is float8_e4m3fn")
-            _, scale, h_sparse = quantize_and_compress(h, sparse_data, pack_sbit)
+            _, scale, h_sparse = relu_quantize_and_compress(z, sparse_data, pack_sbit)
+            h = z
         else:
-            h_sparse = dense_to_tilesparse(h, None, sparse_data, pack_sbit)
+            h, h_sparse = relu_and_compress(z, sparse_data, pack_sbit)
         ctx.h_sparse = h_sparse
 
         h.square_()

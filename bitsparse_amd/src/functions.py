@@ -47,15 +47,17 @@ def _check_input(dense: Tensor) -> None:
         raise ValueError(f"dense_to_tilesparse expects a 2-D tensor, got {tuple(dense.shape)}")
 
 
-def _prepare_tiles(dense: Tensor) -> _PreparedTiles:
-    """Bitmask + uint32 prefix of ``dense`` (count pass, no values).
+def _prepare_tiles(dense: Tensor, relu: bool = False) -> _PreparedTiles:
+    """Bitmask + uint32 prefix of ``dense`` (count pass, no values); ``relu``:
+    of relu(dense), which is also written back into ``dense``.
     Reference: functions.py:23-45 (tile_pack + cumsum)."""
     _check_input(dense)
     M, N = dense.shape
     grid_m, grid_n, num_tiles, TILE_NUMEL, TILE_BYTES = tile_grid(M, N, BLOCK_M, BLOCK_N)
     tile_bitmasks = torch.empty(num_tiles * TILE_BYTES, device=dense.device, dtype=torch.uint8)
     tile_prefix = torch.empty(num_tiles + 1, device=dense.device, dtype=torch.uint32)
-    ops.compress_into(dense, tile_bitmasks, tile_prefix, None, None, None, None, write_vals=False)
+    ops.compress_into(dense, tile_bitmasks, tile_prefix, None, None, None, None, write_vals=False,
+                      relu=relu, relu_out=dense if relu else None)
     return _PreparedTiles(M, N, grid_m, grid_n, num_tiles, TILE_NUMEL, tile_bitmasks, tile_prefix)
 
 
@@ -71,12 +73,30 @@ def dense_to_tilesparse(
     """
     _check_input(dense)
     ops.require_device(dense, "dense_to_tilesparse")
-    dense = dense.contiguous()
+    return _to_tilesparse(dense.contiguous(), scale, sparse_data, pack_sbit, False)
+
+
+def relu_and_compress(z: Tensor, sparse_data: TensorBuffer | None = None,
+                      pack_sbit: bool = False) -> tuple[Tensor, BitsparseTensor]:
+    """``h = z.relu_(); dense_to_tilesparse(h, None, sparse_data, pack_sbit)``
+    (reference layers.py:29,37) with the ReLU fused into the compress pass:
+    the kernel reads z once, writes relu(z) back into z and compresses it.
+    Returns (h, BitsparseTensor) with h = z."""
+    _check_input(z)
+    ops.require_device(z, "relu_and_compress")
+    if not z.is_contiguous():          # the in-place result must land in the caller's z
+        h = z.relu_()
+        return h, dense_to_tilesparse(h, None, sparse_data, pack_sbit)
+    return z, _to_tilesparse(z, None, sparse_data, pack_sbit, True)
+
+
+def _to_tilesparse(dense: Tensor, scale: Tensor | None, sparse_data: TensorBuffer | None,
+                   pack_sbit: bool, relu: bool) -> BitsparseTensor:
     M, N = dense.shape
     grid_m, grid_n, num_tiles, TILE_NUMEL, TILE_BYTES = tile_grid(M, N, BLOCK_M, BLOCK_N)
 
     if sparse_data is None:
-        prepared = _prepare_tiles(dense)
+        prepared = _prepare_tiles(dense, relu)
         vals, vals_offset = ops.compact_vals(
             dense, prepared.bitmasks, prepared.prefix, None, None,
             M, N, grid_n, num_tiles, BLOCK_M, BLOCK_N, TILE_NUMEL, pack_sbit)
@@ -85,8 +105,9 @@ def dense_to_tilesparse(
                                vals_offset=vals_offset, pack_sbit=pack_sbit)
 
     _check_buffer(sparse_data, dense.dtype, pack_sbit)
+    fused = dict(relu=True, relu_out=dense) if relu else {}
     if pack_sbit:
-        return _compress_packed_into_buffer(dense, scale, sparse_data)
+        return _compress_packed_into_buffer(dense, scale, sparse_data, **fused)
     if sparse_data.vals.dtype != dense.dtype:
         raise TypeError(f"TensorBuffer stores {sparse_data.vals.dtype} but the input is {dense.dtype}")
     bitmask = torch.empty(num_tiles * TILE_BYTES, device=dense.device, dtype=torch.uint8)
@@ -94,7 +115,7 @@ def dense_to_tilesparse(
     vals_offset = sparse_data.offset                      # snapshot: never written again
     new_offset = torch.empty(1, device=dense.device, dtype=torch.int64)
     ops.compress_into(dense, bitmask, prefix, sparse_data.vals, vals_offset, new_offset,
-                      sparse_data.err_flags, write_vals=True)
+                      sparse_data.err_flags, write_vals=True, **fused)
     sparse_data.offset = new_offset
     return BitsparseTensor(sparse_data.vals, bitmask, prefix, dense.shape, dense.dtype,
                            grid_m, grid_n, BLOCK_M, BLOCK_N, scale=scale,
@@ -111,8 +132,8 @@ def _check_buffer(buf: TensorBuffer, dtype: torch.dtype, pack_sbit: bool) -> Non
 def _compress_packed_into_buffer(dense: Tensor, scale: Tensor | None, buf: TensorBuffer,
                                  **quant) -> BitsparseTensor:
     """Fused compress into a raw staging buffer, then pack at the 8-aligned
-    cursor; no host synchronisation.  ``quant`` forwards the quantise options
-    of ``compress_into`` (the staging then holds e4m3fn values)."""
+    cursor; no host synchronisation.  ``quant`` forwards the quantise / ReLU
+    options of ``compress_into`` (quantize: the staging holds e4m3fn values)."""
     M, N = dense.shape
     grid_m, grid_n, num_tiles, TILE_NUMEL, TILE_BYTES = tile_grid(M, N, BLOCK_M, BLOCK_N)
     stored = torch.float8_e4m3fn if quant.get("quantize") else dense.dtype
@@ -129,8 +150,22 @@ def _compress_packed_into_buffer(dense: Tensor, scale: Tensor | None, buf: Tenso
                            vals_offset=vals_offset, pack_sbit=True)
 
 
+def relu_quantize_and_compress(
+    z: Tensor, sparse_data: TensorBuffer | None = None, pack_sbit: bool = False,
+) -> tuple[Tensor, Tensor, BitsparseTensor]:
+    """``quantize_and_compress(z.relu_(), ...)`` with the ReLU fused into the
+    amax and compress passes (relu(z) is written back into z, as the
+    reference's in-place relu_ does, layers.py:29-37)."""
+    if z.dtype != torch.bfloat16:
+        raise TypeError("relu_quantize_and_compress expects a bfloat16 tensor")
+    if not z.is_contiguous():
+        return quantize_and_compress(z.relu_(), sparse_data, pack_sbit)
+    return quantize_and_compress(z, sparse_data, pack_sbit, _relu=True)
+
+
 def quantize_and_compress(
     dense: Tensor, sparse_data: TensorBuffer | None = None, pack_sbit: bool = False,
+    _relu: bool = False,
 ) -> tuple[Tensor, Tensor, BitsparseTensor]:
     """bf16 [M, N] -> (e4m3fn dense, fp32 scale, BitsparseTensor of the e4m3fn
     values) with one amax pass and one fused quantize+compress pass.
@@ -144,14 +179,15 @@ def quantize_and_compress(
     dense = dense.contiguous()
     M, N = dense.shape
     grid_m, grid_n, num_tiles, TILE_NUMEL, TILE_BYTES = tile_grid(M, N, BLOCK_M, BLOCK_N)
-    amax_epoch = ops.amax_into_workspace(dense)
+    amax_epoch = ops.amax_into_workspace(dense, relu=_relu)
+    fused = dict(relu=True, relu_out=dense) if _relu else {}
     q = torch.empty((M, N), device=dense.device, dtype=torch.float8_e4m3fn)
     scale = torch.empty((), device=dense.device, dtype=torch.float32)
     bitmask = torch.empty(num_tiles * TILE_BYTES, device=dense.device, dtype=torch.uint8)
     prefix = torch.empty(num_tiles + 1, device=dense.device, dtype=torch.uint32)
     if sparse_data is None:
         ops.compress_into(dense, bitmask, prefix, None, None, None, None, write_vals=False,
-                          quantize=True, scale_out=scale, dense_q_out=q, amax_epoch=amax_epoch)
+                          quantize=True, scale_out=scale, dense_q_out=q, amax_epoch=amax_epoch, **fused)
         vals, vals_offset = ops.compact_vals(q, bitmask, prefix, None, None, M, N, grid_n,
                                              num_tiles, BLOCK_M, BLOCK_N, TILE_NUMEL, pack_sbit)
         sp = BitsparseTensor(vals, bitmask, prefix, q.shape, q.dtype, grid_m, grid_n,
@@ -161,7 +197,7 @@ def quantize_and_compress(
     _check_buffer(sparse_data, torch.float8_e4m3fn, pack_sbit)
     if pack_sbit:
         sp = _compress_packed_into_buffer(dense, scale, sparse_data, quantize=True, scale_out=scale,
-                                          dense_q_out=q, amax_epoch=amax_epoch)
+                                          dense_q_out=q, amax_epoch=amax_epoch, **fused)
         return q, scale, sp
     if sparse_data.vals.dtype != torch.float8_e4m3fn:
         raise TypeError(f"TensorBuffer stores {sparse_data.vals.dtype}, need float8_e4m3fn")
@@ -169,7 +205,7 @@ def quantize_and_compress(
     new_offset = torch.empty(1, device=dense.device, dtype=torch.int64)
     ops.compress_into(dense, bitmask, prefix, sparse_data.vals, vals_offset, new_offset,
                       sparse_data.err_flags, write_vals=True, quantize=True, scale_out=scale,
-                      dense_q_out=q, amax_epoch=amax_epoch)
+                      dense_q_out=q, amax_epoch=amax_epoch, **fused)
     sparse_data.offset = new_offset
     sp = BitsparseTensor(sparse_data.vals, bitmask, prefix, q.shape, q.dtype, grid_m, grid_n,
                          BLOCK_M, BLOCK_N, scale=scale, vals_offset=vals_offset)

@@ -122,11 +122,14 @@ def compress_into(dense: Tensor, bitmask: Tensor, prefix: Tensor, vals: Tensor |
                   vals_offset_in: Tensor | None, vals_offset_out: Tensor | None,
                   err_flags: Tensor | None, write_vals: bool = True,
                   quantize: bool = False, scale_out: Tensor | None = None,
-                  dense_q_out: Tensor | None = None, amax_epoch: int = 0) -> None:
+                  dense_q_out: Tensor | None = None, amax_epoch: int = 0,
+                  relu: bool = False, relu_out: Tensor | None = None) -> None:
     """Single-pass compress (bitmask + prefix + values in one read of dense).
 
     ``quantize``: dense is bf16 and is quantized to e4m3fn with the scale of
-    the amax computed by ``amax_into_workspace`` under ``amax_epoch``."""
+    the amax computed by ``amax_into_workspace`` under ``amax_epoch``.
+    ``relu``: dense is a pre-activation z and relu(z) is compressed (fused
+    ReLU); ``relu_out`` (may be ``dense`` itself) receives relu(z)."""
     require_device(dense, "compress")
     _contig(dense, "dense")
     M, N = dense.shape
@@ -135,18 +138,24 @@ def compress_into(dense: Tensor, bitmask: Tensor, prefix: Tensor, vals: Tensor |
     ws.ensure(L.bs_compress_workspace_bytes(M, N))
     epoch = ws.next_epoch()
     cap = vals.numel() if (vals is not None and write_vals) else 0
-    check(L.bs_compress(
-        dense.data_ptr(), dtype_code(dense.dtype), M, N, int(quantize),
-        ws.amax_slot_ptr() if quantize else None, amax_epoch, ptr(scale_out), ptr(dense_q_out),
-        bitmask.data_ptr(), prefix.data_ptr(),
-        ptr(vals) if write_vals else None, cap, ptr(vals_offset_in), 0,
-        ptr(vals_offset_out), None, int(write_vals), ptr(err_flags),
-        ws.buf.data_ptr(), ws.nbytes, epoch, stream_handle(dense.device)), "bs_compress")
+    args = (dense.data_ptr(), dtype_code(dense.dtype), M, N, int(quantize),
+            ws.amax_slot_ptr() if quantize else None, amax_epoch, ptr(scale_out), ptr(dense_q_out),
+            bitmask.data_ptr(), prefix.data_ptr(),
+            ptr(vals) if write_vals else None, cap, ptr(vals_offset_in), 0,
+            ptr(vals_offset_out), None, int(write_vals), ptr(err_flags),
+            ws.buf.data_ptr(), ws.nbytes, epoch)
+    if relu:
+        if relu_out is not None and (relu_out.shape != dense.shape or relu_out.dtype != dense.dtype
+                                     or not relu_out.is_contiguous()):
+            raise ValueError("compress: relu_out must be a contiguous tensor like dense")
+        check(L.bs_compress_relu(*args, ptr(relu_out), stream_handle(dense.device)), "bs_compress_relu")
+    else:
+        check(L.bs_compress(*args, stream_handle(dense.device)), "bs_compress")
 
 
-def amax_into_workspace(x: Tensor) -> int:
-    """amax(|x|) of a bf16 tensor into the stream's workspace; returns the
-    epoch that tags it."""
+def amax_into_workspace(x: Tensor, relu: bool = False) -> int:
+    """amax(|x|) (``relu``: amax of relu(x)) of a bf16 tensor into the
+    stream's workspace; returns the epoch that tags it."""
     require_device(x, "amax")
     _contig(x, "x")
     if x.dtype != torch.bfloat16:
@@ -155,8 +164,9 @@ def amax_into_workspace(x: Tensor) -> int:
     ws = _lib.workspace_for(x.device)
     ws.ensure(256)
     epoch = ws.next_epoch()
-    check(L.bs_amax(x.data_ptr(), x.numel(), ws.buf.data_ptr(), ws.nbytes, epoch,
-                    stream_handle(x.device)), "bs_amax")
+    fn = L.bs_amax_relu if relu else L.bs_amax
+    check(fn(x.data_ptr(), x.numel(), ws.buf.data_ptr(), ws.nbytes, epoch,
+             stream_handle(x.device)), "bs_amax")
     return epoch
 
 

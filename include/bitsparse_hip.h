@@ -92,6 +92,25 @@ int bs_compress(const void* dense, int in_dtype, int64_t M, int64_t N, int quant
                 int64_t workspace_bytes, uint32_t epoch, void* stream);
 
 /*
+ * bs_compress of relu(preact) with the ReLU fused: `preact` is the
+ * pre-activation z (relu(z) > 0 exactly where z > 0, so the bitmask, prefix and
+ * values are those of relu(z)); `relu_out` (nullable, may alias `preact` for
+ * the reference's in-place z.relu_()) receives relu(z) with the semantics of
+ * torch's GPU relu (x <= 0 -> +0, so -0 -> +0; NaN and positives keep their
+ * bits).  With quantize, the amax must be
+ * that of relu(z) (bs_amax_relu).  Replaces the h = z.relu_() that precedes
+ * compress in lib_sparse/layers.py:29,37 and :107,117 (the minimum entry
+ * point's "optional fused ReLU").
+ */
+int bs_compress_relu(const void* preact, int in_dtype, int64_t M, int64_t N, int quantize,
+                     const uint64_t* amax_slot, uint32_t amax_epoch, float* scale_out,
+                     void* dense_q_out, uint8_t* bitmask, uint32_t* prefix, void* vals,
+                     int64_t vals_capacity, const int64_t* vals_offset_in, int align8,
+                     int64_t* vals_offset_out, int64_t* vals_start_out, int write_vals,
+                     int32_t* err_flags, void* workspace, int64_t workspace_bytes,
+                     uint32_t epoch, void* relu_out, void* stream);
+
+/*
  * Per-tile bitmask and nonzero counts (int32[T]) of a dense [M, N] input.
  * Replaces lib_sparse/src/triton_operators.py:21-33 (tile_pack) /
  * triton_kernels.py:67-97 (_tile_pack_kernel).
@@ -165,6 +184,10 @@ int bs_relu2_grad(void* grad, int64_t M, int64_t N, const void* vals, int vals_d
  */
 int bs_amax(const void* x, int64_t n, void* workspace, int64_t workspace_bytes,
             uint32_t epoch, void* stream);
+
+/* bs_amax of relu(preact) (bf16), for bs_compress_relu with quantize. */
+int bs_amax_relu(const void* preact, int64_t n, void* workspace, int64_t workspace_bytes,
+                 uint32_t epoch, void* stream);
 
 /*
  * q = e4m3fn_RNE(fp32(x) / scale), scale = max(amax/448, 1e-9) with amax
