@@ -735,43 +735,131 @@ void compress_stream_kernel(CompressArgs a)
 // bits (atomicAnd of the run's bit mask complement, then atomicOr of the
 // run's bits: concurrent writers of disjoint bits commute).
 // ===========================================================================
-template <int VB, int PB>
-__global__ __launch_bounds__(256) void pack_bits_kernel(const uint8_t* raw, const uint32_t* count_ptr,
-                                                        int64_t count_max, uint32_t* out, int64_t out_words,
-                                                        const int64_t* start_ptr, int32_t* err)
+// Merge `word` into out[D] keeping the bits outside `mask` (disjoint-bit
+// atomics commute with any other writer of other bits of the dword).
+__device__ __forceinline__ void merge_word(uint32_t* out, int64_t D, uint32_t word, uint32_t mask)
 {
+    if (mask == 0xffffffffu) {
+        out[D] = word;
+    } else if (mask != 0u) {
+        atomicAnd(&out[D], ~mask);
+        atomicOr(&out[D], word & mask);
+    }
+}
+
+// Bits [lb, hb) of a dword as a mask, 0 <= lb <= hb <= 32.
+__device__ __forceinline__ uint32_t bit_range_mask(uint32_t lb, uint32_t hb)
+{
+    const uint32_t hi = hb >= 32u ? 0xffffffffu : ((1u << hb) - 1u);
+    const uint32_t lo = lb >= 32u ? 0xffffffffu : ((1u << lb) - 1u);
+    return hi & ~lo;
+}
+
+constexpr int kPackThreads = 256;
+
+template <int VB, int PB>
+__global__ __launch_bounds__(kPackThreads) void pack_bits_kernel(const uint8_t* raw, const uint32_t* count_ptr,
+                                                                 int64_t count_max, uint32_t* out,
+                                                                 int64_t out_words, const int64_t* start_ptr,
+                                                                 int32_t* err, int raw_vec)
+{
+    // one 8-value group per thread: PB bytes of stream (15 / 7), staged here
+    __shared__ uint32_t s_out[kPackThreads * PB / 4 + 2];
+    const int tid = threadIdx.x;
     const int64_t start = start_ptr ? *start_ptr : 0;
     int64_t count = count_max;
     if (count_ptr) count = min((int64_t)*count_ptr, count_max);
     if (start < 0) {
-        if (err && blockIdx.x == 0 && threadIdx.x == 0) atomicOr(err, 2);
+        if (err && blockIdx.x == 0 && tid == 0) atomicOr(err, 2);
         return;
     }
     const int64_t S = start * PB, E = (start + count) * PB;   // stream bits of the run
-    const int64_t D0 = S >> 5, D1 = (E + 31) >> 5;            // output dwords it touches
-    for (int64_t D = D0 + (int64_t)blockIdx.x * 256 + threadIdx.x; D < D1; D += (int64_t)gridDim.x * 256) {
-        if (D >= out_words) {                                  // past the storage: drop, flag
-            if (err) atomicOr(err, 1);
-            break;
+    if (count <= 0) return;
+    if (E > out_words * 32) {                                 // past the storage: flag, pack what fits
+        if (err && blockIdx.x == 0 && tid == 0) atomicOr(err, 1);
+    }
+
+    if ((start & 7) != 0 || !raw_vec) {
+        // general start (or raw values not aligned for vector loads): one
+        // thread per output dword, gathering the <= 3 / <= 6
+        // values that overlap it
+        const int64_t D0 = S >> 5, D1 = min((E + 31) >> 5, out_words);
+        for (int64_t D = D0 + (int64_t)blockIdx.x * kPackThreads + tid; D < D1;
+             D += (int64_t)gridDim.x * kPackThreads) {
+            const int64_t lo = max(D * 32, S), hi = min(D * 32 + 32, E);
+            const int64_t v0 = (lo - S) / PB, v1 = (hi - 1 - S) / PB;
+            uint64_t acc = 0;
+            for (int64_t v = v0; v <= v1; v++) {
+                const uint32_t x = (VB == 2 ? (uint32_t)reinterpret_cast<const uint16_t*>(raw)[v]
+                                            : (uint32_t)raw[v]) & ((1u << PB) - 1u);
+                const int64_t pos = S + v * PB - D * 32;       // > -PB
+                acc |= pos >= 0 ? ((uint64_t)x << pos) : ((uint64_t)x >> (-pos));
+            }
+            merge_word(out, D, (uint32_t)acc, bit_range_mask((uint32_t)(lo - D * 32), (uint32_t)(hi - D * 32)));
         }
-        const int64_t lo = max(D * 32, S), hi = min(D * 32 + 32, E);
-        const int64_t v0 = (lo - S) / PB, v1 = (hi - 1 - S) / PB;
-        uint64_t acc = 0;
-        for (int64_t v = v0; v <= v1; v++) {
-            const uint32_t x = (VB == 2 ? (uint32_t)reinterpret_cast<const uint16_t*>(raw)[v] : (uint32_t)raw[v]) &
-                               ((1u << PB) - 1u);
-            const int64_t pos = S + v * PB - D * 32;           // > -PB
-            acc |= pos >= 0 ? ((uint64_t)x << pos) : ((uint64_t)x >> (-pos));
-        }
-        const uint32_t word = (uint32_t)acc;
-        const uint32_t lb = (uint32_t)(lo - D * 32), hb = (uint32_t)(hi - D * 32);   // 0 <= lb < hb <= 32
-        const uint32_t mask = (hb == 32u ? 0xffffffffu : ((1u << hb) - 1u)) & ~((1u << lb) - 1u);
-        if (mask == 0xffffffffu) {
-            out[D] = word;
+        return;
+    }
+
+    // start % 8 == 0 (and raw aligned to 8 values): group g (values 8g..8g+7) is exactly PB stream bytes at
+    // byte S/8 + g*PB.  A workgroup packs 256 consecutive groups in registers,
+    // stages their bytes contiguously in LDS at the dword phase of the output,
+    // and stores whole dwords; only the two dwords at the ends of its span
+    // (shared with the neighbouring workgroups or outside bits) are merged.
+    const int64_t ngroups = (count + 7) / 8;
+    const int64_t byte_base = S >> 3;
+    for (int64_t gb = (int64_t)blockIdx.x * kPackThreads; gb < ngroups; gb += (int64_t)gridDim.x * kPackThreads) {
+        const int64_t g = gb + tid;
+        uint32_t w[8];
+        const int64_t v0 = g * 8;
+        if (v0 + 8 <= count) {
+            if constexpr (VB == 2) {
+                const uint4 r = *reinterpret_cast<const uint4*>(raw + v0 * 2);
+                w[0] = r.x & 0xffffu; w[1] = r.x >> 16; w[2] = r.y & 0xffffu; w[3] = r.y >> 16;
+                w[4] = r.z & 0xffffu; w[5] = r.z >> 16; w[6] = r.w & 0xffffu; w[7] = r.w >> 16;
+            } else {
+                const uint2 r = *reinterpret_cast<const uint2*>(raw + v0);
+#pragma unroll
+                for (int e = 0; e < 8; e++) w[e] = ((e < 4 ? r.x : r.y) >> (8 * (e & 3))) & 0xffu;
+            }
         } else {
-            atomicAnd(&out[D], ~mask);
-            atomicOr(&out[D], word & mask);
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                w[e] = (v0 + e < count) ? (VB == 2 ? (uint32_t)reinterpret_cast<const uint16_t*>(raw)[v0 + e]
+                                                   : (uint32_t)raw[v0 + e]) : 0u;
         }
+        // 8 x PB bits, LSB first, into up to 4 dwords
+        uint64_t lo64 = 0, hi64 = 0;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const uint64_t x = w[e] & ((1u << PB) - 1u);
+            const int pos = e * PB;
+            if (pos < 64) {
+                lo64 |= x << pos;
+                if (pos + PB > 64) hi64 |= x >> (64 - pos);
+            } else {
+                hi64 |= x << (pos - 64);
+            }
+        }
+        const int64_t gbytes0 = byte_base + gb * PB;               // the span's first byte
+        const int phase = (int)(gbytes0 & 3);
+        uint8_t* sb = reinterpret_cast<uint8_t*>(s_out);
+        const int o = phase + tid * PB;
+#pragma unroll
+        for (int k = 0; k < PB; k++) {
+            const uint64_t src = k < 8 ? lo64 : hi64;
+            sb[o + k] = (uint8_t)(src >> (8 * (k & 7)));
+        }
+        __syncthreads();
+        // stream bits this span covers: [Sb, Eb)
+        const int64_t Sb = gbytes0 * 8;
+        const int64_t Eb = min(E, (byte_base + min(gb + kPackThreads, ngroups) * PB) * 8);
+        const int64_t D0 = gbytes0 >> 2, D1 = min((Eb + 31) >> 5, out_words);
+        for (int64_t D = D0 + tid; D < D1; D += kPackThreads) {
+            const uint32_t word = s_out[D - D0];
+            const int64_t lo = max(D * 32, Sb), hi = min(D * 32 + 32, Eb);
+            merge_word(out, D, word, bit_range_mask((uint32_t)(lo - D * 32), (uint32_t)(hi - D * 32)));
+        }
+        __syncthreads();
     }
 }
 
@@ -1673,19 +1761,21 @@ extern "C" int bs_pack_bits(const void* raw, int vals_dtype, const uint32_t* cou
     if (((uintptr_t)raw) % vb) return set_error(BS_ERR_INVALID, "bs_pack_bits: raw values misaligned");
     if (((uintptr_t)stream_bytes) & 3u) return set_error(BS_ERR_INVALID, "bs_pack_bits: stream not 4-byte aligned");
     if (count_max > (int64_t)1 << 40) return set_error(BS_ERR_INVALID, "bs_pack_bits: count too large");
-    // dwords a run of count_max values can touch, whatever its start
-    const int64_t words = (count_max * pb + 62) / 32 + 1;
-    const uint32_t blocks = (uint32_t)std::min<int64_t>((words + 255) / 256, 65535);
+    // enough threads for one 8-value group each (aligned start) and for one
+    // output dword each (any other start); the kernel loops over the rest
+    const int64_t work = std::max((count_max + 7) / 8, (count_max * pb + 62) / 32 + 1);
+    const uint32_t blocks = (uint32_t)std::min<int64_t>((work + kPackThreads - 1) / kPackThreads, 8192);
     hipStream_t st = (hipStream_t)stream;
     const uint8_t* r = (const uint8_t*)raw;
+    const bool raw_vec = (((uintptr_t)raw) % (8 * vb)) == 0;
     uint32_t* o = (uint32_t*)stream_bytes;
     const int64_t ow = stream_nbytes / 4;
     if (vals_dtype == DT_BF16)
-        hipLaunchKernelGGL((pack_bits_kernel<2, 15>), dim3(blocks), dim3(256), 0, st, r, count_ptr, count_max, o, ow,
-                           start_index, err_flags);
+        hipLaunchKernelGGL((pack_bits_kernel<2, 15>), dim3(blocks), dim3(kPackThreads), 0, st, r, count_ptr,
+                           count_max, o, ow, start_index, err_flags, (int)raw_vec);
     else
-        hipLaunchKernelGGL((pack_bits_kernel<1, 7>), dim3(blocks), dim3(256), 0, st, r, count_ptr, count_max, o, ow,
-                           start_index, err_flags);
+        hipLaunchKernelGGL((pack_bits_kernel<1, 7>), dim3(blocks), dim3(kPackThreads), 0, st, r, count_ptr,
+                           count_max, o, ow, start_index, err_flags, (int)raw_vec);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(BS_ERR_HIP, "bs_pack_bits launch: %s", hipGetErrorString(e));
     return BS_OK;

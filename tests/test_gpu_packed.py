@@ -60,6 +60,41 @@ def test_pack_bits_kernel_matches_oracle(dev, code, start, n):
 
 
 @pytest.mark.parametrize("code", [O.BF16, O.E4M3FN])
+@pytest.mark.parametrize("start", [0, 8, 16 * 1024 + 8])
+def test_pack_bits_aligned_large(dev, code, start):
+    """8-aligned starts take the staged-group path: several workgroups and
+    grid-stride iterations, partial last group, stale bytes around the run."""
+    rng = np.random.default_rng(start + code)
+    dt = _np_dt(code)
+    b = O.bits_per_value(code)
+    for n in (8 * 256 * 3 + 5, 100_003):
+        raw = rng.integers(0, np.iinfo(dt).max + 1, n).astype(dt)
+        nbytes = (((start + n) * b + 7) // 8 + 11) // 4 * 4
+        init = rng.integers(0, 256, nbytes).astype(np.uint8)
+        got, err = _call_pack(dev, raw, code, init, start)
+        assert err == 0
+        assert (got == O.pack_bits(raw, code, init.copy(), start)).all()
+
+
+def test_pack_bits_unaligned_raw(dev):
+    """Raw values not aligned for 16-byte loads take the per-dword path."""
+    from bitsparse_amd import _lib
+    L = _lib.load()
+    rng = np.random.default_rng(21)
+    raw = rng.integers(0, 1 << 16, 5001).astype(np.uint16)
+    t = from_bits(raw, torch.bfloat16).to(dev)
+    init = rng.integers(0, 256, 4 * ((5000 * 15 // 8 + 16) // 4)).astype(np.uint8)
+    stream = torch.from_numpy(init.copy()).to(dev)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    rc = L.bs_pack_bits(t.data_ptr() + 2, O.BF16, None, 5000, stream.data_ptr(), stream.numel(), None,
+                        err.data_ptr(), _lib.stream_handle(dev))
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    assert (stream.cpu().numpy() == O.pack_bits(raw[1:], O.BF16, init.copy(), 0)).all()
+
+
+@pytest.mark.parametrize("code", [O.BF16, O.E4M3FN])
 def test_pack_bits_device_count_and_capacity(dev, code):
     rng = np.random.default_rng(3)
     dt = _np_dt(code)
