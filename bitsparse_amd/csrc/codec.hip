@@ -103,14 +103,11 @@ __device__ __forceinline__ float scale_from_slot(const uint64_t* slot, uint32_t 
 
 __device__ __forceinline__ uint2 quant_chunk(const uint4 v, float scale, float rcp)
 {
-    uint2 q = {0u, 0u};
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    uint32_t p[4];
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-        uint32_t b = div_to_e4m3(bf16_to_f32(get16(v, e)), scale, rcp);
-        if (e < 4) q.x |= b << (8 * e);
-        else q.y |= b << (8 * (e - 4));
-    }
-    return q;
+    for (int k = 0; k < 4; k++) p[k] = div2_to_e4m3(bf16_to_f32(w[k] & 0xffffu), bf16_to_f32(w[k] >> 16), scale, rcp);
+    return uint2{p[0] | (p[1] << 16), p[2] | (p[3] << 16)};
 }
 
 // Chunk geometry inside tile t of a [*, N] matrix.

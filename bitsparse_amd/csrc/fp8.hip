@@ -97,11 +97,9 @@ __global__ __launch_bounds__(kFp8Threads) void quantize_e4m3_kernel(const uint16
         uint32_t w[4] = {v.x, v.y, v.z, v.w};
         uint32_t o[2] = {0u, 0u};
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            uint32_t lo = div_to_e4m3(bf16_to_f32(w[k] & 0xffffu), scale, rcp);
-            uint32_t hi = div_to_e4m3(bf16_to_f32(w[k] >> 16), scale, rcp);
-            o[k >> 1] |= (lo | (hi << 8)) << (16 * (k & 1));
-        }
+        for (int k = 0; k < 4; k++)
+            o[k >> 1] |= div2_to_e4m3(bf16_to_f32(w[k] & 0xffffu), bf16_to_f32(w[k] >> 16), scale, rcp)
+                         << (16 * (k & 1));
         reinterpret_cast<uint2*>(q)[i] = uint2{o[0], o[1]};
     }
     for (int64_t i = nvec * 8 + (int64_t)blockIdx.x * kFp8Threads + tid; i < n; i += stride)
