@@ -415,7 +415,12 @@ __device__ uint32_t wave_lookback_grouped(const CompressArgs& a, uint32_t u, uin
 //   * the partial slots at the two ends of the run, shared with the
 //     neighbouring runs, get element stores.
 // ===========================================================================
-constexpr int kRingElems = 576;     // >= 15 (pending) + 512 (one round) + 8 (overrun)
+#ifndef BS_STREAM_ROUNDS
+#define BS_STREAM_ROUNDS 2
+#endif
+constexpr int kRoundsPerPass = BS_STREAM_ROUNDS;   // rounds written before each store pass
+// >= 15 (pending) + 512 per round + 8 (overrun), a multiple of 16
+constexpr int kRingElems = 512 * kRoundsPerPass + 32;
 
 #ifndef BS_STREAM_WAVES_PER_EU
 #define BS_STREAM_WAVES_PER_EU 8
@@ -662,34 +667,38 @@ void compress_stream_kernel(CompressArgs a)
                 bool back_done = back_s >= endr;
                 int pend = 0;                   // output slot held in ring slot 0
 #pragma unroll
-                for (int k = 0; k < 8; k++) {
+                for (int k0 = 0; k0 < 8; k0 += kRoundsPerPass) {
                     if (front_done && back_done && max(pend, j_lo) >= j_hi) break;
-                    // one round at a time: nothing of round k is computed early
+                    // one pass at a time: nothing of a later pass is computed early
                     asm volatile("" : "+v"(mp[0]), "+v"(mp[1]) : : "memory");
-                    const uint32_t m = (mp[k >> 2] >> (8 * (k & 3))) & 0xffu;
-                    const uint32_t c = (uint32_t)__popc(m);
-                    const uint32_t ex = wave_incl_scan(c) - c;
-                    const int rb = a0 + (int)P[k] - pend * EPS;           // ring index of the round's first element
-                    RawOut cv;
-                    if constexpr (OUTB == 2) {
-                        const uint4 s0 = *reinterpret_cast<const uint4*>(&s_sel[m * NSEL]);
-                        const uint4 s1 = *reinterpret_cast<const uint4*>(&s_sel[m * NSEL + 4]);
-                        const uint4 v = o[k];
-                        cv.x = __builtin_amdgcn_perm(v.y, v.x, s0.x) | __builtin_amdgcn_perm(v.w, v.z, s1.x);
-                        cv.y = __builtin_amdgcn_perm(v.y, v.x, s0.y) | __builtin_amdgcn_perm(v.w, v.z, s1.y);
-                        cv.z = __builtin_amdgcn_perm(v.y, v.x, s0.z) | __builtin_amdgcn_perm(v.w, v.z, s1.z);
-                        cv.w = __builtin_amdgcn_perm(v.y, v.x, s0.w) | __builtin_amdgcn_perm(v.w, v.z, s1.w);
-                    } else {
-                        const uint2 s0 = *reinterpret_cast<const uint2*>(&s_sel[m * NSEL]);
-                        const uint2 v = o[k];
-                        cv.x = __builtin_amdgcn_perm(v.y, v.x, s0.x);
-                        cv.y = __builtin_amdgcn_perm(v.y, v.x, s0.y);
+#pragma unroll
+                    for (int kk = 0; kk < kRoundsPerPass; kk++) {
+                        const int k = k0 + kk;
+                        const uint32_t m = (mp[k >> 2] >> (8 * (k & 3))) & 0xffu;
+                        const uint32_t c = (uint32_t)__popc(m);
+                        const uint32_t ex = wave_incl_scan(c) - c;
+                        const int rb = a0 + (int)P[k] - pend * EPS;       // ring index of the round's first element
+                        RawOut cv;
+                        if constexpr (OUTB == 2) {
+                            const uint4 s0 = *reinterpret_cast<const uint4*>(&s_sel[m * NSEL]);
+                            const uint4 s1 = *reinterpret_cast<const uint4*>(&s_sel[m * NSEL + 4]);
+                            const uint4 v = o[k];
+                            cv.x = __builtin_amdgcn_perm(v.y, v.x, s0.x) | __builtin_amdgcn_perm(v.w, v.z, s1.x);
+                            cv.y = __builtin_amdgcn_perm(v.y, v.x, s0.y) | __builtin_amdgcn_perm(v.w, v.z, s1.y);
+                            cv.z = __builtin_amdgcn_perm(v.y, v.x, s0.z) | __builtin_amdgcn_perm(v.w, v.z, s1.z);
+                            cv.w = __builtin_amdgcn_perm(v.y, v.x, s0.w) | __builtin_amdgcn_perm(v.w, v.z, s1.w);
+                        } else {
+                            const uint2 s0 = *reinterpret_cast<const uint2*>(&s_sel[m * NSEL]);
+                            const uint2 v = o[k];
+                            cv.x = __builtin_amdgcn_perm(v.y, v.x, s0.x);
+                            cv.y = __builtin_amdgcn_perm(v.y, v.x, s0.y);
+                        }
+                        if (c != 0u) write_compacted<OUTB>(ring + (rb + (int)ex) * OUTB, cv);
                     }
-                    if (c != 0u) write_compacted<OUTB>(ring + (rb + (int)ex) * OUTB, cv);
                     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
                     __builtin_amdgcn_wave_barrier();
                     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-                    const int done = (int)P[k + 1];
+                    const int done = (int)P[k0 + kRoundsPerPass];
                     const int npend = (a0 + done) / EPS;
                     if (!front_done && done >= front_n) {
                         front_done = true;          // pend is still 0 here
