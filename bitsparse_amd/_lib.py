@@ -17,7 +17,7 @@ LIB_NAME = "libbitsparse_hip.so"
 # BITSPARSE_HIP_LIB points at another build of the same sources (tuning sweeps)
 LIB_PATH = os.environ.get("BITSPARSE_HIP_LIB") or os.path.join(
     os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 BS_OK = 0
 BS_ERR_INVALID = 1
@@ -51,8 +51,8 @@ _SIGNATURES = {
     "bs_relu2_grad": [_vp, _i64, _i64, _vp, _int, _i64, _vp, _vp, _vp, _f32, _vp, _vp],
     "bs_amax": [_vp, _i64, _vp, _i64, _u32, _vp],
     "bs_quantize_e4m3fn": [_vp, _i64, _vp, _vp, _vp, _i64, _u32, _vp],
-    "bs_gemm_compressed_b_workspace_bytes": [_i64, _i64, _i64],
-    "bs_gemm_compressed_b": [_vp, _i64, _i64, _i64, _vp, _int, _i64, _vp, _vp, _vp, _i64, _int, _f32,
+    "bs_gemm_compressed_b_workspace_bytes": [_i64, _i64, _i64, _int],
+    "bs_gemm_compressed_b": [_vp, _i64, _i64, _i64, _int, _vp, _int, _i64, _vp, _vp, _vp, _i64, _int, _f32,
                              _vp, _vp, _vp, _i64, _vp],
     "bs_pack_bits": [_vp, _int, _vp, _i64, _vp, _i64, _vp, _vp, _vp],
     "bs_decompress_packed": [_vp, _int, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _int,

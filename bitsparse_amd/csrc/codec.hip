@@ -190,19 +190,6 @@ __device__ __forceinline__ uint32_t chunk_mask(const typename Raw<CompressTraits
     }
 }
 
-// Inclusive wave64 prefix sum (row shifts inside 16-lane rows, then the row
-// broadcasts of lanes 15 and 31).
-__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x)
-{
-    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xf, 0xf, false);   // row_shr:1
-    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xf, 0xf, false);   // row_shr:2
-    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xf, 0xf, false);   // row_shr:4
-    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xf, 0xf, false);   // row_shr:8
-    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x142, 0xa, 0xf, false);   // row_bcast:15
-    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x143, 0xc, 0xf, false);   // row_bcast:31
-    return x;
-}
-
 // Positive-bit byte of 8 bf16 values with packed 16-bit arithmetic:
 // x > 0  <=>  (bits - 1) mod 2^16 < 0x7f80.
 __device__ __forceinline__ uint32_t mask_bf16x8_pk(const uint4 v)

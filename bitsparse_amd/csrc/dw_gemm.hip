@@ -1,30 +1,36 @@
-// Reconstruct-into-LDS MFMA GEMM for gfx950:  C[M, N] = At^T @ B
-// where At is a dense [K, M] bf16 matrix (m contiguous; the MLP backward
-// passes dY itself) and B is a compressed [K, N] activation (64x64-tile
-// bitmask + prefix + values) that is never written to HBM in dense form.
+// Reconstruct-into-LDS MFMA GEMM for gfx950:  C[M, N] = A @ B
+// where A is a dense bf16 [M, K] matrix and B is a compressed [K, N]
+// activation (64x64-tile bitmask + prefix + values) that is never written to
+// HBM in dense form.
 //
 // Replaces the "decompress B to HBM, then library GEMM" of the reference's
 // AspB / AspRelu2B (lib_sparse/src/sparse_matmul.py:24-28, :109-113).  In the
-// MLP backward K = tokens, At = dY [tokens, d_out], B = h [tokens, d_ff],
+// MLP backward K = tokens, A = dY^T [d_out, tokens], B = h [tokens, d_ff],
 // C = dW2 [d_out, d_ff].
 //
-// Workgroup = 512 threads in two roles, output tile 256 (M) x 128 (N), one
-// K-step = one row of compressed B tiles (64 tokens, two tiles wide):
-//   * waves 0-3 (consumers) run the MFMAs, each on a 128 x 64 block of C
-//     (4 x 2 v_mfma_f32_32x32x16_bf16 accumulators);
-//   * waves 4-7 (producers) stage dY rows into LDS, stage the compressed
-//     value runs, and decode B row by row into LDS (one 16-byte store per
-//     bitmask byte), one step ahead of the consumers.
-// Two waves share each SIMD, so the producers' VALU/LDS work issues while
-// the consumers' MFMAs execute.  Both operands stay in their natural
-// k-outer layout in LDS; the k-contiguous MFMA fragments are read with
-// ds_read_b64_tr_b16.  Everything is double-buffered and one barrier per
-// K-step orders producers and consumers.
+// Workgroup = 256 threads: four waves, one per SIMD, output tile 256 x 256,
+// one K-step = one row of compressed B tiles (64 tokens, four tiles wide).
+// Every wave
+//   * multiplies a 128 x 128 block of C (4 x 4 v_mfma_f32_32x32x16_bf16
+//     accumulators = 256 registers per lane, kept in AGPRs), with its A
+//     fragments read straight from global memory: A is consumed k-contiguous
+//     (row-major [M, K]; a dY handed over as [K, M] is transposed once into
+//     the workspace), so A takes no LDS bandwidth;
+//   * decodes one B tile per step into the shared LDS tile: the tile's value
+//     run is loaded one step ahead and staged in LDS as bf16, then every
+//     8-element chunk is expanded from the run with v_perm_b32 byte selectors.
+//     The ReLU^2 square and the fp8 widening are applied once per stored value
+//     while the run is staged, not once per expanded element.
+// B fragments are read with ds_read_b64_tr_b16 (k-contiguous out of the
+// row-major tile).  B is double-buffered; one barrier per K-step.
 //
 // Launch order: workgroups are dispatched round-robin over the 8 XCDs, so
 // the linear workgroup id is remapped to give each XCD a contiguous range of
 // output tiles (N fastest): the workgroups resident on one XCD share their
-// dY rows, which then stay in that XCD's L2.
+// A rows, which then stay in that XCD's L2.
+#include <type_traits>
+#include <utility>
+
 #include "bs_device.h"
 #include "bs_host.h"
 
@@ -36,45 +42,34 @@ typedef short i16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 constexpr int kBM = 256;              // C rows per workgroup
-constexpr int kBN = 128;              // C columns per workgroup (two B tiles)
+constexpr int kBN = 256;              // C columns per workgroup (four B tiles)
 constexpr int kBK = 64;               // K per step (one B tile row)
-constexpr int kThreads = 512;
-constexpr int kProducer0 = 256;       // first producer thread
-#ifndef BS_GEMM_AP
-#define BS_GEMM_AP (kBM + 32)
-#endif
-#ifndef BS_GEMM_BP
-#define BS_GEMM_BP (kBN + 32)
-#endif
-// Row pitches are 64 bytes past a multiple of 256 (LDS has 64 4-byte banks):
-// the four rows read by one 16-lane group of ds_read_b64_tr_b16 then start
-// 16 banks apart and the two column halves of a 32-lane half-wave fill the
-// other 8-bank gaps, so fragment reads are conflict-free.
-constexpr int kAP = BS_GEMM_AP;       // A_s row pitch (elements): 576 bytes
-constexpr int kBP = BS_GEMM_BP;       // B_s row pitch (elements): 320 bytes
-constexpr int kRunSlots = kTileNumel / 8 + 2;   // one tile's value run + phase, 16-byte slots
-constexpr int kMaxSteps = 256;        // K-steps per workgroup (prefixes held in LDS)
+constexpr int kThreads = 256;
+// B_s row pitch (elements): 576 bytes, 64 bytes past a multiple of 256 (LDS
+// has 64 4-byte banks): the four rows read by one 16-lane group of
+// ds_read_b64_tr_b16 start 16 banks apart and the two column halves of a
+// 32-lane half-wave fill the other 8-bank gaps, so fragment reads are
+// conflict-free.
+constexpr int kBP = kBN + 32;
+constexpr int kRunSlots = kTileNumel / 8 + 2;   // one bf16-staged run + phase, 16-byte slots
+constexpr int kMaxSteps = 256;        // K-steps per workgroup (prefixes held in registers)
 constexpr int kCus = 256;             // MI355X compute units (split-K sizing)
 constexpr int kXcds = 8;
 
 // LDS carve-up (bytes)
-constexpr int kOffA = 0;                                   // A_s[2][64][kAP] bf16
-constexpr int kOffB = kOffA + 2 * kBK * kAP * 2;           // B_s[2][64][kBP] bf16
-constexpr int kOffRun = kOffB + 2 * kBK * kBP * 2;         // run_s[2][2 tiles][kRunSlots] uint4
-constexpr int kOffBm = kOffRun + 2 * 2 * kRunSlots * 16;   // bm_s[2][2][64] uint64
-constexpr int kOffRp = kOffBm + 2 * 2 * 64 * 8;           // rp_s[2][2][64] uint32 (row prefixes)
-constexpr int kOffMeta = kOffRp + 2 * 2 * 64 * 4;         // meta_s[2][4] int (run phases)
-constexpr int kOffLut = kOffMeta + 2 * 4 * 4;             // lut_s[256] uint4 byte-permute selectors
+constexpr int kOffB = 0;                                   // B_s[2][64][kBP] bf16
+constexpr int kOffRun = kOffB + 2 * kBK * kBP * 2;         // run_s[2][4 waves][kRunSlots] uint4
+constexpr int kOffBm = kOffRun + 2 * 4 * kRunSlots * 16;   // bm_s[4][64] uint64 (bitmask rows)
+constexpr int kOffRp = kOffBm + 4 * 64 * 8;               // rp_s[4][64] uint32 (row prefixes)
+constexpr int kOffLut = kOffRp + 4 * 64 * 4;              // lut_s[256] uint4 byte-permute selectors
 constexpr int kLds = kOffLut + 256 * 16;
-// epilogue staging (after the main loop), 128 rows per consumer wave
-constexpr int kStF = 64 + 4;          // fp32 staging pitch (floats)
-constexpr int kStH = 64 + 8;          // bf16 staging pitch (elements)
-static_assert(4 * 128 * kStF * 4 <= kLds, "fp32 staging does not fit");
 static_assert(kLds <= 160 * 1024, "LDS budget");
 
 struct GemmArgs {
-    const uint16_t* At;           // [K, M] bf16, row stride ldat
-    int64_t M, K, ldat;
+    const uint16_t* Apk;          // A in MFMA-fragment order (pack_a_*_kernel)
+    int64_t M, K;
+    uint32_t nkb;                 // 16-wide k blocks per 32-row block of Apk
+    uint32_t nrb;                 // 32-row blocks of Apk
     const uint8_t* vals;          // compressed B
     int64_t vals_numel;
     const uint8_t* bitmask;
@@ -146,40 +141,55 @@ __device__ __forceinline__ uint4 load16(bs_rsrc rs, uint32_t off)
 {
     return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)off, 0, 0));
 }
-__device__ __forceinline__ uint64_t load8(bs_rsrc rs, uint32_t off)
+__device__ __forceinline__ uint2 load8(bs_rsrc rs, uint32_t off)
 {
     typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
     const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(rs, (int)off, 0, 0);
-    return (uint64_t)v[0] | ((uint64_t)v[1] << 32);
+    return uint2{v[0], v[1]};
 }
-// 16 bytes at `off` read one element at a time (each element range-checked)
-template <int VB>
-__device__ __forceinline__ uint4 load16_tail(bs_rsrc rs, uint32_t off)
+__device__ __forceinline__ uint32_t load4(bs_rsrc rs, uint32_t off)
+{
+    return __builtin_amdgcn_raw_buffer_load_b32(rs, (int)off, 0, 0);
+}
+
+// A staging unit of the value run: 16 bytes (plain bf16 runs), 8 bytes
+// (bf16 runs to square) or 4 bytes (fp8 runs).
+template <int UB>
+using RunUnit = typename std::conditional<UB == 16, uint4,
+                                          typename std::conditional<UB == 8, uint2, uint32_t>::type>::type;
+
+template <int UB>
+__device__ __forceinline__ RunUnit<UB> load_unit(bs_rsrc rs, uint32_t off)
+{
+    if constexpr (UB == 16) return load16(rs, off);
+    else if constexpr (UB == 8) return load8(rs, off);
+    else return load4(rs, off);
+}
+
+// The unit at `off` read one element at a time: used for the unit that holds
+// the end of `vals`, where a whole-unit read would cross the buffer's end.
+template <int UB, int VB>
+__device__ __forceinline__ RunUnit<UB> load_unit_tail(bs_rsrc rs, uint32_t off)
 {
     uint32_t w[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int e = 0; e < 16 / VB; e++) {
+    for (int e = 0; e < UB / VB; e++) {
         const uint32_t x = VB == 2 ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, (int)(off + 2 * e), 0, 0)
                                    : (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rs, (int)(off + e), 0, 0);
         w[(e * VB) >> 2] |= x << ((e * VB * 8) & 31);
     }
-    return uint4{w[0], w[1], w[2], w[3]};
+    if constexpr (UB == 16) return uint4{w[0], w[1], w[2], w[3]};
+    else if constexpr (UB == 8) return uint2{w[0], w[1]};
+    else return w[0];
 }
 
-// The 4 stored values starting at element r of a run staged in LDS, from
-// dword-aligned reads (unaligned LDS reads stall for tens of cycles):
-// bf16 -> 8 bytes from three dwords, fp8 -> 4 bytes (in .x) from two.
-template <int VB>
+// The 4 bf16 values starting at element r of a run staged in LDS, from
+// dword-aligned reads (unaligned LDS reads stall for tens of cycles).
 __device__ __forceinline__ uint2 window(const uint32_t* run32, uint32_t r)
 {
-    const uint32_t o = r * VB, q = o >> 2, sh = o & 3;
-    const uint32_t d0 = run32[q], d1 = run32[q + 1];
-    if constexpr (VB == 2) {
-        const uint32_t d2 = run32[q + 2];
-        return uint2{__builtin_amdgcn_alignbyte(d1, d0, sh), __builtin_amdgcn_alignbyte(d2, d1, sh)};
-    } else {
-        return uint2{__builtin_amdgcn_alignbyte(d1, d0, sh), 0u};
-    }
+    const uint32_t o = r * 2, q = o >> 2, sh = o & 3;
+    const uint32_t d0 = run32[q], d1 = run32[q + 1], d2 = run32[q + 2];
+    return uint2{__builtin_amdgcn_alignbyte(d1, d0, sh), __builtin_amdgcn_alignbyte(d2, d1, sh)};
 }
 
 // compile-time register-set index
@@ -188,443 +198,526 @@ struct IC {
     static constexpr int value = P;
 };
 
+// f(IC<0>{}), ..., f(IC<N-1>{}) with compile-time indices
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>)
+{
+    (f(IC<I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f)
+{
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
 template <int V_T, bool SQUARE, bool HAS_SCALE>
 __global__ __launch_bounds__(kThreads, 1) void gemm_cb_kernel(GemmArgs a)
 {
-    constexpr int VB = V_T == DT_BF16 ? 2 : 1;
-    constexpr int EPS = 16 / VB;                                 // elements per 16-byte slot
-    constexpr int RUN_REGS = (kTileNumel / EPS + 2 + 255) / 256; // run slots per producer lane per tile
+    constexpr int VB = V_T == DT_BF16 ? 2 : 1;                   // stored value bytes
+    constexpr int GV = SQUARE ? 4 : 8;                           // values per staging unit
+    constexpr int UB = GV * VB;                                  // stored bytes per unit
+    constexpr int RX = ((GV - 1 + kTileNumel + GV - 1) / GV + 63) / 64;   // units per lane, worst case
+    // units per lane loaded one step ahead (<= 20 registers: 2560 plain bf16
+    // values, 1536 bf16 / 1024 fp8 values to square); a denser tile's
+    // remaining units are loaded when the run is staged
+    constexpr int RXP = UB == 16 ? 5 : (UB == 8 ? 6 : 4);
+    typedef RunUnit<UB> Unit;
 
     __shared__ __align__(16) uint8_t lds[kLds];
-    uint16_t* A_s = reinterpret_cast<uint16_t*>(lds + kOffA);
     uint16_t* B_s = reinterpret_cast<uint16_t*>(lds + kOffB);
     uint4* run_s = reinterpret_cast<uint4*>(lds + kOffRun);
     uint64_t* bm_s = reinterpret_cast<uint64_t*>(lds + kOffBm);
     uint32_t* rp_s = reinterpret_cast<uint32_t*>(lds + kOffRp);
-    int* meta_s = reinterpret_cast<int*>(lds + kOffMeta);
     uint4* lut_s = reinterpret_cast<uint4*>(lds + kOffLut);
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
     // ---- XCD-aware tile order: XCD x runs a contiguous range of tile ids
     const uint32_t nb = gridDim.x, b = blockIdx.x;
     const uint32_t xcd = b % kXcds, q = b / kXcds;
     const uint32_t per = nb / kXcds, rem = nb % kXcds;
     const uint32_t id = xcd * per + min(xcd, rem) + q;
-    const uint32_t tn = id % a.tiles_n;
+    // the divisions run on the VALU: pin their (uniform) results to SGPRs so
+    // the buffer descriptors built from them stay scalar
+    const uint32_t tn = (uint32_t)__builtin_amdgcn_readfirstlane((int)(id % a.tiles_n));
     const uint32_t rest = id / a.tiles_n;
-    const uint32_t tm = rest % a.tiles_m;
-    const uint32_t split = rest / a.tiles_m;
+    const uint32_t tm = (uint32_t)__builtin_amdgcn_readfirstlane((int)(rest % a.tiles_m));
+    const uint32_t split = (uint32_t)__builtin_amdgcn_readfirstlane((int)(rest / a.tiles_m));
 
-    const uint32_t nt0 = tn * 2;                       // first B tile column
-    const bool two = nt0 + 1 < a.grid_n;               // second B tile exists
+    const uint32_t nt0 = tn * 4;                       // first B tile column
+    const uint32_t tcol = nt0 + (uint32_t)wave;        // the B tile column this wave decodes
+    const bool has_tile = tcol < a.grid_n;
     const int64_t m0 = (int64_t)tm * kBM;
     const uint32_t kt0 = split * a.ksteps_per_split;
     const uint32_t kt1 = min(a.ksteps, kt0 + a.ksteps_per_split);
     const int nsteps = kt1 > kt0 ? (int)(kt1 - kt0) : 0;
+    const int last = nsteps - 1;
 
-    // Byte-permute selectors per bitmask byte b.  A chunk's values are read
-    // as two windows of 4 stored values: window A from the chunk's first rank
-    // (elements 0-3 draw from it), window B from the rank of element 4.
-    // Selector byte x picks byte x of the window, 0x0c gives 0x00.
-    //   bf16: dword d = elements 2d, 2d+1 (d < 2: window A, else window B)
-    //   fp8 : dword h = elements 4h..4h+3 (h = 0: window A, 1: window B)
-    if (tid >= kProducer0) {
-        const uint32_t b = (uint32_t)(tid - kProducer0);
+    // Byte-permute selectors per bitmask byte b for a bf16 run.  A chunk's
+    // values are read as two windows of 4 values: window A from the chunk's
+    // first rank (elements 0-3 draw from it), window B from the rank of
+    // element 4.  Selector byte x picks byte x of the window, 0x0c gives 0x00;
+    // dword d = elements 2d, 2d+1 (d < 2: window A, else window B).
+    {
+        const uint32_t bb = (uint32_t)tid;
         uint32_t sel[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
         for (int e = 0; e < 8; e++) {
-            const uint32_t nib = e < 4 ? (b & 15u) : (b >> 4);
+            const uint32_t nib = e < 4 ? (bb & 15u) : (bb >> 4);
             const int ee = e & 3;
             const uint32_t bit = (nib >> ee) & 1u;
             const uint32_t rank = (uint32_t)__builtin_popcount(nib & ((1u << ee) - 1u));
-            if constexpr (VB == 2) {
-                const uint32_t lo = bit ? 2u * rank : 12u, hi = bit ? 2u * rank + 1u : 12u;
-                sel[e >> 1] |= (lo | (hi << 8)) << (16 * (e & 1));
-            } else {
-                sel[e >> 2] |= (bit ? rank : 12u) << (8 * ee);
+            const uint32_t lo = bit ? 2u * rank : 12u, hi = bit ? 2u * rank + 1u : 12u;
+            sel[e >> 1] |= (lo | (hi << 8)) << (16 * (e & 1));
+        }
+        lut_s[bb] = uint4{sel[0], sel[1], sel[2], sel[3]};
+    }
+
+    // ---- value transform constants (ReLU^2 square, fp8 scale^2)
+    float s2b = 1.0f;
+    if constexpr (HAS_SCALE) {
+        const float sc = *a.b_scale;
+        s2b = bf16_to_f32(f32_to_bf16(sc * sc));
+    }
+    const float kr = a.relu2_scale;
+    // a cleared bit decodes to the transform of 0 (+0 unless k < 0, or the
+    // scale makes it NaN); the permutes produce +0, fixed up when different
+    const uint32_t zero_b = SQUARE ? b_elem<V_T, SQUARE, HAS_SCALE>(0u, kr, s2b) : 0u;
+    const uint32_t zero_pair = zero_b | (zero_b << 16);
+    const bool zfix = SQUARE && zero_b != 0u;
+
+    // ---- prefix[t], prefix[t+1] of every step of this wave's tile column,
+    // loaded once: lane l of register w holds step 64*w + l
+    // (nsteps <= kMaxSteps = 256); steps are picked with v_readlane
+    uint32_t pq[2][kMaxSteps / 64];
+#pragma unroll
+    for (int w = 0; w < kMaxSteps / 64; w++) {
+        const int st = 64 * w + lane;
+        uint32_t v0 = 0u, v1 = 0u;
+        if (has_tile && st < nsteps) {
+            const size_t t = (size_t)(kt0 + (uint32_t)st) * a.grid_n + tcol;
+            v0 = a.prefix[t];
+            v1 = a.prefix[t + 1];
+        }
+        pq[0][w] = v0;
+        pq[1][w] = v1;
+    }
+    const int64_t vo = a.vals_offset ? *a.vals_offset : 0;
+    // value run of step s (wave-uniform): GV-aligned start e0 (elements),
+    // phase = run start - e0, nunits staging units
+    auto run_geom = [&](int s, int64_t& e0, int& phase, int& nunits) __attribute__((always_inline)) {
+        const int w = s >> 6, l = s & 63;
+        uint32_t p[2];
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            const uint32_t x0 = (uint32_t)__builtin_amdgcn_readlane((int)pq[c][0], l);
+            const uint32_t x1 = (uint32_t)__builtin_amdgcn_readlane((int)pq[c][1], l);
+            const uint32_t x2 = (uint32_t)__builtin_amdgcn_readlane((int)pq[c][2], l);
+            const uint32_t x3 = (uint32_t)__builtin_amdgcn_readlane((int)pq[c][3], l);
+            p[c] = w == 0 ? x0 : w == 1 ? x1 : w == 2 ? x2 : x3;
+        }
+        const int64_t run0 = vo + (int64_t)p[0];
+        int64_t cnt = (int64_t)p[1] - (int64_t)p[0];
+        cnt = cnt < 0 ? 0 : (cnt > kTileNumel ? kTileNumel : cnt);
+        phase = (int)(run0 & (GV - 1));
+        e0 = run0 - phase;
+        nunits = cnt == 0 ? 0 : (phase + (int)cnt + GV - 1) / GV;
+    };
+
+    // ---- run staging: units of step s are loaded into registers one
+    // iteration before they are written to LDS
+    Unit rr[RXP];
+    int rr_nunits = 0;
+    int64_t rr_avail = 0;
+    bool rr_tail = false;
+    bs_rsrc rr_rs;
+    auto unit_at = [&](int u) __attribute__((always_inline)) -> Unit {
+        Unit v = load_unit<UB>(rr_rs, (uint32_t)u * UB);
+        if (rr_tail && (int64_t)(u + 1) * GV > rr_avail && (int64_t)u * GV < rr_avail)
+            v = load_unit_tail<UB, VB>(rr_rs, (uint32_t)u * UB);
+        return v;
+    };
+    auto load_run = [&](int s) __attribute__((always_inline)) {
+        int64_t e0;
+        int phase, nunits;
+        run_geom(s, e0, phase, nunits);
+        const int64_t avail = a.vals_numel - e0;       // elements readable from e0
+        const bool ok = e0 >= 0 && avail > 0 && nunits > 0;
+        int64_t bytes = ok ? avail * VB : 0;
+        if (bytes > (int64_t)nunits * UB) bytes = (int64_t)nunits * UB;
+        rr_nunits = ok ? nunits : 0;
+        rr_avail = avail;
+        rr_rs = make_rsrc(ok ? a.vals + e0 * VB : a.vals, (uint32_t)bytes);
+        rr_tail = ok && (int64_t)nunits * GV > avail;   // the run's last unit crosses the end of vals
+#pragma unroll
+        for (int x = 0; x < RXP; x++)
+            if (x * 64 < rr_nunits) rr[x] = unit_at(x * 64 + lane);
+    };
+    auto store_run = [&](int buf) __attribute__((always_inline)) {
+        uint8_t* dst = reinterpret_cast<uint8_t*>(run_s + (buf * 4 + wave) * kRunSlots);
+#pragma unroll
+        for (int x = 0; x < RX; x++) {
+            if (x * 64 < rr_nunits) {
+                const int u = x * 64 + lane;
+                if (x >= RXP) rr[x % RXP] = unit_at(u);
+                if (u < rr_nunits) {
+                    if constexpr (!SQUARE) {
+                        *reinterpret_cast<uint4*>(dst + u * 16) = rr[x % RXP];
+                    } else {
+                        uint32_t y[4];
+#pragma unroll
+                        for (int e = 0; e < 4; e++) {
+                            uint32_t raw;
+                            const Unit ux = rr[x % RXP];
+                            if constexpr (VB == 2) raw = ((e < 2 ? ux.x : ux.y) >> (16 * (e & 1))) & 0xffffu;
+                            else raw = (ux >> (8 * e)) & 0xffu;
+                            y[e] = b_elem<V_T, SQUARE, HAS_SCALE>(raw, kr, s2b);
+                        }
+                        *reinterpret_cast<uint2*>(dst + u * 8) = uint2{y[0] | (y[1] << 16), y[2] | (y[3] << 16)};
+                    }
+                }
             }
         }
-        lut_s[b] = uint4{sel[0], sel[1], sel[2], sel[3]};
-    }
-    __syncthreads();
+    };
 
-    f32x16_t acc[4][2];
+    // ---- bitmask rows: lane r holds row r of this wave's tile of step s
+    auto load_bm = [&](int s) __attribute__((always_inline)) -> uint64_t {
+        const size_t t = (size_t)(kt0 + (uint32_t)s) * a.grid_n + tcol;
+        const bs_rsrc rs = make_rsrc(a.bitmask + (has_tile ? t : 0) * kTileBytes,
+                                     has_tile ? (uint32_t)kTileBytes : 0u);
+        const uint2 v = load8(rs, (uint32_t)lane * 8u);
+        return (uint64_t)v.x | ((uint64_t)v.y << 32);
+    };
+
+    // ---- decode step s (run in run_s[rb], bitmask rows bmr) into B_s[bb],
+    // columns 64*wave .. +64.  Lane l handles chunk c = l%8 (8 columns at 8c)
+    // of eight rows, row = 8i + roff(l/8), i = 0..7; roff pairs rows two apart
+    // in each 16-lane group so the 16-byte stores of a group hit disjoint banks.
+    const int dc = lane & 7, dg = lane >> 3;
+    const int roff = ((dg & 1) << 1) | ((dg >> 1) & 1) | (dg & 4);
+    const uint64_t below_mask = dc == 0 ? 0ull : (~0ull >> (64 - 8 * dc));
+    // row table of step s: bm_s = bitmask rows, rp_s = run index of each
+    // row's first value (phase + exclusive prefix of the row popcounts)
+    auto decode_rows = [&](int s, uint64_t bmr) __attribute__((always_inline)) {
+        int64_t e0;
+        int phase, nunits;
+        run_geom(s, e0, phase, nunits);
+        const uint32_t c = (uint32_t)__popcll(bmr);
+        const uint32_t rp = wave_incl_scan(c) - c;
+        bm_s[wave * 64 + lane] = bmr;
+        rp_s[wave * 64 + lane] = rp + (uint32_t)phase;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+    // The decode of one chunk in three stages (compile-time chunk index C,
+    // row 8C + roff), so that the stages of successive chunks can be spread
+    // between the MFMAs of the step being multiplied:
+    //   stage_r: the row's bitmask word and run index from the row table
+    //   stage_s: ranks, the byte-permute selectors and the two value windows
+    //   stage_w: the permutes and the 16-byte store into B_s
+    struct DecR {
+        uint64_t mrow;
+        uint32_t rpr;
+    };
+    struct DecS {
+        uint4 sel;
+        uint2 wa, wb;
+    };
+    DecR dr[2];
+    DecS dq[2];
+    auto stage_r = [&](auto CI) __attribute__((always_inline)) {
+        constexpr int C = decltype(CI)::value;
+        const int row = 8 * C + roff;
+        dr[C & 1].mrow = bm_s[wave * 64 + row];
+        dr[C & 1].rpr = rp_s[wave * 64 + row];
+    };
+    auto stage_s = [&](auto CI, const uint32_t* run32) __attribute__((always_inline)) {
+        constexpr int C = decltype(CI)::value;
+        const uint64_t mrow = dr[C & 1].mrow;
+        const uint32_t byte = (uint32_t)(mrow >> (8 * dc)) & 0xffu;
+        const uint32_t ra = dr[C & 1].rpr + (uint32_t)__popcll(mrow & below_mask);
+        const uint32_t rbk = ra + (uint32_t)__builtin_popcount(byte & 15u);
+        dq[C & 1].sel = lut_s[byte];
+        dq[C & 1].wa = window(run32, ra);
+        dq[C & 1].wb = window(run32, rbk);
+    };
+    auto stage_w = [&](auto CI, uint16_t* dst) __attribute__((always_inline)) {
+        constexpr int C = decltype(CI)::value;
+        const DecS& q = dq[C & 1];
+        const uint32_t w0 = __builtin_amdgcn_perm(q.wa.y, q.wa.x, q.sel.x);
+        const uint32_t w1 = __builtin_amdgcn_perm(q.wa.y, q.wa.x, q.sel.y);
+        const uint32_t w2 = __builtin_amdgcn_perm(q.wb.y, q.wb.x, q.sel.z);
+        const uint32_t w3 = __builtin_amdgcn_perm(q.wb.y, q.wb.x, q.sel.w);
+        *reinterpret_cast<uint4*>(&dst[(8 * C + roff) * kBP]) = uint4{w0, w1, w2, w3};
+    };
+    auto run_ptr = [&](int rb) __attribute__((always_inline)) {
+        return reinterpret_cast<const uint32_t*>(run_s + (rb * 4 + wave) * kRunSlots);
+    };
+    auto dst_ptr = [&](int bb) __attribute__((always_inline)) {
+        return B_s + bb * (kBK * kBP) + wave * 64 + dc * 8;
+    };
+    // whole decode of the run in run_s[rb] into B_s[bb] (prologue)
+    auto decode = [&](int rb, int bb) __attribute__((always_inline)) {
+        const uint32_t* run32 = run_ptr(rb);
+        uint16_t* dst = dst_ptr(bb);
+        static_for<8>([&](auto CI) __attribute__((always_inline)) {
+            stage_r(CI);
+            stage_s(CI, run32);
+            stage_w(CI, dst);
+        });
+    };
+
+    // cleared elements of B_s[bb] (this wave's columns) -> zero_b
+    auto zero_fixup = [&](int bb) __attribute__((always_inline)) {
+        uint16_t* dst = B_s + bb * (kBK * kBP) + wave * 64 + dc * 8;
+        for (int i = 0; i < 8; i++) {
+            const int row = 8 * i + roff;
+            const uint32_t byte = (uint32_t)(bm_s[wave * 64 + row] >> (8 * dc)) & 0xffu;
+            uint4 v = *reinterpret_cast<const uint4*>(&dst[row * kBP]);
+            uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int d = 0; d < 4; d++) {
+                const uint32_t keep = (((byte >> (2 * d)) & 1u) ? 0x0000ffffu : 0u) |
+                                      (((byte >> (2 * d + 1)) & 1u) ? 0xffff0000u : 0u);
+                w[d] = (w[d] & keep) | (zero_pair & ~keep);
+            }
+            *reinterpret_cast<uint4*>(&dst[row * kBP]) = uint4{w[0], w[1], w[2], w[3]};
+        }
+    };
+
+    // ---- A fragments: lane (col = l%32, h = l/32) of block i holds row
+    // 32i + col, k = 16kk + 8h .. +7 of the step.  Apk stores exactly these
+    // 16-byte pieces lane after lane, one 1 KiB block per (32 rows, 16 k), so
+    // every fragment load is one contiguous 1 KiB read; rows past M and k past
+    // K are zero in Apk, blocks past its end read as zero.
+    const int wm = wave & 1, wn = wave >> 1;
+    const int g = lane >> 4, j = lane & 15, hh = lane >> 5, col = lane & 31;
+    const int64_t arow0 = m0 + wm * 128;
+    const uint32_t rb0 = (uint32_t)(arow0 / 32);
+    const uint32_t nrbw = rb0 < a.nrb ? min(4u, a.nrb - rb0) : 0u;    // row blocks of this wave
+    const bs_rsrc rsA = make_rsrc(nrbw ? a.Apk + (int64_t)rb0 * a.nkb * 512 : a.Apk, nrbw * a.nkb * 1024u);
+    bf16x8_t areg[4][4];
+    auto a_off = [&](int s, int i, int kk) __attribute__((always_inline)) -> uint32_t {
+        return ((uint32_t)i * a.nkb + (kt0 + (uint32_t)s) * 4u + (uint32_t)kk) * 1024u + (uint32_t)lane * 16u;
+    };
+    auto load_a = [&](int s, int kk) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) areg[i][kk] = __builtin_bit_cast(bf16x8_t, load16(rsA, a_off(s, i, kk)));
+    };
+
+    f32x16_t acc[4][4];
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++)
+        for (int jj = 0; jj < 4; jj++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+            for (int r = 0; r < 16; r++) acc[i][jj][r] = 0.0f;
 
-    // Pipeline (both roles keep two register sets, R = 0, 1, so global loads
-    // are issued two steps before their data is stored to LDS).  At the top
-    // of iteration s: A_s/B_s[s&1] hold step s; run_s[(s+1)&1] holds run(s+1);
-    // consumer set (s+1)&1 holds A(s+1), set s&1 holds A(s+2); producer set
-    // s&1 holds run(s+2), set (s+1)&1 holds run(s+3).  Loads past the last
-    // step re-read it.  Every global read is a raw buffer load through a
-    // wave-uniform resource whose size stops at the operand's end, so
-    // out-of-range lanes read zeros without branches.
-    const int last = nsteps - 1;
-    const IC<0> R0;
-    const IC<1> R1;
-    if (tid >= kProducer0) {
-        // =================== producers: value runs, bitmask, decode ===================
-        const int p = tid - kProducer0;                // 0..255
-        const int64_t vo = a.vals_offset ? *a.vals_offset : 0;
-        float s2b = 1.0f;
-        if constexpr (HAS_SCALE) {
-            const float sc = *a.b_scale;
-            s2b = bf16_to_f32(f32_to_bf16(sc * sc));
-        }
-        const uint32_t zero_b = HAS_SCALE ? hw_bf16(0.0f * s2b) : 0u;
-        const uint32_t zero_pair = zero_b | (zero_b << 16);
-        const float kr = a.relu2_scale;
-        const bool k_plain = kr >= 0.0f;           // k*0*0 is +0: expanded zeros need no fix-up
-        // tile whose bitmask row `lane` this wave loads (two waves per tile)
-        const int ub = __builtin_amdgcn_readfirstlane((p >> 6) & 1);
+    // B fragments of one k-quarter: lo / hi halves of the transposing reads,
+    // two sets (k-quarter parity)
+    i16x4_t blo[2][4], bhi[2][4];
+    auto read_b = [&](const uint16_t* Bs, int kk, int jj, int half, int set) __attribute__((always_inline)) {
+        const uint16_t* p = Bs + (16 * kk + 8 * hh + (j >> 2) + 4 * half) * kBP + wn * 128 + jj * 32 + 16 * (g & 1) +
+                            4 * (j & 3);
+        typedef __attribute__((address_space(3))) i16x4_t lds_i16x4;
+        const i16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p);
+        if (half) bhi[set][jj] = v;
+        else blo[set][jj] = v;
+    };
 
-        uint4 rreg[2][2][RUN_REGS];
-        int nsl[2][2] = {{0, 0}, {0, 0}};              // slots of the staged runs in rreg
-        int phs[2][2] = {{0, 0}, {0, 0}};              // their phases
-        uint64_t bmreg[2] = {0ull, 0ull};
+    // One K-step as 64 segments, one MFMA each (k-quarter kk = X/16, block
+    // i = X%16/4, jj = X%4), fenced by sched_barrier so the order below is the
+    // issue order.  A segment also carries: the reload of A(i, kk) for the
+    // next step after its last use; in the second half of a k-quarter, one
+    // transposing read of the next quarter's B fragments; and one stage of the
+    // software-pipelined decode of the next step (chunk X/8: stage_r at X%8 == 0,
+    // stage_s at X%8 == 4, stage_w four segments later).  Each segment issues
+    // a few VALU / LDS instructions in the shadow of its MFMA.
+    auto step = [&](int s_next, auto PI) __attribute__((always_inline)) {
+        constexpr int P = decltype(PI)::value;
+        const uint16_t* Bs = B_s + P * (kBK * kBP);
+        const uint32_t* run32 = run_ptr(P ^ 1);
+        uint16_t* dst = dst_ptr(P ^ 1);
+        static_for<4>([&](auto JI) __attribute__((always_inline)) {
+            read_b(Bs, 0, decltype(JI)::value, 0, 0);
+            read_b(Bs, 0, decltype(JI)::value, 1, 0);
+        });
+        static_for<64>([&](auto XI) __attribute__((always_inline)) {
+            constexpr int X = decltype(XI)::value;
+            constexpr int kk = X / 16, m = X % 16, i = m / 4, jj = m % 4;
+            const i16x8_t bw = __builtin_shufflevector(blo[kk & 1][jj], bhi[kk & 1][jj], 0, 1, 2, 3, 4, 5, 6, 7);
+            acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(areg[i][kk], __builtin_bit_cast(bf16x8_t, bw),
+                                                                 acc[i][jj], 0, 0, 0);
+            if constexpr (jj == 3) areg[i][kk] = __builtin_bit_cast(bf16x8_t, load16(rsA, a_off(s_next, i, kk)));
+            if constexpr (kk < 3 && m >= 8) read_b(Bs, kk + 1, (m - 8) / 2, (m - 8) % 2, (kk + 1) & 1);
+            if constexpr (X % 8 == 0) stage_r(IC<X / 8>{});
+            if constexpr (X % 8 == 4) stage_s(IC<X / 8>{}, run32);
+            if constexpr (X % 8 == 0 && X >= 8) stage_w(IC<X / 8 - 1>{}, dst);
+            __builtin_amdgcn_sched_barrier(0);
+        });
+        stage_w(IC<7>{}, dst);
+    };
 
-        // prefix[t], prefix[t+1], prefix[t+2] of every step this workgroup
-        // visits, loaded once: lane l of register w holds step 64*w + l
-        // (nsteps <= kMaxSteps = 256); the loop picks them with v_readlane
-        uint32_t pq[3][kMaxSteps / 64];
+    // Pipeline.  At the top of iteration s: B_s[s&1] holds B(s), run_s[(s+1)&1]
+    // holds run(s+1), bm_cur holds the bitmask rows of step s+1 and areg A(s).
+    // The iteration loads run(s+2) and the rows of step s+2, multiplies step s
+    // while decoding B(s+1) and streaming in A(s+1), stages run(s+2) and meets
+    // the other waves at the barrier.  Loads past the last step re-read it.
+    uint64_t bm_cur = 0ull;
+    __syncthreads();                                   // lut_s
+    if (nsteps > 0) {
 #pragma unroll
-        for (int w = 0; w < kMaxSteps / 64; w++) {
-            const int st = 64 * w + lane;
-            uint32_t v0 = 0u, v1 = 0u, v2 = 0u;
-            if (st < nsteps) {
-                const size_t t = (size_t)(kt0 + (uint32_t)st) * a.grid_n + nt0;
-                v0 = a.prefix[t];
-                v1 = a.prefix[t + 1];
-                v2 = two ? a.prefix[t + 2] : v1;
-            }
-            pq[0][w] = v0;
-            pq[1][w] = v1;
-            pq[2][w] = v2;
-        }
-        uint32_t pf[3];
-        auto load_pre = [&](int s) __attribute__((always_inline)) {
-            const int w = s >> 6, l = s & 63;
-#pragma unroll
-            for (int c = 0; c < 3; c++) {
-                const uint32_t x0 = (uint32_t)__builtin_amdgcn_readlane((int)pq[c][0], l);
-                const uint32_t x1 = (uint32_t)__builtin_amdgcn_readlane((int)pq[c][1], l);
-                const uint32_t x2 = (uint32_t)__builtin_amdgcn_readlane((int)pq[c][2], l);
-                const uint32_t x3 = (uint32_t)__builtin_amdgcn_readlane((int)pq[c][3], l);
-                pf[c] = w == 0 ? x0 : w == 1 ? x1 : w == 2 ? x2 : x3;
-            }
-        };
-        // value run of tile u of the step whose prefixes are in pf
-        // (wave-uniform): 16-byte aligned start e0 (elements), phase = run
-        // start - e0, nslots 16-byte slots
-        auto run_geom = [&](int u, int64_t& e0, int& phase, int& nslots) __attribute__((always_inline)) {
-            const uint32_t p0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)(u ? pf[1] : pf[0]));
-            const uint32_t p1 = (uint32_t)__builtin_amdgcn_readfirstlane((int)(u ? pf[2] : pf[1]));
-            const int64_t run0 = vo + (int64_t)p0;
-            int64_t cnt = (int64_t)p1 - (int64_t)p0;
-            cnt = cnt < 0 ? 0 : (cnt > kTileNumel ? kTileNumel : cnt);
-            phase = (int)(run0 & (EPS - 1));             // vals itself is 16-byte aligned
-            e0 = run0 - phase;
-            nslots = (phase + (int)cnt + EPS - 1) / EPS;
-        };
-        // bitmask rows and the 16-byte-aligned value runs of step s's two tiles
-        auto load_run = [&](int s, auto R) __attribute__((always_inline)) {
-            constexpr int RS = decltype(R)::value;
-            const size_t t0 = (size_t)(kt0 + (uint32_t)s) * a.grid_n + nt0;
-            {
-                const bs_rsrc rs = make_rsrc(a.bitmask + (t0 + ub) * kTileBytes,
-                                             (ub == 0 || two) ? (uint32_t)kTileBytes : 0u);
-                bmreg[RS] = load8(rs, (uint32_t)lane * 8u);
-            }
-#pragma unroll
-            for (int u = 0; u < 2; u++) {
-                int64_t e0;
-                int phase, nslots;
-                run_geom(u, e0, phase, nslots);
-                nsl[RS][u] = nslots;
-                phs[RS][u] = phase;
-                const int64_t avail = a.vals_numel - e0;        // elements readable from e0
-                const bool ok = e0 >= 0 && avail > 0;
-                int64_t bytes = ok ? avail * VB : 0;
-                if (bytes > (int64_t)nslots * 16) bytes = (int64_t)nslots * 16;
-                const bs_rsrc rs = make_rsrc(ok ? a.vals + e0 * VB : a.vals, (uint32_t)bytes);
-#pragma unroll
-                for (int i = 0; i < RUN_REGS; i++) {
-                    const int sl = i * 256 + p;
-                    uint4 v = load16(rs, (uint32_t)sl * 16u);
-                    // the slot holding the end of `vals` is read element by element
-                    if ((int64_t)(sl + 1) * EPS > avail && (int64_t)sl * EPS < avail && sl < nslots)
-                        v = load16_tail<VB>(rs, (uint32_t)sl * 16u);
-                    rreg[RS][u][i] = v;
-                }
-            }
-            load_pre(min(s + 1, last));
-        };
-        auto store_run = [&](int buf, auto R) __attribute__((always_inline)) {
-            constexpr int RS = decltype(R)::value;
-#pragma unroll
-            for (int u = 0; u < 2; u++)
-#pragma unroll
-                for (int i = 0; i < RUN_REGS; i++) {
-                    const int sl = i * 256 + p;
-                    if (sl < nsl[RS][u]) run_s[(buf * 2 + u) * kRunSlots + sl] = rreg[RS][u][i];
-                }
-            if (p < 128) {                             // producer waves 0 and 1: one tile each
-                // exclusive scan of the row popcounts (0..64, 7 bits) from
-                // one ballot per bit: no LDS round trip
-                const uint32_t c = (uint32_t)__popcll(bmreg[RS]);
-                uint32_t x = 0;
-#pragma unroll
-                for (int bit = 0; bit < 7; bit++) x += popc_below(__ballot(c & (1u << bit))) << bit;
-                bm_s[(buf * 2 + ub) * 64 + lane] = bmreg[RS];
-                rp_s[(buf * 2 + ub) * 64 + lane] = x;
-                if (lane < 2) meta_s[buf * 4 + lane] = phs[RS][lane];
-            }
-        };
-        // decode step s from run/bitmask buffer rb into B_s[bb]; chunk
-        // c = i*256 + p covers row c/16, tile (c/8)%2, 8 columns at 8*(c%8).
-        // Each chunk reads two 4-value windows of its tile's staged run and
-        // expands them with v_perm_b32 (selectors from lut_s, 0x00 for cleared
-        // bits).  All LDS reads of the four chunks precede the writes.
-        const int du = (p >> 3) & 1, dn0 = (p & 7) * 8;
-        const uint64_t below_mask = dn0 == 0 ? 0ull : (~0ull >> (64 - dn0));
-        auto decode = [&](int rb, int bb) __attribute__((always_inline)) {
-            const uint32_t* run32 = reinterpret_cast<const uint32_t*>(run_s + (rb * 2 + du) * kRunSlots);
-            const uint32_t phu = (uint32_t)meta_s[rb * 4 + du];
-            uint64_t mrow[4];
-            uint32_t rp[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int k = 16 * i + (p >> 4);
-                mrow[i] = bm_s[(rb * 2 + du) * 64 + k];
-                rp[i] = rp_s[(rb * 2 + du) * 64 + k];
-            }
-            uint32_t byte[4];
-            uint4 sel[4];
-            uint2 wa[4], wb[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                byte[i] = (uint32_t)(mrow[i] >> dn0) & 0xffu;
-                const uint32_t ra = phu + rp[i] + (uint32_t)__popcll(mrow[i] & below_mask);
-                const uint32_t rbk = ra + (uint32_t)__builtin_popcount(byte[i] & 15u);
-                sel[i] = lut_s[byte[i]];
-                wa[i] = window<VB>(run32, ra);
-                wb[i] = window<VB>(run32, rbk);
-            }
-            uint16_t* dst = B_s + bb * (kBK * kBP);
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                uint32_t w[4];
-                if constexpr (VB == 2) {
-                    w[0] = __builtin_amdgcn_perm(wa[i].y, wa[i].x, sel[i].x);
-                    w[1] = __builtin_amdgcn_perm(wa[i].y, wa[i].x, sel[i].y);
-                    w[2] = __builtin_amdgcn_perm(wb[i].y, wb[i].x, sel[i].z);
-                    w[3] = __builtin_amdgcn_perm(wb[i].y, wb[i].x, sel[i].w);
-                    if constexpr (SQUARE) {
-#pragma unroll
-                        for (int d = 0; d < 4; d++)
-                            w[d] = b_elem<V_T, SQUARE, HAS_SCALE>(w[d] & 0xffffu, kr, s2b) |
-                                   (b_elem<V_T, SQUARE, HAS_SCALE>(w[d] >> 16, kr, s2b) << 16);
-                    }
-                } else {
-                    const uint32_t d0 = __builtin_amdgcn_perm(wa[i].x, wa[i].x, sel[i].x);
-                    const uint32_t d1 = __builtin_amdgcn_perm(wb[i].x, wb[i].x, sel[i].y);
-#pragma unroll
-                    for (int d = 0; d < 4; d++) {
-                        const uint32_t src = d < 2 ? d0 : d1;
-                        const uint32_t sh = 16 * (d & 1);
-                        w[d] = b_elem<V_T, SQUARE, HAS_SCALE>((src >> sh) & 0xffu, kr, s2b) |
-                               (b_elem<V_T, SQUARE, HAS_SCALE>((src >> (sh + 8)) & 0xffu, kr, s2b) << 16);
-                    }
-                }
-                if constexpr (SQUARE) {
-                    if (!k_plain) {   // negative or NaN k: cleared elements must stay zero_b
-#pragma unroll
-                        for (int d = 0; d < 4; d++) {
-                            const uint32_t keep = (((byte[i] >> (2 * d)) & 1u) ? 0x0000ffffu : 0u) |
-                                                  (((byte[i] >> (2 * d + 1)) & 1u) ? 0xffff0000u : 0u);
-                            w[d] = (w[d] & keep) | (zero_pair & ~keep);
-                        }
-                    }
-                }
-                const int k = 16 * i + (p >> 4);
-                *reinterpret_cast<uint4*>(&dst[k * kBP + du * 64 + dn0]) = uint4{w[0], w[1], w[2], w[3]};
-            }
-        };
-
-        if (nsteps > 0) {
-            load_pre(0);
-            load_run(0, R0);
-            store_run(0, R0);
-            load_run(min(1, last), R1);
-            load_run(min(2, last), R0);
-        }
-        __syncthreads();
-        if (nsteps > 0) {
-            decode(0, 0);
-            store_run(1, R1);
-            load_run(min(3, last), R1);
-        }
-        __syncthreads();
-        // iteration s (R = register set s&1): the consumers multiply step s
-        auto iteration = [&](int s, auto R) __attribute__((always_inline)) {
-            constexpr int P = decltype(R)::value;
-            store_run(P, R);                              // run(s+2)
-            load_run(min(s + 4, last), R);
-            if (s + 1 < nsteps) decode(P ^ 1, P ^ 1);     // B(s+1)
-            __syncthreads();
-        };
-        int s = 0;
-        for (; s + 1 < nsteps; s += 2) {
-            iteration(s, R0);
-            iteration(s + 1, R1);
-        }
-        if (s < nsteps) iteration(s, R0);
-    } else {
-        // =================== consumers: dY tile and MFMAs ===================
-        uint4 areg[2][8];
-        // dY rows of step s: chunk c = i*256 + tid -> row c/32, 8 m at (c%32)*8.
-        // Rows past K lie outside the resource and read as zero; columns past M
-        // only feed C rows that are never stored.
-        auto load_a = [&](int s, auto R) __attribute__((always_inline)) {
-            const int64_t k0 = (int64_t)(kt0 + (uint32_t)s) * kBK;
-            const int64_t rows = a.K - k0 < kBK ? a.K - k0 : kBK;
-            const bs_rsrc rs = make_rsrc(a.At + k0 * a.ldat, (uint32_t)(rows * a.ldat * 2));
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const int c = i * 256 + tid;
-                const uint32_t off = (uint32_t)(((c >> 5) * a.ldat + m0 + (c & 31) * 8) * 2);
-                areg[decltype(R)::value][i] = load16(rs, off);
-            }
-        };
-        auto store_a = [&](int buf, auto R) __attribute__((always_inline)) {
-            uint16_t* dst = A_s + buf * (kBK * kAP);
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const int c = i * 256 + tid;
-                *reinterpret_cast<uint4*>(&dst[(c >> 5) * kAP + (c & 31) * 8]) = areg[decltype(R)::value][i];
-            }
-        };
-        if (nsteps > 0) {
-            load_a(0, R0);
-            store_a(0, R0);
-            load_a(min(1, last), R1);
-            load_a(min(2, last), R0);
-        }
-        __syncthreads();
-        __syncthreads();
-        const int wm = wave & 1, wn = wave >> 1;
-        const int g = lane >> 4, j = lane & 15;
-        auto iteration = [&](int s, auto R) __attribute__((always_inline)) {
-            constexpr int P = decltype(R)::value;
-            const IC<P ^ 1> Rn;
-            const uint16_t* As = A_s + P * (kBK * kAP);
-            const uint16_t* Bs = B_s + P * (kBK * kBP);
-            // A(s+1) is stored to the other buffer and A(s+3) loaded in
-            // quarters between the MFMA blocks
-            const int64_t k0n = (int64_t)(kt0 + (uint32_t)min(s + 3, last)) * kBK;
-            const int64_t rows_n = a.K - k0n < kBK ? a.K - k0n : kBK;
-            const bs_rsrc rs_n = make_rsrc(a.At + k0n * a.ldat, (uint32_t)(rows_n * a.ldat * 2));
-            uint16_t* dst_n = A_s + (P ^ 1) * (kBK * kAP);
-#pragma unroll
-            for (int kk = 0; kk < 4; kk++) {
-                const int k0 = kk * 16 + 8 * (g >> 1);
-                bf16x8_t af[4], bfr[2];
-#pragma unroll
-                for (int i = 0; i < 4; i++) af[i] = tr_frag(As, kAP, k0, wm * 128 + i * 32 + 16 * (g & 1), j);
-#pragma unroll
-                for (int jj = 0; jj < 2; jj++) bfr[jj] = tr_frag(Bs, kBP, k0, wn * 64 + jj * 32 + 16 * (g & 1), j);
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-#pragma unroll
-                    for (int jj = 0; jj < 2; jj++)
-                        acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[jj], acc[i][jj], 0, 0, 0);
-#pragma unroll
-                for (int h = 0; h < 2; h++) {
-                    const int i = kk * 2 + h;
-                    const int c = i * 256 + tid;
-                    *reinterpret_cast<uint4*>(&dst_n[(c >> 5) * kAP + (c & 31) * 8]) = areg[P ^ 1][i];
-                    areg[P ^ 1][i] = load16(rs_n, (uint32_t)(((c >> 5) * a.ldat + m0 + (c & 31) * 8) * 2));
-                }
-            }
-            __syncthreads();
-        };
-        int s = 0;
-        for (; s + 1 < nsteps; s += 2) {
-            iteration(s, R0);
-            iteration(s + 1, R1);
-        }
-        if (s < nsteps) iteration(s, R0);
+        for (int kk = 0; kk < 4; kk++) load_a(0, kk);
+        load_run(0);
+        bm_cur = load_bm(0);
+        store_run(0);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        decode_rows(0, bm_cur);
+        decode(0, 0);
+        if (zfix) zero_fixup(0);
+        load_run(min(1, last));
+        bm_cur = load_bm(min(1, last));
+        store_run(1);
     }
-
-    // ---- epilogue: consumers stage their 128 x 64 block in LDS, then write
-    // rows with 16-byte stores.  Accumulator element r of lane l of a 32x32
-    // block sits at row 8*(r/4) + 4*(l/32) + r%4, column l%32.
     __syncthreads();
-    const bool consumer = tid < kProducer0;
-    const int wm = wave & 1, wn = (wave >> 1) & 1;
-    const int64_t row0 = m0 + wm * 128;
-    const int64_t col0 = (int64_t)nt0 * 64 + wn * 64;
-    const bool out_vec = (a.N % 8 == 0);
-    if (a.part) {
-        float* st = reinterpret_cast<float*>(lds) + (wave & 3) * (128 * kStF);
-        if (consumer) {
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int jj = 0; jj < 2; jj++)
-#pragma unroll
-                    for (int r = 0; r < 16; r++)
-                        st[(i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * kStF + jj * 32 + (lane & 31)] =
-                            acc[i][jj][r];
-        }
+    auto iteration = [&](int s, auto R) __attribute__((always_inline)) {
+        constexpr int P = decltype(R)::value;          // s & 1
+        const int s1 = min(s + 1, last), s2 = min(s + 2, last);
+        load_run(s2);
+        const uint64_t bm_next = load_bm(s2);
+        decode_rows(s1, bm_cur);
+        step(s1, R);
+        if (zfix) zero_fixup(P ^ 1);
+        store_run(P);
+        bm_cur = bm_next;
         __syncthreads();
-        if (!consumer) return;
-        float* dst = a.part + (int64_t)split * a.M * a.N;
-        for (int it = 0; it < 32; it++) {
-            const int rr = it * 4 + (lane >> 4), c4 = (lane & 15) * 4;
-            const int64_t row = row0 + rr, col = col0 + c4;
-            if (row >= a.M || col >= a.N) continue;
-            const float* s = st + rr * kStF + c4;
-            if (out_vec) {
-                *reinterpret_cast<float4*>(&dst[row * a.N + col]) = *reinterpret_cast<const float4*>(s);
-            } else {
-                for (int e = 0; e < 4; e++)
-                    if (col + e < a.N) dst[row * a.N + col + e] = s[e];
-            }
-        }
-    } else {
-        uint16_t* st = reinterpret_cast<uint16_t*>(lds) + (wave & 3) * (128 * kStH);
-        if (consumer) {
+    };
+    int s = 0;
+    for (; s + 1 < nsteps; s += 2) {
+        iteration(s, IC<0>{});
+        iteration(s + 1, IC<1>{});
+    }
+    if (s < nsteps) iteration(s, IC<0>{});
+
+    // ---- epilogue: one 32-row block of accumulators at a time, staged in
+    // LDS (each wave its own 32 x 128 fp32 area), then written as 16-byte row
+    // segments.  Accumulator element r of lane l of a 32x32 block sits at
+    // row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+    constexpr int kStP = 128 + 4;                      // staging pitch (floats)
+    static_assert(4 * 32 * kStP * 4 <= kLds, "epilogue staging does not fit");
+    float* st = reinterpret_cast<float*>(lds) + wave * (32 * kStP);
+    const int64_t col0 = (int64_t)nt0 * 64 + wn * 128;
+    const bool cvec = (a.N % 4 == 0) && (a.part != nullptr || (((uintptr_t)a.C) & 7) == 0);
+    __syncthreads();                                   // last reads of B_s / run_s
 #pragma unroll
-            for (int i = 0; i < 4; i++)
+    for (int i = 0; i < 4; i++) {
 #pragma unroll
-                for (int jj = 0; jj < 2; jj++)
+        for (int jj = 0; jj < 4; jj++)
 #pragma unroll
-                    for (int r = 0; r < 16; r++)
-                        st[(i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * kStH + jj * 32 + (lane & 31)] =
-                            (uint16_t)hw_bf16(acc[i][jj][r]);
-        }
-        __syncthreads();
-        if (!consumer) return;
-        const bool c_vec = out_vec && ((((uintptr_t)a.C) & 15) == 0);
+            for (int r = 0; r < 16; r++)
+                st[(8 * (r >> 2) + 4 * hh + (r & 3)) * kStP + jj * 32 + col] = acc[i][jj][r];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // lane l: columns 4*(l%32) .. +3 of rows 2*it + l/32
+#pragma unroll 4
         for (int it = 0; it < 16; it++) {
-            const int rr = it * 8 + (lane >> 3), c8 = (lane & 7) * 8;
-            const int64_t row = row0 + rr, col = col0 + c8;
-            if (row >= a.M || col >= a.N) continue;
-            const uint16_t* s = st + rr * kStH + c8;
-            if (c_vec) {
-                *reinterpret_cast<uint4*>(&a.C[row * a.N + col]) = *reinterpret_cast<const uint4*>(s);
+            const int rr2 = 2 * it + hh;
+            const int64_t row = arow0 + i * 32 + rr2;
+            const int64_t c4 = col0 + 4 * col;
+            const float4 v = *reinterpret_cast<const float4*>(&st[rr2 * kStP + 4 * col]);
+            if (row >= a.M || c4 >= a.N) continue;
+            if (a.part) {
+                float* dst = a.part + ((int64_t)split * a.M + row) * a.N + c4;
+                if (cvec) {
+                    *reinterpret_cast<float4*>(dst) = v;
+                } else {
+                    const float e[4] = {v.x, v.y, v.z, v.w};
+                    for (int x = 0; x < 4 && c4 + x < a.N; x++) dst[x] = e[x];
+                }
             } else {
-                for (int e = 0; e < 8; e++)
-                    if (col + e < a.N) a.C[row * a.N + col + e] = s[e];
+                uint16_t* dst = a.C + row * a.N + c4;
+                const uint32_t b0 = hw_bf16(v.x), b1 = hw_bf16(v.y), b2 = hw_bf16(v.z), b3 = hw_bf16(v.w);
+                if (cvec) {
+                    *reinterpret_cast<uint2*>(dst) = uint2{b0 | (b1 << 16), b2 | (b3 << 16)};
+                } else {
+                    const uint32_t e[4] = {b0, b1, b2, b3};
+                    for (int x = 0; x < 4 && c4 + x < a.N; x++) dst[x] = (uint16_t)e[x];
+                }
             }
         }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+}
+
+// A -> Apk, the MFMA-fragment order read by gemm_cb_kernel: for row block rb
+// (32 rows) and k block kb (16 k), the 1 KiB block (rb * nkb + kb) holds, at
+// lane l, A[32 rb + l%32][16 kb + 8 (l/32) .. +7]; zero past M and K.
+__device__ __forceinline__ int64_t apk_index(int64_t m, int64_t k, uint32_t nkb)
+{
+    const int64_t rb = m >> 5, kb = k >> 4;
+    const int l = (int)(m & 31) + 32 * (int)((k >> 3) & 1);
+    return ((rb * nkb + kb) * 64 + l) * 8;
+}
+
+// from At [K, M] (row stride ldat, m contiguous): 64 x 64 blocks through LDS
+__global__ __launch_bounds__(256) void pack_a_t_kernel(const uint16_t* At, int64_t K, int64_t M, int64_t ldat,
+                                                       uint16_t* Apk, uint32_t nkb)
+{
+    __shared__ __align__(16) uint16_t t[64][64 + 8];
+    const int tid = threadIdx.x;
+    const int64_t k0 = (int64_t)blockIdx.x * 64, m0 = (int64_t)blockIdx.y * 64;
+#pragma unroll
+    for (int it = 0; it < 2; it++) {
+        const int idx = it * 256 + tid, row = idx >> 3, c8 = (idx & 7) * 8;
+        const int64_t k = k0 + row, m = m0 + c8;
+        uint4 v = {0u, 0u, 0u, 0u};
+        if (k < K && m < M) {
+            const uint16_t* src = At + k * ldat + m;
+            if (m + 8 <= M) {
+                v = *reinterpret_cast<const uint4*>(src);
+            } else {
+                uint32_t w[4] = {0u, 0u, 0u, 0u};
+                for (int e = 0; e < 8 && m + e < M; e++) w[e >> 1] |= (uint32_t)src[e] << (16 * (e & 1));
+                v = uint4{w[0], w[1], w[2], w[3]};
+            }
+        }
+        *reinterpret_cast<uint4*>(&t[row][c8]) = v;
+    }
+    __syncthreads();
+    const int64_t mrows = (M + 31) / 32 * 32;          // Apk rows (whole 32-row blocks)
+#pragma unroll
+    for (int it = 0; it < 2; it++) {
+        const int idx = it * 256 + tid, mm = idx >> 3, kc = (idx & 7) * 8;
+        if (m0 + mm < mrows) {
+            uint32_t w[4];
+#pragma unroll
+            for (int d = 0; d < 4; d++) w[d] = (uint32_t)t[kc + 2 * d][mm] | ((uint32_t)t[kc + 2 * d + 1][mm] << 16);
+            *reinterpret_cast<uint4*>(Apk + apk_index(m0 + mm, k0 + kc, nkb)) = uint4{w[0], w[1], w[2], w[3]};
+        }
+    }
+}
+
+// from A [M, K] (row stride lda, k contiguous, K % 8 == 0): one 16-byte piece
+// per thread
+__global__ __launch_bounds__(256) void pack_a_n_kernel(const uint16_t* A, int64_t K, int64_t M, int64_t lda,
+                                                       uint16_t* Apk, uint32_t nkb, int64_t pieces)
+{
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    for (int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x; p < pieces; p += stride) {
+        const int64_t blk = p >> 6;
+        const int l = (int)(p & 63);
+        const int64_t rb = blk / nkb, kb = blk % nkb;
+        const int64_t m = rb * 32 + (l & 31), k = kb * 16 + 8 * (l >> 5);
+        uint4 v = {0u, 0u, 0u, 0u};
+        if (m < M && k < K) v = *reinterpret_cast<const uint4*>(A + m * lda + k);
+        reinterpret_cast<uint4*>(Apk)[p] = v;
     }
 }
 
@@ -661,7 +754,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* part, i
 // and >= 8 steps per workgroup where possible.
 static int gemm_split(int64_t M, int64_t N, int64_t K)
 {
-    const int64_t tiles = ((N + 2 * kTile - 1) / (2 * kTile)) * ((M + kBM - 1) / kBM);
+    const int64_t tiles = ((N + kBN - 1) / kBN) * ((M + kBM - 1) / kBM);
     const int64_t ksteps = (K + kBK - 1) / kBK;
     const int64_t min_split = (ksteps + kMaxSteps - 1) / kMaxSteps;
     int64_t best = min_split, best_cost = -1;
@@ -677,48 +770,74 @@ static int gemm_split(int64_t M, int64_t N, int64_t K)
     return (int)best;
 }
 
+// Apk geometry: k padded to whole K-steps, rows to whole 32-row blocks
+static int64_t apk_nkb(int64_t K) { return (K + kBK - 1) / kBK * (kBK / 16); }
+static int64_t apk_bytes(int64_t M, int64_t K) { return (M + 31) / 32 * apk_nkb(K) * 1024; }
+static int64_t align_up256(int64_t x) { return (x + 255) / 256 * 256; }
+
 }  // namespace bs
 
 using namespace bs;
 
-extern "C" int64_t bs_gemm_compressed_b_workspace_bytes(int64_t M, int64_t N, int64_t K)
+extern "C" int64_t bs_gemm_compressed_b_workspace_bytes(int64_t M, int64_t N, int64_t K, int a_layout)
 {
     if (M <= 0 || N <= 0 || K <= 0) return 0;
     const int split = gemm_split(M, N, K);
-    return split > 1 ? (int64_t)split * M * N * 4 : 0;
+    int64_t bytes = split > 1 ? align_up256((int64_t)split * M * N * 4) : 0;
+    (void)a_layout;
+    bytes += apk_bytes(M, K);
+    return bytes;
 }
 
-extern "C" int bs_gemm_compressed_b(const void* At, int64_t M, int64_t K, int64_t ldat, const void* vals,
-                                    int vals_dtype, int64_t vals_numel, const uint8_t* bitmask,
-                                    const uint32_t* prefix, const int64_t* vals_offset, int64_t N,
-                                    int square, float relu2_scale, const float* b_scale, void* C,
+extern "C" int bs_gemm_compressed_b(const void* A, int64_t M, int64_t K, int64_t lda, int a_layout,
+                                    const void* vals, int vals_dtype, int64_t vals_numel,
+                                    const uint8_t* bitmask, const uint32_t* prefix, const int64_t* vals_offset,
+                                    int64_t N, int square, float relu2_scale, const float* b_scale, void* C,
                                     void* workspace, int64_t workspace_bytes, void* stream)
 {
     clear_error();
     if (M < 0 || N < 0 || K < 0) return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: negative shape");
+    if (a_layout != 0 && a_layout != 1) return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: bad a_layout");
     if (vals_dtype < 0 || vals_dtype > 2) return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: bad dtype");
     if (!square && vals_dtype != DT_BF16)
         return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: fp8 storage needs square=1");
     if (b_scale != nullptr && !square)
         return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: b_scale is only applied with square=1");
-    if (ldat < M) return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: ldat < M");
+    if (a_layout == 0 && lda < M) return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: lda < M");
+    if (a_layout == 1 && lda < K) return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: lda < K");
+    if (a_layout == 1 && K % 8 != 0)
+        return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: a_layout 1 needs K %% 8 == 0");
     if ((uint64_t)K * (uint64_t)N >= (1ull << 32))
         return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: K*N must be < 2^32");
     if (M == 0 || N == 0) return BS_OK;
-    if (At == nullptr || C == nullptr || bitmask == nullptr || prefix == nullptr ||
+    if (A == nullptr || C == nullptr || bitmask == nullptr || prefix == nullptr ||
         (vals_numel > 0 && vals == nullptr))
         return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: null pointer");
-    if ((((uintptr_t)At) & 15) || (ldat % 8) != 0)
-        return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: At must be 16-byte aligned with ldat %% 8 == 0");
-    if (ldat >= (1ll << 24)) return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: ldat must be < 2^24");
+    if ((((uintptr_t)A) & 15) || (lda % 8) != 0)
+        return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: A must be 16-byte aligned with lda %% 8 == 0");
+    if (lda >= (1ll << 24)) return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: lda must be < 2^24");
     if (((uintptr_t)C) & 1) return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: C misaligned");
     if (((uintptr_t)vals) & 15) return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: vals must be 16-byte aligned");
     hipStream_t st = (hipStream_t)stream;
+    const uint32_t ksteps = (uint32_t)((K + kBK - 1) / kBK);
+    if (ksteps == 0) {
+        hipError_t e = hipMemsetAsync(C, 0, (size_t)M * N * 2, st);
+        return e == hipSuccess ? BS_OK : set_error(BS_ERR_HIP, "bs_gemm_compressed_b: %s", hipGetErrorString(e));
+    }
+    const int split = gemm_split(M, N, K);
+    const int64_t part_bytes = split > 1 ? align_up256((int64_t)split * M * N * 4) : 0;
+    const int64_t nkb = apk_nkb(K), nrb = (M + 31) / 32;
+    if (nkb >= (1ll << 20)) return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: K too large");
+    const int64_t need = part_bytes + apk_bytes(M, K);
+    {
+        if (workspace == nullptr || workspace_bytes < need)
+            return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: workspace too small (%lld < %lld)",
+                             (long long)workspace_bytes, (long long)need);
+        if (((uintptr_t)workspace) & 15) return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: workspace misaligned");
+    }
     GemmArgs g{};
-    g.At = (const uint16_t*)At;
     g.M = M;
     g.K = K;
-    g.ldat = ldat;
     g.vals = (const uint8_t*)vals;
     g.vals_numel = vals_numel;
     g.bitmask = bitmask;
@@ -726,30 +845,33 @@ extern "C" int bs_gemm_compressed_b(const void* At, int64_t M, int64_t K, int64_
     g.vals_offset = vals_offset;
     g.N = N;
     g.grid_n = (uint32_t)((N + kTile - 1) / kTile);
-    g.tiles_n = (g.grid_n + 1) / 2;
+    g.tiles_n = (g.grid_n + 3) / 4;
     g.tiles_m = (uint32_t)((M + kBM - 1) / kBM);
     g.relu2_scale = relu2_scale;
     g.b_scale = b_scale;
     g.C = (uint16_t*)C;
-    g.ksteps = (uint32_t)((K + kBK - 1) / kBK);
-    if (g.ksteps == 0) {
-        hipError_t e = hipMemsetAsync(C, 0, (size_t)M * N * 2, st);
-        return e == hipSuccess ? BS_OK : set_error(BS_ERR_HIP, "bs_gemm_compressed_b: %s", hipGetErrorString(e));
-    }
-    const int split = gemm_split(M, N, K);
-    if (split > 1) {
-        const int64_t need = (int64_t)split * M * N * 4;
-        if (workspace == nullptr || workspace_bytes < need)
-            return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: workspace too small (%lld < %lld)",
-                             (long long)workspace_bytes, (long long)need);
-        if (((uintptr_t)workspace) & 15) return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: workspace misaligned");
-        g.part = (float*)workspace;
-    }
-    g.ksteps_per_split = (g.ksteps + split - 1) / split;
+    g.part = split > 1 ? (float*)workspace : nullptr;
+    g.ksteps = ksteps;
+    g.ksteps_per_split = (ksteps + split - 1) / split;
     if (g.ksteps_per_split > (uint32_t)kMaxSteps)
         return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: internal split error");
     const uint64_t blocks = (uint64_t)g.tiles_m * g.tiles_n * (uint64_t)split;
     if (blocks >= (1ull << 31)) return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: grid too large");
+    // A into MFMA-fragment order (workspace after the partial sums)
+    uint16_t* apk = (uint16_t*)((uint8_t*)workspace + part_bytes);
+    if (a_layout == 0) {
+        hipLaunchKernelGGL(pack_a_t_kernel, dim3((uint32_t)(nkb / 4), (uint32_t)((M + 63) / 64)), dim3(256), 0, st,
+                           (const uint16_t*)A, K, M, lda, apk, (uint32_t)nkb);
+    } else {
+        const int64_t pieces = nrb * nkb * 64;
+        int64_t nblk = (pieces + 255) / 256;
+        if (nblk > 4096) nblk = 4096;
+        hipLaunchKernelGGL(pack_a_n_kernel, dim3((uint32_t)nblk), dim3(256), 0, st, (const uint16_t*)A, K, M, lda, apk,
+                           (uint32_t)nkb, pieces);
+    }
+    g.Apk = apk;
+    g.nkb = (uint32_t)nkb;
+    g.nrb = (uint32_t)nrb;
 #define BS_GEMM_LAUNCH(VT, SQ, SC) \
     hipLaunchKernelGGL((gemm_cb_kernel<VT, SQ, SC>), dim3((uint32_t)blocks), dim3(kThreads), 0, st, g)
     const bool sc = b_scale != nullptr;

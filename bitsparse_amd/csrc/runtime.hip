@@ -24,4 +24,4 @@ void clear_error() { g_err[0] = '\0'; }
 
 extern "C" const char* bs_last_error(void) { return bs::g_err; }
 
-extern "C" int bs_abi_version(void) { return 2; }
+extern "C" int bs_abi_version(void) { return 3; }

@@ -36,20 +36,25 @@ def gemm_compressed_b(A: Tensor, B_sparse, square: bool) -> Tensor:
         raise ValueError("gemm_compressed_b: unsupported operand combination")
     K, N = B_sparse.shape
     M = A.shape[0]
-    At = A.t()                              # [K, M]; for A = dY.T this is dY itself
-    if At.stride(1) != 1 or At.stride(0) % 8 != 0 or At.data_ptr() % 16 != 0:
-        # the kernel reads 8-element row chunks: rows padded to a multiple of 8
-        ld = (M + 7) // 8 * 8
-        pad = torch.zeros((K, ld), device=A.device, dtype=A.dtype)
-        pad[:, :M] = At
-        At = pad
+    if A.stride(1) == 1 and A.stride(0) % 8 == 0 and A.data_ptr() % 16 == 0 and K % 8 == 0:
+        a_layout, a_src, lda = 1, A, A.stride(0)          # k contiguous: read in place
+    else:
+        # the kernel transposes A^T [K, M] (m contiguous; for A = dY.T this
+        # is dY itself) into its workspace; rows padded to a multiple of 8
+        At = A.t()
+        if At.stride(1) != 1 or At.stride(0) % 8 != 0 or At.data_ptr() % 16 != 0:
+            ld = (M + 7) // 8 * 8
+            pad = torch.zeros((K, ld), device=A.device, dtype=A.dtype)
+            pad[:, :M] = At
+            At = pad
+        a_layout, a_src, lda = 0, At, At.stride(0)
     L = _lib.load()
     C = torch.empty((M, N), device=A.device, dtype=torch.bfloat16)
-    need = L.bs_gemm_compressed_b_workspace_bytes(M, N, K)
+    need = L.bs_gemm_compressed_b_workspace_bytes(M, N, K, a_layout)
     ws = torch.empty(max(need, 0), device=A.device, dtype=torch.uint8) if need > 0 else None
     scale = B_sparse.scale if (square and B_sparse.scale is not None) else None
     check(L.bs_gemm_compressed_b(
-        At.data_ptr(), M, K, At.stride(0), B_sparse.vals.data_ptr(), dtype_code(B_sparse.vals.dtype),
+        a_src.data_ptr(), M, K, lda, a_layout, B_sparse.vals.data_ptr(), dtype_code(B_sparse.vals.dtype),
         B_sparse.vals.numel(), B_sparse.bitmask.data_ptr(), B_sparse.prefix.data_ptr(),
         B_sparse.vals_offset.data_ptr(), N, int(square), float(RELU2_SCALE), ptr(scale),
         C.data_ptr(), ptr(ws), need, stream_handle(A.device)), "bs_gemm_compressed_b")

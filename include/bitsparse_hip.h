@@ -199,25 +199,29 @@ int bs_quantize_e4m3fn(const void* x, int64_t n, void* q_out, float* scale_out,
                        void* stream);
 
 /*
- * C[M, N] (bf16, row-major, row stride N) = At^T @ B, where At is a dense
- * bf16 [K, M] matrix with m contiguous (row stride ldat >= M, ldat % 8 == 0,
- * ldat < 2^24, At 16-byte aligned; in the MLP backward At = dY) and B is a
- * compressed [K, N] activation (vals 16-byte aligned) decoded tile by tile
- * into LDS (never written to HBM dense).
+ * C[M, N] (bf16, row-major, row stride N) = A @ B, where A is a dense bf16
+ * [M, K] matrix and B is a compressed [K, N] activation (vals 16-byte
+ * aligned) decoded tile by tile into LDS (never written to HBM dense).
+ * A is given in one of two layouts (16-byte aligned, lda % 8 == 0, lda < 2^24):
+ *   a_layout = 0: as its transpose At [K, M], m contiguous, row stride
+ *                 lda >= M (the MLP backward's A = dY^T, i.e. At = dY); it is
+ *                 transposed into the workspace first
+ *   a_layout = 1: row-major [M, K], k contiguous, row stride lda >= K,
+ *                 K % 8 == 0 (read in place)
  *   square = 0: B = stored bf16 values          (AspB, bf16 storage)
  *   square = 1: B = k*v*v as in bs_decompress   (AspRelu2B), and with
  *               b_scale (fp8 storage) B = bf16(B * bf16(b_scale^2))
- * fp32 MFMA accumulation; small grids split K into fp32 partial sums in
- * `workspace` (bs_gemm_compressed_b_workspace_bytes; 0 = none needed),
- * reduced in a fixed order.
+ * fp32 MFMA accumulation; small grids split K into fp32 partial sums,
+ * reduced in a fixed order.  `workspace` holds the partial sums and the
+ * transposed A (bs_gemm_compressed_b_workspace_bytes; 0 = none needed).
  * Replaces lib_sparse/src/sparse_matmul.py:24-28 (AspB) and :109-113
  * (AspRelu2B): unpack to a dense HBM buffer, then torch.matmul.
  */
-int64_t bs_gemm_compressed_b_workspace_bytes(int64_t M, int64_t N, int64_t K);
-int bs_gemm_compressed_b(const void* At, int64_t M, int64_t K, int64_t ldat, const void* vals,
-                         int vals_dtype, int64_t vals_numel, const uint8_t* bitmask,
-                         const uint32_t* prefix, const int64_t* vals_offset, int64_t N,
-                         int square, float relu2_scale, const float* b_scale, void* C,
+int64_t bs_gemm_compressed_b_workspace_bytes(int64_t M, int64_t N, int64_t K, int a_layout);
+int bs_gemm_compressed_b(const void* A, int64_t M, int64_t K, int64_t lda, int a_layout,
+                         const void* vals, int vals_dtype, int64_t vals_numel,
+                         const uint8_t* bitmask, const uint32_t* prefix, const int64_t* vals_offset,
+                         int64_t N, int square, float relu2_scale, const float* b_scale, void* C,
                          void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
