@@ -56,6 +56,17 @@ def make_activation(M: int, N: int, mu: float, device):
     return (torch.randn((M, N), device=device, generator=g) + mu).to(torch.bfloat16).relu_()
 
 
+def measure_copy_gbs(nbytes: int = 512 << 20, steps: int = 10) -> float:
+    """Achievable HBM rate on this device: torch's device-to-device copy of a
+    512 MiB buffer (read + write bytes / event-timed duration)."""
+    import torch
+    src = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    ms = _timed(lambda: dst.copy_(src), steps, 3)
+    del src, dst
+    return 2.0 * nbytes / (ms * 1e6)
+
+
 def bench_codec(M: int, N: int, mu: float, steps: int, warmup: int):
     import torch
     from bitsparse_amd import _lib
@@ -554,6 +565,8 @@ def main() -> int:
     log(f"codec: {M}x{N} bf16, mu={args.sparsity_mu}, steps={args.steps}, warmup={args.warmup}")
     codec = bench_codec(M, N, args.sparsity_mu, args.steps, args.warmup)
     log(f"codec done: {codec['roundtrip_gbs']:.1f} GB/s round trip")
+    copy_gbs = measure_copy_gbs()
+    log(f"device copy: {copy_gbs:.1f} GB/s")
     if args.calibrate_copy:
         src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
         dst = torch.empty_like(src)
@@ -621,7 +634,9 @@ def main() -> int:
                      "frac": round(codec["compress_gbs"] / HBM_PEAK_GBS, 4),
                      "traffic": traffic, "kernel": "compress_stream_kernel (fused single pass)",
                      "bytes_per_launch": codec["compress_bytes"],
-                     "avg_launch_ms": round(codec["compress_ms"], 5)},
+                     "avg_launch_ms": round(codec["compress_ms"], 5),
+                     "achievable_copy_gbs": round(copy_gbs, 2),
+                     "frac_of_copy": round(codec["compress_gbs"] / copy_gbs, 4)},
         "kernels": {"compress_gbs": round(codec["compress_gbs"], 2),
                     "decompress_gbs": round(codec["decompress_gbs"], 2),
                     "compress_ms": round(codec["compress_ms"], 5),

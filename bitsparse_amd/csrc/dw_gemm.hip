@@ -183,15 +183,6 @@ __device__ __forceinline__ RunUnit<UB> load_unit_tail(bs_rsrc rs, uint32_t off)
     else return w[0];
 }
 
-// The 4 bf16 values starting at element r of a run staged in LDS, from
-// dword-aligned reads (unaligned LDS reads stall for tens of cycles).
-__device__ __forceinline__ uint2 window(const uint32_t* run32, uint32_t r)
-{
-    const uint32_t o = r * 2, q = o >> 2, sh = o & 3;
-    const uint32_t d0 = run32[q], d1 = run32[q + 1], d2 = run32[q + 2];
-    return uint2{__builtin_amdgcn_alignbyte(d1, d0, sh), __builtin_amdgcn_alignbyte(d2, d1, sh)};
-}
-
 // compile-time register-set index
 template <int P>
 struct IC {
@@ -415,15 +406,17 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_cb_kernel(GemmArgs a)
     // row 8C + roff), so that the stages of successive chunks can be spread
     // between the MFMAs of the step being multiplied:
     //   stage_r: the row's bitmask word and run index from the row table
-    //   stage_s: ranks, the byte-permute selectors and the two value windows
-    //   stage_w: the permutes and the 16-byte store into B_s
+    //   stage_s: ranks; issues the reads of the byte-permute selectors and of
+    //            the dwords under the two value windows
+    //   stage_w: aligns the windows, permutes and stores 16 bytes into B_s
     struct DecR {
         uint64_t mrow;
         uint32_t rpr;
     };
     struct DecS {
         uint4 sel;
-        uint2 wa, wb;
+        uint32_t a0, a1, a2, b0, b1, b2;    // dwords under window A / window B
+        uint32_t sha, shb;                  // their byte offsets within the first dword
     };
     DecR dr[2];
     DecS dq[2];
@@ -439,17 +432,29 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_cb_kernel(GemmArgs a)
         const uint32_t byte = (uint32_t)(mrow >> (8 * dc)) & 0xffu;
         const uint32_t ra = dr[C & 1].rpr + (uint32_t)__popcll(mrow & below_mask);
         const uint32_t rbk = ra + (uint32_t)__builtin_popcount(byte & 15u);
-        dq[C & 1].sel = lut_s[byte];
-        dq[C & 1].wa = window(run32, ra);
-        dq[C & 1].wb = window(run32, rbk);
+        DecS& q = dq[C & 1];
+        q.sel = lut_s[byte];
+        const uint32_t qa = ra >> 1, qb = rbk >> 1;     // bf16 value r sits in dword r/2
+        q.sha = (ra & 1u) * 2u;
+        q.shb = (rbk & 1u) * 2u;
+        q.a0 = run32[qa];
+        q.a1 = run32[qa + 1];
+        q.a2 = run32[qa + 2];
+        q.b0 = run32[qb];
+        q.b1 = run32[qb + 1];
+        q.b2 = run32[qb + 2];
     };
     auto stage_w = [&](auto CI, uint16_t* dst) __attribute__((always_inline)) {
         constexpr int C = decltype(CI)::value;
         const DecS& q = dq[C & 1];
-        const uint32_t w0 = __builtin_amdgcn_perm(q.wa.y, q.wa.x, q.sel.x);
-        const uint32_t w1 = __builtin_amdgcn_perm(q.wa.y, q.wa.x, q.sel.y);
-        const uint32_t w2 = __builtin_amdgcn_perm(q.wb.y, q.wb.x, q.sel.z);
-        const uint32_t w3 = __builtin_amdgcn_perm(q.wb.y, q.wb.x, q.sel.w);
+        const uint32_t wax = __builtin_amdgcn_alignbyte(q.a1, q.a0, q.sha);
+        const uint32_t way = __builtin_amdgcn_alignbyte(q.a2, q.a1, q.sha);
+        const uint32_t wbx = __builtin_amdgcn_alignbyte(q.b1, q.b0, q.shb);
+        const uint32_t wby = __builtin_amdgcn_alignbyte(q.b2, q.b1, q.shb);
+        const uint32_t w0 = __builtin_amdgcn_perm(way, wax, q.sel.x);
+        const uint32_t w1 = __builtin_amdgcn_perm(way, wax, q.sel.y);
+        const uint32_t w2 = __builtin_amdgcn_perm(wby, wbx, q.sel.z);
+        const uint32_t w3 = __builtin_amdgcn_perm(wby, wbx, q.sel.w);
         *reinterpret_cast<uint4*>(&dst[(8 * C + roff) * kBP]) = uint4{w0, w1, w2, w3};
     };
     auto run_ptr = [&](int rb) __attribute__((always_inline)) {
