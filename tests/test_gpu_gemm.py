@@ -103,3 +103,29 @@ def test_gemm_identity_reproduces_decoded_operand(dev, storage, square):
     A = torch.eye(K, dtype=torch.bfloat16, device=dev)
     C = dw_gemm.gemm_compressed_b(A, sp, square=square)
     assert torch.equal(C.view(torch.int16), ref.view(torch.int16))
+
+
+def test_gemm_relu2_nonfinite_scale_matches_decompress(dev):
+    """ReLU^2 with fp8 storage and an infinite scale: every decoded element is
+    bf16(k v^2 * bf16(scale^2)), so cleared elements are 0 * inf = NaN, as
+    the decompress kernel (and the reference's unpack-then-scale,
+    lib_sparse/src/triton_operators.py:160-161) produces them.  The LDS GEMM's
+    cleared-element fix-up must give the same NaN / non-NaN pattern as
+    decompress + an fp32 product."""
+    from bitsparse_amd.src import dw_gemm
+    from bitsparse_amd.src.functions import quantize_and_compress
+    from bitsparse_amd.src.hip_operators import unpack_relu2_batch_
+    K, N, M = 192, 320, 256
+    # ~38% of the columns hold no stored value: without the fix-up they
+    # would come out 0 instead of NaN
+    r = relu_input((K, N), 0.995, seed=12).to(dev)
+    A = preact_input((M, K), seed=13).to(dev)
+    _, _, sp = quantize_and_compress(r, None)
+    sp.scale = torch.full_like(sp.scale, float("inf"))
+    dense = torch.empty((K, N), dtype=torch.bfloat16, device=dev)
+    unpack_relu2_batch_(sp, dense, 0, sp.grid_n, N, K, sp.grid_m * sp.grid_n)
+    assert torch.isnan(dense).any() and (~torch.isnan(dense)).any()
+    ref = A.float() @ dense.float()
+    C = dw_gemm.gemm_compressed_b(A, sp, square=True)
+    assert torch.equal(torch.isnan(C), torch.isnan(ref))
+    assert torch.equal(torch.isinf(C), torch.isinf(ref))
