@@ -41,29 +41,54 @@ typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef short i16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
-constexpr int kBM = 256;              // C rows per workgroup
-constexpr int kBN = 256;              // C columns per workgroup (four B tiles)
 constexpr int kBK = 64;               // K per step (one B tile row)
-constexpr int kThreads = 256;
-// B_s row pitch (elements): 576 bytes, 64 bytes past a multiple of 256 (LDS
-// has 64 4-byte banks): the four rows read by one 16-lane group of
-// ds_read_b64_tr_b16 start 16 banks apart and the two column halves of a
-// 32-lane half-wave fill the other 8-bank gaps, so fragment reads are
-// conflict-free.
-constexpr int kBP = kBN + 32;
 constexpr int kRunSlots = kTileNumel / 8 + 2;   // one bf16-staged run + phase, 16-byte slots
 constexpr int kMaxSteps = 256;        // K-steps per workgroup (prefixes held in registers)
 constexpr int kCus = 256;             // MI355X compute units (split-K sizing)
 constexpr int kXcds = 8;
 
-// LDS carve-up (bytes)
-constexpr int kOffB = 0;                                   // B_s[2][64][kBP] bf16
-constexpr int kOffRun = kOffB + 2 * kBK * kBP * 2;         // run_s[2][4 waves][kRunSlots] uint4
-constexpr int kOffBm = kOffRun + 2 * 4 * kRunSlots * 16;   // bm_s[4][64] uint64 (bitmask rows)
-constexpr int kOffRp = kOffBm + 4 * 64 * 8;               // rp_s[4][64] uint32 (row prefixes)
-constexpr int kOffLut = kOffRp + 4 * 64 * 4;              // lut_s[256] uint4 byte-permute selectors
-constexpr int kLds = kOffLut + 256 * 16;
-static_assert(kLds <= 160 * 1024, "LDS budget");
+// Workgroup shape: a WGM x WGN grid of waves, each owning a 128 x WN block of
+// C.  A K-step decodes BN/64 B tiles; each is decoded by NWAVES/NT waves.
+//   Cfg256: 256 x 256, 4 waves (one per SIMD), 128 x 128 per wave
+//   Cfg512: 512 x 128, 8 waves (two per SIMD), 128 x 64 per wave: every
+//           decoded B element feeds 512 rows instead of 256, half the decode
+//           instructions per MFMA
+template <int WGM_, int WGN_, int WN_, bool AQ_>
+struct GemmCfg {
+    // AQ: A fragments are loaded one k-quarter ahead (2 register sets) instead
+    // of one K-step ahead (4 sets); with two waves per SIMD the other wave
+    // covers the shorter lead
+    static constexpr bool AQ = AQ_;
+    static constexpr int ASETS = AQ_ ? 2 : 4;
+    static constexpr int WGM = WGM_, WGN = WGN_, NWAVES = WGM_ * WGN_, THREADS = 64 * NWAVES;
+    static constexpr int WAVE_M = 128, WAVE_N = WN_;
+    static constexpr int IM = WAVE_M / 32, JN = WAVE_N / 32;    // 32x32 accumulator blocks per wave
+    static constexpr int BM = WAVE_M * WGM, BN = WAVE_N * WGN;
+    static constexpr int NT = BN / 64;                           // B tiles per K-step
+    static constexpr int DW = NWAVES / NT;                       // waves decoding one B tile
+    static constexpr int CH = 8 / DW;                            // decode chunk iterations per lane per step
+    // B_s row pitch (elements): 64 bytes past a multiple of 256 bytes (LDS has
+    // 64 4-byte banks): the four rows read by one 16-lane group of
+    // ds_read_b64_tr_b16 start 16 banks apart and the two column halves of a
+    // 32-lane half-wave fill the other 8-bank gaps, so fragment reads are
+    // conflict-free
+    static constexpr int BP = BN + 32;
+    static constexpr int SEG = 4 * IM * JN;                      // MFMAs (segments) per K-step
+    static constexpr int PER = SEG / CH;                         // segments per decoded chunk
+    // LDS carve-up (bytes)
+    static constexpr int OFF_B = 0;                              // B_s[2][64][BP] bf16
+    static constexpr int OFF_RUN = OFF_B + 2 * kBK * BP * 2;     // run_s[2][NT][kRunSlots] uint4
+    static constexpr int OFF_BM = OFF_RUN + 2 * NT * kRunSlots * 16;   // bm_s[NWAVES][64] uint64
+    static constexpr int OFF_RP = OFF_BM + NWAVES * 64 * 8;     // rp_s[NWAVES][64] uint32
+    static constexpr int OFF_LUT = OFF_RP + NWAVES * 64 * 4;    // lut_s[256] uint4
+    static constexpr int LDS = OFF_LUT + 256 * 16;
+    static constexpr int ST_P = WAVE_N + 4;                      // epilogue staging pitch (floats)
+    static_assert(LDS <= 160 * 1024, "LDS budget");
+    static_assert(NWAVES * 32 * ST_P * 4 <= LDS, "epilogue staging does not fit");
+    static_assert(NWAVES % NT == 0 && 8 % DW == 0 && SEG % CH == 0, "decode split");
+};
+using Cfg256 = GemmCfg<2, 2, 128, false>;
+using Cfg512 = GemmCfg<4, 2, 64, true>;
 
 struct GemmArgs {
     const uint16_t* Apk;          // A in MFMA-fragment order (pack_a_*_kernel)
@@ -77,7 +102,7 @@ struct GemmArgs {
     const int64_t* vals_offset;
     int64_t N;
     uint32_t grid_n;              // B tiles along N
-    uint32_t tiles_m, tiles_n;    // C tiles (kBM x kBN)
+    uint32_t tiles_m, tiles_n;    // C tiles (BM x BN of the launch configuration)
     float relu2_scale;
     const float* b_scale;         // square + fp8 storage: multiply by bf16(scale^2)
     uint16_t* C;                  // [M, N] bf16 (no split)
@@ -201,9 +226,10 @@ __device__ __forceinline__ void static_for(F&& f)
     static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
-template <int V_T, bool SQUARE, bool HAS_SCALE>
-__global__ __launch_bounds__(kThreads, 1) void gemm_cb_kernel(GemmArgs a)
+template <typename CFG, int V_T, bool SQUARE, bool HAS_SCALE>
+__global__ __launch_bounds__(CFG::THREADS, 1) void gemm_cb_kernel(GemmArgs a)
 {
+    constexpr int NT = CFG::NT, DW = CFG::DW, CH = CFG::CH, BP = CFG::BP, IM = CFG::IM, JN = CFG::JN;
     constexpr int VB = V_T == DT_BF16 ? 2 : 1;                   // stored value bytes
     constexpr int GV = SQUARE ? 4 : 8;                           // values per staging unit
     constexpr int UB = GV * VB;                                  // stored bytes per unit
@@ -211,15 +237,19 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_cb_kernel(GemmArgs a)
     // units per lane loaded one step ahead (<= 20 registers: 2560 plain bf16
     // values, 1536 bf16 / 1024 fp8 values to square); a denser tile's
     // remaining units are loaded when the run is staged
-    constexpr int RXP = UB == 16 ? 5 : (UB == 8 ? 6 : 4);
+    constexpr int RXP0 = UB == 16 ? 5 : (UB == 8 ? 6 : 4);
+    // the DW waves decoding one tile stage its run together: unit u is staged
+    // by lane u % 64 of wave (u / 64) % DW, in pass u / (64 DW)
+    constexpr int RXD = (RX + DW - 1) / DW;                      // passes per wave, worst case
+    constexpr int RXP = RXP0 < RXD ? RXP0 : RXD;
     typedef RunUnit<UB> Unit;
 
-    __shared__ __align__(16) uint8_t lds[kLds];
-    uint16_t* B_s = reinterpret_cast<uint16_t*>(lds + kOffB);
-    uint4* run_s = reinterpret_cast<uint4*>(lds + kOffRun);
-    uint64_t* bm_s = reinterpret_cast<uint64_t*>(lds + kOffBm);
-    uint32_t* rp_s = reinterpret_cast<uint32_t*>(lds + kOffRp);
-    uint4* lut_s = reinterpret_cast<uint4*>(lds + kOffLut);
+    __shared__ __align__(16) uint8_t lds[CFG::LDS];
+    uint16_t* B_s = reinterpret_cast<uint16_t*>(lds + CFG::OFF_B);
+    uint4* run_s = reinterpret_cast<uint4*>(lds + CFG::OFF_RUN);
+    uint64_t* bm_s = reinterpret_cast<uint64_t*>(lds + CFG::OFF_BM);
+    uint32_t* rp_s = reinterpret_cast<uint32_t*>(lds + CFG::OFF_RP);
+    uint4* lut_s = reinterpret_cast<uint4*>(lds + CFG::OFF_LUT);
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -236,10 +266,12 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_cb_kernel(GemmArgs a)
     const uint32_t tm = (uint32_t)__builtin_amdgcn_readfirstlane((int)(rest % a.tiles_m));
     const uint32_t split = (uint32_t)__builtin_amdgcn_readfirstlane((int)(rest / a.tiles_m));
 
-    const uint32_t nt0 = tn * 4;                       // first B tile column
-    const uint32_t tcol = nt0 + (uint32_t)wave;        // the B tile column this wave decodes
+    const uint32_t nt0 = tn * NT;                      // first B tile column
+    const int tw = wave / DW;                          // the B tile this wave helps decode
+    const int tq = wave % DW;                          // its share: rows 64/DW * tq .. +64/DW
+    const uint32_t tcol = nt0 + (uint32_t)tw;
     const bool has_tile = tcol < a.grid_n;
-    const int64_t m0 = (int64_t)tm * kBM;
+    const int64_t m0 = (int64_t)tm * CFG::BM;
     const uint32_t kt0 = split * a.ksteps_per_split;
     const uint32_t kt1 = min(a.ksteps, kt0 + a.ksteps_per_split);
     const int nsteps = kt1 > kt0 ? (int)(kt1 - kt0) : 0;
@@ -250,7 +282,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_cb_kernel(GemmArgs a)
     // first rank (elements 0-3 draw from it), window B from the rank of
     // element 4.  Selector byte x picks byte x of the window, 0x0c gives 0x00;
     // dword d = elements 2d, 2d+1 (d < 2: window A, else window B).
-    {
+    if (tid < 256) {
         const uint32_t bb = (uint32_t)tid;
         uint32_t sel[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
@@ -343,14 +375,14 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_cb_kernel(GemmArgs a)
         rr_tail = ok && (int64_t)nunits * GV > avail;   // the run's last unit crosses the end of vals
 #pragma unroll
         for (int x = 0; x < RXP; x++)
-            if (x * 64 < rr_nunits) rr[x] = unit_at(x * 64 + lane);
+            if ((x * DW + tq) * 64 < rr_nunits) rr[x] = unit_at((x * DW + tq) * 64 + lane);
     };
     auto store_run = [&](int buf) __attribute__((always_inline)) {
-        uint8_t* dst = reinterpret_cast<uint8_t*>(run_s + (buf * 4 + wave) * kRunSlots);
+        uint8_t* dst = reinterpret_cast<uint8_t*>(run_s + (buf * NT + tw) * kRunSlots);
 #pragma unroll
-        for (int x = 0; x < RX; x++) {
-            if (x * 64 < rr_nunits) {
-                const int u = x * 64 + lane;
+        for (int x = 0; x < RXD; x++) {
+            if ((x * DW + tq) * 64 < rr_nunits) {
+                const int u = (x * DW + tq) * 64 + lane;
                 if (x >= RXP) rr[x % RXP] = unit_at(u);
                 if (u < rr_nunits) {
                     if constexpr (!SQUARE) {
@@ -382,12 +414,14 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_cb_kernel(GemmArgs a)
     };
 
     // ---- decode step s (run in run_s[rb], bitmask rows bmr) into B_s[bb],
-    // columns 64*wave .. +64.  Lane l handles chunk c = l%8 (8 columns at 8c)
-    // of eight rows, row = 8i + roff(l/8), i = 0..7; roff pairs rows two apart
-    // in each 16-lane group so the 16-byte stores of a group hit disjoint banks.
+    // columns 64*tw .. +64, rows rbase .. rbase + 8 CH.  Lane l handles chunk
+    // c = l%8 (8 columns at 8c) of CH rows, row = rbase + 8i + roff(l/8); roff
+    // pairs rows two apart in each 16-lane group so the 16-byte stores of a
+    // group hit disjoint banks.
     const int dc = lane & 7, dg = lane >> 3;
     const int roff = ((dg & 1) << 1) | ((dg >> 1) & 1) | (dg & 4);
     const uint64_t below_mask = dc == 0 ? 0ull : (~0ull >> (64 - 8 * dc));
+    const int rbase = 8 * CH * tq;
     // row table of step s: bm_s = bitmask rows, rp_s = run index of each
     // row's first value (phase + exclusive prefix of the row popcounts)
     auto decode_rows = [&](int s, uint64_t bmr) __attribute__((always_inline)) {
@@ -406,6 +440,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_cb_kernel(GemmArgs a)
     // row 8C + roff), so that the stages of successive chunks can be spread
     // between the MFMAs of the step being multiplied:
     //   stage_r: the row's bitmask word and run index from the row table
+    //            (each wave keeps its own copy of its tile's table)
     //   stage_s: ranks; issues the reads of the byte-permute selectors and of
     //            the dwords under the two value windows
     //   stage_w: aligns the windows, permutes and stores 16 bytes into B_s
@@ -422,7 +457,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_cb_kernel(GemmArgs a)
     DecS dq[2];
     auto stage_r = [&](auto CI) __attribute__((always_inline)) {
         constexpr int C = decltype(CI)::value;
-        const int row = 8 * C + roff;
+        const int row = rbase + 8 * C + roff;
         dr[C & 1].mrow = bm_s[wave * 64 + row];
         dr[C & 1].rpr = rp_s[wave * 64 + row];
     };
@@ -455,19 +490,19 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_cb_kernel(GemmArgs a)
         const uint32_t w1 = __builtin_amdgcn_perm(way, wax, q.sel.y);
         const uint32_t w2 = __builtin_amdgcn_perm(wby, wbx, q.sel.z);
         const uint32_t w3 = __builtin_amdgcn_perm(wby, wbx, q.sel.w);
-        *reinterpret_cast<uint4*>(&dst[(8 * C + roff) * kBP]) = uint4{w0, w1, w2, w3};
+        *reinterpret_cast<uint4*>(&dst[(rbase + 8 * C + roff) * BP]) = uint4{w0, w1, w2, w3};
     };
     auto run_ptr = [&](int rb) __attribute__((always_inline)) {
-        return reinterpret_cast<const uint32_t*>(run_s + (rb * 4 + wave) * kRunSlots);
+        return reinterpret_cast<const uint32_t*>(run_s + (rb * NT + tw) * kRunSlots);
     };
     auto dst_ptr = [&](int bb) __attribute__((always_inline)) {
-        return B_s + bb * (kBK * kBP) + wave * 64 + dc * 8;
+        return B_s + bb * (kBK * BP) + tw * 64 + dc * 8;
     };
     // whole decode of the run in run_s[rb] into B_s[bb] (prologue)
     auto decode = [&](int rb, int bb) __attribute__((always_inline)) {
         const uint32_t* run32 = run_ptr(rb);
         uint16_t* dst = dst_ptr(bb);
-        static_for<8>([&](auto CI) __attribute__((always_inline)) {
+        static_for<CH>([&](auto CI) __attribute__((always_inline)) {
             stage_r(CI);
             stage_s(CI, run32);
             stage_w(CI, dst);
@@ -476,11 +511,11 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_cb_kernel(GemmArgs a)
 
     // cleared elements of B_s[bb] (this wave's columns) -> zero_b
     auto zero_fixup = [&](int bb) __attribute__((always_inline)) {
-        uint16_t* dst = B_s + bb * (kBK * kBP) + wave * 64 + dc * 8;
-        for (int i = 0; i < 8; i++) {
-            const int row = 8 * i + roff;
+        uint16_t* dst = dst_ptr(bb);
+        for (int i = 0; i < CH; i++) {
+            const int row = rbase + 8 * i + roff;
             const uint32_t byte = (uint32_t)(bm_s[wave * 64 + row] >> (8 * dc)) & 0xffu;
-            uint4 v = *reinterpret_cast<const uint4*>(&dst[row * kBP]);
+            uint4 v = *reinterpret_cast<const uint4*>(&dst[row * BP]);
             uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
             for (int d = 0; d < 4; d++) {
@@ -488,7 +523,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_cb_kernel(GemmArgs a)
                                       (((byte >> (2 * d + 1)) & 1u) ? 0xffff0000u : 0u);
                 w[d] = (w[d] & keep) | (zero_pair & ~keep);
             }
-            *reinterpret_cast<uint4*>(&dst[row * kBP]) = uint4{w[0], w[1], w[2], w[3]};
+            *reinterpret_cast<uint4*>(&dst[row * BP]) = uint4{w[0], w[1], w[2], w[3]};
         }
     };
 
@@ -497,72 +532,88 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_cb_kernel(GemmArgs a)
     // 16-byte pieces lane after lane, one 1 KiB block per (32 rows, 16 k), so
     // every fragment load is one contiguous 1 KiB read; rows past M and k past
     // K are zero in Apk, blocks past its end read as zero.
-    const int wm = wave & 1, wn = wave >> 1;
+    const int wm = wave % CFG::WGM, wn = wave / CFG::WGM;
     const int g = lane >> 4, j = lane & 15, hh = lane >> 5, col = lane & 31;
-    const int64_t arow0 = m0 + wm * 128;
+    const int64_t arow0 = m0 + wm * CFG::WAVE_M;
     const uint32_t rb0 = (uint32_t)(arow0 / 32);
-    const uint32_t nrbw = rb0 < a.nrb ? min(4u, a.nrb - rb0) : 0u;    // row blocks of this wave
+    const uint32_t nrbw = rb0 < a.nrb ? min((uint32_t)IM, a.nrb - rb0) : 0u;   // row blocks of this wave
     const bs_rsrc rsA = make_rsrc(nrbw ? a.Apk + (int64_t)rb0 * a.nkb * 512 : a.Apk, nrbw * a.nkb * 1024u);
-    bf16x8_t areg[4][4];
+    bf16x8_t areg[IM][CFG::ASETS];   // [i][kk] (whole step) or [i][kk & 1] (AQ)
     auto a_off = [&](int s, int i, int kk) __attribute__((always_inline)) -> uint32_t {
         return ((uint32_t)i * a.nkb + (kt0 + (uint32_t)s) * 4u + (uint32_t)kk) * 1024u + (uint32_t)lane * 16u;
     };
     auto load_a = [&](int s, int kk) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) areg[i][kk] = __builtin_bit_cast(bf16x8_t, load16(rsA, a_off(s, i, kk)));
+        for (int i = 0; i < IM; i++)
+            areg[i][kk % CFG::ASETS] = __builtin_bit_cast(bf16x8_t, load16(rsA, a_off(s, i, kk)));
     };
 
-    f32x16_t acc[4][4];
+    f32x16_t acc[IM][JN];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < IM; i++)
 #pragma unroll
-        for (int jj = 0; jj < 4; jj++)
+        for (int jj = 0; jj < JN; jj++)
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][jj][r] = 0.0f;
 
     // B fragments of one k-quarter: lo / hi halves of the transposing reads,
     // two sets (k-quarter parity)
-    i16x4_t blo[2][4], bhi[2][4];
+    i16x4_t blo[2][JN], bhi[2][JN];
     auto read_b = [&](const uint16_t* Bs, int kk, int jj, int half, int set) __attribute__((always_inline)) {
-        const uint16_t* p = Bs + (16 * kk + 8 * hh + (j >> 2) + 4 * half) * kBP + wn * 128 + jj * 32 + 16 * (g & 1) +
-                            4 * (j & 3);
+        const uint16_t* p = Bs + (16 * kk + 8 * hh + (j >> 2) + 4 * half) * BP + wn * CFG::WAVE_N + jj * 32 +
+                            16 * (g & 1) + 4 * (j & 3);
         typedef __attribute__((address_space(3))) i16x4_t lds_i16x4;
         const i16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p);
         if (half) bhi[set][jj] = v;
         else blo[set][jj] = v;
     };
 
-    // One K-step as 64 segments, one MFMA each (k-quarter kk = X/16, block
-    // i = X%16/4, jj = X%4), fenced by sched_barrier so the order below is the
-    // issue order.  A segment also carries: the reload of A(i, kk) for the
-    // next step after its last use; in the second half of a k-quarter, one
-    // transposing read of the next quarter's B fragments; and one stage of the
-    // software-pipelined decode of the next step (chunk X/8: stage_r at X%8 == 0,
-    // stage_s at X%8 == 4, stage_w four segments later).  Each segment issues
-    // a few VALU / LDS instructions in the shadow of its MFMA.
-    auto step = [&](int s_next, auto PI) __attribute__((always_inline)) {
+    // One K-step as SEG segments, one MFMA each (k-quarter kk, block i, jj),
+    // fenced by sched_barrier so the order below is the issue order.  A
+    // segment also carries: the reload of A(i, kk) for the next step after its
+    // last use; in the second half of a k-quarter, one transposing read of the
+    // next quarter's B fragments; and one stage of the software-pipelined
+    // decode of the next step (chunk X/PER: stage_r at X%PER == 0, stage_s
+    // half a period later, stage_w at the next chunk's stage_r).  Each segment
+    // issues a few VALU / LDS instructions in the shadow of its MFMA.
+    auto step = [&](int s_cur, int s_next, auto PI) __attribute__((always_inline)) {
         constexpr int P = decltype(PI)::value;
-        const uint16_t* Bs = B_s + P * (kBK * kBP);
+        constexpr int PER = CFG::PER, QB = IM * JN;    // segments per chunk / per k-quarter
+        const uint16_t* Bs = B_s + P * (kBK * BP);
         const uint32_t* run32 = run_ptr(P ^ 1);
         uint16_t* dst = dst_ptr(P ^ 1);
-        static_for<4>([&](auto JI) __attribute__((always_inline)) {
+        static_for<JN>([&](auto JI) __attribute__((always_inline)) {
             read_b(Bs, 0, decltype(JI)::value, 0, 0);
             read_b(Bs, 0, decltype(JI)::value, 1, 0);
         });
-        static_for<64>([&](auto XI) __attribute__((always_inline)) {
+        static_for<CFG::SEG>([&](auto XI) __attribute__((always_inline)) {
             constexpr int X = decltype(XI)::value;
-            constexpr int kk = X / 16, m = X % 16, i = m / 4, jj = m % 4;
+            constexpr int kk = X / QB, m = X % QB, i = m / JN, jj = m % JN;
             const i16x8_t bw = __builtin_shufflevector(blo[kk & 1][jj], bhi[kk & 1][jj], 0, 1, 2, 3, 4, 5, 6, 7);
-            acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(areg[i][kk], __builtin_bit_cast(bf16x8_t, bw),
-                                                                 acc[i][jj], 0, 0, 0);
-            if constexpr (jj == 3) areg[i][kk] = __builtin_bit_cast(bf16x8_t, load16(rsA, a_off(s_next, i, kk)));
-            if constexpr (kk < 3 && m >= 8) read_b(Bs, kk + 1, (m - 8) / 2, (m - 8) % 2, (kk + 1) & 1);
-            if constexpr (X % 8 == 0) stage_r(IC<X / 8>{});
-            if constexpr (X % 8 == 4) stage_s(IC<X / 8>{}, run32);
-            if constexpr (X % 8 == 0 && X >= 8) stage_w(IC<X / 8 - 1>{}, dst);
+            acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(areg[i][kk % CFG::ASETS],
+                                                                 __builtin_bit_cast(bf16x8_t, bw), acc[i][jj], 0, 0, 0);
+            // after the last use of A(i, kk): reload its register set with the
+            // fragment needed ASETS quarters later
+            if constexpr (jj == JN - 1) {
+                if constexpr (CFG::AQ) {
+                    if constexpr (kk < 2)
+                        areg[i][kk % 2] = __builtin_bit_cast(bf16x8_t, load16(rsA, a_off(s_cur, i, kk + 2)));
+                    else
+                        areg[i][kk % 2] = __builtin_bit_cast(bf16x8_t, load16(rsA, a_off(s_next, i, kk - 2)));
+                } else {
+                    areg[i][kk] = __builtin_bit_cast(bf16x8_t, load16(rsA, a_off(s_next, i, kk)));
+                }
+            }
+            if constexpr (kk < 3 && m >= QB - 2 * JN) {
+                constexpr int r = m - (QB - 2 * JN);
+                read_b(Bs, kk + 1, r / 2, r % 2, (kk + 1) & 1);
+            }
+            if constexpr (X % PER == 0) stage_r(IC<X / PER>{});
+            if constexpr (X % PER == PER / 2) stage_s(IC<X / PER>{}, run32);
+            if constexpr (X % PER == 0 && X >= PER) stage_w(IC<X / PER - 1>{}, dst);
             __builtin_amdgcn_sched_barrier(0);
         });
-        stage_w(IC<7>{}, dst);
+        stage_w(IC<CH - 1>{}, dst);
     };
 
     // Pipeline.  At the top of iteration s: B_s[s&1] holds B(s), run_s[(s+1)&1]
@@ -574,7 +625,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_cb_kernel(GemmArgs a)
     __syncthreads();                                   // lut_s
     if (nsteps > 0) {
 #pragma unroll
-        for (int kk = 0; kk < 4; kk++) load_a(0, kk);
+        for (int kk = 0; kk < CFG::ASETS; kk++) load_a(0, kk);
         load_run(0);
         bm_cur = load_bm(0);
         store_run(0);
@@ -595,7 +646,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_cb_kernel(GemmArgs a)
         load_run(s2);
         const uint64_t bm_next = load_bm(s2);
         decode_rows(s1, bm_cur);
-        step(s1, R);
+        step(s, s1, R);
         if (zfix) zero_fixup(P ^ 1);
         store_run(P);
         bm_cur = bm_next;
@@ -609,32 +660,33 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_cb_kernel(GemmArgs a)
     if (s < nsteps) iteration(s, IC<0>{});
 
     // ---- epilogue: one 32-row block of accumulators at a time, staged in
-    // LDS (each wave its own 32 x 128 fp32 area), then written as 16-byte row
-    // segments.  Accumulator element r of lane l of a 32x32 block sits at
+    // LDS (each wave its own 32 x WAVE_N fp32 area), then written as 16-byte
+    // row segments.  Accumulator element r of lane l of a 32x32 block sits at
     // row 8*(r/4) + 4*(l/32) + r%4, column l%32.
-    constexpr int kStP = 128 + 4;                      // staging pitch (floats)
-    static_assert(4 * 32 * kStP * 4 <= kLds, "epilogue staging does not fit");
-    float* st = reinterpret_cast<float*>(lds) + wave * (32 * kStP);
-    const int64_t col0 = (int64_t)nt0 * 64 + wn * 128;
+    constexpr int ST_P = CFG::ST_P;
+    constexpr int LPR = CFG::WAVE_N / 4;               // lanes per staged row (4 columns each)
+    constexpr int RPI = 64 / LPR;                      // rows written per pass
+    float* st = reinterpret_cast<float*>(lds) + wave * (32 * ST_P);
+    const int64_t col0 = (int64_t)nt0 * 64 + wn * CFG::WAVE_N;
     const bool cvec = (a.N % 4 == 0) && (a.part != nullptr || (((uintptr_t)a.C) & 7) == 0);
     __syncthreads();                                   // last reads of B_s / run_s
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
+    for (int i = 0; i < IM; i++) {
 #pragma unroll
-        for (int jj = 0; jj < 4; jj++)
+        for (int jj = 0; jj < JN; jj++)
 #pragma unroll
             for (int r = 0; r < 16; r++)
-                st[(8 * (r >> 2) + 4 * hh + (r & 3)) * kStP + jj * 32 + col] = acc[i][jj][r];
+                st[(8 * (r >> 2) + 4 * hh + (r & 3)) * ST_P + jj * 32 + col] = acc[i][jj][r];
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        // lane l: columns 4*(l%32) .. +3 of rows 2*it + l/32
+        // lane l: columns 4*(l%LPR) .. +3 of row RPI*it + l/LPR
 #pragma unroll 4
-        for (int it = 0; it < 16; it++) {
-            const int rr2 = 2 * it + hh;
+        for (int it = 0; it < 32 / RPI; it++) {
+            const int rr2 = RPI * it + lane / LPR;
             const int64_t row = arow0 + i * 32 + rr2;
-            const int64_t c4 = col0 + 4 * col;
-            const float4 v = *reinterpret_cast<const float4*>(&st[rr2 * kStP + 4 * col]);
+            const int64_t c4 = col0 + 4 * (lane % LPR);
+            const float4 v = *reinterpret_cast<const float4*>(&st[rr2 * ST_P + 4 * (lane % LPR)]);
             if (row >= a.M || c4 >= a.N) continue;
             if (a.part) {
                 float* dst = a.part + ((int64_t)split * a.M + row) * a.N + c4;
@@ -757,9 +809,9 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* part, i
 // Split-K factor: fewest "rounds x steps" with one workgroup per CU on kCus
 // CUs, a small charge for the partial-sum pass, <= kMaxSteps per workgroup
 // and >= 8 steps per workgroup where possible.
-static int gemm_split(int64_t M, int64_t N, int64_t K)
+static int gemm_split(int64_t M, int64_t N, int64_t K, int64_t bm, int64_t bn)
 {
-    const int64_t tiles = ((N + kBN - 1) / kBN) * ((M + kBM - 1) / kBM);
+    const int64_t tiles = ((N + bn - 1) / bn) * ((M + bm - 1) / bm);
     const int64_t ksteps = (K + kBK - 1) / kBK;
     const int64_t min_split = (ksteps + kMaxSteps - 1) / kMaxSteps;
     int64_t best = min_split, best_cost = -1;
@@ -778,6 +830,25 @@ static int gemm_split(int64_t M, int64_t N, int64_t K)
 // Apk geometry: k padded to whole K-steps, rows to whole 32-row blocks
 static int64_t apk_nkb(int64_t K) { return (K + kBK - 1) / kBK * (kBK / 16); }
 static int64_t apk_bytes(int64_t M, int64_t K) { return (M + 31) / 32 * apk_nkb(K) * 1024; }
+
+// Launch plan: 512-row workgroups when they cover M with no more padding
+// than 256-row ones (half the decode work per MFMA), else 256 x 256.
+struct GemmPlan {
+    bool big;
+    int64_t bm, bn;
+    int split;
+};
+static GemmPlan gemm_plan(int64_t M, int64_t N, int64_t K)
+{
+    GemmPlan p;
+    const int64_t pad512 = (M + Cfg512::BM - 1) / Cfg512::BM * Cfg512::BM;
+    const int64_t pad256 = (M + Cfg256::BM - 1) / Cfg256::BM * Cfg256::BM;
+    p.big = M >= Cfg512::BM && pad512 <= pad256;
+    p.bm = p.big ? Cfg512::BM : Cfg256::BM;
+    p.bn = p.big ? Cfg512::BN : Cfg256::BN;
+    p.split = gemm_split(M, N, K, p.bm, p.bn);
+    return p;
+}
 static int64_t align_up256(int64_t x) { return (x + 255) / 256 * 256; }
 
 }  // namespace bs
@@ -787,7 +858,7 @@ using namespace bs;
 extern "C" int64_t bs_gemm_compressed_b_workspace_bytes(int64_t M, int64_t N, int64_t K, int a_layout)
 {
     if (M <= 0 || N <= 0 || K <= 0) return 0;
-    const int split = gemm_split(M, N, K);
+    const int split = gemm_plan(M, N, K).split;
     int64_t bytes = split > 1 ? align_up256((int64_t)split * M * N * 4) : 0;
     (void)a_layout;
     bytes += apk_bytes(M, K);
@@ -829,7 +900,8 @@ extern "C" int bs_gemm_compressed_b(const void* A, int64_t M, int64_t K, int64_t
         hipError_t e = hipMemsetAsync(C, 0, (size_t)M * N * 2, st);
         return e == hipSuccess ? BS_OK : set_error(BS_ERR_HIP, "bs_gemm_compressed_b: %s", hipGetErrorString(e));
     }
-    const int split = gemm_split(M, N, K);
+    const GemmPlan plan = gemm_plan(M, N, K);
+    const int split = plan.split;
     const int64_t part_bytes = split > 1 ? align_up256((int64_t)split * M * N * 4) : 0;
     const int64_t nkb = apk_nkb(K), nrb = (M + 31) / 32;
     if (nkb >= (1ll << 20)) return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: K too large");
@@ -850,8 +922,9 @@ extern "C" int bs_gemm_compressed_b(const void* A, int64_t M, int64_t K, int64_t
     g.vals_offset = vals_offset;
     g.N = N;
     g.grid_n = (uint32_t)((N + kTile - 1) / kTile);
-    g.tiles_n = (g.grid_n + 3) / 4;
-    g.tiles_m = (uint32_t)((M + kBM - 1) / kBM);
+    const uint32_t nt = (uint32_t)(plan.bn / kTile);
+    g.tiles_n = (g.grid_n + nt - 1) / nt;
+    g.tiles_m = (uint32_t)((M + plan.bm - 1) / plan.bm);
     g.relu2_scale = relu2_scale;
     g.b_scale = b_scale;
     g.C = (uint16_t*)C;
@@ -877,8 +950,15 @@ extern "C" int bs_gemm_compressed_b(const void* A, int64_t M, int64_t K, int64_t
     g.Apk = apk;
     g.nkb = (uint32_t)nkb;
     g.nrb = (uint32_t)nrb;
-#define BS_GEMM_LAUNCH(VT, SQ, SC) \
-    hipLaunchKernelGGL((gemm_cb_kernel<VT, SQ, SC>), dim3((uint32_t)blocks), dim3(kThreads), 0, st, g)
+#define BS_GEMM_LAUNCH(VT, SQ, SC)                                                                              \
+    do {                                                                                                        \
+        if (plan.big)                                                                                           \
+            hipLaunchKernelGGL((gemm_cb_kernel<Cfg512, VT, SQ, SC>), dim3((uint32_t)blocks), dim3(Cfg512::THREADS), \
+                               0, st, g);                                                                       \
+        else                                                                                                    \
+            hipLaunchKernelGGL((gemm_cb_kernel<Cfg256, VT, SQ, SC>), dim3((uint32_t)blocks), dim3(Cfg256::THREADS), \
+                               0, st, g);                                                                       \
+    } while (0)
     const bool sc = b_scale != nullptr;
     switch (vals_dtype) {
     case DT_BF16:

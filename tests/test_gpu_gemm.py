@@ -50,12 +50,13 @@ def test_gemm_transposed_a_and_buffer_offset(dev):
         _check(AspB(dY.T, sp), _ref(dY.T, h))
 
 
+@pytest.mark.parametrize("M", [320, 1024])       # 256-row and 512-row workgroups
 @pytest.mark.parametrize("storage", ["bf16", "e4m3fn"])
-def test_gemm_relu2_square(dev, storage):
+def test_gemm_relu2_square(dev, storage, M):
     from bitsparse_amd.src import dw_gemm
     from bitsparse_amd.src.functions import dense_to_tilesparse, quantize_and_compress
     from bitsparse_amd.src.hip_operators import unpack_relu2_batch_
-    K, N, M = 384, 448, 320
+    K, N = 384, 448
     r = preact_input((K, N), seed=6).relu().to(dev)
     A = preact_input((M, K), seed=7).to(dev)
     if storage == "bf16":
@@ -79,8 +80,9 @@ def test_gemm_all_zero_and_dense_operands(dev):
         _check(C, _ref(A, h))
 
 
+@pytest.mark.parametrize("K", [320, 1024])       # 256-row and 512-row workgroups
 @pytest.mark.parametrize("storage,square", [("bf16", False), ("bf16", True), ("e4m3fn", True)])
-def test_gemm_identity_reproduces_decoded_operand(dev, storage, square):
+def test_gemm_identity_reproduces_decoded_operand(dev, storage, square, K):
     """With A = I (K = M) every output is 1.0 * b accumulated in fp32, so C
     must equal the decompressed operand bit for bit: this pins the GEMM's
     in-LDS decode (ranks, byte permutes, hardware bf16 / fp8 conversions,
@@ -89,7 +91,7 @@ def test_gemm_identity_reproduces_decoded_operand(dev, storage, square):
     from bitsparse_amd.src import dw_gemm
     from bitsparse_amd.src.functions import dense_to_tilesparse, quantize_and_compress
     from bitsparse_amd.src.hip_operators import unpack_batch_, unpack_relu2_batch_
-    K, N = 320, 448
+    N = 448
     r = preact_input((K, N), seed=11).relu().to(dev)
     if storage == "bf16":
         sp = dense_to_tilesparse(r, None)
