@@ -12,6 +12,7 @@
 #include "bs_host.h"
 
 #include <algorithm>
+#include <cstdlib>
 
 
 namespace bs {
@@ -150,6 +151,7 @@ struct CompressArgs {
     uint32_t epoch;
     int32_t* err;
     uint32_t* fallbacks;
+    uint64_t patience;          // look-back wait (s_memrealtime ticks) before counting a unit itself
 };
 
 // status word: [63:34] epoch, [33:32] flag (1 aggregate, 2 inclusive), [31:0] value
@@ -162,7 +164,9 @@ __device__ __forceinline__ uint64_t pack_status(uint32_t epoch, uint64_t flag, u
 // 200 us at the 100 MHz s_memrealtime clock: waiting longer than this for a
 // predecessor makes the waiter count that predecessor's tiles itself (a
 // safety net: in-order workgroup dispatch never needs it, and normal waits
-// behind slow predecessors stay well below it).
+// behind slow predecessors stay well below it).  The environment variable
+// BITSPARSE_LOOKBACK_PATIENCE (ticks) overrides it; 0 makes every wait take
+// the fallback, which is how the tests exercise that path.
 constexpr uint64_t kLookbackPatienceTicks = 20000;
 
 template <int IN_T, bool QUANT>
@@ -365,7 +369,7 @@ __device__ uint32_t wave_lookback_grouped(const CompressArgs& a, uint32_t u, uin
                 excl += (uint32_t)s0;
                 break;
             }
-            if (wall_clock64() - since > kLookbackPatienceTicks) {
+            if (wall_clock64() - since > a.patience) {
                 excl += unit_count_wave<IN_T, QUANT, VEC, U>(a, (uint32_t)pos, scale, lane);
                 if (lane == 0 && a.fallbacks) atomicAdd(a.fallbacks, 1u);
                 break;
@@ -383,8 +387,9 @@ __device__ uint32_t wave_lookback_grouped(const CompressArgs& a, uint32_t u, uin
 // ===========================================================================
 // streaming compress (bs_compress FUSED / COUNT)
 //
-// One wave per tile, U tiles (one look-back unit) per workgroup, persistent
-// workgroups that take units from a ticket counter.  Lane l owns chunks
+// One wave per tile, U tiles (one look-back unit) per workgroup; unit u is
+// workgroup u (workgroups are dispatched in id order, so every unit's
+// predecessors are already resident or done when it starts).  Lane l owns chunks
 // 64k + l (k < 8) of its tile: rows 8k + l/8, columns 8(l%8)..+7, so every
 // load instruction covers 8 whole tile rows and the tile's value run is
 // produced in eight in-order rounds of 64 chunks.  The loaded chunks stay in
@@ -1410,6 +1415,12 @@ static int compress_impl(const void* dense, int in_dtype, int64_t M, int64_t N, 
     a.epoch = epoch;
     a.err = err_flags;
     a.fallbacks = reinterpret_cast<uint32_t*>((uint8_t*)workspace + kWsFallbackOffset);
+    a.patience = kLookbackPatienceTicks;
+    if (const char* ev = getenv("BITSPARSE_LOOKBACK_PATIENCE")) {
+        char* end = nullptr;
+        const unsigned long long v = strtoull(ev, &end, 10);
+        if (end != ev) a.patience = (uint64_t)v;
+    }
     a.gstat = a.status + (T + kStreamU - 1) / kStreamU;
     const int inb = in_dtype == DT_BF16 ? 2 : 1;
     bool vec = (N % 8 == 0) && (((uintptr_t)dense) % (8 * inb) == 0) &&
@@ -1481,6 +1492,7 @@ extern "C" int bs_compact_vals(const void* dense, int in_dtype, int64_t M, int64
     a.tile0 = (uint32_t)first_tile;
     a.tend = (uint32_t)(first_tile + num_tiles);
     a.err = err_flags;
+    a.patience = kLookbackPatienceTicks;       // no look-back in this mode
     bool vec = (N % 8 == 0) && (((uintptr_t)dense) % (8 * eb) == 0);
     hipError_t e = launch_compress<MODE_VALS>(a, in_dtype, false, vec, (hipStream_t)stream);
     if (e != hipSuccess) return set_error(BS_ERR_HIP, "bs_compact_vals launch: %s", hipGetErrorString(e));

@@ -177,6 +177,41 @@ def test_c3_size_properties(dev, mu):
     assert torch.equal(sp.vals[:vals_ref.numel()], vals_ref)
 
 
+@pytest.mark.parametrize("quant", [False, True])
+def test_lookback_fallback_path(dev, monkeypatch, quant):
+    """The compress look-back's safety net: with BITSPARSE_LOOKBACK_PATIENCE=0 a
+    unit that finds a predecessor unpublished counts that predecessor's tiles
+    from the dense input at once.  Every wave still finishes (each wait ends
+    after one poll); the output must be bit-identical to the normal path and
+    the fallback counter must show the path ran."""
+    from bitsparse_amd import _lib
+    from bitsparse_amd.src.functions import dense_to_tilesparse, quantize_and_compress
+    M, N = 8192, 8192
+    g = torch.Generator(device=dev).manual_seed(3)
+    x = torch.randn((M, N), device=dev, generator=g).to(torch.bfloat16).relu_()
+
+    def run():
+        if quant:
+            _, _, sp = quantize_and_compress(x, None)
+        else:
+            sp = dense_to_tilesparse(x, None)
+        torch.cuda.synchronize()
+        return sp
+
+    ref = run()
+    ws = _lib.workspace_for(x.device)
+    before = ws.fallback_count()
+    monkeypatch.setenv("BITSPARSE_LOOKBACK_PATIENCE", "0")
+    got = run()
+    after = ws.fallback_count()
+    monkeypatch.delenv("BITSPARSE_LOOKBACK_PATIENCE")
+    assert after > before
+    assert torch.equal(got.bitmask, ref.bitmask)
+    assert torch.equal(got.prefix, ref.prefix)
+    n = int(ref.prefix[-1].item())
+    assert torch.equal(got.vals[:n].view(torch.uint8), ref.vals[:n].view(torch.uint8))
+
+
 @pytest.mark.parametrize("shape", [(129, 131), (300, 200), (448, 512)])
 def test_unpack_row_batches(dev, shape):
     F, H, _ = _bs()
