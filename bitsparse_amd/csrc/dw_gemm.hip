@@ -629,9 +629,11 @@ __global__ __launch_bounds__(CFG::THREADS, 1) void gemm_cb_kernel(GemmArgs a)
         load_run(0);
         bm_cur = load_bm(0);
         store_run(0);
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    // the DW waves of a tile stage its run together: all of it must be in LDS
+    // before any of them decodes (nsteps is uniform, every wave gets here)
+    __syncthreads();
+    if (nsteps > 0) {
         decode_rows(0, bm_cur);
         decode(0, 0);
         if (zfix) zero_fixup(0);
