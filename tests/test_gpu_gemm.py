@@ -34,12 +34,13 @@ def test_gemm_bf16(dev, M, K, N):
     _check(C, _ref(A, h))
 
 
-def test_gemm_transposed_a_and_buffer_offset(dev):
+@pytest.mark.parametrize("d_out", [192, 1024])   # 256-row and 512-row workgroups
+def test_gemm_transposed_a_and_buffer_offset(dev, d_out):
     """AspB's call shape: A = dY.T (a transposed view), h in a shared buffer."""
     from bitsparse_amd.bitsparse import TensorBuffer
     from bitsparse_amd.src.functions import dense_to_tilesparse
     from bitsparse_amd.src.sparse_matmul import AspB
-    dY = preact_input((512, 192), seed=3).to(dev)
+    dY = preact_input((512, d_out), seed=3).to(dev)
     h1 = relu_input((512, 320), 0.7, seed=4).to(dev)
     h2 = relu_input((512, 320), 0.3, seed=5).to(dev)
     buf = TensorBuffer(2 * 2 * 512 * 320, device=dev)
