@@ -47,13 +47,13 @@ constexpr int kMaxSteps = 256;        // K-steps per workgroup (prefixes held in
 constexpr int kCus = 256;             // MI355X compute units (split-K sizing)
 constexpr int kXcds = 8;
 
-// Workgroup shape: a WGM x WGN grid of waves, each owning a 128 x WN block of
+// Workgroup shape: a WGM x WGN grid of waves, each owning a WM x WN block of
 // C.  A K-step decodes BN/64 B tiles; each is decoded by NWAVES/NT waves.
 //   Cfg256: 256 x 256, 4 waves (one per SIMD), 128 x 128 per wave
-//   Cfg512: 512 x 128, 8 waves (two per SIMD), 128 x 64 per wave: every
+//   Cfg512: 512 x 128, 8 waves (two per SIMD), 64 x 128 per wave: every
 //           decoded B element feeds 512 rows instead of 256, half the decode
 //           instructions per MFMA
-template <int WGM_, int WGN_, int WN_, bool AQ_>
+template <int WGM_, int WGN_, int WM_, int WN_, bool AQ_>
 struct GemmCfg {
     // AQ: A fragments are loaded one k-quarter ahead (2 register sets) instead
     // of one K-step ahead (4 sets); with two waves per SIMD the other wave
@@ -61,7 +61,7 @@ struct GemmCfg {
     static constexpr bool AQ = AQ_;
     static constexpr int ASETS = AQ_ ? 2 : 4;
     static constexpr int WGM = WGM_, WGN = WGN_, NWAVES = WGM_ * WGN_, THREADS = 64 * NWAVES;
-    static constexpr int WAVE_M = 128, WAVE_N = WN_;
+    static constexpr int WAVE_M = WM_, WAVE_N = WN_;
     static constexpr int IM = WAVE_M / 32, JN = WAVE_N / 32;    // 32x32 accumulator blocks per wave
     static constexpr int BM = WAVE_M * WGM, BN = WAVE_N * WGN;
     static constexpr int NT = BN / 64;                           // B tiles per K-step
@@ -84,11 +84,13 @@ struct GemmCfg {
     static constexpr int LDS = OFF_LUT + 256 * 16;
     static constexpr int ST_P = WAVE_N + 4;                      // epilogue staging pitch (floats)
     static_assert(LDS <= 160 * 1024, "LDS budget");
-    static_assert(NWAVES * 32 * ST_P * 4 <= LDS, "epilogue staging does not fit");
+    static_assert(NWAVES * 16 * ST_P * 4 <= LDS, "epilogue staging does not fit");
     static_assert(NWAVES % NT == 0 && 8 % DW == 0 && SEG % CH == 0, "decode split");
 };
-using Cfg256 = GemmCfg<2, 2, 128, false>;
-using Cfg512 = GemmCfg<4, 2, 64, true>;
+using Cfg256 = GemmCfg<2, 2, 128, 128, false>;
+// 8 x 1 waves of 64 x 128: each A row block is read by one wave (a 4 x 2 grid
+// of 128 x 64 reads every A block twice and measured 4% slower)
+using Cfg512 = GemmCfg<8, 1, 64, 128, false>;
 
 struct GemmArgs {
     const uint16_t* Apk;          // A in MFMA-fragment order (pack_a_*_kernel)
@@ -661,57 +663,61 @@ __global__ __launch_bounds__(CFG::THREADS, 1) void gemm_cb_kernel(GemmArgs a)
     }
     if (s < nsteps) iteration(s, IC<0>{});
 
-    // ---- epilogue: one 32-row block of accumulators at a time, staged in
-    // LDS (each wave its own 32 x WAVE_N fp32 area), then written as 16-byte
+    // ---- epilogue: half a 32-row block of accumulators at a time, staged in
+    // LDS (each wave its own 16 x WAVE_N fp32 area), then written as 16-byte
     // row segments.  Accumulator element r of lane l of a 32x32 block sits at
-    // row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+    // row 8*(r/4) + 4*(l/32) + r%4, column l%32: elements r < 8 are rows 0-15.
     constexpr int ST_P = CFG::ST_P;
     constexpr int LPR = CFG::WAVE_N / 4;               // lanes per staged row (4 columns each)
     constexpr int RPI = 64 / LPR;                      // rows written per pass
-    float* st = reinterpret_cast<float*>(lds) + wave * (32 * ST_P);
+    float* st = reinterpret_cast<float*>(lds) + wave * (16 * ST_P);
     const int64_t col0 = (int64_t)nt0 * 64 + wn * CFG::WAVE_N;
     const bool cvec = (a.N % 4 == 0) && (a.part != nullptr || (((uintptr_t)a.C) & 7) == 0);
     __syncthreads();                                   // last reads of B_s / run_s
 #pragma unroll
     for (int i = 0; i < IM; i++) {
 #pragma unroll
-        for (int jj = 0; jj < JN; jj++)
+        for (int half = 0; half < 2; half++) {
 #pragma unroll
-            for (int r = 0; r < 16; r++)
-                st[(8 * (r >> 2) + 4 * hh + (r & 3)) * ST_P + jj * 32 + col] = acc[i][jj][r];
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        // lane l: columns 4*(l%LPR) .. +3 of row RPI*it + l/LPR
-#pragma unroll 4
-        for (int it = 0; it < 32 / RPI; it++) {
-            const int rr2 = RPI * it + lane / LPR;
-            const int64_t row = arow0 + i * 32 + rr2;
-            const int64_t c4 = col0 + 4 * (lane % LPR);
-            const float4 v = *reinterpret_cast<const float4*>(&st[rr2 * ST_P + 4 * (lane % LPR)]);
-            if (row >= a.M || c4 >= a.N) continue;
-            if (a.part) {
-                float* dst = a.part + ((int64_t)split * a.M + row) * a.N + c4;
-                if (cvec) {
-                    *reinterpret_cast<float4*>(dst) = v;
+            for (int jj = 0; jj < JN; jj++)
+#pragma unroll
+                for (int r = 8 * half; r < 8 * half + 8; r++)
+                    st[(8 * ((r >> 2) & 1) + 4 * hh + (r & 3)) * ST_P + jj * 32 + col] = acc[i][jj][r];
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            // lane l: columns 4*(l%LPR) .. +3 of staged row RPI*it + l/LPR, which
+            // is block row 16*half + that row
+#pragma unroll
+            for (int it = 0; it < 16 / RPI; it++) {
+                const int rr2 = RPI * it + lane / LPR;
+                const int64_t row = arow0 + i * 32 + 16 * half + rr2;
+                const int64_t c4 = col0 + 4 * (lane % LPR);
+                const float4 v = *reinterpret_cast<const float4*>(&st[rr2 * ST_P + 4 * (lane % LPR)]);
+                if (row >= a.M || c4 >= a.N) continue;
+                if (a.part) {
+                    float* dst = a.part + ((int64_t)split * a.M + row) * a.N + c4;
+                    if (cvec) {
+                        *reinterpret_cast<float4*>(dst) = v;
+                    } else {
+                        const float e[4] = {v.x, v.y, v.z, v.w};
+                        for (int x = 0; x < 4 && c4 + x < a.N; x++) dst[x] = e[x];
+                    }
                 } else {
-                    const float e[4] = {v.x, v.y, v.z, v.w};
-                    for (int x = 0; x < 4 && c4 + x < a.N; x++) dst[x] = e[x];
-                }
-            } else {
-                uint16_t* dst = a.C + row * a.N + c4;
-                const uint32_t b0 = hw_bf16(v.x), b1 = hw_bf16(v.y), b2 = hw_bf16(v.z), b3 = hw_bf16(v.w);
-                if (cvec) {
-                    *reinterpret_cast<uint2*>(dst) = uint2{b0 | (b1 << 16), b2 | (b3 << 16)};
-                } else {
-                    const uint32_t e[4] = {b0, b1, b2, b3};
-                    for (int x = 0; x < 4 && c4 + x < a.N; x++) dst[x] = (uint16_t)e[x];
+                    uint16_t* dst = a.C + row * a.N + c4;
+                    const uint32_t b0 = hw_bf16(v.x), b1 = hw_bf16(v.y), b2 = hw_bf16(v.z), b3 = hw_bf16(v.w);
+                    if (cvec) {
+                        *reinterpret_cast<uint2*>(dst) = uint2{b0 | (b1 << 16), b2 | (b3 << 16)};
+                    } else {
+                        const uint32_t e[4] = {b0, b1, b2, b3};
+                        for (int x = 0; x < 4 && c4 + x < a.N; x++) dst[x] = (uint16_t)e[x];
+                    }
                 }
             }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
 }
 
