@@ -1333,8 +1333,8 @@ static int check_dense(const void* dense, int dtype, int64_t M, int64_t N, const
     if (dtype < 0 || dtype > 2) return set_error(BS_ERR_INVALID, "%s: unknown dtype code %d", what, dtype);
     if (M < 0 || N < 0) return set_error(BS_ERR_INVALID, "%s: negative shape", what);
     if ((M > 0 && N > 0) && dense == nullptr) return set_error(BS_ERR_INVALID, "%s: null input", what);
-    if ((uint64_t)M * (uint64_t)N >= (1ull << 32))
-        return set_error(BS_ERR_INVALID, "%s: M*N must be < 2^32 (uint32 prefix)", what);
+    if ((uint64_t)M * (uint64_t)N >= kMaxElems)
+        return set_error(BS_ERR_INVALID, "%s: M*N must be < 2^31", what);
     int elem = dtype == DT_BF16 ? 2 : 1;
     if (((uintptr_t)dense) % elem)
         return set_error(BS_ERR_INVALID, "%s: input not aligned to its element size", what);
@@ -1584,6 +1584,8 @@ static int decompress_impl(const void* vals, int vals_dtype, int64_t vals_numel,
         return set_error(BS_ERR_INVALID, "bs_decompress: scale is only applied with square=1");
     if ((uint64_t)(first_m_tile * grid_n + num_tiles_in_batch) >= (1ull << 32))
         return set_error(BS_ERR_INVALID, "bs_decompress: tile ids exceed 32 bits");
+    if ((uint64_t)batch_rows * (uint64_t)K >= kMaxElems)
+        return set_error(BS_ERR_INVALID, "bs_decompress: batch_rows*K must be < 2^31");
     const int ob = square ? 2 : (vals_dtype == DT_BF16 ? 2 : 1);
     if (((uintptr_t)out) % ob) return set_error(BS_ERR_INVALID, "bs_decompress: output misaligned");
     GatherArgs a{};
@@ -1651,8 +1653,8 @@ extern "C" int bs_relu_grad(void* grad, int64_t M, int64_t N, const uint8_t* bit
     const int64_t T = ((M + 63) / 64) * ((N + 63) / 64);
     if (T == 0) return BS_OK;
     if (grad == nullptr || bitmask == nullptr) return set_error(BS_ERR_INVALID, "bs_relu_grad: null pointer");
-    if ((uint64_t)M * (uint64_t)N >= (1ull << 32))
-        return set_error(BS_ERR_INVALID, "bs_relu_grad: M*N must be < 2^32");
+    if ((uint64_t)M * (uint64_t)N >= kMaxElems)
+        return set_error(BS_ERR_INVALID, "bs_relu_grad: M*N must be < 2^31");
     if (((uintptr_t)grad) & 1u) return set_error(BS_ERR_INVALID, "bs_relu_grad: grad misaligned");
     bool vec = (N % 8 == 0) && aligned16(grad);
     uint32_t gn = (uint32_t)((N + 63) / 64);
@@ -1697,8 +1699,8 @@ static int relu2_grad_impl(void* grad, int64_t M, int64_t N, const void* vals, i
     const int64_t T = ((M + 63) / 64) * ((N + 63) / 64);
     if (T == 0) return BS_OK;
     if (grad == nullptr) return set_error(BS_ERR_INVALID, "bs_relu2_grad: null grad");
-    if ((uint64_t)M * (uint64_t)N >= (1ull << 32))
-        return set_error(BS_ERR_INVALID, "bs_relu2_grad: M*N must be < 2^32");
+    if ((uint64_t)M * (uint64_t)N >= kMaxElems)
+        return set_error(BS_ERR_INVALID, "bs_relu2_grad: M*N must be < 2^31");
     if (((uintptr_t)grad) & 1u) return set_error(BS_ERR_INVALID, "bs_relu2_grad: grad misaligned");
     GatherArgs a{};
     a.vals = (const uint8_t*)vals;

@@ -891,8 +891,8 @@ extern "C" int bs_gemm_compressed_b(const void* A, int64_t M, int64_t K, int64_t
     if (a_layout == 1 && lda < K) return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: lda < K");
     if (a_layout == 1 && K % 8 != 0)
         return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: a_layout 1 needs K %% 8 == 0");
-    if ((uint64_t)K * (uint64_t)N >= (1ull << 32))
-        return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: K*N must be < 2^32");
+    if ((uint64_t)K * (uint64_t)N >= kMaxElems)
+        return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: K*N must be < 2^31");
     if (M == 0 || N == 0) return BS_OK;
     if (A == nullptr || C == nullptr || bitmask == nullptr || prefix == nullptr ||
         (vals_numel > 0 && vals == nullptr))
