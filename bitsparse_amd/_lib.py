@@ -173,6 +173,8 @@ class Workspace:
 
     def fallback_count(self) -> int:
         """Look-back fallbacks recorded in this workspace (synchronises)."""
+        if self.buf.numel() < 12:
+            return 0
         return int(self.buf[8:12].view(torch.int32).item())
 
 
