@@ -1022,19 +1022,24 @@ __device__ __forceinline__ int stage_run_packed(const GatherArgs& a, int64_t run
 // Shared front half of decompress and relu2_grad: bitmask bytes, in-tile
 // ranks, run staging.  Fills m[][], r0[][] (LDS element index of each chunk's
 // first value) and returns after a barrier.
-template <int VB, int PB, int U>
+// M_LOADED: the caller already holds the mask bytes in m and prefix[t0 + tid]
+// (tid <= ntiles) in pf.
+template <int VB, int PB, int U, bool M_LOADED = false>
 __device__ __forceinline__ int gather_prepare(const GatherArgs& a, uint32_t t0, int ntiles,
                                               uint32_t (&m)[U][2], uint32_t (&r0)[U][2],
                                               uint32_t* s_pref, uint32_t (*s_wtot)[2][4],
-                                              uint8_t* s_vals, int tid)
+                                              uint8_t* s_vals, int tid, uint32_t pf = 0u)
 {
     const int wave = tid >> 6, lane = tid & 63;
+    if constexpr (!M_LOADED) {
 #pragma unroll
-    for (int j = 0; j < U; j++)
+        for (int j = 0; j < U; j++)
 #pragma unroll
-        for (int h = 0; h < 2; h++)
-            m[j][h] = j < ntiles ? a.bitmask[(size_t)(t0 + j) * kTileBytes + h * 256 + tid] : 0u;
-    if (tid <= ntiles) s_pref[tid] = a.prefix[t0 + tid];
+            for (int h = 0; h < 2; h++)
+                m[j][h] = j < ntiles ? a.bitmask[(size_t)(t0 + j) * kTileBytes + h * 256 + tid] : 0u;
+        if (tid <= ntiles) pf = a.prefix[t0 + tid];
+    }
+    if (tid <= ntiles) s_pref[tid] = pf;
     uint32_t ex[U][2];
 #pragma unroll
     for (int j = 0; j < U; j++)
@@ -1119,6 +1124,13 @@ __global__ __launch_bounds__(kThreads) void decompress_kernel(GatherArgs a)
     // raw run: 16-byte phase + the run; packed run: 16-byte phase, the run
     // (PB/8 < VB bytes per value) and a guard slot
     __shared__ __align__(16) uint8_t s_vals[U * kTileNumel * VB + 32];
+    // SQUARE from fp8 storage: every staged value converted once (k v^2, times
+    // bf16(scale^2)) instead of in each of the 8 slots of every chunk; bf16
+    // storage squares inline (its conversion is short and a second 16 KiB
+    // buffer would halve the resident workgroups)
+    constexpr bool STAGE = SQUARE && V_T != DT_BF16;
+    constexpr int kSq = U * kTileNumel + 32;
+    __shared__ __align__(16) uint16_t s_sq[STAGE ? kSq : 1];
     const int tid = threadIdx.x;
     const uint32_t pid0 = blockIdx.x * U;
     const int ntiles = (int)min((uint32_t)U, a.num_tiles - pid0);
@@ -1132,6 +1144,20 @@ __global__ __launch_bounds__(kThreads) void decompress_kernel(GatherArgs a)
         float s = *a.scale;
         s2b = bf16_to_f32(f32_to_bf16(s * s));
     }
+    // an unset element: 0, or bf16(0 * bf16(scale^2)) (NaN for an infinite or NaN scale)
+    const uint32_t zero_x = HAS_SCALE ? f32_to_bf16(0.0f * s2b) : 0u;
+    if constexpr (STAGE) {
+        // staged indices [0, count + 16) cover the run and its <= 15-element
+        // phase (count clamped as the staging clamps it)
+        const int64_t cnt = (int64_t)s_pref[ntiles] - (int64_t)s_pref[0];
+        const int n_conv = (int)min<int64_t>(max<int64_t>(cnt, 0), (int64_t)ntiles * kTileNumel) + 16;
+        for (int i = tid; i < n_conv; i += kThreads) {
+            uint32_t x = relu2_square<V_T>(lds_val<V_T, PB>(s_vals, (uint32_t)i, bitbase), a.relu2_scale);
+            if constexpr (HAS_SCALE) x = f32_to_bf16(bf16_to_f32(x) * s2b);
+            s_sq[i] = (uint16_t)x;
+        }
+        __syncthreads();
+    }
 #pragma unroll
     for (int j = 0; j < U; j++) {
         if (j >= ntiles) break;
@@ -1142,12 +1168,18 @@ __global__ __launch_bounds__(kThreads) void decompress_kernel(GatherArgs a)
             const uint32_t mm = m[j][h];
 #pragma unroll
             for (int e = 0; e < 8; e++) {
-                uint32_t x = 0;
-                if ((mm >> e) & 1u) {
-                    x = lds_val<V_T, PB>(s_vals, r++, bitbase);
-                    if constexpr (SQUARE) x = relu2_square<V_T>(x, a.relu2_scale);
+                uint32_t x;
+                if constexpr (STAGE) {
+                    x = ((mm >> e) & 1u) ? (uint32_t)s_sq[r] : zero_x;
+                } else {
+                    x = 0u;
+                    if ((mm >> e) & 1u) {
+                        x = lds_val<V_T, PB>(s_vals, r, bitbase);
+                        if constexpr (SQUARE) x = relu2_square<V_T>(x, a.relu2_scale);
+                    }
+                    if constexpr (HAS_SCALE) x = f32_to_bf16(bf16_to_f32(x) * s2b);
                 }
-                if constexpr (HAS_SCALE) x = f32_to_bf16(bf16_to_f32(x) * s2b);
+                r += (mm >> e) & 1u;
                 set_elem<OB>(ov, e, x);
             }
             int64_t row, col0;
@@ -1166,28 +1198,49 @@ __global__ __launch_bounds__(kThreads) void relu2_grad_kernel(GatherArgs a)
     __shared__ uint32_t s_pref[U + 1];
     __shared__ uint32_t s_wtot[U][2][4];
     __shared__ __align__(16) uint8_t s_vals[U * kTileNumel * VB + 32];
+    // fp8 or packed storage: each staged value widened once to its bf16 bits
+    // (exact: every e4m3fn / e5m2 value is a bf16 value)
+    constexpr bool WIDEN = V_T != DT_BF16 || PACKED;
+    constexpr int kRv = U * kTileNumel + 32;
+    __shared__ __align__(16) uint16_t s_rv[WIDEN ? kRv : 1];
     const int tid = threadIdx.x;
     const uint32_t t0 = blockIdx.x * U;
     const int ntiles = (int)min((uint32_t)U, a.num_tiles - t0);
 
-    // gradient chunks are independent of the gather: issue their loads first
+    // mask bytes first: a chunk with no bit set is written without reading
+    // its gradient (at 90% zeros 43% of the chunks)
+    uint32_t m[U][2], r0[U][2];
+#pragma unroll
+    for (int j = 0; j < U; j++)
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+            m[j][h] = j < ntiles ? a.bitmask[(size_t)(t0 + j) * kTileBytes + h * 256 + tid] : 0u;
+    const uint32_t pf = tid <= ntiles ? a.prefix[t0 + tid] : 0u;
     uint4 g[U][2];
 #pragma unroll
     for (int j = 0; j < U; j++)
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             g[j][h] = uint4{0u, 0u, 0u, 0u};
-            if (j < ntiles) {
+            if (m[j][h] != 0u) {
                 int64_t row, col0;
                 chunk_pos(t0 + j, a.grid_n, h * 256 + tid, row, col0);
                 g[j][h] = load_chunk<2, VEC>(a.out, a.rows, a.K, row, col0);
             }
         }
-    uint32_t m[U][2], r0[U][2];
-    const int bitbase = gather_prepare<VB, PB, U>(a, t0, ntiles, m, r0, s_pref, s_wtot, s_vals, tid);
+    const int bitbase = gather_prepare<VB, PB, U, true>(a, t0, ntiles, m, r0, s_pref, s_wtot, s_vals, tid, pf);
 
+    if constexpr (WIDEN) {
+        // staged indices [0, count + 16) cover the run and its <= 15-element phase
+        const int64_t cnt = (int64_t)s_pref[ntiles] - (int64_t)s_pref[0];
+        const int n_conv = (int)min<int64_t>(max<int64_t>(cnt, 0), (int64_t)ntiles * kTileNumel) + 16;
+        for (int i = tid; i < n_conv; i += kThreads)
+            s_rv[i] = (uint16_t)(__float_as_uint(val_f32<V_T>(lds_val<V_T, PB>(s_vals, (uint32_t)i, bitbase))) >> 16);
+        __syncthreads();
+    }
     float sb = 1.0f;
     if constexpr (HAS_SCALE) sb = bf16_to_f32(f32_to_bf16(*a.scale));
+    const uint32_t zero_x = HAS_SCALE ? f32_to_bf16(0.0f * sb) : 0u;
     const float k2 = 2.0f * a.relu2_scale;
 #pragma unroll
     for (int j = 0; j < U; j++) {
@@ -1199,12 +1252,13 @@ __global__ __launch_bounds__(kThreads) void relu2_grad_kernel(GatherArgs a)
             const uint32_t mm = m[j][h];
 #pragma unroll
             for (int e = 0; e < 8; e++) {
-                uint32_t x = 0;
+                uint32_t x = zero_x;
                 if ((mm >> e) & 1u) {
-                    float rv = val_f32<V_T>(lds_val<V_T, PB>(s_vals, r++, bitbase));
+                    const float rv = WIDEN ? bf16_to_f32(s_rv[r]) : val_f32<V_T>(lds_val<V_T, PB>(s_vals, r, bitbase));
                     x = f32_to_bf16(bf16_to_f32(get16(g[j][h], e)) * (k2 * rv));
+                    if constexpr (HAS_SCALE) x = f32_to_bf16(bf16_to_f32(x) * sb);
                 }
-                if constexpr (HAS_SCALE) x = f32_to_bf16(bf16_to_f32(x) * sb);
+                r += (mm >> e) & 1u;
                 set_elem<2>(ov, e, x);
             }
             int64_t row, col0;
