@@ -18,6 +18,8 @@ Also reported on the same line:
                 columns)
   stack         configs[4] 12 GPT-2-small blocks: peak activation memory and
                 fwd+bwd time, compressed vs dense storage
+  aux_kernels   the gradient, ReLU^2 unpack and fp8 kernels, each against its
+                algorithmic bytes
   cpu_baseline  the C oracle (single thread) on a bounded row sample of the
                 same workload, same unit
 
@@ -134,6 +136,84 @@ def _timed(fn, steps: int, warmup: int) -> float:
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / steps
+
+
+def bench_kernels(steps: int, warmup: int, copy_gbs: float):
+    """The other kernels of the path, each timed alone (HIP events over
+    back-to-back launches) against its algorithmic bytes: the mask and ReLU^2
+    gradients and the ReLU^2 unpack at configs[2] (bf16, 50% zeros) and at the
+    configs[3] activation shape (4096x16384, e4m3fn storage, 90% zeros), and
+    the fp8 amax / quantize passes.  The in-place gradient kernels are timed
+    on the same buffer launch after launch (their cost does not depend on the
+    gradient values)."""
+    import torch
+    from bitsparse_amd.bitsparse import TensorBuffer
+    from bitsparse_amd.src import hip_operators as H
+    from bitsparse_amd.src.functions import dense_to_tilesparse, quantize_and_compress
+
+    dev = torch.device("cuda", 0)
+    out = {}
+
+    def rec(name, shape, ms, nbytes):
+        gbs = nbytes / (ms * 1e6)
+        out[name] = {"shape": shape, "ms": round(ms, 5), "algorithmic_bytes": int(nbytes),
+                     "gbs": round(gbs, 1), "frac_of_8tbs": round(gbs / HBM_PEAK_GBS, 4),
+                     "frac_of_copy": round(gbs / copy_gbs, 4)}
+
+    def mask_stats(sp):
+        bm = sp.bitmask
+        return int((bm == 0).sum().item()), int((bm == 255).sum().item())
+
+    for (M, N, mu, tag) in [(16384, 16384, 0.0, "configs[2] bf16 50%"),
+                            (4096, 16384, -1.2816, "configs[3] shape 90%")]:
+        T = ((M + 63) // 64) * ((N + 63) // 64)
+        meta = M * N // 8 + 4 * (T + 1)
+        r = make_activation(M, N, mu, dev)
+        g = torch.randn((M, N), device=dev, generator=torch.Generator(device=dev).manual_seed(1)).to(torch.bfloat16)
+        o = torch.empty_like(r)
+        if tag.startswith("configs[2]"):
+            sp = dense_to_tilesparse(r, None)
+            nnz = int(sp.prefix[-1].item())
+            zero_b, full_b = mask_stats(sp)
+            # relu_grad: all-dropped bytes write 16 B, all-kept bytes nothing, others read + write
+            mixed = M * N // 8 - zero_b - full_b
+            rec(f"relu_grad {tag}", [M, N],
+                _timed(lambda: H.mask_with_bitmask_(g, sp), steps, warmup),
+                M * N // 8 + 16 * zero_b + 32 * mixed)
+            rec(f"relu2_grad bf16 {tag}", [M, N],
+                _timed(lambda: H.relu2_grad_sparse_(g, sp), steps, warmup),
+                meta + 2 * nnz + 16 * (M * N // 8) + 16 * (M * N // 8 - zero_b))
+            rec(f"unpack_relu2 bf16 {tag}", [M, N],
+                _timed(lambda: H.unpack_relu2_batch_(sp, o, 0, sp.grid_n, N, M, T), steps, warmup),
+                meta + 2 * nnz + 2 * M * N)
+            ep = H.amax_into_workspace(r)
+            rec(f"amax {tag}", [M, N], _timed(lambda: H.amax_into_workspace(r), steps, warmup), 2 * M * N)
+            rec(f"quantize_e4m3fn {tag}", [M, N],
+                _timed(lambda: H.quantize_e4m3fn(r, ep), steps, warmup), 3 * M * N)
+            qbuf = TensorBuffer(M * N, device=dev, dtype=torch.float8_e4m3fn)
+
+            def qc():
+                qbuf.reset_buffer()
+                return quantize_and_compress(r, qbuf)
+            nq = int(qc()[2].prefix[-1].item())
+            # amax reads h; the fused pass reads h and writes the e4m3fn copy,
+            # bitmask, prefix and values
+            rec(f"quantize_and_compress into a TensorBuffer {tag}", [M, N],
+                _timed(qc, steps, warmup), 2 * M * N + 2 * M * N + M * N + meta + nq)
+            del qbuf
+        else:
+            _, _, spq = quantize_and_compress(r, None)
+            nnz = int(spq.prefix[-1].item())
+            zero_b, _ = mask_stats(spq)
+            rec(f"relu2_grad e4m3fn scaled {tag}", [M, N],
+                _timed(lambda: H.relu2_grad_sparse_(g, spq), steps, warmup),
+                meta + nnz + 16 * (M * N // 8) + 16 * (M * N // 8 - zero_b))
+            rec(f"unpack_relu2 e4m3fn scaled {tag}", [M, N],
+                _timed(lambda: H.unpack_relu2_batch_(spq, o, 0, spq.grid_n, N, M, T), steps, warmup),
+                meta + nnz + 2 * M * N)
+        del r, g, o
+        torch.cuda.empty_cache()
+    return out
 
 
 MFMA_BF16_PEAK_TFLOPS = 2500.0
@@ -542,6 +622,9 @@ def main() -> int:
                     help="skip the GEMM, configs[3] MLP, sparsity sweep and 12-block stack sections")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a 1 GiB device copy (reference for rocprof byte counters)")
+    ap.add_argument("--kernels-only", action="store_true",
+                    help="run only the gradient / unpack / fp8 kernel section and print its JSON "
+                         "(profiling entry point)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -559,6 +642,18 @@ def main() -> int:
 
     if args.gemm_only:
         print(json.dumps({"gemm": bench_gemm(args.steps, args.warmup)}), flush=True)
+        return 0
+    if args.kernels_only:
+        copy_gbs = measure_copy_gbs()
+        if args.calibrate_copy:
+            src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+            dst = torch.empty_like(src)
+            for _ in range(3):
+                dst.copy_(src)
+            torch.cuda.synchronize()
+            del src, dst
+        print(json.dumps({"aux_kernels": bench_kernels(args.steps, args.warmup, copy_gbs),
+                          "achievable_copy_gbs": round(copy_gbs, 2)}), flush=True)
         return 0
 
     M = N = 16384
@@ -579,7 +674,7 @@ def main() -> int:
         log("mlp: configs[1] GPT-2-small block")
         mlp = bench_mlp(max(5, args.steps // 2), max(2, args.warmup // 2))
         log("mlp done")
-    gemm = mlp_c4 = sweep = stack = None
+    gemm = mlp_c4 = sweep = stack = aux = None
     if not args.skip_extras:
         log("gemm: reconstruct-into-LDS dW GEMM")
         gemm = bench_gemm(max(5, args.steps // 2), 3)
@@ -589,6 +684,8 @@ def main() -> int:
         sweep = bench_sweep(10, 3)
         log("stack: configs[4] 12 blocks")
         stack = bench_stack(3, 2)
+        log("aux kernels: gradients, ReLU^2 unpack, fp8")
+        aux = bench_kernels(10, 3, copy_gbs)
         log("extras done")
     cpu = None
     cpu_mlp = None
@@ -649,6 +746,7 @@ def main() -> int:
         "mlp_c4": mlp_c4,
         "sweep": sweep,
         "stack": stack,
+        "aux_kernels": aux,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
