@@ -40,13 +40,12 @@ __device__ __forceinline__ uint32_t pos8(uint32_t b)
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float bf16_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
 
-// fp32 -> bf16 bits, round to nearest even, NaN kept quiet.
+// fp32 -> bf16 bits, round to nearest even, NaN kept quiet: the hardware
+// conversion (v_cvt_pk_bf16_f32), one instruction where the integer form
+// (NaN test, add 0x7fff + lsb, shift) takes five.
 __device__ __forceinline__ uint32_t f32_to_bf16(float f)
 {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return u >> 16;
+    return __builtin_bit_cast(uint16_t, (__bf16)f);
 }
 
 // e4m3fn bits -> fp32 (exact). 0x7f / 0xff are NaN.

@@ -113,12 +113,6 @@ struct GemmArgs {
     uint32_t ksteps_per_split;
 };
 
-// fp32 -> bf16 bits with the hardware conversion (round to nearest even).
-__device__ __forceinline__ uint32_t hw_bf16(float f)
-{
-    return __builtin_bit_cast(uint16_t, (__bf16)f);
-}
-
 // B element after the transform, as bf16 bits.
 template <int V_T, bool SQUARE, bool HAS_SCALE>
 __device__ __forceinline__ uint32_t b_elem(uint32_t raw, float k, float s2b)
@@ -127,13 +121,13 @@ __device__ __forceinline__ uint32_t b_elem(uint32_t raw, float k, float s2b)
     if constexpr (SQUARE) {
         if constexpr (V_T == DT_BF16) {
             const float v = bf16_to_f32(raw);
-            x = hw_bf16(bf16_to_f32(hw_bf16(k * v)) * v);
+            x = f32_to_bf16(bf16_to_f32(f32_to_bf16(k * v)) * v);
         } else {
             const float v = V_T == DT_E4M3FN ? __builtin_amdgcn_cvt_f32_fp8(raw, 0)
                                              : __builtin_amdgcn_cvt_f32_bf8(raw, 0);
-            x = hw_bf16((k * v) * v);
+            x = f32_to_bf16((k * v) * v);
         }
-        if constexpr (HAS_SCALE) x = hw_bf16(bf16_to_f32(x) * s2b);
+        if constexpr (HAS_SCALE) x = f32_to_bf16(bf16_to_f32(x) * s2b);
     } else {
         x = raw;   // bf16 storage only
     }
@@ -705,7 +699,7 @@ __global__ __launch_bounds__(CFG::THREADS, 1) void gemm_cb_kernel(GemmArgs a)
                     }
                 } else {
                     uint16_t* dst = a.C + row * a.N + c4;
-                    const uint32_t b0 = hw_bf16(v.x), b1 = hw_bf16(v.y), b2 = hw_bf16(v.z), b3 = hw_bf16(v.w);
+                    const uint32_t b0 = f32_to_bf16(v.x), b1 = f32_to_bf16(v.y), b2 = f32_to_bf16(v.z), b3 = f32_to_bf16(v.w);
                     if (cvec) {
                         *reinterpret_cast<uint2*>(dst) = uint2{b0 | (b1 << 16), b2 | (b3 << 16)};
                     } else {

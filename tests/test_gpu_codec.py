@@ -276,6 +276,42 @@ def test_relu2_grad_and_square_fp8_scaled(dev, shape):
     assert (bits(sq) == ref).all()
 
 
+def test_relu2_paths_every_bit_pattern(dev):
+    """relu2_grad and the ReLU^2 unpack over every stored value and every
+    gradient bit pattern: bf16 r and g each a permutation of all 65536
+    patterns (r's positives, +Inf included, are the stored values; g's NaN
+    payloads, denormals, infinities and zeros all meet every kind of r), and
+    e4m3fn storage with every fp8 pattern and a scale.  Bit-exact against the
+    oracle, so every rounding inside the kernels (products to bf16 with RNE,
+    NaN kept quiet) is pinned on all the inputs they can receive."""
+    F, H, TB = _bs()
+    rng = np.random.default_rng(70)
+    shape = (256, 256)
+    rb = rng.permutation(np.arange(65536, dtype=np.uint32)).astype(np.uint16).reshape(shape)
+    gb = rng.permutation(np.arange(65536, dtype=np.uint32)).astype(np.uint16).reshape(shape)
+    r, g = from_bits(rb, torch.bfloat16), from_bits(gb, torch.bfloat16)
+    sp = F.dense_to_tilesparse(r.to(dev), None)
+    bm, pf, v = O.compress(rb, O.BF16)
+    out = H.relu2_grad_sparse_(g.to(dev), sp)
+    assert (bits(out) == O.relu2_grad(gb, v, O.BF16, bm, pf)).all(), "relu2_grad bf16"
+    sq = torch.empty(shape, dtype=torch.bfloat16, device=dev)
+    H.unpack_relu2_batch_(sp, sq, 0, sp.grid_n, shape[1], shape[0], sp.grid_m * sp.grid_n)
+    assert (bits(sq) == O.decompress(v, O.BF16, bm, pf, *shape, square=True)).all(), "unpack_relu2 bf16"
+
+    xb = all_fp8_patterns(shape, seed=71)
+    x = from_bits(xb, torch.float8_e4m3fn)
+    for s in (0.0123, 3.0e4):
+        st = torch.tensor(s, device=dev)
+        spq = F.dense_to_tilesparse(x.to(dev), st)
+        bmq, pfq, vq = O.compress(xb, O.E4M3FN)
+        outq = H.relu2_grad_sparse_(g.to(dev), spq)
+        assert (bits(outq) == O.relu2_grad(gb, vq, O.E4M3FN, bmq, pfq, scale=s)).all(), f"relu2_grad e4m3fn s={s}"
+        H.unpack_relu2_batch_(spq, sq, 0, spq.grid_n, shape[1], shape[0], spq.grid_m * spq.grid_n)
+        ref = O.decompress(vq, O.E4M3FN, bmq, pfq, *shape, square=True)
+        ref = O.bf16_mul_scalar_tensor(ref, float(np.float32(s) * np.float32(s)))
+        assert (bits(sq) == ref).all(), f"unpack_relu2 e4m3fn s={s}"
+
+
 def test_unpack_relu2_bf16(dev):
     F, H, _ = _bs()
     r = relu_input((129, 131), 0.5, seed=54)
