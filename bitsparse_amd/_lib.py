@@ -17,7 +17,7 @@ LIB_NAME = "libbitsparse_hip.so"
 # BITSPARSE_HIP_LIB points at another build of the same sources (tuning sweeps)
 LIB_PATH = os.environ.get("BITSPARSE_HIP_LIB") or os.path.join(
     os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 BS_OK = 0
 BS_ERR_INVALID = 1
@@ -60,6 +60,8 @@ _SIGNATURES = {
     "bs_relu2_grad_packed": [_vp, _i64, _i64, _vp, _int, _i64, _vp, _vp, _vp, _f32, _vp, _vp],
     "bs_workspace_amax_slot": [_vp, _i64],
     "bs_workspace_fallback_counter": [_vp, _i64],
+    "bs_launch_timing": [_int],
+    "bs_launch_timing_read": [_vp, _vp, _int, _vp],
 }
 _RESTYPES = {
     "bs_last_error": ctypes.c_char_p,
@@ -71,6 +73,40 @@ _RESTYPES = {
 
 _lib = None
 _lock = threading.Lock()
+
+
+class LaunchTimer:
+    """Kernel durations of this thread's compress / decompress launches,
+    recorded by the library at each kernel's own start and end
+    (``bs_launch_timing``), so launch gaps between kernels are not counted.
+
+        with LaunchTimer() as t:
+            ... compress / decompress calls ...
+        t.times("compress")   # ms per launch, in launch order
+
+    Leaving the block waits for the recorded kernels."""
+    KINDS = {0: "compress", 1: "decompress"}
+    MAX_LAUNCHES = 1 << 16
+
+    def __enter__(self):
+        check(load().bs_launch_timing(1), "bs_launch_timing")
+        self.records = []
+        return self
+
+    def __exit__(self, *exc):
+        L = load()
+        ms = (ctypes.c_float * self.MAX_LAUNCHES)()
+        kinds = (ctypes.c_int * self.MAX_LAUNCHES)()
+        n = ctypes.c_int(0)
+        rc = L.bs_launch_timing_read(ms, kinds, self.MAX_LAUNCHES, ctypes.byref(n))
+        check(L.bs_launch_timing(0), "bs_launch_timing")
+        check(rc, "bs_launch_timing_read")
+        self.records = [(self.KINDS.get(kinds[i], str(kinds[i])), ms[i])
+                        for i in range(min(n.value, self.MAX_LAUNCHES))]
+        return False
+
+    def times(self, kind: str) -> list:
+        return [t for k, t in self.records if k == kind]
 
 
 class BitsparseHipError(RuntimeError):

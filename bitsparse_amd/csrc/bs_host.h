@@ -2,6 +2,8 @@
 // workspace layout shared by the compress and fp8 entry points.
 #pragma once
 
+#include <hip/hip_ext.h>
+#include <hip/hip_runtime.h>
 #include <stdint.h>
 
 #include "bitsparse_hip.h"
@@ -22,6 +24,24 @@ constexpr int64_t kWsFallbackOffset = 8;
 // 2^31 + 2^21 elements faulted without a cause found in this code, so shapes
 // from 2^31 elements up are refused until such a run passes.
 constexpr uint64_t kMaxElems = 1ull << 31;
+
+// Launch timing (bs_launch_timing): the next start/stop event pair for a
+// kernel launch of the given kind (0 compress, 1 decompress), or false when
+// timing is off on this thread.
+bool timing_next(int kind, hipEvent_t* start, hipEvent_t* stop);
+
+// hipLaunchKernelGGL, or hipExtLaunchKernelGGL with a timing event pair while
+// launch timing is on.
+template <typename F, typename... Args>
+inline void launch_timed(int kind, F kernel, dim3 grid, dim3 block, uint32_t shmem, hipStream_t st,
+                         Args... args)
+{
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (timing_next(kind, &e0, &e1))
+        hipExtLaunchKernelGGL(kernel, grid, block, shmem, st, e0, e1, 0u, args...);
+    else
+        hipLaunchKernelGGL(kernel, grid, block, shmem, st, args...);
+}
 
 // Records a formatted message for bs_last_error() and returns `code`.
 int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));

@@ -1337,11 +1337,11 @@ static hipError_t launch_compress_mode(const CompressArgs& a, bool vec, hipStrea
 {
     const uint32_t units = (a.tend - a.tile0 + kStreamU - 1) / kStreamU;
     if (vec)
-        hipLaunchKernelGGL((compress_stream_kernel<IN_T, QUANT, true, MODE, kStreamU>), dim3(units),
-                           dim3(64 * kStreamU), 0, st, a);
+        launch_timed(0, compress_stream_kernel<IN_T, QUANT, true, MODE, kStreamU>, dim3(units),
+                     dim3(64 * kStreamU), 0, st, a);
     else
-        hipLaunchKernelGGL((compress_stream_kernel<IN_T, QUANT, false, MODE, kStreamU>), dim3(units),
-                           dim3(64 * kStreamU), 0, st, a);
+        launch_timed(0, compress_stream_kernel<IN_T, QUANT, false, MODE, kStreamU>, dim3(units),
+                     dim3(64 * kStreamU), 0, st, a);
     return hipGetLastError();
 }
 
@@ -1597,9 +1597,9 @@ static void launch_decompress_t(const GatherArgs& a, bool vec, hipStream_t st)
 {
     const uint32_t blocks = (a.num_tiles + kGatherU - 1) / kGatherU;
     if (vec)
-        hipLaunchKernelGGL((decompress_kernel<V_T, SQ, SC, true, kGatherU, PK>), dim3(blocks), dim3(kThreads), 0, st, a);
+        launch_timed(1, decompress_kernel<V_T, SQ, SC, true, kGatherU, PK>, dim3(blocks), dim3(kThreads), 0, st, a);
     else
-        hipLaunchKernelGGL((decompress_kernel<V_T, SQ, SC, false, kGatherU, PK>), dim3(blocks), dim3(kThreads), 0, st, a);
+        launch_timed(1, decompress_kernel<V_T, SQ, SC, false, kGatherU, PK>, dim3(blocks), dim3(kThreads), 0, st, a);
 }
 
 template <int V_T, bool PK>

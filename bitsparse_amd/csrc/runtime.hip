@@ -1,7 +1,9 @@
-// Error reporting and version entry points of libbitsparse_hip.so.
+// Error reporting, version and launch-timing entry points of libbitsparse_hip.so.
 #include <hip/hip_runtime.h>
 #include <stdarg.h>
 #include <stdio.h>
+
+#include <vector>
 
 #include "bs_host.h"
 
@@ -20,8 +22,74 @@ int set_error(int code, const char* fmt, ...)
 
 void clear_error() { g_err[0] = '\0'; }
 
+// Launch timing (per thread): while enabled, every compress / decompress
+// kernel launch takes the next pair of events from a pool that grows as
+// needed; hipExtLaunchKernel records them at the kernel's start and end.
+namespace {
+struct TimedLaunch {
+    hipEvent_t start, stop;
+    int kind;
+};
+struct LaunchTiming {
+    bool on = false;
+    size_t used = 0;
+    std::vector<TimedLaunch> pool;
+};
+thread_local LaunchTiming g_timing;
+}  // namespace
+
+bool timing_next(int kind, hipEvent_t* start, hipEvent_t* stop)
+{
+    LaunchTiming& t = g_timing;
+    if (!t.on) return false;
+    if (t.used == t.pool.size()) {
+        TimedLaunch l{nullptr, nullptr, 0};
+        if (hipEventCreate(&l.start) != hipSuccess) return false;
+        if (hipEventCreate(&l.stop) != hipSuccess) {
+            (void)hipEventDestroy(l.start);
+            return false;
+        }
+        t.pool.push_back(l);
+    }
+    TimedLaunch& l = t.pool[t.used++];
+    l.kind = kind;
+    *start = l.start;
+    *stop = l.stop;
+    return true;
+}
+
 }  // namespace bs
+
+using namespace bs;
 
 extern "C" const char* bs_last_error(void) { return bs::g_err; }
 
-extern "C" int bs_abi_version(void) { return 3; }
+extern "C" int bs_abi_version(void) { return 4; }
+
+extern "C" int bs_launch_timing(int enable)
+{
+    clear_error();
+    g_timing.on = enable != 0;
+    g_timing.used = 0;
+    return BS_OK;
+}
+
+extern "C" int bs_launch_timing_read(float* ms_out, int* kinds_out, int max_n, int* n_out)
+{
+    clear_error();
+    if (n_out == nullptr) return set_error(BS_ERR_INVALID, "bs_launch_timing_read: null n_out");
+    const int n = (int)g_timing.used;
+    *n_out = n;
+    for (int i = 0; i < n && i < max_n; i++) {
+        const TimedLaunch& l = g_timing.pool[i];
+        hipError_t e = hipEventSynchronize(l.stop);
+        float ms = 0.0f;
+        if (e == hipSuccess) e = hipEventElapsedTime(&ms, l.start, l.stop);
+        if (e != hipSuccess)
+            return set_error(BS_ERR_HIP, "bs_launch_timing_read: %s", hipGetErrorString(e));
+        if (ms_out) ms_out[i] = ms;
+        if (kinds_out) kinds_out[i] = l.kind;
+    }
+    g_timing.used = 0;
+    return BS_OK;
+}

@@ -51,6 +51,22 @@ const char* bs_last_error(void);
 int bs_abi_version(void);
 
 /*
+ * Launch timing (no counterpart in the reference: a measurement hook for
+ * benchmarks and profilers that need a kernel's own duration on its stream).
+ * bs_launch_timing(1) makes every later compress / decompress kernel launch of
+ * the calling thread record a pair of library-owned HIP events at the start
+ * and end of the kernel itself (hipExtLaunchKernel), so launch gaps between
+ * kernels are not counted; bs_launch_timing(0) stops it.  Either call forgets
+ * the launches recorded so far.
+ * bs_launch_timing_read waits for the recorded launches, writes up to max_n
+ * durations (ms) and kinds (0 compress, 1 decompress) in launch order, sets
+ * *n_out to the number recorded, and forgets them.  Events are created (not
+ * device memory) the first time a pool slot is used and kept by the thread.
+ */
+int bs_launch_timing(int enable);
+int bs_launch_timing_read(float* ms_out, int* kinds_out, int max_n, int* n_out);
+
+/*
  * Workspace for the single-pass compress (bs_compress) and the fp8 amax
  * (bs_amax): a status word per compress unit plus an amax slot.  It must be
  * zero-filled once before first use; afterwards every call passes an `epoch`
