@@ -393,10 +393,11 @@ __device__ uint32_t wave_lookback_grouped(const CompressArgs& a, uint32_t u, uin
 // 64k + l (k < 8) of its tile: rows 8k + l/8, columns 8(l%8)..+7, so every
 // load instruction covers 8 whole tile rows and the tile's value run is
 // produced in eight in-order rounds of 64 chunks.  The loaded chunks stay in
-// registers while wave 0 runs the look-back; afterwards each wave streams its
-// run through a private LDS ring:
-//   * a chunk is compacted in registers (v_perm with selectors from a
-//     256-entry table indexed by the mask byte) and its 8 elements are written
+// registers while wave 0 runs the look-back, and are compacted there in the
+// meantime (v_perm with selectors from a 256-entry table indexed by the mask
+// byte: the set elements move to the front; this needs no prefix).  After
+// the look-back each wave streams its run through a private LDS ring:
+//   * a compacted chunk's 8 elements are written
 //     at the chunk's run position in descending element order: the elements
 //     past the chunk's count land on the positions of the following chunks,
 //     which later (lower-index) writes of those chunks overwrite, so no
@@ -597,19 +598,49 @@ void compress_stream_kernel(CompressArgs a)
             __syncthreads();
         }
 
-        // ---- unit total, aggregate, look-back, prefix entries (wave 0)
+        // ---- unit total and aggregate (wave 0)
+        uint32_t v = 0, x = 0, unit_total = 0;
         if (MODE != MODE_VALS && wave == 0) {
-            const uint32_t v = lane < U ? s_cnt[lane] : 0u;
-            uint32_t x = v;
+            v = lane < U ? s_cnt[lane] : 0u;
+            x = v;
 #pragma unroll
             for (int off = 1; off < U; off <<= 1) {
                 const uint32_t y = __shfl_up(x, off, 64);
                 if (lane >= off) x += y;
             }
-            const uint32_t unit_total = __shfl(x, U - 1, 64);
+            unit_total = __shfl(x, U - 1, 64);
             if (lane < U) s_toff[lane] = x - v;
             if (lane == 0)
                 st_relaxed(&a.status[u], pack_status(a.epoch, u == 0 ? kFlagInc : kFlagAgg, unit_total));
+        }
+        // ---- compaction of every chunk in registers, which needs no prefix:
+        // the mask byte indexes a table of v_perm selectors that move the set
+        // elements to the front.  Waves 1.. do it while wave 0 waits in the
+        // look-back; o[k] is replaced by its compacted form.
+        if constexpr (WRITE_VALS) {
+            if (tile_ok) {
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    const uint32_t m = (mp[k >> 2] >> (8 * (k & 3))) & 0xffu;
+                    if constexpr (OUTB == 2) {
+                        const uint4 s0 = *reinterpret_cast<const uint4*>(&s_sel[m * NSEL]);
+                        const uint4 s1 = *reinterpret_cast<const uint4*>(&s_sel[m * NSEL + 4]);
+                        const uint4 w = o[k];
+                        o[k].x = __builtin_amdgcn_perm(w.y, w.x, s0.x) | __builtin_amdgcn_perm(w.w, w.z, s1.x);
+                        o[k].y = __builtin_amdgcn_perm(w.y, w.x, s0.y) | __builtin_amdgcn_perm(w.w, w.z, s1.y);
+                        o[k].z = __builtin_amdgcn_perm(w.y, w.x, s0.z) | __builtin_amdgcn_perm(w.w, w.z, s1.z);
+                        o[k].w = __builtin_amdgcn_perm(w.y, w.x, s0.w) | __builtin_amdgcn_perm(w.w, w.z, s1.w);
+                    } else {
+                        const uint2 s0 = *reinterpret_cast<const uint2*>(&s_sel[m * NSEL]);
+                        const uint2 w = o[k];
+                        o[k].x = __builtin_amdgcn_perm(w.y, w.x, s0.x);
+                        o[k].y = __builtin_amdgcn_perm(w.y, w.x, s0.y);
+                    }
+                }
+            }
+        }
+        // ---- look-back, prefix entries (wave 0)
+        if (MODE != MODE_VALS && wave == 0) {
             uint32_t excl = 0;
             if (u != 0) {
                 excl = wave_lookback_grouped<IN_T, QUANT, VEC, U>(a, u, unit_total, scale, lane);
@@ -670,22 +701,7 @@ void compress_stream_kernel(CompressArgs a)
                         const uint32_t c = (uint32_t)__popc(m);
                         const uint32_t ex = wave_incl_scan(c) - c;
                         const int rb = a0 + (int)P[k] - pend * EPS;       // ring index of the round's first element
-                        RawOut cv;
-                        if constexpr (OUTB == 2) {
-                            const uint4 s0 = *reinterpret_cast<const uint4*>(&s_sel[m * NSEL]);
-                            const uint4 s1 = *reinterpret_cast<const uint4*>(&s_sel[m * NSEL + 4]);
-                            const uint4 v = o[k];
-                            cv.x = __builtin_amdgcn_perm(v.y, v.x, s0.x) | __builtin_amdgcn_perm(v.w, v.z, s1.x);
-                            cv.y = __builtin_amdgcn_perm(v.y, v.x, s0.y) | __builtin_amdgcn_perm(v.w, v.z, s1.y);
-                            cv.z = __builtin_amdgcn_perm(v.y, v.x, s0.z) | __builtin_amdgcn_perm(v.w, v.z, s1.z);
-                            cv.w = __builtin_amdgcn_perm(v.y, v.x, s0.w) | __builtin_amdgcn_perm(v.w, v.z, s1.w);
-                        } else {
-                            const uint2 s0 = *reinterpret_cast<const uint2*>(&s_sel[m * NSEL]);
-                            const uint2 v = o[k];
-                            cv.x = __builtin_amdgcn_perm(v.y, v.x, s0.x);
-                            cv.y = __builtin_amdgcn_perm(v.y, v.x, s0.y);
-                        }
-                        if (c != 0u) write_compacted<OUTB>(ring + (rb + (int)ex) * OUTB, cv);
+                        if (c != 0u) write_compacted<OUTB>(ring + (rb + (int)ex) * OUTB, o[k]);
                     }
                     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
                     __builtin_amdgcn_wave_barrier();
