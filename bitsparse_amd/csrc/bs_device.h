@@ -119,32 +119,27 @@ __device__ __forceinline__ uint32_t div_to_e4m3(float x, float s, float r)
     return f32_to_e4m3(x / s);
 }
 
-// The approximate quotient q (within 2 ulp of the correctly rounded one,
-// see div_to_e4m3) converts to the correctly rounded quotient's e4m3 code
-// when q lies in e4m3's normal range (biased fp32 exponent 121..135, i.e.
-// 2^-6 <= |q| < 512, which also covers the NaN threshold at 464) and no
-// rounding tie of that range (the 20 dropped mantissa bits equal to
-// 0x80000) is within 2 ulp of q.
-__device__ __forceinline__ bool e4m3_quotient_safe(uint32_t qb)
+// The plain product y = x * r (r = 1/s rounded, one more rounding in the
+// product: |y - x/s| <= 2^-23 |x/s|) lies within 3 ulp of the correctly
+// rounded quotient (itself within 2^-24 |x/s|), so y converts to the
+// quotient's e4m3 code when y is in e4m3's normal range and no rounding tie
+// is within 3 ulp of it.
+__device__ __forceinline__ bool e4m3_product_safe(uint32_t yb)
 {
-    return ((((qb >> 23) & 0xffu) - 121u) <= 14u) && (((qb & 0xfffffu) - 0x7fffeu) > 4u);
+    return ((((yb >> 23) & 0xffu) - 121u) <= 14u) && (((yb & 0xfffffu) - 0x7fffdu) > 6u);
 }
 
-// f32_to_e4m3(x0 / s) | f32_to_e4m3(x1 / s) << 8 with r = 1/s: one packed
-// hardware conversion for the pair; zeros keep x's sign; anything outside
-// the safe region takes the exact division.
+// f32_to_e4m3(x0 / s) | f32_to_e4m3(x1 / s) << 8 for a scale s > 0 (or NaN)
+// with r = 1/s: one packed hardware conversion of the two products; x = +-0
+// converts as +-0 (= x/s for every such s that is not NaN); anything else
+// outside the safe region takes the exact division.
 __device__ __forceinline__ uint32_t div2_to_e4m3(float x0, float x1, float s, float r)
 {
     const float y0 = x0 * r, y1 = x1 * r;
-    const float q0 = __builtin_fmaf(__builtin_fmaf(-y0, s, x0), r, y0);
-    const float q1 = __builtin_fmaf(__builtin_fmaf(-y1, s, x1), r, y1);
-    uint32_t out = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q0, q1, 0, false) & 0xffffu;
-    const uint32_t xb0 = __float_as_uint(x0), xb1 = __float_as_uint(x1);
-    const bool z0 = (xb0 & 0x7fffffffu) == 0u && s == s, z1 = (xb1 & 0x7fffffffu) == 0u && s == s;
-    if (z0) out = (out & 0xff00u) | ((xb0 >> 24) & 0x80u);
-    if (z1) out = (out & 0x00ffu) | ((xb1 >> 16) & 0x8000u);
-    const bool ok0 = z0 || e4m3_quotient_safe(__float_as_uint(q0));
-    const bool ok1 = z1 || e4m3_quotient_safe(__float_as_uint(q1));
+    uint32_t out = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(y0, y1, 0, false) & 0xffffu;
+    const bool s_ok = s == s;
+    const bool ok0 = e4m3_product_safe(__float_as_uint(y0)) || ((__float_as_uint(x0) << 1) == 0u && s_ok);
+    const bool ok1 = e4m3_product_safe(__float_as_uint(y1)) || ((__float_as_uint(x1) << 1) == 0u && s_ok);
     if (!ok0) out = (out & 0xff00u) | f32_to_e4m3(x0 / s);
     if (!ok1) out = (out & 0x00ffu) | (f32_to_e4m3(x1 / s) << 8);
     return out;

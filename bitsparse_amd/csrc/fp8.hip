@@ -3,7 +3,7 @@
 //
 // scale = max(fp32(amax|x|) / 448, 1e-9); q = e4m3fn_RNE(fp32(x) / scale)
 // with one correctly rounded fp32 division per element (computed as a
-// reciprocal product with an FMA correction, exact division near ties).
+// reciprocal product converted in hardware, exact division near ties).
 #include "bs_device.h"
 #include "bs_host.h"
 
