@@ -399,6 +399,27 @@ def test_to_fp8_all_bf16_patterns(dev, amax):
     assert (bits(q) == qo).all()
 
 
+def test_to_fp8_and_quantizing_compress_inf_input(dev):
+    """An infinite input makes amax and the scale infinite (1/s = 0): finite
+    values, +-0 included, quantize to zeros of their sign and the infinities
+    to NaN, in to_fp8 and in the fused quantizing compress alike."""
+    from bitsparse_amd.fp8 import to_fp8
+    from bitsparse_amd.src.functions import quantize_and_compress
+    x = special_bf16((129, 131), seed=73)
+    xb = bits(x).copy()
+    xb[(xb & 0x7fff) > 0x7f80] = 0x3f80          # no NaN: the scale must be +Inf
+    xb.reshape(-1)[[5, 77, 900]] = [0x7f80, 0xff80, 0x8000]
+    x = from_bits(xb, torch.bfloat16)
+    q, s = to_fp8(x.to(dev))
+    qo, so = O.to_fp8(xb)
+    assert float(s.item()) == float("inf") and so == float("inf")
+    assert (bits(q) == qo).all()
+    q2, s2, sp = quantize_and_compress(x.to(dev), None)
+    assert (bits(q2) == qo).all() and float(s2.item()) == float("inf")
+    bm, pf, v = O.compress(qo, O.E4M3FN)
+    assert (bits(sp.bitmask) == bm).all() and (bits(sp.prefix) == pf).all()
+
+
 def test_to_fp8_nan_input(dev):
     from bitsparse_amd.fp8 import to_fp8
     x = preact_input((64, 64), seed=72)
