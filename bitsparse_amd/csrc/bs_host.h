@@ -43,6 +43,12 @@ inline void launch_timed(int kind, F kernel, dim3 grid, dim3 block, uint32_t shm
         hipLaunchKernelGGL(kernel, grid, block, shmem, st, args...);
 }
 
+// BS_ERR_INVALID when `stream` is capturing into a HIP graph.  Entry points
+// whose device state is tagged with a host-chosen epoch (the compress
+// look-back's status words, the fp8 amax slot) call it: a graph would replay
+// the same epoch and take the previous replay's values for current ones.
+int refuse_capture(hipStream_t stream, const char* what);
+
 // Records a formatted message for bs_last_error() and returns `code`.
 int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 void clear_error();

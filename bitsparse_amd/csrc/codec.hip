@@ -1439,6 +1439,7 @@ static int compress_impl(const void* dense, int in_dtype, int64_t M, int64_t N, 
         return set_error(BS_ERR_INVALID, "bs_compress: vals_offset_out aliases vals_offset_in");
     if (epoch == 0 || epoch >= (1u << 30))
         return set_error(BS_ERR_INVALID, "bs_compress: epoch must be in [1, 2^30)");
+    if (int rc = refuse_capture((hipStream_t)stream, "bs_compress")) return rc;
     if (workspace == nullptr || workspace_bytes < bs_compress_workspace_bytes(M, N))
         return set_error(BS_ERR_INVALID, "bs_compress: workspace too small (%lld < %lld bytes)",
                          (long long)workspace_bytes, (long long)bs_compress_workspace_bytes(M, N));

@@ -128,6 +128,7 @@ static int amax_impl(const void* x, int64_t n, void* workspace, int64_t workspac
     if (epoch == 0 || epoch >= (1u << 30)) return set_error(BS_ERR_INVALID, "bs_amax: epoch out of range");
     if (n > 0 && x == nullptr) return set_error(BS_ERR_INVALID, "bs_amax: null input");
     if (((uintptr_t)x) & 1u) return set_error(BS_ERR_INVALID, "bs_amax: input misaligned");
+    if (int rc = refuse_capture((hipStream_t)stream, "bs_amax")) return rc;
     if (n == 0) return BS_OK;   // slot keeps an older epoch: readers then see amax = 0
     uint64_t* slot = reinterpret_cast<uint64_t*>((uint8_t*)workspace + kWsAmaxOffset);
     int dev = 0, cus = 0;

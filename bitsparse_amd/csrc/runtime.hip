@@ -58,6 +58,20 @@ bool timing_next(int kind, hipEvent_t* start, hipEvent_t* stop)
     return true;
 }
 
+int refuse_capture(hipStream_t stream, const char* what)
+{
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cs) != hipSuccess) {
+        (void)hipGetLastError();
+        return BS_OK;
+    }
+    if (cs != hipStreamCaptureStatusNone)
+        return set_error(BS_ERR_INVALID,
+                         "%s cannot be captured into a HIP graph: its device state is tagged with a "
+                         "per-call epoch that a replay would repeat", what);
+    return BS_OK;
+}
+
 }  // namespace bs
 
 using namespace bs;

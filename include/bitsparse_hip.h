@@ -75,6 +75,13 @@ int bs_launch_timing_read(float* ms_out, int* kinds_out, int max_n, int* n_out);
  * time.  Returns the byte size needed for a dense [M, N] input.
  */
 int64_t bs_compress_workspace_bytes(int64_t M, int64_t N);
+/*
+ * Because of the epochs, bs_compress, bs_compress_relu, bs_amax and
+ * bs_amax_relu return BS_ERR_INVALID when `stream` is capturing into a HIP
+ * graph (a replay would repeat the captured epoch and read the previous
+ * replay's status words / amax as current).  Every other entry point can be
+ * captured.
+ */
 
 /*
  * Single-pass compress of a dense [M, N] activation: bitmask, prefix and

@@ -28,3 +28,31 @@ def test_first_quantize_in_fresh_process(dev):
     r = subprocess.run([sys.executable, "-c", SCRIPT % root], capture_output=True, text=True,
                        timeout=300)
     assert r.returncode == 0 and "ok" in r.stdout, r.stderr[-2000:]
+
+
+def test_epoch_tagged_entry_points_refuse_graph_capture(dev):
+    """bs_compress and bs_amax tag their device state with a per-call epoch;
+    a captured graph would replay one epoch and read the previous replay's
+    status words / amax as current, so capture is refused with an error
+    (nothing is enqueued) and the stream keeps working afterwards."""
+    import torch
+    from bitsparse_amd.bitsparse import TensorBuffer
+    from bitsparse_amd.src import hip_operators as H
+    from bitsparse_amd.src.functions import dense_to_tilesparse
+    from tests.helpers import relu_input
+    x = relu_input((256, 512), 0.5, seed=90).to(dev)
+    buf = TensorBuffer(2 * x.numel(), device=dev)
+    ref = dense_to_tilesparse(x, None, buf)            # workspace allocated outside capture
+    H.amax_into_workspace(x)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    for fn in (lambda: dense_to_tilesparse(x, None, buf), lambda: H.amax_into_workspace(x)):
+        g = torch.cuda.CUDAGraph()
+        with pytest.raises(ValueError, match="captured into a HIP graph"):
+            with torch.cuda.graph(g, stream=side):
+                fn()
+    torch.cuda.synchronize()
+    buf.reset_buffer()
+    again = dense_to_tilesparse(x, None, buf)
+    assert torch.equal(again.bitmask, ref.bitmask) and torch.equal(again.prefix, ref.prefix)
+    assert torch.equal(again.vals[:x.numel()], ref.vals[:x.numel()])
