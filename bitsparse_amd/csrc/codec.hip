@@ -1270,7 +1270,9 @@ __global__ __launch_bounds__(kThreads) void relu2_grad_kernel(GatherArgs a)
             for (int e = 0; e < 8; e++) {
                 uint32_t x = zero_x;
                 if ((mm >> e) & 1u) {
-                    const float rv = WIDEN ? bf16_to_f32(s_rv[r]) : val_f32<V_T>(lds_val<V_T, PB>(s_vals, r, bitbase));
+                    float rv;
+                    if constexpr (WIDEN) rv = bf16_to_f32(s_rv[r]);
+                    else rv = val_f32<V_T>(lds_val<V_T, PB>(s_vals, r, bitbase));
                     x = f32_to_bf16(bf16_to_f32(get16(g[j][h], e)) * (k2 * rv));
                     if constexpr (HAS_SCALE) x = f32_to_bf16(bf16_to_f32(x) * sb);
                 }
