@@ -174,6 +174,7 @@ struct CompressTraits {
     static constexpr int INB = IN_T == DT_BF16 ? 2 : 1;
     static constexpr int OUTB = (IN_T == DT_BF16 && !QUANT) ? 2 : 1;
     static constexpr int MASK_T = QUANT ? DT_E4M3FN : IN_T;
+    static constexpr int PB = OUTB == 2 ? 15 : 7;       // packed stream bits per value
 };
 
 // Positive-bit byte of a loaded chunk (after quantisation when QUANT).
@@ -490,11 +491,172 @@ __device__ __forceinline__ void ring_elem_store(uint8_t* vals, int64_t gi, const
         vals[gi] = ring[idx];
 }
 
-template <int IN_T, bool QUANT, bool VEC, int MODE, int U>
-__global__ __launch_bounds__(64 * U) __attribute__((amdgpu_waves_per_eu(QUANT ? 6 : BS_STREAM_WAVES_PER_EU)))
+// PACKED (MODE_FUSED only): the values go to a 15/7-bit stream (pack_sbit
+// storage) instead of raw elements: a.vals is the stream (4-byte aligned) and
+// a.vals_capacity its size in dwords.  Each wave still compacts its run into
+// the ring; every pass then builds the stream dwords its values complete (one
+// dword per lane from the <= 4 / <= 6 values overlapping it; the dwords at the
+// two ends of the run, shared with the neighbouring runs, are merged with
+// disjoint-bit atomics) and carries the values the next dword still needs to
+// the front of the ring.
+__device__ __forceinline__ void wave_sync_lds()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Merge `word` into out[D] keeping the bits outside `mask` (disjoint-bit
+// atomics commute with any other writer of other bits of the dword).
+__device__ __forceinline__ void merge_word(uint32_t* out, int64_t D, uint32_t word, uint32_t mask)
+{
+    if (mask == 0xffffffffu) {
+        out[D] = word;
+    } else if (mask != 0u) {
+        atomicAnd(&out[D], ~mask);
+        atomicOr(&out[D], word & mask);
+    }
+}
+
+// Bits [lb, hb) of a dword as a mask, 0 <= lb <= hb <= 32.
+__device__ __forceinline__ uint32_t bit_range_mask(uint32_t lb, uint32_t hb)
+{
+    const uint32_t hi = hb >= 32u ? 0xffffffffu : ((1u << hb) - 1u);
+    const uint32_t lo = lb >= 32u ? 0xffffffffu : ((1u << lb) - 1u);
+    return hi & ~lo;
+}
+
+// Packed stream phase of one wave's run: values [0, cnt) of the tile's run
+// (compacted chunks o[k] of round k at run position P[k] + in-round rank) go
+// to stream bits [g*PB, (g+cnt)*PB) of a.vals (a.vals_capacity dwords).
+// ring[i] holds run value base + i.
+// The run's partial dwords (shared with the neighbouring runs) are OR-ed into
+// s_edge[b], b the first unit boundary (0..U) whose dword they are; the unit
+// writes those dwords afterwards (packed_unit_edges).  s_toff[b] is the run
+// offset of boundary b inside the unit, whose run starts at value gu.
+template <int OUTB, int PB, int U>
+__device__ __forceinline__ void stream_packed(const CompressArgs& a, int64_t g, int cnt, const uint32_t* P,
+                                              const uint32_t* mp, const typename Raw<OUTB>::T* o,
+                                              uint8_t* ring, int lane, int64_t gu, const uint32_t* s_toff,
+                                              uint32_t* s_edge)
+{
+    constexpr int MAXV = PB == 15 ? 4 : 6;      // values overlapping one stream dword
+    constexpr uint32_t VMASK = (1u << PB) - 1u;
+    if (cnt == 0) return;
+    // boundary slots of the run's first and last dwords
+    const int64_t bdw = ((gu + (int64_t)s_toff[min(lane, U)]) * PB) >> 5;
+    const uint64_t mf = __ballot(lane <= U && bdw == ((g * PB) >> 5));
+    const uint64_t ml = __ballot(lane <= U && bdw == (((g + cnt) * PB - 1) >> 5));
+    const int slot_first = mf ? __ffsll((unsigned long long)mf) - 1 : -1;
+    const int slot_last = ml ? __ffsll((unsigned long long)ml) - 1 : -1;
+    // dwords and bits are counted from the run's first dword D0 (32-bit math)
+    const int64_t D0 = (g * PB) >> 5;
+    uint32_t* const out = reinterpret_cast<uint32_t*>(a.vals) + D0;
+    const int sb = (int)((g * PB) & 31), eb = sb + cnt * PB;   // run bits [sb, eb)
+    const int dend = (eb + 31) >> 5;
+    const int dcap = (int)min<int64_t>(a.vals_capacity - D0, (int64_t)dend);   // dwords allowed
+    int dn = 0;                                  // next dword to produce
+    int base = 0;
+    // rounds are written into the ring until the next one might not fit
+    // (a round adds <= 512 values and 8 of overrun); each flush then builds
+    // the dwords its values complete
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        {
+            const uint32_t m = (mp[k >> 2] >> (8 * (k & 3))) & 0xffu;
+            const uint32_t c = (uint32_t)__popc(m);
+            const uint32_t ex = wave_incl_scan(c) - c;
+            if (c != 0u) write_compacted<OUTB>(ring + ((int)P[k] - base + (int)ex) * OUTB, o[k]);
+        }
+        if (k < 7 && (int)P[k + 1] - base + 520 <= kRingElems) continue;
+        wave_sync_lds();
+        const int done = (int)P[k + 1];
+        const int dl = done == cnt ? dend : ((sb + done * PB) >> 5);
+        const int dlw = min(dl, dcap);
+        for (int d = dn + lane; d < dlw; d += 64) {
+            const int lo = max(d * 32, sb), hi = min(d * 32 + 32, eb);
+            const int v0 = (lo - sb) / PB, v1 = (hi - 1 - sb) / PB;
+            uint32_t word = 0;
+#pragma unroll
+            for (int j = 0; j < MAXV; j++) {
+                const int v = v0 + j;
+                if (v <= v1) {
+                    uint32_t x;
+                    if constexpr (OUTB == 2) x = reinterpret_cast<const uint16_t*>(ring)[v - base];
+                    else x = ring[v - base];
+                    const int pos = sb + v * PB - d * 32;                 // in (-PB, 32)
+                    word |= pos >= 0 ? ((x & VMASK) << pos) : ((x & VMASK) >> (-pos));
+                }
+            }
+            if (lo == d * 32 && hi == d * 32 + 32) {
+                out[d] = word;
+            } else {
+                const int slot = d == 0 ? slot_first : slot_last;
+                if (slot >= 0) atomicOr(&s_edge[slot], word);
+                else merge_word(out, d, word, bit_range_mask((uint32_t)(lo - d * 32), (uint32_t)(hi - d * 32)));
+            }
+        }
+        if (dl > dn) dn = dl;
+        if (done == cnt) break;
+        {
+            // values [vf, done) overlap dword dn, which a later flush completes
+            const int rel = dn * 32 - sb;
+            const int vf = rel > 0 ? rel / PB : 0;
+            const int np = done - vf;            // <= MAXV
+            uint32_t x = 0;
+            if (lane < np) {
+                if constexpr (OUTB == 2) x = reinterpret_cast<const uint16_t*>(ring)[vf - base + lane];
+                else x = ring[vf - base + lane];
+            }
+            wave_sync_lds();
+            if (lane < np) {
+                if constexpr (OUTB == 2) reinterpret_cast<uint16_t*>(ring)[lane] = (uint16_t)x;
+                else ring[lane] = (uint8_t)x;
+            }
+            base = vf;
+        }
+        wave_sync_lds();
+    }
+}
+
+// Write the unit's boundary dwords collected in s_edge (wave 0, lane b =
+// boundary b; the unit's run starts at value gu).  A dword is written by the
+// first boundary in it, and only if some run saw it as partial: a boundary
+// inside it, or the unit's range covering part of it.  Dwords inside the unit
+// are stored whole; the two at the unit's ends, shared with the neighbouring
+// units, are merged with disjoint-bit atomics.
+template <int PB, int U>
+__device__ __forceinline__ void packed_unit_edges(const CompressArgs& a, int64_t gu, const uint32_t* s_toff,
+                                                  const uint32_t* s_edge, int lane)
+{
+    const int64_t us = gu * PB, ue = (gu + (int64_t)s_toff[U]) * PB;
+    if (ue <= us || lane > U) return;
+    const int b = lane;
+    const int64_t Bb = (gu + (int64_t)s_toff[b]) * PB, Db = Bb >> 5;
+    if (b > 0 && (((gu + (int64_t)s_toff[b - 1]) * PB) >> 5) == Db) return;   // not the first in its dword
+    bool inner = false;
+    for (int b2 = b; b2 <= U; b2++) {
+        const int64_t B2 = (gu + (int64_t)s_toff[b2]) * PB;
+        if ((B2 >> 5) != Db) break;
+        inner |= (B2 & 31) != 0;
+    }
+    const int64_t lo = max(Db * 32, us), hi = min(Db * 32 + 32, ue);
+    if (lo < hi && Db < a.vals_capacity && (inner || lo > Db * 32 || hi < Db * 32 + 32))
+        merge_word(reinterpret_cast<uint32_t*>(a.vals), Db, s_edge[b],
+                   bit_range_mask((uint32_t)(lo - Db * 32), (uint32_t)(hi - Db * 32)));
+}
+
+#ifndef BS_PACKED_WAVES_PER_EU
+#define BS_PACKED_WAVES_PER_EU 7
+#endif
+
+template <int IN_T, bool QUANT, bool VEC, int MODE, int U, bool PACKED>
+__global__ __launch_bounds__(64 * U) __attribute__((amdgpu_waves_per_eu(
+    QUANT ? 6 : (PACKED ? BS_PACKED_WAVES_PER_EU : BS_STREAM_WAVES_PER_EU))))
 void compress_stream_kernel(CompressArgs a)
 {
     static_assert(!(QUANT && MODE == MODE_VALS), "the values pass copies stored values");
+    static_assert(!PACKED || MODE == MODE_FUSED, "the packed stream is written by the fused pass");
     constexpr bool WRITE_VALS = MODE != MODE_COUNT;
     using TR = CompressTraits<IN_T, QUANT>;
     constexpr int INB = TR::INB, OUTB = TR::OUTB;
@@ -505,12 +667,16 @@ void compress_stream_kernel(CompressArgs a)
     static_assert(U >= 1 && U <= 16, "one wave per tile, at most 16 waves");
 
     __shared__ uint32_t s_cnt[U];
-    __shared__ uint32_t s_toff[U];          // tile offsets inside the unit's run
+    __shared__ uint32_t s_toff[U + 1];      // tile offsets inside the unit's run; [U] = unit total
+    __shared__ uint32_t s_edge[PACKED ? U + 1 : 1];   // packed: boundary dwords of the unit's runs
     __shared__ uint32_t s_excl[1];
     __shared__ __align__(16) uint8_t s_ring[WRITE_VALS ? U * kRingElems * OUTB : 16];
     __shared__ __align__(16) uint32_t s_sel[WRITE_VALS ? 256 * NSEL : 4];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    if constexpr (PACKED) {
+        if (tid <= U) s_edge[tid] = 0u;
+    }
     if constexpr (WRITE_VALS) {
         if (tid < 256) {
             uint32_t sel[NSEL];
@@ -610,6 +776,7 @@ void compress_stream_kernel(CompressArgs a)
             }
             unit_total = __shfl(x, U - 1, 64);
             if (lane < U) s_toff[lane] = x - v;
+            if (lane == U - 1) s_toff[U] = x;
             if (lane == 0)
                 st_relaxed(&a.status[u], pack_status(a.epoch, u == 0 ? kFlagInc : kFlagAgg, unit_total));
         }
@@ -655,7 +822,11 @@ void compress_stream_kernel(CompressArgs a)
                 const int64_t end = start + (int64_t)(excl + unit_total);
                 if (a.offset_out) *a.offset_out = end;
                 if (a.start_out) *a.start_out = start;
-                if (a.err && end > a.vals_capacity && WRITE_VALS) atomicOr(a.err, 1);
+                if constexpr (PACKED) {
+                    if (a.err && end * TR::PB > a.vals_capacity * 32) atomicOr(a.err, 1);
+                } else {
+                    if (a.err && end > a.vals_capacity && WRITE_VALS) atomicOr(a.err, 1);
+                }
                 if (start < 0 && a.err && WRITE_VALS) atomicOr(a.err, 2);
             }
             if constexpr (QUANT) {
@@ -676,6 +847,11 @@ void compress_stream_kernel(CompressArgs a)
                     g = start + (int64_t)__builtin_amdgcn_readfirstlane(s_excl[0]) +
                         (int64_t)__builtin_amdgcn_readfirstlane(s_toff[wave]);
                 const int cnt = (int)P[8];
+                if constexpr (PACKED) {
+                    stream_packed<OUTB, TR::PB, U>(a, g, cnt, P, mp, o, s_ring + wave * (kRingElems * OUTB), lane,
+                                                   start + (int64_t)__builtin_amdgcn_readfirstlane(s_excl[0]),
+                                                   s_toff, s_edge);
+                } else {
                 if (MODE == MODE_VALS && a.err && lane == 0 && g + cnt > a.vals_capacity) atomicOr(a.err, 1);
                 const int a0 = (int)((((uintptr_t)a.vals) + (uint64_t)g * OUTB) & 15u) / OUTB;
                 const int64_t room = a.vals_capacity - g;
@@ -732,6 +908,12 @@ void compress_stream_kernel(CompressArgs a)
                     __builtin_amdgcn_wave_barrier();
                     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
                 }
+                }
+            }
+            if constexpr (PACKED) {
+                __syncthreads();
+                if (wave == 0 && start >= 0)
+                    packed_unit_edges<TR::PB, U>(a, start + (int64_t)s_excl[0], s_toff, s_edge, lane);
             }
         }
     }
@@ -744,30 +926,11 @@ void compress_stream_kernel(CompressArgs a)
 // (byte i*PB/8 holds the low bits); the payload is the low PB bits of the
 // stored value (15 for bf16, 7 for fp8: the sign bit of a ReLU value is 0).
 // The kernel packs raw[0, count) to stream indices [start, start + count):
-// one thread per output dword, each gathering the <= 3 (bf16) / <= 6 (fp8)
+// one thread per output dword, each gathering the <= 4 (bf16) / <= 6 (fp8)
 // values that overlap it.  Dwords shared with bits outside the run keep those
 // bits (atomicAnd of the run's bit mask complement, then atomicOr of the
 // run's bits: concurrent writers of disjoint bits commute).
 // ===========================================================================
-// Merge `word` into out[D] keeping the bits outside `mask` (disjoint-bit
-// atomics commute with any other writer of other bits of the dword).
-__device__ __forceinline__ void merge_word(uint32_t* out, int64_t D, uint32_t word, uint32_t mask)
-{
-    if (mask == 0xffffffffu) {
-        out[D] = word;
-    } else if (mask != 0u) {
-        atomicAnd(&out[D], ~mask);
-        atomicOr(&out[D], word & mask);
-    }
-}
-
-// Bits [lb, hb) of a dword as a mask, 0 <= lb <= hb <= 32.
-__device__ __forceinline__ uint32_t bit_range_mask(uint32_t lb, uint32_t hb)
-{
-    const uint32_t hi = hb >= 32u ? 0xffffffffu : ((1u << hb) - 1u);
-    const uint32_t lo = lb >= 32u ? 0xffffffffu : ((1u << lb) - 1u);
-    return hi & ~lo;
-}
 
 constexpr int kPackThreads = 256;
 
@@ -795,7 +958,7 @@ __global__ __launch_bounds__(kPackThreads) void pack_bits_kernel(const uint8_t* 
 
     if ((start & 7) != 0 || !raw_vec) {
         // general start (or raw values not aligned for vector loads): one
-        // thread per output dword, gathering the <= 3 / <= 6
+        // thread per output dword, gathering the <= 4 / <= 6
         // values that overlap it
         const int64_t D0 = S >> 5, D1 = min((E + 31) >> 5, out_words);
         for (int64_t D = D0 + (int64_t)blockIdx.x * kPackThreads + tid; D < D1;
@@ -1350,30 +1513,30 @@ static inline bool aligned8(const void* p) { return (((uintptr_t)p) & 7u) == 0; 
 #endif
 constexpr int kStreamU = BS_STREAM_U;
 
-template <int IN_T, bool QUANT, int MODE>
+template <int IN_T, bool QUANT, int MODE, bool PACKED>
 static hipError_t launch_compress_mode(const CompressArgs& a, bool vec, hipStream_t st)
 {
     const uint32_t units = (a.tend - a.tile0 + kStreamU - 1) / kStreamU;
     if (vec)
-        launch_timed(0, compress_stream_kernel<IN_T, QUANT, true, MODE, kStreamU>, dim3(units),
+        launch_timed(0, compress_stream_kernel<IN_T, QUANT, true, MODE, kStreamU, PACKED>, dim3(units),
                      dim3(64 * kStreamU), 0, st, a);
     else
-        launch_timed(0, compress_stream_kernel<IN_T, QUANT, false, MODE, kStreamU>, dim3(units),
+        launch_timed(0, compress_stream_kernel<IN_T, QUANT, false, MODE, kStreamU, PACKED>, dim3(units),
                      dim3(64 * kStreamU), 0, st, a);
     return hipGetLastError();
 }
 
-template <int MODE>
+template <int MODE, bool PACKED = false>
 static hipError_t launch_compress(const CompressArgs& a, int in_dtype, bool quant, bool vec,
                                   hipStream_t st)
 {
     if constexpr (MODE != MODE_VALS) {
-        if (quant) return launch_compress_mode<DT_BF16, true, MODE>(a, vec, st);
+        if (quant) return launch_compress_mode<DT_BF16, true, MODE, PACKED>(a, vec, st);
     }
     switch (in_dtype) {
-    case DT_BF16: return launch_compress_mode<DT_BF16, false, MODE>(a, vec, st);
-    case DT_E4M3FN: return launch_compress_mode<DT_E4M3FN, false, MODE>(a, vec, st);
-    default: return launch_compress_mode<DT_E5M2, false, MODE>(a, vec, st);
+    case DT_BF16: return launch_compress_mode<DT_BF16, false, MODE, PACKED>(a, vec, st);
+    case DT_E4M3FN: return launch_compress_mode<DT_E4M3FN, false, MODE, PACKED>(a, vec, st);
+    default: return launch_compress_mode<DT_E5M2, false, MODE, PACKED>(a, vec, st);
     }
 }
 
@@ -1419,9 +1582,19 @@ static int compress_impl(const void* dense, int in_dtype, int64_t M, int64_t N, 
                          int64_t vals_capacity, const int64_t* vals_offset_in, int align8,
                          int64_t* vals_offset_out, int64_t* vals_start_out, int write_vals,
                          int32_t* err_flags, void* workspace, int64_t workspace_bytes,
-                         uint32_t epoch, void* stream, bool relu, void* relu_out)
+                         uint32_t epoch, void* stream, bool relu, void* relu_out, bool packed = false)
 {
     clear_error();
+    if (packed) {
+        // vals is the packed stream and vals_capacity its size in bytes
+        if (!write_vals) return set_error(BS_ERR_INVALID, "bs_compress_packed: write_vals must be 1");
+        if (((uintptr_t)vals) & 3u)
+            return set_error(BS_ERR_INVALID, "bs_compress_packed: stream not 4-byte aligned");
+        if (M > 0 && N > 0 && vals_capacity > 0 && vals == nullptr)
+            return set_error(BS_ERR_INVALID, "bs_compress_packed: null stream");
+        if (M == 0 || N == 0)
+            return set_error(BS_ERR_INVALID, "bs_compress_packed: empty input (the cursor is not advanced here)");
+    }
     if (relu_out != nullptr && !relu)
         return set_error(BS_ERR_INVALID, "bs_compress: relu_out without relu");
     if (relu_out != nullptr && (((uintptr_t)relu_out) % (in_dtype == DT_BF16 ? 2 : 1)))
@@ -1446,7 +1619,7 @@ static int compress_impl(const void* dense, int in_dtype, int64_t M, int64_t N, 
         return set_error(BS_ERR_INVALID, "bs_compress: workspace too small (%lld < %lld bytes)",
                          (long long)workspace_bytes, (long long)bs_compress_workspace_bytes(M, N));
     const int outb = (in_dtype == DT_BF16 && !quantize) ? 2 : 1;
-    if (write_vals && ((uintptr_t)vals) % outb)
+    if (write_vals && !packed && ((uintptr_t)vals) % outb)
         return set_error(BS_ERR_INVALID, "bs_compress: vals not aligned to its element size");
     hipStream_t st = (hipStream_t)stream;
     if (T == 0) {
@@ -1475,9 +1648,9 @@ static int compress_impl(const void* dense, int in_dtype, int64_t M, int64_t N, 
     a.bitmask = bitmask;
     a.prefix = prefix;
     a.vals = (uint8_t*)vals;
-    a.vals_capacity = vals_capacity;
+    a.vals_capacity = packed ? vals_capacity / 4 : vals_capacity;   // packed: stream dwords
     a.offset_in = vals_offset_in;
-    a.align8 = align8;
+    a.align8 = packed ? 1 : align8;
     a.offset_out = vals_offset_out;
     a.start_out = vals_start_out;
     a.tile0 = 0;
@@ -1499,7 +1672,8 @@ static int compress_impl(const void* dense, int in_dtype, int64_t M, int64_t N, 
     bool vec = (N % 8 == 0) && (((uintptr_t)dense) % (8 * inb) == 0) &&
                (dense_q_out == nullptr || aligned8(dense_q_out)) &&
                (relu_out == nullptr || ((uintptr_t)relu_out) % (8 * inb) == 0);
-    hipError_t e = write_vals ? launch_compress<MODE_FUSED>(a, in_dtype, quantize != 0, vec, st)
+    hipError_t e = packed     ? launch_compress<MODE_FUSED, true>(a, in_dtype, quantize != 0, vec, st)
+                 : write_vals ? launch_compress<MODE_FUSED>(a, in_dtype, quantize != 0, vec, st)
                               : launch_compress<MODE_COUNT>(a, in_dtype, quantize != 0, vec, st);
     if (e != hipSuccess) return set_error(BS_ERR_HIP, "bs_compress launch: %s", hipGetErrorString(e));
     return BS_OK;
@@ -1531,6 +1705,20 @@ extern "C" int bs_compress_relu(const void* preact, int in_dtype, int64_t M, int
                          bitmask, prefix, vals, vals_capacity, vals_offset_in, align8, vals_offset_out,
                          vals_start_out, write_vals, err_flags, workspace, workspace_bytes, epoch, stream,
                          true, relu_out);
+}
+
+extern "C" int bs_compress_packed(const void* dense, int in_dtype, int64_t M, int64_t N, int quantize,
+                                  const uint64_t* amax_slot, uint32_t amax_epoch, float* scale_out,
+                                  void* dense_q_out, uint8_t* bitmask, uint32_t* prefix,
+                                  void* stream_bytes, int64_t stream_nbytes, const int64_t* vals_offset_in,
+                                  int64_t* vals_offset_out, int64_t* vals_start_out, int32_t* err_flags,
+                                  void* workspace, int64_t workspace_bytes, uint32_t epoch, int relu,
+                                  void* relu_out, void* stream)
+{
+    return compress_impl(dense, in_dtype, M, N, quantize, amax_slot, amax_epoch, scale_out, dense_q_out,
+                         bitmask, prefix, stream_bytes, stream_nbytes, vals_offset_in, 1, vals_offset_out,
+                         vals_start_out, 1, err_flags, workspace, workspace_bytes, epoch, stream,
+                         relu != 0, relu_out, true);
 }
 
 extern "C" int bs_compact_vals(const void* dense, int in_dtype, int64_t M, int64_t N,

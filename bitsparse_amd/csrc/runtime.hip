@@ -78,7 +78,7 @@ using namespace bs;
 
 extern "C" const char* bs_last_error(void) { return bs::g_err; }
 
-extern "C" int bs_abi_version(void) { return 4; }
+extern "C" int bs_abi_version(void) { return 5; }
 
 extern "C" int bs_launch_timing(int enable)
 {

@@ -131,14 +131,32 @@ def _check_buffer(buf: TensorBuffer, dtype: torch.dtype, pack_sbit: bool) -> Non
 
 def _compress_packed_into_buffer(dense: Tensor, scale: Tensor | None, buf: TensorBuffer,
                                  **quant) -> BitsparseTensor:
-    """Fused compress into a raw staging buffer, then pack at the 8-aligned
-    cursor; no host synchronisation.  ``quant`` forwards the quantise / ReLU
-    options of ``compress_into`` (quantize: the staging holds e4m3fn values)."""
+    """One fused pass writes bitmask, prefix and the packed stream at the
+    8-aligned cursor; no host synchronisation.  ``quant`` forwards the
+    quantise / ReLU options of ``compress_into`` (quantize: e4m3fn values)."""
     M, N = dense.shape
     grid_m, grid_n, num_tiles, TILE_NUMEL, TILE_BYTES = tile_grid(M, N, BLOCK_M, BLOCK_N)
     stored = torch.float8_e4m3fn if quant.get("quantize") else dense.dtype
     bitmask = torch.empty(num_tiles * TILE_BYTES, device=dense.device, dtype=torch.uint8)
     prefix = torch.empty(num_tiles + 1, device=dense.device, dtype=torch.uint32)
+    if M * N == 0:
+        return _compress_packed_staged(dense, scale, buf, bitmask, prefix, stored, **quant)
+    vals_offset = torch.empty(1, device=dense.device, dtype=torch.int64)
+    new_offset = torch.empty(1, device=dense.device, dtype=torch.int64)
+    ops.compress_packed_into(dense, bitmask, prefix, buf.vals, buf.offset, new_offset, vals_offset,
+                             buf.err_flags, **quant)
+    buf.offset = new_offset
+    return BitsparseTensor(buf.vals, bitmask, prefix, dense.shape, stored,
+                           grid_m, grid_n, BLOCK_M, BLOCK_N, scale=scale,
+                           vals_offset=vals_offset, pack_sbit=True)
+
+
+def _compress_packed_staged(dense: Tensor, scale: Tensor | None, buf: TensorBuffer, bitmask: Tensor,
+                            prefix: Tensor, stored: torch.dtype, **quant) -> BitsparseTensor:
+    """Compress into a raw staging buffer, then pack at the 8-aligned cursor
+    (the path for an empty input, whose cursor is still rounded up)."""
+    M, N = dense.shape
+    grid_m, grid_n, num_tiles, TILE_NUMEL, TILE_BYTES = tile_grid(M, N, BLOCK_M, BLOCK_N)
     staging = torch.empty(max(M * N, 1), device=dense.device, dtype=stored)
     nnz = torch.empty(1, device=dense.device, dtype=torch.int64)
     ops.compress_into(dense, bitmask, prefix, staging, None, nnz, None, write_vals=True, **quant)

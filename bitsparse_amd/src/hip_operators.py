@@ -153,6 +153,36 @@ def compress_into(dense: Tensor, bitmask: Tensor, prefix: Tensor, vals: Tensor |
         check(L.bs_compress(*args, stream_handle(dense.device)), "bs_compress")
 
 
+def compress_packed_into(dense: Tensor, bitmask: Tensor, prefix: Tensor, stream: Tensor,
+                         vals_offset_in: Tensor | None, vals_offset_out: Tensor | None,
+                         vals_start_out: Tensor | None, err_flags: Tensor | None,
+                         quantize: bool = False, scale_out: Tensor | None = None,
+                         dense_q_out: Tensor | None = None, amax_epoch: int = 0,
+                         relu: bool = False, relu_out: Tensor | None = None) -> None:
+    """Single-pass compress straight into a 15/7-bit packed stream (uint8
+    storage) at the cursor rounded up to a multiple of 8 values.  Options as
+    for ``compress_into``; ``vals_start_out`` receives the aligned start."""
+    require_device(dense, "compress_packed")
+    _contig(dense, "dense")
+    if stream.dtype != torch.uint8:
+        raise TypeError("compress_packed: the stream storage is uint8")
+    if relu_out is not None and (relu_out.shape != dense.shape or relu_out.dtype != dense.dtype
+                                 or not relu_out.is_contiguous()):
+        raise ValueError("compress_packed: relu_out must be a contiguous tensor like dense")
+    M, N = dense.shape
+    L = _lib.load()
+    ws = _lib.workspace_for(dense.device)
+    ws.ensure(L.bs_compress_workspace_bytes(M, N))
+    epoch = ws.next_epoch()
+    check(L.bs_compress_packed(dense.data_ptr(), dtype_code(dense.dtype), M, N, int(quantize),
+                               ws.amax_slot_ptr() if quantize else None, amax_epoch, ptr(scale_out),
+                               ptr(dense_q_out), bitmask.data_ptr(), prefix.data_ptr(),
+                               stream.data_ptr(), stream.numel(), ptr(vals_offset_in),
+                               ptr(vals_offset_out), ptr(vals_start_out), ptr(err_flags),
+                               ws.buf.data_ptr(), ws.nbytes, epoch, int(relu), ptr(relu_out),
+                               stream_handle(dense.device)), "bs_compress_packed")
+
+
 def amax_into_workspace(x: Tensor, relu: bool = False) -> int:
     """amax(|x|) (``relu``: amax of relu(x)) of a bf16 tensor into the
     stream's workspace; returns the epoch that tags it."""

@@ -138,6 +138,30 @@ int bs_compress_relu(const void* preact, int in_dtype, int64_t M, int64_t N, int
                      uint32_t epoch, void* relu_out, void* stream);
 
 /*
+ * bs_compress with pack_sbit storage: the values are written straight into
+ * the 15/7-bit stream `stream_bytes` (4-byte aligned, stream_nbytes bytes;
+ * value i occupies stream bits [i*b, (i+1)*b), LSB first, b = 15 for bf16
+ * and 7 for fp8 / quantize) at value index align8(*vals_offset_in), the
+ * TensorBuffer cursor rounded up to a multiple of 8 (functions.py:78-81), so
+ * no raw staging buffer is written and read back.  Stream bits outside the
+ * run keep their values; dwords at or past stream_nbytes/4 are not written
+ * and bit 0 of *err_flags is set.  *vals_start_out (nullable) receives the
+ * aligned start and *vals_offset_out (nullable) start + nnz.  relu = 1 takes
+ * `dense` as the pre-activation, as bs_compress_relu does (relu_out
+ * nullable).  M or N = 0 is refused (BS_ERR_INVALID).  Other arguments as
+ * for bs_compress.  Replaces lib_sparse/src/functions.py:76-92 with
+ * pack_sbit=True, which runs the compaction (triton_kernels.py:109-146) and
+ * the bit packer (src/bitpacking.py:58-117) as separate passes.
+ */
+int bs_compress_packed(const void* dense, int in_dtype, int64_t M, int64_t N, int quantize,
+                       const uint64_t* amax_slot, uint32_t amax_epoch, float* scale_out,
+                       void* dense_q_out, uint8_t* bitmask, uint32_t* prefix,
+                       void* stream_bytes, int64_t stream_nbytes, const int64_t* vals_offset_in,
+                       int64_t* vals_offset_out, int64_t* vals_start_out, int32_t* err_flags,
+                       void* workspace, int64_t workspace_bytes, uint32_t epoch, int relu,
+                       void* relu_out, void* stream);
+
+/*
  * Per-tile bitmask and nonzero counts (int32[T]) of a dense [M, N] input.
  * Replaces lib_sparse/src/triton_operators.py:21-33 (tile_pack) /
  * triton_kernels.py:67-97 (_tile_pack_kernel).

@@ -51,6 +51,19 @@ def test_invalid_arguments_rejected_on_host():
     rc = L.bs_compress(fake, 1, 64, 64, 1, fake, 1, None, None, fake, fake, fake, 10, None, 0,
                        None, None, 1, None, fake, 1 << 20, 1, None)
     assert rc == _lib.BS_ERR_INVALID and "bf16" in _err()
+    # packed stream: 4-byte alignment, non-empty input, the usual dense checks
+    rc = L.bs_compress_packed(fake, 0, 64, 64, 0, None, 0, None, None, fake, fake, fake + 2, 64, None,
+                              None, None, None, fake, 1 << 20, 1, 0, None, None)
+    assert rc == _lib.BS_ERR_INVALID and "aligned" in _err()
+    rc = L.bs_compress_packed(fake, 0, 0, 64, 0, None, 0, None, None, fake, fake, fake, 64, None,
+                              None, None, None, fake, 1 << 20, 1, 0, None, None)
+    assert rc == _lib.BS_ERR_INVALID and "empty" in _err()
+    rc = L.bs_compress_packed(fake, 9, 64, 64, 0, None, 0, None, None, fake, fake, fake, 64, None,
+                              None, None, None, fake, 1 << 20, 1, 0, None, None)
+    assert rc == _lib.BS_ERR_INVALID and "dtype" in _err()
+    rc = L.bs_compress_packed(fake, 0, 64, 64, 0, None, 0, None, None, fake, fake, fake, 64, None,
+                              None, None, None, fake, 64, 1, 0, None, None)
+    assert rc == _lib.BS_ERR_INVALID and "workspace" in _err()
     # workspace too small
     rc = L.bs_compress(fake, 0, 4096, 4096, 0, None, 0, None, None, fake, fake, fake, 10, None, 0,
                        None, None, 1, None, fake, 64, 1, None)

@@ -250,3 +250,142 @@ def test_ffn_relu2_fp8_pack_sbit_equals_raw(dev):
         res.append((y, xs.grad, W1s.grad, W2s.grad))
     for a, b in zip(*res):
         assert torch.equal(a, b)
+
+
+def _call_compress_packed(dev, x, stream_np, start, nbytes=None, relu=False):
+    """bs_compress_packed through the C ABI: (bitmask, prefix, stream bytes,
+    aligned start, end cursor, err flags) on the CPU."""
+    from bitsparse_amd import _lib
+    from bitsparse_amd.src.hip_operators import dtype_code
+    L = _lib.load()
+    M, N = x.shape
+    T = ((M + 63) // 64) * ((N + 63) // 64)
+    xd = x.to(dev).contiguous()
+    bm = torch.empty(T * 512, dtype=torch.uint8, device=dev)
+    pf = torch.empty(T + 1, dtype=torch.uint32, device=dev)
+    stream = torch.from_numpy(stream_np.copy()).to(dev)
+    off_in = torch.tensor([start], dtype=torch.int64, device=dev)
+    off_out = torch.full((1,), -7, dtype=torch.int64, device=dev)
+    start_out = torch.full((1,), -7, dtype=torch.int64, device=dev)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    ws = _lib.workspace_for(xd.device)
+    ws.ensure(L.bs_compress_workspace_bytes(M, N))
+    rc = L.bs_compress_packed(xd.data_ptr(), dtype_code(x.dtype), M, N, 0, None, 0, None, None,
+                              bm.data_ptr(), pf.data_ptr(), stream.data_ptr(),
+                              stream.numel() if nbytes is None else nbytes, off_in.data_ptr(),
+                              off_out.data_ptr(), start_out.data_ptr(), err.data_ptr(),
+                              ws.buf.data_ptr(), ws.nbytes, ws.next_epoch(), int(relu),
+                              xd.data_ptr() if relu else None, _lib.stream_handle(dev))
+    assert rc == 0, L.bs_last_error()
+    torch.cuda.synchronize()
+    return (bits(bm), bits(pf), stream.cpu().numpy(), int(start_out.item()), int(off_out.item()),
+            int(err.item()), xd.cpu())
+
+
+@pytest.mark.parametrize("code", [O.BF16, O.E4M3FN, O.E5M2])
+@pytest.mark.parametrize("shape,sparsity", [((64, 64), 0.5), ((129, 131), 0.3), ((200, 70), 0.9),
+                                            ((128, 1024), 0.0), ((77, 256), 1.0), ((1, 9), 0.2)])
+@pytest.mark.parametrize("start", [0, 5, 8, 1003])
+def test_fused_packed_compress_matches_oracle(dev, code, shape, sparsity, start):
+    """One pass writes the packed stream: bytes equal the oracle's packing of
+    the oracle's compacted values at the cursor rounded up to 8 values, every
+    other stream byte keeps its (random) content."""
+    x = relu_input(shape, sparsity, seed=sum(shape) + start + code, dtype=TORCH_DT[code])
+    bm_w, pf_w, v = O.compress(bits(x), code)
+    b = O.bits_per_value(code)
+    a0 = (start + 7) // 8 * 8
+    nbytes = ((a0 + v.size) * b + 7) // 8 // 4 * 4 + 16
+    rng = np.random.default_rng(start + code)
+    init = rng.integers(0, 256, nbytes).astype(np.uint8)
+    bm, pf, got, s0, end, err, _ = _call_compress_packed(dev, x, init, start)
+    want = O.pack_bits(v, code, init.copy(), a0)
+    assert (bm == bm_w).all() and (pf == pf_w).all()
+    assert (s0, end, err) == (a0, a0 + v.size, 0)
+    assert (got == want).all()
+
+
+@pytest.mark.parametrize("code", [O.BF16, O.E4M3FN])
+def test_fused_packed_compress_large_matches_oracle(dev, code):
+    """Many look-back units and every pass of the stream phase (whole-stream
+    comparison at 1024 x 2048, unaligned cursor)."""
+    x = relu_input((1024, 2048), 0.5, seed=31, dtype=TORCH_DT[code])
+    _, _, v = O.compress(bits(x), code)
+    b = O.bits_per_value(code)
+    start = 13
+    a0 = 16
+    nbytes = ((a0 + v.size) * b + 7) // 8 // 4 * 4 + 8
+    init = np.full(nbytes, 0x5A, np.uint8)
+    _, _, got, s0, end, err, _ = _call_compress_packed(dev, x, init, start)
+    want = O.pack_bits(v, code, init.copy(), a0)
+    assert (s0, end, err) == (a0, a0 + v.size, 0)
+    assert (got == want).all()
+
+
+def test_fused_packed_compress_relu(dev):
+    """Fused ReLU: the stream is that of relu(z) and z receives relu(z)."""
+    from tests.helpers import preact_input
+    z = preact_input((192, 320), 0.0, seed=8)
+    h = torch.relu(z)
+    _, _, v = O.compress(bits(h), O.BF16)
+    nbytes = ((8 + v.size) * 15 + 7) // 8 // 4 * 4 + 8
+    init = np.zeros(nbytes, np.uint8)
+    _, _, got, s0, end, err, zout = _call_compress_packed(dev, z, init, 3, relu=True)
+    assert (s0, end, err) == (8, 8 + v.size, 0)
+    assert (got == O.pack_bits(v, O.BF16, init.copy(), 8)).all()
+    assert torch.equal(zout.view(torch.int16), h.view(torch.int16))
+
+
+@pytest.mark.parametrize("code", [O.BF16, O.E4M3FN])
+def test_fused_packed_compress_capacity(dev, code):
+    """A stream declared too small: bit 0 of the error flags is set, the
+    dwords inside the declared size hold the oracle's bits and nothing past
+    it is written."""
+    x = relu_input((256, 256), 0.2, seed=12, dtype=TORCH_DT[code])
+    _, _, v = O.compress(bits(x), code)
+    b = O.bits_per_value(code)
+    full = (v.size * b + 7) // 8 // 4 * 4 + 8
+    declared = (full // 2) // 4 * 4
+    init = np.random.default_rng(3).integers(0, 256, full).astype(np.uint8)
+    _, _, got, s0, end, err, _ = _call_compress_packed(dev, x, init, 0, nbytes=declared)
+    want = O.pack_bits(v, code, init.copy(), 0)
+    assert err & 1 and end == v.size
+    assert (got[:declared] == want[:declared]).all()
+    assert (got[declared:] == init[declared:]).all()
+
+
+def _tile_count_matrix(M, N, counts, code, seed):
+    """[M, N] matrix (bits) whose tile t holds exactly counts[t] positive
+    values at random positions."""
+    rng = np.random.default_rng(seed)
+    dt = _np_dt(code)
+    x = np.zeros((M, N), dt)
+    gn = N // 64
+    one = {O.BF16: 0x3f80, O.E4M3FN: 0x38, O.E5M2: 0x3c}[code]
+    for t, c in enumerate(counts):
+        r0, c0 = (t // gn) * 64, (t % gn) * 64
+        pos = rng.choice(4096, size=int(c), replace=False)
+        x[r0 + pos // 64, c0 + pos % 64] = one + rng.integers(0, 8, size=int(c)).astype(dt)
+    return x
+
+
+@pytest.mark.parametrize("code", [O.BF16, O.E4M3FN])
+@pytest.mark.parametrize("kind", ["tiny_runs", "aligned_runs"])
+@pytest.mark.parametrize("start", [0, 3, 8, 21])
+def test_fused_packed_compress_run_boundaries(dev, code, kind, start):
+    """Tile runs of 0..3 values (several run boundaries inside one stream
+    dword, empty runs) and runs of exactly 32 values (every boundary on a
+    dword edge when the cursor is): stream equal to the oracle's packing."""
+    M, N = 256, 1024                         # 64 tiles = 8 compress units
+    rng = np.random.default_rng(start + 7 * code)
+    counts = rng.integers(0, 4, 64) if kind == "tiny_runs" else np.full(64, 32)
+    xb = _tile_count_matrix(M, N, counts, code, seed=start)
+    x = from_bits(xb, TORCH_DT[code])
+    _, _, v = O.compress(xb, code)
+    assert v.size == counts.sum()
+    b = O.bits_per_value(code)
+    a0 = (start + 7) // 8 * 8
+    nbytes = ((a0 + v.size) * b + 7) // 8 // 4 * 4 + 16
+    init = np.random.default_rng(99).integers(0, 256, nbytes).astype(np.uint8)
+    _, _, got, s0, end, err, _ = _call_compress_packed(dev, x, init, start)
+    assert (s0, end, err) == (a0, a0 + v.size, 0)
+    assert (got == O.pack_bits(v, code, init.copy(), a0)).all()
