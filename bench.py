@@ -424,7 +424,7 @@ def bench_mlp_c4(steps: int, warmup: int):
     return out
 
 
-def bench_sweep(steps: int, warmup: int):
+def bench_sweep(steps: int, warmup: int, packed_only: bool = False):
     """16384 x 16384, N(mu, 1) pre-activation for 50..99% zeros,
     bf16 storage and e4m3fn storage (fused amax + quantize + compress), a
     skewed case with a per-column N(0, 0.5) bias, and the packed 15/7-bit
@@ -442,6 +442,8 @@ def bench_sweep(steps: int, warmup: int):
     cases = [(n, mu, st, False, False) for n, mu in mus for st in ("bf16", "e4m3fn")]
     cases += [("90% skewed columns", -1.2816, "bf16", True, False)]
     cases += [(n, mu, st, False, True) for n, mu in mus[:3:2] for st in ("bf16", "e4m3fn")]
+    if packed_only:
+        cases = [c for c in cases if c[4]]
     for name, mu, storage, skew, pack in cases:
         g = torch.Generator(device=dev).manual_seed(0)
         pre = torch.randn((M, N), device=dev, generator=g) + mu
@@ -651,6 +653,9 @@ def main() -> int:
                     help="skip the GEMM, configs[3] MLP, sparsity sweep and 12-block stack sections")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a 1 GiB device copy (reference for rocprof byte counters)")
+    ap.add_argument("--packed-only", action="store_true",
+                    help="run only the packed-stream (pack_sbit) sweep cases and print their JSON "
+                         "(profiling entry point)")
     ap.add_argument("--kernels-only", action="store_true",
                     help="run only the gradient / unpack / fp8 kernel section and print its JSON "
                          "(profiling entry point)")
@@ -671,6 +676,9 @@ def main() -> int:
 
     if args.gemm_only:
         print(json.dumps({"gemm": bench_gemm(args.steps, args.warmup)}), flush=True)
+        return 0
+    if args.packed_only:
+        print(json.dumps({"sweep": bench_sweep(args.steps, args.warmup, packed_only=True)}), flush=True)
         return 0
     if args.kernels_only:
         copy_gbs = measure_copy_gbs()
