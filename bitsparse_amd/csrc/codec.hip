@@ -554,7 +554,8 @@ __device__ __forceinline__ void stream_packed(const CompressArgs& a, int64_t g, 
     uint32_t* const out = reinterpret_cast<uint32_t*>(a.vals) + D0;
     const int sb = (int)((g * PB) & 31), eb = sb + cnt * PB;   // run bits [sb, eb)
     const int dend = (eb + 31) >> 5;
-    const int dcap = (int)min<int64_t>(a.vals_capacity - D0, (int64_t)dend);   // dwords allowed
+    const int64_t capw = a.vals_capacity - D0;                 // dwords left in the stream (64-bit: a
+    const int dcap = capw <= 0 ? 0 : (int)min<int64_t>(capw, (int64_t)dend);   // far cursor must not wrap)
     int dn = 0;                                  // next dword to produce
     int base = 0;
     // rounds are written into the ring until the next one might not fit

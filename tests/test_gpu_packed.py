@@ -389,3 +389,38 @@ def test_fused_packed_compress_run_boundaries(dev, code, kind, start):
     _, _, got, s0, end, err, _ = _call_compress_packed(dev, x, init, start)
     assert (s0, end, err) == (a0, a0 + v.size, 0)
     assert (got == O.pack_bits(v, code, init.copy(), a0)).all()
+
+
+@pytest.mark.parametrize("shape", [(0, 64), (64, 0)])
+def test_packed_tensorbuffer_empty_input_rounds_cursor(dev, shape):
+    """An empty activation into a packed TensorBuffer takes no values but
+    still rounds the cursor up to 8 values (functions.py:78-92): the next
+    activation starts there, and the stream is untouched."""
+    import bitsparse_amd.src.functions as F
+    from bitsparse_amd.bitsparse import TensorBuffer
+    buf = TensorBuffer(4096, device=dev, pack_sbit=True)
+    buf.vals.fill_(0x3C)
+    buf.offset = torch.tensor([5], dtype=torch.int64, device=dev)
+    sp = F.dense_to_tilesparse(torch.zeros(shape, dtype=torch.bfloat16, device=dev), None, buf,
+                               pack_sbit=True)
+    assert int(sp.vals_offset.item()) == 8 and int(buf.offset.item()) == 8
+    assert sp.nnz() == 0 and bits(sp.prefix).tolist() == [0]
+    x = relu_input((64, 96), 0.5, seed=2)
+    sp2 = F.dense_to_tilesparse(x.to(dev), None, buf, pack_sbit=True)
+    _, _, v = O.compress(bits(x), O.BF16)
+    assert int(sp2.vals_offset.item()) == 8 and int(buf.offset.item()) == 8 + v.size
+    want = O.pack_bits(v, O.BF16, np.full(buf.vals.numel(), 0x3C, np.uint8), 8)
+    assert (buf.vals.cpu().numpy() == want).all()
+    assert torch.equal(_dense(sp2).cpu(), x)
+
+
+def test_fused_packed_compress_cursor_past_stream(dev):
+    """A cursor far past the end of the stream (2^36 values): nothing is
+    written, bit 0 of the error flags is set and the cursor still advances."""
+    x = relu_input((128, 192), 0.5, seed=21)
+    _, _, v = O.compress(bits(x), O.BF16)
+    init = np.random.default_rng(5).integers(0, 256, 4096).astype(np.uint8)
+    start = 1 << 36
+    _, _, got, s0, end, err, _ = _call_compress_packed(dev, x, init, start)
+    assert (s0, end) == (start, start + v.size) and err & 1
+    assert (got == init).all()
