@@ -398,7 +398,7 @@ def test_packed_tensorbuffer_empty_input_rounds_cursor(dev, shape):
     activation starts there, and the stream is untouched."""
     import bitsparse_amd.src.functions as F
     from bitsparse_amd.bitsparse import TensorBuffer
-    buf = TensorBuffer(4096, device=dev, pack_sbit=True)
+    buf = TensorBuffer(16384, device=dev, pack_sbit=True)
     buf.vals.fill_(0x3C)
     buf.offset = torch.tensor([5], dtype=torch.int64, device=dev)
     sp = F.dense_to_tilesparse(torch.zeros(shape, dtype=torch.bfloat16, device=dev), None, buf,
@@ -412,6 +412,7 @@ def test_packed_tensorbuffer_empty_input_rounds_cursor(dev, shape):
     want = O.pack_bits(v, O.BF16, np.full(buf.vals.numel(), 0x3C, np.uint8), 8)
     assert (buf.vals.cpu().numpy() == want).all()
     assert torch.equal(_dense(sp2).cpu(), x)
+    assert not buf.overflowed()
 
 
 def test_fused_packed_compress_cursor_past_stream(dev):
