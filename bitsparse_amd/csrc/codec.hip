@@ -647,13 +647,17 @@ __device__ __forceinline__ void packed_unit_edges(const CompressArgs& a, int64_t
                    bit_range_mask((uint32_t)(lo - Db * 32), (uint32_t)(hi - Db * 32)));
 }
 
+#ifndef BS_QUANT_WAVES_PER_EU
+#define BS_QUANT_WAVES_PER_EU 6
+#endif
+
 #ifndef BS_PACKED_WAVES_PER_EU
 #define BS_PACKED_WAVES_PER_EU 7
 #endif
 
 template <int IN_T, bool QUANT, bool VEC, int MODE, int U, bool PACKED>
 __global__ __launch_bounds__(64 * U) __attribute__((amdgpu_waves_per_eu(
-    QUANT ? 6 : (PACKED ? BS_PACKED_WAVES_PER_EU : BS_STREAM_WAVES_PER_EU))))
+    QUANT ? BS_QUANT_WAVES_PER_EU : (PACKED ? BS_PACKED_WAVES_PER_EU : BS_STREAM_WAVES_PER_EU))))
 void compress_stream_kernel(CompressArgs a)
 {
     static_assert(!(QUANT && MODE == MODE_VALS), "the values pass copies stored values");
