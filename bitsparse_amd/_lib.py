@@ -23,7 +23,7 @@ BS_OK = 0
 BS_ERR_INVALID = 1
 BS_ERR_HIP = 2
 
-# dtype codes == reference codec ids (lib_sparse/bitsparse.py:20-30)
+# dtype codes == reference codec ids (lib_sparse/bitsparse.py:8-18)
 DT_BF16, DT_E4M3FN, DT_E5M2 = 0, 1, 2
 
 _i64 = ctypes.c_int64
@@ -195,11 +195,15 @@ class Workspace:
                 new[:self.buf.numel()].copy_(self.buf)
             self.buf = new
 
-    def next_epoch(self) -> int:
-        self.epoch += 1
-        if self.epoch > _EPOCH_LIMIT:
+    def next_epoch(self, reserve: int = 1) -> int:
+        """A fresh epoch.  ``reserve`` = how many epochs the caller's sequence
+        takes in total (the amax of a quantizing compress reserves 2), so the
+        wrap -- which zeroes the buffer, amax slot included -- never falls
+        between the amax and the compress that reads it."""
+        if self.epoch + reserve > _EPOCH_LIMIT:
             self.buf.zero_()
-            self.epoch = 1
+            self.epoch = 0
+        self.epoch += 1
         return self.epoch
 
     @property

@@ -1,8 +1,8 @@
 """Compressed-activation container types.
 
 Mirrors reference lib_sparse/bitsparse.py: ``pack_codec`` / ``bits_per_value``
-(:20-35), ``BitsparseTensor`` (:38-99), ``TensorBuffer`` (:102-129) and
-``tile_grid`` (:132-139), with the same constructor signatures, attributes
+(:8-23), ``BitsparseTensor`` (:26-87), ``TensorBuffer`` (:90-117) and
+``tile_grid`` (:120-127), with the same constructor signatures, attributes
 and storage-size accounting.
 """
 from __future__ import annotations
@@ -18,7 +18,7 @@ def pack_codec(dtype) -> int:
     """Codec id of a storage dtype: 0 = bf16, 1 = e4m3fn, 2 = e5m2.
 
     The id doubles as the dtype code of the HIP entry points.
-    Reference: lib_sparse/bitsparse.py:20-30.
+    Reference: lib_sparse/bitsparse.py:8-18.
     """
     if dtype == getattr(torch, "float8_e4m3fn", None):
         return 1
@@ -29,7 +29,7 @@ def pack_codec(dtype) -> int:
 
 def bits_per_value(dtype) -> int:
     """Bits per value in the packed stream (sign dropped): 15 bf16, 7 fp8.
-    Reference: lib_sparse/bitsparse.py:33-35."""
+    Reference: lib_sparse/bitsparse.py:21-23."""
     return 7 if pack_codec(dtype) else 15
 
 
@@ -43,7 +43,7 @@ class BitsparseTensor:
     prefix      uint32[T+1], value offset of each tile relative to vals_offset
     vals_offset int64 device tensor
     scale       fp32 0-d tensor for fp8 storage (per-tensor scale) or None
-    Reference: lib_sparse/bitsparse.py:38-99.
+    Reference: lib_sparse/bitsparse.py:26-87.
     """
     vals: Tensor
     bitmask: Tensor
@@ -89,13 +89,13 @@ class BitsparseTensor:
 
     def nnz(self):
         """Number of set bitmask bits as a 0-d int64 tensor (diagnostics;
-        equals prefix[-1]).  Reference: lib_sparse/bitsparse.py:83-86."""
+        equals prefix[-1]).  Reference: lib_sparse/bitsparse.py:71-74."""
         bits = torch.arange(8, device=self.bitmask.device, dtype=torch.uint8)
         return ((self.bitmask[:, None] >> bits) & 1).sum()
 
     def vram_size(self):
         """Stored bytes: values + bitmask + prefix (synchronises).
-        Reference: lib_sparse/bitsparse.py:88-96."""
+        Reference: lib_sparse/bitsparse.py:76-84."""
         nnz = int(self.prefix[-1].item())
         if self.pack_sbit:
             val_size = packed_nbytes(nnz, bits_per_value(self.dtype))
@@ -117,7 +117,7 @@ class TensorBuffer:
     int64 tensor by every compress (the previous tensor becomes that
     BitsparseTensor's ``vals_offset`` snapshot); ``reset_buffer`` starts over.
     Values that do not fit are dropped by the kernel and flagged; see
-    ``overflowed``.  Reference: lib_sparse/bitsparse.py:102-129.
+    ``overflowed``.  Reference: lib_sparse/bitsparse.py:90-117.
     """
     vals: Tensor
     offset: Tensor
@@ -152,7 +152,7 @@ class TensorBuffer:
 
 def tile_grid(M: int, N: int, BLOCK_M: int, BLOCK_N: int) -> tuple[int, int, int, int, int]:
     """(grid_m, grid_n, num_tiles, TILE_NUMEL, TILE_BYTES) of a dense shape.
-    Reference: lib_sparse/bitsparse.py:132-139."""
+    Reference: lib_sparse/bitsparse.py:120-127."""
     TILE_NUMEL = BLOCK_M * BLOCK_N
     TILE_BYTES = TILE_NUMEL // 8
     grid_m = (M + BLOCK_M - 1) // BLOCK_M

@@ -15,3 +15,8 @@ _PACK_CHUNK_TILES = 2**16
 
 # keep fp8 copies of GEMM operands for the backward (reference config.py:12)
 CACHE_FP8_MATMUl = False
+
+# dtype of the gradients MatmulFp8 returns: None = the fp8 dtype of the
+# operand each gradient belongs to, as the reference does (fp8.py:107,112);
+# torch.bfloat16 keeps them in bf16 (an addition, not in the reference)
+FP8_GRAD_DTYPE = None

@@ -1,7 +1,7 @@
 // Device-side building blocks shared by the BitSparse HIP kernels (gfx950).
 //
 // Format facts used everywhere (reference lib_sparse/src/triton_kernels.py:1-17,
-// lib_sparse/bitsparse.py:132-139):
+// lib_sparse/bitsparse.py:120-127):
 //   * 64x64 tiles, tile id t = tm * grid_n + tn;
 //   * a "chunk" is 8 consecutive elements of one tile row; chunk b of a tile
 //     (0..511) covers tile-flat indices 8b..8b+7, i.e. row b/8, columns

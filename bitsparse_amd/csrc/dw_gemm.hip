@@ -28,6 +28,7 @@
 // the linear workgroup id is remapped to give each XCD a contiguous range of
 // output tiles (N fastest): the workgroups resident on one XCD share their
 // A rows, which then stay in that XCD's L2.
+#include <algorithm>
 #include <type_traits>
 #include <utility>
 
@@ -808,6 +809,13 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* part, i
     }
 }
 
+// C[0, n) = 0 (bf16 bits), grid-stride
+__global__ __launch_bounds__(256) void zero_fill_u16_kernel(uint16_t* C, int64_t n)
+{
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) C[i] = 0;
+}
+
 // Split-K factor: fewest "rounds x steps" with one workgroup per CU on kCus
 // CUs, a small charge for the partial-sum pass, <= kMaxSteps per workgroup
 // and >= 8 steps per workgroup where possible.
@@ -888,20 +896,25 @@ extern "C" int bs_gemm_compressed_b(const void* A, int64_t M, int64_t K, int64_t
     if ((uint64_t)K * (uint64_t)N >= kMaxElems)
         return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: K*N must be < 2^31");
     if (M == 0 || N == 0) return BS_OK;
-    if (A == nullptr || C == nullptr || bitmask == nullptr || prefix == nullptr ||
-        (vals_numel > 0 && vals == nullptr))
+    if (C == nullptr) return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: null C");
+    if (((uintptr_t)C) & 1) return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: C misaligned");
+    hipStream_t st = (hipStream_t)stream;
+    const uint32_t ksteps = (uint32_t)((K + kBK - 1) / kBK);
+    if (ksteps == 0) {
+        // an empty sum: C = 0, written by a kernel (a memset node in a captured
+        // graph is avoided, so this path captures like the others)
+        const int64_t n = M * N;
+        const uint32_t nblk = (uint32_t)std::min<int64_t>((n + 255) / 256, 2048);
+        hipLaunchKernelGGL(zero_fill_u16_kernel, dim3(nblk), dim3(256), 0, st, (uint16_t*)C, n);
+        hipError_t e = hipGetLastError();
+        return e == hipSuccess ? BS_OK : set_error(BS_ERR_HIP, "bs_gemm_compressed_b: %s", hipGetErrorString(e));
+    }
+    if (A == nullptr || bitmask == nullptr || prefix == nullptr || (vals_numel > 0 && vals == nullptr))
         return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: null pointer");
     if ((((uintptr_t)A) & 15) || (lda % 8) != 0)
         return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: A must be 16-byte aligned with lda %% 8 == 0");
     if (lda >= (1ll << 24)) return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: lda must be < 2^24");
-    if (((uintptr_t)C) & 1) return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: C misaligned");
     if (((uintptr_t)vals) & 15) return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: vals must be 16-byte aligned");
-    hipStream_t st = (hipStream_t)stream;
-    const uint32_t ksteps = (uint32_t)((K + kBK - 1) / kBK);
-    if (ksteps == 0) {
-        hipError_t e = hipMemsetAsync(C, 0, (size_t)M * N * 2, st);
-        return e == hipSuccess ? BS_OK : set_error(BS_ERR_HIP, "bs_gemm_compressed_b: %s", hipGetErrorString(e));
-    }
     const GemmPlan plan = gemm_plan(M, N, K);
     const int split = plan.split;
     const int64_t part_bytes = split > 1 ? align_up256((int64_t)split * M * N * 4) : 0;

@@ -4,9 +4,10 @@ uncompressed.  They define the denominator of "compressed backward within
 
 Semantics of reference experiments/experiment.py:242-306 (``FFN``: saves
 relu(z) and masks with threshold_backward) and :322-384 (``FFNRelu2_2``:
-saves r = relu(z), rebuilds k*r^2 in backward).  ``DenseFFNRelu2Fp8`` is
-that comparator's fp8 mode (experiment.py:330-384 with an fp8 DTYPE): fp8
-GEMMs, r cached as e4m3fn + scale, k*r^2 rebuilt in bf16.
+saves r = relu(z), rebuilds k*r^2 in backward).  ``DenseFFNReluFp8`` and
+``DenseFFNRelu2Fp8`` are their fp8 modes (the same functions with an fp8
+DTYPE): fp8 GEMMs, the activation cached as e4m3fn + scale, k*r^2 rebuilt
+in bf16.
 """
 from __future__ import annotations
 
@@ -37,6 +38,37 @@ class DenseFFNRelu(Function):
         grad_x = grad_pre @ W1 if ctx.needs_input_grad[0] else None
         grad_W1 = grad_pre.T @ x
         return grad_x, grad_W1, grad_W2
+
+
+class DenseFFNReluFp8(Function):
+    """fp8 mode of DenseFFNRelu (reference experiment.py:242-306 with an fp8
+    DTYPE): fp8 GEMMs, relu(z) saved as e4m3fn + scale, the ReLU mask taken
+    from the saved codes (q > 0); optional first-layer bias b1 (no gradient),
+    added before the activation."""
+
+    @staticmethod
+    def forward(ctx, x, W1, W2, b1=None):
+        z = matmul(x, W1.T, True)
+        if b1 is not None:
+            z = z + b1
+        z.relu_()
+        z8, z_scale = to_fp8(z)
+        ctx.save_for_backward(x, W1, W2, z8)
+        ctx.z_scale = z_scale
+        return matmul(z8, W2.T, True, a_scale=z_scale)
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        x, W1, W2, z8 = ctx.saved_tensors
+        g8, gs = to_fp8(grad_output)
+        grad_z = matmul(g8, W2, True, a_scale=gs)
+        grad_W2 = matmul(g8.T, z8, True, a_scale=gs, b_scale=ctx.z_scale)
+        grad_pre = grad_z * (z8.to(torch.bfloat16) > 0)
+        del grad_z
+        p8, ps = to_fp8(grad_pre)
+        grad_x = matmul(p8, W1, True, a_scale=ps) if ctx.needs_input_grad[0] else None
+        grad_W1 = matmul(p8.T, x, True, a_scale=ps)
+        return grad_x, grad_W1, grad_W2, None
 
 
 class DenseFFNRelu2(Function):

@@ -108,7 +108,8 @@ class Relu2Linear(Function):
         if is_fp8(storage_dtype):
             if storage_dtype != torch.float8_e4m3fn:
                 raise TypeError("fp8 activation storage is float8_e4m3fn")
-            _, scale, h_sparse = relu_quantize_and_compress(z, sparse_data, pack_sbit)
+            # the forward multiplies the bf16 square, so no dense e4m3fn copy
+            _, scale, h_sparse = relu_quantize_and_compress(z, sparse_data, pack_sbit, dense_out=False)
             h = z
         else:
             h, h_sparse = relu_and_compress(z, sparse_data, pack_sbit)

@@ -10,10 +10,12 @@ Mirrors reference lib_sparse/src/functions.py:23-99.  Two execution paths:
   triton_operators.py:50), allocates exactly nnz values, and a compact pass
   fills them.
 
-With ``pack_sbit`` the values are compacted into a raw staging buffer and
-packed into the 15/7-bit stream (``bitpacking.pack_bits``); a TensorBuffer
-cursor is first rounded up to a multiple of 8 values (functions.py:78-81),
-so activations never share stream bytes.
+With ``pack_sbit`` the values go to the 15/7-bit stream.  Into a TensorBuffer
+this is the same single pass (``bs_compress_packed`` writes stream dwords
+instead of raw values) at the cursor rounded up to a multiple of 8 values
+(functions.py:78-81), so activations never share stream bytes.  The
+standalone path, and an empty input into a TensorBuffer, compact raw values
+first and pack them with ``bitpacking.pack_bits``.
 """
 from __future__ import annotations
 
@@ -170,26 +172,30 @@ def _compress_packed_staged(dense: Tensor, scale: Tensor | None, buf: TensorBuff
 
 def relu_quantize_and_compress(
     z: Tensor, sparse_data: TensorBuffer | None = None, pack_sbit: bool = False,
-) -> tuple[Tensor, Tensor, BitsparseTensor]:
+    dense_out: bool = True,
+) -> tuple[Tensor | None, Tensor, BitsparseTensor]:
     """``quantize_and_compress(z.relu_(), ...)`` with the ReLU fused into the
     amax and compress passes (relu(z) is written back into z, as the
     reference's in-place relu_ does, layers.py:29-37)."""
     if z.dtype != torch.bfloat16:
         raise TypeError("relu_quantize_and_compress expects a bfloat16 tensor")
     if not z.is_contiguous():
-        return quantize_and_compress(z.relu_(), sparse_data, pack_sbit)
-    return quantize_and_compress(z, sparse_data, pack_sbit, _relu=True)
+        return quantize_and_compress(z.relu_(), sparse_data, pack_sbit, dense_out=dense_out)
+    return quantize_and_compress(z, sparse_data, pack_sbit, dense_out=dense_out, _relu=True)
 
 
 def quantize_and_compress(
     dense: Tensor, sparse_data: TensorBuffer | None = None, pack_sbit: bool = False,
-    _relu: bool = False,
-) -> tuple[Tensor, Tensor, BitsparseTensor]:
+    dense_out: bool = True, _relu: bool = False,
+) -> tuple[Tensor | None, Tensor, BitsparseTensor]:
     """bf16 [M, N] -> (e4m3fn dense, fp32 scale, BitsparseTensor of the e4m3fn
     values) with one amax pass and one fused quantize+compress pass.
 
     Equivalent to ``h8, s = to_fp8(h); dense_to_tilesparse(h8, s, sparse_data)``
     (reference layers.py:32-37) but reads ``h`` twice instead of three times.
+    ``dense_out=False``: the e4m3fn dense copy is not written (None is
+    returned in its place) when the caller only keeps the compressed form
+    (the ReLU^2 layer multiplies the bf16 square, not h8).
     """
     if dense.dtype != torch.bfloat16:
         raise TypeError("quantize_and_compress expects a bfloat16 tensor")
@@ -199,7 +205,9 @@ def quantize_and_compress(
     grid_m, grid_n, num_tiles, TILE_NUMEL, TILE_BYTES = tile_grid(M, N, BLOCK_M, BLOCK_N)
     amax_epoch = ops.amax_into_workspace(dense, relu=_relu)
     fused = dict(relu=True, relu_out=dense) if _relu else {}
-    q = torch.empty((M, N), device=dense.device, dtype=torch.float8_e4m3fn)
+    # the standalone path compacts from the quantized dense copy
+    need_q = dense_out or sparse_data is None
+    q = torch.empty((M, N), device=dense.device, dtype=torch.float8_e4m3fn) if need_q else None
     scale = torch.empty((), device=dense.device, dtype=torch.float32)
     bitmask = torch.empty(num_tiles * TILE_BYTES, device=dense.device, dtype=torch.uint8)
     prefix = torch.empty(num_tiles + 1, device=dense.device, dtype=torch.uint32)
@@ -211,7 +219,7 @@ def quantize_and_compress(
         sp = BitsparseTensor(vals, bitmask, prefix, q.shape, q.dtype, grid_m, grid_n,
                              BLOCK_M, BLOCK_N, scale=scale, vals_offset=vals_offset,
                              pack_sbit=pack_sbit)
-        return q, scale, sp
+        return (q if dense_out else None), scale, sp
     _check_buffer(sparse_data, torch.float8_e4m3fn, pack_sbit)
     if pack_sbit:
         sp = _compress_packed_into_buffer(dense, scale, sparse_data, quantize=True, scale_out=scale,
@@ -225,6 +233,6 @@ def quantize_and_compress(
                       sparse_data.err_flags, write_vals=True, quantize=True, scale_out=scale,
                       dense_q_out=q, amax_epoch=amax_epoch, **fused)
     sparse_data.offset = new_offset
-    sp = BitsparseTensor(sparse_data.vals, bitmask, prefix, q.shape, q.dtype, grid_m, grid_n,
+    sp = BitsparseTensor(sparse_data.vals, bitmask, prefix, (M, N), torch.float8_e4m3fn, grid_m, grid_n,
                          BLOCK_M, BLOCK_N, scale=scale, vals_offset=vals_offset)
     return q, scale, sp

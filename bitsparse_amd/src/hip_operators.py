@@ -193,7 +193,7 @@ def amax_into_workspace(x: Tensor, relu: bool = False) -> int:
     L = _lib.load()
     ws = _lib.workspace_for(x.device)
     ws.ensure(256)
-    epoch = ws.next_epoch()
+    epoch = ws.next_epoch(reserve=2)     # the compress that reads this amax takes the next one
     fn = L.bs_amax_relu if relu else L.bs_amax
     check(fn(x.data_ptr(), x.numel(), ws.buf.data_ptr(), ws.nbytes, epoch,
              stream_handle(x.device)), "bs_amax")

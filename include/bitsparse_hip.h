@@ -10,7 +10,7 @@
  *     returns an int status: BS_OK, or an error code with a message available
  *     from bs_last_error() (thread local).  Argument checks happen on the
  *     host before anything is enqueued; a failed call enqueues nothing.
- *   - dtype codes are the reference's codec ids (lib_sparse/bitsparse.py:20-30):
+ *   - dtype codes are the reference's codec ids (lib_sparse/bitsparse.py:8-18):
  *     0 = bf16, 1 = float8_e4m3fn, 2 = float8_e5m2.
  *   - matrices are dense, row-major, contiguous ([rows, cols], row stride =
  *     cols), as the reference kernels assume (triton_kernels.py:82).
@@ -19,7 +19,7 @@
  *     BS_ERR_INVALID.  The reference's int32 element offsets
  *     (triton_kernels.py:80) bound it to the same range.
  *
- * Compressed format (reference triton_kernels.py:1-17, bitsparse.py:132-139):
+ * Compressed format (reference triton_kernels.py:1-17, bitsparse.py:120-127):
  *   64x64 tiles, T = ceil(M/64)*ceil(N/64), tile t = tm*grid_n + tn;
  *   bitmask  uint8[T*512]: bit (f%8) of byte t*512 + f/8 is [x > 0] for
  *            tile-flat index f = r*64 + c;

@@ -9,7 +9,7 @@
  * Plain C99, single-threaded, no dependencies.  Element types are carried as
  * raw bit patterns: bf16 = uint16_t, e4m3fn / e5m2 = uint8_t.
  *
- * Format (reference lib_sparse/src/triton_kernels.py:1-17, bitsparse.py:132-139):
+ * Format (reference lib_sparse/src/triton_kernels.py:1-17, bitsparse.py:120-127):
  *   tiles are 64x64, tile id t = tm*grid_n + tn (row-major over the tile grid);
  *   inside a tile the flat index is f = r*64 + c;
  *   bitmask byte t*512 + f/8, bit f%8 (LSB first) is [x > 0];

@@ -17,7 +17,7 @@ against torch's own CPU casts (fp8 / bf16 rounding) and against invariants
 (round trip, popcount == nnz, monotone prefix).
 
 Every array is a raw bit pattern: bf16 -> uint16, e4m3fn / e5m2 -> uint8.
-Codec ids follow reference ``lib_sparse/bitsparse.py:20-30`` (0 bf16,
+Codec ids follow reference ``lib_sparse/bitsparse.py:8-18`` (0 bf16,
 1 e4m3fn, 2 e5m2).
 """
 from __future__ import annotations
@@ -190,7 +190,7 @@ def relu2_grad(grad: np.ndarray, vals: np.ndarray, vdtype: int, bitmask: np.ndar
 
 
 def bits_per_value(dtype: int) -> int:
-    """Stored bits per value of the packed stream (reference bitsparse.py:15-23)."""
+    """Stored bits per value of the packed stream (reference bitsparse.py:21-23)."""
     return 15 if dtype == BF16 else 7
 
 

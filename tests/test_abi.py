@@ -133,7 +133,7 @@ def test_container_helpers_match_reference_definitions():
     assert [bits_per_value(d) for d in (torch.bfloat16, torch.float8_e4m3fn)] == [15, 7]
     with pytest.raises(ValueError):
         TensorBuffer(3, device="cpu", dtype=torch.bfloat16)
-    # vram_size = nnz*vb + T*512 + 4*(T+1) (reference bitsparse.py:88-96), on
+    # vram_size = nnz*vb + T*512 + 4*(T+1) (reference bitsparse.py:76-84), on
     # a container filled from the oracle
     x = relu_input((129, 131), 0.5, seed=0)
     bm, pf, v = O.compress(bits(x), O.BF16)

@@ -132,3 +132,29 @@ def test_gemm_relu2_nonfinite_scale_matches_decompress(dev):
     C = dw_gemm.gemm_compressed_b(A, sp, square=True)
     assert torch.equal(torch.isnan(C), torch.isnan(ref))
     assert torch.equal(torch.isinf(C), torch.isinf(ref))
+
+
+def test_gemm_empty_k_under_graph_capture(dev):
+    """K = 0 (an empty compressed operand): C = 0, written by a kernel, so
+    the call captures into a HIP graph; every replay rewrites the zeros."""
+    from bitsparse_amd.src import dw_gemm
+    from bitsparse_amd.src.functions import dense_to_tilesparse
+    M, N = 96, 130
+    sp = dense_to_tilesparse(torch.zeros((0, N), dtype=torch.bfloat16, device=dev), None)
+    A = torch.empty((M, 0), dtype=torch.bfloat16, device=dev)
+    C = dw_gemm.gemm_compressed_b(A, sp, square=False)
+    assert C.shape == (M, N) and bool((C == 0).all())
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        dw_gemm.gemm_compressed_b(A, sp, square=False)          # warm-up off the graph
+    torch.cuda.current_stream().wait_stream(side)
+    with torch.cuda.graph(graph):
+        out = dw_gemm.gemm_compressed_b(A, sp, square=False)
+    for _ in range(3):
+        out.fill_(7.0)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert bool((out == 0).all())

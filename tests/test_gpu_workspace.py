@@ -56,3 +56,24 @@ def test_epoch_tagged_entry_points_refuse_graph_capture(dev):
     again = dense_to_tilesparse(x, None, buf)
     assert torch.equal(again.bitmask, ref.bitmask) and torch.equal(again.prefix, ref.prefix)
     assert torch.equal(again.vals[:x.numel()], ref.vals[:x.numel()])
+
+
+def test_epoch_wrap_between_amax_and_compress(dev):
+    """The workspace epoch wraps (buffer zeroed) only where no amax is
+    pending: an amax taken at the last epoch still reaches its compress."""
+    import torch
+    from bitsparse_amd import _lib
+    from bitsparse_amd.fp8 import to_fp8
+    from bitsparse_amd.src.functions import dense_to_tilesparse, quantize_and_compress
+    from tests.helpers import preact_input
+    x = (preact_input((256, 512), seed=7).relu() * 5).to(dev)
+    q_ref, s_ref = to_fp8(x)
+    sp_ref = dense_to_tilesparse(q_ref, s_ref)
+    for start in (_lib._EPOCH_LIMIT - 2, _lib._EPOCH_LIMIT - 1, _lib._EPOCH_LIMIT):
+        ws = _lib.workspace_for(x.device)
+        ws.epoch = start
+        q, s, sp = quantize_and_compress(x, None)
+        assert torch.equal(s, s_ref)
+        assert torch.equal(q.view(torch.uint8), q_ref.view(torch.uint8))
+        assert torch.equal(sp.bitmask, sp_ref.bitmask) and torch.equal(sp.prefix, sp_ref.prefix)
+        assert ws.epoch <= _lib._EPOCH_LIMIT
