@@ -17,7 +17,7 @@ LIB_NAME = "libbitsparse_hip.so"
 # BITSPARSE_HIP_LIB points at another build of the same sources (tuning sweeps)
 LIB_PATH = os.environ.get("BITSPARSE_HIP_LIB") or os.path.join(
     os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 BS_OK = 0
 BS_ERR_INVALID = 1
@@ -62,6 +62,9 @@ _SIGNATURES = {
     "bs_relu2_grad_packed": [_vp, _i64, _i64, _vp, _int, _i64, _vp, _vp, _vp, _f32, _vp, _vp],
     "bs_workspace_amax_slot": [_vp, _i64],
     "bs_workspace_fallback_counter": [_vp, _i64],
+    "bs_compress_noalloc": [_vp, _int, _i64, _i64, _int, _int, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _int,
+                            _vp, _vp, _int, _vp, _vp, _vp],
+    "bs_compress_noalloc_max_tiles": [],
     "bs_launch_timing": [_int],
     "bs_launch_timing_read": [_vp, _vp, _int, _vp],
 }
@@ -69,6 +72,7 @@ _RESTYPES = {
     "bs_last_error": ctypes.c_char_p,
     "bs_compress_workspace_bytes": _i64,
     "bs_gemm_compressed_b_workspace_bytes": _i64,
+    "bs_compress_noalloc_max_tiles": _i64,
     "bs_workspace_amax_slot": _vp,
     "bs_workspace_fallback_counter": _vp,
 }

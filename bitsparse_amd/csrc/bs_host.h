@@ -49,6 +49,15 @@ inline void launch_timed(int kind, F kernel, dim3 grid, dim3 block, uint32_t shm
 // the same epoch and take the previous replay's values for current ones.
 int refuse_capture(hipStream_t stream, const char* what);
 
+// The device a stream belongs to (the current device for the null stream).
+hipError_t stream_device(hipStream_t stream, int* dev);
+
+// amax of a bf16 array (of relu(x) with `relu`) into the amax slot of
+// `workspace` under `epoch` (bs_amax / bs_amax_relu without clear_error();
+// `check_capture` = refuse a capturing stream).
+int amax_launch(const void* x, int64_t n, void* workspace, int64_t workspace_bytes, uint32_t epoch,
+                void* stream, bool relu, bool check_capture);
+
 // Records a formatted message for bs_last_error() and returns `code`.
 int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 void clear_error();

@@ -13,6 +13,8 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <functional>
+#include <mutex>
 
 
 namespace bs {
@@ -1502,6 +1504,18 @@ __global__ __launch_bounds__(kThreads) void relu_grad_kernel(uint8_t* grad, int6
         }
 }
 
+// Empty input (T = 0): prefix = [0]; the cursor outputs take the input
+// cursor (or 0) unchanged.
+__global__ void empty_compress_kernel(uint32_t* prefix, const int64_t* offset_in, int64_t* offset_out,
+                                      int64_t* start_out)
+{
+    if (threadIdx.x != 0) return;
+    prefix[0] = 0u;
+    const int64_t c = offset_in ? *offset_in : 0;
+    if (offset_out) *offset_out = c;
+    if (start_out) *start_out = c;
+}
+
 // ===========================================================================
 // host launchers
 // ===========================================================================
@@ -1587,9 +1601,9 @@ static int compress_impl(const void* dense, int in_dtype, int64_t M, int64_t N, 
                          int64_t vals_capacity, const int64_t* vals_offset_in, int align8,
                          int64_t* vals_offset_out, int64_t* vals_start_out, int write_vals,
                          int32_t* err_flags, void* workspace, int64_t workspace_bytes,
-                         uint32_t epoch, void* stream, bool relu, void* relu_out, bool packed = false)
+                         uint32_t epoch, void* stream, bool relu, void* relu_out, bool packed = false,
+                         bool check_capture = true, const std::function<int()>& before_launch = nullptr)
 {
-    clear_error();
     if (packed) {
         // vals is the packed stream and vals_capacity its size in bytes
         if (!write_vals) return set_error(BS_ERR_INVALID, "bs_compress_packed: write_vals must be 1");
@@ -1619,7 +1633,9 @@ static int compress_impl(const void* dense, int in_dtype, int64_t M, int64_t N, 
         return set_error(BS_ERR_INVALID, "bs_compress: vals_offset_out aliases vals_offset_in");
     if (epoch == 0 || epoch >= (1u << 30))
         return set_error(BS_ERR_INVALID, "bs_compress: epoch must be in [1, 2^30)");
-    if (int rc = refuse_capture((hipStream_t)stream, "bs_compress")) return rc;
+    if (check_capture) {
+        if (int rc = refuse_capture((hipStream_t)stream, "bs_compress")) return rc;
+    }
     if (workspace == nullptr || workspace_bytes < bs_compress_workspace_bytes(M, N))
         return set_error(BS_ERR_INVALID, "bs_compress: workspace too small (%lld < %lld bytes)",
                          (long long)workspace_bytes, (long long)bs_compress_workspace_bytes(M, N));
@@ -1627,17 +1643,16 @@ static int compress_impl(const void* dense, int in_dtype, int64_t M, int64_t N, 
     if (write_vals && !packed && ((uintptr_t)vals) % outb)
         return set_error(BS_ERR_INVALID, "bs_compress: vals not aligned to its element size");
     hipStream_t st = (hipStream_t)stream;
+    // every argument is checked: launches may start (the caller's own first)
+    if (before_launch) {
+        if (int rc = before_launch()) return rc;
+    }
     if (T == 0) {
-        // empty input: prefix = [0], cursor unchanged
-        hipError_t e = hipMemsetAsync(prefix, 0, 4, st);
-        if (e == hipSuccess && vals_offset_out) {
-            if (vals_offset_in) e = hipMemcpyAsync(vals_offset_out, vals_offset_in, 8, hipMemcpyDeviceToDevice, st);
-            else e = hipMemsetAsync(vals_offset_out, 0, 8, st);
-        }
-        if (e == hipSuccess && vals_start_out) {
-            if (vals_offset_in) e = hipMemcpyAsync(vals_start_out, vals_offset_in, 8, hipMemcpyDeviceToDevice, st);
-            else e = hipMemsetAsync(vals_start_out, 0, 8, st);
-        }
+        // empty input: prefix = [0], cursor unchanged (one small kernel, so the
+        // no-allocation variant stays capturable)
+        hipLaunchKernelGGL(empty_compress_kernel, dim3(1), dim3(64), 0, st, prefix, vals_offset_in,
+                           vals_offset_out, vals_start_out);
+        hipError_t e = hipGetLastError();
         return e == hipSuccess ? BS_OK : set_error(BS_ERR_HIP, "bs_compress: %s", hipGetErrorString(e));
     }
     CompressArgs a{};
@@ -1692,6 +1707,7 @@ extern "C" int bs_compress(const void* dense, int in_dtype, int64_t M, int64_t N
                            int32_t* err_flags, void* workspace, int64_t workspace_bytes,
                            uint32_t epoch, void* stream)
 {
+    clear_error();
     return compress_impl(dense, in_dtype, M, N, quantize, amax_slot, amax_epoch, scale_out, dense_q_out,
                          bitmask, prefix, vals, vals_capacity, vals_offset_in, align8, vals_offset_out,
                          vals_start_out, write_vals, err_flags, workspace, workspace_bytes, epoch, stream,
@@ -1706,6 +1722,7 @@ extern "C" int bs_compress_relu(const void* preact, int in_dtype, int64_t M, int
                                 int32_t* err_flags, void* workspace, int64_t workspace_bytes,
                                 uint32_t epoch, void* relu_out, void* stream)
 {
+    clear_error();
     return compress_impl(preact, in_dtype, M, N, quantize, amax_slot, amax_epoch, scale_out, dense_q_out,
                          bitmask, prefix, vals, vals_capacity, vals_offset_in, align8, vals_offset_out,
                          vals_start_out, write_vals, err_flags, workspace, workspace_bytes, epoch, stream,
@@ -1720,6 +1737,7 @@ extern "C" int bs_compress_packed(const void* dense, int in_dtype, int64_t M, in
                                   void* workspace, int64_t workspace_bytes, uint32_t epoch, int relu,
                                   void* relu_out, void* stream)
 {
+    clear_error();
     return compress_impl(dense, in_dtype, M, N, quantize, amax_slot, amax_epoch, scale_out, dense_q_out,
                          bitmask, prefix, stream_bytes, stream_nbytes, vals_offset_in, 1, vals_offset_out,
                          vals_start_out, 1, err_flags, workspace, workspace_bytes, epoch, stream,
@@ -2052,4 +2070,98 @@ extern "C" int bs_pack_bits(const void* raw, int vals_dtype, const uint32_t* cou
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(BS_ERR_HIP, "bs_pack_bits launch: %s", hipGetErrorString(e));
     return BS_OK;
+}
+
+// ===========================================================================
+// bs_compress_noalloc: bs_compress / bs_compress_relu with the look-back
+// status words and the amax slot in a library-owned device array instead of
+// a caller-allocated workspace.  Each call clears the part of the array it
+// uses (one small kernel) and runs with epoch 1, so no state carries over
+// between calls and the call sequence can be captured into a HIP graph.
+// ===========================================================================
+namespace bs {
+
+constexpr int64_t kScratchMaxTiles = int64_t(1) << 19;                 // 2^31 elements in 64x64 tiles
+constexpr int64_t kScratchBytes = kWsHeaderBytes + 8 * (kScratchMaxTiles + 2);
+constexpr int kScratchMaxDevices = 64;
+
+// One copy per GPU, held until the process ends.  Host code never uses this
+// name as an address: scratch_base() looks the device address up once per
+// device with hipGetSymbolAddress.
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kScratchMaxDevices];
+
+// Device address of `scratch` on the device of `st`.
+static int scratch_base(hipStream_t st, uint8_t** out)
+{
+    int dev = 0;
+    hipError_t e = stream_device(st, &dev);
+    if (e != hipSuccess) return set_error(BS_ERR_HIP, "bs_compress_noalloc: stream device: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kScratchMaxDevices)
+        return set_error(BS_ERR_INVALID, "bs_compress_noalloc: device %d beyond %d", dev, kScratchMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        int cur = 0;
+        e = hipGetDevice(&cur);
+        if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
+        void* p = nullptr;
+        if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (cur != dev) (void)hipSetDevice(cur);
+        if (e != hipSuccess || p == nullptr)
+            return set_error(BS_ERR_HIP, "bs_compress_noalloc: scratch address: %s", hipGetErrorString(e));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = static_cast<uint8_t*>(g_scratch_ptr[dev]);
+    return BS_OK;
+}
+
+__global__ __launch_bounds__(256) void zero_words_kernel(uint64_t* p, int64_t n)
+{
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) p[i] = 0ull;
+}
+
+}  // namespace bs
+
+extern "C" int64_t bs_compress_noalloc_max_tiles(void) { return kScratchMaxTiles; }
+
+extern "C" int bs_compress_noalloc(const void* dense, int in_dtype, int64_t M, int64_t N, int quantize, int relu,
+                                   float* scale_out, void* dense_q_out, uint8_t* bitmask, uint32_t* prefix,
+                                   void* vals, int64_t vals_capacity, const int64_t* vals_offset_in, int align8,
+                                   int64_t* vals_offset_out, int64_t* vals_start_out, int write_vals,
+                                   int32_t* err_flags, void* relu_out, void* stream)
+{
+    clear_error();
+    if (M < 0 || N < 0) return set_error(BS_ERR_INVALID, "bs_compress_noalloc: negative shape");
+    const int64_t T = ((M + 63) / 64) * ((N + 63) / 64);
+    if (T > kScratchMaxTiles)
+        return set_error(BS_ERR_INVALID, "bs_compress_noalloc: %lld tiles, at most %lld (the scratch array's size)",
+                         (long long)T, (long long)kScratchMaxTiles);
+    if (quantize && in_dtype != DT_BF16)
+        return set_error(BS_ERR_INVALID, "bs_compress_noalloc: quantize needs bf16 input");
+    if (quantize && ((uintptr_t)dense) & 1u) return set_error(BS_ERR_INVALID, "bs_compress_noalloc: input misaligned");
+    hipStream_t st = (hipStream_t)stream;
+    uint8_t* ws = nullptr;
+    if (int rc = scratch_base(st, &ws)) return rc;
+    constexpr uint32_t kEpoch = 1;
+    // after compress_impl has checked every argument: clear the header (amax
+    // slot, fallback counter) and the status words this shape uses (one per
+    // unit of kStreamU tiles, one per unit group), then the amax if quantizing
+    auto prepare = [&]() -> int {
+        const int64_t units = (T + kStreamU - 1) / kStreamU;
+        const int64_t words = kWsHeaderBytes / 8 + units + (units + kGroupUnits - 1) / kGroupUnits + 2;
+        const uint32_t nblk = (uint32_t)std::min<int64_t>((words + 255) / 256, 1024);
+        hipLaunchKernelGGL(zero_words_kernel, dim3(nblk), dim3(256), 0, st, reinterpret_cast<uint64_t*>(ws), words);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return set_error(BS_ERR_HIP, "bs_compress_noalloc launch: %s", hipGetErrorString(e));
+        if (quantize) return amax_launch(dense, M * N, ws, kScratchBytes, kEpoch, stream, relu != 0, false);
+        return BS_OK;
+    };
+    const uint64_t* slot = reinterpret_cast<const uint64_t*>(ws + kWsAmaxOffset);
+    return compress_impl(dense, in_dtype, M, N, quantize, quantize ? slot : nullptr, kEpoch, scale_out, dense_q_out,
+                         bitmask, prefix, vals, vals_capacity, vals_offset_in, align8, vals_offset_out,
+                         vals_start_out, write_vals, err_flags, ws, kScratchBytes, kEpoch, stream, relu != 0,
+                         relu_out, false, false, prepare);
 }

@@ -118,21 +118,22 @@ static uint32_t grid_for(int64_t n)
 
 using namespace bs;
 
-static int amax_impl(const void* x, int64_t n, void* workspace, int64_t workspace_bytes, uint32_t epoch,
-                     void* stream, bool relu)
+int bs::amax_launch(const void* x, int64_t n, void* workspace, int64_t workspace_bytes, uint32_t epoch,
+                    void* stream, bool relu, bool check_capture)
 {
-    clear_error();
     if (n < 0) return set_error(BS_ERR_INVALID, "bs_amax: negative n");
     if (workspace == nullptr || workspace_bytes < kWsHeaderBytes)
         return set_error(BS_ERR_INVALID, "bs_amax: workspace too small");
     if (epoch == 0 || epoch >= (1u << 30)) return set_error(BS_ERR_INVALID, "bs_amax: epoch out of range");
     if (n > 0 && x == nullptr) return set_error(BS_ERR_INVALID, "bs_amax: null input");
     if (((uintptr_t)x) & 1u) return set_error(BS_ERR_INVALID, "bs_amax: input misaligned");
-    if (int rc = refuse_capture((hipStream_t)stream, "bs_amax")) return rc;
+    if (check_capture) {
+        if (int rc = refuse_capture((hipStream_t)stream, "bs_amax")) return rc;
+    }
     if (n == 0) return BS_OK;   // slot keeps an older epoch: readers then see amax = 0
     uint64_t* slot = reinterpret_cast<uint64_t*>((uint8_t*)workspace + kWsAmaxOffset);
     int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
+    if (stream_device((hipStream_t)stream, &dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
         cus = 256;
     uint32_t grid = grid_for(n);
@@ -151,13 +152,15 @@ static int amax_impl(const void* x, int64_t n, void* workspace, int64_t workspac
 extern "C" int bs_amax(const void* x, int64_t n, void* workspace, int64_t workspace_bytes, uint32_t epoch,
                        void* stream)
 {
-    return amax_impl(x, n, workspace, workspace_bytes, epoch, stream, false);
+    clear_error();
+    return amax_launch(x, n, workspace, workspace_bytes, epoch, stream, false, true);
 }
 
 extern "C" int bs_amax_relu(const void* preact, int64_t n, void* workspace, int64_t workspace_bytes,
                             uint32_t epoch, void* stream)
 {
-    return amax_impl(preact, n, workspace, workspace_bytes, epoch, stream, true);
+    clear_error();
+    return amax_launch(preact, n, workspace, workspace_bytes, epoch, stream, true, true);
 }
 
 extern "C" int bs_quantize_e4m3fn(const void* x, int64_t n, void* q_out, float* scale_out,

@@ -58,6 +58,12 @@ bool timing_next(int kind, hipEvent_t* start, hipEvent_t* stop)
     return true;
 }
 
+hipError_t stream_device(hipStream_t stream, int* dev)
+{
+    if (stream == nullptr) return hipGetDevice(dev);
+    return hipStreamGetDevice(stream, dev);
+}
+
 int refuse_capture(hipStream_t stream, const char* what)
 {
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
@@ -78,7 +84,7 @@ using namespace bs;
 
 extern "C" const char* bs_last_error(void) { return bs::g_err; }
 
-extern "C" int bs_abi_version(void) { return 5; }
+extern "C" int bs_abi_version(void) { return 6; }
 
 extern "C" int bs_launch_timing(int enable)
 {

@@ -315,6 +315,31 @@ int bs_relu2_grad_packed(void* grad, int64_t M, int64_t N, const void* stream_by
                          const int64_t* vals_offset, float relu2_scale, const float* scale,
                          void* stream);
 
+/*
+ * bs_compress_noalloc — no counterpart in the reference.  For callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc): bs_compress / bs_compress_relu
+ * with the look-back status words and the fp8 amax slot in a library-owned
+ * device array (one per GPU, 4 MiB + 272 bytes, kept until the process ends)
+ * instead of a caller-allocated workspace.  The call allocates nothing.
+ *   quantize   1: bf16 input quantized to e4m3fn; the amax pass (of relu(x)
+ *              with relu) runs inside the call on the same array
+ *   relu       1: `dense` is the pre-activation z, as for bs_compress_relu
+ *              (`relu_out` nullable); 0: `relu_out` must be NULL
+ * Other arguments as for bs_compress.  Shapes of more than
+ * bs_compress_noalloc_max_tiles() = 2^19 tiles are refused (BS_ERR_INVALID).
+ * Each call clears the part of the array it uses before its kernels run, so
+ * no state carries over and the call can be captured into a HIP graph; but
+ * all calls on one GPU share the array, so calls that overlap on one GPU
+ * (two streams, two threads) race and must be serialised by the caller.
+ */
+int bs_compress_noalloc(const void* dense, int in_dtype, int64_t M, int64_t N, int quantize, int relu,
+                        float* scale_out, void* dense_q_out, uint8_t* bitmask, uint32_t* prefix,
+                        void* vals, int64_t vals_capacity, const int64_t* vals_offset_in, int align8,
+                        int64_t* vals_offset_out, int64_t* vals_start_out, int write_vals,
+                        int32_t* err_flags, void* relu_out, void* stream);
+int64_t bs_compress_noalloc_max_tiles(void);
+
 /* Device pointer of the amax slot inside a workspace (for bs_compress). */
 const uint64_t* bs_workspace_amax_slot(const void* workspace, int64_t workspace_bytes);
 
