@@ -183,6 +183,15 @@ __device__ __forceinline__ uint32_t get8(const uint2 v, int e)
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }
 
+// Lane 0's value of a uint32 in every lane (a scalar register).  The builtin
+// takes and returns int, so a value of 2^31 or more (a tile prefix, which
+// reaches 2^32 - 1) must be widened from the unsigned result: converting the
+// int straight to int64 sign-extends it.
+__device__ __forceinline__ uint32_t uniform_u32(uint32_t x)
+{
+    return (uint32_t)__builtin_amdgcn_readfirstlane((int)x);
+}
+
 // number of set bits of `m` in lanes strictly below this lane
 __device__ __forceinline__ uint32_t popc_below(uint64_t m)
 {

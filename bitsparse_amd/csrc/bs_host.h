@@ -18,12 +18,11 @@ constexpr int64_t kWsAmaxOffset = 0;
 constexpr int64_t kWsFallbackOffset = 8;
 
 // Largest matrix accepted by the codec, gradient and GEMM entry points:
-// fewer than 2^31 elements.  The reference forms element offsets in int32
-// (lib_sparse/src/triton_kernels.py:80), so this is its domain as well.  The
-// kernels here index with 64-bit offsets and a uint32 prefix, but a GPU run at
-// 2^31 + 2^21 elements faulted without a cause found in this code, so shapes
-// from 2^31 elements up are refused until such a run passes.
-constexpr uint64_t kMaxElems = 1ull << 31;
+// fewer than 2^32 elements, the range of the uint32 tile prefix (the kernels
+// index HBM with 64-bit element offsets).  The reference forms element
+// offsets in int32 (lib_sparse/src/triton_kernels.py:80), so its domain ends
+// at 2^31.
+constexpr uint64_t kMaxElems = 1ull << 32;
 
 // Launch timing (bs_launch_timing): the next start/stop event pair for a
 // kernel launch of the given kind (0 compress, 1 decompress), or false when

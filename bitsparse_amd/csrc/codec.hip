@@ -289,8 +289,8 @@ __device__ uint32_t unit_count_wave(const CompressArgs& a, uint32_t q, float sca
 
 __device__ __forceinline__ uint64_t bcast_lane0(uint64_t v)
 {
-    uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
-    uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    const uint32_t lo = uniform_u32((uint32_t)v);
+    const uint32_t hi = uniform_u32((uint32_t)(v >> 32));
     return ((uint64_t)hi << 32) | lo;
 }
 
@@ -851,12 +851,11 @@ void compress_stream_kernel(CompressArgs a)
                 if constexpr (MODE == MODE_VALS)
                     g = start + (int64_t)(a.prefix[t] - a.prefix[a.tile0]);
                 else
-                    g = start + (int64_t)__builtin_amdgcn_readfirstlane(s_excl[0]) +
-                        (int64_t)__builtin_amdgcn_readfirstlane(s_toff[wave]);
+                    g = start + (int64_t)uniform_u32(s_excl[0]) + (int64_t)uniform_u32(s_toff[wave]);
                 const int cnt = (int)P[8];
                 if constexpr (PACKED) {
                     stream_packed<OUTB, TR::PB, U>(a, g, cnt, P, mp, o, s_ring + wave * (kRingElems * OUTB), lane,
-                                                   start + (int64_t)__builtin_amdgcn_readfirstlane(s_excl[0]),
+                                                   start + (int64_t)uniform_u32(s_excl[0]),
                                                    s_toff, s_edge);
                 } else {
                 if (MODE == MODE_VALS && a.err && lane == 0 && g + cnt > a.vals_capacity) atomicOr(a.err, 1);
@@ -1588,7 +1587,7 @@ static int check_dense(const void* dense, int dtype, int64_t M, int64_t N, const
     if (M < 0 || N < 0) return set_error(BS_ERR_INVALID, "%s: negative shape", what);
     if ((M > 0 && N > 0) && dense == nullptr) return set_error(BS_ERR_INVALID, "%s: null input", what);
     if ((uint64_t)M * (uint64_t)N >= kMaxElems)
-        return set_error(BS_ERR_INVALID, "%s: M*N must be < 2^31", what);
+        return set_error(BS_ERR_INVALID, "%s: M*N must be < 2^32", what);
     int elem = dtype == DT_BF16 ? 2 : 1;
     if (((uintptr_t)dense) % elem)
         return set_error(BS_ERR_INVALID, "%s: input not aligned to its element size", what);
@@ -1869,7 +1868,7 @@ static int decompress_impl(const void* vals, int vals_dtype, int64_t vals_numel,
     if ((uint64_t)(first_m_tile * grid_n + num_tiles_in_batch) >= (1ull << 32))
         return set_error(BS_ERR_INVALID, "bs_decompress: tile ids exceed 32 bits");
     if ((uint64_t)batch_rows * (uint64_t)K >= kMaxElems)
-        return set_error(BS_ERR_INVALID, "bs_decompress: batch_rows*K must be < 2^31");
+        return set_error(BS_ERR_INVALID, "bs_decompress: batch_rows*K must be < 2^32");
     const int ob = square ? 2 : (vals_dtype == DT_BF16 ? 2 : 1);
     if (((uintptr_t)out) % ob) return set_error(BS_ERR_INVALID, "bs_decompress: output misaligned");
     GatherArgs a{};
@@ -1938,7 +1937,7 @@ extern "C" int bs_relu_grad(void* grad, int64_t M, int64_t N, const uint8_t* bit
     if (T == 0) return BS_OK;
     if (grad == nullptr || bitmask == nullptr) return set_error(BS_ERR_INVALID, "bs_relu_grad: null pointer");
     if ((uint64_t)M * (uint64_t)N >= kMaxElems)
-        return set_error(BS_ERR_INVALID, "bs_relu_grad: M*N must be < 2^31");
+        return set_error(BS_ERR_INVALID, "bs_relu_grad: M*N must be < 2^32");
     if (((uintptr_t)grad) & 1u) return set_error(BS_ERR_INVALID, "bs_relu_grad: grad misaligned");
     bool vec = (N % 8 == 0) && aligned16(grad);
     uint32_t gn = (uint32_t)((N + 63) / 64);
@@ -1984,7 +1983,7 @@ static int relu2_grad_impl(void* grad, int64_t M, int64_t N, const void* vals, i
     if (T == 0) return BS_OK;
     if (grad == nullptr) return set_error(BS_ERR_INVALID, "bs_relu2_grad: null grad");
     if ((uint64_t)M * (uint64_t)N >= kMaxElems)
-        return set_error(BS_ERR_INVALID, "bs_relu2_grad: M*N must be < 2^31");
+        return set_error(BS_ERR_INVALID, "bs_relu2_grad: M*N must be < 2^32");
     if (((uintptr_t)grad) & 1u) return set_error(BS_ERR_INVALID, "bs_relu2_grad: grad misaligned");
     GatherArgs a{};
     a.vals = (const uint8_t*)vals;
@@ -2081,7 +2080,7 @@ extern "C" int bs_pack_bits(const void* raw, int vals_dtype, const uint32_t* cou
 // ===========================================================================
 namespace bs {
 
-constexpr int64_t kScratchMaxTiles = int64_t(1) << 19;                 // 2^31 elements in 64x64 tiles
+constexpr int64_t kScratchMaxTiles = int64_t(1) << 19;                 // 2^31 elements in 64x64 tiles (half the codec range)
 constexpr int64_t kScratchBytes = kWsHeaderBytes + 8 * (kScratchMaxTiles + 2);
 constexpr int kScratchMaxDevices = 64;
 

@@ -894,7 +894,7 @@ extern "C" int bs_gemm_compressed_b(const void* A, int64_t M, int64_t K, int64_t
     if (a_layout == 1 && K % 8 != 0)
         return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: a_layout 1 needs K %% 8 == 0");
     if ((uint64_t)K * (uint64_t)N >= kMaxElems)
-        return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: K*N must be < 2^31");
+        return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: K*N must be < 2^32");
     if (M == 0 || N == 0) return BS_OK;
     if (C == nullptr) return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: null C");
     if (((uintptr_t)C) & 1) return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: C misaligned");

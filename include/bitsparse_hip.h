@@ -15,9 +15,10 @@
  *   - matrices are dense, row-major, contiguous ([rows, cols], row stride =
  *     cols), as the reference kernels assume (triton_kernels.py:82).
  *   - a matrix handed to the codec, gradient or GEMM entry points holds
- *     fewer than 2^31 elements (M*N, batch_rows*K, K*N); larger shapes return
- *     BS_ERR_INVALID.  The reference's int32 element offsets
- *     (triton_kernels.py:80) bound it to the same range.
+ *     fewer than 2^32 elements (M*N, batch_rows*K, K*N), the range of the
+ *     uint32 tile prefix; larger shapes return BS_ERR_INVALID.  The
+ *     reference's int32 element offsets (triton_kernels.py:80) end its range
+ *     at 2^31.
  *
  * Compressed format (reference triton_kernels.py:1-17, bitsparse.py:120-127):
  *   64x64 tiles, T = ceil(M/64)*ceil(N/64), tile t = tm*grid_n + tn;

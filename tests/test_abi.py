@@ -72,25 +72,26 @@ def test_invalid_arguments_rejected_on_host():
     rc = L.bs_compress(fake, 0, 64, 64, 0, None, 0, None, None, fake, fake, fake, 10, None, 0,
                        None, None, 1, None, fake, 1 << 20, 0, None)
     assert rc == _lib.BS_ERR_INVALID and "epoch" in _err()
-    # matrices of 2^31 elements or more are refused by every codec / GEMM entry
-    big_m, big_n = 1 << 15, 1 << 16
+    # matrices of 2^32 elements or more (the uint32 prefix's range) are
+    # refused by every codec / GEMM entry
+    big_m, big_n = 1 << 16, 1 << 16
     rc = L.bs_tile_pack(fake, 0, big_m, big_n, fake, fake, None)
-    assert rc == _lib.BS_ERR_INVALID and "2^31" in _err()
+    assert rc == _lib.BS_ERR_INVALID and "2^32" in _err()
     rc = L.bs_compress(fake, 0, big_m, big_n, 0, None, 0, None, None, fake, fake, fake, 10, None, 0,
                        None, None, 1, None, fake, 1 << 30, 1, None)
-    assert rc == _lib.BS_ERR_INVALID and "2^31" in _err()
+    assert rc == _lib.BS_ERR_INVALID and "2^32" in _err()
     rc = L.bs_compact_vals(fake, 0, big_m, big_n, fake, fake, fake, 10, None, 0, 1, None, None)
-    assert rc == _lib.BS_ERR_INVALID and "2^31" in _err()
+    assert rc == _lib.BS_ERR_INVALID and "2^32" in _err()
     rc = L.bs_decompress(fake, 0, 10, fake, fake, None, fake, 0, big_n // 64, big_n, big_m, 64, 0, 1.0,
                          None, None)
-    assert rc == _lib.BS_ERR_INVALID and "2^31" in _err()
+    assert rc == _lib.BS_ERR_INVALID and "2^32" in _err()
     rc = L.bs_relu_grad(fake, big_m, big_n, fake, None)
-    assert rc == _lib.BS_ERR_INVALID and "2^31" in _err()
+    assert rc == _lib.BS_ERR_INVALID and "2^32" in _err()
     rc = L.bs_relu2_grad(fake, big_m, big_n, fake, 0, 10, fake, fake, None, 1.0, None, None)
-    assert rc == _lib.BS_ERR_INVALID and "2^31" in _err()
+    assert rc == _lib.BS_ERR_INVALID and "2^32" in _err()
     rc = L.bs_gemm_compressed_b(fake, 64, big_m, 64, 0, fake, 0, 10, fake, fake, None, big_n, 0, 1.0,
                                 None, fake, fake, 1 << 30, None)
-    assert rc == _lib.BS_ERR_INVALID and "2^31" in _err()
+    assert rc == _lib.BS_ERR_INVALID and "2^32" in _err()
     # aliasing cursors
     rc = L.bs_compress(fake, 0, 64, 64, 0, None, 0, None, None, fake, fake, fake, 10, fake + 64, 0,
                        fake + 64, None, 1, None, fake, 1 << 20, 1, None)

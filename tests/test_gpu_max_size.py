@@ -2,15 +2,15 @@
 offsets and a uint32 prefix.  These shapes check that every element offset
 and every prefix value above 2^31 is carried without wrapping.
 
-Skipped: the first GPU run of the codec case faulted the GPU (the box was
-ended, so its log did not come back) and reading the kernels, their generated
-address arithmetic and the host checks found no cause.  The C ABI therefore
-refuses matrices of 2^31 elements or more (the reference's int32 element
-offsets bound it to the same range) and these tests stay skipped until the
-cause is known.  The oracle is far too slow at this size, so the checks are
-size-independent properties computed with torch ops on the GPU: the exact
-round trip, the bitmask and prefix rebuilt from the dense input, the tile-major
-value order, and the GEMM against an fp32 product on the decompressed operand.
+Regression: compress once broadcast the unit's exclusive prefix (a uint32)
+through __builtin_amdgcn_readfirstlane, whose int result was widened to
+int64 with sign extension, so every unit whose prefix had passed 2^31 stored
+its values up to 8 GiB before the value buffer and faulted the GPU.  The
+broadcast now widens the unsigned value (uniform_u32).  The oracle is far too
+slow at this size, so the checks are size-independent properties computed
+with torch ops on the GPU: the exact round trip, the bitmask and prefix
+rebuilt from the dense input, the tile-major value order, and the GEMM
+against an fp32 product on the decompressed operand.
 
 Shape 32768 x 65600 = 2,149,580,800 elements (2^31 + 2,097,152); at mean +4
 about 99.997% of the elements are positive, so the last prefix values (and the
@@ -21,11 +21,7 @@ import torch
 
 from tests.test_gpu_codec import _torch_tile_bitmask, decompress
 
-pytestmark = [
-    pytest.mark.gpu,
-    pytest.mark.skip(reason="a GPU run at 2^31+ elements faulted with no cause found; "
-                            "the C ABI refuses these shapes"),
-]
+pytestmark = pytest.mark.gpu
 
 M_BIG, N_BIG = 32768, 65600
 
