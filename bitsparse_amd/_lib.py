@@ -17,7 +17,7 @@ LIB_NAME = "libbitsparse_hip.so"
 # BITSPARSE_HIP_LIB points at another build of the same sources (tuning sweeps)
 LIB_PATH = os.environ.get("BITSPARSE_HIP_LIB") or os.path.join(
     os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 BS_OK = 0
 BS_ERR_INVALID = 1
@@ -66,6 +66,7 @@ _SIGNATURES = {
                             _vp, _vp, _int, _vp, _vp, _vp],
     "bs_compress_noalloc_max_tiles": [],
     "bs_launch_timing": [_int],
+    "bs_nontemporal_min_bytes": [_i64],
     "bs_launch_timing_read": [_vp, _vp, _int, _vp],
 }
 _RESTYPES = {
@@ -73,6 +74,7 @@ _RESTYPES = {
     "bs_compress_workspace_bytes": _i64,
     "bs_gemm_compressed_b_workspace_bytes": _i64,
     "bs_compress_noalloc_max_tiles": _i64,
+    "bs_nontemporal_min_bytes": _i64,
     "bs_workspace_amax_slot": _vp,
     "bs_workspace_fallback_counter": _vp,
 }

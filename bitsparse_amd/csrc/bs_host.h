@@ -24,6 +24,15 @@ constexpr int64_t kWsFallbackOffset = 8;
 // at 2^31.
 constexpr uint64_t kMaxElems = 1ull << 32;
 
+// Kernels that stream a dense matrix at least this large use nontemporal
+// (`nt`) loads and stores for it: nothing of it can stay in the 256 MiB last
+// level cache for a later kernel, and the streaming hint raises the HBM rate
+// (read-only 6.0 -> 6.8 TB/s; the 16384^2 compress 200 -> 173 us).  Smaller
+// matrices keep plain accesses, which leave them cached for the next kernel
+// (the configs[3]-sized fp8 unpack: 34 us plain, 41 us nontemporal).
+// BITSPARSE_NT_MIN_BYTES overrides the threshold (tuning runs).
+bool use_nontemporal(int64_t dense_bytes);
+
 // Launch timing (bs_launch_timing): the next start/stop event pair for a
 // kernel launch of the given kind (0 compress, 1 decompress), or false when
 // timing is off on this thread.

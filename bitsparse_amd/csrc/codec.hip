@@ -27,6 +27,7 @@ constexpr int kThreads = 256;
 
 
 
+
 // Elements of one chunk as raw bits.
 template <int B>
 __device__ __forceinline__ uint32_t elem(const typename Raw<B>::T& v, int e)
@@ -51,7 +52,7 @@ __device__ __forceinline__ void set_elem(typename Raw<B>::T& v, int e, uint32_t 
 
 // Load chunk (row, col0..col0+7) of a row-major matrix, zeros outside [M, N].
 // VEC: N % 8 == 0 and 8-element alignment, so a chunk is all in or all out.
-template <int B, bool VEC>
+template <int B, bool VEC, bool NT = false>
 __device__ __forceinline__ typename Raw<B>::T load_chunk(const uint8_t* base, int64_t M, int64_t N,
                                                          int64_t row, int64_t col0)
 {
@@ -60,7 +61,7 @@ __device__ __forceinline__ typename Raw<B>::T load_chunk(const uint8_t* base, in
     if (row >= M || col0 >= N) return v;
     const uint8_t* p = base + (row * N + col0) * B;
     if constexpr (VEC) {
-        v = *reinterpret_cast<const T*>(p);
+        v = ld_chunk<NT, T>(p);
     } else {
 #pragma unroll
         for (int e = 0; e < 8; e++) {
@@ -74,7 +75,7 @@ __device__ __forceinline__ typename Raw<B>::T load_chunk(const uint8_t* base, in
     return v;
 }
 
-template <int B, bool VEC>
+template <int B, bool VEC, bool NT = false>
 __device__ __forceinline__ void store_chunk(uint8_t* base, int64_t M, int64_t N, int64_t row,
                                             int64_t col0, const typename Raw<B>::T& v)
 {
@@ -82,7 +83,7 @@ __device__ __forceinline__ void store_chunk(uint8_t* base, int64_t M, int64_t N,
     if (row >= M || col0 >= N) return;
     uint8_t* p = base + (row * N + col0) * B;
     if constexpr (VEC) {
-        *reinterpret_cast<T*>(p) = v;
+        st_chunk<NT, T>(p, v);
     } else {
 #pragma unroll
         for (int e = 0; e < 8; e++) {
@@ -657,7 +658,8 @@ __device__ __forceinline__ void packed_unit_edges(const CompressArgs& a, int64_t
 #define BS_PACKED_WAVES_PER_EU 7
 #endif
 
-template <int IN_T, bool QUANT, bool VEC, int MODE, int U, bool PACKED>
+// NT: nontemporal loads of the dense input and stores of the value slots.
+template <int IN_T, bool QUANT, bool VEC, int MODE, int U, bool PACKED, bool NT>
 __global__ __launch_bounds__(64 * U) __attribute__((amdgpu_waves_per_eu(
     QUANT ? BS_QUANT_WAVES_PER_EU : (PACKED ? BS_PACKED_WAVES_PER_EU : BS_STREAM_WAVES_PER_EU))))
 void compress_stream_kernel(CompressArgs a)
@@ -727,7 +729,7 @@ void compress_stream_kernel(CompressArgs a)
             const int64_t row = row0 + 8 * k;
             if constexpr (VEC) {
                 const int64_t rc = min(row, a.M - 1), cc = min(col0, a.N - 8);
-                d[k] = *reinterpret_cast<const RawIn*>(a.dense + (rc * a.N + cc) * INB);
+                d[k] = ld_chunk<NT, RawIn>(a.dense + (rc * a.N + cc) * INB);
             } else {
                 d[k] = tile_ok ? load_chunk<INB, false>(a.dense, a.M, a.N, row, col0) : RawIn{};
             }
@@ -896,8 +898,8 @@ void compress_stream_kernel(CompressArgs a)
                     }
                     const int jh = min(j_hi, npend);
                     for (int j = max(pend, j_lo) + lane; j < jh; j += 64)
-                        *reinterpret_cast<uint4*>(slot_base + (int64_t)j * 16) =
-                            *reinterpret_cast<const uint4*>(ring + (j - pend) * 16);
+                        st16<NT>(slot_base + (int64_t)j * 16,
+                                        *reinterpret_cast<const uint4*>(ring + (j - pend) * 16));
                     if (!back_done && done >= endr) {
                         back_done = true;
                         const int r = back_s + lane;
@@ -1133,7 +1135,7 @@ struct GatherArgs {
 
 // Stage the value run of tiles [t0, t0+ntiles) in LDS; returns its phase.
 // The run is [vo + prefix[t0], vo + prefix[t0+ntiles]).
-template <int VB>
+template <int VB, bool NT>
 __device__ __forceinline__ int stage_run(const GatherArgs& a, int64_t run0, int64_t run1,
                                          int64_t max_count, uint8_t* s_vals, int tid)
 {
@@ -1149,7 +1151,7 @@ __device__ __forceinline__ int stage_run(const GatherArgs& a, int64_t run0, int6
         const int64_t e0 = run0 - p + (int64_t)s * EPS;
         uint4 v = {0u, 0u, 0u, 0u};
         if (e0 >= 0 && e0 + EPS <= a.vals_numel) {
-            v = *reinterpret_cast<const uint4*>(a.vals + e0 * VB);
+            v = ld16<NT>(a.vals + e0 * VB);
         } else {
             for (int e = 0; e < EPS; e++) {
                 int64_t i = e0 + e;
@@ -1175,7 +1177,7 @@ __device__ __forceinline__ int stage_run(const GatherArgs& a, int64_t run0, int6
 // a PB-bit value stream (vals_numel = stream bytes) from a 16-byte aligned
 // byte, plus one more 16-byte slot so two-dword reads never leave the staged
 // data.  Returns the bit position of value run0 inside the staged bytes.
-template <int PB>
+template <int PB, bool NT>
 __device__ __forceinline__ int stage_run_packed(const GatherArgs& a, int64_t run0, int64_t run1,
                                                 int64_t max_count, uint8_t* s_vals, int tid)
 {
@@ -1189,7 +1191,7 @@ __device__ __forceinline__ int stage_run_packed(const GatherArgs& a, int64_t run
         const int64_t b0 = sb + (int64_t)s * 16;
         uint4 v = {0u, 0u, 0u, 0u};
         if (b0 >= 0 && b0 + 16 <= a.vals_numel) {
-            v = *reinterpret_cast<const uint4*>(a.vals + b0);
+            v = ld16<NT>(a.vals + b0);
         } else {
             for (int e = 0; e < 16; e++) {
                 const int64_t i = b0 + e;
@@ -1209,7 +1211,7 @@ __device__ __forceinline__ int stage_run_packed(const GatherArgs& a, int64_t run
 // first value) and returns after a barrier.
 // M_LOADED: the caller already holds the mask bytes in m and prefix[t0 + tid]
 // (tid <= ntiles) in pf.
-template <int VB, int PB, int U, bool M_LOADED = false>
+template <int VB, int PB, int U, bool NT, bool M_LOADED = false>
 __device__ __forceinline__ int gather_prepare(const GatherArgs& a, uint32_t t0, int ntiles,
                                               uint32_t (&m)[U][2], uint32_t (&r0)[U][2],
                                               uint32_t* s_pref, uint32_t (*s_wtot)[2][4],
@@ -1239,10 +1241,10 @@ __device__ __forceinline__ int gather_prepare(const GatherArgs& a, uint32_t t0, 
     const uint32_t pb = s_pref[0];
     int p = 0, bitbase = 0;
     if constexpr (PB > 0)
-        bitbase = stage_run_packed<PB>(a, vo + pb, vo + s_pref[ntiles], (int64_t)ntiles * kTileNumel,
+        bitbase = stage_run_packed<PB, NT>(a, vo + pb, vo + s_pref[ntiles], (int64_t)ntiles * kTileNumel,
                                        s_vals, tid);
     else
-        p = stage_run<VB>(a, vo + pb, vo + s_pref[ntiles], (int64_t)ntiles * kTileNumel, s_vals, tid);
+        p = stage_run<VB, NT>(a, vo + pb, vo + s_pref[ntiles], (int64_t)ntiles * kTileNumel, s_vals, tid);
 #pragma unroll
     for (int j = 0; j < U; j++) {
         uint32_t tb = j < ntiles ? min(s_pref[j] - pb, (uint32_t)(j * kTileNumel)) : 0u;
@@ -1298,7 +1300,8 @@ __device__ __forceinline__ float val_f32(uint32_t raw)
     else return fp8_to_f32<V_T>(raw);
 }
 
-template <int V_T, bool SQUARE, bool HAS_SCALE, bool VEC, int U, bool PACKED>
+// NT: nontemporal staging loads and dense output stores.
+template <int V_T, bool SQUARE, bool HAS_SCALE, bool VEC, int U, bool PACKED, bool NT>
 __global__ __launch_bounds__(kThreads) void decompress_kernel(GatherArgs a)
 {
     constexpr int VB = V_T == DT_BF16 ? 2 : 1;
@@ -1322,7 +1325,7 @@ __global__ __launch_bounds__(kThreads) void decompress_kernel(GatherArgs a)
     const uint32_t t0 = (uint32_t)a.first_m_tile * a.grid_n + pid0;
 
     uint32_t m[U][2], r0[U][2];
-    const int bitbase = gather_prepare<VB, PB, U>(a, t0, ntiles, m, r0, s_pref, s_wtot, s_vals, tid);
+    const int bitbase = gather_prepare<VB, PB, U, NT>(a, t0, ntiles, m, r0, s_pref, s_wtot, s_vals, tid);
 
     float s2b = 1.0f;
     if constexpr (HAS_SCALE) {
@@ -1369,13 +1372,14 @@ __global__ __launch_bounds__(kThreads) void decompress_kernel(GatherArgs a)
             }
             int64_t row, col0;
             chunk_pos(pid0 + j, a.grid_n, h * 256 + tid, row, col0);
-            store_chunk<OB, VEC>(a.out, a.rows, a.K, row, col0, ov);
+            store_chunk<OB, VEC, NT>(a.out, a.rows, a.K, row, col0, ov);
         }
     }
 }
 
 // grad = bit ? bf16(grad * (2k * r)) : 0, then optionally grad = bf16(grad * bf16(scale))
-template <int V_T, bool HAS_SCALE, bool VEC, int U, bool PACKED>
+// NT: nontemporal gradient loads / stores and staging loads.
+template <int V_T, bool HAS_SCALE, bool VEC, int U, bool PACKED, bool NT>
 __global__ __launch_bounds__(kThreads) void relu2_grad_kernel(GatherArgs a)
 {
     constexpr int VB = V_T == DT_BF16 ? 2 : 1;
@@ -1410,10 +1414,10 @@ __global__ __launch_bounds__(kThreads) void relu2_grad_kernel(GatherArgs a)
             if (m[j][h] != 0u) {
                 int64_t row, col0;
                 chunk_pos(t0 + j, a.grid_n, h * 256 + tid, row, col0);
-                g[j][h] = load_chunk<2, VEC>(a.out, a.rows, a.K, row, col0);
+                g[j][h] = load_chunk<2, VEC, NT>(a.out, a.rows, a.K, row, col0);
             }
         }
-    const int bitbase = gather_prepare<VB, PB, U, true>(a, t0, ntiles, m, r0, s_pref, s_wtot, s_vals, tid, pf);
+    const int bitbase = gather_prepare<VB, PB, U, NT, true>(a, t0, ntiles, m, r0, s_pref, s_wtot, s_vals, tid, pf);
 
     if constexpr (WIDEN) {
         // staged indices [0, count + 16) cover the run and its <= 15-element phase
@@ -1450,7 +1454,7 @@ __global__ __launch_bounds__(kThreads) void relu2_grad_kernel(GatherArgs a)
             }
             int64_t row, col0;
             chunk_pos(t0 + j, a.grid_n, h * 256 + tid, row, col0);
-            store_chunk<2, VEC>(a.out, a.rows, a.K, row, col0, ov);
+            store_chunk<2, VEC, NT>(a.out, a.rows, a.K, row, col0, ov);
         }
     }
 }
@@ -1458,7 +1462,8 @@ __global__ __launch_bounds__(kThreads) void relu2_grad_kernel(GatherArgs a)
 // ===========================================================================
 // ReLU mask gradient (in place)
 // ===========================================================================
-template <bool VEC, int U>
+// NT: nontemporal gradient loads / stores.
+template <bool VEC, int U, bool NT>
 __global__ __launch_bounds__(kThreads) void relu_grad_kernel(uint8_t* grad, int64_t M, int64_t N,
                                                              uint32_t grid_n, uint32_t T,
                                                              const uint8_t* bitmask)
@@ -1481,7 +1486,7 @@ __global__ __launch_bounds__(kThreads) void relu_grad_kernel(uint8_t* grad, int6
             if (m[j][h] != 0u && m[j][h] != 0xffu) {
                 int64_t row, col0;
                 chunk_pos(t0 + j, grid_n, h * 256 + tid, row, col0);
-                g[j][h] = load_chunk<2, VEC>(grad, M, N, row, col0);
+                g[j][h] = load_chunk<2, VEC, NT>(grad, M, N, row, col0);
             }
         }
 #pragma unroll
@@ -1499,7 +1504,7 @@ __global__ __launch_bounds__(kThreads) void relu_grad_kernel(uint8_t* grad, int6
             v.x &= k0; v.y &= k1; v.z &= k2; v.w &= k3;
             int64_t row, col0;
             chunk_pos(t0 + j, grid_n, h * 256 + tid, row, col0);
-            store_chunk<2, VEC>(grad, M, N, row, col0, v);
+            store_chunk<2, VEC, NT>(grad, M, N, row, col0, v);
         }
 }
 
@@ -1532,29 +1537,34 @@ static inline bool aligned8(const void* p) { return (((uintptr_t)p) & 7u) == 0; 
 constexpr int kStreamU = BS_STREAM_U;
 
 template <int IN_T, bool QUANT, int MODE, bool PACKED>
-static hipError_t launch_compress_mode(const CompressArgs& a, bool vec, hipStream_t st)
+static hipError_t launch_compress_mode(const CompressArgs& a, bool vec, bool nt, hipStream_t st)
 {
     const uint32_t units = (a.tend - a.tile0 + kStreamU - 1) / kStreamU;
-    if (vec)
-        launch_timed(0, compress_stream_kernel<IN_T, QUANT, true, MODE, kStreamU, PACKED>, dim3(units),
+    // the streaming hint is built for the fused pass over a vector-loadable input
+    constexpr bool kHasNt = MODE == MODE_FUSED;
+    if (vec && nt && kHasNt)
+        launch_timed(0, compress_stream_kernel<IN_T, QUANT, true, MODE, kStreamU, PACKED, kHasNt>, dim3(units),
+                     dim3(64 * kStreamU), 0, st, a);
+    else if (vec)
+        launch_timed(0, compress_stream_kernel<IN_T, QUANT, true, MODE, kStreamU, PACKED, false>, dim3(units),
                      dim3(64 * kStreamU), 0, st, a);
     else
-        launch_timed(0, compress_stream_kernel<IN_T, QUANT, false, MODE, kStreamU, PACKED>, dim3(units),
+        launch_timed(0, compress_stream_kernel<IN_T, QUANT, false, MODE, kStreamU, PACKED, false>, dim3(units),
                      dim3(64 * kStreamU), 0, st, a);
     return hipGetLastError();
 }
 
 template <int MODE, bool PACKED = false>
-static hipError_t launch_compress(const CompressArgs& a, int in_dtype, bool quant, bool vec,
+static hipError_t launch_compress(const CompressArgs& a, int in_dtype, bool quant, bool vec, bool nt,
                                   hipStream_t st)
 {
     if constexpr (MODE != MODE_VALS) {
-        if (quant) return launch_compress_mode<DT_BF16, true, MODE, PACKED>(a, vec, st);
+        if (quant) return launch_compress_mode<DT_BF16, true, MODE, PACKED>(a, vec, nt, st);
     }
     switch (in_dtype) {
-    case DT_BF16: return launch_compress_mode<DT_BF16, false, MODE, PACKED>(a, vec, st);
-    case DT_E4M3FN: return launch_compress_mode<DT_E4M3FN, false, MODE, PACKED>(a, vec, st);
-    default: return launch_compress_mode<DT_E5M2, false, MODE, PACKED>(a, vec, st);
+    case DT_BF16: return launch_compress_mode<DT_BF16, false, MODE, PACKED>(a, vec, nt, st);
+    case DT_E4M3FN: return launch_compress_mode<DT_E4M3FN, false, MODE, PACKED>(a, vec, nt, st);
+    default: return launch_compress_mode<DT_E5M2, false, MODE, PACKED>(a, vec, nt, st);
     }
 }
 
@@ -1691,9 +1701,10 @@ static int compress_impl(const void* dense, int in_dtype, int64_t M, int64_t N, 
     bool vec = (N % 8 == 0) && (((uintptr_t)dense) % (8 * inb) == 0) &&
                (dense_q_out == nullptr || aligned8(dense_q_out)) &&
                (relu_out == nullptr || ((uintptr_t)relu_out) % (8 * inb) == 0);
-    hipError_t e = packed     ? launch_compress<MODE_FUSED, true>(a, in_dtype, quantize != 0, vec, st)
-                 : write_vals ? launch_compress<MODE_FUSED>(a, in_dtype, quantize != 0, vec, st)
-                              : launch_compress<MODE_COUNT>(a, in_dtype, quantize != 0, vec, st);
+    const bool nt = use_nontemporal(M * N * inb);
+    hipError_t e = packed     ? launch_compress<MODE_FUSED, true>(a, in_dtype, quantize != 0, vec, nt, st)
+                 : write_vals ? launch_compress<MODE_FUSED>(a, in_dtype, quantize != 0, vec, nt, st)
+                              : launch_compress<MODE_COUNT>(a, in_dtype, quantize != 0, vec, nt, st);
     if (e != hipSuccess) return set_error(BS_ERR_HIP, "bs_compress launch: %s", hipGetErrorString(e));
     return BS_OK;
 }
@@ -1777,7 +1788,7 @@ extern "C" int bs_compact_vals(const void* dense, int in_dtype, int64_t M, int64
     a.err = err_flags;
     a.patience = kLookbackPatienceTicks;       // no look-back in this mode
     bool vec = (N % 8 == 0) && (((uintptr_t)dense) % (8 * eb) == 0);
-    hipError_t e = launch_compress<MODE_VALS>(a, in_dtype, false, vec, (hipStream_t)stream);
+    hipError_t e = launch_compress<MODE_VALS>(a, in_dtype, false, vec, false, (hipStream_t)stream);
     if (e != hipSuccess) return set_error(BS_ERR_HIP, "bs_compact_vals launch: %s", hipGetErrorString(e));
     return BS_OK;
 }
@@ -1822,21 +1833,23 @@ extern "C" int bs_prefix_from_counts(const int32_t* tile_counts, int64_t T, uint
 }
 
 template <int V_T, bool SQ, bool SC, bool PK>
-static void launch_decompress_t(const GatherArgs& a, bool vec, hipStream_t st)
+static void launch_decompress_t(const GatherArgs& a, bool vec, bool nt, hipStream_t st)
 {
     const uint32_t blocks = (a.num_tiles + kGatherU - 1) / kGatherU;
-    if (vec)
-        launch_timed(1, decompress_kernel<V_T, SQ, SC, true, kGatherU, PK>, dim3(blocks), dim3(kThreads), 0, st, a);
+    if (vec && nt)
+        launch_timed(1, decompress_kernel<V_T, SQ, SC, true, kGatherU, PK, true>, dim3(blocks), dim3(kThreads), 0, st, a);
+    else if (vec)
+        launch_timed(1, decompress_kernel<V_T, SQ, SC, true, kGatherU, PK, false>, dim3(blocks), dim3(kThreads), 0, st, a);
     else
-        launch_timed(1, decompress_kernel<V_T, SQ, SC, false, kGatherU, PK>, dim3(blocks), dim3(kThreads), 0, st, a);
+        launch_timed(1, decompress_kernel<V_T, SQ, SC, false, kGatherU, PK, false>, dim3(blocks), dim3(kThreads), 0, st, a);
 }
 
 template <int V_T, bool PK>
-static void launch_decompress_v(const GatherArgs& a, bool sq, bool sc, bool vec, hipStream_t st)
+static void launch_decompress_v(const GatherArgs& a, bool sq, bool sc, bool vec, bool nt, hipStream_t st)
 {
-    if (!sq) launch_decompress_t<V_T, false, false, PK>(a, vec, st);
-    else if (!sc) launch_decompress_t<V_T, true, false, PK>(a, vec, st);
-    else launch_decompress_t<V_T, true, true, PK>(a, vec, st);
+    if (!sq) launch_decompress_t<V_T, false, false, PK>(a, vec, nt, st);
+    else if (!sc) launch_decompress_t<V_T, true, false, PK>(a, vec, nt, st);
+    else launch_decompress_t<V_T, true, true, PK>(a, vec, nt, st);
 }
 
 static int check_gather(const void* vals, int vals_dtype, int64_t vals_numel, const uint8_t* bitmask,
@@ -1886,20 +1899,21 @@ static int decompress_impl(const void* vals, int vals_dtype, int64_t vals_numel,
     a.relu2_scale = relu2_scale;
     a.scale = scale;
     bool vec = (K % 8 == 0) && (((uintptr_t)out) % (8 * ob) == 0);
+    const bool nt = use_nontemporal(batch_rows * K * ob);
     hipStream_t st = (hipStream_t)stream;
     const bool sc = scale != nullptr;
     switch (vals_dtype) {
     case DT_BF16:
-        if (packed) launch_decompress_v<DT_BF16, true>(a, square, sc, vec, st);
-        else launch_decompress_v<DT_BF16, false>(a, square, sc, vec, st);
+        if (packed) launch_decompress_v<DT_BF16, true>(a, square, sc, vec, nt, st);
+        else launch_decompress_v<DT_BF16, false>(a, square, sc, vec, nt, st);
         break;
     case DT_E4M3FN:
-        if (packed) launch_decompress_v<DT_E4M3FN, true>(a, square, sc, vec, st);
-        else launch_decompress_v<DT_E4M3FN, false>(a, square, sc, vec, st);
+        if (packed) launch_decompress_v<DT_E4M3FN, true>(a, square, sc, vec, nt, st);
+        else launch_decompress_v<DT_E4M3FN, false>(a, square, sc, vec, nt, st);
         break;
     default:
-        if (packed) launch_decompress_v<DT_E5M2, true>(a, square, sc, vec, st);
-        else launch_decompress_v<DT_E5M2, false>(a, square, sc, vec, st);
+        if (packed) launch_decompress_v<DT_E5M2, true>(a, square, sc, vec, nt, st);
+        else launch_decompress_v<DT_E5M2, false>(a, square, sc, vec, nt, st);
         break;
     }
     hipError_t e = hipGetLastError();
@@ -1943,11 +1957,14 @@ extern "C" int bs_relu_grad(void* grad, int64_t M, int64_t N, const uint8_t* bit
     uint32_t gn = (uint32_t)((N + 63) / 64);
     const uint32_t blocks = (uint32_t)((T + kMaskU - 1) / kMaskU);
     hipStream_t st = (hipStream_t)stream;
-    if (vec)
-        hipLaunchKernelGGL((relu_grad_kernel<true, kMaskU>), dim3(blocks), dim3(kThreads), 0, st,
+    if (vec && use_nontemporal(2 * M * N))
+        hipLaunchKernelGGL((relu_grad_kernel<true, kMaskU, true>), dim3(blocks), dim3(kThreads), 0, st,
+                           (uint8_t*)grad, M, N, gn, (uint32_t)T, bitmask);
+    else if (vec)
+        hipLaunchKernelGGL((relu_grad_kernel<true, kMaskU, false>), dim3(blocks), dim3(kThreads), 0, st,
                            (uint8_t*)grad, M, N, gn, (uint32_t)T, bitmask);
     else
-        hipLaunchKernelGGL((relu_grad_kernel<false, kMaskU>), dim3(blocks), dim3(kThreads), 0, st,
+        hipLaunchKernelGGL((relu_grad_kernel<false, kMaskU, false>), dim3(blocks), dim3(kThreads), 0, st,
                            (uint8_t*)grad, M, N, gn, (uint32_t)T, bitmask);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(BS_ERR_HIP, "bs_relu_grad launch: %s", hipGetErrorString(e));
@@ -1955,20 +1972,22 @@ extern "C" int bs_relu_grad(void* grad, int64_t M, int64_t N, const uint8_t* bit
 }
 
 template <int V_T, bool SC, bool PK>
-static void launch_relu2_t(const GatherArgs& a, bool vec, hipStream_t st)
+static void launch_relu2_t(const GatherArgs& a, bool vec, bool nt, hipStream_t st)
 {
     const uint32_t blocks = (a.num_tiles + kGatherU - 1) / kGatherU;
-    if (vec)
-        hipLaunchKernelGGL((relu2_grad_kernel<V_T, SC, true, kGatherU, PK>), dim3(blocks), dim3(kThreads), 0, st, a);
+    if (vec && nt)
+        hipLaunchKernelGGL((relu2_grad_kernel<V_T, SC, true, kGatherU, PK, true>), dim3(blocks), dim3(kThreads), 0, st, a);
+    else if (vec)
+        hipLaunchKernelGGL((relu2_grad_kernel<V_T, SC, true, kGatherU, PK, false>), dim3(blocks), dim3(kThreads), 0, st, a);
     else
-        hipLaunchKernelGGL((relu2_grad_kernel<V_T, SC, false, kGatherU, PK>), dim3(blocks), dim3(kThreads), 0, st, a);
+        hipLaunchKernelGGL((relu2_grad_kernel<V_T, SC, false, kGatherU, PK, false>), dim3(blocks), dim3(kThreads), 0, st, a);
 }
 
 template <int V_T, bool PK>
-static void launch_relu2_v(const GatherArgs& a, bool sc, bool vec, hipStream_t st)
+static void launch_relu2_v(const GatherArgs& a, bool sc, bool vec, bool nt, hipStream_t st)
 {
-    if (sc) launch_relu2_t<V_T, true, PK>(a, vec, st);
-    else launch_relu2_t<V_T, false, PK>(a, vec, st);
+    if (sc) launch_relu2_t<V_T, true, PK>(a, vec, nt, st);
+    else launch_relu2_t<V_T, false, PK>(a, vec, nt, st);
 }
 
 static int relu2_grad_impl(void* grad, int64_t M, int64_t N, const void* vals, int vals_dtype,
@@ -2000,20 +2019,21 @@ static int relu2_grad_impl(void* grad, int64_t M, int64_t N, const void* vals, i
     a.relu2_scale = relu2_scale;
     a.scale = scale;
     bool vec = (N % 8 == 0) && aligned16(grad);
+    const bool nt = use_nontemporal(2 * M * N);
     hipStream_t st = (hipStream_t)stream;
     const bool sc = scale != nullptr;
     switch (vals_dtype) {
     case DT_BF16:
-        if (packed) launch_relu2_v<DT_BF16, true>(a, sc, vec, st);
-        else launch_relu2_v<DT_BF16, false>(a, sc, vec, st);
+        if (packed) launch_relu2_v<DT_BF16, true>(a, sc, vec, nt, st);
+        else launch_relu2_v<DT_BF16, false>(a, sc, vec, nt, st);
         break;
     case DT_E4M3FN:
-        if (packed) launch_relu2_v<DT_E4M3FN, true>(a, sc, vec, st);
-        else launch_relu2_v<DT_E4M3FN, false>(a, sc, vec, st);
+        if (packed) launch_relu2_v<DT_E4M3FN, true>(a, sc, vec, nt, st);
+        else launch_relu2_v<DT_E4M3FN, false>(a, sc, vec, nt, st);
         break;
     default:
-        if (packed) launch_relu2_v<DT_E5M2, true>(a, sc, vec, st);
-        else launch_relu2_v<DT_E5M2, false>(a, sc, vec, st);
+        if (packed) launch_relu2_v<DT_E5M2, true>(a, sc, vec, nt, st);
+        else launch_relu2_v<DT_E5M2, false>(a, sc, vec, nt, st);
         break;
     }
     hipError_t e = hipGetLastError();

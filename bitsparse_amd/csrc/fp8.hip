@@ -27,7 +27,8 @@ __device__ __forceinline__ uint32_t mag_bits(uint32_t b)
     else return m;
 }
 
-template <bool RELU>
+// NT: nontemporal loads of x.
+template <bool RELU, bool NT>
 __global__ __launch_bounds__(kFp8Threads) void amax_bf16_kernel(const uint16_t* x, int64_t n,
                                                                 uint64_t* slot, uint32_t epoch)
 {
@@ -41,7 +42,7 @@ __global__ __launch_bounds__(kFp8Threads) void amax_bf16_kernel(const uint16_t* 
     for (; i + (kAmaxUnroll - 1) * stride < nvec; i += kAmaxUnroll * stride) {
         uint4 v[kAmaxUnroll];
 #pragma unroll
-        for (int u = 0; u < kAmaxUnroll; u++) v[u] = xv[i + u * stride];
+        for (int u = 0; u < kAmaxUnroll; u++) v[u] = ld16<NT>(xv + i + u * stride);
 #pragma unroll
         for (int u = 0; u < kAmaxUnroll; u++) {
             const uint32_t w[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
@@ -53,7 +54,7 @@ __global__ __launch_bounds__(kFp8Threads) void amax_bf16_kernel(const uint16_t* 
         }
     }
     for (; i < nvec; i += stride) {
-        const uint4 v = xv[i];
+        const uint4 v = ld16<NT>(xv + i);
         const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
         for (int k = 0; k < 4; k++) {
@@ -80,6 +81,8 @@ __device__ __forceinline__ float fp8_scale_from_slot(const uint64_t* slot, uint3
     return (sc < 1e-9f) ? 1e-9f : sc;
 }
 
+// NT: nontemporal loads of x and stores of q.
+template <bool NT>
 __global__ __launch_bounds__(kFp8Threads) void quantize_e4m3_kernel(const uint16_t* x, int64_t n,
                                                                     uint8_t* q, float* scale_out,
                                                                     const uint64_t* slot,
@@ -93,14 +96,14 @@ __global__ __launch_bounds__(kFp8Threads) void quantize_e4m3_kernel(const uint16
     const int64_t nvec = vec ? n / 8 : 0;
     const int64_t stride = (int64_t)gridDim.x * kFp8Threads;
     for (int64_t i = (int64_t)blockIdx.x * kFp8Threads + tid; i < nvec; i += stride) {
-        uint4 v = reinterpret_cast<const uint4*>(x)[i];
+        const uint4 v = ld16<NT>(reinterpret_cast<const uint4*>(x) + i);
         uint32_t w[4] = {v.x, v.y, v.z, v.w};
         uint32_t o[2] = {0u, 0u};
 #pragma unroll
         for (int k = 0; k < 4; k++)
             o[k >> 1] |= div2_to_e4m3(bf16_to_f32(w[k] & 0xffffu), bf16_to_f32(w[k] >> 16), scale, rcp)
                          << (16 * (k & 1));
-        reinterpret_cast<uint2*>(q)[i] = uint2{o[0], o[1]};
+        st8<NT>(reinterpret_cast<uint2*>(q) + i, uint2{o[0], o[1]});
     }
     for (int64_t i = nvec * 8 + (int64_t)blockIdx.x * kFp8Threads + tid; i < n; i += stride)
         q[i] = (uint8_t)div_to_e4m3(bf16_to_f32(x[i]), scale, rcp);
@@ -138,12 +141,11 @@ int bs::amax_launch(const void* x, int64_t n, void* workspace, int64_t workspace
         cus = 256;
     uint32_t grid = grid_for(n);
     if (grid > (uint32_t)(2 * cus)) grid = (uint32_t)(2 * cus);
-    if (relu)
-        hipLaunchKernelGGL(amax_bf16_kernel<true>, dim3(grid), dim3(kFp8Threads), 0, (hipStream_t)stream,
-                           (const uint16_t*)x, n, slot, epoch);
-    else
-        hipLaunchKernelGGL(amax_bf16_kernel<false>, dim3(grid), dim3(kFp8Threads), 0, (hipStream_t)stream,
-                           (const uint16_t*)x, n, slot, epoch);
+    const bool nt = use_nontemporal(2 * n);
+    auto kernel = relu ? (nt ? amax_bf16_kernel<true, true> : amax_bf16_kernel<true, false>)
+                       : (nt ? amax_bf16_kernel<false, true> : amax_bf16_kernel<false, false>);
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(kFp8Threads), 0, (hipStream_t)stream, (const uint16_t*)x, n,
+                       slot, epoch);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(BS_ERR_HIP, "bs_amax launch: %s", hipGetErrorString(e));
     return BS_OK;
@@ -175,7 +177,8 @@ extern "C" int bs_quantize_e4m3fn(const void* x, int64_t n, void* q_out, float* 
         return set_error(BS_ERR_INVALID, "bs_quantize_e4m3fn: null pointer");
     if (((uintptr_t)x) & 1u) return set_error(BS_ERR_INVALID, "bs_quantize_e4m3fn: input misaligned");
     const uint64_t* slot = reinterpret_cast<const uint64_t*>((const uint8_t*)workspace + kWsAmaxOffset);
-    hipLaunchKernelGGL(quantize_e4m3_kernel, dim3(grid_for(n)), dim3(kFp8Threads), 0, (hipStream_t)stream,
+    auto kernel = use_nontemporal(2 * n) ? quantize_e4m3_kernel<true> : quantize_e4m3_kernel<false>;
+    hipLaunchKernelGGL(kernel, dim3(grid_for(n)), dim3(kFp8Threads), 0, (hipStream_t)stream,
                        (const uint16_t*)x, n, (uint8_t*)q_out, scale_out, slot, epoch);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(BS_ERR_HIP, "bs_quantize_e4m3fn launch: %s", hipGetErrorString(e));

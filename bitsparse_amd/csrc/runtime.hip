@@ -2,7 +2,9 @@
 #include <hip/hip_runtime.h>
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 
+#include <atomic>
 #include <vector>
 
 #include "bs_host.h"
@@ -58,6 +60,25 @@ bool timing_next(int kind, hipEvent_t* start, hipEvent_t* stop)
     return true;
 }
 
+constexpr int64_t kNtMinBytesDefault = int64_t(192) << 20;
+
+static int64_t nt_min_bytes_initial()
+{
+    if (const char* ev = getenv("BITSPARSE_NT_MIN_BYTES")) {
+        char* end = nullptr;
+        const long long v = strtoll(ev, &end, 10);
+        if (end != ev && v >= 0) return (int64_t)v;
+    }
+    return kNtMinBytesDefault;
+}
+
+static std::atomic<int64_t> g_nt_min_bytes{nt_min_bytes_initial()};
+
+bool use_nontemporal(int64_t dense_bytes)
+{
+    return dense_bytes >= g_nt_min_bytes.load(std::memory_order_relaxed);
+}
+
 hipError_t stream_device(hipStream_t stream, int* dev)
 {
     if (stream == nullptr) return hipGetDevice(dev);
@@ -84,7 +105,13 @@ using namespace bs;
 
 extern "C" const char* bs_last_error(void) { return bs::g_err; }
 
-extern "C" int bs_abi_version(void) { return 6; }
+extern "C" int bs_abi_version(void) { return 7; }
+
+extern "C" int64_t bs_nontemporal_min_bytes(int64_t bytes)
+{
+    clear_error();
+    return g_nt_min_bytes.exchange(bytes < 0 ? nt_min_bytes_initial() : bytes);
+}
 
 extern "C" int bs_launch_timing(int enable)
 {

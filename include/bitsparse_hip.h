@@ -68,6 +68,19 @@ int bs_launch_timing(int enable);
 int bs_launch_timing_read(float* ms_out, int* kinds_out, int max_n, int* n_out);
 
 /*
+ * Streaming-access threshold (no counterpart in the reference: a tuning and
+ * test hook).  A kernel whose dense matrix (compress input, decompress
+ * output, gradient, amax / quantize input) holds at least this many bytes
+ * loads and stores it with the nontemporal hint: nothing of it can stay in
+ * the last-level cache for a later kernel, and the hint raises the HBM rate.
+ * Smaller matrices keep plain accesses.  Sets the threshold for the process
+ * (bytes < 0: the default, 192 MiB, or BITSPARSE_NT_MIN_BYTES from the
+ * environment at load time) and returns the previous one.  Results do not
+ * depend on it.
+ */
+int64_t bs_nontemporal_min_bytes(int64_t bytes);
+
+/*
  * Workspace for the single-pass compress (bs_compress) and the fp8 amax
  * (bs_amax): a status word per compress unit plus an amax slot.  It must be
  * zero-filled once before first use; afterwards every call passes an `epoch`

@@ -36,6 +36,18 @@ def test_abi_version_and_workspace_size():
     assert L.bs_compress_workspace_bytes(0, 0) == 256 + 8 * 2
 
 
+def test_nontemporal_threshold_round_trip():
+    """bs_nontemporal_min_bytes sets the process threshold and returns the
+    previous one; a negative value restores the default (192 MiB)."""
+    L = _lib.load()
+    prev = L.bs_nontemporal_min_bytes(12345)
+    try:
+        assert L.bs_nontemporal_min_bytes(-1) == 12345
+        assert L.bs_nontemporal_min_bytes(7) == 192 << 20
+    finally:
+        L.bs_nontemporal_min_bytes(prev)
+
+
 def _err():
     return _lib.load().bs_last_error().decode()
 
