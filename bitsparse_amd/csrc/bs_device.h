@@ -271,6 +271,17 @@ __device__ __forceinline__ void wave_scan_count(uint32_t c, uint32_t& excl, uint
     total = (uint32_t)(__popcll(b0) + 2 * __popcll(b1) + 4 * __popcll(b2) + 8 * __popcll(b3));
 }
 
+// The same for a count in [0, 16] (five ballots).
+__device__ __forceinline__ void wave_scan_count16(uint32_t c, uint32_t& excl, uint32_t& total)
+{
+    uint64_t b0 = __ballot(c & 1u), b1 = __ballot(c & 2u), b2 = __ballot(c & 4u);
+    uint64_t b3 = __ballot(c & 8u), b4 = __ballot(c & 16u);
+    excl = popc_below(b0) + 2u * popc_below(b1) + 4u * popc_below(b2) + 8u * popc_below(b3) +
+           16u * popc_below(b4);
+    total = (uint32_t)(__popcll(b0) + 2 * __popcll(b1) + 4 * __popcll(b2) + 8 * __popcll(b3) +
+                       16 * __popcll(b4));
+}
+
 // Inclusive wave64 prefix sum (row shifts inside 16-lane rows, then the row
 // broadcasts of lanes 15 and 31).
 __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x)

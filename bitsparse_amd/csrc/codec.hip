@@ -1377,6 +1377,147 @@ __global__ __launch_bounds__(kThreads) void decompress_kernel(GatherArgs a)
     }
 }
 
+// Plain decompress of fp8 storage (the stored e4m3fn / e5m2 bytes come back
+// unchanged).  A workgroup takes a pair of horizontally adjacent tiles (tile
+// columns 2c, 2c+1 of one tile row; the last tile of an odd row alone), so a
+// 128-byte line of the output -- one row across both tiles -- is written by
+// eight lanes of one store instruction: thread i owns, in pass h, row
+// 32h + i/8 and the 16 elements of piece i%8 (pieces 0-3 in the first tile,
+// 4-7 in the second), i.e. two bitmask bytes.  (A chunk-per-thread layout
+// writes half lines, each finished later by another store.)  From raw storage
+// the 16 outputs are built without a read per element: the thread's value
+// window (16 bytes from its first rank) comes from five dword-aligned LDS
+// reads and v_alignbyte, and each mask byte expands its 8 outputs with two
+// v_perm_b32 whose selectors come from a 256-entry LDS table (selector byte
+// 0x0c gives 0x00); the second byte's window starts popcount(first byte)
+// values later.  Packed storage reads value by value.  Needs K % 16 == 0 and
+// a 16-byte aligned output.
+template <int V_T, int NP, bool PACKED, bool NT>
+__global__ __launch_bounds__(kThreads) void decompress_fp8_kernel(GatherArgs a, uint32_t groups_per_row)
+{
+    constexpr int PB = PACKED ? 7 : 0;
+    constexpr int NTL = 2 * NP;             // tiles per workgroup: NP adjacent pairs of one tile row
+    __shared__ uint32_t s_pref[NTL + 1];
+    __shared__ uint32_t s_wtot[2][NTL][4];  // [pass][tile][wave]
+    // the run, its <= 15-byte phase, and room for the last window's reads
+    __shared__ __align__(16) uint8_t s_vals[NTL * kTileNumel + 48];
+    __shared__ uint2 s_sel[PACKED ? 1 : 256];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const uint32_t tm = blockIdx.x / groups_per_row;
+    const uint32_t tn0 = NTL * (blockIdx.x - tm * groups_per_row);
+    const int ntiles = (int)min((uint32_t)NTL, a.grid_n - tn0);
+    const uint32_t tb0 = tm * a.grid_n + tn0;                       // first tile, batch-relative
+    const uint32_t t0 = (uint32_t)a.first_m_tile * a.grid_n + tb0;  // in the compressed tensor
+    const int piece = tid & 7, jt = piece >> 2, pc = piece & 3;    // tile of the pair, piece in it
+
+    if constexpr (!PACKED) {
+        // selectors of mask byte tid: set element e takes window byte rank(e)
+        uint32_t sel[2] = {0x0c0c0c0cu, 0x0c0c0c0cu};
+        uint32_t rank = 0;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            if ((tid >> e) & 1) {
+                sel[e >> 2] = (sel[e >> 2] & ~(0xffu << (8 * (e & 3)))) | (rank << (8 * (e & 3)));
+                rank++;
+            }
+        }
+        s_sel[tid] = uint2{sel[0], sel[1]};
+    }
+    uint32_t m[NP][2], ex[NP][2];
+#pragma unroll
+    for (int k = 0; k < NP; k++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int row = 32 * h + (tid >> 3), tile = 2 * k + jt;
+            m[k][h] = tile < ntiles ? (uint32_t)*reinterpret_cast<const uint16_t*>(
+                                          a.bitmask + (size_t)(t0 + tile) * kTileBytes + row * 8 + 2 * pc)
+                                    : 0u;
+        }
+    if (tid <= ntiles) s_pref[tid] = a.prefix[t0 + tid];
+#pragma unroll
+    for (int k = 0; k < NP; k++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const uint32_t c = (uint32_t)__popc(m[k][h]);
+            uint32_t eA, eB, tA, tB;
+            wave_scan_count16(jt == 0 ? c : 0u, eA, tA);
+            wave_scan_count16(jt == 1 ? c : 0u, eB, tB);
+            ex[k][h] = jt == 0 ? eA : eB;
+            if (lane == 0) {
+                s_wtot[h][2 * k][wave] = tA;
+                s_wtot[h][2 * k + 1][wave] = tB;
+            }
+        }
+    __syncthreads();
+    const int64_t vo = a.vals_offset ? *a.vals_offset : 0;
+    const uint32_t pb = s_pref[0];
+    int p = 0, bitbase = 0;
+    if constexpr (PACKED)
+        bitbase = stage_run_packed<PB, NT>(a, vo + pb, vo + s_pref[ntiles], (int64_t)ntiles * kTileNumel, s_vals, tid);
+    else
+        p = stage_run<1, NT>(a, vo + pb, vo + s_pref[ntiles], (int64_t)ntiles * kTileNumel, s_vals, tid);
+    // first value of this thread's piece: tile start + earlier pass + earlier
+    // waves of this pass + the in-wave rank
+    uint32_t r0[NP][2];
+#pragma unroll
+    for (int k = 0; k < NP; k++) {
+        const int tile = 2 * k + jt;
+        const uint32_t tstart = tile < ntiles ? min(s_pref[tile] - pb, (uint32_t)(tile * kTileNumel)) : 0u;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            uint32_t below = 0;
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                if (h == 1) below += s_wtot[0][tile][w];
+                if (w < wave) below += s_wtot[h][tile][w];
+            }
+            r0[k][h] = (uint32_t)p + tstart + below + ex[k][h];
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < NP; k++)
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const uint32_t mm = m[k][h];
+        uint4 o;
+        if constexpr (PACKED) {
+            uint32_t w[4] = {0u, 0u, 0u, 0u};
+            uint32_t r = r0[k][h];
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                if ((mm >> e) & 1u) w[e >> 2] |= lds_val<V_T, PB>(s_vals, r, bitbase) << (8 * (e & 3));
+                r += (mm >> e) & 1u;
+            }
+            o = uint4{w[0], w[1], w[2], w[3]};
+        } else {
+            const uint32_t r = r0[k][h];
+            const uint32_t* sv = reinterpret_cast<const uint32_t*>(s_vals) + (r >> 2);
+            const uint32_t sh = r & 3u;
+            const uint32_t d0 = sv[0], d1 = sv[1], d2 = sv[2], d3 = sv[3], d4 = sv[4];
+            const uint32_t w0 = __builtin_amdgcn_alignbyte(d1, d0, sh);
+            const uint32_t w1 = __builtin_amdgcn_alignbyte(d2, d1, sh);
+            const uint32_t w2 = __builtin_amdgcn_alignbyte(d3, d2, sh);
+            const uint32_t w3 = __builtin_amdgcn_alignbyte(d4, d3, sh);
+            const uint32_t m0 = mm & 0xffu, m1 = mm >> 8;
+            const uint2 sa = s_sel[m0], sb = s_sel[m1];
+            // window of the second byte: bytes c0 .. c0+7, c0 = popcount(m0) <= 8
+            const uint32_t c0 = (uint32_t)__popc(m0), q = c0 >> 2, t = c0 & 3u;
+            const uint32_t x0 = q == 0 ? w0 : (q == 1 ? w1 : w2);
+            const uint32_t x1 = q == 0 ? w1 : (q == 1 ? w2 : w3);
+            const uint32_t x2 = q == 0 ? w2 : w3;      // q == 2 has t == 0: unused
+            const uint32_t v0 = __builtin_amdgcn_alignbyte(x1, x0, t);
+            const uint32_t v1 = __builtin_amdgcn_alignbyte(x2, x1, t);
+            o = uint4{__builtin_amdgcn_perm(w1, w0, sa.x), __builtin_amdgcn_perm(w1, w0, sa.y),
+                      __builtin_amdgcn_perm(v1, v0, sb.x), __builtin_amdgcn_perm(v1, v0, sb.y)};
+        }
+        const int tile = 2 * k + jt;
+        const int64_t row = (int64_t)tm * 64 + 32 * h + (tid >> 3);
+        const int64_t col0 = (int64_t)(tn0 + tile) * 64 + 16 * pc;
+        if (tile < ntiles && row < a.rows && col0 < a.K) st16<NT>(a.out + row * a.K + col0, o);
+    }
+}
+
 // grad = bit ? bf16(grad * (2k * r)) : 0, then optionally grad = bf16(grad * bf16(scale))
 // NT: nontemporal gradient loads / stores and staging loads.
 template <int V_T, bool HAS_SCALE, bool VEC, int U, bool PACKED, bool NT>
@@ -1525,6 +1666,12 @@ __global__ void empty_compress_kernel(uint32_t* prefix, const int64_t* offset_in
 // ===========================================================================
 // compress unit: tiles per workgroup and workgroup size
 constexpr int kGatherU = 2;
+// adjacent tile pairs per workgroup of the plain fp8 decompress
+#ifndef BS_FP8_PAIRS
+#define BS_FP8_PAIRS 2
+#endif
+constexpr int kFp8Pairs = BS_FP8_PAIRS;
+
 constexpr int kMaskU = 4;
 
 static inline bool aligned16(const void* p) { return (((uintptr_t)p) & 15u) == 0; }
@@ -1836,6 +1983,19 @@ template <int V_T, bool SQ, bool SC, bool PK>
 static void launch_decompress_t(const GatherArgs& a, bool vec, bool nt, hipStream_t st)
 {
     const uint32_t blocks = (a.num_tiles + kGatherU - 1) / kGatherU;
+    if constexpr (V_T != DT_BF16 && !SQ) {
+        // fp8 bytes out: 16-byte stores when rows are whole 16-byte pieces
+        if (a.K % 16 == 0 && aligned16(a.out) && a.num_tiles % a.grid_n == 0) {
+            // one workgroup per kFp8Pairs adjacent tile pairs of a tile row
+            const uint32_t gpr = (a.grid_n + 2 * kFp8Pairs - 1) / (2 * kFp8Pairs);
+            const uint32_t b8 = (a.num_tiles / a.grid_n) * gpr;
+            if (nt)
+                launch_timed(1, decompress_fp8_kernel<V_T, kFp8Pairs, PK, true>, dim3(b8), dim3(kThreads), 0, st, a, gpr);
+            else
+                launch_timed(1, decompress_fp8_kernel<V_T, kFp8Pairs, PK, false>, dim3(b8), dim3(kThreads), 0, st, a, gpr);
+            return;
+        }
+    }
     if (vec && nt)
         launch_timed(1, decompress_kernel<V_T, SQ, SC, true, kGatherU, PK, true>, dim3(blocks), dim3(kThreads), 0, st, a);
     else if (vec)

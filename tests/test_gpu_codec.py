@@ -231,6 +231,37 @@ def test_unpack_row_batches(dev, shape):
             assert (bits(out) == ref).all()
 
 
+@pytest.mark.parametrize("code", [O.E4M3FN, O.E5M2])
+@pytest.mark.parametrize("shape", [(129, 144), (448, 512), (300, 200), (70, 24)])
+@pytest.mark.parametrize("packed", [False, True])
+def test_unpack_row_batches_fp8(dev, code, shape, packed):
+    """fp8 storage decompressed in row batches, bit-exact against the oracle.
+    Rows of whole 16-byte pieces (K % 16 == 0) take the 16-byte-store kernel,
+    other widths and an output that is not 16-byte aligned the chunk kernel."""
+    F, H, _ = _bs()
+    dt = torch.float8_e4m3fn if code == O.E4M3FN else torch.float8_e5m2
+    x = from_bits(all_fp8_patterns(shape, seed=31), dt)
+    xr = torch.where(x.float() > 0, x.float(), torch.zeros(())).to(dt)     # stored values are positive
+    sp = F.dense_to_tilesparse(xr.to(dev), None, pack_sbit=packed)
+    M, N = shape
+    gn = sp.grid_n
+    bm, pf, v = O.compress(bits(xr), code)
+    for first in range(sp.grid_m):
+        for nrows in (1, 2):
+            if first + nrows > sp.grid_m:
+                continue
+            rows = min(nrows * 64, M - first * 64)
+            ref = O.unpack(v, code, bm, pf, 0, first, gn, N, rows, nrows * gn)
+            out = torch.empty((rows, N), dtype=dt, device=dev)
+            H.unpack_batch_(sp, out, first, gn, N, rows, nrows * gn)
+            assert (bits(out) == ref).all()
+            # the same batch into an output 8 bytes past a 16-byte boundary
+            raw = torch.empty(rows * N + 16, dtype=torch.uint8, device=dev)
+            out8 = raw[8:8 + rows * N].view(dt).view(rows, N)
+            H.unpack_batch_(sp, out8, first, gn, N, rows, nrows * gn)
+            assert (bits(out8) == ref).all()
+
+
 def test_relu_grad(dev):
     F, H, _ = _bs()
     for shape in [(129, 131), (512, 768), (64, 8)]:
