@@ -56,6 +56,9 @@ _SIGNATURES = {
     "bs_gemm_compressed_b_workspace_bytes": [_i64, _i64, _i64, _int],
     "bs_gemm_compressed_b": [_vp, _i64, _i64, _i64, _int, _vp, _int, _i64, _vp, _vp, _vp, _i64, _int, _f32,
                              _vp, _vp, _vp, _i64, _vp],
+    "bs_gemm_compressed_b_fp8_workspace_bytes": [_i64, _i64, _i64, _int],
+    "bs_gemm_compressed_b_fp8": [_vp, _vp, _i64, _i64, _i64, _int, _vp, _int, _i64, _vp, _vp, _vp, _i64, _int,
+                                 _f32, _vp, _vp, _vp, _vp, _i64, _vp],
     "bs_pack_bits": [_vp, _int, _vp, _i64, _vp, _i64, _vp, _vp, _vp],
     "bs_decompress_packed": [_vp, _int, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _int,
                              _f32, _vp, _vp],
@@ -73,6 +76,7 @@ _RESTYPES = {
     "bs_last_error": ctypes.c_char_p,
     "bs_compress_workspace_bytes": _i64,
     "bs_gemm_compressed_b_workspace_bytes": _i64,
+    "bs_gemm_compressed_b_fp8_workspace_bytes": _i64,
     "bs_compress_noalloc_max_tiles": _i64,
     "bs_nontemporal_min_bytes": _i64,
     "bs_workspace_amax_slot": _vp,

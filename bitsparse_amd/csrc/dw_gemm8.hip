@@ -1,0 +1,913 @@
+// Reconstruct-into-LDS fp8 MFMA GEMM for gfx950:
+//     C[M, N] = bf16(sA * sB * (A @ Bq))
+// A: e4m3fn codes [M, K] with fp32 scale sA (in the MLP backward A = dY^T,
+// quantized by to_fp8).  B: a compressed [K, N] fp8 activation (64x64-tile
+// bitmask + prefix + values), decoded tile by tile into LDS and never
+// written to HBM in dense form:
+//   * square = 0 (AspB): Bq = the stored codes, sB = their stored scale;
+//   * square = 1 (AspRelu2B): Bq, sB = to_fp8(D) of the bf16 dense operand
+//     D = bf16(bf16((k r) r) * bf16(s^2)) that the reference decompresses and
+//     re-quantizes (lib_sparse/src/sparse_matmul.py:109-113,
+//     lib_sparse/src/triton_operators.py:160-161, lib_sparse/fp8.py:123-129).
+//     D is a function of the stored code alone, so is Bq: a 256-entry table
+//     code -> Bq code, built on the device before the GEMM from sB =
+//     max(amax|D| / 448, 1e-9).  amax|D| is |D(c)| of the stored code c of
+//     largest magnitude (|D| grows with |r|: each rounding is monotone; a NaN
+//     code sorts above every finite one, as in the amax kernel), or |D(0)| of
+//     the cleared elements.  Bq(c) = e4m3fn_RNE(D(c) / sB) with one correctly
+//     rounded division, the to_fp8 rule, so the decoded operand is bit for
+//     bit to_fp8(unpack_relu2_batch_(B)).
+// Replaces "decompress B to HBM, re-quantize, library fp8 GEMM" (hipBLASLt
+// scaled_mm) of the reference's fp8 AspB / AspRelu2B.
+//
+// Workgroup: a WGM x WGN grid of waves, each owning a WAVE_M x WAVE_N block
+// of C in v_mfma_scale_f32_32x32x64_f8f6f4 accumulators (e4m3 x e4m3, or
+// e4m3 x e5m2 for square = 0 from e5m2 storage; unit block scales).  One
+// K-step = 64 tokens = one row of B tiles = one MFMA deep.  Per step:
+//   * the step's B tiles are decoded into a double-buffered LDS tile (one
+//     8-byte chunk per lane per decode row): value runs are loaded one step
+//     ahead, staged in LDS (mapped through the code table on the way), and
+//     each chunk is built from an 8-byte window of its run with v_alignbyte
+//     and two v_perm_b32 (selectors from a 256-entry table per bitmask byte);
+//   * B fragments come out of the row-major tile with ds_read_b64_tr_b8
+//     (within a 16-lane group, output lane i byte b = source lane 2b + i/8,
+//     byte i%8), four per 32-column block;
+//   * A fragments (32 contiguous k of one row per lane) come from a packed
+//     copy of A in MFMA-fragment order, one 2 KiB block per (32 rows, 64 k),
+//     double-buffered across steps.
+// Workgroup ids are remapped so each XCD walks a contiguous range of C tiles.
+#include <algorithm>
+
+#include "bs_device.h"
+#include "bs_host.h"
+#include "gemm_common.h"
+
+namespace bs {
+
+typedef int i32x8_t __attribute__((ext_vector_type(8)));
+typedef int i32x2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kRun8Slots = kTileNumel / 16 + 2;   // one fp8 run + its phase, 16-byte slots
+
+template <int WGM_, int WGN_, int WM_, int WN_>
+struct Gemm8Cfg {
+    static constexpr int WGM = WGM_, WGN = WGN_, NWAVES = WGM_ * WGN_, THREADS = 64 * NWAVES;
+    static constexpr int WAVE_M = WM_, WAVE_N = WN_;
+    static constexpr int IM = WAVE_M / 32, JN = WAVE_N / 32;    // 32x32 accumulator blocks per wave
+    static constexpr int BM = WAVE_M * WGM, BN = WAVE_N * WGN;
+    static constexpr int NT = BN / 64;                           // B tiles per K-step
+    static constexpr int DW = NWAVES / NT;                       // waves decoding one B tile
+    static constexpr int CH = 8 / DW;                            // decode rows per lane per step
+    // B_s row pitch (bytes): BN + 32, an odd multiple of 32 bytes past a
+    // multiple of 256: any 8 consecutive rows start 8 banks apart around all
+    // 64, so a transposing fragment read (16 rows x 32 bytes) and a decode
+    // store (8 rows x 64 bytes) touch every bank exactly twice
+    static constexpr int BP = BN + 32;
+    static constexpr int SEG = IM * JN;                          // MFMAs per K-step
+    static constexpr int PER = SEG / CH;                         // MFMAs per decoded chunk
+    static constexpr int OFF_B = 0;                              // B_s[2][64][BP] bytes
+    static constexpr int OFF_RUN = OFF_B + 2 * kBK * BP;         // run_s[3][NT][kRun8Slots] uint4
+    static constexpr int OFF_BM = OFF_RUN + 3 * NT * kRun8Slots * 16;   // bm_s[NWAVES][64] uint64
+    static constexpr int OFF_RP = OFF_BM + NWAVES * 64 * 8;     // rp_s[NWAVES][64] uint32
+    static constexpr int OFF_SEL = OFF_RP + NWAVES * 64 * 4;    // sel_s[256] uint2
+    static constexpr int OFF_LUT = OFF_SEL + 256 * 8;           // lut_s[256] bytes
+    static constexpr int OFF_PF = OFF_LUT + 256;                 // pf_s[NT][kMaxSteps] uint2: prefix[t], prefix[t+1]
+    static constexpr int ST_P = WAVE_N + 4;                      // epilogue staging pitch (floats)
+    static constexpr int LDS_MAIN = OFF_PF + NT * kMaxSteps * 8;
+    static constexpr int LDS_EPI = NWAVES * 16 * ST_P * 4;      // the epilogue reuses the space
+    static constexpr int LDS = LDS_MAIN > LDS_EPI ? LDS_MAIN : LDS_EPI;
+    static_assert(LDS <= 160 * 1024, "LDS budget");
+    static_assert(NWAVES * 16 * ST_P * 4 <= LDS, "epilogue staging does not fit");
+    static_assert(NWAVES % NT == 0 && 8 % DW == 0 && SEG % CH == 0, "decode split");
+    static_assert(BP % 256 == 32 || BP % 256 == 160, "fragment-read bank spread");
+};
+// 4 x 1 waves of 128 x 128 (one per SIMD, accumulators in AGPRs): each
+// decoded B byte feeds 512 rows.  (8 x 1 waves of 64 x 128, two per SIMD, cap a
+// wave at 256 registers and spill.)
+using Cfg8_512 = Gemm8Cfg<8, 1, 64, 128>;
+// 2 x 2 waves of 128 x 128 (one per SIMD)
+using Cfg8_256 = Gemm8Cfg<2, 2, 128, 128>;
+
+struct Gemm8Args {
+    const uint8_t* Apk;           // A codes in MFMA-fragment order (pack_a8_*_kernel)
+    int64_t M, K;
+    uint32_t nkb;                 // 64-wide k blocks per 32-row block of Apk
+    uint32_t nrb;                 // 32-row blocks of Apk
+    const uint8_t* vals;          // compressed B
+    int64_t vals_numel;
+    const uint8_t* bitmask;
+    const uint32_t* prefix;
+    const int64_t* vals_offset;
+    int64_t N;
+    uint32_t grid_n;              // B tiles along N
+    uint32_t tiles_m, tiles_n;    // C tiles
+    const uint8_t* lut;           // code -> B code (square), 256 bytes
+    const float* a_scale;
+    const float* b_scale;         // sB
+    uint16_t* C;                  // [M, N] bf16 (no split)
+    float* part;                  // [split, M, N] fp32 unscaled partial sums (split > 1)
+    uint32_t ksteps;
+    uint32_t ksteps_per_split;
+};
+
+// LUT: stored codes are mapped through lut_s while staged.  FMT_B: MFMA
+// format of B (0 e4m3, 1 e5m2).
+template <typename CFG, bool LUT, int FMT_B>
+__global__ __launch_bounds__(CFG::THREADS, 1) void gemm_cb8_kernel(Gemm8Args a)
+{
+    constexpr int NT = CFG::NT, DW = CFG::DW, CH = CFG::CH, BP = CFG::BP, IM = CFG::IM, JN = CFG::JN;
+    constexpr int RX = (15 + kTileNumel + 15) / 16;              // 16-byte units of a run, worst case
+    constexpr int RXD = (RX + 64 * DW - 1) / (64 * DW);          // per lane, worst case
+
+    __shared__ __align__(16) uint8_t lds[CFG::LDS];
+    uint8_t* B_s = lds + CFG::OFF_B;
+    uint4* run_s = reinterpret_cast<uint4*>(lds + CFG::OFF_RUN);
+    uint64_t* bm_s = reinterpret_cast<uint64_t*>(lds + CFG::OFF_BM);
+    uint32_t* rp_s = reinterpret_cast<uint32_t*>(lds + CFG::OFF_RP);
+    uint2* sel_s = reinterpret_cast<uint2*>(lds + CFG::OFF_SEL);
+    uint8_t* lut_s = lds + CFG::OFF_LUT;
+    uint2* pf_s = reinterpret_cast<uint2*>(lds + CFG::OFF_PF);
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+    // ---- XCD-aware tile order: XCD x runs a contiguous range of tile ids
+    const uint32_t nb = gridDim.x, b = blockIdx.x;
+    const uint32_t xcd = b % kXcds, q = b / kXcds;
+    const uint32_t per = nb / kXcds, rem = nb % kXcds;
+    const uint32_t id = xcd * per + min(xcd, rem) + q;
+    const uint32_t tn = (uint32_t)__builtin_amdgcn_readfirstlane((int)(id % a.tiles_n));
+    const uint32_t rest = id / a.tiles_n;
+    const uint32_t tm = (uint32_t)__builtin_amdgcn_readfirstlane((int)(rest % a.tiles_m));
+    const uint32_t split = (uint32_t)__builtin_amdgcn_readfirstlane((int)(rest / a.tiles_m));
+
+    const uint32_t nt0 = tn * NT;                      // first B tile column
+    const int tw = wave / DW;                          // the B tile this wave helps decode
+    const int tq = wave % DW;                          // its share: rows 8 CH tq .. +8 CH
+    const uint32_t tcol = nt0 + (uint32_t)tw;
+    const bool has_tile = tcol < a.grid_n;
+    const int64_t m0 = (int64_t)tm * CFG::BM;
+    const uint32_t kt0 = split * a.ksteps_per_split;
+    const uint32_t kt1 = min(a.ksteps, kt0 + a.ksteps_per_split);
+    const int nsteps = kt1 > kt0 ? (int)(kt1 - kt0) : 0;
+    const int last = nsteps - 1;
+
+    // selectors of bitmask byte x: set element e takes window byte rank(e),
+    // 0x0c gives 0x00; the code table
+    if (tid < 256) {
+        uint32_t sel[2] = {0x0c0c0c0cu, 0x0c0c0c0cu};
+        uint32_t rank = 0;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            if ((tid >> e) & 1) {
+                sel[e >> 2] = (sel[e >> 2] & ~(0xffu << (8 * (e & 3)))) | (rank << (8 * (e & 3)));
+                rank++;
+            }
+        }
+        sel_s[tid] = uint2{sel[0], sel[1]};
+        lut_s[tid] = LUT ? a.lut[tid] : (uint8_t)tid;
+    }
+    // a cleared element decodes to the code of 0 (not 0x00 for k < 0 or a
+    // NaN scale): fixed up after the permutes when different
+    const uint32_t zero_b = LUT ? (uint32_t)a.lut[0] : 0u;
+    const bool zfix = zero_b != 0u;
+
+    // ---- prefix[t], prefix[t+1] of every step of each B tile column of the
+    // workgroup, in LDS (nsteps <= kMaxSteps)
+    for (int i = tid; i < NT * kMaxSteps; i += CFG::THREADS) {
+        const int tc = i / kMaxSteps, st = i % kMaxSteps;
+        const uint32_t col = nt0 + (uint32_t)tc;
+        uint2 v = {0u, 0u};
+        if (col < a.grid_n && st < nsteps) {
+            const size_t t = (size_t)(kt0 + (uint32_t)st) * a.grid_n + col;
+            v = uint2{a.prefix[t], a.prefix[t + 1]};
+        }
+        pf_s[i] = v;
+    }
+    const int64_t vo = a.vals_offset ? *a.vals_offset : 0;
+    // value run of step s (wave-uniform): 16-byte aligned start e0, phase =
+    // run start - e0, nunits 16-byte staging units
+    auto run_geom = [&](int s, int64_t& e0, int& phase, int& nunits) __attribute__((always_inline)) {
+        const uint2 pv = pf_s[tw * kMaxSteps + s];
+        const uint32_t p[2] = {uniform_u32(pv.x), uniform_u32(pv.y)};
+        const int64_t run0 = vo + (int64_t)p[0];
+        int64_t cnt = (int64_t)p[1] - (int64_t)p[0];
+        cnt = cnt < 0 ? 0 : (cnt > kTileNumel ? kTileNumel : cnt);
+        phase = (int)(run0 & 15);
+        e0 = run0 - phase;
+        nunits = cnt == 0 ? 0 : (phase + (int)cnt + 15) / 16;
+    };
+
+    // ---- run staging: the units of step s are loaded into registers one
+    // iteration before they are written to LDS (unit u by lane u % 64 of
+    // wave (u / 64) % DW of the tile's waves, pass u / (64 DW))
+    uint4 rr[2][RXD];
+    int rr_nunits[2] = {0, 0};
+    auto load_run = [&](int s, auto SL) __attribute__((always_inline)) {
+        constexpr int SLOT = decltype(SL)::value;
+        int64_t e0;
+        int phase, nunits;
+        run_geom(s, e0, phase, nunits);
+        const int64_t avail = a.vals_numel - e0;       // bytes readable from e0
+        const bool ok = e0 >= 0 && avail > 0 && nunits > 0;
+        int64_t bytes = ok ? avail : 0;
+        if (bytes > (int64_t)nunits * 16) bytes = (int64_t)nunits * 16;
+        rr_nunits[SLOT] = ok ? nunits : 0;
+        const bs_rsrc rs = make_rsrc(ok ? a.vals + e0 : a.vals, (uint32_t)bytes);
+        const bool tail = ok && (int64_t)nunits * 16 > avail;   // the run's last unit crosses the end of vals
+#pragma unroll
+        for (int x = 0; x < RXD; x++) {
+            const int u = (x * DW + tq) * 64 + lane;
+            if ((x * DW + tq) * 64 < rr_nunits[SLOT]) {
+                uint4 v = load16(rs, (uint32_t)u * 16u);
+                if (tail && (int64_t)(u + 1) * 16 > avail && (int64_t)u * 16 < avail) {
+                    uint32_t w[4] = {0u, 0u, 0u, 0u};
+                    for (int e = 0; e < 16; e++)
+                        w[e >> 2] |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rs, (int)(u * 16 + e), 0, 0)
+                                     << (8 * (e & 3));
+                    v = uint4{w[0], w[1], w[2], w[3]};
+                }
+                rr[SLOT][x] = v;
+            }
+        }
+    };
+    auto store_run = [&](int buf, auto SL) __attribute__((always_inline)) {
+        constexpr int SLOT = decltype(SL)::value;
+        uint4* dst = run_s + (buf * NT + tw) * kRun8Slots;
+#pragma unroll
+        for (int x = 0; x < RXD; x++) {
+            const int u = (x * DW + tq) * 64 + lane;
+            if ((x * DW + tq) * 64 < rr_nunits[SLOT] && u < rr_nunits[SLOT]) {
+                const uint4 v = rr[SLOT][x];
+                if constexpr (LUT) {
+                    // one dword at a time (few live registers)
+                    uint32_t* d32 = reinterpret_cast<uint32_t*>(dst + u);
+                    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                    for (int d = 0; d < 4; d++) {
+                        uint32_t o = 0;
+#pragma unroll
+                        for (int e = 0; e < 4; e++) o |= (uint32_t)lut_s[(w[d] >> (8 * e)) & 0xffu] << (8 * e);
+                        d32[d] = o;
+                    }
+                } else {
+                    dst[u] = v;
+                }
+            }
+        }
+    };
+
+    // ---- bitmask rows: lane r holds row r of this wave's tile of step s
+    auto load_bm = [&](int s) __attribute__((always_inline)) -> uint64_t {
+        const size_t t = (size_t)(kt0 + (uint32_t)s) * a.grid_n + tcol;
+        const bs_rsrc rs = make_rsrc(a.bitmask + (has_tile ? t : 0) * kTileBytes,
+                                     has_tile ? (uint32_t)kTileBytes : 0u);
+        const uint2 v = load8(rs, (uint32_t)lane * 8u);
+        return (uint64_t)v.x | ((uint64_t)v.y << 32);
+    };
+
+    // ---- decode: lane l handles chunk dc = l%8 (8 bytes at column 8 dc) of
+    // CH rows, row = rbase + 8i + l/8
+    const int dc = lane & 7, dg = lane >> 3;
+    const uint64_t below_mask = dc == 0 ? 0ull : (~0ull >> (64 - 8 * dc));
+    const int rbase = 8 * CH * tq;
+    auto decode_rows = [&](int s, uint64_t bmr) __attribute__((always_inline)) {
+        int64_t e0;
+        int phase, nunits;
+        run_geom(s, e0, phase, nunits);
+        const uint32_t c = (uint32_t)__popcll(bmr);
+        const uint32_t rp = wave_incl_scan(c) - c;
+        bm_s[wave * 64 + lane] = bmr;
+        rp_s[wave * 64 + lane] = rp + (uint32_t)phase;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+    struct Dec {
+        uint64_t mrow;
+        uint32_t rpr;
+        uint2 sel;
+        uint32_t d0, d1, d2, sh;
+    };
+    Dec dq[2];
+    auto stage_r = [&](auto CI) __attribute__((always_inline)) {
+        constexpr int C = decltype(CI)::value;
+        const int row = rbase + 8 * C + dg;
+        dq[C & 1].mrow = bm_s[wave * 64 + row];
+        dq[C & 1].rpr = rp_s[wave * 64 + row];
+    };
+    auto stage_s = [&](auto CI, const uint32_t* run32) __attribute__((always_inline)) {
+        constexpr int C = decltype(CI)::value;
+        Dec& d = dq[C & 1];
+        const uint32_t byte = (uint32_t)(d.mrow >> (8 * dc)) & 0xffu;
+        const uint32_t ra = d.rpr + (uint32_t)__popcll(d.mrow & below_mask);
+        d.sel = sel_s[byte];
+        d.sh = ra & 3u;
+        d.d0 = run32[(ra >> 2)];
+        d.d1 = run32[(ra >> 2) + 1];
+        d.d2 = run32[(ra >> 2) + 2];
+    };
+    auto stage_w = [&](auto CI, uint8_t* dst) __attribute__((always_inline)) {
+        constexpr int C = decltype(CI)::value;
+        const Dec& d = dq[C & 1];
+        const uint32_t w0 = __builtin_amdgcn_alignbyte(d.d1, d.d0, d.sh);
+        const uint32_t w1 = __builtin_amdgcn_alignbyte(d.d2, d.d1, d.sh);
+        const uint32_t o0 = __builtin_amdgcn_perm(w1, w0, d.sel.x);
+        const uint32_t o1 = __builtin_amdgcn_perm(w1, w0, d.sel.y);
+        *reinterpret_cast<uint2*>(&dst[(rbase + 8 * C + dg) * BP]) = uint2{o0, o1};
+    };
+    auto run_ptr = [&](int rb) __attribute__((always_inline)) {
+        return reinterpret_cast<const uint32_t*>(run_s + (rb * NT + tw) * kRun8Slots);
+    };
+    auto dst_ptr = [&](int bb) __attribute__((always_inline)) {
+        return B_s + bb * (kBK * BP) + tw * 64 + dc * 8;
+    };
+    auto decode = [&](int rb, int bb) __attribute__((always_inline)) {
+        const uint32_t* run32 = run_ptr(rb);
+        uint8_t* dst = dst_ptr(bb);
+        static_for<CH>([&](auto CI) __attribute__((always_inline)) {
+            stage_r(CI);
+            stage_s(CI, run32);
+            stage_w(CI, dst);
+        });
+    };
+    // cleared elements of this wave's rows of B_s[bb] -> zero_b
+    auto zero_fixup = [&](int bb) __attribute__((always_inline)) {
+        uint8_t* dst = dst_ptr(bb);
+        for (int i = 0; i < CH; i++) {
+            const int row = rbase + 8 * i + dg;
+            const uint32_t byte = (uint32_t)(bm_s[wave * 64 + row] >> (8 * dc)) & 0xffu;
+            uint2 v = *reinterpret_cast<const uint2*>(&dst[row * BP]);
+            uint32_t w[2] = {v.x, v.y};
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                if (!((byte >> e) & 1u)) w[e >> 2] = (w[e >> 2] & ~(0xffu << (8 * (e & 3)))) | (zero_b << (8 * (e & 3)));
+            *reinterpret_cast<uint2*>(&dst[row * BP]) = uint2{w[0], w[1]};
+        }
+    };
+
+    // ---- A fragments: lane l of block i holds row 32i + l%32, k = 32(l/32)
+    // .. +31 of the step: 32 contiguous bytes of Apk at 32 l of its 2 KiB block
+    const int wm = wave % CFG::WGM, wn = wave / CFG::WGM;
+    const int64_t arow0 = m0 + wm * CFG::WAVE_M;
+    const uint32_t rb0 = (uint32_t)(arow0 / 32);
+    const uint32_t nrbw = rb0 < a.nrb ? min((uint32_t)IM, a.nrb - rb0) : 0u;
+    const bs_rsrc rsA = make_rsrc(nrbw ? a.Apk + (int64_t)rb0 * a.nkb * 2048 : a.Apk, nrbw * a.nkb * 2048u);
+    i32x8_t areg[2][IM];
+    auto load_a = [&](int s, auto SI) __attribute__((always_inline)) {
+        constexpr int SET = decltype(SI)::value;
+#pragma unroll
+        for (int i = 0; i < IM; i++) {
+            const uint32_t off = ((uint32_t)i * a.nkb + kt0 + (uint32_t)s) * 2048u + (uint32_t)lane * 32u;
+            const uint4 lo = load16(rsA, off), hi = load16(rsA, off + 16u);
+            areg[SET][i] = i32x8_t{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+        }
+    };
+
+    f32x16_t acc[IM][JN];
+#pragma unroll
+    for (int i = 0; i < IM; i++)
+#pragma unroll
+        for (int jj = 0; jj < JN; jj++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][jj][r] = 0.0f;
+
+    // ---- B fragments of column block jj: lane L (group g = L/16, j = L%16)
+    // points read c at row 32(g/2) + 8c + j/2, columns 16(g%2) + 8(j%2) ..+7
+    // of the wave's block; the four reads are k = 8c .. 8c+7 of its column
+    const int fg = lane >> 4, fj = lane & 15;
+    const int fr = 32 * (fg >> 1) + (fj >> 1);
+    const int fc = wn * CFG::WAVE_N + 16 * (fg & 1) + 8 * (fj & 1);
+    i32x8_t breg[2];
+    auto read_b = [&](const uint8_t* Bs, int jj, int set) __attribute__((always_inline)) {
+        typedef __attribute__((address_space(3))) i32x2_t lds_i32x2;
+        i32x2_t v[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+            v[c] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)(Bs + (fr + 8 * c) * BP + fc + jj * 32));
+        breg[set] = i32x8_t{v[0][0], v[0][1], v[1][0], v[1][1], v[2][0], v[2][1], v[3][0], v[3][1]};
+    };
+
+    // One K-step: SEG MFMAs (column block jj outer, row block i inner), fenced
+    // by sched_barrier so the order below is the issue order.  The next column
+    // block's B fragments are read during the current one; one stage of the
+    // software-pipelined decode of the next step goes with each MFMA (chunk
+    // X/PER: stage_r at X%PER == 0, stage_s half a period later, stage_w at
+    // the next chunk's stage_r).
+    auto step = [&](int s, auto RI) __attribute__((always_inline)) {
+        constexpr int P = decltype(RI)::value;          // s & 1: B_s buffer and A register set
+        constexpr int AS = P;
+        constexpr int PER = CFG::PER;
+        const uint8_t* Bs = B_s + P * (kBK * BP);
+        const uint32_t* run32 = run_ptr((s + 1) % 3);   // run(s+1) -> B_s[P ^ 1]
+        uint8_t* dst = dst_ptr(P ^ 1);
+        read_b(Bs, 0, 0);
+        static_for<CFG::SEG>([&](auto XI) __attribute__((always_inline)) {
+            constexpr int X = decltype(XI)::value;
+            constexpr int jj = X / IM, i = X % IM;
+            if constexpr (i == 0 && jj + 1 < JN) read_b(Bs, jj + 1, (jj + 1) & 1);
+            acc[i][jj] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(areg[AS][i], breg[jj & 1], acc[i][jj],
+                                                                       0, FMT_B, 0, 127, 0, 127);
+            // keep the MFMA in its segment: its result is next needed a step
+            // later, and the compiler would otherwise sink all of them past
+            // the run staging to the end of the iteration
+            asm volatile("" : "+a"(acc[i][jj]));
+            if constexpr (X % PER == 0) stage_r(IC<X / PER>{});
+            if constexpr (X % PER == PER / 2) stage_s(IC<X / PER>{}, run32);
+            if constexpr (X % PER == 0 && X >= PER) stage_w(IC<X / PER - 1>{}, dst);
+            __builtin_amdgcn_sched_barrier(0);
+        });
+        stage_w(IC<CH - 1>{}, dst);
+    };
+
+    // Pipeline.  Step j: run(j) staged in run_s[j % 3] through register slot
+    // j & 1, bitmask rows in bmq[j & 1], A(j) in areg[j & 1], B(j) decoded
+    // into B_s[j & 1].  Iteration s builds the row table of step s+1, then
+    // issues (in this order, so that waiting for a run never waits for A) the
+    // rows and run of step s+3 and A(s+1); multiplies step s while decoding
+    // B(s+1) from run_s[(s+1) % 3]; stages run(s+2), loaded an iteration ago,
+    // into run_s[(s+2) % 3] (freed by the decode of step s-1) and meets the
+    // other waves at the barrier.  Runs thus get two iterations to arrive, A
+    // one.  Loads past the last step re-read it.
+    uint64_t bmq[2] = {0ull, 0ull};
+    __syncthreads();                                   // sel_s, lut_s, pf_s
+    if (nsteps > 0) {
+        load_run(0, IC<0>{});
+        store_run(0, IC<0>{});
+        load_run(min(1, last), IC<1>{});
+        store_run(1, IC<1>{});
+        bmq[0] = load_bm(0);
+        bmq[1] = load_bm(min(1, last));
+        load_a(0, IC<0>{});
+    }
+    __syncthreads();
+    if (nsteps > 0) {
+        decode_rows(0, bmq[0]);
+        decode(0, 0);
+        if (zfix) zero_fixup(0);
+        bmq[0] = load_bm(min(2, last));
+        load_run(min(2, last), IC<0>{});
+    }
+    __syncthreads();
+    auto iteration = [&](int s, auto RI) __attribute__((always_inline)) {
+        constexpr int P = decltype(RI)::value;         // s & 1
+        const int s1 = min(s + 1, last), s3 = min(s + 3, last);
+        decode_rows(s1, bmq[P ^ 1]);
+        bmq[P ^ 1] = load_bm(s3);
+        load_run(s3, IC<P ^ 1>{});
+        load_a(s1, IC<P ^ 1>{});
+        step(s, RI);
+        if (zfix) zero_fixup(P ^ 1);
+        store_run((s + 2) % 3, IC<P>{});
+        __syncthreads();
+    };
+    int s = 0;
+    for (; s + 1 < nsteps; s += 2) {
+        iteration(s, IC<0>{});
+        iteration(s + 1, IC<1>{});
+    }
+    if (s < nsteps) iteration(s, IC<0>{});
+
+    // ---- epilogue: as the bf16 GEMM's (half a 32-row block at a time through
+    // LDS, 16-byte row segments), scaled by sA * sB; split partials unscaled
+    const float sc = (*a.a_scale) * (*a.b_scale);
+    constexpr int ST_P = CFG::ST_P;
+    constexpr int LPR = CFG::WAVE_N / 4;
+    constexpr int RPI = 64 / LPR;
+    const int hh = lane >> 5, col = lane & 31;
+    float* st = reinterpret_cast<float*>(lds) + wave * (16 * ST_P);
+    const int64_t col0 = (int64_t)nt0 * 64 + wn * CFG::WAVE_N;
+    const bool cvec = (a.N % 4 == 0) && (a.part != nullptr || (((uintptr_t)a.C) & 7) == 0);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < IM; i++) {
+#pragma unroll
+        for (int half = 0; half < 2; half++) {
+#pragma unroll
+            for (int jj = 0; jj < JN; jj++)
+#pragma unroll
+                for (int r = 8 * half; r < 8 * half + 8; r++)
+                    st[(8 * ((r >> 2) & 1) + 4 * hh + (r & 3)) * ST_P + jj * 32 + col] = acc[i][jj][r];
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+            for (int it = 0; it < 16 / RPI; it++) {
+                const int rr2 = RPI * it + lane / LPR;
+                const int64_t row = arow0 + i * 32 + 16 * half + rr2;
+                const int64_t c4 = col0 + 4 * (lane % LPR);
+                const float4 v = *reinterpret_cast<const float4*>(&st[rr2 * ST_P + 4 * (lane % LPR)]);
+                if (row >= a.M || c4 >= a.N) continue;
+                if (a.part) {
+                    float* dst = a.part + ((int64_t)split * a.M + row) * a.N + c4;
+                    if (cvec) {
+                        *reinterpret_cast<float4*>(dst) = v;
+                    } else {
+                        const float e[4] = {v.x, v.y, v.z, v.w};
+                        for (int x = 0; x < 4 && c4 + x < a.N; x++) dst[x] = e[x];
+                    }
+                } else {
+                    uint16_t* dst = a.C + row * a.N + c4;
+                    const uint32_t b0 = f32_to_bf16(v.x * sc), b1 = f32_to_bf16(v.y * sc);
+                    const uint32_t b2 = f32_to_bf16(v.z * sc), b3 = f32_to_bf16(v.w * sc);
+                    if (cvec) {
+                        *reinterpret_cast<uint2*>(dst) = uint2{b0 | (b1 << 16), b2 | (b3 << 16)};
+                    } else {
+                        const uint32_t e[4] = {b0, b1, b2, b3};
+                        for (int x = 0; x < 4 && c4 + x < a.N; x++) dst[x] = (uint16_t)e[x];
+                    }
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+    }
+}
+
+// A codes -> Apk8: block (rb * nkb + kb) of 2 KiB holds, at 32 l, A[32 rb +
+// l%32][64 kb + 32 (l/32) .. +31]; zero past M and K.
+__device__ __forceinline__ int64_t apk8_index(int64_t m, int64_t k, uint32_t nkb)
+{
+    const int64_t rb = m >> 5, kb = k >> 6;
+    const int l = (int)(m & 31) + 32 * (int)((k >> 5) & 1);
+    return (rb * nkb + kb) * 2048 + l * 32 + (k & 31);
+}
+
+// from At [K, M] (row stride ldat, m contiguous): 64 x 64 blocks through LDS
+__global__ __launch_bounds__(256) void pack_a8_t_kernel(const uint8_t* At, int64_t K, int64_t M, int64_t ldat,
+                                                        uint8_t* Apk, uint32_t nkb)
+{
+    __shared__ __align__(16) uint8_t t[64][64 + 16];
+    const int tid = threadIdx.x;
+    const int64_t k0 = (int64_t)blockIdx.x * 64, m0 = (int64_t)blockIdx.y * 64;
+    {
+        const int row = tid >> 2, c16 = (tid & 3) * 16;          // k row, 16 m
+        const int64_t k = k0 + row, m = m0 + c16;
+        uint4 v = {0u, 0u, 0u, 0u};
+        if (k < K && m < M) {
+            const uint8_t* src = At + k * ldat + m;
+            if (m + 16 <= M && (((uintptr_t)src) & 15) == 0) {
+                v = *reinterpret_cast<const uint4*>(src);
+            } else {
+                uint32_t w[4] = {0u, 0u, 0u, 0u};
+                for (int e = 0; e < 16 && m + e < M; e++) w[e >> 2] |= (uint32_t)src[e] << (8 * (e & 3));
+                v = uint4{w[0], w[1], w[2], w[3]};
+            }
+        }
+        *reinterpret_cast<uint4*>(&t[row][c16]) = v;
+    }
+    __syncthreads();
+    const int64_t mrows = (M + 31) / 32 * 32;           // Apk rows (whole 32-row blocks)
+    {
+        const int mm = tid >> 2, kc = (tid & 3) * 16;           // m row, 16 k
+        if (m0 + mm < mrows) {
+            uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int e = 0; e < 16; e++) w[e >> 2] |= (uint32_t)t[kc + e][mm] << (8 * (e & 3));
+            *reinterpret_cast<uint4*>(Apk + apk8_index(m0 + mm, k0 + kc, nkb)) = uint4{w[0], w[1], w[2], w[3]};
+        }
+    }
+}
+
+// from A [M, K] (row stride lda, k contiguous): one 16-byte piece per thread
+__global__ __launch_bounds__(256) void pack_a8_n_kernel(const uint8_t* A, int64_t K, int64_t M, int64_t lda,
+                                                        uint8_t* Apk, uint32_t nkb, int64_t pieces)
+{
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    for (int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x; p < pieces; p += stride) {
+        const int64_t blk = p >> 7;                    // 128 pieces per 2 KiB block
+        const int l = (int)((p >> 1) & 63), h = (int)(p & 1);
+        const int64_t rb = blk / nkb, kb = blk % nkb;
+        const int64_t m = rb * 32 + (l & 31), k = kb * 64 + 32 * (l >> 5) + 16 * h;
+        uint4 v = {0u, 0u, 0u, 0u};
+        if (m < M && k < K) {
+            const uint8_t* src = A + m * lda + k;
+            if (k + 16 <= K && (((uintptr_t)src) & 15) == 0) {
+                v = *reinterpret_cast<const uint4*>(src);
+            } else {
+                uint32_t w[4] = {0u, 0u, 0u, 0u};
+                for (int e = 0; e < 16 && k + e < K; e++) w[e >> 2] |= (uint32_t)src[e] << (8 * (e & 3));
+                v = uint4{w[0], w[1], w[2], w[3]};
+            }
+        }
+        reinterpret_cast<uint4*>(Apk)[p] = v;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// square = 1: the code table and sB
+// ---------------------------------------------------------------------------
+struct Lut8Args {
+    const uint8_t* vals;
+    int64_t vals_numel;
+    const uint32_t* prefix;       // prefix[0], prefix[T]: the tensor's run relative to vals_offset
+    int64_t T;
+    const int64_t* vals_offset;
+    int64_t dense_numel;          // K * N (cleared elements exist iff nnz < this)
+    float relu2_scale;
+    const float* r_scale;         // stored values' scale (may be null: bf16(scale^2) not applied)
+    uint32_t* cmax;               // reduction slot (zeroed by the caller's launch order)
+    uint8_t* lut;                 // 256 bytes
+    float* b_scale;               // sB
+    float* b_scale_out;           // optional copy for the caller
+};
+
+// magnitude order of a stored code: its low 7 bits (e4m3fn / e5m2 codes of
+// equal sign sort like their values; NaN codes above every finite one)
+__global__ __launch_bounds__(256) void code_max_kernel(Lut8Args a)
+{
+    const int64_t vo = a.vals_offset ? *a.vals_offset : 0;
+    const int64_t b0 = vo + (int64_t)a.prefix[0];
+    int64_t b1 = vo + (int64_t)a.prefix[a.T];
+    if (b1 > a.vals_numel) b1 = a.vals_numel;
+    uint32_t m = 0;
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    for (int64_t i = b0 + (int64_t)blockIdx.x * 256 + threadIdx.x; i < b1; i += stride)
+        m = max(m, (uint32_t)a.vals[i] & 0x7fu);
+    m = wave_max_u32(m);
+    __shared__ uint32_t s_w[4];
+    if ((threadIdx.x & 63) == 0) s_w[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        m = max(max(s_w[0], s_w[1]), max(s_w[2], s_w[3]));
+        if (m != 0u) atomicMax(a.cmax, m | 0x100u);       // bit 8: some value is stored
+    }
+}
+
+// D(c) of code c as bf16 bits: the ReLU^2 unpack of fp8 storage
+// (bf16((k v) v), then bf16(. * bf16(s^2)) with a scale)
+template <int V_T>
+__device__ __forceinline__ uint32_t relu2_dense_bits(uint32_t c, float k, bool has_scale, float s2b)
+{
+    const float v = fp8_to_f32<V_T>(c);
+    uint32_t x = f32_to_bf16((k * v) * v);
+    if (has_scale) x = f32_to_bf16(bf16_to_f32(x) * s2b);
+    return x;
+}
+
+template <int V_T>
+__global__ __launch_bounds__(256) void relu2_lut_kernel(Lut8Args a)
+{
+    __shared__ float s_scale;
+    const uint32_t c = threadIdx.x;
+    const bool has_scale = a.r_scale != nullptr;
+    float s2b = 1.0f;
+    if (has_scale) {
+        const float s = *a.r_scale;
+        s2b = bf16_to_f32(f32_to_bf16(s * s));
+    }
+    const float k = a.relu2_scale;
+    // code 0 stands for the cleared elements, which the ReLU^2 unpack writes
+    // as bf16(0 * bf16(s^2)) (0 without a scale); stored codes are positive
+    const uint32_t zero_x = has_scale ? f32_to_bf16(0.0f * s2b) : 0u;
+    const uint32_t x = c == 0 ? zero_x : relu2_dense_bits<V_T>(c, k, has_scale, s2b);
+    if (c == 0) {
+        const uint32_t cm = *a.cmax;
+        const int64_t nnz = (int64_t)a.prefix[a.T] - (int64_t)a.prefix[0];
+        // amax over |D| of the stored codes (the one of largest magnitude) and
+        // of the cleared elements; NaN magnitudes sort above Inf
+        uint32_t amag = 0;
+        if (cm & 0x100u) {
+            const uint32_t cmax = cm & 0x7fu;
+            const uint32_t dmax = relu2_dense_bits<V_T>(cmax, k, has_scale, s2b);
+            amag = dmax & 0x7fffu;
+        }
+        if (nnz < a.dense_numel) amag = max(amag, zero_x & 0x7fffu);
+        const float amax = bf16_to_f32(amag);
+        const float sc = amax / 448.0f;
+        s_scale = (sc < 1e-9f) ? 1e-9f : sc;
+        *a.b_scale = s_scale;
+        if (a.b_scale_out) *a.b_scale_out = s_scale;
+    }
+    __syncthreads();
+    a.lut[c] = (uint8_t)f32_to_e4m3(bf16_to_f32(x) / s_scale);
+}
+
+__global__ void write_u32_kernel(uint32_t* p, uint32_t v)
+{
+    if (threadIdx.x == 0) *p = v;
+}
+
+__global__ void copy_scale_kernel(const float* src, float* dst, float* dst2)
+{
+    if (threadIdx.x == 0) {
+        *dst = *src;
+        if (dst2) *dst2 = *src;
+    }
+}
+
+// C = bf16(scale * sum over splits of part), summed in split order
+__global__ __launch_bounds__(256) void splitk_reduce_scaled_kernel(const float* part, int split, int64_t n,
+                                                                   const float* a_scale, const float* b_scale,
+                                                                   uint16_t* C)
+{
+    const float sc = (*a_scale) * (*b_scale);
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) {
+        float s = part[i];
+        for (int k = 1; k < split; k++) s += part[(int64_t)k * n + i];
+        C[i] = (uint16_t)f32_to_bf16(s * sc);
+    }
+}
+
+__global__ __launch_bounds__(256) void zero_fill_u16_8_kernel(uint16_t* C, int64_t n)
+{
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) C[i] = 0;
+}
+
+static int gemm8_split(int64_t M, int64_t N, int64_t K, int64_t bm, int64_t bn)
+{
+    const int64_t tiles = ((N + bn - 1) / bn) * ((M + bm - 1) / bm);
+    const int64_t ksteps = (K + kBK - 1) / kBK;
+    const int64_t min_split = (ksteps + kMaxSteps - 1) / kMaxSteps;
+    int64_t best = min_split, best_cost = -1;
+    for (int64_t s = min_split; s <= 64; s++) {
+        if (s > min_split && ksteps / s < 8) break;
+        const int64_t rounds = (tiles * s + kCus - 1) / kCus;
+        const int64_t cost = rounds * ((ksteps + s - 1) / s) + (s > 1 ? 2 : 0);
+        if (best_cost < 0 || cost < best_cost) {
+            best = s;
+            best_cost = cost;
+        }
+    }
+    return (int)best;
+}
+
+struct Gemm8Plan {
+    bool big;
+    int64_t bm, bn;
+    int split;
+};
+static Gemm8Plan gemm8_plan(int64_t M, int64_t N, int64_t K)
+{
+    Gemm8Plan p;
+    const int64_t pad512 = (M + Cfg8_512::BM - 1) / Cfg8_512::BM * Cfg8_512::BM;
+    const int64_t pad256 = (M + Cfg8_256::BM - 1) / Cfg8_256::BM * Cfg8_256::BM;
+    p.big = M >= Cfg8_512::BM && pad512 <= pad256;
+    p.bm = p.big ? Cfg8_512::BM : Cfg8_256::BM;
+    p.bn = p.big ? Cfg8_512::BN : Cfg8_256::BN;
+    p.split = gemm8_split(M, N, K, p.bm, p.bn);
+    return p;
+}
+
+static int64_t apk8_nkb(int64_t K) { return (K + kBK - 1) / kBK; }
+static int64_t apk8_bytes(int64_t M, int64_t K) { return (M + 31) / 32 * apk8_nkb(K) * 2048; }
+static int64_t up256(int64_t x) { return (x + 255) / 256 * 256; }
+constexpr int64_t kLutAreaBytes = 512;     // lut[256], sB, code-max slot
+
+}  // namespace bs
+
+using namespace bs;
+
+extern "C" int64_t bs_gemm_compressed_b_fp8_workspace_bytes(int64_t M, int64_t N, int64_t K, int a_layout)
+{
+    (void)a_layout;
+    if (M <= 0 || N <= 0 || K <= 0) return kLutAreaBytes;
+    const int split = gemm8_plan(M, N, K).split;
+    int64_t bytes = split > 1 ? up256((int64_t)split * M * N * 4) : 0;
+    bytes += up256(apk8_bytes(M, K));
+    return bytes + kLutAreaBytes;
+}
+
+extern "C" int bs_gemm_compressed_b_fp8(const void* A, const float* a_scale, int64_t M, int64_t K, int64_t lda,
+                                        int a_layout, const void* vals, int vals_dtype, int64_t vals_numel,
+                                        const uint8_t* bitmask, const uint32_t* prefix, const int64_t* vals_offset,
+                                        int64_t N, int square, float relu2_scale, const float* b_scale, void* C,
+                                        float* b_scale_out, void* workspace, int64_t workspace_bytes, void* stream)
+{
+    clear_error();
+    const char* fn = "bs_gemm_compressed_b_fp8";
+    if (M < 0 || N < 0 || K < 0) return set_error(BS_ERR_INVALID, "%s: negative shape", fn);
+    if (a_layout != 0 && a_layout != 1) return set_error(BS_ERR_INVALID, "%s: bad a_layout", fn);
+    if (vals_dtype != DT_E4M3FN && vals_dtype != DT_E5M2)
+        return set_error(BS_ERR_INVALID, "%s: B must hold fp8 (e4m3fn or e5m2) values", fn);
+    if (!square && b_scale == nullptr) return set_error(BS_ERR_INVALID, "%s: square=0 needs the stored scale", fn);
+    if (a_scale == nullptr) return set_error(BS_ERR_INVALID, "%s: null a_scale", fn);
+    if (a_layout == 0 && lda < M) return set_error(BS_ERR_INVALID, "%s: lda < M", fn);
+    if (a_layout == 1 && lda < K) return set_error(BS_ERR_INVALID, "%s: lda < K", fn);
+    if ((uint64_t)K * (uint64_t)N >= kMaxElems) return set_error(BS_ERR_INVALID, "%s: K*N must be < 2^32", fn);
+    if (lda >= (1ll << 31)) return set_error(BS_ERR_INVALID, "%s: lda must be < 2^31", fn);
+    if (M == 0 || N == 0) return BS_OK;
+    if (C == nullptr) return set_error(BS_ERR_INVALID, "%s: null C", fn);
+    if (((uintptr_t)C) & 1) return set_error(BS_ERR_INVALID, "%s: C misaligned", fn);
+    const int64_t need = bs_gemm_compressed_b_fp8_workspace_bytes(M, N, K, a_layout);
+    if (workspace == nullptr || workspace_bytes < need)
+        return set_error(BS_ERR_INVALID, "%s: workspace too small (%lld < %lld)", fn, (long long)workspace_bytes,
+                         (long long)need);
+    if (((uintptr_t)workspace) & 255) return set_error(BS_ERR_INVALID, "%s: workspace must be 256-byte aligned", fn);
+    hipStream_t st = (hipStream_t)stream;
+    const uint32_t ksteps = (uint32_t)((K + kBK - 1) / kBK);
+    uint8_t* lut_area = (uint8_t*)workspace + need - kLutAreaBytes;
+    uint8_t* lut = lut_area;
+    float* sB = reinterpret_cast<float*>(lut_area + 256);
+    uint32_t* cmax = reinterpret_cast<uint32_t*>(lut_area + 260);
+    if (ksteps == 0) {
+        // an empty sum: C = 0 (a fill kernel, no memset node in a captured graph)
+        const int64_t n = M * N;
+        const uint32_t nblk = (uint32_t)std::min<int64_t>((n + 255) / 256, 2048);
+        hipLaunchKernelGGL(zero_fill_u16_8_kernel, dim3(nblk), dim3(256), 0, st, (uint16_t*)C, n);
+        hipError_t e = hipGetLastError();
+        return e == hipSuccess ? BS_OK : set_error(BS_ERR_HIP, "%s: %s", fn, hipGetErrorString(e));
+    }
+    if (A == nullptr || bitmask == nullptr || prefix == nullptr || (vals_numel > 0 && vals == nullptr))
+        return set_error(BS_ERR_INVALID, "%s: null pointer", fn);
+    if (((uintptr_t)vals) & 15) return set_error(BS_ERR_INVALID, "%s: vals must be 16-byte aligned", fn);
+    const Gemm8Plan plan = gemm8_plan(M, N, K);
+    const int split = plan.split;
+    const int64_t part_bytes = split > 1 ? up256((int64_t)split * M * N * 4) : 0;
+    const int64_t nkb = apk8_nkb(K), nrb = (M + 31) / 32;
+    // A fragment offsets (row block < 4 of a wave, k block, lane) are 32-bit
+    if (nkb >= (1ll << 18)) return set_error(BS_ERR_INVALID, "%s: K must be < 2^24", fn);
+    const int64_t grid_n = (N + kTile - 1) / kTile;
+    const int64_t T = (int64_t)ksteps * grid_n;
+
+    // B code table and scale
+    Lut8Args la{};
+    la.vals = (const uint8_t*)vals;
+    la.vals_numel = vals_numel;
+    la.prefix = prefix;
+    la.T = T;
+    la.vals_offset = vals_offset;
+    la.dense_numel = K * N;
+    la.relu2_scale = relu2_scale;
+    la.r_scale = b_scale;
+    la.cmax = cmax;
+    la.lut = lut;
+    la.b_scale = sB;
+    la.b_scale_out = b_scale_out;
+    if (square) {
+        hipLaunchKernelGGL(write_u32_kernel, dim3(1), dim3(64), 0, st, cmax, 0u);
+        hipLaunchKernelGGL(code_max_kernel, dim3(512), dim3(256), 0, st, la);
+        if (vals_dtype == DT_E4M3FN)
+            hipLaunchKernelGGL(relu2_lut_kernel<DT_E4M3FN>, dim3(1), dim3(256), 0, st, la);
+        else
+            hipLaunchKernelGGL(relu2_lut_kernel<DT_E5M2>, dim3(1), dim3(256), 0, st, la);
+    } else {
+        hipLaunchKernelGGL(copy_scale_kernel, dim3(1), dim3(64), 0, st, b_scale, sB, b_scale_out);
+    }
+
+    // A into MFMA-fragment order (workspace after the partial sums)
+    uint8_t* apk = (uint8_t*)workspace + part_bytes;
+    if (a_layout == 0) {
+        hipLaunchKernelGGL(pack_a8_t_kernel, dim3((uint32_t)nkb, (uint32_t)((M + 63) / 64)), dim3(256), 0, st,
+                           (const uint8_t*)A, K, M, lda, apk, (uint32_t)nkb);
+    } else {
+        const int64_t pieces = nrb * nkb * 128;
+        int64_t nblk = (pieces + 255) / 256;
+        if (nblk > 4096) nblk = 4096;
+        hipLaunchKernelGGL(pack_a8_n_kernel, dim3((uint32_t)nblk), dim3(256), 0, st, (const uint8_t*)A, K, M, lda,
+                           apk, (uint32_t)nkb, pieces);
+    }
+    Gemm8Args g{};
+    g.Apk = apk;
+    g.M = M;
+    g.K = K;
+    g.nkb = (uint32_t)nkb;
+    g.nrb = (uint32_t)nrb;
+    g.vals = (const uint8_t*)vals;
+    g.vals_numel = vals_numel;
+    g.bitmask = bitmask;
+    g.prefix = prefix;
+    g.vals_offset = vals_offset;
+    g.N = N;
+    g.grid_n = (uint32_t)grid_n;
+    const uint32_t nt = (uint32_t)(plan.bn / kTile);
+    g.tiles_n = (g.grid_n + nt - 1) / nt;
+    g.tiles_m = (uint32_t)((M + plan.bm - 1) / plan.bm);
+    g.lut = lut;
+    g.a_scale = a_scale;
+    g.b_scale = sB;
+    g.C = (uint16_t*)C;
+    g.part = split > 1 ? (float*)workspace : nullptr;
+    g.ksteps = ksteps;
+    g.ksteps_per_split = (ksteps + split - 1) / split;
+    if (g.ksteps_per_split > (uint32_t)kMaxSteps) return set_error(BS_ERR_INVALID, "%s: internal split error", fn);
+    const uint64_t blocks = (uint64_t)g.tiles_m * g.tiles_n * (uint64_t)split;
+    if (blocks >= (1ull << 31)) return set_error(BS_ERR_INVALID, "%s: grid too large", fn);
+#define BS_GEMM8_LAUNCH(LUTV, FMT)                                                                                \
+    do {                                                                                                          \
+        if (plan.big)                                                                                             \
+            hipLaunchKernelGGL((gemm_cb8_kernel<Cfg8_512, LUTV, FMT>), dim3((uint32_t)blocks),                    \
+                               dim3(Cfg8_512::THREADS), 0, st, g);                                                \
+        else                                                                                                      \
+            hipLaunchKernelGGL((gemm_cb8_kernel<Cfg8_256, LUTV, FMT>), dim3((uint32_t)blocks),                    \
+                               dim3(Cfg8_256::THREADS), 0, st, g);                                                \
+    } while (0)
+    if (square) BS_GEMM8_LAUNCH(true, 0);
+    else if (vals_dtype == DT_E4M3FN) BS_GEMM8_LAUNCH(false, 0);
+    else BS_GEMM8_LAUNCH(false, 1);
+#undef BS_GEMM8_LAUNCH
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess && split > 1) {
+        const int64_t n = M * N;
+        int64_t nblk = (n + 255) / 256;
+        if (nblk > 2048) nblk = 2048;
+        hipLaunchKernelGGL(splitk_reduce_scaled_kernel, dim3((uint32_t)nblk), dim3(256), 0, st,
+                           (const float*)workspace, split, n, a_scale, (const float*)sB, (uint16_t*)C);
+        e = hipGetLastError();
+    }
+    if (e != hipSuccess) return set_error(BS_ERR_HIP, "%s launch: %s", fn, hipGetErrorString(e));
+    return BS_OK;
+}

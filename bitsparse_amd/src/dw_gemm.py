@@ -30,6 +30,54 @@ def supports(A: Tensor, B_sparse, square: bool) -> bool:
     return square and vdt in (torch.float8_e4m3fn, torch.float8_e5m2)
 
 
+def supports_fp8(A: Tensor, B_sparse) -> bool:
+    """The fp8-operand kernel: e4m3fn A on the GPU (2-D, any strides) and B
+    stored as raw (not pack_sbit) e4m3fn / e5m2 values."""
+    if not A.is_cuda or A.dim() != 2 or A.dtype != torch.float8_e4m3fn or B_sparse.pack_sbit:
+        return False
+    if A.shape[1] != B_sparse.shape[0]:
+        return False
+    if B_sparse.vals.data_ptr() % 16 != 0:
+        return False
+    return B_sparse.vals.dtype in (torch.float8_e4m3fn, torch.float8_e5m2)
+
+
+def gemm_compressed_b_fp8(A: Tensor, A_scale: Tensor, B_sparse, square: bool,
+                          b_scale_out: Tensor | None = None) -> Tensor:
+    """bf16(A_scale * sB * (A @ Bq)) with A in e4m3fn and B compressed fp8:
+    square=False multiplies the stored codes with their scale (AspB);
+    square=True the to_fp8 re-quantization of the bf16 k*v^2 (times
+    bf16(scale^2)) that AspRelu2B unpacks, formed from the codes in the
+    kernel.  ``b_scale_out`` (fp32 0-d) receives sB."""
+    from .hip_operators import dtype_code
+    if not supports_fp8(A, B_sparse):
+        raise ValueError("gemm_compressed_b_fp8: unsupported operand combination")
+    if A_scale is None or not A_scale.is_cuda or A_scale.dtype != torch.float32:
+        raise TypeError("gemm_compressed_b_fp8: A_scale must be an fp32 GPU tensor")
+    K, N = B_sparse.shape
+    M = A.shape[0]
+    if A.stride(1) == 1 and A.stride(0) >= max(K, 1):
+        a_layout, a_src, lda = 1, A, A.stride(0)
+    elif A.stride(0) == 1 and A.stride(1) >= max(M, 1):
+        a_layout, a_src, lda = 0, A.t(), A.stride(1)      # At [K, M] is m-contiguous
+    else:
+        a_layout, a_src, lda = 1, A.contiguous(), K
+    stored_scale = B_sparse.scale
+    if not square and stored_scale is None:
+        raise ValueError("gemm_compressed_b_fp8: fp8 values without their scale")
+    L = _lib.load()
+    C = torch.empty((M, N), device=A.device, dtype=torch.bfloat16)
+    need = L.bs_gemm_compressed_b_fp8_workspace_bytes(M, N, K, a_layout)
+    ws = torch.empty(need, device=A.device, dtype=torch.uint8)
+    check(L.bs_gemm_compressed_b_fp8(
+        a_src.data_ptr(), A_scale.data_ptr(), M, K, lda, a_layout, B_sparse.vals.data_ptr(),
+        dtype_code(B_sparse.vals.dtype), B_sparse.vals.numel(), B_sparse.bitmask.data_ptr(),
+        B_sparse.prefix.data_ptr(), B_sparse.vals_offset.data_ptr(), N, int(square), float(RELU2_SCALE),
+        ptr(stored_scale), C.data_ptr(), ptr(b_scale_out), ws.data_ptr(), need, stream_handle(A.device)),
+        "bs_gemm_compressed_b_fp8")
+    return C
+
+
 def gemm_compressed_b(A: Tensor, B_sparse, square: bool) -> Tensor:
     from .hip_operators import dtype_code
     if not supports(A, B_sparse, square):

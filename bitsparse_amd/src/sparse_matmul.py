@@ -5,13 +5,18 @@ Public surface of reference lib_sparse/src/sparse_matmul.py: ``AspB``
 
 Design.  The compressed operand is consumed where it lies:
 
-* B compressed, bf16 A (the MLP backward's dW = dY^T h): the reconstruct-
-  into-LDS MFMA GEMM (``dw_gemm``) decodes each 64x64 tile of B into LDS
-  inside the GEMM, so no dense B exists in HBM at any point.  ``row_batch``,
-  which in the reference bounds the size of the dense B it decompresses, has
-  nothing to bound there and the product is computed in one launch (one fp32
-  accumulation over all of K instead of one bf16 rounding per batch).
-* Every other case (fp8 dY, packed values, a compressed left operand)
+* B compressed (the MLP backward's dW = dY^T h): the reconstruct-into-LDS
+  MFMA GEMM (``dw_gemm``) decodes each 64x64 tile of B into LDS inside the
+  GEMM, so no dense B exists in HBM at any point.  bf16 storage multiplies
+  in bf16; fp8 storage in fp8, as the reference does (A quantized by
+  ``to_fp8`` when it comes in bf16; for AspRelu2B the kernel forms the
+  ``to_fp8`` re-quantization of the bf16 k*v^2 from the stored codes).
+  ``row_batch``, which in the reference bounds the size of the dense B it
+  decompresses, has nothing to bound for bf16 and the product is computed in
+  one launch (one fp32 accumulation over all of K instead of one bf16
+  rounding per batch).
+* Every other case (packed values, fp8 row batches -- whose per-batch
+  re-quantization is part of their result --, a compressed left operand)
   decodes B to dense -- whole, or ``row_batch`` rows at a time through a
   tile-row view of the compressed tensor (``tile_rows``: bitmask and prefix
   slices over the same values, no copy) -- and multiplies with the library
@@ -67,7 +72,11 @@ def _row_blocks(sp: BitsparseTensor, row_batch: int):
 def _times_compressed(A: Tensor, B_sparse: BitsparseTensor, A_scale: Tensor | None, row_batch: int,
                       square: bool) -> Tensor:
     """A @ op(B) with op = identity or k * (.)^2, B compressed [K, N]."""
-    if USE_LDS_GEMM and dw_gemm.supports(A, B_sparse, square=square):
+    if USE_LDS_GEMM and B_sparse.fp8 and row_batch <= 0:
+        opa = as_fp8_operand(A, A_scale)
+        if dw_gemm.supports_fp8(opa.codes, B_sparse):
+            return dw_gemm.gemm_compressed_b_fp8(opa.codes, opa.scale, B_sparse, square)
+    if USE_LDS_GEMM and not B_sparse.fp8 and dw_gemm.supports(A, B_sparse, square=square):
         return dw_gemm.gemm_compressed_b(A, B_sparse, square=square)
     # fp8 values are multiplied in fp8: with their stored scale, or (square)
     # re-quantized from the bf16 square, as the reference does

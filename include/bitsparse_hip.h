@@ -290,6 +290,35 @@ int bs_gemm_compressed_b(const void* A, int64_t M, int64_t K, int64_t lda, int a
                          void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * fp8 operands: C[M, N] (bf16) = bf16(a_scale * sB * (A @ Bq)), A an e4m3fn
+ * [M, K] matrix with device fp32 scale a_scale (to_fp8 output), B a
+ * compressed [K, N] activation with fp8 values (vals_dtype 1 or 2, vals
+ * 16-byte aligned), decoded tile by tile into LDS:
+ *   square = 0: Bq = the stored codes, sB = *b_scale (their scale);
+ *   square = 1: Bq, sB = to_fp8(bs_decompress(B, square=1, b_scale)) -- the
+ *               bf16 dense k*v*v (times bf16(b_scale^2) when b_scale is not
+ *               null), re-quantized with the to_fp8 rule; computed on the
+ *               device from the stored codes (no dense operand is formed).
+ *               sB is also written to *b_scale_out when not null.
+ * A layouts as bs_gemm_compressed_b (a_layout 0: its transpose At [K, M],
+ * m contiguous, lda >= M; 1: row-major, lda >= K), any alignment, lda < 2^31.
+ * fp32 MFMA accumulation (v_mfma_scale_f32_32x32x64_f8f6f4, unit block
+ * scales), scaled once at the end; small grids split K into fp32 partial
+ * sums reduced in a fixed order.  `workspace` (256-byte aligned,
+ * bs_gemm_compressed_b_fp8_workspace_bytes) holds the partial sums, A in
+ * fragment order and the code table.
+ * Replaces, for fp8 storage, lib_sparse/src/sparse_matmul.py:24-28 (AspB)
+ * and :109-113 (AspRelu2B): unpack to a dense HBM buffer, re-quantize
+ * (fp8.py:123-129) and the scaled fp8 GEMM (fp8.py:25-49).
+ */
+int64_t bs_gemm_compressed_b_fp8_workspace_bytes(int64_t M, int64_t N, int64_t K, int a_layout);
+int bs_gemm_compressed_b_fp8(const void* A, const float* a_scale, int64_t M, int64_t K, int64_t lda,
+                             int a_layout, const void* vals, int vals_dtype, int64_t vals_numel,
+                             const uint8_t* bitmask, const uint32_t* prefix, const int64_t* vals_offset,
+                             int64_t N, int square, float relu2_scale, const float* b_scale, void* C,
+                             float* b_scale_out, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * Packed value stream (pack_sbit storage, reference lib_sparse/src/bitpacking.py).
  * Value i of a stream occupies stream bits [i*PB, (i+1)*PB), least significant
  * bit first (byte i*PB/8 holds the low bits); PB = 15 for bf16 and 7 for fp8
