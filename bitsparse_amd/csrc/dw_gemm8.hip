@@ -607,32 +607,48 @@ struct Lut8Args {
     int64_t dense_numel;          // K * N (cleared elements exist iff nnz < this)
     float relu2_scale;
     const float* r_scale;         // stored values' scale (may be null: bf16(scale^2) not applied)
-    uint32_t* cmax;               // reduction slot (zeroed by the caller's launch order)
+    uint32_t* cmax;               // per-block maxima of code_max_kernel (kCodeMaxBlocks)
     uint8_t* lut;                 // 256 bytes
     float* b_scale;               // sB
     float* b_scale_out;           // optional copy for the caller
 };
 
+constexpr int kCodeMaxBlocks = 256;
+
 // magnitude order of a stored code: its low 7 bits (e4m3fn / e5m2 codes of
-// equal sign sort like their values; NaN codes above every finite one)
+// equal sign sort like their values; NaN codes above every finite one).
+// Block b writes the largest magnitude of its 16-byte units of the run
+// [vo + prefix[0], vo + prefix[T]) to cmax[b] (every block writes, so the
+// slots need no clearing).
 __global__ __launch_bounds__(256) void code_max_kernel(Lut8Args a)
 {
     const int64_t vo = a.vals_offset ? *a.vals_offset : 0;
-    const int64_t b0 = vo + (int64_t)a.prefix[0];
+    int64_t b0 = vo + (int64_t)a.prefix[0];
     int64_t b1 = vo + (int64_t)a.prefix[a.T];
+    if (b0 < 0) b0 = 0;
     if (b1 > a.vals_numel) b1 = a.vals_numel;
     uint32_t m = 0;
-    const int64_t stride = (int64_t)gridDim.x * 256;
-    for (int64_t i = b0 + (int64_t)blockIdx.x * 256 + threadIdx.x; i < b1; i += stride)
-        m = max(m, (uint32_t)a.vals[i] & 0x7fu);
+    if (b1 > b0) {
+        const int64_t u0 = b0 >> 4, u1 = (b1 + 15) >> 4;
+        const bs_rsrc rs = make_rsrc(a.vals + u0 * 16, (uint32_t)std::min<int64_t>(a.vals_numel - u0 * 16, 0xffffffffll));
+        const int64_t stride = (int64_t)gridDim.x * 256;
+        for (int64_t u = u0 + (int64_t)blockIdx.x * 256 + threadIdx.x; u < u1; u += stride) {
+            const uint4 v = load16(rs, (uint32_t)((u - u0) * 16));
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+            const int64_t e0 = u * 16;
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const uint32_t c = (w[e >> 2] >> (8 * (e & 3))) & 0x7fu;
+                const bool in = e0 + e >= b0 && e0 + e < b1;
+                m = max(m, in ? c : 0u);
+            }
+        }
+    }
     m = wave_max_u32(m);
     __shared__ uint32_t s_w[4];
     if ((threadIdx.x & 63) == 0) s_w[threadIdx.x >> 6] = m;
     __syncthreads();
-    if (threadIdx.x == 0) {
-        m = max(max(s_w[0], s_w[1]), max(s_w[2], s_w[3]));
-        if (m != 0u) atomicMax(a.cmax, m | 0x100u);       // bit 8: some value is stored
-    }
+    if (threadIdx.x == 0) a.cmax[blockIdx.x] = max(max(s_w[0], s_w[1]), max(s_w[2], s_w[3]));
 }
 
 // D(c) of code c as bf16 bits: the ReLU^2 unpack of fp8 storage
@@ -662,17 +678,18 @@ __global__ __launch_bounds__(256) void relu2_lut_kernel(Lut8Args a)
     // as bf16(0 * bf16(s^2)) (0 without a scale); stored codes are positive
     const uint32_t zero_x = has_scale ? f32_to_bf16(0.0f * s2b) : 0u;
     const uint32_t x = c == 0 ? zero_x : relu2_dense_bits<V_T>(c, k, has_scale, s2b);
+    // the stored codes' largest magnitude, over code_max_kernel's blocks
+    __shared__ uint32_t s_cm[4];
+    const uint32_t cmw = wave_max_u32(c < (uint32_t)kCodeMaxBlocks ? a.cmax[c] : 0u);
+    if ((c & 63) == 0) s_cm[c >> 6] = cmw;
+    __syncthreads();
     if (c == 0) {
-        const uint32_t cm = *a.cmax;
+        const uint32_t cmax = max(max(s_cm[0], s_cm[1]), max(s_cm[2], s_cm[3]));
         const int64_t nnz = (int64_t)a.prefix[a.T] - (int64_t)a.prefix[0];
         // amax over |D| of the stored codes (the one of largest magnitude) and
         // of the cleared elements; NaN magnitudes sort above Inf
         uint32_t amag = 0;
-        if (cm & 0x100u) {
-            const uint32_t cmax = cm & 0x7fu;
-            const uint32_t dmax = relu2_dense_bits<V_T>(cmax, k, has_scale, s2b);
-            amag = dmax & 0x7fffu;
-        }
+        if (cmax != 0u) amag = relu2_dense_bits<V_T>(cmax, k, has_scale, s2b) & 0x7fffu;
         if (nnz < a.dense_numel) amag = max(amag, zero_x & 0x7fffu);
         const float amax = bf16_to_f32(amag);
         const float sc = amax / 448.0f;
@@ -682,11 +699,6 @@ __global__ __launch_bounds__(256) void relu2_lut_kernel(Lut8Args a)
     }
     __syncthreads();
     a.lut[c] = (uint8_t)f32_to_e4m3(bf16_to_f32(x) / s_scale);
-}
-
-__global__ void write_u32_kernel(uint32_t* p, uint32_t v)
-{
-    if (threadIdx.x == 0) *p = v;
 }
 
 __global__ void copy_scale_kernel(const float* src, float* dst, float* dst2)
@@ -755,7 +767,7 @@ static Gemm8Plan gemm8_plan(int64_t M, int64_t N, int64_t K)
 static int64_t apk8_nkb(int64_t K) { return (K + kBK - 1) / kBK; }
 static int64_t apk8_bytes(int64_t M, int64_t K) { return (M + 31) / 32 * apk8_nkb(K) * 2048; }
 static int64_t up256(int64_t x) { return (x + 255) / 256 * 256; }
-constexpr int64_t kLutAreaBytes = 512;     // lut[256], sB, code-max slot
+constexpr int64_t kLutAreaBytes = 512 + 4 * kCodeMaxBlocks;     // lut[256], sB, code_max_kernel's maxima at 512
 
 }  // namespace bs
 
@@ -802,7 +814,7 @@ extern "C" int bs_gemm_compressed_b_fp8(const void* A, const float* a_scale, int
     uint8_t* lut_area = (uint8_t*)workspace + need - kLutAreaBytes;
     uint8_t* lut = lut_area;
     float* sB = reinterpret_cast<float*>(lut_area + 256);
-    uint32_t* cmax = reinterpret_cast<uint32_t*>(lut_area + 260);
+    uint32_t* cmax = reinterpret_cast<uint32_t*>(lut_area + 512);
     if (ksteps == 0) {
         // an empty sum: C = 0 (a fill kernel, no memset node in a captured graph)
         const int64_t n = M * N;
@@ -838,8 +850,7 @@ extern "C" int bs_gemm_compressed_b_fp8(const void* A, const float* a_scale, int
     la.b_scale = sB;
     la.b_scale_out = b_scale_out;
     if (square) {
-        hipLaunchKernelGGL(write_u32_kernel, dim3(1), dim3(64), 0, st, cmax, 0u);
-        hipLaunchKernelGGL(code_max_kernel, dim3(512), dim3(256), 0, st, la);
+        hipLaunchKernelGGL(code_max_kernel, dim3(kCodeMaxBlocks), dim3(256), 0, st, la);
         if (vals_dtype == DT_E4M3FN)
             hipLaunchKernelGGL(relu2_lut_kernel<DT_E4M3FN>, dim3(1), dim3(256), 0, st, la);
         else

@@ -85,6 +85,42 @@ def test_stored_codes_bit_exact_with_identity(dev, KN, storage):
     assert torch.equal(C.view(torch.int16), want.view(torch.int16))
 
 
+def _trimmed(sp, lead):
+    """sp with its values alone in a buffer of exactly lead + nnz bytes, at
+    vals_offset = lead: the last run ends at the buffer's end."""
+    from bitsparse_amd.bitsparse import BitsparseTensor
+    p = sp.prefix.cpu().to(torch.int64)
+    vo = int(sp.vals_offset.item())
+    nnz = int(p[-1] - p[0])
+    buf = torch.zeros(lead + nnz, dtype=torch.uint8, device=sp.vals.device)
+    buf[lead:] = sp.vals.view(torch.uint8)[vo + int(p[0]):vo + int(p[0]) + nnz]
+    prefix = (p - p[0]).to(torch.int32).view(torch.uint32).to(sp.prefix.device)
+    return BitsparseTensor(buf.view(sp.vals.dtype), sp.bitmask, prefix, sp.shape, sp.dtype, sp.grid_m, sp.grid_n,
+                           sp.BLOCK_M, sp.BLOCK_N, scale=sp.scale,
+                           vals_offset=torch.full((), lead, dtype=torch.int64, device=sp.vals.device))
+
+
+@pytest.mark.parametrize("lead", [0, 5, 16])
+@pytest.mark.parametrize("square", [True, False])
+def test_vals_ending_inside_a_run_unit(dev, lead, square):
+    """Values in a buffer that ends mid 16-byte unit (and starts off a unit
+    boundary when lead % 16 != 0): the unit crossing the end must carry the
+    last bytes, as from the full-size buffer."""
+    from bitsparse_amd.src import dw_gemm
+    K, N = 512, 320
+    for seed in range(20, 40):
+        sp = _compressed_e4m3(K, N, -0.8, seed, dev)
+        p = sp.prefix.cpu().to(torch.int64)
+        if (lead + int(p[-1] - p[0])) % 16:
+            break
+    spt = _trimmed(sp, lead)
+    assert spt.vals.numel() % 16 != 0
+    A, sa = _identity_fp8(K, dev)
+    want = dw_gemm.gemm_compressed_b_fp8(A, sa, sp, square=square)
+    got = dw_gemm.gemm_compressed_b_fp8(A, sa, spt, square=square)
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
 @pytest.mark.parametrize("M,K,N", [(256, 256, 256), (512, 1024, 384), (192, 640, 200), (64, 4096, 64),
                                    (1000, 512, 700)])
 @pytest.mark.parametrize("square", [True, False])
