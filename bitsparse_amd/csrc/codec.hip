@@ -10,6 +10,7 @@
 // contiguous bytes of bf16.
 #include "bs_device.h"
 #include "bs_host.h"
+#include "compact.h"
 
 #include <algorithm>
 #include <cstdlib>
@@ -18,10 +19,6 @@
 
 
 namespace bs {
-
-template <int B> struct Raw;
-template <> struct Raw<2> { using T = uint4; };   // 8 x bf16
-template <> struct Raw<1> { using T = uint2; };   // 8 x fp8
 
 constexpr int kThreads = 256;
 
@@ -156,13 +153,6 @@ struct CompressArgs {
     uint32_t* fallbacks;
     uint64_t patience;          // look-back wait (s_memrealtime ticks) before counting a unit itself
 };
-
-// status word: [63:34] epoch, [33:32] flag (1 aggregate, 2 inclusive), [31:0] value
-constexpr uint64_t kFlagAgg = 1, kFlagInc = 2;
-__device__ __forceinline__ uint64_t pack_status(uint32_t epoch, uint64_t flag, uint32_t v)
-{
-    return ((uint64_t)epoch << 34) | (flag << 32) | v;
-}
 
 // 200 us at the 100 MHz s_memrealtime clock: waiting longer than this for a
 // predecessor makes the waiter count that predecessor's tiles itself (a
@@ -428,71 +418,6 @@ __device__ __forceinline__ void opaque(uint4& v)
     asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w));
 }
 __device__ __forceinline__ void opaque(uint2& v) { asm volatile("" : "+v"(v.x), "+v"(v.y)); }
-
-// Compaction selectors of mask byte m: the set elements move to the front.
-// bf16 (OUTB 2): output dword j = perm(D1, D0, s[j]) | perm(D3, D2, s[4 + j]);
-// fp8 (OUTB 1): output dword j = perm(D1, D0, s[j]), j < 2.
-template <int OUTB>
-__device__ __forceinline__ void compaction_selectors(uint32_t m, uint32_t* s)
-{
-    constexpr int NS = OUTB == 2 ? 8 : 2;
-#pragma unroll
-    for (int i = 0; i < NS; i++) s[i] = 0x0c0c0c0cu;   // 0x0c selects a zero byte
-    uint32_t q = 0;
-#pragma unroll
-    for (int e = 0; e < 8; e++) {
-        if ((m >> e) & 1u) {
-            if constexpr (OUTB == 2) {
-                const uint32_t ee = (uint32_t)(e & 3);
-                const uint32_t pair = (2u * ee) | ((2u * ee + 1u) << 8);
-                const uint32_t sh = (q & 1u) * 16u;
-#pragma unroll
-                for (int j = 0; j < 4; j++)
-                    if ((uint32_t)j == (q >> 1)) {
-                        uint32_t& w = s[(e < 4 ? 0 : 4) + j];
-                        w = (w & ~(0xffffu << sh)) | (pair << sh);
-                    }
-            } else {
-                const uint32_t sh = (q & 3u) * 8u;
-#pragma unroll
-                for (int j = 0; j < 2; j++)
-                    if ((uint32_t)j == (q >> 2)) s[j] = (s[j] & ~(0xffu << sh)) | ((uint32_t)e << sh);
-            }
-            q++;
-        }
-    }
-}
-
-// Write the 8 elements of a compacted chunk at consecutive positions from p,
-// last element first (see the kernel comment for why the order matters).
-template <int OUTB>
-__device__ __forceinline__ void write_compacted(uint8_t* p, const typename Raw<OUTB>::T& c)
-{
-    if constexpr (OUTB == 2) {
-        const uint32_t w[4] = {c.x, c.y, c.z, c.w};
-#pragma unroll
-        for (int i = 7; i >= 0; i--) {
-            *reinterpret_cast<uint16_t*>(p + 2 * i) = (uint16_t)(w[i >> 1] >> (16 * (i & 1)));
-            asm volatile("" ::: "memory");
-        }
-    } else {
-        const uint32_t w[2] = {c.x, c.y};
-#pragma unroll
-        for (int i = 7; i >= 0; i--) {
-            p[i] = (uint8_t)(w[i >> 2] >> (8 * (i & 3)));
-            asm volatile("" ::: "memory");
-        }
-    }
-}
-
-template <int OUTB>
-__device__ __forceinline__ void ring_elem_store(uint8_t* vals, int64_t gi, const uint8_t* ring, int idx)
-{
-    if constexpr (OUTB == 2)
-        reinterpret_cast<uint16_t*>(vals)[gi] = reinterpret_cast<const uint16_t*>(ring)[idx];
-    else
-        vals[gi] = ring[idx];
-}
 
 // PACKED (MODE_FUSED only): the values go to a 15/7-bit stream (pack_sbit
 // storage) instead of raw elements: a.vals is the stream (4-byte aligned) and

@@ -1,0 +1,465 @@
+// Up-projection GEMM with the ReLU and the compress in its epilogue (gfx950):
+//     z = bf16(bf16(x @ W^T) + b),  h = relu(z)
+//     h -> 64x64-tile bitmask + prefix + values (the BitsparseTensor format)
+// in one kernel, so the activation is never read back from HBM to be
+// compressed.  Replaces the reference's z = x @ W1^T; z = z + b1;
+// h = z.relu_(); dense_to_tilesparse(h) (lib_sparse/layers.py:86-89, :29, :37;
+// lib_sparse/src/functions.py:55-99).  The two bf16 roundings (the GEMM's
+// output, then the bias add) are the reference's; the fp32 accumulation order
+// is this kernel's own.
+//
+// GEMM: a workgroup is 4 waves (2 x 2, one per SIMD) on a 256 x 192 tile of
+// z; each wave holds 128 x 96 in 4 x 3 v_mfma_f32_32x32x16_bf16 accumulators
+// (192 AGPRs).  x [M, K] and W [N, K] are both k-contiguous, so a K-step (64)
+// stages a 256 x 64 slab of x and a 192 x 64 slab of W in LDS as 16-byte
+// chunks, eight per row.  The chunk index is XOR-swizzled with (row / 2) % 8:
+// 16 lanes storing two rows, or reading one chunk of 16 rows, then touch all
+// 64 banks once.  Slabs are double-buffered (one barrier per step); the next
+// step's slabs are loaded into registers while the current step's MFMAs run.
+//
+// Epilogue: the tile (bias, roundings, torch's GPU relu) is staged in LDS as
+// bf16; elements outside the matrix are staged as 0.  Wave w then owns tile
+// row w of the workgroup: three format tiles, one look-back "unit".  Units
+// are consecutive in tile order (unit (tm, cb) = tiles tm * grid_n + 3 cb ..
+// +2), so the decoupled look-back of the codec applies unchanged.  The wave
+//   * writes its 64 rows of h (16-byte stores) and the tiles' bitmask bytes,
+//   * publishes the unit's count, resolves its offset from the preceding
+//     units' status words and writes the tiles' prefix entries,
+//   * compacts each tile's set elements into a per-wave LDS run (v_perm
+//     selectors per mask byte) and stores the run with 16-byte stores, with
+//     element stores at its two partial ends.
+//
+// Look-back order: unit (tm, cb) waits for every unit before it in tile
+// order, among them (tm - 1, NB - 1), the last workgroup of the same
+// 256-row strip when tm is not the strip's first tile row: a workgroup
+// dispatched after it.  Every workgroup publishes its counts before it waits
+// for anything, so a strip completes once all of its NB workgroups have been
+// resident; the host caps NB at kUpMaxNB, half the workgroups the GPU holds
+// at once (one per CU).
+#include <algorithm>
+
+#include "bs_device.h"
+#include "bs_host.h"
+#include "compact.h"
+#include "gemm_common.h"
+
+namespace bs {
+
+typedef __bf16 up_bf16x8_t __attribute__((ext_vector_type(8)));
+
+constexpr int kUpBM = 256, kUpBN = 192;
+constexpr int kUpIM = 4, kUpJN = 3;                     // 32x32 accumulator blocks per wave
+constexpr int kUpTiles = kUpBN / kTile;                 // format tiles per unit
+constexpr int kUpAStage = kUpBM * 128;                  // x slab: 256 rows x 64 k bf16
+constexpr int kUpBStage = kUpBN * 128;                  // W slab: 192 rows x 64 k bf16
+constexpr int kUpMainLds = 2 * (kUpAStage + kUpBStage);
+constexpr int kUpHP = kUpBN * 2 + 16;                   // staged h row pitch, bytes
+constexpr int kUpRunElems = kTileNumel + 16;            // per-wave compaction run (+ phase, + tail)
+constexpr int kUpOffRun = kUpBM * kUpHP;
+constexpr int kUpOffSel = kUpOffRun + 4 * kUpRunElems * 2;
+constexpr int kUpLds = kUpOffSel + 256 * 32;            // + compaction selectors (8 dwords per mask byte)
+static_assert(kUpMainLds <= kUpOffSel, "the selectors are written before the main loop");
+static_assert(kUpLds <= 160 * 1024, "LDS budget");
+constexpr int64_t kUpMaxNB = 128;
+
+struct UpArgs {
+    const uint16_t* x;            // [M, K], row stride ldx
+    const uint16_t* w;            // [N, K], row stride ldw
+    const uint16_t* bias;         // [N] or null
+    uint16_t* h;                  // [M, N], row stride ldh, or null
+    int64_t ldx, ldw, ldh;
+    int64_t M, N, K;
+    uint32_t grid_n, grid_m;      // format tiles
+    uint32_t nb;                  // workgroups (units) per tile row
+    uint32_t T;
+    uint8_t* bitmask;
+    uint32_t* prefix;
+    uint16_t* vals;
+    int64_t vals_capacity;        // elements
+    const int64_t* offset_in;
+    int32_t align8;
+    int64_t* offset_out;
+    int64_t* start_out;
+    int32_t* err;
+    uint64_t* status;             // one word per unit
+    uint32_t epoch;
+};
+
+// torch's GPU relu on bf16 bits: x <= 0 (either zero included) -> +0, NaN
+// and positive values keep their bits
+__device__ __forceinline__ uint32_t relu_bf16_bits(uint32_t b) { return (b - 0x8000u) < 0x7f81u ? 0u : b; }
+
+// A look-back wait longer than this (s_memrealtime ticks, 100 MHz: 20 ms)
+// ends the wait with bit 2 of *err set: every predecessor publishes without
+// waiting for anything, so this bound is never reached by a correct launch;
+// it only guarantees that every wave ends.
+constexpr uint64_t kUpLookbackGiveUpTicks = 2000000;
+
+// Exclusive prefix of unit u from the status words of units 0 .. u-1: 64
+// words per read (lane j: unit pos - j), summing aggregates back to the
+// nearest inclusive prefix; re-read while a needed word is unpublished.
+__device__ uint32_t up_lookback(const UpArgs& a, uint32_t u, int lane)
+{
+    uint32_t excl = 0;
+    int64_t pos = (int64_t)u - 1;
+    const uint64_t t0 = wall_clock64();
+    while (pos >= 0) {
+        const int64_t q = pos - lane;
+        const uint64_t s = q >= 0 ? ld_relaxed(&a.status[q]) : pack_status(a.epoch, kFlagInc, 0u);
+        const uint32_t flag = (uint32_t)(s >> 34) == a.epoch ? (uint32_t)(s >> 32) & 3u : 0u;
+        const uint64_t inc = __ballot(flag == kFlagInc);
+        const uint64_t unpub = __ballot(flag == 0u);
+        const int first = inc ? __ffsll((unsigned long long)inc) - 1 : 63;   // last lane needed
+        const uint64_t need = first == 63 ? ~0ull : ((2ull << first) - 1ull);
+        if (unpub & need) {
+            if (wall_clock64() - t0 > kUpLookbackGiveUpTicks) {
+                if (lane == 0 && a.err) atomicOr(a.err, 4);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+            continue;
+        }
+        excl += wave_sum_u32(lane <= first ? (uint32_t)s : 0u);
+        if (inc) break;
+        pos -= 64;
+    }
+    return excl;
+}
+
+__global__ __launch_bounds__(256, 1) void up_relu_compress_kernel(UpArgs a)
+{
+    __shared__ __align__(16) uint8_t lds[kUpLds];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave & 1, wn = wave >> 1;
+    const uint32_t strip = blockIdx.x / a.nb, cb = blockIdx.x % a.nb;
+    const int64_t m0 = (int64_t)strip * kUpBM, n0 = (int64_t)cb * kUpBN;
+
+    uint32_t* sel_s = reinterpret_cast<uint32_t*>(lds + kUpOffSel);
+    {
+        uint32_t sel[8];
+        compaction_selectors<2>((uint32_t)tid, sel);
+        *reinterpret_cast<uint4*>(&sel_s[tid * 8]) = uint4{sel[0], sel[1], sel[2], sel[3]};
+        *reinterpret_cast<uint4*>(&sel_s[tid * 8 + 4]) = uint4{sel[4], sel[5], sel[6], sel[7]};
+    }
+
+    // ---- slab loads: thread t moves chunk t % 8 of rows t / 8 + 32 i; rows
+    // past the matrix read zero through the resources, chunks past K are
+    // zeroed when stored (K % 8 == 0: a chunk is wholly inside or outside)
+    const int64_t rows_a = std::min<int64_t>(kUpBM, a.M - m0);
+    const int64_t rows_b = std::min<int64_t>(kUpBN, a.N - n0);
+    const bs_rsrc rsx = make_rsrc(a.x + m0 * a.ldx, (uint32_t)(((rows_a - 1) * a.ldx + a.K) * 2));
+    const bs_rsrc rsw = make_rsrc(a.w + n0 * a.ldw, (uint32_t)(((rows_b - 1) * a.ldw + a.K) * 2));
+    const int c8 = tid & 7, r8 = tid >> 3;
+    const uint32_t swz = (uint32_t)((r8 >> 1) & 7);        // rows r8 + 32 i share it
+    const uint32_t xrow = (uint32_t)(r8 * a.ldx * 2), xstep = (uint32_t)(32 * a.ldx * 2);
+    const uint32_t wrow = (uint32_t)(r8 * a.ldw * 2), wstep = (uint32_t)(32 * a.ldw * 2);
+    uint4 ga[kUpBM / 32], gb[kUpBN / 32];
+    auto gload = [&](int s) __attribute__((always_inline)) {
+        const uint32_t koff = (uint32_t)(s * 64 + 8 * c8) * 2u;
+#pragma unroll
+        for (int i = 0; i < kUpBM / 32; i++) ga[i] = load16(rsx, xrow + (uint32_t)i * xstep + koff);
+#pragma unroll
+        for (int i = 0; i < kUpBN / 32; i++) gb[i] = load16(rsw, wrow + (uint32_t)i * wstep + koff);
+    };
+    auto lstore = [&](int s, int buf) __attribute__((always_inline)) {
+        // a mask, not a select of two values: a select of an array element
+        // becomes a load through a selected pointer, which puts the array in
+        // scratch memory
+        const uint32_t km = (int64_t)s * 64 + 8 * c8 < a.K ? 0xffffffffu : 0u;
+        uint8_t* As = lds + buf * kUpAStage;
+        uint8_t* Bs = lds + 2 * kUpAStage + buf * kUpBStage;
+        const uint32_t coff = ((uint32_t)c8 ^ swz) << 4;
+#pragma unroll
+        for (int i = 0; i < kUpBM / 32; i++)
+            *reinterpret_cast<uint4*>(As + (r8 + 32 * i) * 128 + coff) =
+                uint4{ga[i].x & km, ga[i].y & km, ga[i].z & km, ga[i].w & km};
+#pragma unroll
+        for (int i = 0; i < kUpBN / 32; i++)
+            *reinterpret_cast<uint4*>(Bs + (r8 + 32 * i) * 128 + coff) =
+                uint4{gb[i].x & km, gb[i].y & km, gb[i].z & km, gb[i].w & km};
+    };
+
+    // ---- fragments of k-slice ks (16 k): lane l reads row 32 i + l % 32,
+    // chunk 2 ks + l / 32 of its wave's rows
+    const int fl = lane & 31;
+    const uint32_t fswz = (uint32_t)((fl >> 1) & 7);
+    const int arow = wm * 128 + fl, brow = wn * 96 + fl;
+    up_bf16x8_t fa[2][kUpIM], fb[2][kUpJN];
+    auto fread = [&](int buf, int ks, auto SET) __attribute__((always_inline)) {
+        constexpr int S = decltype(SET)::value;
+        const uint8_t* As = lds + buf * kUpAStage;
+        const uint8_t* Bs = lds + 2 * kUpAStage + buf * kUpBStage;
+        const uint32_t coff = (((uint32_t)(2 * ks + (lane >> 5))) ^ fswz) << 4;
+#pragma unroll
+        for (int i = 0; i < kUpIM; i++)
+            fa[S][i] = __builtin_bit_cast(up_bf16x8_t, *reinterpret_cast<const uint4*>(As + (arow + 32 * i) * 128 + coff));
+#pragma unroll
+        for (int j = 0; j < kUpJN; j++)
+            fb[S][j] = __builtin_bit_cast(up_bf16x8_t, *reinterpret_cast<const uint4*>(Bs + (brow + 32 * j) * 128 + coff));
+    };
+
+    f32x16_t acc[kUpIM][kUpJN];
+#pragma unroll
+    for (int i = 0; i < kUpIM; i++)
+#pragma unroll
+        for (int j = 0; j < kUpJN; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+
+    // Step s: slab s in buffer s & 1; its k-slice ks fragments in set ks & 1,
+    // the next slice's read during the current slice's MFMAs; slab s + 1 is
+    // loaded into registers at the top and stored into the other buffer at
+    // the bottom, before the barrier.
+    const int nsteps = (int)((a.K + 63) / 64);
+    if (nsteps > 0) {
+        gload(0);
+        lstore(0, 0);
+    }
+    __syncthreads();
+    if (nsteps > 0) fread(0, 0, IC<0>{});
+    for (int s = 0; s < nsteps; s++) {
+        const int buf = s & 1;
+        if (s + 1 < nsteps) gload(s + 1);
+        static_for<4>([&](auto KS) __attribute__((always_inline)) {
+            constexpr int ks = decltype(KS)::value, cur = ks & 1;
+            // issue order fixed by the sched barriers: the next slice's reads,
+            // then this slice's twelve MFMAs, which hide their latency
+            if constexpr (ks < 3) fread(buf, ks + 1, IC<cur ^ 1>{});
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < kUpIM; i++)
+#pragma unroll
+                for (int j = 0; j < kUpJN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cur][i], fb[cur][j], acc[i][j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        });
+        if (s + 1 < nsteps) lstore(s + 1, buf ^ 1);
+        __syncthreads();
+        if (s + 1 < nsteps) fread(buf ^ 1, 0, IC<0>{});
+    }
+
+    // ---- stage h = relu(bf16(bf16(acc) + b)) as bf16 (0 outside the matrix).
+    // Accumulator element r of lane l of a 32x32 block is row 8 (r / 4) +
+    // 4 (l / 32) + r % 4, column l % 32.
+    uint8_t* hs = lds;
+    {
+        const int rq = 4 * (lane >> 5);
+#pragma unroll
+        for (int j = 0; j < kUpJN; j++) {
+            const int col = wn * 96 + 32 * j + fl;
+            const bool cin = n0 + col < a.N;
+            const float bj = (a.bias != nullptr && cin) ? bf16_to_f32(a.bias[n0 + col]) : 0.0f;
+#pragma unroll
+            for (int i = 0; i < kUpIM; i++) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int row = wm * 128 + 32 * i + 8 * (r >> 2) + rq + (r & 3);
+                    uint32_t hb = f32_to_bf16(acc[i][j][r]);
+                    if (a.bias != nullptr) hb = f32_to_bf16(bf16_to_f32(hb) + bj);
+                    hb = relu_bf16_bits(hb);
+                    if (!cin || m0 + row >= a.M) hb = 0u;
+                    *reinterpret_cast<uint16_t*>(hs + row * kUpHP + col * 2) = (uint16_t)hb;
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- wave w: tile row w of the workgroup (rows 64 w .. +63 of hs)
+    const uint32_t tm = strip * 4u + (uint32_t)wave;
+    if (tm >= a.grid_m) return;                         // past the matrix: no unit
+    const uint8_t* hw = hs + wave * 64 * kUpHP;
+    const int64_t grow0 = m0 + (int64_t)wave * 64;
+
+    // dense h: 64 rows x 24 chunks, 16-byte stores (N % 8 == 0, ldh % 8 == 0)
+    if (a.h != nullptr) {
+#pragma unroll 4
+        for (int q = lane; q < 64 * (kUpBN / 8); q += 64) {
+            const int row = q / (kUpBN / 8), cc = q % (kUpBN / 8);
+            const int64_t grow = grow0 + row, gcol = n0 + cc * 8;
+            if (grow < a.M && gcol < a.N)
+                *reinterpret_cast<uint4*>(a.h + grow * a.ldh + gcol) =
+                    *reinterpret_cast<const uint4*>(hw + row * kUpHP + cc * 16);
+        }
+    }
+
+    // bitmask bytes and counts: tile tt, round k: lane l takes chunk 64 k + l
+    // (tile row 8 k + l / 8, columns 8 (l % 8) .. +7) -- the format's byte order
+    const uint32_t t0 = tm * a.grid_n + cb * (uint32_t)kUpTiles;
+    const int ntiles = (int)std::min<uint32_t>((uint32_t)kUpTiles, a.grid_n - cb * (uint32_t)kUpTiles);
+    const int lrow = lane >> 3, lcol = (lane & 7) * 16;   // byte offset of the lane's chunk in a tile row
+    uint32_t mk[kUpTiles][2];                           // the 8 mask bytes of each tile, 4 per register
+    uint32_t P[kUpTiles][9];                            // round offsets inside each tile's run
+    uint32_t tcnt[kUpTiles], toff[kUpTiles + 1];
+    toff[0] = 0;
+#pragma unroll
+    for (int tt = 0; tt < kUpTiles; tt++) {
+        mk[tt][0] = mk[tt][1] = 0u;
+        P[tt][0] = 0u;
+        const bool tin = tt < ntiles;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            uint32_t m = 0u;
+            if (tin) {
+                const uint4 v = *reinterpret_cast<const uint4*>(hw + (8 * k + lrow) * kUpHP + tt * 128 + lcol);
+                m = mask_bf16x8(v);
+                a.bitmask[(size_t)(t0 + tt) * kTileBytes + 64 * k + lane] = (uint8_t)m;
+            }
+            mk[tt][k >> 2] |= m << (8 * (k & 3));
+            P[tt][k + 1] = P[tt][k] + wave_sum_count(__popc(m));
+        }
+        tcnt[tt] = P[tt][8];
+        toff[tt + 1] = toff[tt] + tcnt[tt];
+    }
+    const uint32_t unit_total = toff[kUpTiles];
+    const uint32_t u = tm * a.nb + cb;
+    if (lane == 0) st_relaxed(&a.status[u], pack_status(a.epoch, u == 0 ? kFlagInc : kFlagAgg, unit_total));
+
+    int64_t start = a.offset_in ? *a.offset_in : 0;
+    if (a.align8) start = (start + 7) & ~(int64_t)7;
+
+    uint32_t excl = 0;
+    if (u != 0) {
+        excl = up_lookback(a, u, lane);
+        if (lane == 0) st_relaxed(&a.status[u], pack_status(a.epoch, kFlagInc, excl + unit_total));
+    }
+#pragma unroll
+    for (int tt = 0; tt < kUpTiles; tt++)
+        if (lane == tt && tt < ntiles) a.prefix[t0 + tt] = excl + toff[tt];
+    const uint32_t nunits = a.grid_m * a.nb;
+    if (lane == 0 && u == nunits - 1) {
+        a.prefix[a.T] = excl + unit_total;
+        const int64_t end = start + (int64_t)(excl + unit_total);
+        if (a.offset_out) *a.offset_out = end;
+        if (a.start_out) *a.start_out = start;
+        if (a.err && end > a.vals_capacity) atomicOr(a.err, 1);
+        if (a.err && start < 0) atomicOr(a.err, 2);
+    }
+    if (start < 0) return;
+
+    // ---- values, tile by tile: compact into the wave's run (phase a0 = the
+    // run's start modulo 8 elements, so run slot j is the 16-byte vals slot
+    // holding elements g - a0 + 8 j .. +7), then store the slots
+    uint16_t* run = reinterpret_cast<uint16_t*>(lds + kUpOffRun) + wave * kUpRunElems;
+#pragma unroll
+    for (int tt = 0; tt < kUpTiles; tt++) {
+        if (tt >= ntiles) break;
+        const int64_t g = start + (int64_t)excl + (int64_t)toff[tt];
+        const int cnt = (int)tcnt[tt];
+        const int a0 = (int)(g & 7);
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const uint32_t m = (mk[tt][k >> 2] >> (8 * (k & 3))) & 0xffu;
+            const uint32_t c = (uint32_t)__popc(m);
+            const uint32_t ex = wave_incl_scan(c) - c;
+            if (c != 0u) {
+                const uint4 w = *reinterpret_cast<const uint4*>(hw + (8 * k + lrow) * kUpHP + tt * 128 + lcol);
+                const uint4 s0 = *reinterpret_cast<const uint4*>(&sel_s[m * 8]);
+                const uint4 s1 = *reinterpret_cast<const uint4*>(&sel_s[m * 8 + 4]);
+                uint4 o;
+                o.x = __builtin_amdgcn_perm(w.y, w.x, s0.x) | __builtin_amdgcn_perm(w.w, w.z, s1.x);
+                o.y = __builtin_amdgcn_perm(w.y, w.x, s0.y) | __builtin_amdgcn_perm(w.w, w.z, s1.y);
+                o.z = __builtin_amdgcn_perm(w.y, w.x, s0.z) | __builtin_amdgcn_perm(w.w, w.z, s1.z);
+                o.w = __builtin_amdgcn_perm(w.y, w.x, s0.w) | __builtin_amdgcn_perm(w.w, w.z, s1.w);
+                write_compacted<2>(reinterpret_cast<uint8_t*>(run + a0 + (int)P[tt][k] + (int)ex), o);
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // elements past the capacity are not written (flagged above)
+        const int64_t room = a.vals_capacity - g;
+        const int endr = (int)std::max<int64_t>(0, std::min<int64_t>((int64_t)cnt, room));
+        const int nslots = (a0 + endr + 7) >> 3;
+        uint16_t* const base = a.vals + (g - a0);          // 16-byte aligned
+        for (int j = lane; j < nslots; j += 64) {
+            const int lo = std::max(8 * j, a0), hi = std::min(8 * j + 8, a0 + endr);
+            if (lo == 8 * j && hi == 8 * j + 8) {
+                *reinterpret_cast<uint4*>(base + 8 * j) = *reinterpret_cast<const uint4*>(run + 8 * j);
+            } else {
+                for (int e = lo; e < hi; e++) base[e] = run[e];
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+}
+
+}  // namespace bs
+
+using namespace bs;
+
+extern "C" int bs_linear_relu_compress(const void* x, int64_t M, int64_t K, int64_t ldx, const void* w, int64_t N,
+                                       int64_t ldw, const void* bias, void* h_out, int64_t ldh, uint8_t* bitmask,
+                                       uint32_t* prefix, void* vals, int64_t vals_capacity,
+                                       const int64_t* vals_offset_in, int align8, int64_t* vals_offset_out,
+                                       int64_t* vals_start_out, int32_t* err_flags, void* workspace,
+                                       int64_t workspace_bytes, uint32_t epoch, void* stream)
+{
+    clear_error();
+    const char* fn = "bs_linear_relu_compress";
+    if (M <= 0 || N <= 0 || K < 0) return set_error(BS_ERR_INVALID, "%s: needs M, N > 0 and K >= 0", fn);
+    if (K % 8 || N % 8) return set_error(BS_ERR_INVALID, "%s: K and N must be multiples of 8", fn);
+    if ((uint64_t)M * (uint64_t)N >= kMaxElems) return set_error(BS_ERR_INVALID, "%s: M*N must be < 2^32", fn);
+    if (x == nullptr || w == nullptr || bitmask == nullptr || prefix == nullptr)
+        return set_error(BS_ERR_INVALID, "%s: null pointer", fn);
+    if (ldx < K || ldw < K || ldx % 8 || ldw % 8)
+        return set_error(BS_ERR_INVALID, "%s: row strides must be >= K and multiples of 8", fn);
+    // 32-bit buffer offsets: a slab's rows stay below 2^31 bytes from its base
+    if ((int64_t)kUpBM * std::max(ldx, ldw) * 2 >= (1ll << 31))
+        return set_error(BS_ERR_INVALID, "%s: row stride too large", fn);
+    if ((((uintptr_t)x) & 15) || (((uintptr_t)w) & 15))
+        return set_error(BS_ERR_INVALID, "%s: x and W must be 16-byte aligned", fn);
+    if (bias != nullptr && (((uintptr_t)bias) & 1)) return set_error(BS_ERR_INVALID, "%s: bias misaligned", fn);
+    if (h_out != nullptr && ((((uintptr_t)h_out) & 15) || ldh < N || ldh % 8))
+        return set_error(BS_ERR_INVALID, "%s: h must be 16-byte aligned with a row stride >= N, a multiple of 8",
+                         fn);
+    if (vals_capacity < 0) return set_error(BS_ERR_INVALID, "%s: negative capacity", fn);
+    if (vals_capacity > 0 && vals == nullptr) return set_error(BS_ERR_INVALID, "%s: null vals", fn);
+    if (((uintptr_t)vals) & 15) return set_error(BS_ERR_INVALID, "%s: vals must be 16-byte aligned", fn);
+    if (vals_offset_out != nullptr && vals_offset_out == vals_offset_in)
+        return set_error(BS_ERR_INVALID, "%s: vals_offset_out aliases vals_offset_in", fn);
+    if (epoch == 0 || epoch >= (1u << 30)) return set_error(BS_ERR_INVALID, "%s: epoch must be in [1, 2^30)", fn);
+    const int64_t nb = (N + kUpBN - 1) / kUpBN;
+    if (nb > kUpMaxNB)
+        return set_error(BS_ERR_INVALID, "%s: N must be at most %lld", fn, (long long)(kUpMaxNB * kUpBN));
+    if (int rc = refuse_capture((hipStream_t)stream, fn)) return rc;
+    if (workspace == nullptr || workspace_bytes < bs_compress_workspace_bytes(M, N))
+        return set_error(BS_ERR_INVALID, "%s: workspace too small (%lld < %lld bytes)", fn, (long long)workspace_bytes,
+                         (long long)bs_compress_workspace_bytes(M, N));
+    UpArgs a{};
+    a.x = (const uint16_t*)x;
+    a.w = (const uint16_t*)w;
+    a.bias = (const uint16_t*)bias;
+    a.h = (uint16_t*)h_out;
+    a.ldx = ldx;
+    a.ldw = ldw;
+    a.ldh = ldh;
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.grid_n = (uint32_t)((N + kTile - 1) / kTile);
+    a.grid_m = (uint32_t)((M + kTile - 1) / kTile);
+    a.nb = (uint32_t)nb;
+    a.T = a.grid_m * a.grid_n;
+    a.bitmask = bitmask;
+    a.prefix = prefix;
+    a.vals = (uint16_t*)vals;
+    a.vals_capacity = vals_capacity;
+    a.offset_in = vals_offset_in;
+    a.align8 = align8 ? 1 : 0;
+    a.offset_out = vals_offset_out;
+    a.start_out = vals_start_out;
+    a.err = err_flags;
+    a.status = reinterpret_cast<uint64_t*>((uint8_t*)workspace + kWsHeaderBytes);
+    a.epoch = epoch;
+    const int64_t strips = (M + kUpBM - 1) / kUpBM;
+    const int64_t blocks = strips * nb;
+    if (blocks >= (1ll << 31)) return set_error(BS_ERR_INVALID, "%s: grid too large", fn);
+    hipLaunchKernelGGL(up_relu_compress_kernel, dim3((uint32_t)blocks), dim3(256), 0, (hipStream_t)stream, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(BS_ERR_HIP, "%s launch: %s", fn, hipGetErrorString(e));
+    return BS_OK;
+}

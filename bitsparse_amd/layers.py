@@ -17,9 +17,15 @@ from torch.autograd import Function
 from .bitsparse import BitsparseTensor, TensorBuffer
 from .config import RELU2_SCALE
 from .fp8 import is_fp8, matmul, to_fp8
-from .src.functions import relu_and_compress, relu_quantize_and_compress
+from .src.functions import (fused_linear_relu_ok, linear_relu_and_compress, relu_and_compress,
+                            relu_quantize_and_compress)
 from .src.hip_operators import mask_with_bitmask_, relu2_grad_sparse_
 from .src.sparse_matmul import AspB, AspRelu2B
+
+# FFNRelu / FFNRelu2 with bf16 storage into a TensorBuffer run the up-projection
+# GEMM, ReLU and compress as one kernel (bs_linear_relu_compress) when the
+# operands qualify; False keeps the library GEMM + bias add + compress path.
+USE_FUSED_UP = False
 
 
 # ------------------------------------------------------------
@@ -82,10 +88,13 @@ class FFNRelu:
         bs_dims = x.shape[:-1]
         x = x.reshape(-1, x.shape[-1])
 
-        z = matmul(x, W1.T, is_fp8(dtype))
-        if b1 is not None:
-            z = z + b1
-        y = ReluLinear.apply(z, W2, sparse_data, pack_sbit, dtype)
+        if not is_fp8(dtype) and not pack_sbit and USE_FUSED_UP and fused_linear_relu_ok(x, W1, b1, sparse_data):
+            y = _UpReluLinear.apply(x, W1, b1, W2, sparse_data, False)
+        else:
+            z = matmul(x, W1.T, is_fp8(dtype))
+            if b1 is not None:
+                z = z + b1
+            y = ReluLinear.apply(z, W2, sparse_data, pack_sbit, dtype)
 
         y = y.reshape(*bs_dims, y.shape[-1])
         if b2 is not None:
@@ -153,11 +162,61 @@ class FFNRelu2:
               storage_dtype: torch.dtype = torch.bfloat16):
         bs_dims = x.shape[:-1]
         x = x.reshape(-1, x.shape[-1])
-        z = matmul(x, W1.T, is_fp8(storage_dtype))
-        if b1 is not None:
-            z = z + b1
-        y = Relu2Linear.apply(z, W2, sparse_data, pack_sbit, storage_dtype)
+        if (not is_fp8(storage_dtype) and not pack_sbit and USE_FUSED_UP
+                and fused_linear_relu_ok(x, W1, b1, sparse_data)):
+            y = _UpReluLinear.apply(x, W1, b1, W2, sparse_data, True)
+        else:
+            z = matmul(x, W1.T, is_fp8(storage_dtype))
+            if b1 is not None:
+                z = z + b1
+            y = Relu2Linear.apply(z, W2, sparse_data, pack_sbit, storage_dtype)
         y = y.reshape(*bs_dims, y.shape[-1])
         if b2 is not None:
             y = y + b2
         return y
+
+
+# ------------------------------------------------------------
+# fused up-projection (bf16 storage into a TensorBuffer)
+# ------------------------------------------------------------
+class _UpReluLinear(Function):
+    """The autograd node of ``z = x @ W1.T + b1`` followed by ReluLinear
+    (square=False) or Relu2Linear (square=True), with z, relu(z) and its
+    compressed form produced by one kernel.  Backward repeats the calls of the
+    two-node graph: the same dz from the bitmask (or the ReLU^2 gradient), then
+    autograd's own products for x, W1 and b1."""
+
+    @staticmethod
+    def forward(ctx, x, W1, b1, W2, sparse_data: TensorBuffer, square: bool):
+        h, h_sparse = linear_relu_and_compress(x, W1, b1, sparse_data)
+        ctx.h_sparse = h_sparse
+        ctx.square = square
+        ctx.has_b1 = b1 is not None
+        ctx.save_for_backward(x, W1, W2)
+        if square:
+            h.square_()
+            h.mul_(RELU2_SCALE)
+        return matmul(h, W2.T, False)
+
+    @staticmethod
+    @torch.compiler.disable
+    def backward(ctx, grad_output: Tensor):
+        x, W1, W2 = ctx.saved_tensors
+        h: BitsparseTensor = ctx.h_sparse
+        ctx.h_sparse = None
+        if ctx.square:
+            grad_W2 = AspRelu2B(grad_output.T, h)
+        else:
+            grad_W2 = AspB(grad_output.T, h)
+        grad_x = grad_W1 = grad_b1 = None
+        if any(ctx.needs_input_grad[:3]):
+            grad_h = matmul(grad_output, W2, fp8=False)
+            grad_z = relu2_grad_sparse_(grad_h, h) if ctx.square else mask_with_bitmask_(grad_h, h)
+            # the products autograd forms for z = x @ W1.T + b1
+            if ctx.needs_input_grad[0]:
+                grad_x = grad_z.mm(W1)
+            if ctx.needs_input_grad[1]:
+                grad_W1 = x.t().mm(grad_z).t()
+            if ctx.has_b1 and ctx.needs_input_grad[2]:
+                grad_b1 = grad_z.sum(0)
+        return grad_x, grad_W1, grad_b1, grad_W2, None, None

@@ -92,6 +92,37 @@ def relu_and_compress(z: Tensor, sparse_data: TensorBuffer | None = None,
     return z, _to_tilesparse(z, None, sparse_data, pack_sbit, True)
 
 
+def linear_relu_and_compress(x: Tensor, W: Tensor, b: Tensor | None,
+                             sparse_data: TensorBuffer) -> tuple[Tensor, BitsparseTensor]:
+    """``z = x @ W.T; z = z + b; h = z.relu_(); dense_to_tilesparse(h, None,
+    sparse_data)`` (reference layers.py:86-89, :29, :37) as one kernel: the
+    up-projection GEMM writes h and its compressed form from its epilogue, so
+    h is not read back to be compressed.  bf16 values into a (raw, not
+    pack_sbit) TensorBuffer; ``fused_linear_relu_ok`` tells whether the
+    operands qualify.  Returns (h, BitsparseTensor)."""
+    if not fused_linear_relu_ok(x, W, b, sparse_data):
+        raise ValueError("linear_relu_and_compress: operands do not qualify (fused_linear_relu_ok)")
+    M, N = x.shape[0], W.shape[0]
+    grid_m, grid_n, num_tiles, TILE_NUMEL, TILE_BYTES = tile_grid(M, N, BLOCK_M, BLOCK_N)
+    h = torch.empty((M, N), device=x.device, dtype=torch.bfloat16)
+    bitmask = torch.empty(num_tiles * TILE_BYTES, device=x.device, dtype=torch.uint8)
+    prefix = torch.empty(num_tiles + 1, device=x.device, dtype=torch.uint32)
+    vals_offset = sparse_data.offset
+    new_offset = torch.empty(1, device=x.device, dtype=torch.int64)
+    ops.linear_relu_compress_into(x, W, b, h, bitmask, prefix, sparse_data.vals, vals_offset, new_offset,
+                                  sparse_data.err_flags)
+    sparse_data.offset = new_offset
+    return h, BitsparseTensor(sparse_data.vals, bitmask, prefix, (M, N), torch.bfloat16, grid_m, grid_n,
+                              BLOCK_M, BLOCK_N, scale=None, vals_offset=vals_offset)
+
+
+def fused_linear_relu_ok(x: Tensor, W: Tensor, b: Tensor | None, sparse_data: TensorBuffer | None) -> bool:
+    """The fused up-projection applies: bf16 operands the kernel takes as
+    they are, and a raw bf16 TensorBuffer to compress into."""
+    return (sparse_data is not None and not sparse_data.pack_sbit and sparse_data.vals.dtype == torch.bfloat16
+            and x.is_cuda and ops.linear_relu_compress_supported(x, W, b))
+
+
 def _to_tilesparse(dense: Tensor, scale: Tensor | None, sparse_data: TensorBuffer | None,
                    pack_sbit: bool, relu: bool) -> BitsparseTensor:
     M, N = dense.shape

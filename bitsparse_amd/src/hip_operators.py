@@ -153,6 +153,56 @@ def compress_into(dense: Tensor, bitmask: Tensor, prefix: Tensor, vals: Tensor |
         check(L.bs_compress(*args, stream_handle(dense.device)), "bs_compress")
 
 
+def linear_relu_compress_into(x: Tensor, W: Tensor, bias: Tensor | None, h_out: Tensor | None,
+                              bitmask: Tensor, prefix: Tensor, vals: Tensor,
+                              vals_offset_in: Tensor | None, vals_offset_out: Tensor | None,
+                              err_flags: Tensor | None) -> None:
+    """h = relu(x @ W.T + bias) with its compressed form, in one kernel
+    (bs_linear_relu_compress): x [M, K], W [N, K], bias [N] (or None), bf16,
+    rows contiguous; h_out (or None) [M, N] bf16 receives h; bitmask / prefix /
+    vals / cursors as for ``compress_into`` (bf16 values)."""
+    require_device(x, "linear_relu_compress")
+    for t, what in ((x, "x"), (W, "W")):
+        if t.dtype != torch.bfloat16 or t.dim() != 2 or t.stride(1) != 1:
+            raise ValueError(f"linear_relu_compress: {what} must be a bf16 matrix with contiguous rows")
+    M, K = x.shape
+    N = W.shape[0]
+    if W.shape[1] != K:
+        raise ValueError("linear_relu_compress: x and W disagree on K")
+    if bias is not None and (bias.dtype != torch.bfloat16 or bias.numel() != N or not bias.is_contiguous()):
+        raise ValueError("linear_relu_compress: bias must be a contiguous bf16 [N]")
+    if h_out is not None and (h_out.shape != (M, N) or h_out.dtype != torch.bfloat16 or h_out.stride(1) != 1):
+        raise ValueError("linear_relu_compress: h_out must be a bf16 [M, N] matrix with contiguous rows")
+    if vals.dtype != torch.bfloat16:
+        raise TypeError("linear_relu_compress: the values are bf16")
+    L = _lib.load()
+    ws = _lib.workspace_for(x.device)
+    ws.ensure(L.bs_compress_workspace_bytes(M, N))
+    epoch = ws.next_epoch()
+    check(L.bs_linear_relu_compress(x.data_ptr(), M, K, x.stride(0), W.data_ptr(), N, W.stride(0), ptr(bias),
+                                    ptr(h_out), h_out.stride(0) if h_out is not None else N,
+                                    bitmask.data_ptr(), prefix.data_ptr(), vals.data_ptr(), vals.numel(),
+                                    ptr(vals_offset_in), 0, ptr(vals_offset_out), None, ptr(err_flags),
+                                    ws.buf.data_ptr(), ws.nbytes, epoch, stream_handle(x.device)),
+          "bs_linear_relu_compress")
+
+
+def linear_relu_compress_supported(x: Tensor, W: Tensor, bias: Tensor | None) -> bool:
+    """Whether bs_linear_relu_compress takes these operands as they are."""
+    if x.dim() != 2 or W.dim() != 2 or x.dtype != torch.bfloat16 or W.dtype != torch.bfloat16:
+        return False
+    M, K = x.shape
+    N = W.shape[0]
+    if M == 0 or N == 0 or K % 8 or N % 8 or N > 24576:
+        return False
+    for t in (x, W):
+        if t.stride(1) != 1 or t.stride(0) % 8 or t.data_ptr() % 16:
+            return False
+    if bias is not None and (bias.dtype != torch.bfloat16 or not bias.is_contiguous() or bias.numel() != N):
+        return False
+    return True
+
+
 def compress_packed_into(dense: Tensor, bitmask: Tensor, prefix: Tensor, stream: Tensor,
                          vals_offset_in: Tensor | None, vals_offset_out: Tensor | None,
                          vals_start_out: Tensor | None, err_flags: Tensor | None,

@@ -152,6 +152,32 @@ int bs_compress_relu(const void* preact, int in_dtype, int64_t M, int64_t N, int
                      uint32_t epoch, void* relu_out, void* stream);
 
 /*
+ * Up-projection GEMM with the ReLU and the compress fused into its epilogue:
+ *     z = bf16(bf16(x @ W^T) + bias),  h = relu(z)   (torch's GPU relu)
+ * and h compressed exactly as bs_compress_relu would compress z, in one
+ * kernel: h is never read back from HBM.  x: bf16 [M, K] (row stride ldx),
+ * W: bf16 [N, K] (row stride ldw), bias: bf16 [N] (nullable: no bias add,
+ * one rounding), h_out: bf16 [M, N] (row stride ldh; nullable: h is not
+ * written).  Needs M, N > 0, K >= 0, K and N multiples of 8, ldx, ldw, ldh
+ * multiples of 8, x, W, h_out and vals 16-byte aligned, N <= 24576.  The
+ * values are bf16; vals_capacity, vals_offset_in, align8, vals_offset_out,
+ * vals_start_out, err_flags, workspace (bs_compress_workspace_bytes(M, N))
+ * and epoch as for bs_compress (refused while `stream` is capturing).  The
+ * fp32 accumulation order is the kernel's own, so z can differ from a
+ * library GEMM's in the last bit of some elements; the compressed form is
+ * always exactly that of the h it writes.  Bit 2 of *err_flags reports a
+ * look-back wait that was cut off after 20 ms (results then wrong; not
+ * expected on a GPU this launch has to itself).  Replaces z = x @ W1^T; z = z + b1;
+ * h = z.relu_(); dense_to_tilesparse(h) in lib_sparse/layers.py:86-89,
+ * :29, :37.
+ */
+int bs_linear_relu_compress(const void* x, int64_t M, int64_t K, int64_t ldx, const void* w, int64_t N,
+                            int64_t ldw, const void* bias, void* h_out, int64_t ldh, uint8_t* bitmask,
+                            uint32_t* prefix, void* vals, int64_t vals_capacity, const int64_t* vals_offset_in,
+                            int align8, int64_t* vals_offset_out, int64_t* vals_start_out, int32_t* err_flags,
+                            void* workspace, int64_t workspace_bytes, uint32_t epoch, void* stream);
+
+/*
  * bs_compress with pack_sbit storage: the values are written straight into
  * the 15/7-bit stream `stream_bytes` (4-byte aligned, stream_nbytes bytes;
  * value i occupies stream bits [i*b, (i+1)*b), LSB first, b = 15 for bf16

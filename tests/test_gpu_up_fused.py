@@ -1,0 +1,193 @@
+"""Up-projection GEMM with the ReLU and the compress in its epilogue
+(bs_linear_relu_compress), the fused form of reference lib_sparse/layers.py:86-89
+(z = x @ W1^T; z = z + b1), :29 (h = z.relu_()) and :37 (dense_to_tilesparse).
+
+Pinned two ways:
+* the compressed form is bit-exact against the oracle's compress of the h the
+  kernel wrote (same bitmask, prefix and values), at every shape, with NaN /
+  Inf / -0 in the products, and at configs[1]'s full 8192 x 768 -> 3072;
+* h against an fp32 product rounded as the reference rounds
+  (relu(bf16(bf16(x @ W^T) + b))): the kernel's fp32 accumulation order is its
+  own, so each element is within rtol 2^-7 (two bf16 roundings of a slightly
+  different sum) plus atol 2^-8 * max|h| (sums that cancel to near zero).
+"""
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests.helpers import bits, preact_input, special_bf16
+
+pytestmark = pytest.mark.gpu
+
+
+def _ops():
+    import bitsparse_amd.src.hip_operators as H
+    return H
+
+
+def _operands(M, N, K, seed, dev, bias=True, scale=None):
+    x = preact_input((M, K), seed=seed).to(dev)
+    s = scale if scale is not None else K ** -0.5
+    W = (preact_input((N, K), seed=seed + 1).float() * s).to(torch.bfloat16).to(dev)
+    b = preact_input((N,), mu=-0.3, seed=seed + 2).to(dev) if bias else None
+    return x, W, b
+
+
+def _run(x, W, b, cap=None, offset=0):
+    H = _ops()
+    M, N = x.shape[0], W.shape[0]
+    T = ((M + 63) // 64) * ((N + 63) // 64)
+    dev = x.device
+    h = torch.empty((M, N), device=dev, dtype=torch.bfloat16)
+    bm = torch.empty(T * 512, device=dev, dtype=torch.uint8)
+    pf = torch.empty(T + 1, device=dev, dtype=torch.uint32)
+    vals = torch.zeros(cap if cap is not None else offset + M * N, device=dev, dtype=torch.bfloat16)
+    off_in = torch.full((1,), offset, device=dev, dtype=torch.int64)
+    off_out = torch.empty(1, device=dev, dtype=torch.int64)
+    err = torch.zeros(1, device=dev, dtype=torch.int32)
+    H.linear_relu_compress_into(x, W, b, h, bm, pf, vals, off_in, off_out, err)
+    return h, bm, pf, vals, off_out, err
+
+
+def _reference_h(x, W, b):
+    z = (x.float() @ W.float().T).to(torch.bfloat16)
+    if b is not None:
+        z = (z.float() + b.float()).to(torch.bfloat16)
+    return torch.relu(z)
+
+
+def _check_compressed(h, bm, pf, vals, off_out, offset=0):
+    obm, opf, ov = O.compress(bits(h), O.BF16)
+    assert (bits(bm) == obm).all(), "bitmask"
+    assert (bits(pf) == opf).all(), "prefix"
+    got = bits(vals)[offset:offset + ov.size]
+    assert (got == ov).all(), "vals"
+    assert int(off_out.item()) == offset + ov.size
+
+
+def _check_h(h, x, W, b):
+    ref = _reference_h(x, W, b).float()
+    fin = ref[torch.isfinite(ref)]
+    atol = 2 ** -8 * ((fin.abs().max().item() if fin.numel() else 0.0) + 1e-30)
+    torch.testing.assert_close(h.float(), ref, rtol=2 ** -7, atol=atol, equal_nan=True)
+
+
+# (M, N, K): whole and partial 256 x 192 workgroup tiles, partial 64 x 64
+# format tiles, K not a multiple of the 64-deep step, one-tile matrices
+SHAPES = [(256, 192, 64), (300, 200, 72), (64, 8, 8), (1000, 768, 256), (513, 392, 40), (40, 1000, 128),
+          (2048, 3072, 96)]
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("bias", [True, False])
+def test_compressed_form_is_that_of_h(dev, shape, bias):
+    M, N, K = shape
+    x, W, b = _operands(M, N, K, 3, dev, bias)
+    h, bm, pf, vals, off_out, err = _run(x, W, b)
+    assert int(err.item()) == 0
+    _check_compressed(h, bm, pf, vals, off_out)
+    _check_h(h, x, W, b)
+
+
+def test_special_values(dev):
+    """NaN / Inf / -0 / denormals in x: torch's relu keeps NaN in h, the
+    bitmask excludes it; -0 and negatives become +0."""
+    M, N, K = 320, 384, 64
+    x = special_bf16((M, K), seed=4).to(dev)
+    _, W, b = _operands(M, N, K, 5, dev)
+    h, bm, pf, vals, off_out, err = _run(x, W, b)
+    _check_compressed(h, bm, pf, vals, off_out)
+    _check_h(h, x, W, b)
+    hb = bits(h)
+    assert not ((hb >= 0x8000) & (hb <= 0xff80)).any(), "relu leaves no negative or -0 bits"
+
+
+def test_cursor_capacity_and_offset(dev):
+    """Values land at the cursor; the next cursor is start + nnz; values past
+    the capacity are not written and flag bit 0."""
+    M, N, K = 512, 384, 64
+    x, W, b = _operands(M, N, K, 6, dev)
+    h, bm, pf, vals, off_out, err = _run(x, W, b, offset=37)
+    _check_compressed(h, bm, pf, vals, off_out, offset=37)
+    assert (bits(vals)[:37] == 0).all()
+    nnz = int(off_out.item()) - 37
+    cap = 37 + nnz // 2
+    h2, bm2, pf2, vals2, off2, err2 = _run(x, W, b, cap=cap, offset=37)
+    assert int(err2.item()) & 1
+    assert int(off2.item()) == 37 + nnz
+    _, _, ov = O.compress(bits(h2), O.BF16)
+    assert (bits(vals2)[37:cap] == ov[:cap - 37]).all()
+
+
+def test_shared_buffer_two_activations(dev):
+    """Two fused compresses into one TensorBuffer, then both decompress."""
+    from bitsparse_amd.bitsparse import TensorBuffer
+    from bitsparse_amd.src import functions as F
+    H = _ops()
+    buf = TensorBuffer(2 * 320 * 392, device=dev)
+    outs = []
+    for seed in (7, 9):
+        x, W, b = _operands(320, 392, 64, seed, dev)
+        h, sp = F.linear_relu_and_compress(x, W, b, buf)
+        outs.append((h.clone(), sp))
+    assert not buf.overflowed()
+    for h, sp in outs:
+        d = torch.empty_like(h)
+        H.unpack_batch_(sp, d, 0, sp.grid_n, h.shape[1], h.shape[0], sp.grid_m * sp.grid_n)
+        assert torch.equal(d.view(torch.int16), torch.where(h > 0, h, torch.zeros_like(h)).view(torch.int16))
+
+
+def test_configs1_full_size(dev):
+    """configs[1]'s up-projection: x 8192 x 768, W1 3072 x 768 N(0, 0.02), b1."""
+    M, N, K = 8192, 3072, 768
+    x, W, b = _operands(M, N, K, 11, dev, scale=0.02)
+    h, bm, pf, vals, off_out, err = _run(x, W, b)
+    assert int(err.item()) == 0
+    _check_compressed(h, bm, pf, vals, off_out)
+    _check_h(h, x, W, b)
+    zeros = 1.0 - int(off_out.item()) / (M * N)
+    assert 0.3 < zeros < 0.7
+
+
+@pytest.mark.parametrize("square", [False, True])
+def test_layers_take_the_fused_path(dev, monkeypatch, square):
+    """FFNRelu / FFNRelu2 (bf16, TensorBuffer) run the fused kernel and agree
+    with the library-GEMM path: y and the gradients within bf16 tolerance
+    (z differs in the last bit of some elements, so a few bitmask bits near
+    zero may too)."""
+    from bitsparse_amd import layers
+    from bitsparse_amd.bitsparse import TensorBuffer
+    from bitsparse_amd.src import functions as F
+    calls = []
+    real = F.linear_relu_and_compress
+    monkeypatch.setattr(layers, "linear_relu_and_compress", lambda *a: calls.append(1) or real(*a))
+    M, D, FF = 512, 256, 768
+    x0 = preact_input((M, D), seed=12).to(dev)
+    W1 = (preact_input((FF, D), seed=13).float() * 0.05).to(torch.bfloat16).to(dev)
+    W2 = (preact_input((D, FF), seed=14).float() * 0.05).to(torch.bfloat16).to(dev)
+    b1 = (preact_input((FF,), seed=15).float() * 0.1).to(torch.bfloat16).to(dev)
+    dy = preact_input((M, D), seed=16).to(dev)
+    fn = layers.FFNRelu2 if square else layers.FFNRelu
+    res = []
+    for fused in (True, False):
+        monkeypatch.setattr(layers, "USE_FUSED_UP", fused)
+        x = x0.clone().requires_grad_(True)
+        p = [t.clone().requires_grad_(True) for t in (W1, W2, b1)]
+        buf = TensorBuffer(M * FF, device=dev)
+        y = fn.apply(x, p[0], p[1], p[2], sparse_data=buf)
+        y.backward(dy)
+        res.append([y.detach(), x.grad, p[0].grad, p[1].grad, p[2].grad])
+    assert len(calls) == 1
+    for got, want in zip(*res):
+        tol = 2 ** -6 * want.float().abs().max().item()
+        torch.testing.assert_close(got.float(), want.float(), rtol=2 ** -6, atol=tol)
+
+
+def test_unsupported_operands_are_refused(dev):
+    """K or N not a multiple of 8 is refused by the entry point (the layers
+    then keep the library path)."""
+    H = _ops()
+    x, W, b = _operands(64, 100, 12, 17, dev)
+    assert not H.linear_relu_compress_supported(x, W, b)
+    with pytest.raises(ValueError, match="multiples of 8"):
+        _run(x, W, b)
