@@ -188,24 +188,6 @@ __device__ __forceinline__ uint32_t chunk_mask(const typename Raw<CompressTraits
     }
 }
 
-// Positive-bit byte of 8 bf16 values with packed 16-bit arithmetic:
-// x > 0  <=>  (bits - 1) mod 2^16 < 0x7f80.
-__device__ __forceinline__ uint32_t mask_bf16x8_pk(const uint4 v)
-{
-    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-    uint32_t q[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const u16x2 h = __builtin_bit_cast(u16x2, w[i]);
-        const u16x2 t = h - (u16x2)(1);
-        const u16x2 s = __builtin_elementwise_sub_sat((u16x2)(0x7f80), t);
-        q[i] = __builtin_bit_cast(uint32_t, __builtin_elementwise_min(s, (u16x2)(1)));   // bits 0, 16
-    }
-    const uint32_t x = q[0] | (q[1] << 2) | (q[2] << 4) | (q[3] << 6);
-    return (x & 0x55u) | ((x >> 15) & 0xaau);
-}
-
 template <int IN_T, bool QUANT>
 __device__ __forceinline__ uint32_t stream_chunk_mask(const typename Raw<CompressTraits<IN_T, QUANT>::INB>::T& d,
                                                       typename Raw<CompressTraits<IN_T, QUANT>::OUTB>::T& o,
@@ -296,11 +278,6 @@ __device__ __forceinline__ uint64_t bcast_lane0(uint64_t v)
 // unit that stays unpublished for kLookbackPatienceTicks is counted from the
 // dense input instead.  Returns the exclusive prefix of unit u in every lane.
 constexpr int kGroupUnits = 64;
-
-__device__ __forceinline__ uint32_t wave_total(uint32_t v)
-{
-    return (uint32_t)__builtin_amdgcn_readlane((int)wave_incl_scan(v), 63);
-}
 
 template <int IN_T, bool QUANT, bool VEC, int U>
 __device__ uint32_t wave_lookback_grouped(const CompressArgs& a, uint32_t u, uint32_t unit_total,

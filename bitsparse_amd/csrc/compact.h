@@ -18,6 +18,30 @@ __device__ __forceinline__ uint64_t pack_status(uint32_t epoch, uint64_t flag, u
     return ((uint64_t)epoch << 34) | (flag << 32) | v;
 }
 
+// Positive-bit byte of 8 bf16 values with packed 16-bit arithmetic:
+// x > 0  <=>  (bits - 1) mod 2^16 < 0x7f80.
+__device__ __forceinline__ uint32_t mask_bf16x8_pk(const uint4 v)
+{
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    uint32_t q[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const u16x2 h = __builtin_bit_cast(u16x2, w[i]);
+        const u16x2 t = h - (u16x2)(1);
+        const u16x2 s = __builtin_elementwise_sub_sat((u16x2)(0x7f80), t);
+        q[i] = __builtin_bit_cast(uint32_t, __builtin_elementwise_min(s, (u16x2)(1)));   // bits 0, 16
+    }
+    const uint32_t x = q[0] | (q[1] << 2) | (q[2] << 4) | (q[3] << 6);
+    return (x & 0x55u) | ((x >> 15) & 0xaau);
+}
+
+// wave total of a per-lane value (every lane)
+__device__ __forceinline__ uint32_t wave_total(uint32_t v)
+{
+    return (uint32_t)__builtin_amdgcn_readlane((int)wave_incl_scan(v), 63);
+}
+
 // Compaction selectors of mask byte m: the set elements move to the front.
 // bf16 (OUTB 2): output dword j = perm(D1, D0, s[j]) | perm(D3, D2, s[4 + j]);
 // fp8 (OUTB 1): output dword j = perm(D1, D0, s[j]), j < 2.

@@ -95,23 +95,33 @@ __device__ __forceinline__ uint32_t relu_bf16_bits(uint32_t b) { return (b - 0x8
 // it only guarantees that every wave ends.
 constexpr uint64_t kUpLookbackGiveUpTicks = 2000000;
 
-// Exclusive prefix of unit u from the status words of units 0 .. u-1: 64
-// words per read (lane j: unit pos - j), summing aggregates back to the
-// nearest inclusive prefix; re-read while a needed word is unpublished.
+// Exclusive prefix of unit u from the status words of units 0 .. u-1.  Each
+// read covers 256 units: lane j takes units pos - 4j .. pos - 4j - 3, nearest
+// first, and the walk sums values back to the nearest inclusive prefix; it
+// re-reads while a word it needs is unpublished.
 __device__ uint32_t up_lookback(const UpArgs& a, uint32_t u, int lane)
 {
     uint32_t excl = 0;
     int64_t pos = (int64_t)u - 1;
     const uint64_t t0 = wall_clock64();
     while (pos >= 0) {
-        const int64_t q = pos - lane;
-        const uint64_t s = q >= 0 ? ld_relaxed(&a.status[q]) : pack_status(a.epoch, kFlagInc, 0u);
-        const uint32_t flag = (uint32_t)(s >> 34) == a.epoch ? (uint32_t)(s >> 32) & 3u : 0u;
-        const uint64_t inc = __ballot(flag == kFlagInc);
-        const uint64_t unpub = __ballot(flag == 0u);
-        const int first = inc ? __ffsll((unsigned long long)inc) - 1 : 63;   // last lane needed
+        uint32_t sum = 0;
+        bool unpub = false, inc = false;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int64_t q = pos - 4 * lane - i;
+            const uint64_t s = q >= 0 ? ld_relaxed(&a.status[q]) : pack_status(a.epoch, kFlagInc, 0u);
+            const uint32_t flag = (uint32_t)(s >> 34) == a.epoch ? (uint32_t)(s >> 32) & 3u : 0u;
+            if (!inc) {                  // words up to the lane's nearest inclusive prefix
+                unpub |= flag == 0u;
+                sum += (uint32_t)s;
+                inc = flag == kFlagInc;
+            }
+        }
+        const uint64_t incs = __ballot(inc);
+        const int first = incs ? __ffsll((unsigned long long)incs) - 1 : 63;   // last lane needed
         const uint64_t need = first == 63 ? ~0ull : ((2ull << first) - 1ull);
-        if (unpub & need) {
+        if (__ballot(unpub) & need) {
             if (wall_clock64() - t0 > kUpLookbackGiveUpTicks) {
                 if (lane == 0 && a.err) atomicOr(a.err, 4);
                 break;
@@ -119,9 +129,9 @@ __device__ uint32_t up_lookback(const UpArgs& a, uint32_t u, int lane)
             __builtin_amdgcn_s_sleep(2);
             continue;
         }
-        excl += wave_sum_u32(lane <= first ? (uint32_t)s : 0u);
-        if (inc) break;
-        pos -= 64;
+        excl += wave_sum_u32(lane <= first ? sum : 0u);
+        if (incs) break;
+        pos -= 256;
     }
     return excl;
 }
@@ -154,15 +164,19 @@ __global__ __launch_bounds__(256, 1) void up_relu_compress_kernel(UpArgs a)
     const uint32_t swz = (uint32_t)((r8 >> 1) & 7);        // rows r8 + 32 i share it
     const uint32_t xrow = (uint32_t)(r8 * a.ldx * 2), xstep = (uint32_t)(32 * a.ldx * 2);
     const uint32_t wrow = (uint32_t)(r8 * a.ldw * 2), wstep = (uint32_t)(32 * a.ldw * 2);
-    uint4 ga[kUpBM / 32], gb[kUpBN / 32];
-    auto gload = [&](int s) __attribute__((always_inline)) {
+    // two register sets: slab s + 2 is loaded while slab s + 1, loaded a
+    // step earlier, waits to be stored -- each load gets two steps of MFMAs
+    uint4 ga[2][kUpBM / 32], gb[2][kUpBN / 32];
+    auto gload = [&](int s, auto SET) __attribute__((always_inline)) {
+        constexpr int R = decltype(SET)::value;
         const uint32_t koff = (uint32_t)(s * 64 + 8 * c8) * 2u;
 #pragma unroll
-        for (int i = 0; i < kUpBM / 32; i++) ga[i] = load16(rsx, xrow + (uint32_t)i * xstep + koff);
+        for (int i = 0; i < kUpBM / 32; i++) ga[R][i] = load16(rsx, xrow + (uint32_t)i * xstep + koff);
 #pragma unroll
-        for (int i = 0; i < kUpBN / 32; i++) gb[i] = load16(rsw, wrow + (uint32_t)i * wstep + koff);
+        for (int i = 0; i < kUpBN / 32; i++) gb[R][i] = load16(rsw, wrow + (uint32_t)i * wstep + koff);
     };
-    auto lstore = [&](int s, int buf) __attribute__((always_inline)) {
+    auto lstore = [&](int s, int buf, auto SET) __attribute__((always_inline)) {
+        constexpr int R = decltype(SET)::value;
         // a mask, not a select of two values: a select of an array element
         // becomes a load through a selected pointer, which puts the array in
         // scratch memory
@@ -173,12 +187,36 @@ __global__ __launch_bounds__(256, 1) void up_relu_compress_kernel(UpArgs a)
 #pragma unroll
         for (int i = 0; i < kUpBM / 32; i++)
             *reinterpret_cast<uint4*>(As + (r8 + 32 * i) * 128 + coff) =
-                uint4{ga[i].x & km, ga[i].y & km, ga[i].z & km, ga[i].w & km};
+                uint4{ga[R][i].x & km, ga[R][i].y & km, ga[R][i].z & km, ga[R][i].w & km};
 #pragma unroll
         for (int i = 0; i < kUpBN / 32; i++)
             *reinterpret_cast<uint4*>(Bs + (r8 + 32 * i) * 128 + coff) =
-                uint4{gb[i].x & km, gb[i].y & km, gb[i].z & km, gb[i].w & km};
+                uint4{gb[R][i].x & km, gb[R][i].y & km, gb[R][i].z & km, gb[R][i].w & km};
     };
+
+    // one chunk of the slab traffic: n < 8 the x rows r8 + 32 n, else the W
+    // rows r8 + 32 (n - 8)
+    auto gload1 = [&](int s, auto SET, auto NI) __attribute__((always_inline)) {
+        constexpr int R = decltype(SET)::value, n = decltype(NI)::value;
+        const uint32_t koff = (uint32_t)(s * 64 + 8 * c8) * 2u;
+        if constexpr (n < kUpBM / 32) ga[R][n] = load16(rsx, xrow + (uint32_t)n * xstep + koff);
+        else gb[R][n - kUpBM / 32] = load16(rsw, wrow + (uint32_t)(n - kUpBM / 32) * wstep + koff);
+    };
+    auto lstore1 = [&](int buf, uint32_t km, auto SET, auto NI) __attribute__((always_inline)) {
+        constexpr int R = decltype(SET)::value, n = decltype(NI)::value;
+        const uint32_t coff = ((uint32_t)c8 ^ swz) << 4;
+        if constexpr (n < kUpBM / 32) {
+            uint8_t* As = lds + buf * kUpAStage;
+            *reinterpret_cast<uint4*>(As + (r8 + 32 * n) * 128 + coff) =
+                uint4{ga[R][n].x & km, ga[R][n].y & km, ga[R][n].z & km, ga[R][n].w & km};
+        } else {
+            constexpr int nb = n - kUpBM / 32;
+            uint8_t* Bs = lds + 2 * kUpAStage + buf * kUpBStage;
+            *reinterpret_cast<uint4*>(Bs + (r8 + 32 * nb) * 128 + coff) =
+                uint4{gb[R][nb].x & km, gb[R][nb].y & km, gb[R][nb].z & km, gb[R][nb].w & km};
+        }
+    };
+    constexpr int kChunks = kUpBM / 32 + kUpBN / 32;     // slab chunks per thread per step
 
     // ---- fragments of k-slice ks (16 k): lane l reads row 32 i + l % 32,
     // chunk 2 ks + l / 32 of its wave's rows
@@ -207,59 +245,88 @@ __global__ __launch_bounds__(256, 1) void up_relu_compress_kernel(UpArgs a)
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
 
-    // Step s: slab s in buffer s & 1; its k-slice ks fragments in set ks & 1,
-    // the next slice's read during the current slice's MFMAs; slab s + 1 is
-    // loaded into registers at the top and stored into the other buffer at
-    // the bottom, before the barrier.
+    // Step s: slab s in LDS buffer s & 1, its k-slice ks fragments in set
+    // ks & 1 (the next slice's read during the current slice's MFMAs).
+    // During step s, slab s + 2 is loaded into register set s & 1 and slab
+    // s + 1 (register set (s + 1) & 1, loaded during step s - 1) is stored
+    // into the other LDS buffer, each load and store behind an MFMA; one
+    // barrier ends the step.
     const int nsteps = (int)((a.K + 63) / 64);
     if (nsteps > 0) {
-        gload(0);
-        lstore(0, 0);
+        gload(0, IC<0>{});
+        gload(std::min(1, nsteps - 1), IC<1>{});
+        lstore(0, 0, IC<0>{});
     }
     __syncthreads();
     if (nsteps > 0) fread(0, 0, IC<0>{});
-    for (int s = 0; s < nsteps; s++) {
-        const int buf = s & 1;
-        if (s + 1 < nsteps) gload(s + 1);
+    auto step = [&](int s, auto PI) __attribute__((always_inline)) {
+        constexpr int P = decltype(PI)::value;           // s & 1
+        // slab s + 2 (past the end: the last slab again, so the loads in
+        // flight, and the waits that count them, are the same on every path)
+        // streams into register set P and slab s + 1 out of set P ^ 1 into
+        // LDS buffer P ^ 1 (unused during this step; after the last step the
+        // store is harmless), one chunk after each of the first MFMAs
+        const int sl = std::min(s + 2, nsteps - 1);
+        const uint32_t km = (int64_t)(s + 1) * 64 + 8 * c8 < a.K ? 0xffffffffu : 0u;
         static_for<4>([&](auto KS) __attribute__((always_inline)) {
             constexpr int ks = decltype(KS)::value, cur = ks & 1;
-            // issue order fixed by the sched barriers: the next slice's reads,
-            // then this slice's twelve MFMAs, which hide their latency
-            if constexpr (ks < 3) fread(buf, ks + 1, IC<cur ^ 1>{});
+            // the next slice's fragment reads first, then this slice's twelve
+            // MFMAs (the sched barriers fix the issue order)
+            if constexpr (ks < 3) fread(P, ks + 1, IC<cur ^ 1>{});
             __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int i = 0; i < kUpIM; i++)
-#pragma unroll
-                for (int j = 0; j < kUpJN; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cur][i], fb[cur][j], acc[i][j], 0, 0, 0);
-            __builtin_amdgcn_sched_barrier(0);
+            static_for<kUpIM * kUpJN>([&](auto MI) __attribute__((always_inline)) {
+                constexpr int m = decltype(MI)::value, i = m / kUpJN, j = m % kUpJN;
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cur][i], fb[cur][j], acc[i][j], 0, 0, 0);
+                constexpr int q = ks * kUpIM * kUpJN + m;
+                if constexpr (q < 2 * kChunks) {
+                    if constexpr (q % 2 == 0) lstore1(P ^ 1, km, IC<P ^ 1>{}, IC<q / 2>{});
+                    else gload1(sl, IC<P>{}, IC<q / 2>{});
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            });
         });
-        if (s + 1 < nsteps) lstore(s + 1, buf ^ 1);
         __syncthreads();
-        if (s + 1 < nsteps) fread(buf ^ 1, 0, IC<0>{});
+        if (s + 1 < nsteps) fread(P ^ 1, 0, IC<0>{});
+    };
+    int s = 0;
+    for (; s + 1 < nsteps; s += 2) {
+        step(s, IC<0>{});
+        step(s + 1, IC<1>{});
     }
+    if (s < nsteps) step(s, IC<0>{});
 
     // ---- stage h = relu(bf16(bf16(acc) + b)) as bf16 (0 outside the matrix).
     // Accumulator element r of lane l of a 32x32 block is row 8 (r / 4) +
-    // 4 (l / 32) + r % 4, column l % 32.
+    // 4 (l / 32) + r % 4, column l % 32; elements r, r + 1 (r even) are two
+    // consecutive rows of one column and are converted together.  Without a
+    // bias the add of +0 is exact (it can only turn -0 into +0, which the
+    // relu does anyway), so every element takes the same branch-free path.
     uint8_t* hs = lds;
     {
         const int rq = 4 * (lane >> 5);
+        const int rows_in = (int)std::min<int64_t>(kUpBM, a.M - m0);
+        typedef float f32x2_t __attribute__((ext_vector_type(2)));
+        typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 #pragma unroll
         for (int j = 0; j < kUpJN; j++) {
             const int col = wn * 96 + 32 * j + fl;
             const bool cin = n0 + col < a.N;
             const float bj = (a.bias != nullptr && cin) ? bf16_to_f32(a.bias[n0 + col]) : 0.0f;
+            uint8_t* cp = hs + col * 2;
 #pragma unroll
             for (int i = 0; i < kUpIM; i++) {
 #pragma unroll
-                for (int r = 0; r < 16; r++) {
+                for (int r = 0; r < 16; r += 2) {
                     const int row = wm * 128 + 32 * i + 8 * (r >> 2) + rq + (r & 3);
-                    uint32_t hb = f32_to_bf16(acc[i][j][r]);
-                    if (a.bias != nullptr) hb = f32_to_bf16(bf16_to_f32(hb) + bj);
-                    hb = relu_bf16_bits(hb);
-                    if (!cin || m0 + row >= a.M) hb = 0u;
-                    *reinterpret_cast<uint16_t*>(hs + row * kUpHP + col * 2) = (uint16_t)hb;
+                    const uint32_t zp = __builtin_bit_cast(
+                        uint32_t, __builtin_convertvector(f32x2_t{acc[i][j][r], acc[i][j][r + 1]}, bf16x2_t));
+                    const f32x2_t zb = {__uint_as_float(zp << 16) + bj, __uint_as_float(zp & 0xffff0000u) + bj};
+                    const uint32_t hp = __builtin_bit_cast(uint32_t, __builtin_convertvector(zb, bf16x2_t));
+                    uint32_t h0 = relu_bf16_bits(hp & 0xffffu), h1 = relu_bf16_bits(hp >> 16);
+                    h0 = (cin && row < rows_in) ? h0 : 0u;
+                    h1 = (cin && row + 1 < rows_in) ? h1 : 0u;
+                    *reinterpret_cast<uint16_t*>(cp + row * kUpHP) = (uint16_t)h0;
+                    *reinterpret_cast<uint16_t*>(cp + (row + 1) * kUpHP) = (uint16_t)h1;
                 }
             }
         }
@@ -272,6 +339,36 @@ __global__ __launch_bounds__(256, 1) void up_relu_compress_kernel(UpArgs a)
     const uint8_t* hw = hs + wave * 64 * kUpHP;
     const int64_t grow0 = m0 + (int64_t)wave * 64;
 
+    // bitmask bytes and counts: tile tt, round k: lane l takes chunk 64 k + l
+    // (tile row 8 k + l / 8, columns 8 (l % 8) .. +7) -- the format's byte order
+    const uint32_t t0 = tm * a.grid_n + cb * (uint32_t)kUpTiles;
+    const int ntiles = (int)std::min<uint32_t>((uint32_t)kUpTiles, a.grid_n - cb * (uint32_t)kUpTiles);
+    const int lrow = lane >> 3, lcol = (lane & 7) * 16;   // byte offset of the lane's chunk in a tile row
+    uint32_t mk[kUpTiles][2];                           // the 8 mask bytes of each tile, 4 per register
+    uint32_t tcnt[kUpTiles], toff[kUpTiles + 1];
+    toff[0] = 0;
+#pragma unroll
+    for (int tt = 0; tt < kUpTiles; tt++) {
+        mk[tt][0] = mk[tt][1] = 0u;
+        uint32_t cl = 0;
+        if (tt < ntiles) {
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const uint4 v = *reinterpret_cast<const uint4*>(hw + (8 * k + lrow) * kUpHP + tt * 128 + lcol);
+                const uint32_t m = mask_bf16x8_pk(v);
+                a.bitmask[(size_t)(t0 + tt) * kTileBytes + 64 * k + lane] = (uint8_t)m;
+                mk[tt][k >> 2] |= m << (8 * (k & 3));
+                cl += (uint32_t)__popc(m);
+            }
+        }
+        tcnt[tt] = wave_total(cl);
+        toff[tt + 1] = toff[tt] + tcnt[tt];
+    }
+    const uint32_t unit_total = toff[kUpTiles];
+    const uint32_t u = tm * a.nb + cb;
+    if (lane == 0) st_relaxed(&a.status[u], pack_status(a.epoch, u == 0 ? kFlagInc : kFlagAgg, unit_total));
+
+    // the dense h stores go out while the preceding units publish
     // dense h: 64 rows x 24 chunks, 16-byte stores (N % 8 == 0, ldh % 8 == 0)
     if (a.h != nullptr) {
 #pragma unroll 4
@@ -284,37 +381,6 @@ __global__ __launch_bounds__(256, 1) void up_relu_compress_kernel(UpArgs a)
         }
     }
 
-    // bitmask bytes and counts: tile tt, round k: lane l takes chunk 64 k + l
-    // (tile row 8 k + l / 8, columns 8 (l % 8) .. +7) -- the format's byte order
-    const uint32_t t0 = tm * a.grid_n + cb * (uint32_t)kUpTiles;
-    const int ntiles = (int)std::min<uint32_t>((uint32_t)kUpTiles, a.grid_n - cb * (uint32_t)kUpTiles);
-    const int lrow = lane >> 3, lcol = (lane & 7) * 16;   // byte offset of the lane's chunk in a tile row
-    uint32_t mk[kUpTiles][2];                           // the 8 mask bytes of each tile, 4 per register
-    uint32_t P[kUpTiles][9];                            // round offsets inside each tile's run
-    uint32_t tcnt[kUpTiles], toff[kUpTiles + 1];
-    toff[0] = 0;
-#pragma unroll
-    for (int tt = 0; tt < kUpTiles; tt++) {
-        mk[tt][0] = mk[tt][1] = 0u;
-        P[tt][0] = 0u;
-        const bool tin = tt < ntiles;
-#pragma unroll
-        for (int k = 0; k < 8; k++) {
-            uint32_t m = 0u;
-            if (tin) {
-                const uint4 v = *reinterpret_cast<const uint4*>(hw + (8 * k + lrow) * kUpHP + tt * 128 + lcol);
-                m = mask_bf16x8(v);
-                a.bitmask[(size_t)(t0 + tt) * kTileBytes + 64 * k + lane] = (uint8_t)m;
-            }
-            mk[tt][k >> 2] |= m << (8 * (k & 3));
-            P[tt][k + 1] = P[tt][k] + wave_sum_count(__popc(m));
-        }
-        tcnt[tt] = P[tt][8];
-        toff[tt + 1] = toff[tt] + tcnt[tt];
-    }
-    const uint32_t unit_total = toff[kUpTiles];
-    const uint32_t u = tm * a.nb + cb;
-    if (lane == 0) st_relaxed(&a.status[u], pack_status(a.epoch, u == 0 ? kFlagInc : kFlagAgg, unit_total));
 
     int64_t start = a.offset_in ? *a.offset_in : 0;
     if (a.align8) start = (start + 7) & ~(int64_t)7;
@@ -348,11 +414,15 @@ __global__ __launch_bounds__(256, 1) void up_relu_compress_kernel(UpArgs a)
         const int64_t g = start + (int64_t)excl + (int64_t)toff[tt];
         const int cnt = (int)tcnt[tt];
         const int a0 = (int)(g & 7);
+        uint32_t P = 0;                                 // offset of round k in the tile's run
 #pragma unroll
         for (int k = 0; k < 8; k++) {
             const uint32_t m = (mk[tt][k >> 2] >> (8 * (k & 3))) & 0xffu;
             const uint32_t c = (uint32_t)__popc(m);
-            const uint32_t ex = wave_incl_scan(c) - c;
+            const uint32_t incl = wave_incl_scan(c);
+            const uint32_t ex = incl - c;
+            const uint32_t base = P;
+            P += (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
             if (c != 0u) {
                 const uint4 w = *reinterpret_cast<const uint4*>(hw + (8 * k + lrow) * kUpHP + tt * 128 + lcol);
                 const uint4 s0 = *reinterpret_cast<const uint4*>(&sel_s[m * 8]);
@@ -362,7 +432,7 @@ __global__ __launch_bounds__(256, 1) void up_relu_compress_kernel(UpArgs a)
                 o.y = __builtin_amdgcn_perm(w.y, w.x, s0.y) | __builtin_amdgcn_perm(w.w, w.z, s1.y);
                 o.z = __builtin_amdgcn_perm(w.y, w.x, s0.z) | __builtin_amdgcn_perm(w.w, w.z, s1.z);
                 o.w = __builtin_amdgcn_perm(w.y, w.x, s0.w) | __builtin_amdgcn_perm(w.w, w.z, s1.w);
-                write_compacted<2>(reinterpret_cast<uint8_t*>(run + a0 + (int)P[tt][k] + (int)ex), o);
+                write_compacted<2>(reinterpret_cast<uint8_t*>(run + a0 + (int)base + (int)ex), o);
             }
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
