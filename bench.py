@@ -22,7 +22,7 @@ Also reported on the same line:
                 fwd+bwd time, compressed vs dense storage
   aux_kernels   the gradient, ReLU^2 unpack and fp8 kernels, each against its
                 algorithmic bytes
-  cpu_baseline  the C oracle (single thread) on a bounded row sample of the
+  cpu_baseline  the C oracle (one row block per host thread) on a bounded sample of the
                 same workload, same unit
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-mlp] [--skip-cpu]
@@ -246,14 +246,19 @@ def bench_kernels(steps: int, warmup: int, copy_gbs: float):
 
 
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+MFMA_FP8_PEAK_TFLOPS = 5000.0
 
 
 def bench_gemm(steps: int, warmup: int):
-    """dW = dY^T @ h with h compressed, at the two MLP configs' dW shapes."""
+    """dW = dY^T @ h with h compressed, at the two MLP configs' dW shapes, as
+    the layers call it: configs[1] bf16 (bf16 reconstruct-into-LDS GEMM),
+    configs[3] ReLU^2 with e4m3fn storage (fp8 reconstruct-into-LDS GEMM on
+    to_fp8(dY)), each against the decompress + library GEMM path
+    (AspB / AspRelu2B with the LDS GEMMs switched off)."""
     import torch
-    from bitsparse_amd.src import dw_gemm
+    from bitsparse_amd.fp8 import to_fp8
+    from bitsparse_amd.src import sparse_matmul
     from bitsparse_amd.src.functions import dense_to_tilesparse, quantize_and_compress
-    from bitsparse_amd.src.hip_operators import unpack_batch_, unpack_relu2_batch_
 
     dev = torch.device("cuda", 0)
     out = {}
@@ -263,35 +268,35 @@ def bench_gemm(steps: int, warmup: int):
         g = torch.Generator(device=dev).manual_seed(0)
         h = (torch.randn((K, N), device=dev, generator=g) + mu).to(torch.bfloat16).relu_()
         dY = torch.randn((K, M), device=dev, generator=g).to(torch.bfloat16)
-        A = dY.T
         if relu2_fp8:
             _, _, sp = quantize_and_compress(h, None)
+            qd, sd = to_fp8(dY)
+
+            def call():
+                return sparse_matmul.AspRelu2B(qd.T, sp, A_scale=sd)
+            peak, dt = MFMA_FP8_PEAK_TFLOPS, "fp8 e4m3 x e4m3, fp32 accumulate"
         else:
             sp = dense_to_tilesparse(h, None)
-        dense = torch.empty((K, N), device=dev, dtype=torch.bfloat16)
-        nt = sp.grid_m * sp.grid_n
 
-        def lds():
-            return dw_gemm.gemm_compressed_b(A, sp, square=relu2_fp8)
-
-        def ref():
-            if relu2_fp8:
-                unpack_relu2_batch_(sp, dense, 0, sp.grid_n, N, K, nt)
-            else:
-                unpack_batch_(sp, dense, 0, sp.grid_n, N, K, nt)
-            return A @ dense
-
-        t_lds = _timed(lds, steps, warmup)
-        t_ref = _timed(ref, steps, warmup)
+            def call():
+                return sparse_matmul.AspB(dY.T, sp)
+            peak, dt = MFMA_BF16_PEAK_TFLOPS, "bf16, fp32 accumulate"
+        t_lds = _timed(call, steps, warmup)
+        sparse_matmul.USE_LDS_GEMM = False
+        try:
+            t_ref = _timed(call, steps, warmup)
+        finally:
+            sparse_matmul.USE_LDS_GEMM = True
         flop = 2.0 * M * N * K
         tf = flop / (t_lds * 1e9)
-        out[name] = {"M": M, "K": K, "N": N,
+        out[name] = {"M": M, "K": K, "N": N, "dtype": dt,
                      "operand": "relu^2 (e4m3fn storage)" if relu2_fp8 else "relu (bf16 storage)",
                      "sparsity": round(1 - int(sp.prefix[-1].item()) / (K * N), 4),
                      "lds_gemm_ms": round(t_lds, 4), "lds_gemm_tflops": round(tf, 1),
-                     "mfma_frac_of_bf16_peak": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
-                     "decompress_plus_hipblaslt_ms": round(t_ref, 4)}
-        del h, dY, dense, sp
+                     "mfma_frac_of_peak": round(tf / peak, 4), "mfma_peak_tflops": peak,
+                     "decompress_plus_library_gemm_ms": round(t_ref, 4),
+                     "speedup_over_library_path": round(t_ref / t_lds, 3)}
+        del h, dY, sp
     return out
 
 
@@ -311,14 +316,20 @@ def bench_mlp(steps: int, warmup: int):
     dY = torch.randn((8, 1024, D), device=dev, generator=g).to(torch.bfloat16)
     buf = TensorBuffer(2 * B * H, device=dev)
 
-    def run(compressed: bool, ev=None):
+    from bitsparse_amd import layers
+
+    def run(mode: str, ev=None):
         for p in (x, W1, W2):
             p.grad = None
         if ev is not None:
             ev[0].record()
-        if compressed:
+        if mode != "dense":
             buf.reset_buffer()
-            y = FFNRelu.apply(x, W1, W2, sparse_data=buf)
+            layers.USE_FUSED_UP = mode == "compressed_fused_up"
+            try:
+                y = FFNRelu.apply(x, W1, W2, sparse_data=buf)
+            finally:
+                layers.USE_FUSED_UP = False
         else:
             y = DenseFFNRelu.apply(x.reshape(-1, D), W1, W2).reshape(8, 1024, D)
         if ev is not None:
@@ -328,20 +339,23 @@ def bench_mlp(steps: int, warmup: int):
             ev[2].record()
 
     out = {}
-    for mode in ("dense", "compressed"):
-        comp = mode == "compressed"
+    # compressed: library GEMM for z, then the ReLU + compress kernel;
+    # compressed_fused_up: z, ReLU and compress from one kernel
+    # (bs_linear_relu_compress, layers.USE_FUSED_UP)
+    for mode in ("dense", "compressed", "compressed_fused_up"):
         for _ in range(warmup):
-            run(comp)
+            run(mode)
         torch.cuda.synchronize()
         evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
         for i in range(steps):
-            run(comp, evs[i])
+            run(mode, evs[i])
         torch.cuda.synchronize()
         out[mode] = {
             "step_ms": sum(e[0].elapsed_time(e[2]) for e in evs) / steps,
             "fwd_ms": sum(e[0].elapsed_time(e[1]) for e in evs) / steps,
             "bwd_ms": sum(e[1].elapsed_time(e[2]) for e in evs) / steps,
         }
+    out["fwd_ratio_fused_up_over_compressed"] = out["compressed_fused_up"]["fwd_ms"] / out["compressed"]["fwd_ms"]
     # saved activation bytes (reference BitsparseTensor.vram_size definition)
     from bitsparse_amd.src.functions import dense_to_tilesparse
     with torch.no_grad():
@@ -549,42 +563,72 @@ def bench_stack(steps: int, warmup: int):
     return out
 
 
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline_codec(N: int, mu: float, budget_s: float = 12.0):
-    """C oracle compress + decompress (one thread) on row blocks of the
-    workload's distribution, repeated for about `budget_s` seconds."""
+    """C oracle compress + decompress on row blocks of the workload's
+    distribution, one block per host thread (the ctypes calls release the
+    GIL), repeated for about `budget_s` seconds.  Threads: every core the
+    process may use, capped by OMP_NUM_THREADS (the GPU box's CPU share)."""
+    import concurrent.futures as cf
     import numpy as np
     import torch
     from oracle import oracle as O
 
+    ncpu = os.cpu_count() or 1
+    threads = max(1, min(ncpu, int(os.environ.get("OMP_NUM_THREADS", ncpu))))
     rows = 1024
     g = torch.Generator().manual_seed(0)
     x = (torch.randn((rows, N), generator=g) + mu).to(torch.bfloat16).relu_()
     xb = x.view(torch.int16).numpy().view(np.uint16)
     T = (rows // 64) * ((N + 63) // 64)
-    bm = np.zeros(T * 512, np.uint8)
-    pf = np.zeros(T + 1, np.uint32)
-    cnt = np.zeros(T, np.int32)
-    vals = np.zeros(rows * N, np.uint16)
-    reps, t_c, t_d = 0, 0.0, 0.0
-    nnz = 0
-    t_start = time.perf_counter()
-    while time.perf_counter() - t_start < budget_s or reps < 2:
-        a = time.perf_counter()
-        nnz = O.compress_timed_call(xb, O.BF16, bm, pf, cnt, vals)
-        b = time.perf_counter()
-        out = O.decompress(vals, O.BF16, bm, pf, rows, N)
-        c = time.perf_counter()
-        t_c += b - a
-        t_d += c - b
-        reps += 1
-    assert (out == xb).all()
+    O.lib()                                  # build / load once, before the threads
+
+    def worker(_):
+        bm = np.zeros(T * 512, np.uint8)
+        pf = np.zeros(T + 1, np.uint32)
+        cnt = np.zeros(T, np.int32)
+        vals = np.zeros(rows * N, np.uint16)
+        reps, t_c, t_d, nnz, ok = 0, 0.0, 0.0, 0, True
+        t_start = time.perf_counter()
+        while time.perf_counter() - t_start < budget_s or reps < 2:
+            a = time.perf_counter()
+            nnz = O.compress_timed_call(xb, O.BF16, bm, pf, cnt, vals)
+            b = time.perf_counter()
+            out = O.decompress(vals, O.BF16, bm, pf, rows, N)
+            c = time.perf_counter()
+            t_c += b - a
+            t_d += c - b
+            reps += 1
+        ok = bool((out == xb).all())
+        return reps, t_c, t_d, nnz, ok
+
+    t0 = time.perf_counter()
+    with cf.ThreadPoolExecutor(threads) as ex:
+        res = list(ex.map(worker, range(threads)))
+    wall = time.perf_counter() - t0
+    assert all(r[4] for r in res)
+    nnz = res[0][3]
+    reps = sum(r[0] for r in res)
     cb, db = codec_bytes(rows, N, nnz)
-    return {"value": round((cb + db) * reps / ((t_c + t_d) * 1e9), 4), "unit": "GB/s",
-            "cores": 1, "kind": "port",
-            "sample": f"{rows}x{N} row block (seed 0), {reps} compress+decompress reps, "
-                      f"C oracle -O2 single thread",
-            "compress_gbs": round(cb * reps / (t_c * 1e9), 4),
-            "decompress_gbs": round(db * reps / (t_d * 1e9), 4)}
+    t_c = sum(r[1] for r in res)
+    t_d = sum(r[2] for r in res)
+    return {"value": round((cb + db) * reps / (wall * 1e9), 4), "unit": "GB/s",
+            "cores": threads, "kind": "port",
+            "sample": f"{rows}x{N} row block (seed 0) per thread, {reps} compress+decompress reps over "
+                      f"{threads} threads in {wall:.1f} s, C oracle -O2",
+            "os_cpu_count": ncpu, "torch_threads": torch.get_num_threads(), "cpu_model": _cpu_model(),
+            "per_thread_compress_gbs": round(cb * reps / (t_c * 1e9), 4),
+            "per_thread_decompress_gbs": round(db * reps / (t_d * 1e9), 4)}
 
 
 def cpu_baseline_mlp(budget_s: float = 15.0):

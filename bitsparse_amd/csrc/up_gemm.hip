@@ -54,11 +54,11 @@ constexpr int kUpAStage = kUpBM * 128;                  // x slab: 256 rows x 64
 constexpr int kUpBStage = kUpBN * 128;                  // W slab: 192 rows x 64 k bf16
 constexpr int kUpMainLds = 2 * (kUpAStage + kUpBStage);
 constexpr int kUpHP = kUpBN * 2 + 16;                   // staged h row pitch, bytes
-constexpr int kUpRunElems = kTileNumel + 16;            // per-wave compaction run (+ phase, + tail)
-constexpr int kUpOffRun = kUpBM * kUpHP;
-constexpr int kUpOffSel = kUpOffRun + 4 * kUpRunElems * 2;
+constexpr int kUpOffSel = kUpMainLds > kUpBM * kUpHP ? kUpMainLds : kUpBM * kUpHP;
 constexpr int kUpLds = kUpOffSel + 256 * 32;            // + compaction selectors (8 dwords per mask byte)
-static_assert(kUpMainLds <= kUpOffSel, "the selectors are written before the main loop");
+// a unit's compacted run (phase <= 7, three tiles, the 8-element write
+// overrun) fits in the wave's 64 staged rows, where it is built
+static_assert(2 * (7 + kUpTiles * kTileNumel + 8) <= 64 * kUpHP, "unit run");
 static_assert(kUpLds <= 160 * 1024, "LDS budget");
 constexpr int64_t kUpMaxNB = 128;
 
@@ -96,9 +96,11 @@ __device__ __forceinline__ uint32_t relu_bf16_bits(uint32_t b) { return (b - 0x8
 constexpr uint64_t kUpLookbackGiveUpTicks = 2000000;
 
 // Exclusive prefix of unit u from the status words of units 0 .. u-1.  Each
-// read covers 256 units: lane j takes units pos - 4j .. pos - 4j - 3, nearest
-// first, and the walk sums values back to the nearest inclusive prefix; it
-// re-reads while a word it needs is unpublished.
+// read covers kUpLbWords * 64 units: lane j
+// takes units pos - kUpLbWords j - i, i < kUpLbWords, nearest first, and the
+// walk sums values back to the nearest inclusive prefix; it re-reads while a
+// word it needs is unpublished.
+constexpr int kUpLbWords = 4;
 __device__ uint32_t up_lookback(const UpArgs& a, uint32_t u, int lane)
 {
     uint32_t excl = 0;
@@ -108,8 +110,8 @@ __device__ uint32_t up_lookback(const UpArgs& a, uint32_t u, int lane)
         uint32_t sum = 0;
         bool unpub = false, inc = false;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int64_t q = pos - 4 * lane - i;
+        for (int i = 0; i < kUpLbWords; i++) {
+            const int64_t q = pos - kUpLbWords * lane - i;
             const uint64_t s = q >= 0 ? ld_relaxed(&a.status[q]) : pack_status(a.epoch, kFlagInc, 0u);
             const uint32_t flag = (uint32_t)(s >> 34) == a.epoch ? (uint32_t)(s >> 32) & 3u : 0u;
             if (!inc) {                  // words up to the lane's nearest inclusive prefix
@@ -131,7 +133,7 @@ __device__ uint32_t up_lookback(const UpArgs& a, uint32_t u, int lane)
         }
         excl += wave_sum_u32(lane <= first ? sum : 0u);
         if (incs) break;
-        pos -= 256;
+        pos -= 64 * kUpLbWords;
     }
     return excl;
 }
@@ -307,29 +309,46 @@ __global__ __launch_bounds__(256, 1) void up_relu_compress_kernel(UpArgs a)
         const int rows_in = (int)std::min<int64_t>(kUpBM, a.M - m0);
         typedef float f32x2_t __attribute__((ext_vector_type(2)));
         typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+        typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+        // relu of two bf16 halves with packed 16-bit arithmetic: a half is
+        // kept iff (bits - 0x8000) mod 2^16 >= 0x7f81 (positive or NaN), i.e.
+        // iff the saturating (bits - 0x8000) - 0x7f80 is nonzero; `in` (1 or
+        // 0 per half) also zeroes elements outside the matrix
+        auto relu2x = [](uint32_t hp, u16x2_t in) __attribute__((always_inline)) {
+            const u16x2_t h = __builtin_bit_cast(u16x2_t, hp);
+            const u16x2_t keep = __builtin_elementwise_min(
+                __builtin_elementwise_sub_sat((u16x2_t)(h - (u16x2_t)(0x8000)), (u16x2_t)(0x7f80)), in);
+            return __builtin_bit_cast(uint32_t, (u16x2_t)(h * keep));
+        };
+        auto stage = [&](auto BOUNDS) __attribute__((always_inline)) {
+            constexpr bool BD = decltype(BOUNDS)::value;
 #pragma unroll
-        for (int j = 0; j < kUpJN; j++) {
-            const int col = wn * 96 + 32 * j + fl;
-            const bool cin = n0 + col < a.N;
-            const float bj = (a.bias != nullptr && cin) ? bf16_to_f32(a.bias[n0 + col]) : 0.0f;
-            uint8_t* cp = hs + col * 2;
+            for (int j = 0; j < kUpJN; j++) {
+                const int col = wn * 96 + 32 * j + fl;
+                const bool cin = n0 + col < a.N;
+                const float bj = (a.bias != nullptr && cin) ? bf16_to_f32(a.bias[n0 + col]) : 0.0f;
+                uint8_t* cp = hs + col * 2;
 #pragma unroll
-            for (int i = 0; i < kUpIM; i++) {
+                for (int i = 0; i < kUpIM; i++) {
 #pragma unroll
-                for (int r = 0; r < 16; r += 2) {
-                    const int row = wm * 128 + 32 * i + 8 * (r >> 2) + rq + (r & 3);
-                    const uint32_t zp = __builtin_bit_cast(
-                        uint32_t, __builtin_convertvector(f32x2_t{acc[i][j][r], acc[i][j][r + 1]}, bf16x2_t));
-                    const f32x2_t zb = {__uint_as_float(zp << 16) + bj, __uint_as_float(zp & 0xffff0000u) + bj};
-                    const uint32_t hp = __builtin_bit_cast(uint32_t, __builtin_convertvector(zb, bf16x2_t));
-                    uint32_t h0 = relu_bf16_bits(hp & 0xffffu), h1 = relu_bf16_bits(hp >> 16);
-                    h0 = (cin && row < rows_in) ? h0 : 0u;
-                    h1 = (cin && row + 1 < rows_in) ? h1 : 0u;
-                    *reinterpret_cast<uint16_t*>(cp + row * kUpHP) = (uint16_t)h0;
-                    *reinterpret_cast<uint16_t*>(cp + (row + 1) * kUpHP) = (uint16_t)h1;
+                    for (int r = 0; r < 16; r += 2) {
+                        const int row = wm * 128 + 32 * i + 8 * (r >> 2) + rq + (r & 3);
+                        const uint32_t zp = __builtin_bit_cast(
+                            uint32_t, __builtin_convertvector(f32x2_t{acc[i][j][r], acc[i][j][r + 1]}, bf16x2_t));
+                        const f32x2_t zb = {__uint_as_float(zp << 16) + bj, __uint_as_float(zp & 0xffff0000u) + bj};
+                        const uint32_t hp = __builtin_bit_cast(uint32_t, __builtin_convertvector(zb, bf16x2_t));
+                        u16x2_t in = (u16x2_t)(1);
+                        if constexpr (BD)
+                            in = u16x2_t{(unsigned short)(cin && row < rows_in), (unsigned short)(cin && row + 1 < rows_in)};
+                        const uint32_t h2 = relu2x(hp, in);
+                        *reinterpret_cast<uint16_t*>(cp + row * kUpHP) = (uint16_t)h2;
+                        *reinterpret_cast<uint16_t*>(cp + (row + 1) * kUpHP) = (uint16_t)(h2 >> 16);
+                    }
                 }
             }
-        }
+        };
+        if (rows_in == kUpBM && n0 + kUpBN <= a.N) stage(IC<false>{});
+        else stage(IC<true>{});
     }
     __syncthreads();
 
@@ -345,6 +364,7 @@ __global__ __launch_bounds__(256, 1) void up_relu_compress_kernel(UpArgs a)
     const int ntiles = (int)std::min<uint32_t>((uint32_t)kUpTiles, a.grid_n - cb * (uint32_t)kUpTiles);
     const int lrow = lane >> 3, lcol = (lane & 7) * 16;   // byte offset of the lane's chunk in a tile row
     uint32_t mk[kUpTiles][2];                           // the 8 mask bytes of each tile, 4 per register
+    uint4 hv[kUpTiles][8];                              // the lane's chunks, reused by the compaction
     uint32_t tcnt[kUpTiles], toff[kUpTiles + 1];
     toff[0] = 0;
 #pragma unroll
@@ -355,6 +375,7 @@ __global__ __launch_bounds__(256, 1) void up_relu_compress_kernel(UpArgs a)
 #pragma unroll
             for (int k = 0; k < 8; k++) {
                 const uint4 v = *reinterpret_cast<const uint4*>(hw + (8 * k + lrow) * kUpHP + tt * 128 + lcol);
+                hv[tt][k] = v;
                 const uint32_t m = mask_bf16x8_pk(v);
                 a.bitmask[(size_t)(t0 + tt) * kTileBytes + 64 * k + lane] = (uint8_t)m;
                 mk[tt][k >> 2] |= m << (8 * (k & 3));
@@ -382,9 +403,44 @@ __global__ __launch_bounds__(256, 1) void up_relu_compress_kernel(UpArgs a)
     }
 
 
+    // ---- values, first into LDS: the unit's runs are consecutive in vals,
+    // so the wave compacts all of them into one run at phase 0 -- in its own
+    // 64 staged rows, whose values it holds in registers and whose h stores
+    // have read them.  This needs no offset, so the preceding units have
+    // this long to publish before the look-back below.
+    uint16_t* run = reinterpret_cast<uint16_t*>(hs + wave * 64 * kUpHP);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int tt = 0; tt < kUpTiles; tt++) {
+        if (tt >= ntiles) break;
+        uint32_t P = toff[tt];                          // offset of round k in the unit's run
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const uint32_t m = (mk[tt][k >> 2] >> (8 * (k & 3))) & 0xffu;
+            const uint32_t c = (uint32_t)__popc(m);
+            const uint32_t incl = wave_incl_scan(c);
+            const uint32_t ex = incl - c;
+            const uint32_t base = P;
+            P += (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+            if (c != 0u) {
+                const uint4 w = hv[tt][k];
+                const uint4 s0 = *reinterpret_cast<const uint4*>(&sel_s[m * 8]);
+                const uint4 s1 = *reinterpret_cast<const uint4*>(&sel_s[m * 8 + 4]);
+                uint4 o;
+                o.x = __builtin_amdgcn_perm(w.y, w.x, s0.x) | __builtin_amdgcn_perm(w.w, w.z, s1.x);
+                o.y = __builtin_amdgcn_perm(w.y, w.x, s0.y) | __builtin_amdgcn_perm(w.w, w.z, s1.y);
+                o.z = __builtin_amdgcn_perm(w.y, w.x, s0.z) | __builtin_amdgcn_perm(w.w, w.z, s1.z);
+                o.w = __builtin_amdgcn_perm(w.y, w.x, s0.w) | __builtin_amdgcn_perm(w.w, w.z, s1.w);
+                write_compacted<2>(reinterpret_cast<uint8_t*>(run + (int)base + (int)ex), o);
+            }
+        }
+    }
+
+    // ---- offset: look-back, prefix entries, cursor and flags
     int64_t start = a.offset_in ? *a.offset_in : 0;
     if (a.align8) start = (start + 7) & ~(int64_t)7;
-
     uint32_t excl = 0;
     if (u != 0) {
         excl = up_lookback(a, u, lane);
@@ -404,56 +460,43 @@ __global__ __launch_bounds__(256, 1) void up_relu_compress_kernel(UpArgs a)
     }
     if (start < 0) return;
 
-    // ---- values, tile by tile: compact into the wave's run (phase a0 = the
-    // run's start modulo 8 elements, so run slot j is the 16-byte vals slot
-    // holding elements g - a0 + 8 j .. +7), then store the slots
-    uint16_t* run = reinterpret_cast<uint16_t*>(lds + kUpOffRun) + wave * kUpRunElems;
+    // ---- values out: run element p is vals element g + p.  16-byte vals
+    // slot j holds elements g - a0 + 8 j .. +7 (a0 = g mod 8), run elements
+    // 8 j - a0 .. +7: its 16 bytes start at run byte 16 j - 2 a0, inside the
+    // 8-byte-aligned 24 bytes from (16 j - 2 a0) & ~7, at byte offset
+    // (-2 a0) mod 8 (the same for every slot).  Partial slots at the two ends
+    // take element stores; elements past the capacity are not written.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int64_t g = start + (int64_t)excl;
+    const int a0 = (int)(g & 7);
+    const int64_t room = a.vals_capacity - g;
+    const int endr = (int)std::max<int64_t>(0, std::min<int64_t>((int64_t)unit_total, room));
+    const int nslots = (a0 + endr + 7) >> 3;
+    uint16_t* const vbase = a.vals + (g - a0);             // 16-byte aligned
+    const uint32_t off = (uint32_t)((8 - 2 * a0) & 7);     // byte offset in the window
+    const uint8_t* runb = reinterpret_cast<const uint8_t*>(run);
+    for (int j = lane; j < nslots; j += 64) {
+        const int lo = std::max(8 * j, a0), hi = std::min(8 * j + 8, a0 + endr);
+        if (lo == 8 * j && hi == 8 * j + 8) {
+            const uint8_t* wp = runb + ((16 * j - 2 * a0) & ~7);
+            const uint2 q0 = *reinterpret_cast<const uint2*>(wp);
+            const uint2 q1 = *reinterpret_cast<const uint2*>(wp + 8);
+            const uint2 q2 = *reinterpret_cast<const uint2*>(wp + 16);
+            const uint32_t d[6] = {q0.x, q0.y, q1.x, q1.y, q2.x, q2.y};
+            uint32_t o[4];
+            if (off >= 4) {
 #pragma unroll
-    for (int tt = 0; tt < kUpTiles; tt++) {
-        if (tt >= ntiles) break;
-        const int64_t g = start + (int64_t)excl + (int64_t)toff[tt];
-        const int cnt = (int)tcnt[tt];
-        const int a0 = (int)(g & 7);
-        uint32_t P = 0;                                 // offset of round k in the tile's run
-#pragma unroll
-        for (int k = 0; k < 8; k++) {
-            const uint32_t m = (mk[tt][k >> 2] >> (8 * (k & 3))) & 0xffu;
-            const uint32_t c = (uint32_t)__popc(m);
-            const uint32_t incl = wave_incl_scan(c);
-            const uint32_t ex = incl - c;
-            const uint32_t base = P;
-            P += (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
-            if (c != 0u) {
-                const uint4 w = *reinterpret_cast<const uint4*>(hw + (8 * k + lrow) * kUpHP + tt * 128 + lcol);
-                const uint4 s0 = *reinterpret_cast<const uint4*>(&sel_s[m * 8]);
-                const uint4 s1 = *reinterpret_cast<const uint4*>(&sel_s[m * 8 + 4]);
-                uint4 o;
-                o.x = __builtin_amdgcn_perm(w.y, w.x, s0.x) | __builtin_amdgcn_perm(w.w, w.z, s1.x);
-                o.y = __builtin_amdgcn_perm(w.y, w.x, s0.y) | __builtin_amdgcn_perm(w.w, w.z, s1.y);
-                o.z = __builtin_amdgcn_perm(w.y, w.x, s0.z) | __builtin_amdgcn_perm(w.w, w.z, s1.z);
-                o.w = __builtin_amdgcn_perm(w.y, w.x, s0.w) | __builtin_amdgcn_perm(w.w, w.z, s1.w);
-                write_compacted<2>(reinterpret_cast<uint8_t*>(run + a0 + (int)base + (int)ex), o);
-            }
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        // elements past the capacity are not written (flagged above)
-        const int64_t room = a.vals_capacity - g;
-        const int endr = (int)std::max<int64_t>(0, std::min<int64_t>((int64_t)cnt, room));
-        const int nslots = (a0 + endr + 7) >> 3;
-        uint16_t* const base = a.vals + (g - a0);          // 16-byte aligned
-        for (int j = lane; j < nslots; j += 64) {
-            const int lo = std::max(8 * j, a0), hi = std::min(8 * j + 8, a0 + endr);
-            if (lo == 8 * j && hi == 8 * j + 8) {
-                *reinterpret_cast<uint4*>(base + 8 * j) = *reinterpret_cast<const uint4*>(run + 8 * j);
+                for (int i = 0; i < 4; i++) o[i] = __builtin_amdgcn_alignbyte(d[i + 2], d[i + 1], off - 4);
             } else {
-                for (int e = lo; e < hi; e++) base[e] = run[e];
+#pragma unroll
+                for (int i = 0; i < 4; i++) o[i] = __builtin_amdgcn_alignbyte(d[i + 1], d[i], off);
             }
+            *reinterpret_cast<uint4*>(vbase + 8 * j) = uint4{o[0], o[1], o[2], o[3]};
+        } else {
+            for (int e = lo; e < hi; e++) vbase[e] = run[e - a0];
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
 }
 
