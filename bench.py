@@ -700,6 +700,11 @@ def main() -> int:
     ap.add_argument("--packed-only", action="store_true",
                     help="run only the packed-stream (pack_sbit) sweep cases and print their JSON "
                          "(profiling entry point)")
+    ap.add_argument("--mlp-only", action="store_true",
+                    help="run only the configs[1] MLP section (dense, compressed, fused up-projection) "
+                         "and print its JSON (profiling entry point)")
+    ap.add_argument("--sweep-only", action="store_true",
+                    help="run only the configs[2] sparsity sweep and print its JSON (profiling entry point)")
     ap.add_argument("--kernels-only", action="store_true",
                     help="run only the gradient / unpack / fp8 kernel section and print its JSON "
                          "(profiling entry point)")
@@ -718,8 +723,22 @@ def main() -> int:
     from bitsparse_amd import _lib
     _lib.load()
 
+    if args.calibrate_copy and (args.gemm_only or args.mlp_only or args.sweep_only or args.packed_only):
+        # a 1 GiB device copy: the reference of the rocprof byte counters
+        src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     if args.gemm_only:
         print(json.dumps({"gemm": bench_gemm(args.steps, args.warmup)}), flush=True)
+        return 0
+    if args.mlp_only:
+        print(json.dumps({"mlp": bench_mlp(args.steps, args.warmup)}), flush=True)
+        return 0
+    if args.sweep_only:
+        print(json.dumps({"sweep": bench_sweep(args.steps, args.warmup)}), flush=True)
         return 0
     if args.packed_only:
         print(json.dumps({"sweep": bench_sweep(args.steps, args.warmup, packed_only=True)}), flush=True)
