@@ -111,6 +111,35 @@ __device__ __forceinline__ uint2 quant_chunk(const uint4 v, float scale, float r
     return uint2{p[0] | (p[1] << 16), p[2] | (p[3] << 16)};
 }
 
+// The quantizer through a code table: for a fixed scale, f32_to_e4m3(x / s)
+// of a bf16 x depends only on x's 15 magnitude bits (RNE and the NaN rule
+// are symmetric, so the sign bit is x's), so qtab[m] = f32_to_e4m3(m / s)
+// for the 32,768 magnitudes gives every code with one LDS byte read.
+constexpr int kQtabEntries = 1 << 15;
+
+__device__ __forceinline__ uint32_t qtab_code(const uint8_t* qtab, uint32_t b16)
+{
+    return (uint32_t)qtab[b16 & 0x7fffu] | ((b16 >> 8) & 0x80u);
+}
+
+__device__ __forceinline__ uint2 quant_chunk_tab(const uint4 v, const uint8_t* qtab)
+{
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    uint32_t p[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) p[k] = qtab_code(qtab, w[k] & 0xffffu) | (qtab_code(qtab, w[k] >> 16) << 8);
+    return uint2{p[0] | (p[1] << 16), p[2] | (p[3] << 16)};
+}
+
+// qtab[m] = f32_to_e4m3(bf16(m) / scale), scale from the amax slot (one
+// correctly rounded division per entry: the quantizer's own rule)
+__global__ __launch_bounds__(256) void qtab_build_kernel(const uint64_t* slot, uint32_t epoch, uint8_t* qtab)
+{
+    const uint32_t m = blockIdx.x * 256 + threadIdx.x;
+    const float scale = scale_from_slot(slot, epoch);
+    if (m < (uint32_t)kQtabEntries) qtab[m] = (uint8_t)f32_to_e4m3(bf16_to_f32(m) / scale);
+}
+
 // Chunk geometry inside tile t of a [*, N] matrix.
 __device__ __forceinline__ void chunk_pos(uint32_t t, uint32_t grid_n, int b, int64_t& row,
                                           int64_t& col0)
@@ -152,6 +181,7 @@ struct CompressArgs {
     int32_t* err;
     uint32_t* fallbacks;
     uint64_t patience;          // look-back wait (s_memrealtime ticks) before counting a unit itself
+    const uint8_t* qtab;        // quantize: the code table (kQtabEntries bytes), copied into LDS
 };
 
 // 200 us at the 100 MHz s_memrealtime clock: waiting longer than this for a
@@ -171,13 +201,15 @@ struct CompressTraits {
 };
 
 // Positive-bit byte of a loaded chunk (after quantisation when QUANT).
-template <int IN_T, bool QUANT>
+// TAB: quantize through the code table `qtab` (LDS) instead of dividing.
+template <int IN_T, bool QUANT, bool TAB = false>
 __device__ __forceinline__ uint32_t chunk_mask(const typename Raw<CompressTraits<IN_T, QUANT>::INB>::T& d,
                                                typename Raw<CompressTraits<IN_T, QUANT>::OUTB>::T& o,
-                                               float scale, float rcp)
+                                               float scale, float rcp, const uint8_t* qtab = nullptr)
 {
     if constexpr (QUANT) {
-        o = quant_chunk(d, scale, rcp);
+        if constexpr (TAB) o = quant_chunk_tab(d, qtab);
+        else o = quant_chunk(d, scale, rcp);
         return mask_fp8x8<DT_E4M3FN>(o);
     } else if constexpr (IN_T == DT_BF16) {
         o = d;
@@ -188,16 +220,16 @@ __device__ __forceinline__ uint32_t chunk_mask(const typename Raw<CompressTraits
     }
 }
 
-template <int IN_T, bool QUANT>
+template <int IN_T, bool QUANT, bool TAB = false>
 __device__ __forceinline__ uint32_t stream_chunk_mask(const typename Raw<CompressTraits<IN_T, QUANT>::INB>::T& d,
                                                       typename Raw<CompressTraits<IN_T, QUANT>::OUTB>::T& o,
-                                                      float scale, float rcp)
+                                                      float scale, float rcp, const uint8_t* qtab = nullptr)
 {
     if constexpr (IN_T == DT_BF16 && !QUANT) {
         o = d;
         return mask_bf16x8_pk(d);
     } else {
-        return chunk_mask<IN_T, QUANT>(d, o, scale, rcp);
+        return chunk_mask<IN_T, QUANT, TAB>(d, o, scale, rcp, qtab);
     }
 }
 
@@ -583,11 +615,13 @@ void compress_stream_kernel(CompressArgs a)
     __shared__ uint32_t s_excl[1];
     __shared__ __align__(16) uint8_t s_ring[WRITE_VALS ? U * kRingElems * OUTB : 16];
     __shared__ __align__(16) uint32_t s_sel[WRITE_VALS ? 256 * NSEL : 4];
+    __shared__ __align__(16) uint8_t s_qtab[QUANT ? kQtabEntries : 16];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     if constexpr (PACKED) {
         if (tid <= U) s_edge[tid] = 0u;
     }
+
     if constexpr (WRITE_VALS) {
         if (tid < 256) {
             uint32_t sel[NSEL];
@@ -637,6 +671,12 @@ void compress_stream_kernel(CompressArgs a)
             }
             if constexpr (MODE == MODE_VALS) vm[k] = a.bitmask[(size_t)tc * kTileBytes + 64 * k + lane];
         }
+        if constexpr (QUANT) {
+            // the code table into LDS, behind the dense loads (16-byte copies)
+            for (int i = tid; i < kQtabEntries / 16; i += 64 * U)
+                reinterpret_cast<uint4*>(s_qtab)[i] = reinterpret_cast<const uint4*>(a.qtab)[i];
+            __syncthreads();
+        }
         if constexpr (MODE != MODE_VALS) {
             if (a.relu) {
 #pragma unroll
@@ -656,7 +696,8 @@ void compress_stream_kernel(CompressArgs a)
                 o[k] = d[k];
                 m = tile_ok ? vm[k] & 0xffu : 0u;
             } else {
-                m = stream_chunk_mask<IN_T, QUANT>(d[k], o[k], scale, rcp) & (8 * k < rows_in ? 0xffu : 0u);
+                m = stream_chunk_mask<IN_T, QUANT, QUANT>(d[k], o[k], scale, rcp, s_qtab) &
+                    (8 * k < rows_in ? 0xffu : 0u);
                 if (tile_ok) {
                     if (a.relu_out != nullptr)
                         store_chunk<INB, VEC>(a.relu_out, a.M, a.N, row0 + 8 * k, col0, d[k]);
@@ -1621,13 +1662,17 @@ static hipError_t launch_compress(const CompressArgs& a, int in_dtype, bool quan
 
 using namespace bs;
 
+// The quantizer's code table sits after the status words (256-byte aligned).
+static int64_t ws_qtab_offset(int64_t T) { return (kWsHeaderBytes + 8 * (T + 2) + 255) / 256 * 256; }
+
 extern "C" int64_t bs_compress_workspace_bytes(int64_t M, int64_t N)
 {
     if (M < 0 || N < 0) return -1;
     int64_t T = ((M + 63) / 64) * ((N + 63) / 64);
     // status words: one per tile covers the units and the unit groups of the
-    // streaming kernel (T/8 + T/512 words) and the units of the others
-    return kWsHeaderBytes + 8 * (T + 2);
+    // streaming kernel (T/8 + T/512 words) and the units of the others; then
+    // the quantizer's code table
+    return ws_qtab_offset(T) + kQtabEntries;
 }
 
 extern "C" const uint64_t* bs_workspace_amax_slot(const void* ws, int64_t)
@@ -1746,6 +1791,12 @@ static int compress_impl(const void* dense, int in_dtype, int64_t M, int64_t N, 
         if (end != ev) a.patience = (uint64_t)v;
     }
     a.gstat = a.status + (T + kStreamU - 1) / kStreamU;
+    if (quantize) {
+        // the code table of this call's scale, built after the amax it reads
+        uint8_t* qtab = (uint8_t*)workspace + ws_qtab_offset(T);
+        hipLaunchKernelGGL(qtab_build_kernel, dim3(kQtabEntries / 256), dim3(256), 0, st, amax_slot, amax_epoch, qtab);
+        a.qtab = qtab;
+    }
     const int inb = in_dtype == DT_BF16 ? 2 : 1;
     bool vec = (N % 8 == 0) && (((uintptr_t)dense) % (8 * inb) == 0) &&
                (dense_q_out == nullptr || aligned8(dense_q_out)) &&
@@ -2163,7 +2214,7 @@ extern "C" int bs_pack_bits(const void* raw, int vals_dtype, const uint32_t* cou
 namespace bs {
 
 constexpr int64_t kScratchMaxTiles = int64_t(1) << 19;                 // 2^31 elements in 64x64 tiles (half the codec range)
-constexpr int64_t kScratchBytes = kWsHeaderBytes + 8 * (kScratchMaxTiles + 2);
+constexpr int64_t kScratchBytes = (kWsHeaderBytes + 8 * (kScratchMaxTiles + 2) + 255) / 256 * 256 + kQtabEntries;
 constexpr int kScratchMaxDevices = 64;
 
 // One copy per GPU, held until the process ends.  Host code never uses this
