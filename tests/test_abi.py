@@ -31,9 +31,13 @@ def test_library_exports_every_declared_symbol():
 def test_abi_version_and_workspace_size():
     L = _lib.load()
     assert L.bs_abi_version() == _lib.ABI_VERSION
-    assert L.bs_compress_workspace_bytes(4096, 4096) == 256 + 8 * (4096 + 2)
-    assert L.bs_compress_workspace_bytes(129, 131) == 256 + 8 * (9 + 2)
-    assert L.bs_compress_workspace_bytes(0, 0) == 256 + 8 * 2
+    # header + one status word per tile (+2), rounded up to 256 bytes, then the
+    # quantizer's 32 KiB code table
+    def want(T):
+        return (256 + 8 * (T + 2) + 255) // 256 * 256 + 32768
+    assert L.bs_compress_workspace_bytes(4096, 4096) == want(4096)
+    assert L.bs_compress_workspace_bytes(129, 131) == want(9)
+    assert L.bs_compress_workspace_bytes(0, 0) == want(0)
 
 
 def test_nontemporal_threshold_round_trip():
