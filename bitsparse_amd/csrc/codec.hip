@@ -1608,7 +1608,10 @@ __global__ void empty_compress_kernel(uint32_t* prefix, const int64_t* offset_in
 // host launchers
 // ===========================================================================
 // compress unit: tiles per workgroup and workgroup size
-constexpr int kGatherU = 2;
+#ifndef BS_GATHER_U
+#define BS_GATHER_U 2
+#endif
+constexpr int kGatherU = BS_GATHER_U;
 // adjacent tile pairs per workgroup of the plain fp8 decompress
 #ifndef BS_FP8_PAIRS
 #define BS_FP8_PAIRS 2

@@ -81,9 +81,8 @@ struct Gemm8Cfg {
     static_assert(NWAVES % NT == 0 && 8 % DW == 0 && SEG % CH == 0, "decode split");
     static_assert(BP % 256 == 32 || BP % 256 == 160, "fragment-read bank spread");
 };
-// 4 x 1 waves of 128 x 128 (one per SIMD, accumulators in AGPRs): each
-// decoded B byte feeds 512 rows.  (8 x 1 waves of 64 x 128, two per SIMD, cap a
-// wave at 256 registers and spill.)
+// 8 x 1 waves of 64 x 128 (two per SIMD, 128 VGPRs + 128 AGPRs each, the
+// accumulators in the AGPRs): each decoded B byte feeds 512 rows.
 using Cfg8_512 = Gemm8Cfg<8, 1, 64, 128>;
 // 2 x 2 waves of 128 x 128 (one per SIMD)
 using Cfg8_256 = Gemm8Cfg<2, 2, 128, 128>;
