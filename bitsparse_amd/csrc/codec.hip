@@ -617,7 +617,10 @@ void compress_stream_kernel(CompressArgs a)
     __shared__ __align__(16) uint32_t s_sel[WRITE_VALS ? 256 * NSEL : 4];
     __shared__ __align__(16) uint8_t s_qtab[QUANT ? kQtabEntries : 16];
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    // the wave index in a scalar register: branches on it are scalar
+    // branches, not exec masks, so nothing the compiler places at their joins
+    // (register spills among them) runs with some lanes switched off
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     if constexpr (PACKED) {
         if (tid <= U) s_edge[tid] = 0u;
     }
@@ -705,7 +708,10 @@ void compress_stream_kernel(CompressArgs a)
                         if (a.dense_q_out != nullptr)
                             store_chunk<1, VEC>(a.dense_q_out, a.M, a.N, row0 + 8 * k, col0, o[k]);
                     }
-                    a.bitmask[(size_t)t * kTileBytes + 64 * k + lane] = (uint8_t)m;
+                    // wave 0 stores its bytes after the look-back: a store
+                    // ahead of a status read delays the read until it is
+                    // acknowledged (vector memory counts retire in order)
+                    if (wave != 0) a.bitmask[(size_t)t * kTileBytes + 64 * k + lane] = (uint8_t)m;
                 }
             }
             mp[k >> 2] |= m << (8 * (k & 3));
@@ -729,8 +735,17 @@ void compress_stream_kernel(CompressArgs a)
             unit_total = __shfl(x, U - 1, 64);
             if (lane < U) s_toff[lane] = x - v;
             if (lane == U - 1) s_toff[U] = x;
-            if (lane == 0)
+            if (U == 1 && lane == 0)
                 st_relaxed(&a.status[u], pack_status(a.epoch, u == 0 ? kFlagInc : kFlagAgg, unit_total));
+        }
+        if (MODE != MODE_VALS && U > 1 && wave == 1) {
+            // the unit's aggregate is published by wave 1, so that wave 0
+            // enters the look-back with no store outstanding.  Wave 0's
+            // inclusive word may land first and this aggregate over it: a
+            // walk that reads the aggregate adds the unit's total and goes
+            // on, so either word gives the same prefix.
+            const uint32_t total = wave_total(lane < U ? s_cnt[lane] : 0u);
+            if (lane == 0) st_relaxed(&a.status[u], pack_status(a.epoch, u == 0 ? kFlagInc : kFlagAgg, total));
         }
         // ---- compaction of every chunk in registers, which needs no prefix:
         // the mask byte indexes a table of v_perm selectors that move the set
@@ -768,6 +783,11 @@ void compress_stream_kernel(CompressArgs a)
             if (lane == 0 && ((u + 1) & (kGroupUnits - 1)) == 0)
                 st_relaxed(&a.gstat[u / kGroupUnits], pack_status(a.epoch, kFlagInc, excl + unit_total));
             if (lane == 0) s_excl[0] = excl;
+            if (tile_ok) {
+#pragma unroll
+                for (int k = 0; k < 8; k++)
+                    a.bitmask[(size_t)t * kTileBytes + 64 * k + lane] = (uint8_t)(mp[k >> 2] >> (8 * (k & 3)));
+            }
             if (lane < ntiles) a.prefix[t0 + lane] = excl + (x - v);
             if (lane == 0 && t0 + ntiles == a.tend) {
                 a.prefix[a.tend] = excl + unit_total;
