@@ -474,7 +474,7 @@ def bench_sweep(steps: int, warmup: int, packed_only: bool = False):
         def comp():
             buf.reset_buffer()
             if fp8:
-                holder["sp"] = quantize_and_compress(x, buf, pack_sbit=pack)[2]
+                holder["sp"] = quantize_and_compress(x, buf, pack_sbit=pack, dense_out=False)[2]
             else:
                 holder["sp"] = dense_to_tilesparse(x, None, buf, pack_sbit=pack)
 

@@ -111,33 +111,68 @@ __device__ __forceinline__ uint2 quant_chunk(const uint4 v, float scale, float r
     return uint2{p[0] | (p[1] << 16), p[2] | (p[3] << 16)};
 }
 
-// The quantizer through a code table: for a fixed scale, f32_to_e4m3(x / s)
-// of a bf16 x depends only on x's 15 magnitude bits (RNE and the NaN rule
-// are symmetric, so the sign bit is x's), so qtab[m] = f32_to_e4m3(m / s)
-// for the 32,768 magnitudes gives every code with one LDS byte read.
-constexpr int kQtabEntries = 1 << 15;
+// The quantizer through a code table.  For a fixed scale s, f32_to_e4m3(x / s)
+// of a bf16 x depends only on x's 15 magnitude bits m (RNE and the NaN rule
+// are symmetric, so the sign bit is x's), and only a window of 24 exponents
+// around s's gives codes other than 0 and 0x7f.  With Es the biased exponent
+// of s (s < 2^(Es-126)):
+//   * m below (Es - 12) * 128 is x < 2^(Es-139) <= s * 2^-12: the quotient
+//     rounds below 2^-12 and converts to 0;
+//   * m at or above (Es + 12) * 128 is x >= 2^(Es-115) > s * 2^11: the
+//     quotient is above 464 (or Inf / NaN for the Inf and NaN magnitudes)
+//     and converts to 0x7f.
+// A NaN scale makes every code NaN: the scale's own (positive, 0x7f) for a
+// non-NaN x, x's for a NaN x (a quotient with one NaN operand is that NaN).
+// An infinite scale puts the window past the Inf/NaN exponent, whose entries
+// are then computed like the others.
+// Table, one half per sign of x (kQtabEntries each, negative half second):
+// [0] the code of every magnitude below the window, [1 + i] the code of
+// magnitude base + i (i < 3072), [3073] the code of every magnitude above it,
+// each from one correctly rounded division (the quantizer's own rule); a
+// lookup is qtab[clamp(m - base + 1, 0, 3073) + sign * kQtabEntries].
+constexpr int kQwinExps = 24;
+constexpr int kQtabEntries = kQwinExps * 128 + 2;
+constexpr int kQtabBytes = (2 * kQtabEntries + 15) / 16 * 16;     // the table's space (16-byte copies)
 
-__device__ __forceinline__ uint32_t qtab_code(const uint8_t* qtab, uint32_t b16)
+// window base (a magnitude) of a scale, minus 1: the lookup's offset
+__device__ __forceinline__ int qtab_offset(float scale)
 {
-    return (uint32_t)qtab[b16 & 0x7fffu] | ((b16 >> 8) & 0x80u);
+    return ((int)((__float_as_uint(scale) >> 23) & 0xffu) - kQwinExps / 2) * 128 - 1;
 }
 
-__device__ __forceinline__ uint2 quant_chunk_tab(const uint4 v, const uint8_t* qtab)
+__device__ __forceinline__ uint32_t qtab_code(const uint8_t* qtab, uint32_t m, uint32_t sign, int qoff)
+{
+    const int i = min(max((int)m - qoff, 0), kQtabEntries - 1);
+    return (uint32_t)qtab[i + (int)sign * kQtabEntries];
+}
+
+__device__ __forceinline__ uint2 quant_chunk_tab(const uint4 v, const uint8_t* qtab, int qoff)
 {
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
     uint32_t p[4];
 #pragma unroll
-    for (int k = 0; k < 4; k++) p[k] = qtab_code(qtab, w[k] & 0xffffu) | (qtab_code(qtab, w[k] >> 16) << 8);
+    for (int k = 0; k < 4; k++)
+        p[k] = qtab_code(qtab, w[k] & 0x7fffu, (w[k] >> 15) & 1u, qoff) |
+               (qtab_code(qtab, (w[k] >> 16) & 0x7fffu, w[k] >> 31, qoff) << 8);
     return uint2{p[0] | (p[1] << 16), p[2] | (p[3] << 16)};
 }
 
-// qtab[m] = f32_to_e4m3(bf16(m) / scale), scale from the amax slot (one
-// correctly rounded division per entry: the quantizer's own rule)
+// entry i of each half stands for magnitude base + i - 1 (the end entries
+// for every magnitude past them); scale from the amax slot
 __global__ __launch_bounds__(256) void qtab_build_kernel(const uint64_t* slot, uint32_t epoch, uint8_t* qtab)
 {
-    const uint32_t m = blockIdx.x * 256 + threadIdx.x;
+    const int i = (int)(blockIdx.x * 256 + threadIdx.x);
+    if (i >= kQtabEntries) return;
     const float scale = scale_from_slot(slot, epoch);
-    if (m < (uint32_t)kQtabEntries) qtab[m] = (uint8_t)f32_to_e4m3(bf16_to_f32(m) / scale);
+    const int m = min(max(qtab_offset(scale) + i, 0), 0x7fff);
+    const uint32_t c = f32_to_e4m3(bf16_to_f32((uint32_t)m) / scale);
+    if (scale != scale) {
+        qtab[i] = 0x7fu;
+        qtab[kQtabEntries + i] = m > 0x7f80 ? 0xffu : 0x7fu;
+    } else {
+        qtab[i] = (uint8_t)c;
+        qtab[kQtabEntries + i] = (uint8_t)(c | 0x80u);
+    }
 }
 
 // Chunk geometry inside tile t of a [*, N] matrix.
@@ -181,7 +216,7 @@ struct CompressArgs {
     int32_t* err;
     uint32_t* fallbacks;
     uint64_t patience;          // look-back wait (s_memrealtime ticks) before counting a unit itself
-    const uint8_t* qtab;        // quantize: the code table (kQtabEntries bytes), copied into LDS
+    const uint8_t* qtab;        // quantize: the code table (kQtabBytes), copied into LDS
 };
 
 // 200 us at the 100 MHz s_memrealtime clock: waiting longer than this for a
@@ -205,10 +240,11 @@ struct CompressTraits {
 template <int IN_T, bool QUANT, bool TAB = false>
 __device__ __forceinline__ uint32_t chunk_mask(const typename Raw<CompressTraits<IN_T, QUANT>::INB>::T& d,
                                                typename Raw<CompressTraits<IN_T, QUANT>::OUTB>::T& o,
-                                               float scale, float rcp, const uint8_t* qtab = nullptr)
+                                               float scale, float rcp, const uint8_t* qtab = nullptr,
+                                               int qoff = 0)
 {
     if constexpr (QUANT) {
-        if constexpr (TAB) o = quant_chunk_tab(d, qtab);
+        if constexpr (TAB) o = quant_chunk_tab(d, qtab, qoff);
         else o = quant_chunk(d, scale, rcp);
         return mask_fp8x8<DT_E4M3FN>(o);
     } else if constexpr (IN_T == DT_BF16) {
@@ -223,13 +259,14 @@ __device__ __forceinline__ uint32_t chunk_mask(const typename Raw<CompressTraits
 template <int IN_T, bool QUANT, bool TAB = false>
 __device__ __forceinline__ uint32_t stream_chunk_mask(const typename Raw<CompressTraits<IN_T, QUANT>::INB>::T& d,
                                                       typename Raw<CompressTraits<IN_T, QUANT>::OUTB>::T& o,
-                                                      float scale, float rcp, const uint8_t* qtab = nullptr)
+                                                      float scale, float rcp, const uint8_t* qtab = nullptr,
+                                                      int qoff = 0)
 {
     if constexpr (IN_T == DT_BF16 && !QUANT) {
         o = d;
         return mask_bf16x8_pk(d);
     } else {
-        return chunk_mask<IN_T, QUANT, TAB>(d, o, scale, rcp, qtab);
+        return chunk_mask<IN_T, QUANT, TAB>(d, o, scale, rcp, qtab, qoff);
     }
 }
 
@@ -585,7 +622,7 @@ __device__ __forceinline__ void packed_unit_edges(const CompressArgs& a, int64_t
 }
 
 #ifndef BS_QUANT_WAVES_PER_EU
-#define BS_QUANT_WAVES_PER_EU 6
+#define BS_QUANT_WAVES_PER_EU 8
 #endif
 
 #ifndef BS_PACKED_WAVES_PER_EU
@@ -613,9 +650,14 @@ void compress_stream_kernel(CompressArgs a)
     __shared__ uint32_t s_toff[U + 1];      // tile offsets inside the unit's run; [U] = unit total
     __shared__ uint32_t s_edge[PACKED ? U + 1 : 1];   // packed: boundary dwords of the unit's runs
     __shared__ uint32_t s_excl[1];
-    __shared__ __align__(16) uint8_t s_ring[WRITE_VALS ? U * kRingElems * OUTB : 16];
     __shared__ __align__(16) uint32_t s_sel[WRITE_VALS ? 256 * NSEL : 4];
-    __shared__ __align__(16) uint8_t s_qtab[QUANT ? kQtabEntries : 16];
+    // the quantizer's code table is read only while the chunks are masked,
+    // the value rings only after the look-back's barrier: they share LDS
+    constexpr int kRingBytes = WRITE_VALS ? U * kRingElems * OUTB : 16;
+    constexpr int kShared = QUANT && kQtabBytes > kRingBytes ? kQtabBytes : kRingBytes;
+    __shared__ __align__(16) uint8_t s_area[kShared];
+    uint8_t* const s_ring = s_area;
+    uint8_t* const s_qtab = s_area;
 
     // the wave index in a scalar register: branches on it are scalar
     // branches, not exec masks, so nothing the compiler places at their joins
@@ -637,6 +679,7 @@ void compress_stream_kernel(CompressArgs a)
     float scale = 1.0f;
     if constexpr (QUANT) scale = scale_from_slot(a.amax_slot, a.amax_epoch);
     const float rcp = 1.0f / scale;
+    const int qoff = QUANT ? qtab_offset(scale) : 0;
     int64_t start = 0;
     if (a.offset_in) start = *a.offset_in;
     if (a.align8) start = (start + 7) & ~(int64_t)7;
@@ -663,12 +706,22 @@ void compress_stream_kernel(CompressArgs a)
         uint32_t vm[8];                         // MODE_VALS: the given bitmask bytes
         // chunk k is inside the matrix iff 8k < rows_in (rows_in <= 0: none)
         const int64_t rows_in = (tile_ok && col0 < a.N) ? a.M - row0 : 0;
+        // VEC addressing: the tile origin and chunk k's row step are uniform
+        // over the wave (64-bit, scalar registers); the lane's place in the
+        // tile is one 32-bit register, (lane/8) rows of N elements plus its
+        // column (< 8 N elements: the host takes this path only when 8 N
+        // elements of the widest operand fit 32 bits)
+        const uint64_t t_org = (uint64_t)tm * 64 * (uint64_t)a.N + (uint64_t)tn * 64;
+        const uint32_t r_in = (uint32_t)(lane >> 3) * (uint32_t)a.N;
+        const uint32_t c_in = (uint32_t)(min(col0, a.N - 8) - (int64_t)tn * 64);
 #pragma unroll
         for (int k = 0; k < 8; k++) {
             const int64_t row = row0 + 8 * k;
             if constexpr (VEC) {
-                const int64_t rc = min(row, a.M - 1), cc = min(col0, a.N - 8);
-                d[k] = ld_chunk<NT, RawIn>(a.dense + (rc * a.N + cc) * INB);
+                // rows past the matrix read the tile's first row (in range)
+                const uint32_t lo = (row < a.M ? r_in : 0u) + c_in;
+                d[k] = ld_chunk<NT, RawIn>(a.dense + (t_org + (uint64_t)(8 * k) * (uint64_t)a.N) * INB +
+                                           (uint64_t)(lo * (uint32_t)INB));
             } else {
                 d[k] = tile_ok ? load_chunk<INB, false>(a.dense, a.M, a.N, row, col0) : RawIn{};
             }
@@ -676,7 +729,7 @@ void compress_stream_kernel(CompressArgs a)
         }
         if constexpr (QUANT) {
             // the code table into LDS, behind the dense loads (16-byte copies)
-            for (int i = tid; i < kQtabEntries / 16; i += 64 * U)
+            for (int i = tid; i < kQtabBytes / 16; i += 64 * U)
                 reinterpret_cast<uint4*>(s_qtab)[i] = reinterpret_cast<const uint4*>(a.qtab)[i];
             __syncthreads();
         }
@@ -699,14 +752,26 @@ void compress_stream_kernel(CompressArgs a)
                 o[k] = d[k];
                 m = tile_ok ? vm[k] & 0xffu : 0u;
             } else {
-                m = stream_chunk_mask<IN_T, QUANT, QUANT>(d[k], o[k], scale, rcp, s_qtab) &
+                m = stream_chunk_mask<IN_T, QUANT, QUANT>(d[k], o[k], scale, rcp, s_qtab, qoff) &
                     (8 * k < rows_in ? 0xffu : 0u);
                 if (tile_ok) {
-                    if (a.relu_out != nullptr)
-                        store_chunk<INB, VEC>(a.relu_out, a.M, a.N, row0 + 8 * k, col0, d[k]);
-                    if constexpr (QUANT) {
-                        if (a.dense_q_out != nullptr)
-                            store_chunk<1, VEC>(a.dense_q_out, a.M, a.N, row0 + 8 * k, col0, o[k]);
+                    if constexpr (VEC) {
+                        // in range, the lane's unclamped place in the tile
+                        const uint64_t ko = t_org + (uint64_t)(8 * k) * (uint64_t)a.N;
+                        const uint32_t lo = r_in + c_in;
+                        if (a.relu_out != nullptr && 8 * k < rows_in)
+                            st_chunk<false, RawIn>(a.relu_out + ko * INB + (uint64_t)(lo * (uint32_t)INB), d[k]);
+                        if constexpr (QUANT) {
+                            if (a.dense_q_out != nullptr && 8 * k < rows_in)
+                                st_chunk<false, RawOut>(a.dense_q_out + ko + (uint64_t)lo, o[k]);
+                        }
+                    } else {
+                        if (a.relu_out != nullptr)
+                            store_chunk<INB, VEC>(a.relu_out, a.M, a.N, row0 + 8 * k, col0, d[k]);
+                        if constexpr (QUANT) {
+                            if (a.dense_q_out != nullptr)
+                                store_chunk<1, VEC>(a.dense_q_out, a.M, a.N, row0 + 8 * k, col0, o[k]);
+                        }
                     }
                     // wave 0 stores its bytes after the look-back: a store
                     // ahead of a status read delays the read until it is
@@ -1649,6 +1714,10 @@ static inline bool aligned8(const void* p) { return (((uintptr_t)p) & 7u) == 0; 
 #endif
 constexpr int kStreamU = BS_STREAM_U;
 
+// The streaming compress addresses a lane's chunk inside its tile with a
+// 32-bit byte offset below 8 rows of N elements of `eb` bytes.
+static bool vec_rows_fit(int64_t N, int eb) { return 8 * N * (int64_t)eb < (int64_t(1) << 32); }
+
 template <int IN_T, bool QUANT, int MODE, bool PACKED>
 static hipError_t launch_compress_mode(const CompressArgs& a, bool vec, bool nt, hipStream_t st)
 {
@@ -1695,7 +1764,7 @@ extern "C" int64_t bs_compress_workspace_bytes(int64_t M, int64_t N)
     // status words: one per tile covers the units and the unit groups of the
     // streaming kernel (T/8 + T/512 words) and the units of the others; then
     // the quantizer's code table
-    return ws_qtab_offset(T) + kQtabEntries;
+    return ws_qtab_offset(T) + kQtabBytes;
 }
 
 extern "C" const uint64_t* bs_workspace_amax_slot(const void* ws, int64_t)
@@ -1817,11 +1886,12 @@ static int compress_impl(const void* dense, int in_dtype, int64_t M, int64_t N, 
     if (quantize) {
         // the code table of this call's scale, built after the amax it reads
         uint8_t* qtab = (uint8_t*)workspace + ws_qtab_offset(T);
-        hipLaunchKernelGGL(qtab_build_kernel, dim3(kQtabEntries / 256), dim3(256), 0, st, amax_slot, amax_epoch, qtab);
+        hipLaunchKernelGGL(qtab_build_kernel, dim3((kQtabEntries + 255) / 256), dim3(256), 0, st, amax_slot, amax_epoch,
+                           qtab);
         a.qtab = qtab;
     }
     const int inb = in_dtype == DT_BF16 ? 2 : 1;
-    bool vec = (N % 8 == 0) && (((uintptr_t)dense) % (8 * inb) == 0) &&
+    bool vec = (N % 8 == 0) && (((uintptr_t)dense) % (8 * inb) == 0) && vec_rows_fit(N, inb) &&
                (dense_q_out == nullptr || aligned8(dense_q_out)) &&
                (relu_out == nullptr || ((uintptr_t)relu_out) % (8 * inb) == 0);
     const bool nt = use_nontemporal(M * N * inb);
@@ -1910,7 +1980,7 @@ extern "C" int bs_compact_vals(const void* dense, int in_dtype, int64_t M, int64
     a.tend = (uint32_t)(first_tile + num_tiles);
     a.err = err_flags;
     a.patience = kLookbackPatienceTicks;       // no look-back in this mode
-    bool vec = (N % 8 == 0) && (((uintptr_t)dense) % (8 * eb) == 0);
+    bool vec = (N % 8 == 0) && (((uintptr_t)dense) % (8 * eb) == 0) && vec_rows_fit(N, eb);
     hipError_t e = launch_compress<MODE_VALS>(a, in_dtype, false, vec, false, (hipStream_t)stream);
     if (e != hipSuccess) return set_error(BS_ERR_HIP, "bs_compact_vals launch: %s", hipGetErrorString(e));
     return BS_OK;
@@ -2237,7 +2307,7 @@ extern "C" int bs_pack_bits(const void* raw, int vals_dtype, const uint32_t* cou
 namespace bs {
 
 constexpr int64_t kScratchMaxTiles = int64_t(1) << 19;                 // 2^31 elements in 64x64 tiles (half the codec range)
-constexpr int64_t kScratchBytes = (kWsHeaderBytes + 8 * (kScratchMaxTiles + 2) + 255) / 256 * 256 + kQtabEntries;
+constexpr int64_t kScratchBytes = (kWsHeaderBytes + 8 * (kScratchMaxTiles + 2) + 255) / 256 * 256 + kQtabBytes;
 constexpr int kScratchMaxDevices = 64;
 
 // One copy per GPU, held until the process ends.  Host code never uses this

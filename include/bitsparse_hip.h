@@ -389,7 +389,7 @@ int bs_relu2_grad_packed(void* grad, int64_t M, int64_t N, const void* stream_by
  * cannot allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc): bs_compress / bs_compress_relu
  * with the look-back status words and the fp8 amax slot in a library-owned
- * device array (one per GPU, 4 MiB + 33,024 bytes, kept until the process ends)
+ * device array (one per GPU, 4 MiB + 6,672 bytes, kept until the process ends)
  * instead of a caller-allocated workspace.  The call allocates nothing.
  *   quantize   1: bf16 input quantized to e4m3fn; the amax pass (of relu(x)
  *              with relu) runs inside the call on the same array

@@ -32,9 +32,10 @@ def test_abi_version_and_workspace_size():
     L = _lib.load()
     assert L.bs_abi_version() == _lib.ABI_VERSION
     # header + one status word per tile (+2), rounded up to 256 bytes, then the
-    # quantizer's 32 KiB code table
+    # quantizer's windowed code table (per sign of x: 24 exponents x 128
+    # mantissas + 2 end entries; rounded up to 16 bytes)
     def want(T):
-        return (256 + 8 * (T + 2) + 255) // 256 * 256 + 32768
+        return (256 + 8 * (T + 2) + 255) // 256 * 256 + 6160
     assert L.bs_compress_workspace_bytes(4096, 4096) == want(4096)
     assert L.bs_compress_workspace_bytes(129, 131) == want(9)
     assert L.bs_compress_workspace_bytes(0, 0) == want(0)

@@ -413,8 +413,11 @@ def _all_finite_bf16_upto(amax_bits):
     return np.concatenate([mags, mags | np.uint16(0x8000)])
 
 
-@pytest.mark.parametrize("amax", [448.0, 1.0, 3.0e38, 1e-30, 6.5, 0.0173, 1234.5, 2.0 ** -20] +
-                         [float(v) for v in np.random.default_rng(5).lognormal(0.0, 6.0, 16)])
+_AMAXES = [448.0, 1.0, 3.0e38, 1e-30, 6.5, 0.0173, 1234.5, 2.0 ** -20] + \
+    [float(v) for v in np.random.default_rng(5).lognormal(0.0, 6.0, 16)]
+
+
+@pytest.mark.parametrize("amax", _AMAXES)
 def test_to_fp8_all_bf16_patterns(dev, amax):
     """Every finite bf16 input at a given amax (scale = amax / 448) against the
     oracle's division and RNE rounding: pins the reciprocal/FMA quotient and the
@@ -428,6 +431,48 @@ def test_to_fp8_all_bf16_patterns(dev, amax):
     qo, so = O.to_fp8(bits(x))
     assert float(s.item()) == so
     assert (bits(q) == qo).all()
+
+
+@pytest.mark.parametrize("amax", _AMAXES)
+def test_quantizing_compress_all_bf16_patterns(dev, amax):
+    """quantize_and_compress over every finite bf16 input at a given amax
+    (zero padding to whole rows leaves the amax alone): the compress kernel's
+    code table, which holds the exponents around the scale's and one code for
+    every magnitude below or above them, against the oracle's division and RNE
+    rounding, through the dense codes, the bitmask, the prefix and the values."""
+    F, _, _ = _bs()
+    a_bits = int(np.array([amax], dtype=np.float32).view(np.uint32)[0] >> 16)
+    a_bits = min(a_bits, 0x7f7f)
+    x_bits = _all_finite_bf16_upto(a_bits)
+    cols = 256
+    xb = np.zeros(-(-x_bits.size // cols) * cols, np.uint16)
+    xb[:x_bits.size] = x_bits
+    xb = xb.reshape(-1, cols)
+    qo, so = O.to_fp8(xb)
+    bm, pf, v = O.compress(qo, O.E4M3FN)
+    q, s, sp = F.quantize_and_compress(from_bits(xb, torch.bfloat16).to(dev), None)
+    assert float(s.item()) == so
+    assert (bits(q) == qo).all()
+    assert (bits(sp.bitmask) == bm).all() and (bits(sp.prefix) == pf).all()
+    assert (bits(sp.vals)[:v.size] == v).all()
+
+
+def test_quantizing_compress_nan_input(dev):
+    """A NaN input makes the scale NaN and every code NaN: the scale's
+    (positive) NaN for a non-NaN x whatever its sign, x's own for a NaN x (a
+    quotient with one NaN operand is that NaN), as in the oracle's division."""
+    F, _, _ = _bs()
+    x = preact_input((129, 131), seed=74)
+    xb = bits(x).copy()
+    xb[7, 9], xb[30, 40], xb[100, 3] = 0x7fc0, 0xffc0, 0xff80      # +NaN, -NaN, -Inf
+    x = from_bits(xb, torch.bfloat16)
+    qo, so = O.to_fp8(bits(x))
+    bm, pf, v = O.compress(qo, O.E4M3FN)
+    q, s, sp = F.quantize_and_compress(x.to(dev), None)
+    assert np.isnan(float(s.item())) and np.isnan(so)
+    assert (bits(q) == qo).all()
+    assert (bits(sp.bitmask) == bm).all() and (bits(sp.prefix) == pf).all()
+    assert (bits(sp.vals)[:v.size] == v).all()
 
 
 def test_to_fp8_and_quantizing_compress_inf_input(dev):
