@@ -1238,12 +1238,14 @@ __device__ __forceinline__ int stage_run_packed(const GatherArgs& a, int64_t run
 // ranks, run staging.  Fills m[][], r0[][] (LDS element index of each chunk's
 // first value) and returns after a barrier.
 // M_LOADED: the caller already holds the mask bytes in m and prefix[t0 + tid]
-// (tid <= ntiles) in pf.
+// (tid <= ntiles) in pf.  vo: the run's cursor (*vals_offset, 0 without),
+// which callers read at their start with the mask bytes, so that the staging
+// waits for one memory round trip before it rather than two.
 template <int VB, int PB, int U, bool NT, bool M_LOADED = false>
 __device__ __forceinline__ int gather_prepare(const GatherArgs& a, uint32_t t0, int ntiles,
                                               uint32_t (&m)[U][2], uint32_t (&r0)[U][2],
                                               uint32_t* s_pref, uint32_t (*s_wtot)[2][4],
-                                              uint8_t* s_vals, int tid, uint32_t pf = 0u)
+                                              uint8_t* s_vals, int tid, int64_t vo, uint32_t pf = 0u)
 {
     const int wave = tid >> 6, lane = tid & 63;
     if constexpr (!M_LOADED) {
@@ -1265,7 +1267,6 @@ __device__ __forceinline__ int gather_prepare(const GatherArgs& a, uint32_t t0, 
             if (lane == 0) s_wtot[j][h][wave] = tot;
         }
     __syncthreads();
-    const int64_t vo = a.vals_offset ? *a.vals_offset : 0;
     const uint32_t pb = s_pref[0];
     int p = 0, bitbase = 0;
     if constexpr (PB > 0)
@@ -1353,13 +1354,14 @@ __global__ __launch_bounds__(kThreads) void decompress_kernel(GatherArgs a)
     const uint32_t t0 = (uint32_t)a.first_m_tile * a.grid_n + pid0;
 
     uint32_t m[U][2], r0[U][2];
-    const int bitbase = gather_prepare<VB, PB, U, NT>(a, t0, ntiles, m, r0, s_pref, s_wtot, s_vals, tid);
+    // cursor and scale read with the front half's loads
+    const int64_t vo = a.vals_offset ? *a.vals_offset : 0;
+    float s = 1.0f;
+    if constexpr (HAS_SCALE) s = *a.scale;
+    const int bitbase = gather_prepare<VB, PB, U, NT>(a, t0, ntiles, m, r0, s_pref, s_wtot, s_vals, tid, vo);
 
     float s2b = 1.0f;
-    if constexpr (HAS_SCALE) {
-        float s = *a.scale;
-        s2b = bf16_to_f32(f32_to_bf16(s * s));
-    }
+    if constexpr (HAS_SCALE) s2b = bf16_to_f32(f32_to_bf16(s * s));
     // an unset element: 0, or bf16(0 * bf16(scale^2)) (NaN for an infinite or NaN scale)
     const uint32_t zero_x = HAS_SCALE ? f32_to_bf16(0.0f * s2b) : 0u;
     if constexpr (STAGE) {
@@ -1451,6 +1453,7 @@ __global__ __launch_bounds__(kThreads) void decompress_fp8_kernel(GatherArgs a, 
         }
         s_sel[tid] = uint2{sel[0], sel[1]};
     }
+    const int64_t vo = a.vals_offset ? *a.vals_offset : 0;      // with the mask bytes
     uint32_t m[NP][2], ex[NP][2];
 #pragma unroll
     for (int k = 0; k < NP; k++)
@@ -1477,7 +1480,6 @@ __global__ __launch_bounds__(kThreads) void decompress_fp8_kernel(GatherArgs a, 
             }
         }
     __syncthreads();
-    const int64_t vo = a.vals_offset ? *a.vals_offset : 0;
     const uint32_t pb = s_pref[0];
     int p = 0, bitbase = 0;
     if constexpr (PACKED)
@@ -1566,7 +1568,10 @@ __global__ __launch_bounds__(kThreads) void relu2_grad_kernel(GatherArgs a)
     const int ntiles = (int)min((uint32_t)U, a.num_tiles - t0);
 
     // mask bytes first: a chunk with no bit set is written without reading
-    // its gradient (at 90% zeros 43% of the chunks)
+    // its gradient (at 90% zeros 43% of the chunks); cursor and scale with them
+    const int64_t vo = a.vals_offset ? *a.vals_offset : 0;
+    float sc = 1.0f;
+    if constexpr (HAS_SCALE) sc = *a.scale;
     uint32_t m[U][2], r0[U][2];
 #pragma unroll
     for (int j = 0; j < U; j++)
@@ -1586,7 +1591,7 @@ __global__ __launch_bounds__(kThreads) void relu2_grad_kernel(GatherArgs a)
                 g[j][h] = load_chunk<2, VEC, NT>(a.out, a.rows, a.K, row, col0);
             }
         }
-    const int bitbase = gather_prepare<VB, PB, U, NT, true>(a, t0, ntiles, m, r0, s_pref, s_wtot, s_vals, tid, pf);
+    const int bitbase = gather_prepare<VB, PB, U, NT, true>(a, t0, ntiles, m, r0, s_pref, s_wtot, s_vals, tid, vo, pf);
 
     if constexpr (WIDEN) {
         // staged indices [0, count + 16) cover the run and its <= 15-element phase
@@ -1597,7 +1602,7 @@ __global__ __launch_bounds__(kThreads) void relu2_grad_kernel(GatherArgs a)
         __syncthreads();
     }
     float sb = 1.0f;
-    if constexpr (HAS_SCALE) sb = bf16_to_f32(f32_to_bf16(*a.scale));
+    if constexpr (HAS_SCALE) sb = bf16_to_f32(f32_to_bf16(sc));
     const uint32_t zero_x = HAS_SCALE ? f32_to_bf16(0.0f * sb) : 0u;
     const float k2 = 2.0f * a.relu2_scale;
 #pragma unroll
