@@ -703,6 +703,9 @@ def main() -> int:
     ap.add_argument("--mlp-only", action="store_true",
                     help="run only the configs[1] MLP section (dense, compressed, fused up-projection) "
                          "and print its JSON (profiling entry point)")
+    ap.add_argument("--mlp-c4-only", action="store_true",
+                    help="run only the configs[3] fp8 ReLU^2 MLP section (dense, compressed) and print its "
+                         "JSON (profiling entry point)")
     ap.add_argument("--sweep-only", action="store_true",
                     help="run only the configs[2] sparsity sweep and print its JSON (profiling entry point)")
     ap.add_argument("--kernels-only", action="store_true",
@@ -723,7 +726,8 @@ def main() -> int:
     from bitsparse_amd import _lib
     _lib.load()
 
-    if args.calibrate_copy and (args.gemm_only or args.mlp_only or args.sweep_only or args.packed_only):
+    if args.calibrate_copy and (args.gemm_only or args.mlp_only or args.mlp_c4_only or args.sweep_only or
+                                args.packed_only):
         # a 1 GiB device copy: the reference of the rocprof byte counters
         src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
         dst = torch.empty_like(src)
@@ -736,6 +740,9 @@ def main() -> int:
         return 0
     if args.mlp_only:
         print(json.dumps({"mlp": bench_mlp(args.steps, args.warmup)}), flush=True)
+        return 0
+    if args.mlp_c4_only:
+        print(json.dumps({"mlp_c4": bench_mlp_c4(args.steps, args.warmup)}), flush=True)
         return 0
     if args.sweep_only:
         print(json.dumps({"sweep": bench_sweep(args.steps, args.warmup)}), flush=True)

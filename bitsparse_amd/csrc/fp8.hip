@@ -117,6 +117,68 @@ static uint32_t grid_for(int64_t n)
     return (uint32_t)g;
 }
 
+
+// Byte transpose out[c * ld_out + r] = in[r * ld_in + c] (r < R, c < C): the
+// fp8 GEMM operand layout change (row-major <-> column-major) that hipBLASLt's
+// fp8 path needs.  A 256-thread workgroup moves a 128 x 128 tile: 16-byte
+// loads (eight lanes cover one 128-byte input row), the tile in LDS as
+// dwords with the dword column XOR-swizzled by row / 4, then per lane a 4 x 4
+// byte block (four LDS dwords from four consecutive rows) transposed in
+// registers with v_perm_b32 and stored as one dword of each of four output
+// rows, 32 lanes covering one 128-byte output row.  Needs C % 16 == 0,
+// R % 4 == 0, ld_in % 16 == 0, ld_out % 4 == 0 and in / out 16 / 4-byte
+// aligned (the host checks).
+constexpr int kTrTile = 128;
+
+__device__ __forceinline__ void transpose4x4_bytes(const uint32_t (&a)[4], uint32_t (&o)[4])
+{
+    // a[k] = bytes (k, 0..3); o[i] = bytes (0..3, i)
+    const uint32_t t0 = __builtin_amdgcn_perm(a[1], a[0], 0x05010400u);   // a0.b0 a1.b0 a0.b1 a1.b1
+    const uint32_t t1 = __builtin_amdgcn_perm(a[1], a[0], 0x07030602u);   // a0.b2 a1.b2 a0.b3 a1.b3
+    const uint32_t u0 = __builtin_amdgcn_perm(a[3], a[2], 0x05010400u);
+    const uint32_t u1 = __builtin_amdgcn_perm(a[3], a[2], 0x07030602u);
+    o[0] = __builtin_amdgcn_perm(u0, t0, 0x05040100u);
+    o[1] = __builtin_amdgcn_perm(u0, t0, 0x07060302u);
+    o[2] = __builtin_amdgcn_perm(u1, t1, 0x05040100u);
+    o[3] = __builtin_amdgcn_perm(u1, t1, 0x07060302u);
+}
+
+__global__ __launch_bounds__(256) void transpose_u8_kernel(const uint8_t* in, int64_t R, int64_t C, int64_t ld_in,
+                                                           uint8_t* out, int64_t ld_out, uint32_t tiles_c)
+{
+    __shared__ uint32_t s[kTrTile * 32];
+    const int t = threadIdx.x;
+    const uint32_t tr = blockIdx.x / tiles_c, tc = blockIdx.x - tr * tiles_c;
+    const int64_t r0 = (int64_t)tr * kTrTile, c0 = (int64_t)tc * kTrTile;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const int rr = t / 8 + 32 * q, cc = 16 * (t % 8);
+        const int64_t r = r0 + rr, c = c0 + cc;
+        uint4 v = make_uint4(0u, 0u, 0u, 0u);
+        if (r < R && c < C) v = *reinterpret_cast<const uint4*>(in + r * ld_in + c);
+        const int sw = (rr >> 2) & 31, d0 = cc / 4;
+        uint32_t* row = s + rr * 32;
+        row[(d0 + 0) ^ sw] = v.x;
+        row[(d0 + 1) ^ sw] = v.y;
+        row[(d0 + 2) ^ sw] = v.z;
+        row[(d0 + 3) ^ sw] = v.w;
+    }
+    __syncthreads();
+    const int rb = t % 32;                  // input rows 4 rb .. 4 rb + 3 (swizzle rb)
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        const int cb = t / 32 + 8 * p;      // input dword column: columns 4 cb .. 4 cb + 3
+        uint32_t a[4], o[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) a[k] = s[(4 * rb + k) * 32 + (cb ^ rb)];
+        transpose4x4_bytes(a, o);
+        const int64_t orow = c0 + 4 * cb, ocol = r0 + 4 * rb;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (orow + i < C && ocol < R) *reinterpret_cast<uint32_t*>(out + (orow + i) * ld_out + ocol) = o[i];
+    }
+}
+
 }  // namespace bs
 
 using namespace bs;
@@ -182,5 +244,28 @@ extern "C" int bs_quantize_e4m3fn(const void* x, int64_t n, void* q_out, float* 
                        (const uint16_t*)x, n, (uint8_t*)q_out, scale_out, slot, epoch);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(BS_ERR_HIP, "bs_quantize_e4m3fn launch: %s", hipGetErrorString(e));
+    return BS_OK;
+}
+
+extern "C" int bs_transpose_u8(const void* in, int64_t R, int64_t C, int64_t ld_in, void* out, int64_t ld_out,
+                               void* stream)
+{
+    clear_error();
+    if (R < 0 || C < 0) return set_error(BS_ERR_INVALID, "bs_transpose_u8: negative size");
+    if (R == 0 || C == 0) return BS_OK;
+    if (in == nullptr || out == nullptr) return set_error(BS_ERR_INVALID, "bs_transpose_u8: null pointer");
+    if (C % 16 != 0 || R % 4 != 0)
+        return set_error(BS_ERR_INVALID, "bs_transpose_u8: C must be a multiple of 16 and R of 4");
+    if (ld_in < C || ld_in % 16 != 0 || ld_out < R || ld_out % 4 != 0)
+        return set_error(BS_ERR_INVALID, "bs_transpose_u8: ld_in >= C, multiple of 16; ld_out >= R, multiple of 4");
+    if (((uintptr_t)in) % 16 != 0 || ((uintptr_t)out) % 4 != 0)
+        return set_error(BS_ERR_INVALID, "bs_transpose_u8: in must be 16-byte and out 4-byte aligned");
+    const uint64_t tiles_r = (uint64_t)((R + kTrTile - 1) / kTrTile), tiles_c = (uint64_t)((C + kTrTile - 1) / kTrTile);
+    if (tiles_r * tiles_c >= (1ull << 31) || tiles_c >= (1ull << 32))
+        return set_error(BS_ERR_INVALID, "bs_transpose_u8: too many tiles");
+    hipLaunchKernelGGL(transpose_u8_kernel, dim3((uint32_t)(tiles_r * tiles_c)), dim3(256), 0, (hipStream_t)stream,
+                       (const uint8_t*)in, R, C, ld_in, (uint8_t*)out, ld_out, (uint32_t)tiles_c);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(BS_ERR_HIP, "bs_transpose_u8 launch: %s", hipGetErrorString(e));
     return BS_OK;
 }

@@ -72,9 +72,12 @@ def as_fp8_operand(x: Tensor, scale: Tensor | None) -> Fp8Operand:
 def fp8_gemm(a: Fp8Operand, b: Fp8Operand, out_dtype: torch.dtype) -> Tensor:
     """(a.codes * a.scale) @ (b.codes * b.scale) on hipBLASLt, fp32
     accumulation, rounded once to ``out_dtype`` (bf16, fp32 or an fp8 dtype,
-    which saturates)."""
-    qa = a.codes.contiguous()
-    qb = b.codes if b.codes.stride(0) == 1 else b.codes.t().contiguous().t()
+    which saturates).  hipBLASLt's fp8 path takes A row-major and B
+    column-major (both k-contiguous); an operand in the other layout is
+    transposed by the HIP byte-transpose kernel (reference fp8.py:36-43)."""
+    from .src import hip_operators as ops
+    qa = ops.row_major_bytes(a.codes)
+    qb = b.codes if b.codes.stride(0) == 1 else ops.row_major_bytes(b.codes.t()).t()
     return F.scaled_mm(mat_a=qa, mat_b=qb, scale_a=a.scale, scale_b=b.scale, output_dtype=out_dtype,
                        scale_recipe_a=F.ScalingType.TensorWise, scale_recipe_b=F.ScalingType.TensorWise)
 

@@ -262,6 +262,40 @@ def quantize_e4m3fn(x: Tensor, amax_epoch: int) -> tuple[Tensor, Tensor]:
     return q, scale
 
 
+def transpose_u8(x: Tensor, out: Tensor | None = None) -> Tensor:
+    """x.T as a new row-major tensor for a 2-D row-major 1-byte tensor (fp8,
+    uint8) through bs_transpose_u8: the fp8 GEMM operands' layout change
+    (reference fp8.py:36-43, :111).  Needs x.shape[1] % 16 == 0 and
+    x.shape[0] % 4 == 0 (``transpose_u8_supported``)."""
+    if x.dim() != 2 or x.element_size() != 1 or x.stride(1) != 1:
+        raise ValueError("transpose_u8 expects a row-major 2-D tensor of 1-byte elements")
+    R, C = x.shape
+    if out is None:
+        out = torch.empty((C, R), device=x.device, dtype=x.dtype)
+    if out.shape != (C, R) or out.stride(1) != 1 or out.element_size() != 1:
+        raise ValueError("transpose_u8: out must be a row-major [C, R] 1-byte tensor")
+    L = _lib.load()
+    check(L.bs_transpose_u8(x.data_ptr(), R, C, x.stride(0), out.data_ptr(), out.stride(0),
+                            stream_handle(x.device)), "bs_transpose_u8")
+    return out
+
+
+def transpose_u8_supported(x: Tensor) -> bool:
+    return (x.dim() == 2 and x.element_size() == 1 and x.stride(1) == 1 and x.shape[1] % 16 == 0 and
+            x.shape[0] % 4 == 0 and x.stride(0) % 16 == 0 and x.data_ptr() % 16 == 0)
+
+
+def row_major_bytes(x: Tensor) -> Tensor:
+    """A 2-D 1-byte tensor in row-major layout: x itself when it is, the
+    transpose kernel's copy when x is a transposed view of row-major storage
+    of supported shape, torch's copy otherwise."""
+    if x.is_contiguous():
+        return x
+    if x.dim() == 2 and x.stride(0) == 1 and transpose_u8_supported(x.t()):
+        return transpose_u8(x.t())
+    return x.contiguous()
+
+
 # ---------------------------------------------------------------------------
 # decompress
 # ---------------------------------------------------------------------------

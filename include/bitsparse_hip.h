@@ -290,6 +290,18 @@ int bs_quantize_e4m3fn(const void* x, int64_t n, void* q_out, float* scale_out,
                        void* stream);
 
 /*
+ * out[c * ld_out + r] = in[r * ld_in + c] for an [R, C] byte matrix: the
+ * fp8 operand layout change in front of the fp8 GEMM.  Replaces the
+ * a.contiguous() / b.T.contiguous().T / a_fp8.T.contiguous() copies of
+ * lib_sparse/fp8.py:36-43 and :111 (torch's elementwise float8 copy).
+ * Needs C % 16 == 0, R % 4 == 0, ld_in >= C with ld_in % 16 == 0,
+ * ld_out >= R with ld_out % 4 == 0, `in` 16-byte and `out` 4-byte aligned;
+ * out must not overlap in.
+ */
+int bs_transpose_u8(const void* in, int64_t R, int64_t C, int64_t ld_in, void* out, int64_t ld_out,
+                    void* stream);
+
+/*
  * C[M, N] (bf16, row-major, row stride N) = A @ B, where A is a dense bf16
  * [M, K] matrix and B is a compressed [K, N] activation (vals 16-byte
  * aligned) decoded tile by tile into LDS (never written to HBM dense).

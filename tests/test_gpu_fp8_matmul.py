@@ -195,3 +195,53 @@ def test_ffn_relu_fp8_storage_matches_fp8_dense(dev, use_buffer, monkeypatch):
         hi_r = torch.maximum(lo, hi).float().clamp(-448, 448).to(torch.float8_e4m3fn).double()
         g = g8.double()
         assert bool(((g >= lo_r) & (g <= hi_r)).all()), f"{name}: not the e4m3fn rounding of the bf16 gradient"
+
+
+# ---------------------------------------------------------------------------
+# operand layout change: bs_transpose_u8 (the fp8 GEMM's row-major /
+# column-major copies, reference fp8.py:36-43, :111)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("shape", [(4, 16), (16, 16), (128, 128), (300, 208), (132, 400), (4096, 1024),
+                                   (1028, 4112)])
+def test_transpose_u8_bit_exact(dev, shape):
+    """Every byte lands at its transposed place: whole and partial 128 x 128
+    tiles, rows not a multiple of 128 or 16, padded leading dimensions."""
+    from bitsparse_amd.src import hip_operators as H
+    R, C = shape
+    a = np.random.default_rng(R * 131 + C).integers(0, 256, size=(R, C), dtype=np.uint8)
+    x = torch.from_numpy(a).to(dev)
+    assert (H.transpose_u8(x).cpu().numpy() == a.T).all()
+    # strided input (row stride C + 32) into a strided output (row stride R + 4)
+    big = torch.zeros((R, C + 32), dtype=torch.uint8, device=dev)
+    big[:, :C] = x
+    obig = torch.full((C, R + 4), 7, dtype=torch.uint8, device=dev)
+    H.transpose_u8(big[:, :C], out=obig[:, :R])
+    ob = obig.cpu().numpy()
+    assert (ob[:, :R] == a.T).all() and (ob[:, R:] == 7).all()
+
+
+def test_transpose_u8_fp8_view_and_row_major_bytes(dev):
+    """fp8 codes keep their bits; row_major_bytes copies a transposed view
+    through the kernel and returns a row-major tensor unchanged."""
+    from bitsparse_amd.src import hip_operators as H
+    a = np.random.default_rng(9).integers(0, 256, size=(256, 512), dtype=np.uint8)
+    q = torch.from_numpy(a).to(dev).view(torch.float8_e4m3fn)
+    assert H.row_major_bytes(q) is q
+    r = H.row_major_bytes(q.t())
+    assert r.is_contiguous() and r.dtype == torch.float8_e4m3fn
+    assert (r.view(torch.uint8).cpu().numpy() == a.T).all()
+
+
+def test_transpose_u8_refuses_unsupported_shapes(dev):
+    """Invalid arguments come back as ValueError (BS_ERR_INVALID)."""
+    from bitsparse_amd.src import hip_operators as H
+    x = torch.zeros((8, 24), dtype=torch.uint8, device=dev)          # C % 16 != 0
+    assert not H.transpose_u8_supported(x)
+    with pytest.raises(ValueError, match="C must be a multiple of 16 and R of 4"):
+        H.transpose_u8(x)
+    y = torch.zeros((6, 32), dtype=torch.uint8, device=dev)          # R % 4 != 0
+    assert not H.transpose_u8_supported(y)
+    with pytest.raises(ValueError, match="C must be a multiple of 16 and R of 4"):
+        H.transpose_u8(y)
+    z = torch.zeros((6, 24), dtype=torch.uint8, device=dev)          # falls back to torch's copy
+    assert torch.equal(H.row_major_bytes(z.t()), z.t().contiguous())
