@@ -179,6 +179,45 @@ __global__ __launch_bounds__(256) void transpose_u8_kernel(const uint8_t* in, in
     }
 }
 
+
+// e4m3fn -> bf16 bits, exact (every e4m3fn value is a bf16 value); NaN codes
+// give 0x7fc0, the quiet NaN torch's float8 -> bfloat16 cast produces
+__device__ __forceinline__ uint32_t e4m3_to_bf16_bits(uint32_t c)
+{
+    const uint32_t s = (c & 0x80u) << 8, a = c & 0x7fu;
+    if (a == 0x7fu) return 0x7fc0u;
+    const uint32_t e = a >> 3, m = a & 7u;
+    if (e != 0u) return s | ((e + 120u) << 7) | (m << 4);
+    if (m == 0u) return s;
+    const uint32_t p = 31u - (uint32_t)__builtin_clz(m);       // subnormal m 2^-9 = 1.f 2^(p-9)
+    return s | ((p + 118u) << 7) | ((m << (7u - p)) & 0x7fu);
+}
+
+// out[i] = bf16(in[i]) for e4m3fn codes: 16 codes per lane (one 16-byte load,
+// two 16-byte stores), grid-stride; a tail of n % 16 codes element by element
+__global__ __launch_bounds__(256) void widen_e4m3_kernel(const uint8_t* in, int64_t n, uint16_t* out)
+{
+    const int64_t groups = n / 16;
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    for (int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x; g < groups; g += stride) {
+        const uint4 v = *reinterpret_cast<const uint4*>(in + g * 16);
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+        uint32_t o[8];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            o[2 * k] = e4m3_to_bf16_bits(w[k] & 0xffu) | (e4m3_to_bf16_bits((w[k] >> 8) & 0xffu) << 16);
+            o[2 * k + 1] = e4m3_to_bf16_bits((w[k] >> 16) & 0xffu) | (e4m3_to_bf16_bits(w[k] >> 24) << 16);
+        }
+        uint4* dst = reinterpret_cast<uint4*>(out + g * 16);
+        dst[0] = uint4{o[0], o[1], o[2], o[3]};
+        dst[1] = uint4{o[4], o[5], o[6], o[7]};
+    }
+    if (blockIdx.x == 0 && threadIdx.x < (unsigned)(n - groups * 16)) {
+        const int64_t i = groups * 16 + threadIdx.x;
+        out[i] = (uint16_t)e4m3_to_bf16_bits(in[i]);
+    }
+}
+
 }  // namespace bs
 
 using namespace bs;
@@ -267,5 +306,24 @@ extern "C" int bs_transpose_u8(const void* in, int64_t R, int64_t C, int64_t ld_
                        (const uint8_t*)in, R, C, ld_in, (uint8_t*)out, ld_out, (uint32_t)tiles_c);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(BS_ERR_HIP, "bs_transpose_u8 launch: %s", hipGetErrorString(e));
+    return BS_OK;
+}
+
+extern "C" int bs_widen_e4m3fn(const void* in, int64_t n, void* out, void* stream)
+{
+    clear_error();
+    if (n < 0) return set_error(BS_ERR_INVALID, "bs_widen_e4m3fn: negative n");
+    if (n == 0) return BS_OK;
+    if (in == nullptr || out == nullptr) return set_error(BS_ERR_INVALID, "bs_widen_e4m3fn: null pointer");
+    if (((uintptr_t)in) % 16 != 0 || ((uintptr_t)out) % 16 != 0)
+        return set_error(BS_ERR_INVALID, "bs_widen_e4m3fn: in and out must be 16-byte aligned");
+    const int64_t groups = n / 16;
+    int64_t blocks = (groups + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    if (blocks < 1) blocks = 1;
+    hipLaunchKernelGGL(widen_e4m3_kernel, dim3((uint32_t)blocks), dim3(256), 0, (hipStream_t)stream,
+                       (const uint8_t*)in, n, (uint16_t*)out);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(BS_ERR_HIP, "bs_widen_e4m3fn launch: %s", hipGetErrorString(e));
     return BS_OK;
 }

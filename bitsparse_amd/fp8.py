@@ -111,6 +111,11 @@ class MatmulFp8(Function):
             ctx.save_for_backward(a, b)
             ctx.given_scales = (a_scale, b_scale)
         ctx.grad_dtypes = (opa.codes.dtype, opb.codes.dtype)
+        ctx.in_dtypes = (a.dtype, b.dtype)
+        # b given as a transposed view of row-major storage (W.T): its
+        # gradient is formed in that storage's layout, so that autograd hands
+        # it to W without a layout copy
+        ctx.b_transposed = b.dim() == 2 and not b.is_contiguous() and b.t().is_contiguous()
         return fp8_gemm(opa, opb, torch.bfloat16)
 
     @staticmethod
@@ -124,9 +129,25 @@ class MatmulFp8(Function):
             opb = as_fp8_operand(b, ctx.given_scales[1])
         g = Fp8Operand(*to_fp8(grad_output))
         need_a, need_b = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
-        grad_a = fp8_gemm(g, opb.T, _grad_dtype(ctx.grad_dtypes[0])) if need_a else None
-        grad_b = fp8_gemm(opa.T, g, _grad_dtype(ctx.grad_dtypes[1])) if need_b else None
+        grad_a = grad_b = None
+        if need_a:
+            grad_a = _as_input_dtype(fp8_gemm(g, opb.T, _grad_dtype(ctx.grad_dtypes[0])), ctx.in_dtypes[0])
+        if need_b:
+            if ctx.b_transposed:
+                # (a^T g)^T = g^T a, delivered as a transposed view
+                grad_b = _as_input_dtype(fp8_gemm(g.T, opa, _grad_dtype(ctx.grad_dtypes[1])), ctx.in_dtypes[1]).t()
+            else:
+                grad_b = _as_input_dtype(fp8_gemm(opa.T, g, _grad_dtype(ctx.grad_dtypes[1])), ctx.in_dtypes[1])
         return grad_a, grad_b, None, None
+
+
+def _as_input_dtype(grad: Tensor, in_dtype: torch.dtype) -> Tensor:
+    """An e4m3fn gradient of a bf16 input widened to bf16 by the HIP kernel
+    (exact; the cast autograd would otherwise make with torch's float8 copy)."""
+    if grad.dtype == torch.float8_e4m3fn and in_dtype == torch.bfloat16:
+        from .src import hip_operators as ops
+        return ops.widen_e4m3fn(grad)
+    return grad
 
 
 def matmul(a: Tensor, b: Tensor, fp8: bool, a_scale: Tensor | None = None,

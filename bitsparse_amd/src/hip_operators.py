@@ -285,6 +285,24 @@ def transpose_u8_supported(x: Tensor) -> bool:
             x.shape[0] % 4 == 0 and x.stride(0) % 16 == 0 and x.data_ptr() % 16 == 0)
 
 
+def widen_e4m3fn(x: Tensor) -> Tensor:
+    """bf16 copy of an e4m3fn tensor (exact; NaN -> 0x7fc0 as torch's cast)
+    through bs_widen_e4m3fn, in x's layout when x is row-major or a
+    transposed view of row-major storage."""
+    if x.dtype != torch.float8_e4m3fn:
+        raise TypeError("widen_e4m3fn expects a float8_e4m3fn tensor")
+    if x.dim() == 2 and not x.is_contiguous() and x.t().is_contiguous():
+        return widen_e4m3fn(x.t()).t()
+    x = x.contiguous()
+    out = torch.empty(x.shape, device=x.device, dtype=torch.bfloat16)
+    if x.data_ptr() % 16 != 0:
+        return x.to(torch.bfloat16)
+    L = _lib.load()
+    check(L.bs_widen_e4m3fn(x.data_ptr(), x.numel(), out.data_ptr(), stream_handle(x.device)),
+          "bs_widen_e4m3fn")
+    return out
+
+
 def row_major_bytes(x: Tensor) -> Tensor:
     """A 2-D 1-byte tensor in row-major layout: x itself when it is, the
     transpose kernel's copy when x is a transposed view of row-major storage

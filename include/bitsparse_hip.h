@@ -302,6 +302,14 @@ int bs_transpose_u8(const void* in, int64_t R, int64_t C, int64_t ld_in, void* o
                     void* stream);
 
 /*
+ * out[i] = bf16(in[i]) for n e4m3fn codes (exact; NaN codes give 0x7fc0, as
+ * torch's float8 -> bfloat16 cast does).  Replaces autograd's cast of the
+ * e4m3fn gradients that lib_sparse/fp8.py:105-113 returns for bf16 inputs.
+ * in and out 16-byte aligned.
+ */
+int bs_widen_e4m3fn(const void* in, int64_t n, void* out, void* stream);
+
+/*
  * C[M, N] (bf16, row-major, row stride N) = A @ B, where A is a dense bf16
  * [M, K] matrix and B is a compressed [K, N] activation (vals 16-byte
  * aligned) decoded tile by tile into LDS (never written to HBM dense).

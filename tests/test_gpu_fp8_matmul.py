@@ -245,3 +245,42 @@ def test_transpose_u8_refuses_unsupported_shapes(dev):
         H.transpose_u8(y)
     z = torch.zeros((6, 24), dtype=torch.uint8, device=dev)          # falls back to torch's copy
     assert torch.equal(H.row_major_bytes(z.t()), z.t().contiguous())
+
+
+# ---------------------------------------------------------------------------
+# gradient delivery: e4m3fn gradients of bf16 inputs widened by
+# bs_widen_e4m3fn, and a W.T operand's gradient formed in W's own layout
+# ---------------------------------------------------------------------------
+def test_widen_e4m3fn_every_code(dev):
+    """All 256 codes (NaN, +-0, subnormals, +-448), a length that is not a
+    multiple of 16, and a transposed view: bit-identical to torch's cast on
+    the GPU and on the CPU."""
+    from bitsparse_amd.src import hip_operators as H
+    codes = torch.arange(256, dtype=torch.uint8).repeat(5)[:1000]
+    q = codes.view(torch.float8_e4m3fn)
+    want_cpu = q.to(torch.bfloat16).view(torch.int16)
+    got = H.widen_e4m3fn(q.to(dev))
+    assert torch.equal(got.view(torch.int16).cpu(), want_cpu)
+    assert torch.equal(got.view(torch.int16), q.to(dev).to(torch.bfloat16).view(torch.int16))
+    m = q[:992].reshape(31, 32).to(dev)
+    gt = H.widen_e4m3fn(m.t())
+    assert gt.shape == (32, 31) and gt.t().is_contiguous()
+    assert torch.equal(gt.view(torch.int16), m.t().to(torch.bfloat16).view(torch.int16))
+
+
+def test_transposed_weight_operand_gradient(dev):
+    """matmul(x, W.T): W.grad arrives in W's row-major layout (formed as
+    g^T x), the same saturating e4m3fn rounding of the same product as the
+    gradient of an untransposed operand, and x.grad is bit-identical."""
+    from bitsparse_amd.fp8 import matmul, to_fp8
+    a, b, dy = _operands(256, 384, 320, seed=6)
+    W = b.t().contiguous()                            # [N, K]: the layer's weight layout
+    ad, Wd = a.to(dev).requires_grad_(), W.to(dev).requires_grad_()
+    matmul(ad, Wd.T, True).backward(dy.to(dev))
+    assert Wd.grad.is_contiguous() and Wd.grad.dtype == torch.bfloat16
+    qa, sa = to_fp8(a.to(dev))
+    qg, sg = to_fp8(dy.to(dev))
+    _check_rounded(Wd.grad.t(), qa.t(), sa, qg, sg, _round_e4m3_sat, what="dW")
+    a2, b2 = a.to(dev).requires_grad_(), b.to(dev).requires_grad_()
+    matmul(a2, b2, True).backward(dy.to(dev))
+    assert torch.equal(ad.grad, a2.grad)
