@@ -242,6 +242,18 @@ def bench_kernels(steps: int, warmup: int, copy_gbs: float):
                 meta + nnz + 2 * M * N)
         del r, g, o
         torch.cuda.empty_cache()
+    # fp8 GEMM operand plumbing at the configs[3] weight / activation size
+    # (4096 x 16384 bytes): the layout change and the gradient widening
+    R8, C8 = 4096, 16384
+    q8 = torch.randint(0, 256, (R8, C8), dtype=torch.uint8, device=dev)
+    t8 = torch.empty((C8, R8), dtype=torch.uint8, device=dev)
+    rec("transpose_u8 (fp8 operand layout) 4096x16384", [R8, C8],
+        _timed(lambda: H.transpose_u8(q8, out=t8), steps, warmup), 2 * R8 * C8)
+    f8 = (q8 & 0x77).view(torch.float8_e4m3fn)
+    rec("widen_e4m3fn (fp8 gradient to bf16) 4096x16384", [R8, C8],
+        _timed(lambda: H.widen_e4m3fn(f8), steps, warmup), 3 * R8 * C8)
+    del q8, t8, f8
+    torch.cuda.empty_cache()
     return out
 
 
