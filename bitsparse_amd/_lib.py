@@ -57,6 +57,7 @@ _SIGNATURES = {
     "bs_quantize_e4m3fn": [_vp, _i64, _vp, _vp, _vp, _i64, _u32, _vp],
     "bs_transpose_u8": [_vp, _i64, _i64, _i64, _vp, _i64, _vp],
     "bs_widen_e4m3fn": [_vp, _i64, _vp, _vp],
+    "bs_relu2_square_amax": [_vp, _i64, ctypes.c_float, _vp, _i64, _u32, _vp],
     "bs_gemm_compressed_b_workspace_bytes": [_i64, _i64, _i64, _int],
     "bs_gemm_compressed_b": [_vp, _i64, _i64, _i64, _int, _vp, _int, _i64, _vp, _vp, _vp, _i64, _int, _f32,
                              _vp, _vp, _vp, _i64, _vp],

@@ -218,6 +218,55 @@ __global__ __launch_bounds__(256) void widen_e4m3_kernel(const uint8_t* in, int6
     }
 }
 
+
+// The ReLU^2 forward's h = k * r^2 as torch forms it (h.square_() then
+// h.mul_(k): bf16(bf16(r * r) * k), a NaN as torch's 0x7fc0), written back in
+// place, with amax|h| into the slot: the square and scale passes and the
+// amax pass of to_fp8(h) in one read and one write of r.
+__device__ __forceinline__ uint32_t relu2_sq_bits(uint32_t b, float k)
+{
+    const float r = bf16_to_f32(b);
+    const uint32_t sq = f32_to_bf16(r * r);
+    const uint32_t h = f32_to_bf16(bf16_to_f32(sq) * k);
+    return (h & 0x7fffu) > 0x7f80u ? 0x7fc0u : h;
+}
+
+template <bool NT>
+__global__ __launch_bounds__(kFp8Threads) void relu2_square_amax_kernel(uint16_t* x, int64_t n, float k,
+                                                                        uint64_t* slot, uint32_t epoch)
+{
+    __shared__ uint32_t s_w[kFp8Threads / 64];
+    const int tid = threadIdx.x;
+    uint32_t m = 0;
+    const int64_t nvec = ((((uintptr_t)x) & 15u) == 0) ? n / 8 : 0;
+    const int64_t stride = (int64_t)gridDim.x * kFp8Threads;
+    uint4* xv = reinterpret_cast<uint4*>(x);
+    for (int64_t i = (int64_t)blockIdx.x * kFp8Threads + tid; i < nvec; i += stride) {
+        const uint4 v = ld16<NT>(xv + i);
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+        uint32_t o[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const uint32_t lo = relu2_sq_bits(w[q] & 0xffffu, k), hi = relu2_sq_bits(w[q] >> 16, k);
+            m = max(m, max(lo & 0x7fffu, hi & 0x7fffu));
+            o[q] = lo | (hi << 16);
+        }
+        st16<NT>(xv + i, uint4{o[0], o[1], o[2], o[3]});
+    }
+    for (int64_t j = nvec * 8 + (int64_t)blockIdx.x * kFp8Threads + tid; j < n; j += stride) {
+        const uint32_t h = relu2_sq_bits(x[j], k);
+        m = max(m, h & 0x7fffu);
+        x[j] = (uint16_t)h;
+    }
+    m = wave_max_u32(m);
+    if ((tid & 63) == 0) s_w[tid >> 6] = m;
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < kFp8Threads / 64; w++) m = max(m, s_w[w]);
+        atomicMax((unsigned long long*)slot, (unsigned long long)(((uint64_t)epoch << 32) | m));
+    }
+}
+
 }  // namespace bs
 
 using namespace bs;
@@ -325,5 +374,32 @@ extern "C" int bs_widen_e4m3fn(const void* in, int64_t n, void* out, void* strea
                        (const uint8_t*)in, n, (uint16_t*)out);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(BS_ERR_HIP, "bs_widen_e4m3fn launch: %s", hipGetErrorString(e));
+    return BS_OK;
+}
+
+extern "C" int bs_relu2_square_amax(void* r, int64_t n, float k, void* workspace, int64_t workspace_bytes,
+                                    uint32_t epoch, void* stream)
+{
+    clear_error();
+    if (n < 0) return set_error(BS_ERR_INVALID, "bs_relu2_square_amax: negative n");
+    if (workspace == nullptr || workspace_bytes < kWsHeaderBytes)
+        return set_error(BS_ERR_INVALID, "bs_relu2_square_amax: workspace too small");
+    if (epoch == 0 || epoch >= (1u << 30)) return set_error(BS_ERR_INVALID, "bs_relu2_square_amax: epoch out of range");
+    if (n > 0 && r == nullptr) return set_error(BS_ERR_INVALID, "bs_relu2_square_amax: null input");
+    if (((uintptr_t)r) & 1u) return set_error(BS_ERR_INVALID, "bs_relu2_square_amax: input misaligned");
+    if (int rc = refuse_capture((hipStream_t)stream, "bs_relu2_square_amax")) return rc;
+    if (n == 0) return BS_OK;
+    uint64_t* slot = reinterpret_cast<uint64_t*>((uint8_t*)workspace + kWsAmaxOffset);
+    int dev = 0, cus = 0;
+    if (stream_device((hipStream_t)stream, &dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+        cus = 256;
+    uint32_t grid = grid_for(n);
+    if (grid > (uint32_t)(4 * cus)) grid = (uint32_t)(4 * cus);
+    auto kernel = use_nontemporal(2 * n) ? relu2_square_amax_kernel<true> : relu2_square_amax_kernel<false>;
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(kFp8Threads), 0, (hipStream_t)stream, (uint16_t*)r, n, k, slot,
+                       epoch);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(BS_ERR_HIP, "bs_relu2_square_amax launch: %s", hipGetErrorString(e));
     return BS_OK;
 }

@@ -19,7 +19,7 @@ from .config import RELU2_SCALE
 from .fp8 import is_fp8, matmul, to_fp8
 from .src.functions import (fused_linear_relu_ok, linear_relu_and_compress, relu_and_compress,
                             relu_quantize_and_compress)
-from .src.hip_operators import mask_with_bitmask_, relu2_grad_sparse_
+from .src.hip_operators import mask_with_bitmask_, quantize_e4m3fn, relu2_grad_sparse_, relu2_square_amax_
 from .src.sparse_matmul import AspB, AspRelu2B
 
 # FFNRelu / FFNRelu2 with bf16 storage into a TensorBuffer run the up-projection
@@ -124,10 +124,15 @@ class Relu2Linear(Function):
             h, h_sparse = relu_and_compress(z, sparse_data, pack_sbit)
         ctx.h_sparse = h_sparse
 
+        if is_fp8(storage_dtype):
+            # h.square_(); h.mul_(k) and the amax of to_fp8(h) in one pass
+            # (h still ends up in z, as the in-place ops leave it)
+            epoch = relu2_square_amax_(h, RELU2_SCALE)
+            h8, h_scale = quantize_e4m3fn(h, epoch)
+            return matmul(h8, W.T, True, a_scale=h_scale)
         h.square_()
         h.mul_(RELU2_SCALE)
-        y = matmul(h, W.T, is_fp8(storage_dtype))
-        return y
+        return matmul(h, W.T, False)
 
     @staticmethod
     @torch.compiler.disable

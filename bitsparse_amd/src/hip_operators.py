@@ -250,6 +250,23 @@ def amax_into_workspace(x: Tensor, relu: bool = False) -> int:
     return epoch
 
 
+def relu2_square_amax_(h: Tensor, k: float) -> int:
+    """h <- bf16(bf16(h * h) * k) in place (torch's h.square_(); h.mul_(k))
+    and amax|h| into the stream's workspace; returns the epoch that tags it
+    (quantize_e4m3fn(h, epoch) is then to_fp8(h))."""
+    require_device(h, "relu2_square_amax_")
+    _contig(h, "h")
+    if h.dtype != torch.bfloat16:
+        raise TypeError("relu2_square_amax_ expects a bfloat16 tensor")
+    L = _lib.load()
+    ws = _lib.workspace_for(h.device)
+    ws.ensure(256)
+    epoch = ws.next_epoch(reserve=2)
+    check(L.bs_relu2_square_amax(h.data_ptr(), h.numel(), float(k), ws.buf.data_ptr(), ws.nbytes, epoch,
+                                 stream_handle(h.device)), "bs_relu2_square_amax")
+    return epoch
+
+
 def quantize_e4m3fn(x: Tensor, amax_epoch: int) -> tuple[Tensor, Tensor]:
     """(e4m3fn tensor, fp32 0-d scale) from the amax of ``amax_epoch``."""
     L = _lib.load()

@@ -290,6 +290,17 @@ int bs_quantize_e4m3fn(const void* x, int64_t n, void* q_out, float* scale_out,
                        void* stream);
 
 /*
+ * r <- k * r^2 in place on a bf16 array, rounded as h.square_() then
+ * h.mul_(k) round (bf16(bf16(r*r) * k), NaN -> 0x7fc0), and amax|h| into
+ * the workspace's amax slot tagged with `epoch` (then bs_quantize_e4m3fn
+ * with that epoch gives to_fp8(h)).  Replaces the h.square_(); h.mul_(k)
+ * and the amax of to_fp8(h) in the fp8 ReLU^2 forward of
+ * lib_sparse/layers.py:103-120 (with fp8.py:123-129).  Refuses graph capture.
+ */
+int bs_relu2_square_amax(void* r, int64_t n, float k, void* workspace, int64_t workspace_bytes,
+                         uint32_t epoch, void* stream);
+
+/*
  * out[c * ld_out + r] = in[r * ld_in + c] for an [R, C] byte matrix: the
  * fp8 operand layout change in front of the fp8 GEMM.  Replaces the
  * a.contiguous() / b.T.contiguous().T / a_fp8.T.contiguous() copies of

@@ -100,3 +100,58 @@ def test_ffn_relu2_fp8_storage_matches_fp8_dense(dev):
         scale = b.abs().max().item() + 1e-6
         err = (a.float() - b.float()).abs().max().item() / scale
         assert err < 2 ** -3, f"{name}: {err:.3e}"
+
+
+@pytest.mark.parametrize("k", [1.0, 0.5, 3.0])
+@pytest.mark.parametrize("case", ["finite", "inf", "nan"])
+def test_relu2_square_amax_matches_torch_ops(dev, k, case):
+    """The fused pass of the fp8 ReLU^2 forward (reference layers.py:103-120:
+    h.square_(); h.mul_(k); to_fp8(h)) against torch's own ops on the same GPU:
+    h bit for bit (-0, subnormals, negatives; with Inf, or NaN of both signs,
+    or values whose square overflows), then the amax it leaves gives the same
+    codes and the same scale bits as to_fp8(h)."""
+    from bitsparse_amd.fp8 import to_fp8
+    from bitsparse_amd.src import hip_operators as H
+    from tests.helpers import special_bf16
+    xb = special_bf16((257, 136), seed=31).view(torch.int16).clone()
+    mag = xb.view(torch.int16).to(torch.int32) & 0x7fff
+    xb[mag >= 0x7f80] = 0x3f80                           # no Inf / NaN unless asked for
+    xb[mag == 0x7f7f] = 0x4100
+    if case == "inf":
+        xb.view(-1)[:3] = torch.tensor([0x7f80, -0x80, 0x5f80], dtype=torch.int16)   # +-Inf, 2^64 (square -> Inf)
+    if case == "nan":
+        xb.view(-1)[:2] = torch.tensor([0x7fc0, -0x40], dtype=torch.int16)           # +-NaN
+    x = xb.to(dev).view(torch.bfloat16)
+    want = x.clone()
+    want.square_()
+    want.mul_(k)
+    h = x.clone()
+    epoch = H.relu2_square_amax_(h, k)
+    assert torch.equal(h.view(torch.int16), want.view(torch.int16))
+    q, s = H.quantize_e4m3fn(h, epoch)
+    qt, st = to_fp8(want)
+    assert torch.equal(q.view(torch.uint8), qt.view(torch.uint8))
+    assert torch.equal(s.view(torch.int32), st.view(torch.int32))
+    if case == "finite":
+        assert 0 < int((q.view(torch.uint8) & 0x7f).max().item()) < 0x7f   # real codes, not NaN
+
+
+def test_ffn_relu2_fp8_forward_bit_identical_to_dense(dev):
+    """With the fused square / scale / amax pass the compressed fp8 layer's y
+    is bit-identical to the fp8 dense comparator's (the same h8, scale and
+    GEMM), and z ends up holding k * relu(z)^2 as the in-place ops leave it."""
+    from bitsparse_amd.dense import DenseFFNRelu2Fp8
+    from bitsparse_amd.fp8 import matmul
+    from bitsparse_amd.layers import FFNRelu2, Relu2Linear
+    from bitsparse_amd.config import RELU2_SCALE
+    x, W1, W2, _ = _mlp_inputs(256, 256, 512, seed=9)
+    xs, W1s, W2s = (t.to(dev) for t in (x, W1, W2))
+    ys = FFNRelu2.apply(xs, W1s, W2s, storage_dtype=torch.float8_e4m3fn)
+    yd = DenseFFNRelu2Fp8.apply(xs, W1s, W2s)
+    assert torch.equal(ys.view(torch.int16), yd.view(torch.int16))
+    z = matmul(xs, W1s.T, True)
+    want = z.clone().relu_()
+    want.square_()
+    want.mul_(RELU2_SCALE)
+    Relu2Linear.apply(z, W2s, None, False, torch.float8_e4m3fn)
+    assert torch.equal(z.view(torch.int16), want.view(torch.int16))
