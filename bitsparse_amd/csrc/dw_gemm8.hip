@@ -16,7 +16,11 @@
 //     code sorts above every finite one, as in the amax kernel), or |D(0)| of
 //     the cleared elements.  Bq(c) = e4m3fn_RNE(D(c) / sB) with one correctly
 //     rounded division, the to_fp8 rule, so the decoded operand is bit for
-//     bit to_fp8(unpack_relu2_batch_(B)).
+//     bit to_fp8(unpack_relu2_batch_(B)).  The tensor's value run is mapped
+//     through the table once, into the workspace (nnz bytes read and
+//     written), and the GEMM stages the mapped codes: every row block of C
+//     reads the run, so mapping while staging would repeat the table lookups
+//     once per row block.
 // Replaces "decompress B to HBM, re-quantize, library fp8 GEMM" (hipBLASLt
 // scaled_mm) of the reference's fp8 AspB / AspRelu2B.
 //
@@ -26,7 +30,7 @@
 // K-step = 64 tokens = one row of B tiles = one MFMA deep.  Per step:
 //   * the step's B tiles are decoded into a double-buffered LDS tile (one
 //     8-byte chunk per lane per decode row): value runs are loaded one step
-//     ahead, staged in LDS (mapped through the code table on the way), and
+//     ahead, staged in LDS, and
 //     each chunk is built from an 8-byte window of its run with v_alignbyte
 //     and two v_perm_b32 (selectors from a 256-entry table per bitmask byte);
 //   * B fragments come out of the row-major tile with ds_read_b64_tr_b8
@@ -70,8 +74,7 @@ struct Gemm8Cfg {
     static constexpr int OFF_BM = OFF_RUN + 3 * NT * kRun8Slots * 16;   // bm_s[NWAVES][64] uint64
     static constexpr int OFF_RP = OFF_BM + NWAVES * 64 * 8;     // rp_s[NWAVES][64] uint32
     static constexpr int OFF_SEL = OFF_RP + NWAVES * 64 * 4;    // sel_s[256] uint2
-    static constexpr int OFF_LUT = OFF_SEL + 256 * 8;           // lut_s[256] bytes
-    static constexpr int OFF_PF = OFF_LUT + 256;                 // pf_s[NT][kMaxSteps] uint2: prefix[t], prefix[t+1]
+    static constexpr int OFF_PF = OFF_SEL + 256 * 8;            // pf_s[NT][kMaxSteps] uint2: prefix[t], prefix[t+1]
     static constexpr int ST_P = WAVE_N + 4;                      // epilogue staging pitch (floats)
     static constexpr int LDS_MAIN = OFF_PF + NT * kMaxSteps * 8;
     static constexpr int LDS_EPI = NWAVES * 16 * ST_P * 4;      // the epilogue reuses the space
@@ -100,7 +103,6 @@ struct Gemm8Args {
     int64_t N;
     uint32_t grid_n;              // B tiles along N
     uint32_t tiles_m, tiles_n;    // C tiles
-    const uint8_t* lut;           // code -> B code (square), 256 bytes
     const float* a_scale;
     const float* b_scale;         // sB
     uint16_t* C;                  // [M, N] bf16 (no split)
@@ -109,9 +111,8 @@ struct Gemm8Args {
     uint32_t ksteps_per_split;
 };
 
-// LUT: stored codes are mapped through lut_s while staged.  FMT_B: MFMA
-// format of B (0 e4m3, 1 e5m2).
-template <typename CFG, bool LUT, int FMT_B>
+// FMT_B: MFMA format of B (0 e4m3, 1 e5m2).
+template <typename CFG, int FMT_B>
 __global__ __launch_bounds__(CFG::THREADS, 1) void gemm_cb8_kernel(Gemm8Args a)
 {
     constexpr int NT = CFG::NT, DW = CFG::DW, CH = CFG::CH, BP = CFG::BP, IM = CFG::IM, JN = CFG::JN;
@@ -124,7 +125,6 @@ __global__ __launch_bounds__(CFG::THREADS, 1) void gemm_cb8_kernel(Gemm8Args a)
     uint64_t* bm_s = reinterpret_cast<uint64_t*>(lds + CFG::OFF_BM);
     uint32_t* rp_s = reinterpret_cast<uint32_t*>(lds + CFG::OFF_RP);
     uint2* sel_s = reinterpret_cast<uint2*>(lds + CFG::OFF_SEL);
-    uint8_t* lut_s = lds + CFG::OFF_LUT;
     uint2* pf_s = reinterpret_cast<uint2*>(lds + CFG::OFF_PF);
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -152,7 +152,7 @@ __global__ __launch_bounds__(CFG::THREADS, 1) void gemm_cb8_kernel(Gemm8Args a)
     const int last = nsteps - 1;
 
     // selectors of bitmask byte x: set element e takes window byte rank(e),
-    // 0x0c gives 0x00; the code table
+    // 0x0c gives 0x00
     if (tid < 256) {
         uint32_t sel[2] = {0x0c0c0c0cu, 0x0c0c0c0cu};
         uint32_t rank = 0;
@@ -164,12 +164,13 @@ __global__ __launch_bounds__(CFG::THREADS, 1) void gemm_cb8_kernel(Gemm8Args a)
             }
         }
         sel_s[tid] = uint2{sel[0], sel[1]};
-        lut_s[tid] = LUT ? a.lut[tid] : (uint8_t)tid;
     }
-    // a cleared element decodes to the code of 0 (not 0x00 for k < 0 or a
-    // NaN scale): fixed up after the permutes when different
-    const uint32_t zero_b = LUT ? (uint32_t)a.lut[0] : 0u;
-    const bool zfix = zero_b != 0u;
+    // A cleared element decodes to 0x00.  For square = 1 the reference's
+    // operand holds to_fp8(D(0)) there: +0 (0x00), -0 (0x80, for k < 0) or
+    // NaN.  -0 in place of +0 leaves every output bit unchanged (its products
+    // are zeros, and the fp32 accumulators start at +0, to which a zero of
+    // either sign adds nothing); a NaN D(0) makes amax, sB and so every
+    // output NaN whatever B holds.
 
     // ---- prefix[t], prefix[t+1] of every step of each B tile column of the
     // workgroup, in LDS (nsteps <= kMaxSteps)
@@ -202,11 +203,8 @@ __global__ __launch_bounds__(CFG::THREADS, 1) void gemm_cb8_kernel(Gemm8Args a)
     // wave (u / 64) % DW of the tile's waves, pass u / (64 DW))
     uint4 rr[2][RXD];
     int rr_nunits[2] = {0, 0};
-    auto load_run = [&](int s, auto SL) __attribute__((always_inline)) {
+    auto load_run_at = [&](int64_t e0, int nunits, auto SL) __attribute__((always_inline)) {
         constexpr int SLOT = decltype(SL)::value;
-        int64_t e0;
-        int phase, nunits;
-        run_geom(s, e0, phase, nunits);
         const int64_t avail = a.vals_numel - e0;       // bytes readable from e0
         const bool ok = e0 >= 0 && avail > 0 && nunits > 0;
         int64_t bytes = ok ? avail : 0;
@@ -230,29 +228,19 @@ __global__ __launch_bounds__(CFG::THREADS, 1) void gemm_cb8_kernel(Gemm8Args a)
             }
         }
     };
+    auto load_run = [&](int s, auto SL) __attribute__((always_inline)) {
+        int64_t e0;
+        int phase, nunits;
+        run_geom(s, e0, phase, nunits);
+        load_run_at(e0, nunits, SL);
+    };
     auto store_run = [&](int buf, auto SL) __attribute__((always_inline)) {
         constexpr int SLOT = decltype(SL)::value;
         uint4* dst = run_s + (buf * NT + tw) * kRun8Slots;
 #pragma unroll
         for (int x = 0; x < RXD; x++) {
             const int u = (x * DW + tq) * 64 + lane;
-            if ((x * DW + tq) * 64 < rr_nunits[SLOT] && u < rr_nunits[SLOT]) {
-                const uint4 v = rr[SLOT][x];
-                if constexpr (LUT) {
-                    // one dword at a time (few live registers)
-                    uint32_t* d32 = reinterpret_cast<uint32_t*>(dst + u);
-                    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-                    for (int d = 0; d < 4; d++) {
-                        uint32_t o = 0;
-#pragma unroll
-                        for (int e = 0; e < 4; e++) o |= (uint32_t)lut_s[(w[d] >> (8 * e)) & 0xffu] << (8 * e);
-                        d32[d] = o;
-                    }
-                } else {
-                    dst[u] = v;
-                }
-            }
+            if ((x * DW + tq) * 64 < rr_nunits[SLOT] && u < rr_nunits[SLOT]) dst[u] = rr[SLOT][x];
         }
     };
 
@@ -270,10 +258,7 @@ __global__ __launch_bounds__(CFG::THREADS, 1) void gemm_cb8_kernel(Gemm8Args a)
     const int dc = lane & 7, dg = lane >> 3;
     const uint64_t below_mask = dc == 0 ? 0ull : (~0ull >> (64 - 8 * dc));
     const int rbase = 8 * CH * tq;
-    auto decode_rows = [&](int s, uint64_t bmr) __attribute__((always_inline)) {
-        int64_t e0;
-        int phase, nunits;
-        run_geom(s, e0, phase, nunits);
+    auto decode_rows_at = [&](int phase, uint64_t bmr) __attribute__((always_inline)) {
         const uint32_t c = (uint32_t)__popcll(bmr);
         const uint32_t rp = wave_incl_scan(c) - c;
         bm_s[wave * 64 + lane] = bmr;
@@ -281,6 +266,12 @@ __global__ __launch_bounds__(CFG::THREADS, 1) void gemm_cb8_kernel(Gemm8Args a)
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+    auto decode_rows = [&](int s, uint64_t bmr) __attribute__((always_inline)) {
+        int64_t e0;
+        int phase, nunits;
+        run_geom(s, e0, phase, nunits);
+        decode_rows_at(phase, bmr);
     };
     struct Dec {
         uint64_t mrow;
@@ -329,20 +320,6 @@ __global__ __launch_bounds__(CFG::THREADS, 1) void gemm_cb8_kernel(Gemm8Args a)
             stage_s(CI, run32);
             stage_w(CI, dst);
         });
-    };
-    // cleared elements of this wave's rows of B_s[bb] -> zero_b
-    auto zero_fixup = [&](int bb) __attribute__((always_inline)) {
-        uint8_t* dst = dst_ptr(bb);
-        for (int i = 0; i < CH; i++) {
-            const int row = rbase + 8 * i + dg;
-            const uint32_t byte = (uint32_t)(bm_s[wave * 64 + row] >> (8 * dc)) & 0xffu;
-            uint2 v = *reinterpret_cast<const uint2*>(&dst[row * BP]);
-            uint32_t w[2] = {v.x, v.y};
-#pragma unroll
-            for (int e = 0; e < 8; e++)
-                if (!((byte >> e) & 1u)) w[e >> 2] = (w[e >> 2] & ~(0xffu << (8 * (e & 3)))) | (zero_b << (8 * (e & 3)));
-            *reinterpret_cast<uint2*>(&dst[row * BP]) = uint2{w[0], w[1]};
-        }
     };
 
     // ---- A fragments: lane l of block i holds row 32i + l%32, k = 32(l/32)
@@ -443,7 +420,6 @@ __global__ __launch_bounds__(CFG::THREADS, 1) void gemm_cb8_kernel(Gemm8Args a)
     if (nsteps > 0) {
         decode_rows(0, bmq[0]);
         decode(0, 0);
-        if (zfix) zero_fixup(0);
         bmq[0] = load_bm(min(2, last));
         load_run(min(2, last), IC<0>{});
     }
@@ -451,12 +427,17 @@ __global__ __launch_bounds__(CFG::THREADS, 1) void gemm_cb8_kernel(Gemm8Args a)
     auto iteration = [&](int s, auto RI) __attribute__((always_inline)) {
         constexpr int P = decltype(RI)::value;         // s & 1
         const int s1 = min(s + 1, last), s3 = min(s + 3, last);
-        decode_rows(s1, bmq[P ^ 1]);
+        // both steps' run geometry first: the two prefix reads share one
+        // LDS round trip (the row-table stores would otherwise order them)
+        int64_t e0a, e0b;
+        int pha, phb, nua, nub;
+        run_geom(s1, e0a, pha, nua);
+        run_geom(s3, e0b, phb, nub);
+        decode_rows_at(pha, bmq[P ^ 1]);
         bmq[P ^ 1] = load_bm(s3);
-        load_run(s3, IC<P ^ 1>{});
+        load_run_at(e0b, nub, IC<P ^ 1>{});
         load_a(s1, IC<P ^ 1>{});
         step(s, RI);
-        if (zfix) zero_fixup(P ^ 1);
         store_run((s + 2) % 3, IC<P>{});
         __syncthreads();
     };
@@ -632,9 +613,18 @@ __global__ __launch_bounds__(256) void code_max_kernel(Lut8Args a)
         const bs_rsrc rs = make_rsrc(a.vals + u0 * 16, (uint32_t)std::min<int64_t>(a.vals_numel - u0 * 16, 0xffffffffll));
         const int64_t stride = (int64_t)gridDim.x * 256;
         for (int64_t u = u0 + (int64_t)blockIdx.x * 256 + threadIdx.x; u < u1; u += stride) {
-            const uint4 v = load16(rs, (uint32_t)((u - u0) * 16));
-            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
             const int64_t e0 = u * 16;
+            uint32_t w[4];
+            if (e0 + 16 <= a.vals_numel) {
+                const uint4 v = load16(rs, (uint32_t)((u - u0) * 16));
+                w[0] = v.x, w[1] = v.y, w[2] = v.z, w[3] = v.w;
+            } else {
+                // the unit crosses the end of vals: its readable bytes one by one
+                w[0] = w[1] = w[2] = w[3] = 0u;
+                for (int e = 0; e < 16 && e0 + e < a.vals_numel; e++)
+                    w[e >> 2] |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rs, (int)((u - u0) * 16 + e), 0, 0)
+                                 << (8 * (e & 3));
+            }
 #pragma unroll
             for (int e = 0; e < 16; e++) {
                 const uint32_t c = (w[e >> 2] >> (8 * (e & 3))) & 0x7fu;
@@ -698,6 +688,54 @@ __global__ __launch_bounds__(256) void relu2_lut_kernel(Lut8Args a)
     }
     __syncthreads();
     a.lut[c] = (uint8_t)f32_to_e4m3(bf16_to_f32(x) / s_scale);
+}
+
+// square = 1: out[i] = lut[vals[vo + prefix[0] + i]] for i < n, n = the
+// run's length (prefix[T] - prefix[0], within vals and cap; cap a multiple of
+// 16, so the whole 16-byte units the GEMM reads stay inside out), and
+// *out_vo = -prefix[0]: the GEMM then finds tile t's run at out[prefix[t] +
+// *out_vo].  16 codes per thread and pass.
+__global__ __launch_bounds__(256) void map_codes_kernel(Lut8Args a, uint8_t* out, int64_t cap, int64_t* out_vo)
+{
+    __shared__ uint8_t t[256];
+    t[threadIdx.x] = a.lut[threadIdx.x];
+    const int64_t vo = a.vals_offset ? *a.vals_offset : 0;
+    const int64_t p0 = (int64_t)a.prefix[0];
+    const int64_t b0 = vo + p0;
+    int64_t n = (int64_t)a.prefix[a.T] - p0;
+    if (n > cap) n = cap;
+    if (b0 < 0 || b0 >= a.vals_numel) n = 0;
+    else if (n > a.vals_numel - b0) n = a.vals_numel - b0;
+    if (blockIdx.x == 0 && threadIdx.x == 0) *out_vo = -p0;
+    __syncthreads();
+    if (n <= 0) return;
+    // dword-aligned source base; sh = the run start's byte within its dword
+    const int64_t base = b0 & ~(int64_t)3;
+    const uint32_t sh = (uint32_t)(b0 & 3);
+    const int64_t readable = std::min<int64_t>(a.vals_numel - base, 0xffffffffll);
+    const bs_rsrc rs = make_rsrc(a.vals + base, (uint32_t)readable);
+    const int64_t stride = (int64_t)gridDim.x * 256 * 16;
+    for (int64_t j = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 16; j < n; j += stride) {
+        uint32_t w[5];
+        if (j + 20 <= readable) {
+            const uint4 v = load16(rs, (uint32_t)j);
+            w[0] = v.x, w[1] = v.y, w[2] = v.z, w[3] = v.w;
+            w[4] = load4(rs, (uint32_t)j + 16u);
+        } else {
+            // the window crosses the end of vals: its readable bytes one by one
+            w[0] = w[1] = w[2] = w[3] = w[4] = 0u;
+            for (int e = 0; e < 20 && j + e < readable; e++)
+                w[e >> 2] |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rs, (int)(j + e), 0, 0) << (8 * (e & 3));
+        }
+        uint32_t o[4];
+#pragma unroll
+        for (int d = 0; d < 4; d++) {
+            const uint32_t x = __builtin_amdgcn_alignbyte(w[d + 1], w[d], sh);
+            o[d] = (uint32_t)t[x & 0xffu] | ((uint32_t)t[(x >> 8) & 0xffu] << 8) |
+                   ((uint32_t)t[(x >> 16) & 0xffu] << 16) | ((uint32_t)t[x >> 24] << 24);
+        }
+        *reinterpret_cast<uint4*>(out + j) = uint4{o[0], o[1], o[2], o[3]};
+    }
 }
 
 __global__ void copy_scale_kernel(const float* src, float* dst, float* dst2)
@@ -767,18 +805,24 @@ static int64_t apk8_nkb(int64_t K) { return (K + kBK - 1) / kBK; }
 static int64_t apk8_bytes(int64_t M, int64_t K) { return (M + 31) / 32 * apk8_nkb(K) * 2048; }
 static int64_t up256(int64_t x) { return (x + 255) / 256 * 256; }
 constexpr int64_t kLutAreaBytes = 512 + 4 * kCodeMaxBlocks;     // lut[256], sB, code_max_kernel's maxima at 512
+// square = 1: room for the mapped value run (at most K N codes, whole 16-byte
+// units) and its offset word
+static int64_t map8_cap(int64_t K, int64_t N) { return (K * N + 15) / 16 * 16; }
+static int64_t map8_area(int64_t K, int64_t N) { return up256(map8_cap(K, N)) + 256; }
 
 }  // namespace bs
 
 using namespace bs;
 
-extern "C" int64_t bs_gemm_compressed_b_fp8_workspace_bytes(int64_t M, int64_t N, int64_t K, int a_layout)
+extern "C" int64_t bs_gemm_compressed_b_fp8_workspace_bytes(int64_t M, int64_t N, int64_t K, int a_layout,
+                                                            int square)
 {
     (void)a_layout;
     if (M <= 0 || N <= 0 || K <= 0) return kLutAreaBytes;
     const int split = gemm8_plan(M, N, K).split;
     int64_t bytes = split > 1 ? up256((int64_t)split * M * N * 4) : 0;
     bytes += up256(apk8_bytes(M, K));
+    if (square) bytes += map8_area(K, N);
     return bytes + kLutAreaBytes;
 }
 
@@ -803,7 +847,7 @@ extern "C" int bs_gemm_compressed_b_fp8(const void* A, const float* a_scale, int
     if (M == 0 || N == 0) return BS_OK;
     if (C == nullptr) return set_error(BS_ERR_INVALID, "%s: null C", fn);
     if (((uintptr_t)C) & 1) return set_error(BS_ERR_INVALID, "%s: C misaligned", fn);
-    const int64_t need = bs_gemm_compressed_b_fp8_workspace_bytes(M, N, K, a_layout);
+    const int64_t need = bs_gemm_compressed_b_fp8_workspace_bytes(M, N, K, a_layout, square);
     if (workspace == nullptr || workspace_bytes < need)
         return set_error(BS_ERR_INVALID, "%s: workspace too small (%lld < %lld)", fn, (long long)workspace_bytes,
                          (long long)need);
@@ -848,12 +892,18 @@ extern "C" int bs_gemm_compressed_b_fp8(const void* A, const float* a_scale, int
     la.lut = lut;
     la.b_scale = sB;
     la.b_scale_out = b_scale_out;
+    // square: the mapped value run after A's packed copy
+    const int64_t map_cap = map8_cap(K, N);
+    uint8_t* map_out = (uint8_t*)workspace + part_bytes + up256(apk8_bytes(M, K));
+    int64_t* map_vo = reinterpret_cast<int64_t*>(map_out + up256(map_cap));
     if (square) {
         hipLaunchKernelGGL(code_max_kernel, dim3(kCodeMaxBlocks), dim3(256), 0, st, la);
         if (vals_dtype == DT_E4M3FN)
             hipLaunchKernelGGL(relu2_lut_kernel<DT_E4M3FN>, dim3(1), dim3(256), 0, st, la);
         else
             hipLaunchKernelGGL(relu2_lut_kernel<DT_E5M2>, dim3(1), dim3(256), 0, st, la);
+        const uint32_t mblk = (uint32_t)std::min<int64_t>((map_cap + 4095) / 4096, 2048);
+        hipLaunchKernelGGL(map_codes_kernel, dim3(mblk), dim3(256), 0, st, la, map_out, map_cap, map_vo);
     } else {
         hipLaunchKernelGGL(copy_scale_kernel, dim3(1), dim3(64), 0, st, b_scale, sB, b_scale_out);
     }
@@ -876,17 +926,16 @@ extern "C" int bs_gemm_compressed_b_fp8(const void* A, const float* a_scale, int
     g.K = K;
     g.nkb = (uint32_t)nkb;
     g.nrb = (uint32_t)nrb;
-    g.vals = (const uint8_t*)vals;
-    g.vals_numel = vals_numel;
+    g.vals = square ? map_out : (const uint8_t*)vals;
+    g.vals_numel = square ? map_cap : vals_numel;
     g.bitmask = bitmask;
     g.prefix = prefix;
-    g.vals_offset = vals_offset;
+    g.vals_offset = square ? map_vo : vals_offset;
     g.N = N;
     g.grid_n = (uint32_t)grid_n;
     const uint32_t nt = (uint32_t)(plan.bn / kTile);
     g.tiles_n = (g.grid_n + nt - 1) / nt;
     g.tiles_m = (uint32_t)((M + plan.bm - 1) / plan.bm);
-    g.lut = lut;
     g.a_scale = a_scale;
     g.b_scale = sB;
     g.C = (uint16_t*)C;
@@ -896,18 +945,18 @@ extern "C" int bs_gemm_compressed_b_fp8(const void* A, const float* a_scale, int
     if (g.ksteps_per_split > (uint32_t)kMaxSteps) return set_error(BS_ERR_INVALID, "%s: internal split error", fn);
     const uint64_t blocks = (uint64_t)g.tiles_m * g.tiles_n * (uint64_t)split;
     if (blocks >= (1ull << 31)) return set_error(BS_ERR_INVALID, "%s: grid too large", fn);
-#define BS_GEMM8_LAUNCH(LUTV, FMT)                                                                                \
+#define BS_GEMM8_LAUNCH(FMT)                                                                                      \
     do {                                                                                                          \
         if (plan.big)                                                                                             \
-            hipLaunchKernelGGL((gemm_cb8_kernel<Cfg8_512, LUTV, FMT>), dim3((uint32_t)blocks),                    \
-                               dim3(Cfg8_512::THREADS), 0, st, g);                                                \
+            hipLaunchKernelGGL((gemm_cb8_kernel<Cfg8_512, FMT>), dim3((uint32_t)blocks), dim3(Cfg8_512::THREADS), \
+                               0, st, g);                                                                         \
         else                                                                                                      \
-            hipLaunchKernelGGL((gemm_cb8_kernel<Cfg8_256, LUTV, FMT>), dim3((uint32_t)blocks),                    \
-                               dim3(Cfg8_256::THREADS), 0, st, g);                                                \
+            hipLaunchKernelGGL((gemm_cb8_kernel<Cfg8_256, FMT>), dim3((uint32_t)blocks), dim3(Cfg8_256::THREADS), \
+                               0, st, g);                                                                         \
     } while (0)
-    if (square) BS_GEMM8_LAUNCH(true, 0);
-    else if (vals_dtype == DT_E4M3FN) BS_GEMM8_LAUNCH(false, 0);
-    else BS_GEMM8_LAUNCH(false, 1);
+    // square: the mapped codes are e4m3fn (to_fp8's); else the stored format
+    if (square || vals_dtype == DT_E4M3FN) BS_GEMM8_LAUNCH(0);
+    else BS_GEMM8_LAUNCH(1);
 #undef BS_GEMM8_LAUNCH
     hipError_t e = hipGetLastError();
     if (e == hipSuccess && split > 1) {

@@ -67,7 +67,7 @@ def gemm_compressed_b_fp8(A: Tensor, A_scale: Tensor, B_sparse, square: bool,
         raise ValueError("gemm_compressed_b_fp8: fp8 values without their scale")
     L = _lib.load()
     C = torch.empty((M, N), device=A.device, dtype=torch.bfloat16)
-    need = L.bs_gemm_compressed_b_fp8_workspace_bytes(M, N, K, a_layout)
+    need = L.bs_gemm_compressed_b_fp8_workspace_bytes(M, N, K, a_layout, int(square))
     ws = torch.empty(need, device=A.device, dtype=torch.uint8)
     check(L.bs_gemm_compressed_b_fp8(
         a_src.data_ptr(), A_scale.data_ptr(), M, K, lda, a_layout, B_sparse.vals.data_ptr(),

@@ -362,13 +362,15 @@ int bs_gemm_compressed_b(const void* A, int64_t M, int64_t K, int64_t lda, int a
  * fp32 MFMA accumulation (v_mfma_scale_f32_32x32x64_f8f6f4, unit block
  * scales), scaled once at the end; small grids split K into fp32 partial
  * sums reduced in a fixed order.  `workspace` (256-byte aligned,
- * bs_gemm_compressed_b_fp8_workspace_bytes) holds the partial sums, A in
- * fragment order and the code table.
+ * bs_gemm_compressed_b_fp8_workspace_bytes with the call's `square`) holds
+ * the partial sums, A in fragment order, the code table and, for square = 1,
+ * the tensor's value run mapped through the code table once (K*N bytes
+ * reserved, the run's nnz bytes written), which the GEMM then stages.
  * Replaces, for fp8 storage, lib_sparse/src/sparse_matmul.py:24-28 (AspB)
  * and :109-113 (AspRelu2B): unpack to a dense HBM buffer, re-quantize
  * (fp8.py:123-129) and the scaled fp8 GEMM (fp8.py:25-49).
  */
-int64_t bs_gemm_compressed_b_fp8_workspace_bytes(int64_t M, int64_t N, int64_t K, int a_layout);
+int64_t bs_gemm_compressed_b_fp8_workspace_bytes(int64_t M, int64_t N, int64_t K, int a_layout, int square);
 int bs_gemm_compressed_b_fp8(const void* A, const float* a_scale, int64_t M, int64_t K, int64_t lda,
                              int a_layout, const void* vals, int vals_dtype, int64_t vals_numel,
                              const uint8_t* bitmask, const uint32_t* prefix, const int64_t* vals_offset,

@@ -121,6 +121,34 @@ def test_vals_ending_inside_a_run_unit(dev, lead, square):
     assert torch.equal(got.view(torch.int16), want.view(torch.int16))
 
 
+@pytest.mark.parametrize("lead", [0, 5])
+def test_relu2_largest_code_in_the_last_partial_unit(dev, lead):
+    """sB comes from the largest stored code, and the value run is mapped
+    through the code table before the GEMM: with the one largest code as the
+    last byte of a buffer that ends mid 16-byte unit (and a run that starts
+    off a dword boundary for lead = 5), the unit crossing the end must still
+    be read in full, by the code maximum and by the mapping."""
+    from bitsparse_amd.src import dw_gemm
+    K, N = 512, 320
+    for seed in range(20, 40):
+        sp = _compressed_e4m3(K, N, -0.8, seed, dev)
+        p = sp.prefix.cpu().to(torch.int64)
+        if (lead + int(p[-1] - p[0])) % 16:
+            break
+    spt = _trimmed(sp, lead)
+    raw = spt.vals.view(torch.uint8)
+    assert raw.numel() % 16 != 0
+    raw[lead:].clamp_(max=0x40)               # stored codes stay positive, all below the last
+    raw[-1] = 0x7e                            # e4m3fn 448, the only code above 0x40
+    q, s = _relu2_operand(spt)
+    A, sa = _identity_fp8(K, dev)
+    sb_out = torch.empty((), device=dev)
+    C = dw_gemm.gemm_compressed_b_fp8(A, sa, spt, square=True, b_scale_out=sb_out)
+    assert torch.equal(sb_out.view(torch.int32), s.view(torch.int32)), (sb_out.item(), s.item())
+    want = (q.float() * s).to(torch.bfloat16)
+    assert torch.equal(C.view(torch.int16), want.view(torch.int16))
+
+
 @pytest.mark.parametrize("M,K,N", [(256, 256, 256), (512, 1024, 384), (192, 640, 200), (64, 4096, 64),
                                    (1000, 512, 700)])
 @pytest.mark.parametrize("square", [True, False])
