@@ -406,7 +406,7 @@ __global__ __launch_bounds__(CFG::THREADS, 1) void gemm_cb8_kernel(Gemm8Args a)
     // other waves at the barrier.  Runs thus get two iterations to arrive, A
     // one.  Loads past the last step re-read it.
     uint64_t bmq[2] = {0ull, 0ull};
-    __syncthreads();                                   // sel_s, lut_s, pf_s
+    __syncthreads();                                   // sel_s, pf_s
     if (nsteps > 0) {
         load_run(0, IC<0>{});
         store_run(0, IC<0>{});
