@@ -1348,10 +1348,33 @@ __global__ __launch_bounds__(kThreads) void decompress_kernel(GatherArgs a)
     constexpr bool STAGE = SQUARE && V_T != DT_BF16;
     constexpr int kSq = U * kTileNumel + 32;
     __shared__ __align__(16) uint16_t s_sq[STAGE ? kSq : 1];
+    // plain bf16 values: each half (4 elements) of a chunk is built from a
+    // 4-value window of the staged run at its first rank (three aligned dword
+    // reads and two v_alignbyte) with two v_perm_b32, whose selectors come
+    // from this table per mask nibble (element e takes window halfword
+    // rank(e), bytes 2 rank(e) and 2 rank(e) + 1; 0x0c gives 0x00).  The
+    // reads past a run's last value stay inside s_vals (its 32-byte slack)
+    // and feed only cleared elements.
+    constexpr bool PERM = V_T == DT_BF16 && !SQUARE && !HAS_SCALE && !PACKED;
+    __shared__ uint2 s_sel4[PERM ? 16 : 1];
     const int tid = threadIdx.x;
     const uint32_t pid0 = blockIdx.x * U;
     const int ntiles = (int)min((uint32_t)U, a.num_tiles - pid0);
     const uint32_t t0 = (uint32_t)a.first_m_tile * a.grid_n + pid0;
+    if constexpr (PERM) {
+        if (tid < 16) {
+            uint32_t sel[2] = {0x0c0c0c0cu, 0x0c0c0c0cu}, k = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                if ((tid >> e) & 1) {
+                    const uint32_t pair = (2u * k) | ((2u * k + 1u) << 8);
+                    sel[e >> 1] = (sel[e >> 1] & ~(0xffffu << (16 * (e & 1)))) | (pair << (16 * (e & 1)));
+                    k++;
+                }
+            }
+            s_sel4[tid] = uint2{sel[0], sel[1]};      // ordered by gather_prepare's barriers
+        }
+    }
 
     uint32_t m[U][2], r0[U][2];
     // cursor and scale read with the front half's loads
@@ -1384,8 +1407,25 @@ __global__ __launch_bounds__(kThreads) void decompress_kernel(GatherArgs a)
             typename Raw<OB>::T ov = {};
             uint32_t r = r0[j][h];
             const uint32_t mm = m[j][h];
+            if constexpr (PERM) {
+                const uint32_t* s32 = reinterpret_cast<const uint32_t*>(s_vals);
+                uint32_t o[4];
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
+                for (int q = 0; q < 2; q++) {
+                    const uint32_t nib = (mm >> (4 * q)) & 15u;
+                    const uint32_t d = r >> 1, sh = (r & 1u) * 2u;
+                    const uint32_t w0 = s32[d], w1 = s32[d + 1], w2 = s32[d + 2];
+                    const uint32_t lo = __builtin_amdgcn_alignbyte(w1, w0, sh);
+                    const uint32_t hi = __builtin_amdgcn_alignbyte(w2, w1, sh);
+                    const uint2 sel = s_sel4[nib];
+                    o[2 * q] = __builtin_amdgcn_perm(hi, lo, sel.x);
+                    o[2 * q + 1] = __builtin_amdgcn_perm(hi, lo, sel.y);
+                    r += (uint32_t)__popc(nib);
+                }
+                ov = uint4{o[0], o[1], o[2], o[3]};
+            }
+#pragma unroll
+            for (int e = 0; e < (PERM ? 0 : 8); e++) {
                 uint32_t x;
                 if constexpr (STAGE) {
                     x = ((mm >> e) & 1u) ? (uint32_t)s_sq[r] : zero_x;
