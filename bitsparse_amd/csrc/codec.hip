@@ -1262,8 +1262,13 @@ __device__ __forceinline__ int gather_prepare(const GatherArgs& a, uint32_t t0, 
     for (int j = 0; j < U; j++)
 #pragma unroll
         for (int h = 0; h < 2; h++) {
-            uint32_t tot;
-            wave_scan_count(__popc(m[j][h]), ex[j][h], tot);
+            // DPP prefix sum: the four chunks' scans are independent, so their
+            // DPP steps interleave (fewer VALU instructions than bit-plane
+            // ballots and mbcnt)
+            const uint32_t c = (uint32_t)__popc(m[j][h]);
+            const uint32_t incl = wave_incl_scan(c);
+            ex[j][h] = incl - c;
+            const uint32_t tot = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
             if (lane == 0) s_wtot[j][h][wave] = tot;
         }
     __syncthreads();
