@@ -1514,14 +1514,16 @@ __global__ __launch_bounds__(kThreads) void decompress_fp8_kernel(GatherArgs a, 
     for (int k = 0; k < NP; k++)
 #pragma unroll
         for (int h = 0; h < 2; h++) {
+            // both tiles' counts in one DPP prefix sum, tile jt in bits
+            // [16 jt, 16 jt + 16) (a wave's sum, <= 64 * 16, stays in its half)
             const uint32_t c = (uint32_t)__popc(m[k][h]);
-            uint32_t eA, eB, tA, tB;
-            wave_scan_count16(jt == 0 ? c : 0u, eA, tA);
-            wave_scan_count16(jt == 1 ? c : 0u, eB, tB);
-            ex[k][h] = jt == 0 ? eA : eB;
+            const uint32_t v = c << (16 * jt);
+            const uint32_t incl = wave_incl_scan(v);
+            ex[k][h] = ((incl - v) >> (16 * jt)) & 0xffffu;
+            const uint32_t tot = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
             if (lane == 0) {
-                s_wtot[h][2 * k][wave] = tA;
-                s_wtot[h][2 * k + 1][wave] = tB;
+                s_wtot[h][2 * k][wave] = tot & 0xffffu;
+                s_wtot[h][2 * k + 1][wave] = tot >> 16;
             }
         }
     __syncthreads();
