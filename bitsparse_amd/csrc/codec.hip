@@ -146,14 +146,27 @@ __device__ __forceinline__ uint32_t qtab_code(const uint8_t* qtab, uint32_t m, u
     return (uint32_t)qtab[i + (int)sign * kQtabEntries];
 }
 
+// qtab_code of 8 bf16 values, the table indices formed two at a time with
+// packed 16-bit arithmetic: clamp(m - qoff, 0, E - 1) = clamp(m, L, L') - qoff
+// with L = max(qoff, 0), L' = qoff + E - 1 (qoff >= -1537, so L <= L' < 2^16),
+// the subtraction taken mod 2^16 (its result is in [0, E - 1]); + E for x < 0.
 __device__ __forceinline__ uint2 quant_chunk_tab(const uint4 v, const uint8_t* qtab, int qoff)
 {
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    const u16x2 lo = (u16x2)(unsigned short)(qoff > 0 ? qoff : 0);
+    const u16x2 hi = (u16x2)(unsigned short)(qoff + kQtabEntries - 1);
+    const u16x2 off = (u16x2)(unsigned short)(uint32_t)qoff;
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
     uint32_t p[4];
 #pragma unroll
-    for (int k = 0; k < 4; k++)
-        p[k] = qtab_code(qtab, w[k] & 0x7fffu, (w[k] >> 15) & 1u, qoff) |
-               (qtab_code(qtab, (w[k] >> 16) & 0x7fffu, w[k] >> 31, qoff) << 8);
+    for (int k = 0; k < 4; k++) {
+        const u16x2 h = __builtin_bit_cast(u16x2, w[k]);
+        const u16x2 m = h & (u16x2)(unsigned short)0x7fff;
+        const u16x2 i = __builtin_elementwise_min(__builtin_elementwise_max(m, lo), hi) - off +
+                        (h >> (u16x2)(unsigned short)15) * (u16x2)(unsigned short)kQtabEntries;
+        const uint32_t ii = __builtin_bit_cast(uint32_t, i);
+        p[k] = (uint32_t)qtab[ii & 0xffffu] | ((uint32_t)qtab[ii >> 16] << 8);
+    }
     return uint2{p[0] | (p[1] << 16), p[2] | (p[3] << 16)};
 }
 
