@@ -696,7 +696,9 @@ void compress_stream_kernel(CompressArgs a)
     int64_t start = 0;
     if (a.offset_in) start = *a.offset_in;
     if (a.align8) start = (start + 7) & ~(int64_t)7;
-    __syncthreads();
+    // no barrier here: the dense loads below go out at once, and the
+    // selector table (and the packed edge slots) are next read after the
+    // barrier that follows the masks (or, for the values pass, the one below)
 
     {
         const uint32_t u = blockIdx.x;
@@ -797,8 +799,8 @@ void compress_stream_kernel(CompressArgs a)
         }
         if constexpr (MODE != MODE_VALS) {
             if (lane == 0) s_cnt[wave] = P[8];
-            __syncthreads();
         }
+        __syncthreads();                        // s_cnt; the selector table
 
         // ---- unit total and aggregate (wave 0)
         uint32_t v = 0, x = 0, unit_total = 0;
