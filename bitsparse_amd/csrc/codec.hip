@@ -680,15 +680,6 @@ void compress_stream_kernel(CompressArgs a)
         if (tid <= U) s_edge[tid] = 0u;
     }
 
-    if constexpr (WRITE_VALS) {
-        if (tid < 256) {
-            uint32_t sel[NSEL];
-            compaction_selectors<OUTB>((uint32_t)tid, sel);
-#pragma unroll
-            for (int i = 0; i < NSEL; i += 2)
-                *reinterpret_cast<uint2*>(&s_sel[tid * NSEL + i]) = make_uint2(sel[i], sel[i + 1]);
-        }
-    }
     float scale = 1.0f;
     if constexpr (QUANT) scale = scale_from_slot(a.amax_slot, a.amax_epoch);
     const float rcp = 1.0f / scale;
@@ -741,6 +732,16 @@ void compress_stream_kernel(CompressArgs a)
                 d[k] = tile_ok ? load_chunk<INB, false>(a.dense, a.M, a.N, row, col0) : RawIn{};
             }
             if constexpr (MODE == MODE_VALS) vm[k] = a.bitmask[(size_t)tc * kTileBytes + 64 * k + lane];
+        }
+        // the compaction selector table, while the loads are in flight
+        if constexpr (WRITE_VALS) {
+            if (tid < 256) {
+                uint32_t sel[NSEL];
+                compaction_selectors<OUTB>((uint32_t)tid, sel);
+#pragma unroll
+                for (int i = 0; i < NSEL; i += 2)
+                    *reinterpret_cast<uint2*>(&s_sel[tid * NSEL + i]) = make_uint2(sel[i], sel[i + 1]);
+            }
         }
         if constexpr (QUANT) {
             // the code table into LDS, behind the dense loads (16-byte copies)
