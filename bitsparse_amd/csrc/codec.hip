@@ -1501,6 +1501,19 @@ __global__ __launch_bounds__(kThreads) void decompress_fp8_kernel(GatherArgs a, 
     const uint32_t t0 = (uint32_t)a.first_m_tile * a.grid_n + tb0;  // in the compressed tensor
     const int piece = tid & 7, jt = piece >> 2, pc = piece & 3;    // tile of the pair, piece in it
 
+    const int64_t vo = a.vals_offset ? *a.vals_offset : 0;      // with the mask bytes
+    uint32_t m[NP][2], ex[NP][2];
+#pragma unroll
+    for (int k = 0; k < NP; k++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int row = 32 * h + (tid >> 3), tile = 2 * k + jt;
+            m[k][h] = tile < ntiles ? (uint32_t)*reinterpret_cast<const uint16_t*>(
+                                          a.bitmask + (size_t)(t0 + tile) * kTileBytes + row * 8 + 2 * pc)
+                                    : 0u;
+        }
+    if (tid <= ntiles) s_pref[tid] = a.prefix[t0 + tid];
+    // the selector table while the mask bytes and prefixes are in flight
     if constexpr (!PACKED) {
         // selectors of mask byte tid: set element e takes window byte rank(e)
         uint32_t sel[2] = {0x0c0c0c0cu, 0x0c0c0c0cu};
@@ -1514,18 +1527,6 @@ __global__ __launch_bounds__(kThreads) void decompress_fp8_kernel(GatherArgs a, 
         }
         s_sel[tid] = uint2{sel[0], sel[1]};
     }
-    const int64_t vo = a.vals_offset ? *a.vals_offset : 0;      // with the mask bytes
-    uint32_t m[NP][2], ex[NP][2];
-#pragma unroll
-    for (int k = 0; k < NP; k++)
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const int row = 32 * h + (tid >> 3), tile = 2 * k + jt;
-            m[k][h] = tile < ntiles ? (uint32_t)*reinterpret_cast<const uint16_t*>(
-                                          a.bitmask + (size_t)(t0 + tile) * kTileBytes + row * 8 + 2 * pc)
-                                    : 0u;
-        }
-    if (tid <= ntiles) s_pref[tid] = a.prefix[t0 + tid];
 #pragma unroll
     for (int k = 0; k < NP; k++)
 #pragma unroll
