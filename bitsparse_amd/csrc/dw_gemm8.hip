@@ -588,7 +588,6 @@ struct Lut8Args {
     float relu2_scale;
     const float* r_scale;         // stored values' scale (may be null: bf16(scale^2) not applied)
     uint32_t* cmax;               // per-block maxima of code_max_kernel (kCodeMaxBlocks)
-    uint8_t* lut;                 // 256 bytes
     float* b_scale;               // sB
     float* b_scale_out;           // optional copy for the caller
 };
@@ -651,8 +650,11 @@ __device__ __forceinline__ uint32_t relu2_dense_bits(uint32_t c, float k, bool h
     return x;
 }
 
+// The code table of square = 1 into tab[256] (all 256 threads of the block
+// call this): sB = max(amax / 448, 1e-9) from code_max_kernel's maxima, and
+// tab[c] = e4m3fn_RNE(D(c) / sB); the block with write_scale stores sB.
 template <int V_T>
-__global__ __launch_bounds__(256) void relu2_lut_kernel(Lut8Args a)
+__device__ __forceinline__ void relu2_table(const Lut8Args& a, uint8_t* tab, bool write_scale)
 {
     __shared__ float s_scale;
     const uint32_t c = threadIdx.x;
@@ -683,22 +685,28 @@ __global__ __launch_bounds__(256) void relu2_lut_kernel(Lut8Args a)
         const float amax = bf16_to_f32(amag);
         const float sc = amax / 448.0f;
         s_scale = (sc < 1e-9f) ? 1e-9f : sc;
-        *a.b_scale = s_scale;
-        if (a.b_scale_out) *a.b_scale_out = s_scale;
+        if (write_scale) {
+            *a.b_scale = s_scale;
+            if (a.b_scale_out) *a.b_scale_out = s_scale;
+        }
     }
     __syncthreads();
-    a.lut[c] = (uint8_t)f32_to_e4m3(bf16_to_f32(x) / s_scale);
+    tab[c] = (uint8_t)f32_to_e4m3(bf16_to_f32(x) / s_scale);
+    __syncthreads();
 }
 
-// square = 1: out[i] = lut[vals[vo + prefix[0] + i]] for i < n, n = the
+// square = 1: out[i] = table[vals[vo + prefix[0] + i]] for i < n, n = the
 // run's length (prefix[T] - prefix[0], within vals and cap; cap a multiple of
 // 16, so the whole 16-byte units the GEMM reads stay inside out), and
 // *out_vo = -prefix[0]: the GEMM then finds tile t's run at out[prefix[t] +
-// *out_vo].  16 codes per thread and pass.
+// *out_vo].  Every block forms the code table itself (256 entries, a few
+// instructions each; no separate launch); block 0 stores sB.  16 codes per
+// thread and pass.
+template <int V_T>
 __global__ __launch_bounds__(256) void map_codes_kernel(Lut8Args a, uint8_t* out, int64_t cap, int64_t* out_vo)
 {
     __shared__ uint8_t t[256];
-    t[threadIdx.x] = a.lut[threadIdx.x];
+    relu2_table<V_T>(a, t, blockIdx.x == 0);
     const int64_t vo = a.vals_offset ? *a.vals_offset : 0;
     const int64_t p0 = (int64_t)a.prefix[0];
     const int64_t b0 = vo + p0;
@@ -707,7 +715,6 @@ __global__ __launch_bounds__(256) void map_codes_kernel(Lut8Args a, uint8_t* out
     if (b0 < 0 || b0 >= a.vals_numel) n = 0;
     else if (n > a.vals_numel - b0) n = a.vals_numel - b0;
     if (blockIdx.x == 0 && threadIdx.x == 0) *out_vo = -p0;
-    __syncthreads();
     if (n <= 0) return;
     // dword-aligned source base; sh = the run start's byte within its dword
     const int64_t base = b0 & ~(int64_t)3;
@@ -804,7 +811,7 @@ static Gemm8Plan gemm8_plan(int64_t M, int64_t N, int64_t K)
 static int64_t apk8_nkb(int64_t K) { return (K + kBK - 1) / kBK; }
 static int64_t apk8_bytes(int64_t M, int64_t K) { return (M + 31) / 32 * apk8_nkb(K) * 2048; }
 static int64_t up256(int64_t x) { return (x + 255) / 256 * 256; }
-constexpr int64_t kLutAreaBytes = 512 + 4 * kCodeMaxBlocks;     // lut[256], sB, code_max_kernel's maxima at 512
+constexpr int64_t kLutAreaBytes = 512 + 4 * kCodeMaxBlocks;     // sB at 256, code_max_kernel's maxima at 512
 // square = 1: room for the mapped value run (at most K N codes, whole 16-byte
 // units) and its offset word
 static int64_t map8_cap(int64_t K, int64_t N) { return (K * N + 15) / 16 * 16; }
@@ -855,7 +862,6 @@ extern "C" int bs_gemm_compressed_b_fp8(const void* A, const float* a_scale, int
     hipStream_t st = (hipStream_t)stream;
     const uint32_t ksteps = (uint32_t)((K + kBK - 1) / kBK);
     uint8_t* lut_area = (uint8_t*)workspace + need - kLutAreaBytes;
-    uint8_t* lut = lut_area;
     float* sB = reinterpret_cast<float*>(lut_area + 256);
     uint32_t* cmax = reinterpret_cast<uint32_t*>(lut_area + 512);
     if (ksteps == 0) {
@@ -889,7 +895,6 @@ extern "C" int bs_gemm_compressed_b_fp8(const void* A, const float* a_scale, int
     la.relu2_scale = relu2_scale;
     la.r_scale = b_scale;
     la.cmax = cmax;
-    la.lut = lut;
     la.b_scale = sB;
     la.b_scale_out = b_scale_out;
     // square: the mapped value run after A's packed copy
@@ -898,12 +903,11 @@ extern "C" int bs_gemm_compressed_b_fp8(const void* A, const float* a_scale, int
     int64_t* map_vo = reinterpret_cast<int64_t*>(map_out + up256(map_cap));
     if (square) {
         hipLaunchKernelGGL(code_max_kernel, dim3(kCodeMaxBlocks), dim3(256), 0, st, la);
-        if (vals_dtype == DT_E4M3FN)
-            hipLaunchKernelGGL(relu2_lut_kernel<DT_E4M3FN>, dim3(1), dim3(256), 0, st, la);
-        else
-            hipLaunchKernelGGL(relu2_lut_kernel<DT_E5M2>, dim3(1), dim3(256), 0, st, la);
         const uint32_t mblk = (uint32_t)std::min<int64_t>((map_cap + 4095) / 4096, 2048);
-        hipLaunchKernelGGL(map_codes_kernel, dim3(mblk), dim3(256), 0, st, la, map_out, map_cap, map_vo);
+        if (vals_dtype == DT_E4M3FN)
+            hipLaunchKernelGGL(map_codes_kernel<DT_E4M3FN>, dim3(mblk), dim3(256), 0, st, la, map_out, map_cap, map_vo);
+        else
+            hipLaunchKernelGGL(map_codes_kernel<DT_E5M2>, dim3(mblk), dim3(256), 0, st, la, map_out, map_cap, map_vo);
     } else {
         hipLaunchKernelGGL(copy_scale_kernel, dim3(1), dim3(64), 0, st, b_scale, sB, b_scale_out);
     }
