@@ -1481,7 +1481,9 @@ __global__ __launch_bounds__(kThreads) void decompress_kernel(GatherArgs a)
 // reads and v_alignbyte, and each mask byte expands its 8 outputs with two
 // v_perm_b32 whose selectors come from a 256-entry LDS table (selector byte
 // 0x0c gives 0x00); the second byte's window starts popcount(first byte)
-// values later.  Packed storage reads value by value.  Needs K % 16 == 0 and
+// values later.  Packed storage first widens the 16 7-bit fields from the
+// thread's first rank (a 128-bit window of the staged stream) to bytes, then
+// expands them the same way.  Needs K % 16 == 0 and
 // a 16-byte aligned output.
 template <int V_T, int NP, bool PACKED, bool NT>
 __global__ __launch_bounds__(kThreads) void decompress_fp8_kernel(GatherArgs a, uint32_t groups_per_row)
@@ -1492,7 +1494,7 @@ __global__ __launch_bounds__(kThreads) void decompress_fp8_kernel(GatherArgs a, 
     __shared__ uint32_t s_wtot[2][NTL][4];  // [pass][tile][wave]
     // the run, its <= 15-byte phase, and room for the last window's reads
     __shared__ __align__(16) uint8_t s_vals[NTL * kTileNumel + 48];
-    __shared__ uint2 s_sel[PACKED ? 1 : 256];
+    __shared__ uint2 s_sel[256];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const uint32_t tm = blockIdx.x / groups_per_row;
     const uint32_t tn0 = NTL * (blockIdx.x - tm * groups_per_row);
@@ -1514,7 +1516,7 @@ __global__ __launch_bounds__(kThreads) void decompress_fp8_kernel(GatherArgs a, 
         }
     if (tid <= ntiles) s_pref[tid] = a.prefix[t0 + tid];
     // the selector table while the mask bytes and prefixes are in flight
-    if constexpr (!PACKED) {
+    {
         // selectors of mask byte tid: set element e takes window byte rank(e)
         uint32_t sel[2] = {0x0c0c0c0cu, 0x0c0c0c0cu};
         uint32_t rank = 0;
@@ -1575,24 +1577,39 @@ __global__ __launch_bounds__(kThreads) void decompress_fp8_kernel(GatherArgs a, 
     for (int h = 0; h < 2; h++) {
         const uint32_t mm = m[k][h];
         uint4 o;
-        if constexpr (PACKED) {
-            uint32_t w[4] = {0u, 0u, 0u, 0u};
-            uint32_t r = r0[k][h];
-#pragma unroll
-            for (int e = 0; e < 16; e++) {
-                if ((mm >> e) & 1u) w[e >> 2] |= lds_val<V_T, PB>(s_vals, r, bitbase) << (8 * (e & 3));
-                r += (mm >> e) & 1u;
-            }
-            o = uint4{w[0], w[1], w[2], w[3]};
-        } else {
+        {
             const uint32_t r = r0[k][h];
-            const uint32_t* sv = reinterpret_cast<const uint32_t*>(s_vals) + (r >> 2);
-            const uint32_t sh = r & 3u;
-            const uint32_t d0 = sv[0], d1 = sv[1], d2 = sv[2], d3 = sv[3], d4 = sv[4];
-            const uint32_t w0 = __builtin_amdgcn_alignbyte(d1, d0, sh);
-            const uint32_t w1 = __builtin_amdgcn_alignbyte(d2, d1, sh);
-            const uint32_t w2 = __builtin_amdgcn_alignbyte(d3, d2, sh);
-            const uint32_t w3 = __builtin_amdgcn_alignbyte(d4, d3, sh);
+            uint32_t w0, w1, w2, w3;            // the 16 values from rank r, one byte each
+            if constexpr (PACKED) {
+                // the 16 7-bit fields from stream bit bitbase + 7 r: a 128-bit
+                // window (five aligned dword reads, v_alignbit), each field
+                // widened to its byte (a stored e4m3fn code: sign bit 0)
+                const uint32_t bit = (uint32_t)bitbase + r * (uint32_t)PB;
+                const uint32_t* sv = reinterpret_cast<const uint32_t*>(s_vals) + (bit >> 5);
+                const uint32_t sh = bit & 31u;
+                const uint32_t u0 = sv[0], u1 = sv[1], u2 = sv[2], u3 = sv[3], u4 = sv[4];
+                const uint32_t x[5] = {__builtin_amdgcn_alignbit(u1, u0, sh), __builtin_amdgcn_alignbit(u2, u1, sh),
+                                       __builtin_amdgcn_alignbit(u3, u2, sh), __builtin_amdgcn_alignbit(u4, u3, sh),
+                                       0u};
+                uint32_t wb[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+                for (int j = 0; j < 16; j++) {
+                    constexpr int kPB = PB > 0 ? PB : 1;
+                    const int lo = j * kPB, q = lo >> 5, off = lo & 31;
+                    uint32_t f = x[q] >> off;
+                    if (off + kPB > 32) f |= x[q + 1] << (32 - off);
+                    wb[j >> 2] |= (f & ((1u << kPB) - 1u)) << (8 * (j & 3));
+                }
+                w0 = wb[0], w1 = wb[1], w2 = wb[2], w3 = wb[3];
+            } else {
+                const uint32_t* sv = reinterpret_cast<const uint32_t*>(s_vals) + (r >> 2);
+                const uint32_t sh = r & 3u;
+                const uint32_t d0 = sv[0], d1 = sv[1], d2 = sv[2], d3 = sv[3], d4 = sv[4];
+                w0 = __builtin_amdgcn_alignbyte(d1, d0, sh);
+                w1 = __builtin_amdgcn_alignbyte(d2, d1, sh);
+                w2 = __builtin_amdgcn_alignbyte(d3, d2, sh);
+                w3 = __builtin_amdgcn_alignbyte(d4, d3, sh);
+            }
             const uint32_t m0 = mm & 0xffu, m1 = mm >> 8;
             const uint2 sa = s_sel[m0], sb = s_sel[m1];
             // window of the second byte: bytes c0 .. c0+7, c0 = popcount(m0) <= 8
