@@ -1376,7 +1376,7 @@ __global__ __launch_bounds__(kThreads) void decompress_kernel(GatherArgs a)
     // rank(e), bytes 2 rank(e) and 2 rank(e) + 1; 0x0c gives 0x00).  The
     // reads past a run's last value stay inside s_vals (its 32-byte slack)
     // and feed only cleared elements.
-    constexpr bool PERM = V_T == DT_BF16 && !SQUARE && !HAS_SCALE && !PACKED;
+    constexpr bool PERM = V_T == DT_BF16 && !SQUARE && !HAS_SCALE;
     __shared__ uint2 s_sel4[PERM ? 16 : 1];
     const int tid = threadIdx.x;
     const uint32_t pid0 = blockIdx.x * U;
@@ -1434,10 +1434,23 @@ __global__ __launch_bounds__(kThreads) void decompress_kernel(GatherArgs a)
 #pragma unroll
                 for (int q = 0; q < 2; q++) {
                     const uint32_t nib = (mm >> (4 * q)) & 15u;
-                    const uint32_t d = r >> 1, sh = (r & 1u) * 2u;
-                    const uint32_t w0 = s32[d], w1 = s32[d + 1], w2 = s32[d + 2];
-                    const uint32_t lo = __builtin_amdgcn_alignbyte(w1, w0, sh);
-                    const uint32_t hi = __builtin_amdgcn_alignbyte(w2, w1, sh);
+                    uint32_t lo, hi;
+                    if constexpr (PACKED) {
+                        // the four 15-bit fields from stream bit bitbase + 15 r
+                        // (a 64-bit window), widened to halfwords
+                        const uint32_t bit = (uint32_t)bitbase + r * 15u;
+                        const uint32_t d = bit >> 5, sh = bit & 31u;
+                        const uint32_t w0 = s32[d], w1 = s32[d + 1], w2 = s32[d + 2];
+                        const uint32_t x0 = __builtin_amdgcn_alignbit(w1, w0, sh);
+                        const uint32_t x1 = __builtin_amdgcn_alignbit(w2, w1, sh);
+                        lo = (x0 & 0x7fffu) | ((x0 << 1) & 0x7fff0000u);
+                        hi = (((x0 >> 30) | (x1 << 2)) & 0x7fffu) | ((x1 << 3) & 0x7fff0000u);
+                    } else {
+                        const uint32_t d = r >> 1, sh = (r & 1u) * 2u;
+                        const uint32_t w0 = s32[d], w1 = s32[d + 1], w2 = s32[d + 2];
+                        lo = __builtin_amdgcn_alignbyte(w1, w0, sh);
+                        hi = __builtin_amdgcn_alignbyte(w2, w1, sh);
+                    }
                     const uint2 sel = s_sel4[nib];
                     o[2 * q] = __builtin_amdgcn_perm(hi, lo, sel.x);
                     o[2 * q + 1] = __builtin_amdgcn_perm(hi, lo, sel.y);
