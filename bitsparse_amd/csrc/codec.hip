@@ -564,18 +564,23 @@ __device__ __forceinline__ void stream_packed(const CompressArgs& a, int64_t g, 
         for (int d = dn + lane; d < dlw; d += 64) {
             const int lo = max(d * 32, sb), hi = min(d * 32 + 32, eb);
             const int v0 = (lo - sb) / PB, v1 = (hi - 1 - sb) / PB;
-            uint32_t word = 0;
+            // values v0 .. v1 side by side in a 64-bit window (value v0 + j at
+            // bit PB j, MAXV PB <= 60 bits), then shifted so that stream bit
+            // 32 d lands on bit 0: by s0 = 32 d - (sb + v0 PB), which is in
+            // [0, PB) inside the run and negative only for its first dword
+            uint64_t win = 0;
 #pragma unroll
             for (int j = 0; j < MAXV; j++) {
                 const int v = v0 + j;
+                uint32_t x = 0;
                 if (v <= v1) {
-                    uint32_t x;
                     if constexpr (OUTB == 2) x = reinterpret_cast<const uint16_t*>(ring)[v - base];
                     else x = ring[v - base];
-                    const int pos = sb + v * PB - d * 32;                 // in (-PB, 32)
-                    word |= pos >= 0 ? ((x & VMASK) << pos) : ((x & VMASK) >> (-pos));
                 }
+                win |= (uint64_t)(x & VMASK) << (PB * j);
             }
+            const int s0 = d * 32 - (sb + v0 * PB);
+            const uint32_t word = s0 >= 0 ? (uint32_t)(win >> s0) : (uint32_t)(win << (-s0));
             if (lo == d * 32 && hi == d * 32 + 32) {
                 out[d] = word;
             } else {
