@@ -248,6 +248,71 @@ def f32_to_bf16(f: np.ndarray) -> np.ndarray:
     return np.fromiter((L.or_f32_to_bf16(float(v)) for v in f), np.uint16, f.size)
 
 
+def _row_blocks(M: int, threads: int) -> list[tuple[int, int]]:
+    """Split [0, M) into `threads` ranges whose starts are multiples of 64."""
+    gm = (M + TILE - 1) // TILE
+    per = max(1, (gm + threads - 1) // threads)
+    return [(tm * TILE, min(M, (tm + per) * TILE)) for tm in range(0, gm, per)]
+
+
+def _pool_map(fn, items, threads: int):
+    from concurrent.futures import ThreadPoolExecutor   # ctypes calls drop the GIL
+    with ThreadPoolExecutor(max_workers=threads) as ex:
+        return list(ex.map(fn, items))
+
+
+def compress_mt(x: np.ndarray, dtype: int, threads: int | None = None):
+    """``compress`` with the C loops run over row blocks on `threads` host
+    threads: the same per-tile functions (or_tile_pack on each block of tile
+    rows, one or_prefix, or_compact over each block's tiles at that block's
+    prefix), so the result is the single-threaded one."""
+    _check_bits(x, dtype)
+    x = np.ascontiguousarray(x)
+    M, N = x.shape
+    gm, gn, T = tile_grid(M, N)
+    threads = threads or min(16, os.cpu_count() or 1)
+    L, eb = lib(), x.itemsize
+    bm = np.zeros(T * TILE_BYTES, np.uint8)
+    counts = np.zeros(T, np.int32)
+    blocks = _row_blocks(M, threads)
+
+    def pack(b):
+        r0, r1 = b
+        t0 = (r0 // TILE) * gn
+        L.or_tile_pack(_p(x) + r0 * N * eb, dtype, r1 - r0, N,
+                       _p(bm) + t0 * TILE_BYTES, _p(counts) + 4 * t0)
+    _pool_map(pack, blocks, threads)
+    pref = prefix(counts)
+    vals = np.zeros(int(pref[-1]), x.dtype)
+
+    def comp(b):
+        r0, r1 = b
+        t0, t1 = (r0 // TILE) * gn, ((r1 + TILE - 1) // TILE) * gn
+        L.or_compact(_p(x), dtype, M, N, _p(bm), _p(pref), _p(vals), int(pref[t0]), t0, t1 - t0)
+    _pool_map(comp, blocks, threads)
+    return bm, pref, vals
+
+
+def to_fp8_mt(x: np.ndarray, threads: int | None = None) -> tuple[np.ndarray, float]:
+    """``to_fp8`` over slices on `threads` host threads (amax is a max of
+    per-slice maxima, NaN-propagating as or_amax_bf16 is; the quantizer is
+    elementwise)."""
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    flat = x.reshape(-1)
+    threads = threads or min(16, os.cpu_count() or 1)
+    step = (flat.size + threads - 1) // threads
+    parts = [(i, min(flat.size, i + step)) for i in range(0, flat.size, step)]
+    L = lib()
+    maxima = _pool_map(lambda p: float(L.or_amax_bf16(_p(flat) + 2 * p[0], p[1] - p[0])),
+                       parts, threads)
+    amax = float("nan") if any(m != m for m in maxima) else max(maxima, default=0.0)
+    s = fp8_scale(amax)
+    q = np.zeros(flat.size, np.uint8)
+    _pool_map(lambda p: L.or_quantize_bf16_to_e4m3fn(_p(flat) + 2 * p[0], p[1] - p[0], s,
+                                                      _p(q) + p[0]), parts, threads)
+    return q.reshape(x.shape), s
+
+
 def compress_timed_call(x: np.ndarray, dtype: int, bm, pref, counts, vals) -> int:
     """Single C call doing the whole compress (the CPU baseline's unit of work)."""
     M, N = x.shape

@@ -154,29 +154,6 @@ def _torch_tile_bitmask(x: torch.Tensor) -> torch.Tensor:
     return (t * w).sum(-1, dtype=torch.int32).to(torch.uint8).reshape(-1)
 
 
-@pytest.mark.parametrize("mu", [0.0, -2.3263])
-def test_c3_size_properties(dev, mu):
-    """configs[2] shape 16384x16384 at 50% and 99% zeros: exact round trip,
-    bitmask = torch's tile bitmask, prefix = scan of per-tile counts."""
-    F, _, TB = _bs()
-    M = N = 16384
-    g = torch.Generator(device=dev).manual_seed(0)
-    x = (torch.randn((M, N), device=dev, generator=g) + mu).to(torch.bfloat16).relu_()
-    buf = TB(2 * M * N, device=dev)
-    sp = F.dense_to_tilesparse(x, None, buf)
-    d = decompress(sp)
-    assert torch.equal(d, x)
-    assert torch.equal(sp.bitmask, _torch_tile_bitmask(x))
-    counts = (x > 0).reshape(M // 64, 64, N // 64, 64).sum((1, 3), dtype=torch.int64).reshape(-1)
-    pref = torch.zeros(counts.numel() + 1, dtype=torch.int64, device=dev)
-    pref[1:] = counts.cumsum(0)
-    assert torch.equal(sp.prefix.to(torch.int64), pref)
-    assert int(buf.offset.item()) == int(pref[-1].item())
-    vals_ref = x.reshape(M // 64, 64, N // 64, 64).permute(0, 2, 1, 3).reshape(-1)
-    vals_ref = vals_ref[vals_ref > 0]
-    assert torch.equal(sp.vals[:vals_ref.numel()], vals_ref)
-
-
 @pytest.mark.parametrize("quant", [False, True])
 def test_lookback_fallback_path(dev, monkeypatch, quant):
     """The compress look-back's safety net: with BITSPARSE_LOOKBACK_PATIENCE=0 a

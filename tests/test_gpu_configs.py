@@ -15,8 +15,8 @@
   bf16 tolerance, and a lower peak memory; with the library GEMM for dW2 the
   whole tracking vector of experiment.py:56-66 matches at the reference's
   3e-6 (experiment.py:24, :160-164).
-* 16384^2 with e4m3fn value storage and with skewed columns,
-  checked through size-independent properties.
+* every sweep point, bit-exact against the oracle, lives in
+  tests/test_gpu_configs2.py.
 * the reference's benchmark matrix (experiments/benchmark.py:12, :121-146):
   shapes (1000, 4096), (4000, 4096), (15000, 4096) x sparsity 0.5 / 0.8 x
   pack_sbit, exact round trip and the vram_size() storage ratio.
@@ -186,69 +186,6 @@ def test_configs4_twelve_block_stack(dev, lds_gemm, monkeypatch):
             return torch.stack([v.float() for v in t]) * 1e3
         torch.testing.assert_close(tracking(lc, gxc, dW1c, dW2c), tracking(ld, gxd, dW1d, dW2d),
                                    atol=3e-6, rtol=3e-6)
-
-
-def _torch_tile_bitmask_pos(pos):
-    M, N = pos.shape
-    t = pos.to(torch.uint8).reshape(M // 64, 64, N // 64, 64).permute(0, 2, 1, 3).reshape(-1, 512, 8)
-    w = (2 ** torch.arange(8, device=pos.device, dtype=torch.int32)).to(torch.uint8)
-    return (t * w).sum(-1, dtype=torch.int32).to(torch.uint8).reshape(-1)
-
-
-def _check_properties(sp, dense, pos, buf_offset):
-    """Compressed form of `dense` (positives `pos`), 16384^2-sized checks."""
-    from tests.test_gpu_codec import decompress
-    M, N = dense.shape
-    # compared as raw bits (fp8 tensors support few torch ops)
-    view = (lambda t: t.view(torch.uint8)) if dense.dtype != torch.bfloat16 else (lambda t: t.view(torch.int16))
-    assert torch.equal(view(decompress(sp)), view(dense))
-    assert torch.equal(sp.bitmask, _torch_tile_bitmask_pos(pos))
-    counts = pos.reshape(M // 64, 64, N // 64, 64).sum((1, 3), dtype=torch.int64).reshape(-1)
-    pref = torch.zeros(counts.numel() + 1, dtype=torch.int64, device=dense.device)
-    pref[1:] = counts.cumsum(0)
-    assert torch.equal(sp.prefix.to(torch.int64), pref)
-    assert buf_offset == int(pref[-1].item())
-    tiles = view(dense).reshape(M // 64, 64, N // 64, 64).permute(0, 2, 1, 3).reshape(-1)
-    tpos = pos.reshape(M // 64, 64, N // 64, 64).permute(0, 2, 1, 3).reshape(-1)
-    ref = tiles[tpos]
-    assert torch.equal(view(sp.vals[:ref.numel()]), ref)
-
-
-@pytest.mark.parametrize("mu", [0.0, -1.2816])
-def test_configs2_e4m3fn_storage_properties(dev, mu):
-    from bitsparse_amd.bitsparse import TensorBuffer
-    from bitsparse_amd.fp8 import to_fp8
-    from bitsparse_amd.src.functions import quantize_and_compress
-    M = N = 16384
-    gen = torch.Generator(device=dev).manual_seed(0)
-    x = (torch.randn((M, N), device=dev, generator=gen) + mu).to(torch.bfloat16).relu_()
-    buf = TensorBuffer(M * N, device=dev, dtype=torch.float8_e4m3fn)
-    q, s, sp = quantize_and_compress(x, buf)
-    q2, s2 = to_fp8(x)
-    assert torch.equal(q.view(torch.uint8), q2.view(torch.uint8)) and torch.equal(s, s2)
-    pos = q.float() > 0
-    _check_properties(sp, q, pos, int(buf.offset.item()))
-
-
-def test_configs2_skewed_columns_properties(dev):
-    """90% zeros overall with a per-column N(0, 0.5) bias (mu scaled by
-    sqrt(1.25) to keep the overall sparsity)."""
-    from bitsparse_amd.bitsparse import TensorBuffer
-    from bitsparse_amd.src.functions import dense_to_tilesparse
-    M = N = 16384
-    gen = torch.Generator(device=dev).manual_seed(0)
-    pre = torch.randn((M, N), device=dev, generator=gen) - 1.4328
-    pre += 0.5 * torch.randn((1, N), device=dev, generator=gen)
-    x = pre.to(torch.bfloat16).relu_()
-    del pre
-    buf = TensorBuffer(2 * M * N, device=dev)
-    sp = dense_to_tilesparse(x, None, buf)
-    pos = x > 0
-    sparsity = 1 - pos.sum().item() / x.numel()
-    assert 0.85 < sparsity < 0.95
-    col_nnz = pos.sum(0).float()
-    assert col_nnz.std() > 0.2 * col_nnz.mean()          # columns really are skewed
-    _check_properties(sp, x, pos, int(buf.offset.item()))
 
 
 @pytest.mark.parametrize("pack_sbit", [False, True])

@@ -335,3 +335,31 @@ def test_pack_bits_eight_value_groups_are_byte_aligned():
         s = np.zeros(64, np.uint8)
         O.pack_bits(np.full(8, (1 << b) - 1, dt), code, s, 8)
         assert not s[:b].any() and (s[b:2 * b] == 0xFF).all() and not s[2 * b:].any()
+
+
+@pytest.mark.parametrize("threads", [1, 3, 8])
+@pytest.mark.parametrize("shape", [(1, 1), (64, 64), (130, 129), (700, 300)])
+def test_compress_mt_matches_single_thread(shape, threads):
+    """The row-block threaded oracle (used at configs[2]'s full size) is the
+    single-threaded compress: same bitmask, prefix and values."""
+    x = bits(preact_input(shape, mu=-0.3, seed=11).relu())
+    want = O.compress(x, O.BF16)
+    got = O.compress_mt(x, O.BF16, threads)
+    for a, b in zip(want, got):
+        assert a.dtype == b.dtype and np.array_equal(a, b)
+    q = all_fp8_patterns(shape, seed=2)
+    for a, b in zip(O.compress(q, O.E4M3FN), O.compress_mt(q, O.E4M3FN, threads)):
+        assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("threads", [1, 5])
+def test_to_fp8_mt_matches_single_thread(threads):
+    x = bits(preact_input((257, 129), mu=0.2, seed=4))
+    q1, s1 = O.to_fp8(x)
+    q2, s2 = O.to_fp8_mt(x, threads)
+    assert s1 == s2 and np.array_equal(q1, q2)
+    y = x.copy()
+    y[100, 7] = 0x7fc0                                     # a NaN anywhere -> NaN scale
+    q1, s1 = O.to_fp8(y)
+    q2, s2 = O.to_fp8_mt(y, threads)
+    assert s1 != s1 and s2 != s2 and np.array_equal(q1, q2)
