@@ -54,10 +54,82 @@ def codec_bytes(M: int, N: int, nnz: int, vb_in: int = 2, vb: int = 2, vb_out: i
     return M * N * vb_in + meta + nnz * vb, meta + nnz * vb + M * N * vb_out
 
 
-def make_activation(M: int, N: int, mu: float, device):
+_BASE = {}
+
+
+def base_normal(M: int, N: int, device):
+    """X ~ N(0, 1) [M, N] fp32 and a column bias 0.5 * N(0, 1) [N], drawn on
+    the CPU in that order with torch.Generator().manual_seed(0) (so the CPU
+    oracle regenerates the same bits), cached on the GPU for the run."""
     import torch
-    g = torch.Generator(device=device).manual_seed(0)
-    return (torch.randn((M, N), device=device, generator=g) + mu).to(torch.bfloat16).relu_()
+    key = (M, N, str(device))
+    if key not in _BASE:
+        g = torch.Generator().manual_seed(0)
+        X = torch.randn((M, N), generator=g, dtype=torch.float32)
+        b = 0.5 * torch.randn((N,), generator=g, dtype=torch.float32)
+        _BASE[key] = (X.to(device), b.to(device))
+    return _BASE[key]
+
+
+def drop_base() -> None:
+    import torch
+    _BASE.clear()
+    torch.cuda.empty_cache()
+
+
+def make_activation(M: int, N: int, mu: float, device, skew: bool = False):
+    """relu(bf16(X + mu [+ column bias])) with X from base_normal."""
+    import torch
+    X, b = base_normal(M, N, device)
+    pre = X + mu
+    if skew:
+        pre += b
+    return pre.to(torch.bfloat16).relu_()
+
+
+def measure_floors(steps: int, warmup: int, nnz_headline: int | None = None):
+    """The access-mix floors at the headline shape (its measured nonzeros, or
+    half the elements) and at the configs[1] activation size (8192 x 3072,
+    half the elements nonzero)."""
+    M = N = 16384
+    out = {"configs[2] 16384x16384": measure_mix_floor(M, N, nnz_headline or M * N // 2, steps, warmup),
+           "configs[1] activation 8192x3072": measure_mix_floor(8192, 3072, 8192 * 3072 // 2, steps, warmup)}
+    return out
+
+
+def measure_mix_floor(M: int, N: int, nnz: int, steps: int = 10, warmup: int = 3, nt: bool | None = None):
+    """Duration of the library's streaming probes (bs_stream_probe) with the
+    exact access mix of a compress and of a decompress launch of an [M, N]
+    bf16 activation with `nnz` nonzeros (value bytes spread evenly over the
+    8-tile units, rounded up to 128 bytes per unit), no scan or compaction:
+    the floor the codec kernels are measured against."""
+    import torch
+    from bitsparse_amd import _lib
+    L = _lib.load()
+    dev = torch.device("cuda", 0)
+    T = (M // 64) * (N // 64)
+    units = T // 8
+    vpu = (2 * nnz + units * 128 - 1) // (units * 128) * 128
+    dense = torch.empty((M, N), dtype=torch.bfloat16, device=dev).fill_(1.0)
+    vals = torch.empty(units * vpu, dtype=torch.uint8, device=dev)
+    bm = torch.empty(T * 512, dtype=torch.uint8, device=dev)
+    if nt is None:
+        thr = int(L.bs_nontemporal_min_bytes(-1))     # read the threshold, then put it back
+        L.bs_nontemporal_min_bytes(thr)
+        nt = 2 * M * N >= thr
+    out = {"shape": [M, N], "value_bytes_per_unit": vpu, "nontemporal": bool(nt)}
+    for mode, name in ((0, "compress_mix"), (1, "decompress_mix")):
+        def call():
+            _lib.check(L.bs_stream_probe(mode, dense.data_ptr(), M, N, vals.data_ptr(), vals.numel(), vpu,
+                                         bm.data_ptr(), bm.numel(), int(nt), _lib.stream_handle(dev)),
+                       "bs_stream_probe")
+        ms = _timed(call, steps, warmup)
+        nbytes = 2 * M * N + T * 512 + units * vpu
+        out[name + "_ms"] = round(ms, 5)
+        out[name + "_gbs"] = round(nbytes / (ms * 1e6), 1)
+    del dense, vals, bm
+    torch.cuda.empty_cache()
+    return out
 
 
 def measure_copy_gbs(nbytes: int = 512 << 20, steps: int = 10) -> float:
@@ -277,9 +349,9 @@ def bench_gemm(steps: int, warmup: int):
     cases = [("configs[1] dW2", 768, 8192, 3072, 0.0, False),
              ("configs[3] dW2", 4096, 4096, 16384, -1.2816, True)]
     for name, M, K, N, mu, relu2_fp8 in cases:
-        g = torch.Generator(device=dev).manual_seed(0)
-        h = (torch.randn((K, N), device=dev, generator=g) + mu).to(torch.bfloat16).relu_()
-        dY = torch.randn((K, M), device=dev, generator=g).to(torch.bfloat16)
+        g = torch.Generator().manual_seed(0)
+        h = (torch.randn((K, N), generator=g) + mu).to(torch.bfloat16).relu_().to(dev)
+        dY = torch.randn((K, M), generator=g).to(torch.bfloat16).to(dev)
         if relu2_fp8:
             _, _, sp = quantize_and_compress(h, None)
             qd, sd = to_fp8(dY)
@@ -320,12 +392,12 @@ def bench_mlp(steps: int, warmup: int):
     from bitsparse_amd.layers import FFNRelu
 
     dev = torch.device("cuda", 0)
-    g = torch.Generator(device=dev).manual_seed(0)
+    g = torch.Generator().manual_seed(0)       # CPU draws, in the config's order
     B, D, H = 8192, 768, 3072
-    x = torch.randn((8, 1024, D), device=dev, generator=g).to(torch.bfloat16).requires_grad_()
-    W1 = (0.02 * torch.randn((H, D), device=dev, generator=g)).to(torch.bfloat16).requires_grad_()
-    W2 = (0.02 * torch.randn((D, H), device=dev, generator=g)).to(torch.bfloat16).requires_grad_()
-    dY = torch.randn((8, 1024, D), device=dev, generator=g).to(torch.bfloat16)
+    x = torch.randn((8, 1024, D), generator=g).to(torch.bfloat16).to(dev).requires_grad_()
+    W1 = (0.02 * torch.randn((H, D), generator=g)).to(torch.bfloat16).to(dev).requires_grad_()
+    W2 = (0.02 * torch.randn((D, H), generator=g)).to(torch.bfloat16).to(dev).requires_grad_()
+    dY = torch.randn((8, 1024, D), generator=g).to(torch.bfloat16).to(dev)
     buf = TensorBuffer(2 * B * H, device=dev)
 
     from bitsparse_amd import layers
@@ -395,41 +467,50 @@ def bench_mlp_c4(steps: int, warmup: int):
     from bitsparse_amd.layers import FFNRelu2
 
     dev = torch.device("cuda", 0)
-    g = torch.Generator(device=dev).manual_seed(0)
+    g = torch.Generator().manual_seed(0)       # CPU draws, in the config's order
     B, D, H = 4096, 4096, 16384
-    x = torch.randn((B, D), device=dev, generator=g).to(torch.bfloat16).requires_grad_()
-    W1 = (0.02 * torch.randn((H, D), device=dev, generator=g)).to(torch.bfloat16).requires_grad_()
-    W2 = (0.02 * torch.randn((D, H), device=dev, generator=g)).to(torch.bfloat16).requires_grad_()
+    x = torch.randn((B, D), generator=g).to(torch.bfloat16).to(dev).requires_grad_()
+    W1 = (0.02 * torch.randn((H, D), generator=g)).to(torch.bfloat16).to(dev).requires_grad_()
+    W2 = (0.02 * torch.randn((D, H), generator=g)).to(torch.bfloat16).to(dev).requires_grad_()
     # z = x @ W1.T has std 0.02 * sqrt(D); shift by -1.2816 std for 90% zeros
     b1 = torch.full((H,), -1.2816 * 0.02 * D ** 0.5, device=dev, dtype=torch.bfloat16)
-    dY = torch.randn((B, D), device=dev, generator=g).to(torch.bfloat16)
+    dY = torch.randn((B, D), generator=g).to(torch.bfloat16).to(dev)
     buf = TensorBuffer(B * H, device=dev, dtype=torch.float8_e4m3fn)
 
-    def run(compressed: bool, ev=None):
+    def run(mode: str, ev=None):
         for p in (x, W1, W2):
             p.grad = None
         if ev is not None:
             ev[0].record()
-        if compressed:
+        if mode == "compressed":
             buf.reset_buffer()
             y = FFNRelu2.apply(x, W1, W2, b1, sparse_data=buf, storage_dtype=torch.float8_e4m3fn)
         else:
-            y = DenseFFNRelu2Fp8.apply(x, W1, W2, b1)
+            DenseFFNRelu2Fp8.WIDEN_WITH_HIP = mode == "dense_hip_widen"
+            try:
+                y = DenseFFNRelu2Fp8.apply(x, W1, W2, b1)
+            finally:
+                DenseFFNRelu2Fp8.WIDEN_WITH_HIP = False
         if ev is not None:
             ev[1].record()
-        y.backward(dY)
+        DenseFFNRelu2Fp8.WIDEN_WITH_HIP = mode == "dense_hip_widen"
+        try:
+            y.backward(dY)
+        finally:
+            DenseFFNRelu2Fp8.WIDEN_WITH_HIP = False
         if ev is not None:
             ev[2].record()
 
     out = {}
-    for mode in ("dense", "compressed"):
-        comp = mode == "compressed"
+    # dense: the reference's comparator (saved codes widened with torch's
+    # float8 cast); dense_hip_widen: the same with the library's widening kernel
+    for mode in ("dense", "dense_hip_widen", "compressed"):
         for _ in range(warmup):
-            run(comp)
+            run(mode)
         torch.cuda.synchronize()
         evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
         for i in range(steps):
-            run(comp, evs[i])
+            run(mode, evs[i])
         torch.cuda.synchronize()
         out[mode] = {"step_ms": round(sum(e[0].elapsed_time(e[2]) for e in evs) / steps, 4),
                      "fwd_ms": round(sum(e[0].elapsed_time(e[1]) for e in evs) / steps, 4),
@@ -447,6 +528,10 @@ def bench_mlp_c4(steps: int, warmup: int):
                                      "ratio": round(stored / dense_bytes, 4)}
     out["bwd_ratio_compressed_over_dense"] = round(out["compressed"]["bwd_ms"] / out["dense"]["bwd_ms"], 4)
     out["step_ratio_compressed_over_dense"] = round(out["compressed"]["step_ms"] / out["dense"]["step_ms"], 4)
+    out["bwd_ratio_compressed_over_dense_hip_widen"] = round(
+        out["compressed"]["bwd_ms"] / out["dense_hip_widen"]["bwd_ms"], 4)
+    out["step_ratio_compressed_over_dense_hip_widen"] = round(
+        out["compressed"]["step_ms"] / out["dense_hip_widen"]["step_ms"], 4)
     return out
 
 
@@ -466,17 +551,12 @@ def bench_sweep(steps: int, warmup: int, packed_only: bool = False):
     out = []
     mus = [("50%", 0.0), ("75%", -0.6745), ("90%", -1.2816), ("95%", -1.6449), ("99%", -2.3263)]
     cases = [(n, mu, st, False, False) for n, mu in mus for st in ("bf16", "e4m3fn")]
-    cases += [("90% skewed columns", -1.2816, "bf16", True, False)]
+    cases += [("90% skewed columns", -1.4328, st, True, False) for st in ("bf16", "e4m3fn")]
     cases += [(n, mu, st, False, True) for n, mu in mus[:3:2] for st in ("bf16", "e4m3fn")]
     if packed_only:
         cases = [c for c in cases if c[4]]
     for name, mu, storage, skew, pack in cases:
-        g = torch.Generator(device=dev).manual_seed(0)
-        pre = torch.randn((M, N), device=dev, generator=g) + mu
-        if skew:
-            pre += 0.5 * torch.randn((1, N), device=dev, generator=g)
-        x = pre.to(torch.bfloat16).relu_()
-        del pre
+        x = make_activation(M, N, mu, dev, skew)
         fp8 = storage == "e4m3fn"
         vdt = torch.float8_e4m3fn if fp8 else torch.bfloat16
         buf = TensorBuffer(M * N * (1 if fp8 else 2), device=dev, dtype=vdt, pack_sbit=pack)
@@ -525,13 +605,13 @@ def bench_stack(steps: int, warmup: int):
     from bitsparse_amd.layers import FFNRelu
 
     dev = torch.device("cuda", 0)
-    g = torch.Generator(device=dev).manual_seed(0)
+    g = torch.Generator().manual_seed(0)       # CPU draws: each block's W1, W2 in turn, then x, dY
     L, B, D, H = 12, 8192, 768, 3072
-    Ws = [((0.02 * torch.randn((H, D), device=dev, generator=g)).to(torch.bfloat16).requires_grad_(),
-           (0.02 * torch.randn((D, H), device=dev, generator=g)).to(torch.bfloat16).requires_grad_())
+    Ws = [((0.02 * torch.randn((H, D), generator=g)).to(torch.bfloat16).to(dev).requires_grad_(),
+           (0.02 * torch.randn((D, H), generator=g)).to(torch.bfloat16).to(dev).requires_grad_())
           for _ in range(L)]
-    x0 = torch.randn((B, D), device=dev, generator=g).to(torch.bfloat16).requires_grad_()
-    dY = torch.randn((B, D), device=dev, generator=g).to(torch.bfloat16)
+    x0 = torch.randn((B, D), generator=g).to(torch.bfloat16).to(dev).requires_grad_()
+    dY = torch.randn((B, D), generator=g).to(torch.bfloat16).to(dev)
     # value buffer sized to the stack's measured nonzeros (+8 per block for
     # alignment slack), as a user would size it for their sparsity
     with torch.no_grad():
@@ -543,7 +623,11 @@ def bench_stack(steps: int, warmup: int):
         del h, a
     buf = TensorBuffer(2 * nnz, device=dev)
     out = {}
-    for mode in ("dense", "compressed"):
+    # dense: every activation saved dense; checkpointed: every block
+    # recomputed in backward (the reference's activation-checkpointing
+    # comparator, experiment.py:300-306 via FFNReluABC.forward_base);
+    # compressed: every activation saved compressed
+    for mode in ("dense", "checkpointed", "compressed"):
         def run():
             for W1, W2 in Ws:
                 W1.grad = W2.grad = None
@@ -554,6 +638,8 @@ def bench_stack(steps: int, warmup: int):
             for W1, W2 in Ws:
                 if mode == "compressed":
                     h = h + FFNRelu.apply(h, W1, W2, sparse_data=buf)
+                elif mode == "checkpointed":
+                    h = h + DenseFFNRelu.apply_ckpt(h, W1, W2)
                 else:
                     h = h + DenseFFNRelu.apply(h, W1, W2)
             h.backward(dY)
@@ -567,8 +653,10 @@ def bench_stack(steps: int, warmup: int):
         if mode == "compressed":
             peak += buf.vals.numel() * buf.vals.element_size()   # allocated before `base`
         out[mode] = {"step_ms": round(ms, 4), "peak_bytes_above_base": int(peak)}
-    out["peak_ratio_compressed_over_dense"] = round(out["compressed"]["peak_bytes_above_base"] /
-                                                    out["dense"]["peak_bytes_above_base"], 4)
+    for mode in ("compressed", "checkpointed"):
+        out[f"peak_ratio_{mode}_over_dense"] = round(out[mode]["peak_bytes_above_base"] /
+                                                     out["dense"]["peak_bytes_above_base"], 4)
+        out[f"step_ratio_{mode}_over_dense"] = round(out[mode]["step_ms"] / out["dense"]["step_ms"], 4)
     out["note"] = ("residual stream h + block(h); the compressed peak counts its TensorBuffer "
                    "(sized to the stack's nonzeros) in full")
     out["buffer_bytes"] = int(2 * nnz)
@@ -720,6 +808,9 @@ def main() -> int:
                          "JSON (profiling entry point)")
     ap.add_argument("--sweep-only", action="store_true",
                     help="run only the configs[2] sparsity sweep and print its JSON (profiling entry point)")
+    ap.add_argument("--floor-only", action="store_true",
+                    help="run only the access-mix floor probes (bs_stream_probe) at the headline and "
+                         "configs[1] activation sizes and print their JSON (profiling entry point)")
     ap.add_argument("--kernels-only", action="store_true",
                     help="run only the gradient / unpack / fp8 kernel section and print its JSON "
                          "(profiling entry point)")
@@ -762,6 +853,9 @@ def main() -> int:
     if args.packed_only:
         print(json.dumps({"sweep": bench_sweep(args.steps, args.warmup, packed_only=True)}), flush=True)
         return 0
+    if args.floor_only:
+        print(json.dumps({"floor": measure_floors(args.steps, args.warmup)}), flush=True)
+        return 0
     if args.kernels_only:
         copy_gbs = measure_copy_gbs()
         if args.calibrate_copy:
@@ -781,6 +875,9 @@ def main() -> int:
     log(f"codec done: {codec['roundtrip_gbs']:.1f} GB/s round trip")
     copy_gbs = measure_copy_gbs()
     log(f"device copy: {copy_gbs:.1f} GB/s")
+    floor = measure_floors(args.steps, args.warmup, nnz_headline=codec["nnz"])
+    log(f"access-mix floor: compress {floor['configs[2] 16384x16384']['compress_mix_ms']} ms, "
+        f"decompress {floor['configs[2] 16384x16384']['decompress_mix_ms']} ms")
     if args.calibrate_copy:
         src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
         dst = torch.empty_like(src)
@@ -840,7 +937,7 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic: relu(N(mu,1)) drawn on the GPU with seed 0",
+        "data": "synthetic: relu(bf16(N(mu,1))), N(0,1) drawn on the CPU with torch.Generator seed 0",
         "config": {"workload": "configs[2] 16384x16384 bf16 ReLU activation round trip "
                                "(compress to bitmask+prefix+bf16 vals, decompress)",
                    "M": M, "N": N, "sparsity": codec["sparsity"], "value_storage": "bf16",
@@ -855,7 +952,11 @@ def main() -> int:
                                "(hipExtLaunchKernel via bs_launch_timing) on the launch stream, "
                                "over a second pass of the timed steps",
                      "achievable_copy_gbs": round(copy_gbs, 2),
-                     "frac_of_copy": round(codec["compress_gbs"] / copy_gbs, 4)},
+                     "frac_of_copy": round(codec["compress_gbs"] / copy_gbs, 4),
+                     "access_mix_floor_ms": floor["configs[2] 16384x16384"]["compress_mix_ms"],
+                     "frac_of_access_mix_floor": round(floor["configs[2] 16384x16384"]["compress_mix_ms"] /
+                                                       codec["compress_kernel_ms"], 4)},
+        "floor": floor,
         "kernels": {"compress_gbs": round(codec["compress_gbs"], 2),
                     "decompress_gbs": round(codec["decompress_gbs"], 2),
                     "compress_kernel_ms": round(codec["compress_kernel_ms"], 5),

@@ -17,7 +17,7 @@ LIB_NAME = "libbitsparse_hip.so"
 # BITSPARSE_HIP_LIB points at another build of the same sources (tuning sweeps)
 LIB_PATH = os.environ.get("BITSPARSE_HIP_LIB") or os.path.join(
     os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 BS_OK = 0
 BS_ERR_INVALID = 1
@@ -42,7 +42,8 @@ _SIGNATURES = {
     "bs_compress_relu": [_vp, _int, _i64, _i64, _int, _vp, _u32, _vp, _vp, _vp, _vp, _vp, _i64, _vp,
                          _int, _vp, _vp, _int, _vp, _vp, _i64, _u32, _vp, _vp],
     "bs_linear_relu_compress": [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _i64,
-                                _vp, _int, _vp, _vp, _vp, _vp, _i64, _u32, _vp],
+                                _vp, _int, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _u32, _vp],
+    "bs_linear_relu_compress_max_n": [_int],
     "bs_compress_packed": [_vp, _int, _i64, _i64, _int, _vp, _u32, _vp, _vp, _vp, _vp, _vp, _i64, _vp,
                            _vp, _vp, _vp, _vp, _i64, _u32, _int, _vp, _vp],
     "bs_amax_relu": [_vp, _i64, _vp, _i64, _u32, _vp],
@@ -76,6 +77,7 @@ _SIGNATURES = {
     "bs_launch_timing": [_int],
     "bs_nontemporal_min_bytes": [_i64],
     "bs_launch_timing_read": [_vp, _vp, _int, _vp],
+    "bs_stream_probe": [_int, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _int, _vp],
 }
 _RESTYPES = {
     "bs_last_error": ctypes.c_char_p,
@@ -83,6 +85,7 @@ _RESTYPES = {
     "bs_gemm_compressed_b_workspace_bytes": _i64,
     "bs_gemm_compressed_b_fp8_workspace_bytes": _i64,
     "bs_compress_noalloc_max_tiles": _i64,
+    "bs_linear_relu_compress_max_n": _i64,
     "bs_nontemporal_min_bytes": _i64,
     "bs_workspace_amax_slot": _vp,
     "bs_workspace_fallback_counter": _vp,

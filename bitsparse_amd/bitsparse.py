@@ -72,6 +72,9 @@ class BitsparseTensor:
         self.BLOCK_M = BLOCK_M
         self.BLOCK_N = BLOCK_N
         self.shape = shape
+        # produced by the fused up-projection: its look-back time-out flag
+        # (functions.LookbackCheck), checked before the values are first read
+        self.lookback_check = None
 
     @property
     def fp8(self) -> bool:
@@ -83,15 +86,16 @@ class BitsparseTensor:
         return self.grid_m * self.grid_n
 
     def __repr__(self):
-        return (f"BitsparseTensor(shape={list(self.shape)}, "
-                f"nnz={self.nnz()}, sparsity={self.sparsity_ratio():.2f}, "
-                f"pack_sbit={self.pack_sbit})")
+        M, N = self.shape
+        n = int(self.nnz().item())
+        store = f"{self.dtype}".replace("torch.", "") + (" packed" if self.pack_sbit else "")
+        return f"BitsparseTensor[{M}x{N}, {store}, {n} nonzeros, {100.0 * (1 - n / max(1, M * N)):.1f}% zeros]"
 
     def nnz(self):
-        """Number of set bitmask bits as a 0-d int64 tensor (diagnostics;
-        equals prefix[-1]).  Reference: lib_sparse/bitsparse.py:71-74."""
-        bits = torch.arange(8, device=self.bitmask.device, dtype=torch.uint8)
-        return ((self.bitmask[:, None] >> bits) & 1).sum()
+        """Number of nonzeros as a 0-d int64 tensor (diagnostics): the last
+        tile prefix, which counts every set bitmask bit.  Reference:
+        lib_sparse/bitsparse.py:71-74."""
+        return self.prefix[-1:].view(torch.int32).to(torch.int64)[0] & 0xFFFFFFFF
 
     def vram_size(self):
         """Stored bytes: values + bitmask + prefix (synchronises).
@@ -113,22 +117,30 @@ class TensorBuffer:
     """Preallocated value storage shared by several BitsparseTensors.
 
     Each compress appends at ``offset`` and advances it on the device, so no
-    host synchronisation is needed.  ``offset`` is rebound to a new 1-element
-    int64 tensor by every compress (the previous tensor becomes that
-    BitsparseTensor's ``vals_offset`` snapshot); ``reset_buffer`` starts over.
-    Values that do not fit are dropped by the kernel and flagged; see
-    ``overflowed``.  Reference: lib_sparse/bitsparse.py:90-117.
+    host synchronisation is needed.  By default ``offset`` is rebound to a new
+    1-element int64 tensor by every compress (the previous tensor becomes that
+    BitsparseTensor's ``vals_offset`` snapshot, so no copy is made).  With
+    ``inplace_offset=True`` the cursor keeps its identity as in the reference
+    (lib_sparse/src/functions.py:80-94): each compress snapshots it with a
+    device copy and writes the advanced cursor into the same tensor, so code
+    that holds ``buf.offset`` across a compress sees it move.
+    ``reset_buffer`` starts over.  Values that do not fit are dropped by the
+    kernel and flagged; see ``overflowed``.  Reference:
+    lib_sparse/bitsparse.py:90-117.
     """
     vals: Tensor
     offset: Tensor
 
     def __init__(self, size: int, device="cuda", dtype=torch.bfloat16,
-                 pack_sbit: bool = False):
-        """size: storage bytes; device: buffer device; dtype: stored dtype."""
+                 pack_sbit: bool = False, *, inplace_offset: bool = False):
+        """size: storage bytes; device: buffer device; dtype: stored dtype;
+        inplace_offset: advance ``offset`` in place (the reference's cursor
+        semantics) instead of rebinding it."""
         self.size = size
         self.device = device
         self.dtype = dtype
         self.pack_sbit = pack_sbit
+        self.inplace_offset = bool(inplace_offset)
         if pack_sbit:
             storage_size = (self.size + 3) // 4 * 4 + 4
             self.vals = torch.zeros(storage_size, device=self.device, dtype=torch.uint8)
@@ -142,7 +154,24 @@ class TensorBuffer:
 
     def reset_buffer(self):
         """Start filling from offset 0 again (once per training step)."""
-        self.offset = torch.zeros(1, device=self.device, dtype=torch.int64)
+        if self.inplace_offset:
+            self.offset.zero_()
+        else:
+            self.offset = torch.zeros(1, device=self.device, dtype=torch.int64)
+
+    def cursor(self) -> tuple[Tensor, Tensor]:
+        """(start, out) for one compress into this buffer: the kernel reads the
+        cursor from ``start`` and writes the advanced cursor into ``out``;
+        ``advance(out)`` afterwards.  In place: ``start`` is a snapshot copy and
+        ``out`` the cursor tensor itself."""
+        if self.inplace_offset:
+            return self.offset.clone(), self.offset
+        return self.offset, torch.empty(1, device=self.offset.device, dtype=torch.int64)
+
+    def advance(self, out: Tensor) -> None:
+        """Make ``out`` (from ``cursor``) the buffer's cursor."""
+        if not self.inplace_offset:
+            self.offset = out
 
     def overflowed(self) -> bool:
         """True if a compress ran out of capacity since construction

@@ -14,7 +14,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 PKG = os.path.join(ROOT, "bitsparse_amd")
 CSRC = os.path.join(PKG, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
-SOURCES = ["runtime.hip", "fp8.hip", "codec.hip", "dw_gemm.hip", "dw_gemm8.hip", "up_gemm.hip"]
+SOURCES = ["runtime.hip", "fp8.hip", "codec.hip", "dw_gemm.hip", "dw_gemm8.hip", "up_gemm.hip", "probe.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

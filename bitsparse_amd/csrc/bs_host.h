@@ -17,12 +17,17 @@ constexpr int64_t kWsHeaderBytes = 256;
 constexpr int64_t kWsAmaxOffset = 0;
 constexpr int64_t kWsFallbackOffset = 8;
 
-// Largest matrix accepted by the codec, gradient and GEMM entry points:
-// fewer than 2^32 elements, the range of the uint32 tile prefix (the kernels
-// index HBM with 64-bit element offsets).  The reference forms element
-// offsets in int32 (lib_sparse/src/triton_kernels.py:80), so its domain ends
-// at 2^31.
+// Largest matrix accepted: fewer than 2^32 elements, the range of the uint32
+// tile prefix (the kernels index HBM with 64-bit element offsets), on the
+// paths run past 2^31 elements on the GPU (raw bf16 compress: into a value
+// buffer, or count + values of the standalone path; bf16 decompress; the
+// bf16 dW GEMM); every other entry point (fp8
+// or packed storage, quantizing compress, gradients, the fp8 dW GEMM, the
+// fused up-projection, the reference-API pieces) stops at 2^31 until its
+// own run past that size exists.  The reference forms element offsets in
+// int32 (lib_sparse/src/triton_kernels.py:80), so its domain ends at 2^31.
 constexpr uint64_t kMaxElems = 1ull << 32;
+constexpr uint64_t kMaxElemsUntested = 1ull << 31;
 
 // Kernels that stream a dense matrix at least this large use nontemporal
 // (`nt`) loads and stores for it: nothing of it can stay in the 256 MiB last

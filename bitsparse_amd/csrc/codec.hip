@@ -1881,13 +1881,15 @@ extern "C" const uint32_t* bs_workspace_fallback_counter(const void* ws, int64_t
     return reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint8_t*>(ws) + kWsFallbackOffset);
 }
 
-static int check_dense(const void* dense, int dtype, int64_t M, int64_t N, const char* what)
+static int check_dense(const void* dense, int dtype, int64_t M, int64_t N, const char* what,
+                       uint64_t max_elems = kMaxElemsUntested)
 {
     if (dtype < 0 || dtype > 2) return set_error(BS_ERR_INVALID, "%s: unknown dtype code %d", what, dtype);
     if (M < 0 || N < 0) return set_error(BS_ERR_INVALID, "%s: negative shape", what);
     if ((M > 0 && N > 0) && dense == nullptr) return set_error(BS_ERR_INVALID, "%s: null input", what);
-    if ((uint64_t)M * (uint64_t)N >= kMaxElems)
-        return set_error(BS_ERR_INVALID, "%s: M*N must be < 2^32", what);
+    if ((uint64_t)M * (uint64_t)N >= max_elems)
+        return set_error(BS_ERR_INVALID, "%s: M*N must be < 2^%d on this path", what,
+                         max_elems == kMaxElems ? 32 : 31);
     int elem = dtype == DT_BF16 ? 2 : 1;
     if (((uintptr_t)dense) % elem)
         return set_error(BS_ERR_INVALID, "%s: input not aligned to its element size", what);
@@ -1917,7 +1919,12 @@ static int compress_impl(const void* dense, int in_dtype, int64_t M, int64_t N, 
         return set_error(BS_ERR_INVALID, "bs_compress: relu_out without relu");
     if (relu_out != nullptr && (((uintptr_t)relu_out) % (in_dtype == DT_BF16 ? 2 : 1)))
         return set_error(BS_ERR_INVALID, "bs_compress_relu: relu_out misaligned");
-    if (int rc = check_dense(dense, in_dtype, M, N, "bs_compress")) return rc;
+    // raw bf16 compress (values into a buffer, or the count pass of the
+    // standalone path) runs past 2^31 elements on the GPU; the quantizing,
+    // fp8-input and packed variants stop at 2^31
+    const bool big_ok = in_dtype == DT_BF16 && !quantize && !packed;
+    if (int rc = check_dense(dense, in_dtype, M, N, "bs_compress", big_ok ? kMaxElems : kMaxElemsUntested))
+        return rc;
     if (quantize && in_dtype != DT_BF16)
         return set_error(BS_ERR_INVALID, "bs_compress: quantize needs bf16 input");
     if (quantize && amax_slot == nullptr)
@@ -2057,7 +2064,10 @@ extern "C" int bs_compact_vals(const void* dense, int in_dtype, int64_t M, int64
                                int64_t num_tiles, int32_t* err_flags, void* stream)
 {
     clear_error();
-    if (int rc = check_dense(dense, in_dtype, M, N, "bs_compact_vals")) return rc;
+    // the bf16 values pass of the standalone path runs past 2^31 elements on the GPU
+    if (int rc = check_dense(dense, in_dtype, M, N, "bs_compact_vals",
+                             in_dtype == DT_BF16 ? kMaxElems : kMaxElemsUntested))
+        return rc;
     const int64_t T = ((M + 63) / 64) * ((N + 63) / 64);
     if (first_tile < 0 || num_tiles < 0 || first_tile + num_tiles > T)
         return set_error(BS_ERR_INVALID, "bs_compact_vals: tile range [%lld, %lld) outside [0, %lld)",
@@ -2190,8 +2200,11 @@ static int decompress_impl(const void* vals, int vals_dtype, int64_t vals_numel,
         return set_error(BS_ERR_INVALID, "bs_decompress: scale is only applied with square=1");
     if ((uint64_t)(first_m_tile * grid_n + num_tiles_in_batch) >= (1ull << 32))
         return set_error(BS_ERR_INVALID, "bs_decompress: tile ids exceed 32 bits");
-    if ((uint64_t)batch_rows * (uint64_t)K >= kMaxElems)
-        return set_error(BS_ERR_INVALID, "bs_decompress: batch_rows*K must be < 2^32");
+    // bf16 values without the square run past 2^31 elements on the GPU
+    const bool big_ok = vals_dtype == DT_BF16 && !square && !packed;
+    if ((uint64_t)batch_rows * (uint64_t)K >= (big_ok ? kMaxElems : kMaxElemsUntested))
+        return set_error(BS_ERR_INVALID, "bs_decompress: batch_rows*K must be < 2^%d on this path",
+                         big_ok ? 32 : 31);
     const int ob = square ? 2 : (vals_dtype == DT_BF16 ? 2 : 1);
     if (((uintptr_t)out) % ob) return set_error(BS_ERR_INVALID, "bs_decompress: output misaligned");
     GatherArgs a{};
@@ -2260,8 +2273,8 @@ extern "C" int bs_relu_grad(void* grad, int64_t M, int64_t N, const uint8_t* bit
     const int64_t T = ((M + 63) / 64) * ((N + 63) / 64);
     if (T == 0) return BS_OK;
     if (grad == nullptr || bitmask == nullptr) return set_error(BS_ERR_INVALID, "bs_relu_grad: null pointer");
-    if ((uint64_t)M * (uint64_t)N >= kMaxElems)
-        return set_error(BS_ERR_INVALID, "bs_relu_grad: M*N must be < 2^32");
+    if ((uint64_t)M * (uint64_t)N >= kMaxElemsUntested)
+        return set_error(BS_ERR_INVALID, "bs_relu_grad: M*N must be < 2^31");
     if (((uintptr_t)grad) & 1u) return set_error(BS_ERR_INVALID, "bs_relu_grad: grad misaligned");
     bool vec = (N % 8 == 0) && aligned16(grad);
     uint32_t gn = (uint32_t)((N + 63) / 64);
@@ -2311,8 +2324,8 @@ static int relu2_grad_impl(void* grad, int64_t M, int64_t N, const void* vals, i
     const int64_t T = ((M + 63) / 64) * ((N + 63) / 64);
     if (T == 0) return BS_OK;
     if (grad == nullptr) return set_error(BS_ERR_INVALID, "bs_relu2_grad: null grad");
-    if ((uint64_t)M * (uint64_t)N >= kMaxElems)
-        return set_error(BS_ERR_INVALID, "bs_relu2_grad: M*N must be < 2^32");
+    if ((uint64_t)M * (uint64_t)N >= kMaxElemsUntested)
+        return set_error(BS_ERR_INVALID, "bs_relu2_grad: M*N must be < 2^31");
     if (((uintptr_t)grad) & 1u) return set_error(BS_ERR_INVALID, "bs_relu2_grad: grad misaligned");
     GatherArgs a{};
     a.vals = (const uint8_t*)vals;

@@ -849,8 +849,10 @@ extern "C" int bs_gemm_compressed_b(const void* A, int64_t M, int64_t K, int64_t
     if (a_layout == 1 && lda < K) return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: lda < K");
     if (a_layout == 1 && K % 8 != 0)
         return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: a_layout 1 needs K %% 8 == 0");
-    if ((uint64_t)K * (uint64_t)N >= kMaxElems)
-        return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: K*N must be < 2^32");
+    // bf16 storage without the square runs past 2^31 elements on the GPU
+    const bool big_ok = vals_dtype == DT_BF16 && !square;
+    if ((uint64_t)K * (uint64_t)N >= (big_ok ? kMaxElems : kMaxElemsUntested))
+        return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: K*N must be < 2^%d on this path", big_ok ? 32 : 31);
     if (M == 0 || N == 0) return BS_OK;
     if (C == nullptr) return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: null C");
     if (((uintptr_t)C) & 1) return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: C misaligned");

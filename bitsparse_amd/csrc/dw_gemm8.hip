@@ -849,7 +849,7 @@ extern "C" int bs_gemm_compressed_b_fp8(const void* A, const float* a_scale, int
     if (a_scale == nullptr) return set_error(BS_ERR_INVALID, "%s: null a_scale", fn);
     if (a_layout == 0 && lda < M) return set_error(BS_ERR_INVALID, "%s: lda < M", fn);
     if (a_layout == 1 && lda < K) return set_error(BS_ERR_INVALID, "%s: lda < K", fn);
-    if ((uint64_t)K * (uint64_t)N >= kMaxElems) return set_error(BS_ERR_INVALID, "%s: K*N must be < 2^32", fn);
+    if ((uint64_t)K * (uint64_t)N >= kMaxElemsUntested) return set_error(BS_ERR_INVALID, "%s: K*N must be < 2^31", fn);
     if (lda >= (1ll << 31)) return set_error(BS_ERR_INVALID, "%s: lda must be < 2^31", fn);
     if (M == 0 || N == 0) return BS_OK;
     if (C == nullptr) return set_error(BS_ERR_INVALID, "%s: null C", fn);

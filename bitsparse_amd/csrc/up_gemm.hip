@@ -34,8 +34,11 @@
 // 256-row strip when tm is not the strip's first tile row: a workgroup
 // dispatched after it.  Every workgroup publishes its counts before it waits
 // for anything, so a strip completes once all of its NB workgroups have been
-// resident; the host caps NB at kUpMaxNB, half the workgroups the GPU holds
-// at once (one per CU).
+// resident.  The host bounds NB by half the workgroups the GPU holds at once
+// (the occupancy API's count per CU times the CUs).  Work from other streams
+// can still lower residency below that: a wait then ends after the caller's
+// patience with the time-out flag set (its own word, never the capacity
+// flags), the unit's offset is wrong, and the caller must discard the result.
 #include <algorithm>
 
 #include "bs_device.h"
@@ -60,7 +63,6 @@ constexpr int kUpLds = kUpOffSel + 256 * 32;            // + compaction selector
 // overrun) fits in the wave's 64 staged rows, where it is built
 static_assert(2 * (7 + kUpTiles * kTileNumel + 8) <= 64 * kUpHP, "unit run");
 static_assert(kUpLds <= 160 * 1024, "LDS budget");
-constexpr int64_t kUpMaxNB = 128;
 
 struct UpArgs {
     const uint16_t* x;            // [M, K], row stride ldx
@@ -81,18 +83,22 @@ struct UpArgs {
     int64_t* offset_out;
     int64_t* start_out;
     int32_t* err;
+    int32_t* timeout;             // set to 1 when a look-back wait gave up
     uint64_t* status;             // one word per unit
     uint32_t epoch;
+    uint64_t patience;            // ticks a look-back wait may last (0: give up at once)
 };
 
 // torch's GPU relu on bf16 bits: x <= 0 (either zero included) -> +0, NaN
 // and positive values keep their bits
 __device__ __forceinline__ uint32_t relu_bf16_bits(uint32_t b) { return (b - 0x8000u) < 0x7f81u ? 0u : b; }
 
-// A look-back wait longer than this (s_memrealtime ticks, 100 MHz: 20 ms)
-// ends the wait with bit 2 of *err set: every predecessor publishes without
-// waiting for anything, so this bound is never reached by a correct launch;
-// it only guarantees that every wave ends.
+// Default look-back patience (s_memrealtime ticks, 100 MHz: 20 ms).  A wait
+// longer than the patience ends with *timeout set: every predecessor
+// publishes before it waits for anything, so with all of a strip's
+// workgroups resident no wait comes near it; it guarantees that every wave
+// ends when they are not.  Patience 0 makes every unit but the first give up
+// without waiting (the tests force the time-out path that way).
 constexpr uint64_t kUpLookbackGiveUpTicks = 2000000;
 
 // Exclusive prefix of unit u from the status words of units 0 .. u-1.  Each
@@ -105,6 +111,10 @@ __device__ uint32_t up_lookback(const UpArgs& a, uint32_t u, int lane)
 {
     uint32_t excl = 0;
     int64_t pos = (int64_t)u - 1;
+    if (a.patience == 0 && pos >= 0) {          // the forced time-out: no wait at all
+        if (lane == 0 && a.timeout) atomicOr(a.timeout, 1);
+        return 0u;
+    }
     const uint64_t t0 = wall_clock64();
     while (pos >= 0) {
         uint32_t sum = 0;
@@ -124,8 +134,8 @@ __device__ uint32_t up_lookback(const UpArgs& a, uint32_t u, int lane)
         const int first = incs ? __ffsll((unsigned long long)incs) - 1 : 63;   // last lane needed
         const uint64_t need = first == 63 ? ~0ull : ((2ull << first) - 1ull);
         if (__ballot(unpub) & need) {
-            if (wall_clock64() - t0 > kUpLookbackGiveUpTicks) {
-                if (lane == 0 && a.err) atomicOr(a.err, 4);
+            if (wall_clock64() - t0 > a.patience) {
+                if (lane == 0 && a.timeout) atomicOr(a.timeout, 1);
                 break;
             }
             __builtin_amdgcn_s_sleep(2);
@@ -500,22 +510,49 @@ __global__ __launch_bounds__(256, 1) void up_relu_compress_kernel(UpArgs a)
     }
 }
 
+// Workgroups per tile row the launch accepts on device `dev`: half of what
+// the device holds at once (the occupancy API's count per CU times its CUs),
+// so that a strip's workgroups are co-resident with room to spare; 0 if the
+// queries fail.
+static int64_t up_max_nb(int dev)
+{
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        return 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, up_relu_compress_kernel, 256, 0) != hipSuccess ||
+        per_cu <= 0)
+        return 0;
+    return (int64_t)cus * per_cu / 2;
+}
+
 }  // namespace bs
 
 using namespace bs;
+
+extern "C" int64_t bs_linear_relu_compress_max_n(int device)
+{
+    clear_error();
+    const int64_t nb = up_max_nb(device);
+    if (nb <= 0) {
+        set_error(BS_ERR_HIP, "bs_linear_relu_compress_max_n: occupancy query failed");
+        return -1;
+    }
+    return nb * kUpBN;
+}
 
 extern "C" int bs_linear_relu_compress(const void* x, int64_t M, int64_t K, int64_t ldx, const void* w, int64_t N,
                                        int64_t ldw, const void* bias, void* h_out, int64_t ldh, uint8_t* bitmask,
                                        uint32_t* prefix, void* vals, int64_t vals_capacity,
                                        const int64_t* vals_offset_in, int align8, int64_t* vals_offset_out,
-                                       int64_t* vals_start_out, int32_t* err_flags, void* workspace,
-                                       int64_t workspace_bytes, uint32_t epoch, void* stream)
+                                       int64_t* vals_start_out, int32_t* err_flags, int32_t* timeout_flag,
+                                       int64_t patience_ticks, void* workspace, int64_t workspace_bytes,
+                                       uint32_t epoch, void* stream)
 {
     clear_error();
     const char* fn = "bs_linear_relu_compress";
     if (M <= 0 || N <= 0 || K < 0) return set_error(BS_ERR_INVALID, "%s: needs M, N > 0 and K >= 0", fn);
     if (K % 8 || N % 8) return set_error(BS_ERR_INVALID, "%s: K and N must be multiples of 8", fn);
-    if ((uint64_t)M * (uint64_t)N >= kMaxElems) return set_error(BS_ERR_INVALID, "%s: M*N must be < 2^32", fn);
+    if ((uint64_t)M * (uint64_t)N >= kMaxElemsUntested) return set_error(BS_ERR_INVALID, "%s: M*N must be < 2^31", fn);
     if (x == nullptr || w == nullptr || bitmask == nullptr || prefix == nullptr)
         return set_error(BS_ERR_INVALID, "%s: null pointer", fn);
     if (ldx < K || ldw < K || ldx % 8 || ldw % 8)
@@ -536,8 +573,14 @@ extern "C" int bs_linear_relu_compress(const void* x, int64_t M, int64_t K, int6
         return set_error(BS_ERR_INVALID, "%s: vals_offset_out aliases vals_offset_in", fn);
     if (epoch == 0 || epoch >= (1u << 30)) return set_error(BS_ERR_INVALID, "%s: epoch must be in [1, 2^30)", fn);
     const int64_t nb = (N + kUpBN - 1) / kUpBN;
-    if (nb > kUpMaxNB)
-        return set_error(BS_ERR_INVALID, "%s: N must be at most %lld", fn, (long long)(kUpMaxNB * kUpBN));
+    int dev = 0;
+    if (stream_device((hipStream_t)stream, &dev) != hipSuccess)
+        return set_error(BS_ERR_HIP, "%s: cannot resolve the stream's device", fn);
+    const int64_t max_nb = up_max_nb(dev);
+    if (max_nb <= 0) return set_error(BS_ERR_HIP, "%s: occupancy query failed", fn);
+    if (nb > max_nb)
+        return set_error(BS_ERR_INVALID, "%s: N must be at most %lld on this device", fn,
+                         (long long)(max_nb * kUpBN));
     if (int rc = refuse_capture((hipStream_t)stream, fn)) return rc;
     if (workspace == nullptr || workspace_bytes < bs_compress_workspace_bytes(M, N))
         return set_error(BS_ERR_INVALID, "%s: workspace too small (%lld < %lld bytes)", fn, (long long)workspace_bytes,
@@ -566,8 +609,10 @@ extern "C" int bs_linear_relu_compress(const void* x, int64_t M, int64_t K, int6
     a.offset_out = vals_offset_out;
     a.start_out = vals_start_out;
     a.err = err_flags;
+    a.timeout = timeout_flag;
     a.status = reinterpret_cast<uint64_t*>((uint8_t*)workspace + kWsHeaderBytes);
     a.epoch = epoch;
+    a.patience = patience_ticks < 0 ? kUpLookbackGiveUpTicks : (uint64_t)patience_ticks;
     const int64_t strips = (M + kUpBM - 1) / kUpBM;
     const int64_t blocks = strips * nb;
     if (blocks >= (1ll << 31)) return set_error(BS_ERR_INVALID, "%s: grid too large", fn);

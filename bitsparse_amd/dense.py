@@ -8,10 +8,15 @@ saves r = relu(z), rebuilds k*r^2 in backward).  ``DenseFFNReluFp8`` and
 ``DenseFFNRelu2Fp8`` are their fp8 modes (the same functions with an fp8
 DTYPE): fp8 GEMMs, the activation cached as e4m3fn + scale, k*r^2 rebuilt
 in bf16.
+
+``apply_ckpt`` / ``forward_ckpt`` are the reference's activation-checkpointing
+comparator (experiment.py:300-306, :378-384): the block saves only its inputs
+and recomputes the activation in backward.
 """
 from __future__ import annotations
 
 import torch
+import torch.utils.checkpoint
 from torch.autograd import Function
 
 from .config import RELU2_SCALE
@@ -38,6 +43,15 @@ class DenseFFNRelu(Function):
         grad_x = grad_pre @ W1 if ctx.needs_input_grad[0] else None
         grad_W1 = grad_pre.T @ x
         return grad_x, grad_W1, grad_W2
+
+    @staticmethod
+    def forward_ckpt(x, W1, W2):
+        """The block as plain autograd ops (recomputed in backward)."""
+        return (x @ W1.T).relu_() @ W2.T
+
+    @staticmethod
+    def apply_ckpt(x, W1, W2):
+        return torch.utils.checkpoint.checkpoint(DenseFFNRelu.forward_ckpt, x, W1, W2, use_reentrant=False)
 
 
 class DenseFFNReluFp8(Function):
@@ -95,11 +109,28 @@ class DenseFFNRelu2(Function):
         grad_W1 = grad_pre.T @ x
         return grad_x, grad_W1, grad_W2
 
+    @staticmethod
+    def forward_ckpt(x, W1, W2):
+        r = (x @ W1.T).relu_()
+        return r.square().mul_(RELU2_SCALE) @ W2.T
+
+    @staticmethod
+    def apply_ckpt(x, W1, W2):
+        return torch.utils.checkpoint.checkpoint(DenseFFNRelu2.forward_ckpt, x, W1, W2, use_reentrant=False)
+
 
 class DenseFFNRelu2Fp8(Function):
     """fp8 mode of DenseFFNRelu2: every GEMM per-tensor fp8, r = relu(z)
     saved as e4m3fn + scale (reference experiment.py:330-384); optional
-    first-layer bias b1 (no gradient), added before the activation."""
+    first-layer bias b1 (no gradient), added before the activation.
+
+    ``WIDEN_WITH_HIP``: the reference dequantizes the saved codes with torch's
+    float8 -> bf16 cast (``r_fp8.to(bfloat16)``, experiment.py:362), an
+    elementwise copy that runs at a fraction of HBM speed on ROCm; set True,
+    the comparator widens them with the library's exact e4m3fn -> bf16
+    kernel instead (same bits), so the compressed path is timed against a
+    comparator with the same fp8 plumbing."""
+    WIDEN_WITH_HIP = False
 
     @staticmethod
     def forward(ctx, x, W1, W2, b1=None):
@@ -118,7 +149,11 @@ class DenseFFNRelu2Fp8(Function):
     def backward(ctx, grad_output):
         x, W1, W2, r_fp8 = ctx.saved_tensors
         g8, gs = to_fp8(grad_output)
-        r = r_fp8.to(torch.bfloat16) * ctx.r_scale
+        if DenseFFNRelu2Fp8.WIDEN_WITH_HIP:
+            from .src.hip_operators import widen_e4m3fn
+            r = widen_e4m3fn(r_fp8) * ctx.r_scale
+        else:
+            r = r_fp8.to(torch.bfloat16) * ctx.r_scale
         h = r.square().mul_(RELU2_SCALE)
         grad_W2 = matmul(g8.T, h, True, a_scale=gs)
         del h

@@ -41,8 +41,8 @@ class ReluLinear(Function):
         ctx.save_for_backward(W)
         # h = z.relu_() fused into the compress pass (z is still updated in place)
         if is_fp8(dtype):
-            if dtype != torch.float8_e4m3fn:
-                raise TypeError("fp8 activation storage is float8_e4m3fn")
+            # any fp8 dtype stores e4m3fn codes + scale: the reference quantizes
+            # with to_fp8, whose output is e4m3fn for e5m2 too (fp8.py:123-129)
             h, scale, h_sparse = relu_quantize_and_compress(z, sparse_data, pack_sbit)
         else:
             scale = None
@@ -115,8 +115,7 @@ class Relu2Linear(Function):
         ctx.save_for_backward(W)
         # h = z.relu_() fused into the compress pass (z is still updated in place)
         if is_fp8(storage_dtype):
-            if storage_dtype != torch.float8_e4m3fn:
-                raise TypeError("fp8 activation storage is float8_e4m3fn")
+            # e4m3fn codes for every fp8 storage dtype, as to_fp8 makes them;
             # the forward multiplies the bf16 square, so no dense e4m3fn copy
             _, scale, h_sparse = relu_quantize_and_compress(z, sparse_data, pack_sbit, dense_out=False)
             h = z
@@ -209,6 +208,9 @@ class _UpReluLinear(Function):
         x, W1, W2 = ctx.saved_tensors
         h: BitsparseTensor = ctx.h_sparse
         ctx.h_sparse = None
+        # the forward kernel's look-back must not have given up (checked here,
+        # where the compressed form is first read; waits for that kernel only)
+        h.lookback_check.raise_if_timed_out()
         if ctx.square:
             grad_W2 = AspRelu2B(grad_output.T, h)
         else:

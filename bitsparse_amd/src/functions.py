@@ -107,13 +107,43 @@ def linear_relu_and_compress(x: Tensor, W: Tensor, b: Tensor | None,
     h = torch.empty((M, N), device=x.device, dtype=torch.bfloat16)
     bitmask = torch.empty(num_tiles * TILE_BYTES, device=x.device, dtype=torch.uint8)
     prefix = torch.empty(num_tiles + 1, device=x.device, dtype=torch.uint32)
-    vals_offset = sparse_data.offset
-    new_offset = torch.empty(1, device=x.device, dtype=torch.int64)
+    vals_offset, new_offset = sparse_data.cursor()
+    timeout = torch.zeros(1, device=x.device, dtype=torch.int32)
     ops.linear_relu_compress_into(x, W, b, h, bitmask, prefix, sparse_data.vals, vals_offset, new_offset,
-                                  sparse_data.err_flags)
-    sparse_data.offset = new_offset
-    return h, BitsparseTensor(sparse_data.vals, bitmask, prefix, (M, N), torch.bfloat16, grid_m, grid_n,
-                              BLOCK_M, BLOCK_N, scale=None, vals_offset=vals_offset)
+                                  sparse_data.err_flags, timeout)
+    sparse_data.advance(new_offset)
+    sp = BitsparseTensor(sparse_data.vals, bitmask, prefix, (M, N), torch.bfloat16, grid_m, grid_n,
+                         BLOCK_M, BLOCK_N, scale=None, vals_offset=vals_offset)
+    sp.lookback_check = LookbackCheck(timeout)
+    return h, sp
+
+
+class LookbackTimeout(RuntimeError):
+    """A fused up-projection's look-back wait gave up: its workgroups were not
+    all resident (other work on the GPU), so the compressed activation it
+    produced is wrong."""
+
+
+class LookbackCheck:
+    """The time-out flag of one fused up-projection launch, copied to pinned
+    host memory behind the kernel with an event, so that reading it waits for
+    that kernel only (not for everything queued since)."""
+
+    def __init__(self, flag: Tensor):
+        self.flag = flag
+        self.host = torch.empty(1, dtype=torch.int32, pin_memory=True)
+        self.host.copy_(flag, non_blocking=True)
+        self.event = torch.cuda.Event()
+        self.event.record()
+
+    def timed_out(self) -> bool:
+        self.event.synchronize()
+        return int(self.host[0]) != 0
+
+    def raise_if_timed_out(self) -> None:
+        if self.timed_out():
+            raise LookbackTimeout("fused up-projection: a look-back wait gave up (the GPU did not hold all "
+                                  "of a strip's workgroups at once); its compressed activation is invalid")
 
 
 def fused_linear_relu_ok(x: Tensor, W: Tensor, b: Tensor | None, sparse_data: TensorBuffer | None) -> bool:
@@ -145,11 +175,10 @@ def _to_tilesparse(dense: Tensor, scale: Tensor | None, sparse_data: TensorBuffe
         raise TypeError(f"TensorBuffer stores {sparse_data.vals.dtype} but the input is {dense.dtype}")
     bitmask = torch.empty(num_tiles * TILE_BYTES, device=dense.device, dtype=torch.uint8)
     prefix = torch.empty(num_tiles + 1, device=dense.device, dtype=torch.uint32)
-    vals_offset = sparse_data.offset                      # snapshot: never written again
-    new_offset = torch.empty(1, device=dense.device, dtype=torch.int64)
+    vals_offset, new_offset = sparse_data.cursor()        # the snapshot is never written again
     ops.compress_into(dense, bitmask, prefix, sparse_data.vals, vals_offset, new_offset,
                       sparse_data.err_flags, write_vals=True, **fused)
-    sparse_data.offset = new_offset
+    sparse_data.advance(new_offset)
     return BitsparseTensor(sparse_data.vals, bitmask, prefix, dense.shape, dense.dtype,
                            grid_m, grid_n, BLOCK_M, BLOCK_N, scale=scale,
                            vals_offset=vals_offset, pack_sbit=pack_sbit)
@@ -175,10 +204,10 @@ def _compress_packed_into_buffer(dense: Tensor, scale: Tensor | None, buf: Tenso
     if M * N == 0:
         return _compress_packed_staged(dense, scale, buf, bitmask, prefix, stored, **quant)
     vals_offset = torch.empty(1, device=dense.device, dtype=torch.int64)
-    new_offset = torch.empty(1, device=dense.device, dtype=torch.int64)
-    ops.compress_packed_into(dense, bitmask, prefix, buf.vals, buf.offset, new_offset, vals_offset,
+    start, new_offset = buf.cursor()
+    ops.compress_packed_into(dense, bitmask, prefix, buf.vals, start, new_offset, vals_offset,
                              buf.err_flags, **quant)
-    buf.offset = new_offset
+    buf.advance(new_offset)
     return BitsparseTensor(buf.vals, bitmask, prefix, dense.shape, stored,
                            grid_m, grid_n, BLOCK_M, BLOCK_N, scale=scale,
                            vals_offset=vals_offset, pack_sbit=True)
@@ -195,7 +224,10 @@ def _compress_packed_staged(dense: Tensor, scale: Tensor | None, buf: TensorBuff
     ops.compress_into(dense, bitmask, prefix, staging, None, nnz, None, write_vals=True, **quant)
     vals_offset = (buf.offset + 7) // 8 * 8
     pack_bits(staging, buf.vals, vals_offset, M * N, prefix[num_tiles:num_tiles + 1], buf.err_flags)
-    buf.offset = vals_offset + nnz
+    if buf.inplace_offset:
+        buf.offset.copy_(vals_offset + nnz)
+    else:
+        buf.offset = vals_offset + nnz
     return BitsparseTensor(buf.vals, bitmask, prefix, dense.shape, stored,
                            grid_m, grid_n, BLOCK_M, BLOCK_N, scale=scale,
                            vals_offset=vals_offset, pack_sbit=True)
@@ -258,12 +290,11 @@ def quantize_and_compress(
         return q, scale, sp
     if sparse_data.vals.dtype != torch.float8_e4m3fn:
         raise TypeError(f"TensorBuffer stores {sparse_data.vals.dtype}, need float8_e4m3fn")
-    vals_offset = sparse_data.offset
-    new_offset = torch.empty(1, device=dense.device, dtype=torch.int64)
+    vals_offset, new_offset = sparse_data.cursor()
     ops.compress_into(dense, bitmask, prefix, sparse_data.vals, vals_offset, new_offset,
                       sparse_data.err_flags, write_vals=True, quantize=True, scale_out=scale,
                       dense_q_out=q, amax_epoch=amax_epoch, **fused)
-    sparse_data.offset = new_offset
+    sparse_data.advance(new_offset)
     sp = BitsparseTensor(sparse_data.vals, bitmask, prefix, (M, N), torch.float8_e4m3fn, grid_m, grid_n,
                          BLOCK_M, BLOCK_N, scale=scale, vals_offset=vals_offset)
     return q, scale, sp

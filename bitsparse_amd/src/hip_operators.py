@@ -153,14 +153,22 @@ def compress_into(dense: Tensor, bitmask: Tensor, prefix: Tensor, vals: Tensor |
         check(L.bs_compress(*args, stream_handle(dense.device)), "bs_compress")
 
 
+# Look-back patience of the fused up-projection in s_memrealtime ticks
+# (100 MHz); -1: the library's default (20 ms); 0: every unit but the first
+# gives up at once (a test hook: the time-out path with every wave ending).
+UP_LOOKBACK_PATIENCE_TICKS = -1
+
+
 def linear_relu_compress_into(x: Tensor, W: Tensor, bias: Tensor | None, h_out: Tensor | None,
                               bitmask: Tensor, prefix: Tensor, vals: Tensor,
                               vals_offset_in: Tensor | None, vals_offset_out: Tensor | None,
-                              err_flags: Tensor | None) -> None:
+                              err_flags: Tensor | None, timeout_flag: Tensor | None = None) -> None:
     """h = relu(x @ W.T + bias) with its compressed form, in one kernel
     (bs_linear_relu_compress): x [M, K], W [N, K], bias [N] (or None), bf16,
     rows contiguous; h_out (or None) [M, N] bf16 receives h; bitmask / prefix /
-    vals / cursors as for ``compress_into`` (bf16 values)."""
+    vals / cursors as for ``compress_into`` (bf16 values); ``timeout_flag``
+    (int32 [1], zeroed, or None) is set to 1 if a look-back wait gave up, in
+    which case the compressed form is wrong."""
     require_device(x, "linear_relu_compress")
     for t, what in ((x, "x"), (W, "W")):
         if t.dtype != torch.bfloat16 or t.dim() != 2 or t.stride(1) != 1:
@@ -183,8 +191,22 @@ def linear_relu_compress_into(x: Tensor, W: Tensor, bias: Tensor | None, h_out: 
                                     ptr(h_out), h_out.stride(0) if h_out is not None else N,
                                     bitmask.data_ptr(), prefix.data_ptr(), vals.data_ptr(), vals.numel(),
                                     ptr(vals_offset_in), 0, ptr(vals_offset_out), None, ptr(err_flags),
+                                    ptr(timeout_flag), int(UP_LOOKBACK_PATIENCE_TICKS),
                                     ws.buf.data_ptr(), ws.nbytes, epoch, stream_handle(x.device)),
           "bs_linear_relu_compress")
+
+
+_UP_MAX_N: dict[int, int] = {}
+
+
+def linear_relu_compress_max_n(device: torch.device) -> int:
+    """Largest N the fused up-projection takes on ``device`` (its strips'
+    workgroups must be co-resident: half of what the device holds)."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    if idx not in _UP_MAX_N:
+        n = int(_lib.load().bs_linear_relu_compress_max_n(idx))
+        _UP_MAX_N[idx] = max(n, 0)
+    return _UP_MAX_N[idx]
 
 
 def linear_relu_compress_supported(x: Tensor, W: Tensor, bias: Tensor | None) -> bool:
@@ -193,7 +215,7 @@ def linear_relu_compress_supported(x: Tensor, W: Tensor, bias: Tensor | None) ->
         return False
     M, K = x.shape
     N = W.shape[0]
-    if M == 0 or N == 0 or K % 8 or N % 8 or N > 24576:
+    if M == 0 or N == 0 or K % 8 or N % 8 or not x.is_cuda or N > linear_relu_compress_max_n(x.device):
         return False
     for t in (x, W):
         if t.stride(1) != 1 or t.stride(0) % 8 or t.data_ptr() % 16:

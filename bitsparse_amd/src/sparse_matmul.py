@@ -72,18 +72,19 @@ def _row_blocks(sp: BitsparseTensor, row_batch: int):
 def _times_compressed(A: Tensor, B_sparse: BitsparseTensor, A_scale: Tensor | None, row_batch: int,
                       square: bool) -> Tensor:
     """A @ op(B) with op = identity or k * (.)^2, B compressed [K, N]."""
-    if USE_LDS_GEMM and B_sparse.fp8 and row_batch <= 0:
-        opa = as_fp8_operand(A, A_scale)
-        if dw_gemm.supports_fp8(opa.codes, B_sparse):
-            return dw_gemm.gemm_compressed_b_fp8(opa.codes, opa.scale, B_sparse, square)
-    if USE_LDS_GEMM and not B_sparse.fp8 and dw_gemm.supports(A, B_sparse, square=square):
-        return dw_gemm.gemm_compressed_b(A, B_sparse, square=square)
     # fp8 values are multiplied in fp8: with their stored scale, or (square)
     # re-quantized from the bf16 square, as the reference does
     fp8 = B_sparse.fp8
     b_scale = None if square else B_sparse.scale
+    if fp8 and row_batch <= 0:
+        opa = as_fp8_operand(A, A_scale)           # quantized once, whichever GEMM runs
+        if USE_LDS_GEMM and dw_gemm.supports_fp8(opa.codes, B_sparse):
+            return dw_gemm.gemm_compressed_b_fp8(opa.codes, opa.scale, B_sparse, square)
+        return fp8_gemm(opa, as_fp8_operand(decoded(B_sparse, square), b_scale), torch.bfloat16)
+    if USE_LDS_GEMM and not fp8 and dw_gemm.supports(A, B_sparse, square=square):
+        return dw_gemm.gemm_compressed_b(A, B_sparse, square=square)
     if row_batch <= 0:
-        return matmul(A, decoded(B_sparse, square), fp8, a_scale=A_scale, b_scale=b_scale)
+        return matmul(A, decoded(B_sparse, square), False)
     M, N = A.shape[0], B_sparse.shape[1]
     if not fp8:
         out = torch.zeros((M, N), device=A.device, dtype=A.dtype)

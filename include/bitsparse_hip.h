@@ -159,23 +159,37 @@ int bs_compress_relu(const void* preact, int in_dtype, int64_t M, int64_t N, int
  * W: bf16 [N, K] (row stride ldw), bias: bf16 [N] (nullable: no bias add,
  * one rounding), h_out: bf16 [M, N] (row stride ldh; nullable: h is not
  * written).  Needs M, N > 0, K >= 0, K and N multiples of 8, ldx, ldw, ldh
- * multiples of 8, x, W, h_out and vals 16-byte aligned, N <= 24576.  The
- * values are bf16; vals_capacity, vals_offset_in, align8, vals_offset_out,
- * vals_start_out, err_flags, workspace (bs_compress_workspace_bytes(M, N))
+ * multiples of 8, x, W, h_out and vals 16-byte aligned, and
+ * N <= bs_linear_relu_compress_max_n(device).  The values are bf16;
+ * vals_capacity, vals_offset_in, align8, vals_offset_out, vals_start_out,
+ * err_flags (capacity bits only), workspace (bs_compress_workspace_bytes(M, N))
  * and epoch as for bs_compress (refused while `stream` is capturing).  The
  * fp32 accumulation order is the kernel's own, so z can differ from a
  * library GEMM's in the last bit of some elements; the compressed form is
- * always exactly that of the h it writes.  Bit 2 of *err_flags reports a
- * look-back wait that was cut off after 20 ms (results then wrong; not
- * expected on a GPU this launch has to itself).  Replaces z = x @ W1^T; z = z + b1;
- * h = z.relu_(); dense_to_tilesparse(h) in lib_sparse/layers.py:86-89,
- * :29, :37.
+ * always exactly that of the h it writes.
+ *   timeout_flag    nullable int32 the kernel sets to 1 when a look-back wait
+ *                   gave up (the compressed form is then wrong and must be
+ *                   discarded).  A unit can wait for a workgroup dispatched
+ *                   after it in the same 256-row strip, so the strip's
+ *                   workgroups must be co-resident: the N bound keeps them to
+ *                   half of what the device holds, but other streams' work
+ *                   can still crowd them out.
+ *   patience_ticks  how long one wait may last, in s_memrealtime ticks
+ *                   (100 MHz); < 0: 20 ms; 0: every unit but the first
+ *                   gives up without waiting (a test hook: forces the
+ *                   time-out path with every wave still ending normally).
+ * Replaces z = x @ W1^T; z = z + b1; h = z.relu_(); dense_to_tilesparse(h) in
+ * lib_sparse/layers.py:86-89, :29, :37.
  */
 int bs_linear_relu_compress(const void* x, int64_t M, int64_t K, int64_t ldx, const void* w, int64_t N,
                             int64_t ldw, const void* bias, void* h_out, int64_t ldh, uint8_t* bitmask,
                             uint32_t* prefix, void* vals, int64_t vals_capacity, const int64_t* vals_offset_in,
                             int align8, int64_t* vals_offset_out, int64_t* vals_start_out, int32_t* err_flags,
-                            void* workspace, int64_t workspace_bytes, uint32_t epoch, void* stream);
+                            int32_t* timeout_flag, int64_t patience_ticks, void* workspace,
+                            int64_t workspace_bytes, uint32_t epoch, void* stream);
+/* Largest N bs_linear_relu_compress accepts on `device` (-1 if the occupancy
+ * query fails).  No counterpart in the reference. */
+int64_t bs_linear_relu_compress_max_n(int device);
 
 /*
  * bs_compress with pack_sbit storage: the values are written straight into
@@ -441,6 +455,23 @@ int bs_compress_noalloc(const void* dense, int in_dtype, int64_t M, int64_t N, i
                         int64_t* vals_offset_out, int64_t* vals_start_out, int write_vals,
                         int32_t* err_flags, void* relu_out, void* stream);
 int64_t bs_compress_noalloc_max_tiles(void);
+
+/*
+ * bs_stream_probe — no counterpart in the reference: a measurement kernel, the
+ * floor of the codec kernels' HBM access mix.  mode 0 (compress mix): read the
+ * [M, N] bf16 matrix `dense` in the compress kernel's load pattern (8 tiles per
+ * 512-thread workgroup, nontemporal when `nontemporal`), store one byte per
+ * 8-element chunk into `bitmask` (T*512 bytes) and `vals_per_unit` bytes per
+ * 8 tiles into `vals` (16-byte stores); mode 1 (decompress mix): read those
+ * bitmask and value bytes and write `dense`.  No scan, compaction or gather:
+ * the bytes of a compress (decompress) launch with `vals_per_unit` = the
+ * mean value bytes of 8 tiles, and nothing else.  M, N multiples of 64, T a
+ * multiple of 8, vals_per_unit a multiple of 128 in [0, 65536], `vals_bytes` >=
+ * T/8 * vals_per_unit, `bitmask_bytes` >= T*512.
+ */
+int bs_stream_probe(int mode, void* dense, int64_t M, int64_t N, void* vals, int64_t vals_bytes,
+                    int64_t vals_per_unit, uint8_t* bitmask, int64_t bitmask_bytes, int nontemporal,
+                    void* stream);
 
 /* Device pointer of the amax slot inside a workspace (for bs_compress). */
 const uint64_t* bs_workspace_amax_slot(const void* workspace, int64_t workspace_bytes);

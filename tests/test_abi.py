@@ -90,25 +90,46 @@ def test_invalid_arguments_rejected_on_host():
                        None, None, 1, None, fake, 1 << 20, 0, None)
     assert rc == _lib.BS_ERR_INVALID and "epoch" in _err()
     # matrices of 2^32 elements or more (the uint32 prefix's range) are
-    # refused by every codec / GEMM entry
+    # refused by every codec / GEMM entry; the paths not yet run past 2^31
+    # elements on the GPU (everything but the raw bf16 compress, bf16
+    # decompress and the bf16 dW GEMM) already at 2^31
     big_m, big_n = 1 << 16, 1 << 16
-    rc = L.bs_tile_pack(fake, 0, big_m, big_n, fake, fake, None)
-    assert rc == _lib.BS_ERR_INVALID and "2^32" in _err()
-    rc = L.bs_compress(fake, 0, big_m, big_n, 0, None, 0, None, None, fake, fake, fake, 10, None, 0,
-                       None, None, 1, None, fake, 1 << 30, 1, None)
-    assert rc == _lib.BS_ERR_INVALID and "2^32" in _err()
-    rc = L.bs_compact_vals(fake, 0, big_m, big_n, fake, fake, fake, 10, None, 0, 1, None, None)
+    mid_m = 1 << 15                     # mid_m * big_n = 2^31
+    rc = L.bs_compress(fake, 0, big_m, big_n, 0, None, 0, None, None, fake, fake, fake, 10, fake, 0,
+                       fake + 64, None, 1, None, fake, 1 << 30, 1, None)
     assert rc == _lib.BS_ERR_INVALID and "2^32" in _err()
     rc = L.bs_decompress(fake, 0, 10, fake, fake, None, fake, 0, big_n // 64, big_n, big_m, 64, 0, 1.0,
                          None, None)
     assert rc == _lib.BS_ERR_INVALID and "2^32" in _err()
-    rc = L.bs_relu_grad(fake, big_m, big_n, fake, None)
-    assert rc == _lib.BS_ERR_INVALID and "2^32" in _err()
-    rc = L.bs_relu2_grad(fake, big_m, big_n, fake, 0, 10, fake, fake, None, 1.0, None, None)
-    assert rc == _lib.BS_ERR_INVALID and "2^32" in _err()
     rc = L.bs_gemm_compressed_b(fake, 64, big_m, 64, 0, fake, 0, 10, fake, fake, None, big_n, 0, 1.0,
                                 None, fake, fake, 1 << 30, None)
     assert rc == _lib.BS_ERR_INVALID and "2^32" in _err()
+    rc = L.bs_compact_vals(fake, 0, big_m, big_n, fake, fake, fake, 10, None, 0, 1, None, None)
+    assert rc == _lib.BS_ERR_INVALID and "2^32" in _err()
+    for m in (big_m, mid_m):
+        rc = L.bs_tile_pack(fake, 0, m, big_n, fake, fake, None)
+        assert rc == _lib.BS_ERR_INVALID and "2^31" in _err()
+        rc = L.bs_compact_vals(fake, 1, m, big_n, fake, fake, fake, 10, None, 0, 1, None, None)
+        assert rc == _lib.BS_ERR_INVALID and "2^31" in _err()                     # e4m3fn values
+        rc = L.bs_compress(fake, 0, m, big_n, 1, fake, 1, None, None, fake, fake, fake, 10, fake, 0,
+                           fake + 64, None, 1, None, fake, 1 << 30, 1, None)      # quantizing
+        assert rc == _lib.BS_ERR_INVALID and "2^31" in _err()
+        rc = L.bs_compress_packed(fake, 0, m, big_n, 0, None, 0, None, None, fake, fake, fake, 64, fake,
+                                  fake + 64, None, None, fake, 1 << 30, 1, 0, None, None)
+        assert rc == _lib.BS_ERR_INVALID and "2^31" in _err()
+        rc = L.bs_decompress(fake, 1, 10, fake, fake, None, fake, 0, big_n // 64, big_n, m, 64, 0, 1.0,
+                             None, None)                                           # e4m3fn values
+        assert rc == _lib.BS_ERR_INVALID and "2^31" in _err()
+        rc = L.bs_decompress(fake, 0, 10, fake, fake, None, fake, 0, big_n // 64, big_n, m, 64, 1, 1.0,
+                             None, None)                                           # ReLU^2 square
+        assert rc == _lib.BS_ERR_INVALID and "2^31" in _err()
+        rc = L.bs_relu_grad(fake, m, big_n, fake, None)
+        assert rc == _lib.BS_ERR_INVALID and "2^31" in _err()
+        rc = L.bs_relu2_grad(fake, m, big_n, fake, 0, 10, fake, fake, None, 1.0, None, None)
+        assert rc == _lib.BS_ERR_INVALID and "2^31" in _err()
+        rc = L.bs_gemm_compressed_b(fake, 64, m, 64, 0, fake, 0, 10, fake, fake, None, big_n, 1, 1.0,
+                                    None, fake, fake, 1 << 30, None)              # ReLU^2 square
+        assert rc == _lib.BS_ERR_INVALID and "2^31" in _err()
     # aliasing cursors
     rc = L.bs_compress(fake, 0, 64, 64, 0, None, 0, None, None, fake, fake, fake, 10, fake + 64, 0,
                        fake + 64, None, 1, None, fake, 1 << 20, 1, None)

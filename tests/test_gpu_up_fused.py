@@ -191,3 +191,76 @@ def test_unsupported_operands_are_refused(dev):
     assert not H.linear_relu_compress_supported(x, W, b)
     with pytest.raises(ValueError, match="multiples of 8"):
         _run(x, W, b)
+
+
+def test_forced_lookback_timeout_sets_its_own_flag(dev, monkeypatch):
+    """Patience 0 makes every unit but the first give up without waiting (the
+    host forces the time-out; every wave still ends normally): the time-out
+    word is set and the capacity flags stay clear."""
+    H = _ops()
+    monkeypatch.setattr(H, "UP_LOOKBACK_PATIENCE_TICKS", 0)
+    x, W, b = _operands(512, 768, 64, 21, dev)          # 2 strips x 4 workgroups x 4 units
+    M, N = x.shape[0], W.shape[0]
+    T = (M // 64) * (N // 64)
+    h = torch.empty((M, N), device=dev, dtype=torch.bfloat16)
+    bm = torch.empty(T * 512, device=dev, dtype=torch.uint8)
+    pf = torch.empty(T + 1, device=dev, dtype=torch.uint32)
+    vals = torch.zeros(M * N, device=dev, dtype=torch.bfloat16)
+    off_in = torch.zeros(1, device=dev, dtype=torch.int64)
+    off_out = torch.empty(1, device=dev, dtype=torch.int64)
+    err = torch.zeros(1, device=dev, dtype=torch.int32)
+    timeout = torch.zeros(1, device=dev, dtype=torch.int32)
+    H.linear_relu_compress_into(x, W, b, h, bm, pf, vals, off_in, off_out, err, timeout)
+    torch.cuda.synchronize()
+    assert int(timeout.item()) == 1
+    assert int(err.item()) == 0
+    # the default patience on the same operands: no time-out, exact result
+    monkeypatch.setattr(H, "UP_LOOKBACK_PATIENCE_TICKS", -1)
+    timeout.zero_()
+    off_out.zero_()
+    H.linear_relu_compress_into(x, W, b, h, bm, pf, vals, off_in, off_out, err, timeout)
+    torch.cuda.synchronize()
+    assert int(timeout.item()) == 0 and int(err.item()) == 0
+    _check_compressed(h, bm, pf, vals, off_out)
+
+
+@pytest.mark.parametrize("relu2", [False, True])
+def test_layer_raises_on_lookback_timeout(dev, monkeypatch, relu2):
+    """FFNRelu / FFNRelu2 through the fused up-projection refuse to use an
+    activation whose look-back gave up: backward raises LookbackTimeout
+    instead of computing gradients from a misplaced value run."""
+    from bitsparse_amd import layers
+    from bitsparse_amd.bitsparse import TensorBuffer
+    from bitsparse_amd.src.functions import LookbackTimeout
+    H = _ops()
+    monkeypatch.setattr(layers, "USE_FUSED_UP", True)
+    monkeypatch.setattr(H, "UP_LOOKBACK_PATIENCE_TICKS", 0)
+    x, W1, b1 = _operands(512, 768, 128, 22, dev)
+    W2 = (0.05 * preact_input((128, 768), seed=23).float()).to(torch.bfloat16).to(dev).requires_grad_()
+    W1 = W1.clone().requires_grad_()
+    buf = TensorBuffer(2 * 512 * 768, device=dev)
+    fn = layers.FFNRelu2 if relu2 else layers.FFNRelu
+    y = fn.apply(x, W1, W2, b1, sparse_data=buf)
+    with pytest.raises(LookbackTimeout):
+        y.backward(torch.ones_like(y))
+    assert not buf.overflowed()
+
+
+def test_width_bound_from_occupancy(dev):
+    """The widest N the fused kernel takes comes from the occupancy API (half
+    of the workgroups the device holds, 192 columns each); wider is refused by
+    the entry point and routed to the library path by the layers."""
+    H = _ops()
+    from bitsparse_amd import _lib
+    from bitsparse_amd.src.functions import fused_linear_relu_ok
+    from bitsparse_amd.bitsparse import TensorBuffer
+    max_n = H.linear_relu_compress_max_n(dev)
+    props = torch.cuda.get_device_properties(dev)
+    assert max_n > 0 and max_n % 192 == 0
+    assert max_n <= 192 * props.multi_processor_count      # at most one workgroup per CU here
+    assert int(_lib.load().bs_linear_relu_compress_max_n(dev.index or 0)) == max_n
+    x, W, b = _operands(64, max_n + 192, 16, 24, dev, bias=False)
+    assert not H.linear_relu_compress_supported(x, W, b)
+    assert not fused_linear_relu_ok(x, W, b, TensorBuffer(2 * 64 * (max_n + 192), device=dev))
+    with pytest.raises(ValueError, match="at most"):
+        _run(x, W, b)
