@@ -50,8 +50,9 @@ constexpr int kRunSlots = kTileNumel / 8 + 2;   // one bf16-staged run + phase, 
 //   Cfg512: 512 x 128, 8 waves (two per SIMD), 64 x 128 per wave: every
 //           decoded B element feeds 512 rows instead of 256, half the decode
 //           instructions per MFMA
-template <int WGM_, int WGN_, int WM_, int WN_, bool AQ_>
+template <int WGM_, int WGN_, int WM_, int WN_, bool AQ_, int MINB_ = 1>
 struct GemmCfg {
+    static constexpr int MINB = MINB_;                           // workgroups per CU (launch bound)
     // AQ: A fragments are loaded one k-quarter ahead (2 register sets) instead
     // of one K-step ahead (4 sets); with two waves per SIMD the other wave
     // covers the shorter lead
@@ -69,7 +70,7 @@ struct GemmCfg {
     // ds_read_b64_tr_b16 start 16 banks apart and the two column halves of a
     // 32-lane half-wave fill the other 8-bank gaps, so fragment reads are
     // conflict-free
-    static constexpr int BP = BN + 32;
+    static constexpr int BP = ((BN * 2 + 255) / 256 * 256 + 64) / 2;
     static constexpr int SEG = 4 * IM * JN;                      // MFMAs (segments) per K-step
     static constexpr int PER = SEG / CH;                         // segments per decoded chunk
     // LDS carve-up (bytes)
@@ -88,6 +89,17 @@ using Cfg256 = GemmCfg<2, 2, 128, 128, false>;
 // 8 x 1 waves of 64 x 128: each A row block is read by one wave (a 4 x 2 grid
 // of 128 x 64 reads every A block twice and measured 4% slower)
 using Cfg512 = GemmCfg<8, 1, 64, 128, false>;
+//   Cfg768: 768 x 64, 8 waves (two per SIMD) of 96 x 64: a C tile spans up
+//           to 768 rows (the MLP dW shapes with d_out <= 768), so each B tile
+//           is decoded once per K-step for all of M; one tile per step, one
+//           decoded chunk per lane
+using Cfg768 = GemmCfg<8, 1, 96, 64, false>;
+//   Cfg256h: 256 x 128, 4 waves of 128 x 64 (2 x 2), two workgroups per CU:
+//            with a wave of the other workgroup on every SIMD, the value-run
+//            and A loads of one workgroup hide behind the other's MFMAs
+//   Cfg256v: 256 x 128, 4 waves of 64 x 128 (4 x 1), two workgroups per CU
+using Cfg256h = GemmCfg<2, 2, 128, 64, true, 2>;
+using Cfg256v = GemmCfg<4, 1, 64, 128, true, 2>;
 
 struct GemmArgs {
     const uint16_t* Apk;          // A in MFMA-fragment order (pack_a_*_kernel)
@@ -180,7 +192,7 @@ __device__ __forceinline__ RunUnit<UB> load_unit_tail(bs_rsrc rs, uint32_t off)
 }
 
 template <typename CFG, int V_T, bool SQUARE, bool HAS_SCALE>
-__global__ __launch_bounds__(CFG::THREADS, 1) void gemm_cb_kernel(GemmArgs a)
+__global__ __launch_bounds__(CFG::THREADS, CFG::MINB) void gemm_cb_kernel(GemmArgs a)
 {
     constexpr int NT = CFG::NT, DW = CFG::DW, CH = CFG::CH, BP = CFG::BP, IM = CFG::IM, JN = CFG::JN;
     constexpr int VB = V_T == DT_BF16 ? 2 : 1;                   // stored value bytes
@@ -190,7 +202,9 @@ __global__ __launch_bounds__(CFG::THREADS, 1) void gemm_cb_kernel(GemmArgs a)
     // units per lane loaded one step ahead (<= 20 registers: 2560 plain bf16
     // values, 1536 bf16 / 1024 fp8 values to square); a denser tile's
     // remaining units are loaded when the run is staged
-    constexpr int RXP0 = UB == 16 ? 5 : (UB == 8 ? 6 : 4);
+    // (two workgroups per CU: 2 units, the 50% zeros tile of a plain run,
+    // to stay within 256 registers)
+    constexpr int RXP0 = CFG::MINB > 1 ? 2 : (UB == 16 ? 5 : (UB == 8 ? 6 : 4));
     // the DW waves decoding one tile stage its run together: unit u is staged
     // by lane u % 64 of wave (u / 64) % DW, in pass u / (64 DW)
     constexpr int RXD = (RX + DW - 1) / DW;                      // passes per wave, worst case
@@ -772,18 +786,19 @@ __global__ __launch_bounds__(256) void zero_fill_u16_kernel(uint16_t* C, int64_t
     for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) C[i] = 0;
 }
 
-// Split-K factor: fewest "rounds x steps" with one workgroup per CU on kCus
-// CUs, a small charge for the partial-sum pass, <= kMaxSteps per workgroup
+// Split-K factor: fewest "rounds x steps" with `per_cu` workgroups per CU on
+// kCus CUs, a small charge for the partial-sum pass, <= kMaxSteps per workgroup
 // and >= 8 steps per workgroup where possible.
-static int gemm_split(int64_t M, int64_t N, int64_t K, int64_t bm, int64_t bn)
+static int gemm_split(int64_t M, int64_t N, int64_t K, int64_t bm, int64_t bn, int per_cu)
 {
+    const int64_t slots = (int64_t)kCus * per_cu;
     const int64_t tiles = ((N + bn - 1) / bn) * ((M + bm - 1) / bm);
     const int64_t ksteps = (K + kBK - 1) / kBK;
     const int64_t min_split = (ksteps + kMaxSteps - 1) / kMaxSteps;
     int64_t best = min_split, best_cost = -1;
     for (int64_t s = min_split; s <= 64; s++) {
         if (s > min_split && ksteps / s < 8) break;
-        const int64_t rounds = (tiles * s + kCus - 1) / kCus;
+        const int64_t rounds = (tiles * s + slots - 1) / slots;
         const int64_t cost = rounds * ((ksteps + s - 1) / s) + (s > 1 ? 2 : 0);
         if (best_cost < 0 || cost < best_cost) {
             best = s;
@@ -798,9 +813,15 @@ static int64_t apk_nkb(int64_t K) { return (K + kBK - 1) / kBK * (kBK / 16); }
 static int64_t apk_bytes(int64_t M, int64_t K) { return (M + 31) / 32 * apk_nkb(K) * 1024; }
 
 // Launch plan: 512-row workgroups when they cover M with no more padding
-// than 256-row ones (half the decode work per MFMA), else 256 x 256.
+// than 256-row ones (half the decode work per MFMA); else 256 x 128 with two
+// workgroups per CU (configs[1]'s 768 x 8192 x 3072: 78 us per call against
+// 87 us with one 256 x 256 workgroup per CU, and 104 us with 768 x 64
+// workgroups, which decode each B tile once but re-read A for every 64
+// columns).  BITSPARSE_DW_CFG (256 / 512 / 768 / 2561 for 256h / 2562 for
+// 256v) forces a shape (tuning runs).
+enum { CFG_256 = 0, CFG_512 = 1, CFG_768 = 2, CFG_256H = 3, CFG_256V = 4 };
 struct GemmPlan {
-    bool big;
+    int cfg;
     int64_t bm, bn;
     int split;
 };
@@ -809,10 +830,25 @@ static GemmPlan gemm_plan(int64_t M, int64_t N, int64_t K)
     GemmPlan p;
     const int64_t pad512 = (M + Cfg512::BM - 1) / Cfg512::BM * Cfg512::BM;
     const int64_t pad256 = (M + Cfg256::BM - 1) / Cfg256::BM * Cfg256::BM;
-    p.big = M >= Cfg512::BM && pad512 <= pad256;
-    p.bm = p.big ? Cfg512::BM : Cfg256::BM;
-    p.bn = p.big ? Cfg512::BN : Cfg256::BN;
-    p.split = gemm_split(M, N, K, p.bm, p.bn);
+    if (M >= Cfg512::BM && pad512 <= pad256) p.cfg = CFG_512;
+    else p.cfg = CFG_256V;
+    if (const char* ev = getenv("BITSPARSE_DW_CFG")) {
+        const int v = atoi(ev);
+        if (v == 256) p.cfg = CFG_256;
+        else if (v == 512) p.cfg = CFG_512;
+        else if (v == 768) p.cfg = CFG_768;
+        else if (v == 2561) p.cfg = CFG_256H;
+        else if (v == 2562) p.cfg = CFG_256V;
+    }
+    switch (p.cfg) {
+    case CFG_768: p.bm = Cfg768::BM; p.bn = Cfg768::BN; break;
+    case CFG_512: p.bm = Cfg512::BM; p.bn = Cfg512::BN; break;
+    case CFG_256H: p.bm = Cfg256h::BM; p.bn = Cfg256h::BN; break;
+    case CFG_256V: p.bm = Cfg256v::BM; p.bn = Cfg256v::BN; break;
+    default: p.bm = Cfg256::BM; p.bn = Cfg256::BN; break;
+    }
+    const int per_cu = (p.cfg == CFG_256H || p.cfg == CFG_256V) ? 2 : 1;
+    p.split = gemm_split(M, N, K, p.bm, p.bn, per_cu);
     return p;
 }
 static int64_t align_up256(int64_t x) { return (x + 255) / 256 * 256; }
@@ -925,7 +961,16 @@ extern "C" int bs_gemm_compressed_b(const void* A, int64_t M, int64_t K, int64_t
     g.nrb = (uint32_t)nrb;
 #define BS_GEMM_LAUNCH(VT, SQ, SC)                                                                              \
     do {                                                                                                        \
-        if (plan.big)                                                                                           \
+        if (plan.cfg == CFG_768)                                                                                \
+            hipLaunchKernelGGL((gemm_cb_kernel<Cfg768, VT, SQ, SC>), dim3((uint32_t)blocks), dim3(Cfg768::THREADS), \
+                               0, st, g);                                                                       \
+        else if (plan.cfg == CFG_256H)                                                                          \
+            hipLaunchKernelGGL((gemm_cb_kernel<Cfg256h, VT, SQ, SC>), dim3((uint32_t)blocks),                   \
+                               dim3(Cfg256h::THREADS), 0, st, g);                                               \
+        else if (plan.cfg == CFG_256V)                                                                          \
+            hipLaunchKernelGGL((gemm_cb_kernel<Cfg256v, VT, SQ, SC>), dim3((uint32_t)blocks),                   \
+                               dim3(Cfg256v::THREADS), 0, st, g);                                               \
+        else if (plan.cfg == CFG_512)                                                                           \
             hipLaunchKernelGGL((gemm_cb_kernel<Cfg512, VT, SQ, SC>), dim3((uint32_t)blocks), dim3(Cfg512::THREADS), \
                                0, st, g);                                                                       \
         else                                                                                                    \

@@ -106,8 +106,12 @@ def test_hip_reproduces_golden(dev, case):
     g = from_bits(d[f"{case}/grad"], torch.bfloat16).to(dev)
     assert np.array_equal(bits(H.relu2_grad_sparse_(g, sp)), d[f"{case}/relu2_grad"])
     pk = dense_to_tilesparse(x, scale, pack_sbit=True)
-    nb = (nv * O.bits_per_value(CODES[name]) + 7) // 8
-    assert np.array_equal(pk.vals.cpu().numpy()[:nb], d[f"{case}/stream"][:nb])
+    nbits = nv * O.bits_per_value(CODES[name])
+    got, want = pk.vals.cpu().numpy(), d[f"{case}/stream"]
+    assert np.array_equal(got[:nbits // 8], want[:nbits // 8])
+    if nbits % 8:      # the last byte's bits past the run are unspecified (padding)
+        keep = (1 << (nbits % 8)) - 1
+        assert got[nbits // 8] & keep == want[nbits // 8] & keep
     if name == "bf16":
         q, s = to_fp8(x)
         assert np.array_equal(bits(q), d[f"{case}/to_fp8_q"])

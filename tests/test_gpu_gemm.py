@@ -22,7 +22,8 @@ def _check(C, ref):
 
 
 @pytest.mark.parametrize("M,K,N", [(256, 64, 64), (300, 200, 130), (64, 100, 64), (768, 8192, 3072),
-                                   (1000, 512, 700), (33, 64, 1), (255, 4096, 130)])
+                                   (1000, 512, 700), (33, 64, 1), (255, 4096, 130), (600, 1000, 200),
+                                   (513, 64, 65)])
 def test_gemm_bf16(dev, M, K, N):
     from bitsparse_amd.src import dw_gemm
     from bitsparse_amd.src.functions import dense_to_tilesparse
@@ -34,7 +35,7 @@ def test_gemm_bf16(dev, M, K, N):
     _check(C, _ref(A, h))
 
 
-@pytest.mark.parametrize("d_out", [192, 1024])   # 256-row and 512-row workgroups
+@pytest.mark.parametrize("d_out", [192, 1024, 768])   # 256-, 512- and 768-row workgroups
 def test_gemm_transposed_a_and_buffer_offset(dev, d_out):
     """AspB's call shape: A = dY.T (a transposed view), h in a shared buffer."""
     from bitsparse_amd.bitsparse import TensorBuffer
@@ -51,7 +52,7 @@ def test_gemm_transposed_a_and_buffer_offset(dev, d_out):
         _check(AspB(dY.T, sp), _ref(dY.T, h))
 
 
-@pytest.mark.parametrize("M", [320, 1024])       # 256-row and 512-row workgroups
+@pytest.mark.parametrize("M", [320, 1024, 700])  # 256-, 512- and 768-row workgroups
 @pytest.mark.parametrize("storage", ["bf16", "e4m3fn"])
 def test_gemm_relu2_square(dev, storage, M):
     from bitsparse_amd.src import dw_gemm
@@ -81,7 +82,7 @@ def test_gemm_all_zero_and_dense_operands(dev):
         _check(C, _ref(A, h))
 
 
-@pytest.mark.parametrize("K", [320, 1024])       # 256-row and 512-row workgroups
+@pytest.mark.parametrize("K", [320, 1024, 768])  # 256-, 512- and 768-row workgroups
 @pytest.mark.parametrize("storage,square", [("bf16", False), ("bf16", True), ("e4m3fn", True)])
 def test_gemm_identity_reproduces_decoded_operand(dev, storage, square, K):
     """With A = I (K = M) every output is 1.0 * b accumulated in fp32, so C
