@@ -53,8 +53,9 @@ typedef int i32x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kRun8Slots = kTileNumel / 16 + 2;   // one fp8 run + its phase, 16-byte slots
 
-template <int WGM_, int WGN_, int WM_, int WN_>
+template <int WGM_, int WGN_, int WM_, int WN_, int MINB_ = 1>
 struct Gemm8Cfg {
+    static constexpr int MINB = MINB_;                           // workgroups per CU (launch bound)
     static constexpr int WGM = WGM_, WGN = WGN_, NWAVES = WGM_ * WGN_, THREADS = 64 * NWAVES;
     static constexpr int WAVE_M = WM_, WAVE_N = WN_;
     static constexpr int IM = WAVE_M / 32, JN = WAVE_N / 32;    // 32x32 accumulator blocks per wave
@@ -93,8 +94,8 @@ using Cfg8_256 = Gemm8Cfg<2, 2, 128, 128>;
 struct Gemm8Args {
     const uint8_t* Apk;           // A codes in MFMA-fragment order (pack_a8_*_kernel)
     int64_t M, K;
-    uint32_t nkb;                 // 64-wide k blocks per 32-row block of Apk
-    uint32_t nrb;                 // 32-row blocks of Apk
+    uint32_t nkb;                 // 64-wide k blocks of Apk
+    uint32_t nrb;                 // 32-row blocks of Apk (per k block)
     const uint8_t* vals;          // compressed B
     int64_t vals_numel;
     const uint8_t* bitmask;
@@ -113,7 +114,7 @@ struct Gemm8Args {
 
 // FMT_B: MFMA format of B (0 e4m3, 1 e5m2).
 template <typename CFG, int FMT_B>
-__global__ __launch_bounds__(CFG::THREADS, 1) void gemm_cb8_kernel(Gemm8Args a)
+__global__ __launch_bounds__(CFG::THREADS, CFG::MINB) void gemm_cb8_kernel(Gemm8Args a)
 {
     constexpr int NT = CFG::NT, DW = CFG::DW, CH = CFG::CH, BP = CFG::BP, IM = CFG::IM, JN = CFG::JN;
     constexpr int RX = (15 + kTileNumel + 15) / 16;              // 16-byte units of a run, worst case
@@ -212,20 +213,23 @@ __global__ __launch_bounds__(CFG::THREADS, 1) void gemm_cb8_kernel(Gemm8Args a)
         rr_nunits[SLOT] = ok ? nunits : 0;
         const bs_rsrc rs = make_rsrc(ok ? a.vals + e0 : a.vals, (uint32_t)bytes);
         const bool tail = ok && (int64_t)nunits * 16 > avail;   // the run's last unit crosses the end of vals
+        // Every pass is issued whatever the run's length (units past it read
+        // zeros through the resource's range check): a load skipped on some
+        // paths would make the compiler's count of loads in flight a lower
+        // bound, and the waits for A before the MFMAs would then also wait
+        // for the run and bitmask loads issued in the same iteration.
 #pragma unroll
         for (int x = 0; x < RXD; x++) {
             const int u = (x * DW + tq) * 64 + lane;
-            if ((x * DW + tq) * 64 < rr_nunits[SLOT]) {
-                uint4 v = load16(rs, (uint32_t)u * 16u);
-                if (tail && (int64_t)(u + 1) * 16 > avail && (int64_t)u * 16 < avail) {
-                    uint32_t w[4] = {0u, 0u, 0u, 0u};
-                    for (int e = 0; e < 16; e++)
-                        w[e >> 2] |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rs, (int)(u * 16 + e), 0, 0)
-                                     << (8 * (e & 3));
-                    v = uint4{w[0], w[1], w[2], w[3]};
-                }
-                rr[SLOT][x] = v;
+            uint4 v = load16(rs, (uint32_t)u * 16u);
+            if (tail && (int64_t)(u + 1) * 16 > avail && (int64_t)u * 16 < avail) {
+                uint32_t w[4] = {0u, 0u, 0u, 0u};
+                for (int e = 0; e < 16; e++)
+                    w[e >> 2] |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rs, (int)(u * 16 + e), 0, 0)
+                                 << (8 * (e & 3));
+                v = uint4{w[0], w[1], w[2], w[3]};
             }
+            rr[SLOT][x] = v;
         }
     };
     auto load_run = [&](int s, auto SL) __attribute__((always_inline)) {
@@ -323,19 +327,23 @@ __global__ __launch_bounds__(CFG::THREADS, 1) void gemm_cb8_kernel(Gemm8Args a)
     };
 
     // ---- A fragments: lane l of block i holds row 32i + l%32, k = 32(l/32)
-    // .. +31 of the step: 32 contiguous bytes of Apk at 32 l of its 2 KiB block
+    // .. +31 of the step: the 16 bytes at 16 l and at 1024 + 16 l of its
+    // 2 KiB block of Apk
     const int wm = wave % CFG::WGM, wn = wave / CFG::WGM;
     const int64_t arow0 = m0 + wm * CFG::WAVE_M;
     const uint32_t rb0 = (uint32_t)(arow0 / 32);
-    const uint32_t nrbw = rb0 < a.nrb ? min((uint32_t)IM, a.nrb - rb0) : 0u;
-    const bs_rsrc rsA = make_rsrc(nrbw ? a.Apk + (int64_t)rb0 * a.nkb * 2048 : a.Apk, nrbw * a.nkb * 2048u);
+    // Apk holds at most 2^31 bytes (host check): an offset of 2^31 or more
+    // reads zeros, for row blocks past M
+    const bs_rsrc rsA = make_rsrc(a.Apk, a.nrb * a.nkb * 2048u);
     i32x8_t areg[2][IM];
     auto load_a = [&](int s, auto SI) __attribute__((always_inline)) {
         constexpr int SET = decltype(SI)::value;
 #pragma unroll
         for (int i = 0; i < IM; i++) {
-            const uint32_t off = ((uint32_t)i * a.nkb + kt0 + (uint32_t)s) * 2048u + (uint32_t)lane * 32u;
-            const uint4 lo = load16(rsA, off), hi = load16(rsA, off + 16u);
+            const uint32_t rb = rb0 + (uint32_t)i;
+            const uint32_t off = rb < a.nrb ? ((kt0 + (uint32_t)s) * a.nrb + rb) * 2048u + (uint32_t)lane * 16u
+                                            : 0x80000000u;
+            const uint4 lo = load16(rsA, off), hi = load16(rsA, off + 1024u);
             areg[SET][i] = i32x8_t{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
         }
     };
@@ -399,8 +407,9 @@ __global__ __launch_bounds__(CFG::THREADS, 1) void gemm_cb8_kernel(Gemm8Args a)
     // Pipeline.  Step j: run(j) staged in run_s[j % 3] through register slot
     // j & 1, bitmask rows in bmq[j & 1], A(j) in areg[j & 1], B(j) decoded
     // into B_s[j & 1].  Iteration s builds the row table of step s+1, then
-    // issues (in this order, so that waiting for a run never waits for A) the
-    // rows and run of step s+3 and A(s+1); multiplies step s while decoding
+    // issues (in this order: loads complete in order, and A is needed an
+    // iteration before the run) A(s+1) and the rows and run of step s+3;
+    // multiplies step s while decoding
     // B(s+1) from run_s[(s+1) % 3]; stages run(s+2), loaded an iteration ago,
     // into run_s[(s+2) % 3] (freed by the decode of step s-1) and meets the
     // other waves at the barrier.  Runs thus get two iterations to arrive, A
@@ -434,9 +443,9 @@ __global__ __launch_bounds__(CFG::THREADS, 1) void gemm_cb8_kernel(Gemm8Args a)
         run_geom(s1, e0a, pha, nua);
         run_geom(s3, e0b, phb, nub);
         decode_rows_at(pha, bmq[P ^ 1]);
+        load_a(s1, IC<P ^ 1>{});
         bmq[P ^ 1] = load_bm(s3);
         load_run_at(e0b, nub, IC<P ^ 1>{});
-        load_a(s1, IC<P ^ 1>{});
         step(s, RI);
         store_run((s + 2) % 3, IC<P>{});
         __syncthreads();
@@ -505,18 +514,22 @@ __global__ __launch_bounds__(CFG::THREADS, 1) void gemm_cb8_kernel(Gemm8Args a)
     }
 }
 
-// A codes -> Apk8: block (rb * nkb + kb) of 2 KiB holds, at 32 l, A[32 rb +
-// l%32][64 kb + 32 (l/32) .. +31]; zero past M and K.
-__device__ __forceinline__ int64_t apk8_index(int64_t m, int64_t k, uint32_t nkb)
+// A codes -> Apk8: block (kb * nrb + rb) of 2 KiB holds the 32 fragment
+// bytes of lane l -- A[32 rb + l%32][64 kb + 32 (l/32) .. +31] -- as two
+// 16-byte halves, at 16 l (bytes 0..15) and 1024 + 16 l (16..31), so that
+// each of a wave's two 16-byte loads reads 1 KiB of whole cache lines; zero
+// past M and K.  k-block major: the A rows a workgroup reads in one step
+// are one contiguous range (spread over all L2 channels).
+__device__ __forceinline__ int64_t apk8_index(int64_t m, int64_t k, uint32_t nrb)
 {
     const int64_t rb = m >> 5, kb = k >> 6;
     const int l = (int)(m & 31) + 32 * (int)((k >> 5) & 1);
-    return (rb * nkb + kb) * 2048 + l * 32 + (k & 31);
+    return (kb * nrb + rb) * 2048 + ((k >> 4) & 1) * 1024 + l * 16 + (k & 15);
 }
 
 // from At [K, M] (row stride ldat, m contiguous): 64 x 64 blocks through LDS
 __global__ __launch_bounds__(256) void pack_a8_t_kernel(const uint8_t* At, int64_t K, int64_t M, int64_t ldat,
-                                                        uint8_t* Apk, uint32_t nkb)
+                                                        uint8_t* Apk, uint32_t nrb)
 {
     __shared__ __align__(16) uint8_t t[64][64 + 16];
     const int tid = threadIdx.x;
@@ -545,20 +558,20 @@ __global__ __launch_bounds__(256) void pack_a8_t_kernel(const uint8_t* At, int64
             uint32_t w[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
             for (int e = 0; e < 16; e++) w[e >> 2] |= (uint32_t)t[kc + e][mm] << (8 * (e & 3));
-            *reinterpret_cast<uint4*>(Apk + apk8_index(m0 + mm, k0 + kc, nkb)) = uint4{w[0], w[1], w[2], w[3]};
+            *reinterpret_cast<uint4*>(Apk + apk8_index(m0 + mm, k0 + kc, nrb)) = uint4{w[0], w[1], w[2], w[3]};
         }
     }
 }
 
 // from A [M, K] (row stride lda, k contiguous): one 16-byte piece per thread
 __global__ __launch_bounds__(256) void pack_a8_n_kernel(const uint8_t* A, int64_t K, int64_t M, int64_t lda,
-                                                        uint8_t* Apk, uint32_t nkb, int64_t pieces)
+                                                        uint8_t* Apk, uint32_t nrb, int64_t pieces)
 {
     const int64_t stride = (int64_t)gridDim.x * 256;
     for (int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x; p < pieces; p += stride) {
         const int64_t blk = p >> 7;                    // 128 pieces per 2 KiB block
-        const int l = (int)((p >> 1) & 63), h = (int)(p & 1);
-        const int64_t rb = blk / nkb, kb = blk % nkb;
+        const int l = (int)(p & 63), h = (int)((p >> 6) & 1);   // half h of lane l's fragment
+        const int64_t rb = blk % nrb, kb = blk / nrb;
         const int64_t m = rb * 32 + (l & 31), k = kb * 64 + 32 * (l >> 5) + 16 * h;
         uint4 v = {0u, 0u, 0u, 0u};
         if (m < M && k < K) {
@@ -773,15 +786,16 @@ __global__ __launch_bounds__(256) void zero_fill_u16_8_kernel(uint16_t* C, int64
     for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) C[i] = 0;
 }
 
-static int gemm8_split(int64_t M, int64_t N, int64_t K, int64_t bm, int64_t bn)
+static int gemm8_split(int64_t M, int64_t N, int64_t K, int64_t bm, int64_t bn, int per_cu)
 {
+    const int64_t slots = (int64_t)kCus * per_cu;
     const int64_t tiles = ((N + bn - 1) / bn) * ((M + bm - 1) / bm);
     const int64_t ksteps = (K + kBK - 1) / kBK;
     const int64_t min_split = (ksteps + kMaxSteps - 1) / kMaxSteps;
     int64_t best = min_split, best_cost = -1;
     for (int64_t s = min_split; s <= 64; s++) {
         if (s > min_split && ksteps / s < 8) break;
-        const int64_t rounds = (tiles * s + kCus - 1) / kCus;
+        const int64_t rounds = (tiles * s + slots - 1) / slots;
         const int64_t cost = rounds * ((ksteps + s - 1) / s) + (s > 1 ? 2 : 0);
         if (best_cost < 0 || cost < best_cost) {
             best = s;
@@ -791,20 +805,34 @@ static int gemm8_split(int64_t M, int64_t N, int64_t K, int64_t bm, int64_t bn)
     return (int)best;
 }
 
+enum { CFG8_512 = 0, CFG8_256 = 1 };
 struct Gemm8Plan {
-    bool big;
+    int cfg;
     int64_t bm, bn;
     int split;
 };
+template <typename CFG>
+static void gemm8_shape(Gemm8Plan& p, int64_t M, int64_t N, int64_t K)
+{
+    p.bm = CFG::BM;
+    p.bn = CFG::BN;
+    p.split = gemm8_split(M, N, K, p.bm, p.bn, CFG::MINB);
+}
 static Gemm8Plan gemm8_plan(int64_t M, int64_t N, int64_t K)
 {
     Gemm8Plan p;
     const int64_t pad512 = (M + Cfg8_512::BM - 1) / Cfg8_512::BM * Cfg8_512::BM;
     const int64_t pad256 = (M + Cfg8_256::BM - 1) / Cfg8_256::BM * Cfg8_256::BM;
-    p.big = M >= Cfg8_512::BM && pad512 <= pad256;
-    p.bm = p.big ? Cfg8_512::BM : Cfg8_256::BM;
-    p.bn = p.big ? Cfg8_512::BN : Cfg8_256::BN;
-    p.split = gemm8_split(M, N, K, p.bm, p.bn);
+    p.cfg = M >= Cfg8_512::BM && pad512 <= pad256 ? CFG8_512 : CFG8_256;
+    // BITSPARSE_DW8_CFG selects a shape for tuning runs: 512 (8 waves of
+    // 64 x 128) or 256 (2 x 2 waves of 128 x 128)
+    if (const char* ev = getenv("BITSPARSE_DW8_CFG")) {
+        const int v = atoi(ev);
+        if (v == 512) p.cfg = CFG8_512;
+        else if (v == 256) p.cfg = CFG8_256;
+    }
+    if (p.cfg == CFG8_512) gemm8_shape<Cfg8_512>(p, M, N, K);
+    else gemm8_shape<Cfg8_256>(p, M, N, K);
     return p;
 }
 
@@ -881,6 +909,8 @@ extern "C" int bs_gemm_compressed_b_fp8(const void* A, const float* a_scale, int
     const int64_t nkb = apk8_nkb(K), nrb = (M + 31) / 32;
     // A fragment offsets (row block < 4 of a wave, k block, lane) are 32-bit
     if (nkb >= (1ll << 18)) return set_error(BS_ERR_INVALID, "%s: K must be < 2^24", fn);
+    if (apk8_bytes(M, K) > (1ll << 31))
+        return set_error(BS_ERR_INVALID, "%s: M*K must be < 2^31 (A's fragment-order copy)", fn);
     const int64_t grid_n = (N + kTile - 1) / kTile;
     const int64_t T = (int64_t)ksteps * grid_n;
 
@@ -916,13 +946,13 @@ extern "C" int bs_gemm_compressed_b_fp8(const void* A, const float* a_scale, int
     uint8_t* apk = (uint8_t*)workspace + part_bytes;
     if (a_layout == 0) {
         hipLaunchKernelGGL(pack_a8_t_kernel, dim3((uint32_t)nkb, (uint32_t)((M + 63) / 64)), dim3(256), 0, st,
-                           (const uint8_t*)A, K, M, lda, apk, (uint32_t)nkb);
+                           (const uint8_t*)A, K, M, lda, apk, (uint32_t)nrb);
     } else {
         const int64_t pieces = nrb * nkb * 128;
         int64_t nblk = (pieces + 255) / 256;
         if (nblk > 4096) nblk = 4096;
         hipLaunchKernelGGL(pack_a8_n_kernel, dim3((uint32_t)nblk), dim3(256), 0, st, (const uint8_t*)A, K, M, lda,
-                           apk, (uint32_t)nkb, pieces);
+                           apk, (uint32_t)nrb, pieces);
     }
     Gemm8Args g{};
     g.Apk = apk;
@@ -949,19 +979,18 @@ extern "C" int bs_gemm_compressed_b_fp8(const void* A, const float* a_scale, int
     if (g.ksteps_per_split > (uint32_t)kMaxSteps) return set_error(BS_ERR_INVALID, "%s: internal split error", fn);
     const uint64_t blocks = (uint64_t)g.tiles_m * g.tiles_n * (uint64_t)split;
     if (blocks >= (1ull << 31)) return set_error(BS_ERR_INVALID, "%s: grid too large", fn);
-#define BS_GEMM8_LAUNCH(FMT)                                                                                      \
-    do {                                                                                                          \
-        if (plan.big)                                                                                             \
-            hipLaunchKernelGGL((gemm_cb8_kernel<Cfg8_512, FMT>), dim3((uint32_t)blocks), dim3(Cfg8_512::THREADS), \
-                               0, st, g);                                                                         \
-        else                                                                                                      \
-            hipLaunchKernelGGL((gemm_cb8_kernel<Cfg8_256, FMT>), dim3((uint32_t)blocks), dim3(Cfg8_256::THREADS), \
-                               0, st, g);                                                                         \
+#define BS_GEMM8_GO(CFG, FMT) \
+    hipLaunchKernelGGL((gemm_cb8_kernel<CFG, FMT>), dim3((uint32_t)blocks), dim3(CFG::THREADS), 0, st, g)
+#define BS_GEMM8_LAUNCH(FMT)                                     \
+    do {                                                         \
+        if (plan.cfg == CFG8_512) BS_GEMM8_GO(Cfg8_512, FMT);   \
+        else BS_GEMM8_GO(Cfg8_256, FMT);                         \
     } while (0)
     // square: the mapped codes are e4m3fn (to_fp8's); else the stored format
     if (square || vals_dtype == DT_E4M3FN) BS_GEMM8_LAUNCH(0);
     else BS_GEMM8_LAUNCH(1);
 #undef BS_GEMM8_LAUNCH
+#undef BS_GEMM8_GO
     hipError_t e = hipGetLastError();
     if (e == hipSuccess && split > 1) {
         const int64_t n = M * N;
