@@ -307,9 +307,10 @@ __global__ __launch_bounds__(CFG::THREADS, CFG::MINB) void gemm_cb_kernel(GemmAr
             const uint32_t x3 = (uint32_t)__builtin_amdgcn_readlane((int)pq[c][3], l);
             p[c] = w == 0 ? x0 : w == 1 ? x1 : w == 2 ? x2 : x3;
         }
+        // wave-uniform: 32-bit tests (a 64-bit compare is a vector
+        // instruction on this target and takes a VGPR temporary)
+        const uint32_t cnt = p[1] >= p[0] ? min(p[1] - p[0], (uint32_t)kTileNumel) : 0u;
         const int64_t run0 = vo + (int64_t)p[0];
-        int64_t cnt = (int64_t)p[1] - (int64_t)p[0];
-        cnt = cnt < 0 ? 0 : (cnt > kTileNumel ? kTileNumel : cnt);
         phase = (int)(run0 & (GV - 1));
         e0 = run0 - phase;
         nunits = cnt == 0 ? 0 : (phase + (int)cnt + GV - 1) / GV;
@@ -319,12 +320,12 @@ __global__ __launch_bounds__(CFG::THREADS, CFG::MINB) void gemm_cb_kernel(GemmAr
     // iteration before they are written to LDS
     Unit rr[RXP];
     int rr_nunits = 0;
-    int64_t rr_avail = 0;
+    uint32_t rr_avail = 0;
     bool rr_tail = false;
     bs_rsrc rr_rs;
     auto unit_at = [&](int u) __attribute__((always_inline)) -> Unit {
         Unit v = load_unit<UB>(rr_rs, (uint32_t)u * UB);
-        if (rr_tail && (int64_t)(u + 1) * GV > rr_avail && (int64_t)u * GV < rr_avail)
+        if (rr_tail && (uint32_t)(u + 1) * GV > rr_avail && (uint32_t)u * GV < rr_avail)
             v = load_unit_tail<UB, VB>(rr_rs, (uint32_t)u * UB);
         return v;
     };
@@ -333,16 +334,21 @@ __global__ __launch_bounds__(CFG::THREADS, CFG::MINB) void gemm_cb_kernel(GemmAr
         int phase, nunits;
         run_geom(s, e0, phase, nunits);
         const int64_t avail = a.vals_numel - e0;       // elements readable from e0
-        const bool ok = e0 >= 0 && avail > 0 && nunits > 0;
-        int64_t bytes = ok ? avail * VB : 0;
-        if (bytes > (int64_t)nunits * UB) bytes = (int64_t)nunits * UB;
+        // 64-bit tests by sign and high bits, which stay scalar instructions;
+        // avail32 = avail clamped to 2^24 (a run holds at most 4096 elements)
+        const bool ok = ((uint64_t)e0 >> 63) == 0 && ((uint64_t)(avail - 1) >> 63) == 0 && nunits > 0;
+        const uint32_t avail32 = ((uint64_t)avail >> 24) != 0 ? (1u << 24) : (uint32_t)avail;
+        const uint32_t bytes = ok ? min(avail32 * (uint32_t)VB, (uint32_t)nunits * (uint32_t)UB) : 0u;
         rr_nunits = ok ? nunits : 0;
-        rr_avail = avail;
-        rr_rs = make_rsrc(ok ? a.vals + e0 * VB : a.vals, (uint32_t)bytes);
-        rr_tail = ok && (int64_t)nunits * GV > avail;   // the run's last unit crosses the end of vals
+        rr_avail = avail32;
+        rr_rs = make_rsrc(ok ? a.vals + e0 * VB : a.vals, bytes);
+        rr_tail = ok && (uint32_t)nunits * GV > avail32;   // the run's last unit crosses the end of vals
+        // the prefetched passes are issued whatever the run's length (units
+        // past it read zeros through the resource's range check): a load
+        // skipped on some paths makes the compiler's count of loads in flight
+        // a lower bound, and the waits for A would then cover these loads too
 #pragma unroll
-        for (int x = 0; x < RXP; x++)
-            if ((x * DW + tq) * 64 < rr_nunits) rr[x] = unit_at((x * DW + tq) * 64 + lane);
+        for (int x = 0; x < RXP; x++) rr[x] = unit_at((x * DW + tq) * 64 + lane);
     };
     auto store_run = [&](int buf) __attribute__((always_inline)) {
         uint8_t* dst = reinterpret_cast<uint8_t*>(run_s + (buf * NT + tw) * kRunSlots);

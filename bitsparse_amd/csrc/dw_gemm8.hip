@@ -191,9 +191,10 @@ __global__ __launch_bounds__(CFG::THREADS, CFG::MINB) void gemm_cb8_kernel(Gemm8
     auto run_geom = [&](int s, int64_t& e0, int& phase, int& nunits) __attribute__((always_inline)) {
         const uint2 pv = pf_s[tw * kMaxSteps + s];
         const uint32_t p[2] = {uniform_u32(pv.x), uniform_u32(pv.y)};
+        // wave-uniform: 32-bit tests (a 64-bit compare is a vector
+        // instruction on this target and takes a VGPR temporary)
+        const uint32_t cnt = p[1] >= p[0] ? min(p[1] - p[0], (uint32_t)kTileNumel) : 0u;
         const int64_t run0 = vo + (int64_t)p[0];
-        int64_t cnt = (int64_t)p[1] - (int64_t)p[0];
-        cnt = cnt < 0 ? 0 : (cnt > kTileNumel ? kTileNumel : cnt);
         phase = (int)(run0 & 15);
         e0 = run0 - phase;
         nunits = cnt == 0 ? 0 : (phase + (int)cnt + 15) / 16;
@@ -207,12 +208,14 @@ __global__ __launch_bounds__(CFG::THREADS, CFG::MINB) void gemm_cb8_kernel(Gemm8
     auto load_run_at = [&](int64_t e0, int nunits, auto SL) __attribute__((always_inline)) {
         constexpr int SLOT = decltype(SL)::value;
         const int64_t avail = a.vals_numel - e0;       // bytes readable from e0
-        const bool ok = e0 >= 0 && avail > 0 && nunits > 0;
-        int64_t bytes = ok ? avail : 0;
-        if (bytes > (int64_t)nunits * 16) bytes = (int64_t)nunits * 16;
+        // 64-bit tests by sign and high bits, which stay scalar instructions;
+        // avail32 = avail clamped to 2^24 (a run holds at most 4096 bytes)
+        const bool ok = ((uint64_t)e0 >> 63) == 0 && ((uint64_t)(avail - 1) >> 63) == 0 && nunits > 0;
+        const uint32_t avail32 = ((uint64_t)avail >> 24) != 0 ? (1u << 24) : (uint32_t)avail;
+        const uint32_t bytes = ok ? min(avail32, (uint32_t)nunits * 16u) : 0u;
         rr_nunits[SLOT] = ok ? nunits : 0;
-        const bs_rsrc rs = make_rsrc(ok ? a.vals + e0 : a.vals, (uint32_t)bytes);
-        const bool tail = ok && (int64_t)nunits * 16 > avail;   // the run's last unit crosses the end of vals
+        const bs_rsrc rs = make_rsrc(ok ? a.vals + e0 : a.vals, bytes);
+        const bool tail = ok && (uint32_t)nunits * 16u > avail32;   // the run's last unit crosses the end of vals
         // Every pass is issued whatever the run's length (units past it read
         // zeros through the resource's range check): a load skipped on some
         // paths would make the compiler's count of loads in flight a lower
@@ -222,7 +225,7 @@ __global__ __launch_bounds__(CFG::THREADS, CFG::MINB) void gemm_cb8_kernel(Gemm8
         for (int x = 0; x < RXD; x++) {
             const int u = (x * DW + tq) * 64 + lane;
             uint4 v = load16(rs, (uint32_t)u * 16u);
-            if (tail && (int64_t)(u + 1) * 16 > avail && (int64_t)u * 16 < avail) {
+            if (tail && (uint32_t)(u + 1) * 16u > avail32 && (uint32_t)u * 16u < avail32) {
                 uint32_t w[4] = {0u, 0u, 0u, 0u};
                 for (int e = 0; e < 16; e++)
                     w[e >> 2] |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rs, (int)(u * 16 + e), 0, 0)
