@@ -17,7 +17,7 @@ LIB_NAME = "libbitsparse_hip.so"
 # BITSPARSE_HIP_LIB points at another build of the same sources (tuning sweeps)
 LIB_PATH = os.environ.get("BITSPARSE_HIP_LIB") or os.path.join(
     os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 BS_OK = 0
 BS_ERR_INVALID = 1
@@ -65,6 +65,10 @@ _SIGNATURES = {
     "bs_gemm_compressed_b_fp8_workspace_bytes": [_i64, _i64, _i64, _int, _int],
     "bs_gemm_compressed_b_fp8": [_vp, _vp, _i64, _i64, _i64, _int, _vp, _int, _i64, _vp, _vp, _vp, _i64, _int,
                                  _f32, _vp, _vp, _vp, _vp, _i64, _vp],
+    "bs_gemm_compressed_b_packed": [_vp, _i64, _i64, _i64, _int, _vp, _int, _i64, _vp, _vp, _vp, _i64, _int,
+                                    _f32, _vp, _vp, _vp, _i64, _vp],
+    "bs_gemm_compressed_b_fp8_packed": [_vp, _vp, _i64, _i64, _i64, _int, _vp, _int, _i64, _vp, _vp, _vp, _i64,
+                                        _int, _f32, _vp, _vp, _vp, _vp, _i64, _vp],
     "bs_pack_bits": [_vp, _int, _vp, _i64, _vp, _i64, _vp, _vp, _vp],
     "bs_decompress_packed": [_vp, _int, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _int,
                              _f32, _vp, _vp],

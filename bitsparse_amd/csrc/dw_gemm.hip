@@ -191,25 +191,69 @@ __device__ __forceinline__ RunUnit<UB> load_unit_tail(bs_rsrc rs, uint32_t off)
     else return w[0];
 }
 
-template <typename CFG, int V_T, bool SQUARE, bool HAS_SCALE>
+// A staging unit of a packed value run: the NWD dwords that hold its PB
+// bytes (8 values of PB bits), read from the dword boundary at or below them.
+template <int NWD>
+struct PkUnit {
+    uint32_t w[NWD];
+};
+
+template <int NWD>
+__device__ __forceinline__ PkUnit<NWD> load_pk(bs_rsrc rs, uint32_t off)
+{
+    PkUnit<NWD> v;
+    if constexpr (NWD == 5) {
+        const uint4 x = load16(rs, off);
+        v.w[0] = x.x, v.w[1] = x.y, v.w[2] = x.z, v.w[3] = x.w;
+        v.w[4] = load4(rs, off + 16u);
+    } else {
+        static_assert(NWD == 3, "packed unit of 15 or 7 bytes");
+        const uint2 x = load8(rs, off);
+        v.w[0] = x.x, v.w[1] = x.y;
+        v.w[2] = load4(rs, off + 8u);
+    }
+    return v;
+}
+
+// The unit's dwords one byte at a time (bytes past the resource read 0): the
+// unit whose dwords reach the stream's last, partial dword.
+template <int NWD>
+__device__ __forceinline__ PkUnit<NWD> load_pk_tail(bs_rsrc rs, uint32_t off)
+{
+    PkUnit<NWD> v;
+#pragma unroll
+    for (int i = 0; i < NWD; i++) v.w[i] = 0u;
+#pragma unroll
+    for (int e = 0; e < 4 * NWD; e++)
+        v.w[e >> 2] |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rs, (int)(off + (uint32_t)e), 0, 0)
+                       << (8 * (e & 3));
+    return v;
+}
+
+// PK: the values come from a packed stream (pack_sbit storage): value i at
+// stream bits [i PB, (i+1) PB), PB = 15 (bf16) / 7 (fp8), sign bit 0.
+template <typename CFG, int V_T, bool SQUARE, bool HAS_SCALE, bool PK = false>
 __global__ __launch_bounds__(CFG::THREADS, CFG::MINB) void gemm_cb_kernel(GemmArgs a)
 {
     constexpr int NT = CFG::NT, DW = CFG::DW, CH = CFG::CH, BP = CFG::BP, IM = CFG::IM, JN = CFG::JN;
     constexpr int VB = V_T == DT_BF16 ? 2 : 1;                   // stored value bytes
-    constexpr int GV = SQUARE ? 4 : 8;                           // values per staging unit
-    constexpr int UB = GV * VB;                                  // stored bytes per unit
+    constexpr int PB = V_T == DT_BF16 ? 15 : 7;                  // PK: stream bits per value
+    // values per staging unit: a packed unit of 8 values is PB whole bytes
+    constexpr int GV = (SQUARE && !PK) ? 4 : 8;
+    constexpr int UB = GV * VB;                                  // stored bytes per unit (raw runs)
+    constexpr int NWD = PB == 15 ? 5 : 3;                        // PK: dwords read per unit
     constexpr int RX = ((GV - 1 + kTileNumel + GV - 1) / GV + 63) / 64;   // units per lane, worst case
     // units per lane loaded one step ahead (<= 20 registers: 2560 plain bf16
     // values, 1536 bf16 / 1024 fp8 values to square); a denser tile's
     // remaining units are loaded when the run is staged
     // (two workgroups per CU: 2 units, the 50% zeros tile of a plain run,
     // to stay within 256 registers)
-    constexpr int RXP0 = CFG::MINB > 1 ? 2 : (UB == 16 ? 5 : (UB == 8 ? 6 : 4));
+    constexpr int RXP0 = CFG::MINB > 1 ? 2 : (PK ? (NWD == 5 ? 4 : 6) : (UB == 16 ? 5 : (UB == 8 ? 6 : 4)));
     // the DW waves decoding one tile stage its run together: unit u is staged
     // by lane u % 64 of wave (u / 64) % DW, in pass u / (64 DW)
     constexpr int RXD = (RX + DW - 1) / DW;                      // passes per wave, worst case
     constexpr int RXP = RXP0 < RXD ? RXP0 : RXD;
-    typedef RunUnit<UB> Unit;
+    typedef typename std::conditional<PK, PkUnit<NWD>, RunUnit<UB>>::type Unit;
 
     __shared__ __align__(16) uint8_t lds[CFG::LDS];
     uint16_t* B_s = reinterpret_cast<uint16_t*>(lds + CFG::OFF_B);
@@ -323,16 +367,47 @@ __global__ __launch_bounds__(CFG::THREADS, CFG::MINB) void gemm_cb_kernel(GemmAr
     uint32_t rr_avail = 0;
     bool rr_tail = false;
     bs_rsrc rr_rs;
+    uint32_t rr_b0 = 0;                                // PK: byte of the run's first unit in its dword
     auto unit_at = [&](int u) __attribute__((always_inline)) -> Unit {
-        Unit v = load_unit<UB>(rr_rs, (uint32_t)u * UB);
-        if (rr_tail && (uint32_t)(u + 1) * GV > rr_avail && (uint32_t)u * GV < rr_avail)
-            v = load_unit_tail<UB, VB>(rr_rs, (uint32_t)u * UB);
-        return v;
+        if constexpr (PK) {
+            // unit u: bytes [rr_b0 + u PB, +PB) of the resource, read as the
+            // NWD dwords from the dword boundary at or below them
+            const uint32_t o4 = (rr_b0 + (uint32_t)u * PB) & ~3u;
+            Unit v = load_pk<NWD>(rr_rs, o4);
+            if (rr_tail && o4 + 4u * NWD > rr_avail) v = load_pk_tail<NWD>(rr_rs, o4);
+            return v;
+        } else {
+            Unit v = load_unit<UB>(rr_rs, (uint32_t)u * UB);
+            if (rr_tail && (uint32_t)(u + 1) * GV > rr_avail && (uint32_t)u * GV < rr_avail)
+                v = load_unit_tail<UB, VB>(rr_rs, (uint32_t)u * UB);
+            return v;
+        }
     };
     auto load_run = [&](int s) __attribute__((always_inline)) {
         int64_t e0;
         int phase, nunits;
         run_geom(s, e0, phase, nunits);
+        if constexpr (PK) {
+            // unit j = e0/8 + u is stream bytes [j PB, (j+1) PB); the resource
+            // starts at the dword holding byte e0/8 PB and reaches the end of
+            // the last unit's dwords, so that every unit's loads lie wholly
+            // inside it -- unless the stream ends first: the units that reach
+            // its last, partial dword are then read byte by byte
+            const int64_t byte0 = (e0 >> 3) * PB;
+            const int64_t base = byte0 & ~(int64_t)3;
+            const int64_t avail = a.vals_numel - base;  // stream bytes readable from base
+            const bool ok = ((uint64_t)e0 >> 63) == 0 && ((uint64_t)(avail - 1) >> 63) == 0 && nunits > 0;
+            const uint32_t avail32 = ((uint64_t)avail >> 24) != 0 ? (1u << 24) : (uint32_t)avail;
+            rr_b0 = (uint32_t)(byte0 & 3);
+            const uint32_t wend = ((rr_b0 + (uint32_t)(nunits - 1) * PB) & ~3u) + 4u * NWD;
+            rr_nunits = ok ? nunits : 0;
+            rr_avail = avail32 & ~3u;                   // whole dwords readable
+            rr_rs = make_rsrc(ok ? a.vals + base : a.vals, ok ? min(avail32, wend) : 0u);
+            rr_tail = ok && avail32 < wend;
+#pragma unroll
+            for (int x = 0; x < RXP; x++) rr[x] = unit_at((x * DW + tq) * 64 + lane);
+            return;
+        }
         const int64_t avail = a.vals_numel - e0;       // elements readable from e0
         // 64-bit tests by sign and high bits, which stay scalar instructions;
         // avail32 = avail clamped to 2^24 (a run holds at most 4096 elements)
@@ -358,7 +433,27 @@ __global__ __launch_bounds__(CFG::THREADS, CFG::MINB) void gemm_cb_kernel(GemmAr
                 const int u = (x * DW + tq) * 64 + lane;
                 if (x >= RXP) rr[x % RXP] = unit_at(u);
                 if (u < rr_nunits) {
-                    if constexpr (!SQUARE) {
+                    if constexpr (PK) {
+                        // the unit's PB bytes from byte sh of its first dword,
+                        // then value e at bits [PB e, PB e + PB): bf16 bits
+                        // (sign 0), through the transform when SQUARE
+                        const Unit ux = rr[x % RXP];
+                        const uint32_t sh = (rr_b0 + (uint32_t)u * PB) & 3u;
+                        uint32_t q[NWD - 1];
+#pragma unroll
+                        for (int i = 0; i < NWD - 1; i++) q[i] = __builtin_amdgcn_alignbyte(ux.w[i + 1], ux.w[i], sh);
+                        uint32_t y[8];
+#pragma unroll
+                        for (int e = 0; e < 8; e++) {
+                            const int bit = PB * e, wi = bit >> 5, bs = bit & 31;
+                            uint32_t raw = bs + PB <= 32 ? q[wi] >> bs
+                                                         : __builtin_amdgcn_alignbit(q[min(wi + 1, NWD - 2)], q[wi], bs);
+                            raw &= (1u << PB) - 1u;
+                            y[e] = b_elem<V_T, SQUARE, HAS_SCALE>(raw, kr, s2b);
+                        }
+                        *reinterpret_cast<uint4*>(dst + u * 16) =
+                            uint4{y[0] | (y[1] << 16), y[2] | (y[3] << 16), y[4] | (y[5] << 16), y[6] | (y[7] << 16)};
+                    } else if constexpr (!SQUARE) {
                         *reinterpret_cast<uint4*>(dst + u * 16) = rr[x % RXP];
                     } else {
                         uint32_t y[4];
@@ -831,14 +926,16 @@ struct GemmPlan {
     int64_t bm, bn;
     int split;
 };
-static GemmPlan gemm_plan(int64_t M, int64_t N, int64_t K)
+// packed: the two default shapes only (the tuning override is not applied)
+static GemmPlan gemm_plan(int64_t M, int64_t N, int64_t K, bool packed = false)
 {
     GemmPlan p;
     const int64_t pad512 = (M + Cfg512::BM - 1) / Cfg512::BM * Cfg512::BM;
     const int64_t pad256 = (M + Cfg256::BM - 1) / Cfg256::BM * Cfg256::BM;
     if (M >= Cfg512::BM && pad512 <= pad256) p.cfg = CFG_512;
     else p.cfg = CFG_256V;
-    if (const char* ev = getenv("BITSPARSE_DW_CFG")) {
+    const char* ev = packed ? nullptr : getenv("BITSPARSE_DW_CFG");
+    if (ev) {
         const int v = atoi(ev);
         if (v == 256) p.cfg = CFG_256;
         else if (v == 512) p.cfg = CFG_512;
@@ -866,38 +963,39 @@ using namespace bs;
 extern "C" int64_t bs_gemm_compressed_b_workspace_bytes(int64_t M, int64_t N, int64_t K, int a_layout)
 {
     if (M <= 0 || N <= 0 || K <= 0) return 0;
-    const int split = gemm_plan(M, N, K).split;
+    // enough for either entry point (the packed one ignores a tuning override)
+    const int split = std::max(gemm_plan(M, N, K).split, gemm_plan(M, N, K, true).split);
     int64_t bytes = split > 1 ? align_up256((int64_t)split * M * N * 4) : 0;
     (void)a_layout;
     bytes += apk_bytes(M, K);
     return bytes;
 }
 
-extern "C" int bs_gemm_compressed_b(const void* A, int64_t M, int64_t K, int64_t lda, int a_layout,
-                                    const void* vals, int vals_dtype, int64_t vals_numel,
-                                    const uint8_t* bitmask, const uint32_t* prefix, const int64_t* vals_offset,
-                                    int64_t N, int square, float relu2_scale, const float* b_scale, void* C,
-                                    void* workspace, int64_t workspace_bytes, void* stream)
+// packed: vals is a packed value stream of vals_numel bytes (4-byte aligned)
+static int gemm_cb_impl(const void* A, int64_t M, int64_t K, int64_t lda, int a_layout, const void* vals,
+                        int vals_dtype, int64_t vals_numel, const uint8_t* bitmask, const uint32_t* prefix,
+                        const int64_t* vals_offset, int64_t N, int square, float relu2_scale, const float* b_scale,
+                        void* C, void* workspace, int64_t workspace_bytes, void* stream, bool packed, const char* fn)
 {
     clear_error();
-    if (M < 0 || N < 0 || K < 0) return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: negative shape");
-    if (a_layout != 0 && a_layout != 1) return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: bad a_layout");
-    if (vals_dtype < 0 || vals_dtype > 2) return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: bad dtype");
+    if (M < 0 || N < 0 || K < 0) return set_error(BS_ERR_INVALID, "%s: negative shape", fn);
+    if (a_layout != 0 && a_layout != 1) return set_error(BS_ERR_INVALID, "%s: bad a_layout", fn);
+    if (vals_dtype < 0 || vals_dtype > 2) return set_error(BS_ERR_INVALID, "%s: bad dtype", fn);
     if (!square && vals_dtype != DT_BF16)
-        return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: fp8 storage needs square=1");
+        return set_error(BS_ERR_INVALID, "%s: fp8 storage needs square=1", fn);
     if (b_scale != nullptr && !square)
-        return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: b_scale is only applied with square=1");
-    if (a_layout == 0 && lda < M) return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: lda < M");
-    if (a_layout == 1 && lda < K) return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: lda < K");
+        return set_error(BS_ERR_INVALID, "%s: b_scale is only applied with square=1", fn);
+    if (a_layout == 0 && lda < M) return set_error(BS_ERR_INVALID, "%s: lda < M", fn);
+    if (a_layout == 1 && lda < K) return set_error(BS_ERR_INVALID, "%s: lda < K", fn);
     if (a_layout == 1 && K % 8 != 0)
-        return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: a_layout 1 needs K %% 8 == 0");
+        return set_error(BS_ERR_INVALID, "%s: a_layout 1 needs K %% 8 == 0", fn);
     // bf16 storage without the square runs past 2^31 elements on the GPU
-    const bool big_ok = vals_dtype == DT_BF16 && !square;
+    const bool big_ok = !packed && vals_dtype == DT_BF16 && !square;
     if ((uint64_t)K * (uint64_t)N >= (big_ok ? kMaxElems : kMaxElemsUntested))
-        return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: K*N must be < 2^%d on this path", big_ok ? 32 : 31);
+        return set_error(BS_ERR_INVALID, "%s: K*N must be < 2^%d on this path", fn, big_ok ? 32 : 31);
     if (M == 0 || N == 0) return BS_OK;
-    if (C == nullptr) return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: null C");
-    if (((uintptr_t)C) & 1) return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: C misaligned");
+    if (C == nullptr) return set_error(BS_ERR_INVALID, "%s: null C", fn);
+    if (((uintptr_t)C) & 1) return set_error(BS_ERR_INVALID, "%s: C misaligned", fn);
     hipStream_t st = (hipStream_t)stream;
     const uint32_t ksteps = (uint32_t)((K + kBK - 1) / kBK);
     if (ksteps == 0) {
@@ -907,25 +1005,28 @@ extern "C" int bs_gemm_compressed_b(const void* A, int64_t M, int64_t K, int64_t
         const uint32_t nblk = (uint32_t)std::min<int64_t>((n + 255) / 256, 2048);
         hipLaunchKernelGGL(zero_fill_u16_kernel, dim3(nblk), dim3(256), 0, st, (uint16_t*)C, n);
         hipError_t e = hipGetLastError();
-        return e == hipSuccess ? BS_OK : set_error(BS_ERR_HIP, "bs_gemm_compressed_b: %s", hipGetErrorString(e));
+        return e == hipSuccess ? BS_OK : set_error(BS_ERR_HIP, "%s: %s", fn, hipGetErrorString(e));
     }
     if (A == nullptr || bitmask == nullptr || prefix == nullptr || (vals_numel > 0 && vals == nullptr))
-        return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: null pointer");
+        return set_error(BS_ERR_INVALID, "%s: null pointer", fn);
     if ((((uintptr_t)A) & 15) || (lda % 8) != 0)
-        return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: A must be 16-byte aligned with lda %% 8 == 0");
-    if (lda >= (1ll << 24)) return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: lda must be < 2^24");
-    if (((uintptr_t)vals) & 15) return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: vals must be 16-byte aligned");
-    const GemmPlan plan = gemm_plan(M, N, K);
+        return set_error(BS_ERR_INVALID, "%s: A must be 16-byte aligned with lda %% 8 == 0", fn);
+    if (lda >= (1ll << 24)) return set_error(BS_ERR_INVALID, "%s: lda must be < 2^24", fn);
+    if (((uintptr_t)vals) & (packed ? 3 : 15))
+        return set_error(BS_ERR_INVALID, "%s: vals must be %d-byte aligned", fn, packed ? 4 : 16);
+    if (packed && vals_dtype != DT_BF16)
+        return set_error(BS_ERR_INVALID, "%s: packed fp8 values go to bs_gemm_compressed_b_fp8_packed", fn);
+    const GemmPlan plan = gemm_plan(M, N, K, packed);
     const int split = plan.split;
     const int64_t part_bytes = split > 1 ? align_up256((int64_t)split * M * N * 4) : 0;
     const int64_t nkb = apk_nkb(K), nrb = (M + 31) / 32;
-    if (nkb >= (1ll << 20)) return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: K too large");
+    if (nkb >= (1ll << 20)) return set_error(BS_ERR_INVALID, "%s: K too large", fn);
     const int64_t need = part_bytes + apk_bytes(M, K);
     {
         if (workspace == nullptr || workspace_bytes < need)
-            return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: workspace too small (%lld < %lld)",
+            return set_error(BS_ERR_INVALID, "%s: workspace too small (%lld < %lld)", fn,
                              (long long)workspace_bytes, (long long)need);
-        if (((uintptr_t)workspace) & 15) return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: workspace misaligned");
+        if (((uintptr_t)workspace) & 15) return set_error(BS_ERR_INVALID, "%s: workspace misaligned", fn);
     }
     GemmArgs g{};
     g.M = M;
@@ -947,9 +1048,9 @@ extern "C" int bs_gemm_compressed_b(const void* A, int64_t M, int64_t K, int64_t
     g.ksteps = ksteps;
     g.ksteps_per_split = (ksteps + split - 1) / split;
     if (g.ksteps_per_split > (uint32_t)kMaxSteps)
-        return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: internal split error");
+        return set_error(BS_ERR_INVALID, "%s: internal split error", fn);
     const uint64_t blocks = (uint64_t)g.tiles_m * g.tiles_n * (uint64_t)split;
-    if (blocks >= (1ull << 31)) return set_error(BS_ERR_INVALID, "bs_gemm_compressed_b: grid too large");
+    if (blocks >= (1ull << 31)) return set_error(BS_ERR_INVALID, "%s: grid too large", fn);
     // A into MFMA-fragment order (workspace after the partial sums)
     uint16_t* apk = (uint16_t*)((uint8_t*)workspace + part_bytes);
     if (a_layout == 0) {
@@ -983,8 +1084,21 @@ extern "C" int bs_gemm_compressed_b(const void* A, int64_t M, int64_t K, int64_t
             hipLaunchKernelGGL((gemm_cb_kernel<Cfg256, VT, SQ, SC>), dim3((uint32_t)blocks), dim3(Cfg256::THREADS), \
                                0, st, g);                                                                       \
     } while (0)
+#define BS_GEMM_LAUNCH_PK(SQ, SC)                                                                        \
+    do {                                                                                                 \
+        if (plan.cfg == CFG_512)                                                                         \
+            hipLaunchKernelGGL((gemm_cb_kernel<Cfg512, DT_BF16, SQ, SC, true>), dim3((uint32_t)blocks),   \
+                               dim3(Cfg512::THREADS), 0, st, g);                                         \
+        else                                                                                             \
+            hipLaunchKernelGGL((gemm_cb_kernel<Cfg256v, DT_BF16, SQ, SC, true>), dim3((uint32_t)blocks),  \
+                               dim3(Cfg256v::THREADS), 0, st, g);                                        \
+    } while (0)
     const bool sc = b_scale != nullptr;
-    switch (vals_dtype) {
+    if (packed) {
+        if (!square) BS_GEMM_LAUNCH_PK(false, false);
+        else if (!sc) BS_GEMM_LAUNCH_PK(true, false);
+        else BS_GEMM_LAUNCH_PK(true, true);
+    } else switch (vals_dtype) {
     case DT_BF16:
         if (!square) BS_GEMM_LAUNCH(DT_BF16, false, false);
         else if (!sc) BS_GEMM_LAUNCH(DT_BF16, true, false);
@@ -1000,6 +1114,7 @@ extern "C" int bs_gemm_compressed_b(const void* A, int64_t M, int64_t K, int64_t
         break;
     }
 #undef BS_GEMM_LAUNCH
+#undef BS_GEMM_LAUNCH_PK
     hipError_t e = hipGetLastError();
     if (e == hipSuccess && split > 1) {
         const int64_t n = M * N;
@@ -1010,6 +1125,29 @@ extern "C" int bs_gemm_compressed_b(const void* A, int64_t M, int64_t K, int64_t
                            (const float*)workspace, split, n, (uint16_t*)C);
         e = hipGetLastError();
     }
-    if (e != hipSuccess) return set_error(BS_ERR_HIP, "bs_gemm_compressed_b launch: %s", hipGetErrorString(e));
+    if (e != hipSuccess) return set_error(BS_ERR_HIP, "%s launch: %s", fn, hipGetErrorString(e));
     return BS_OK;
+}
+
+extern "C" int bs_gemm_compressed_b(const void* A, int64_t M, int64_t K, int64_t lda, int a_layout,
+                                    const void* vals, int vals_dtype, int64_t vals_numel,
+                                    const uint8_t* bitmask, const uint32_t* prefix, const int64_t* vals_offset,
+                                    int64_t N, int square, float relu2_scale, const float* b_scale, void* C,
+                                    void* workspace, int64_t workspace_bytes, void* stream)
+{
+    return gemm_cb_impl(A, M, K, lda, a_layout, vals, vals_dtype, vals_numel, bitmask, prefix, vals_offset, N,
+                        square, relu2_scale, b_scale, C, workspace, workspace_bytes, stream, false,
+                        "bs_gemm_compressed_b");
+}
+
+extern "C" int bs_gemm_compressed_b_packed(const void* A, int64_t M, int64_t K, int64_t lda, int a_layout,
+                                           const void* stream_bytes, int vals_dtype, int64_t stream_nbytes,
+                                           const uint8_t* bitmask, const uint32_t* prefix,
+                                           const int64_t* vals_offset, int64_t N, int square, float relu2_scale,
+                                           const float* b_scale, void* C, void* workspace,
+                                           int64_t workspace_bytes, void* stream)
+{
+    return gemm_cb_impl(A, M, K, lda, a_layout, stream_bytes, vals_dtype, stream_nbytes, bitmask, prefix,
+                        vals_offset, N, square, relu2_scale, b_scale, C, workspace, workspace_bytes, stream, true,
+                        "bs_gemm_compressed_b_packed");
 }

@@ -761,6 +761,117 @@ __global__ __launch_bounds__(256) void map_codes_kernel(Lut8Args a, uint8_t* out
     }
 }
 
+// ---------------------------------------------------------------------------
+// packed fp8 storage (pack_sbit): value i of the stream at bits [7 i, 7 i + 7)
+// (least significant first), the code's low 7 bits (its sign bit is 0).  The
+// GEMM stages unpacked codes, so the stream is unpacked by the pass that maps
+// the codes (square = 1) or, for square = 0, by the same pass with the
+// identity for its table: into the workspace run the GEMM reads.
+// ---------------------------------------------------------------------------
+
+// 16 consecutive codes from stream bit `bit` (counted from the resource's
+// first byte, which is dword aligned): the five dwords from the one holding
+// `bit` -- whole-dword reads while they lie inside the `readable` bytes, else
+// byte by byte (bytes past the resource read 0) -- then code e at bits
+// [7 e, 7 e + 7) past `bit`.
+__device__ __forceinline__ uint4 packed7_x16(bs_rsrc rs, uint64_t bit, int64_t readable)
+{
+    const uint32_t o4 = (uint32_t)(bit >> 5) * 4u, sb = (uint32_t)(bit & 31u);
+    uint32_t w[5];
+    if ((int64_t)o4 + 20 <= readable) {
+        const uint4 v = load16(rs, o4);
+        w[0] = v.x, w[1] = v.y, w[2] = v.z, w[3] = v.w;
+        w[4] = load4(rs, o4 + 16u);
+    } else {
+        w[0] = w[1] = w[2] = w[3] = w[4] = 0u;
+        for (int e = 0; e < 20; e++)
+            w[e >> 2] |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rs, (int)(o4 + (uint32_t)e), 0, 0)
+                         << (8 * (e & 3));
+    }
+    uint32_t q[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) q[i] = __builtin_amdgcn_alignbit(w[i + 1], w[i], sb);
+    uint32_t o[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int e = 0; e < 16; e++) {
+        const int b = 7 * e, wi = b >> 5, bs = b & 31;
+        const uint32_t raw = bs + 7 <= 32 ? q[wi] >> bs : __builtin_amdgcn_alignbit(q[min(wi + 1, 3)], q[wi], bs);
+        o[e >> 2] |= (raw & 0x7fu) << (8 * (e & 3));
+    }
+    return uint4{o[0], o[1], o[2], o[3]};
+}
+
+// The run [vo + prefix[0], vo + prefix[T]) of a packed stream (vals_numel
+// bytes): its first value index b0, its length n (values wholly inside the
+// stream), the resource from the dword holding value b0's first bit, and that
+// bit's offset in the resource.
+struct PackedRun {
+    int64_t b0, n;
+    bs_rsrc rs;
+    int64_t readable;
+    uint64_t bit0;
+};
+__device__ __forceinline__ PackedRun packed_run(const Lut8Args& a)
+{
+    PackedRun r;
+    const int64_t vo = a.vals_offset ? *a.vals_offset : 0;
+    r.b0 = vo + (int64_t)a.prefix[0];
+    const int64_t whole = a.vals_numel * 8 / 7;         // values wholly inside the stream
+    r.n = (int64_t)a.prefix[a.T] - (int64_t)a.prefix[0];
+    if (r.b0 < 0 || r.b0 >= whole) r.n = 0;
+    else if (r.n > whole - r.b0) r.n = whole - r.b0;
+    const int64_t base = r.n > 0 ? ((r.b0 * 7) >> 5) * 4 : 0;
+    r.readable = r.n > 0 ? std::min<int64_t>(a.vals_numel - base, 0xffffffffll) : 0;
+    r.rs = make_rsrc(a.vals + base, (uint32_t)r.readable);
+    r.bit0 = r.n > 0 ? (uint64_t)(r.b0 * 7 - base * 8) : 0;
+    return r;
+}
+
+// code_max_kernel over a packed run
+__global__ __launch_bounds__(256) void code_max_packed_kernel(Lut8Args a)
+{
+    const PackedRun r = packed_run(a);
+    uint32_t m = 0;
+    const int64_t stride = (int64_t)gridDim.x * 256 * 16;
+    for (int64_t j = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 16; j < r.n; j += stride) {
+        const uint4 v = packed7_x16(r.rs, r.bit0 + (uint64_t)j * 7u, r.readable);
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int e = 0; e < 16; e++) m = max(m, j + e < r.n ? (w[e >> 2] >> (8 * (e & 3))) & 0x7fu : 0u);
+    }
+    m = wave_max_u32(m);
+    __shared__ uint32_t s_w[4];
+    if ((threadIdx.x & 63) == 0) s_w[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) a.cmax[blockIdx.x] = max(max(s_w[0], s_w[1]), max(s_w[2], s_w[3]));
+}
+
+// map_codes_kernel reading a packed run; IDENT (square = 0): out[i] = the
+// code itself, and the stored scale is copied to sB by copy_scale_kernel
+template <int V_T, bool IDENT>
+__global__ __launch_bounds__(256) void map_packed_kernel(Lut8Args a, uint8_t* out, int64_t cap, int64_t* out_vo)
+{
+    __shared__ uint8_t t[256];
+    if constexpr (!IDENT) relu2_table<V_T>(a, t, blockIdx.x == 0);
+    const PackedRun r = packed_run(a);
+    const int64_t n = std::min<int64_t>(r.n, cap);
+    if (blockIdx.x == 0 && threadIdx.x == 0) *out_vo = -(int64_t)a.prefix[0];
+    const int64_t stride = (int64_t)gridDim.x * 256 * 16;
+    for (int64_t j = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 16; j < n; j += stride) {
+        const uint4 v = packed7_x16(r.rs, r.bit0 + (uint64_t)j * 7u, r.readable);
+        uint32_t o[4] = {v.x, v.y, v.z, v.w};
+        if constexpr (!IDENT) {
+#pragma unroll
+            for (int d = 0; d < 4; d++) {
+                const uint32_t x = o[d];
+                o[d] = (uint32_t)t[x & 0xffu] | ((uint32_t)t[(x >> 8) & 0xffu] << 8) |
+                       ((uint32_t)t[(x >> 16) & 0xffu] << 16) | ((uint32_t)t[x >> 24] << 24);
+            }
+        }
+        *reinterpret_cast<uint4*>(out + j) = uint4{o[0], o[1], o[2], o[3]};
+    }
+}
+
 __global__ void copy_scale_kernel(const float* src, float* dst, float* dst2)
 {
     if (threadIdx.x == 0) {
@@ -864,14 +975,15 @@ extern "C" int64_t bs_gemm_compressed_b_fp8_workspace_bytes(int64_t M, int64_t N
     return bytes + kLutAreaBytes;
 }
 
-extern "C" int bs_gemm_compressed_b_fp8(const void* A, const float* a_scale, int64_t M, int64_t K, int64_t lda,
-                                        int a_layout, const void* vals, int vals_dtype, int64_t vals_numel,
-                                        const uint8_t* bitmask, const uint32_t* prefix, const int64_t* vals_offset,
-                                        int64_t N, int square, float relu2_scale, const float* b_scale, void* C,
-                                        float* b_scale_out, void* workspace, int64_t workspace_bytes, void* stream)
+// packed: vals is a packed stream of vals_numel bytes (7-bit codes), unpacked
+// (and for square = 1 mapped) into the workspace run the GEMM stages
+static int gemm8_impl(const void* A, const float* a_scale, int64_t M, int64_t K, int64_t lda, int a_layout,
+                      const void* vals, int vals_dtype, int64_t vals_numel, const uint8_t* bitmask,
+                      const uint32_t* prefix, const int64_t* vals_offset, int64_t N, int square, float relu2_scale,
+                      const float* b_scale, void* C, float* b_scale_out, void* workspace, int64_t workspace_bytes,
+                      void* stream, bool packed, const char* fn)
 {
     clear_error();
-    const char* fn = "bs_gemm_compressed_b_fp8";
     if (M < 0 || N < 0 || K < 0) return set_error(BS_ERR_INVALID, "%s: negative shape", fn);
     if (a_layout != 0 && a_layout != 1) return set_error(BS_ERR_INVALID, "%s: bad a_layout", fn);
     if (vals_dtype != DT_E4M3FN && vals_dtype != DT_E5M2)
@@ -885,7 +997,8 @@ extern "C" int bs_gemm_compressed_b_fp8(const void* A, const float* a_scale, int
     if (M == 0 || N == 0) return BS_OK;
     if (C == nullptr) return set_error(BS_ERR_INVALID, "%s: null C", fn);
     if (((uintptr_t)C) & 1) return set_error(BS_ERR_INVALID, "%s: C misaligned", fn);
-    const int64_t need = bs_gemm_compressed_b_fp8_workspace_bytes(M, N, K, a_layout, square);
+    // packed: the unpacked run takes the room of square = 1's mapped run
+    const int64_t need = bs_gemm_compressed_b_fp8_workspace_bytes(M, N, K, a_layout, square || packed);
     if (workspace == nullptr || workspace_bytes < need)
         return set_error(BS_ERR_INVALID, "%s: workspace too small (%lld < %lld)", fn, (long long)workspace_bytes,
                          (long long)need);
@@ -905,7 +1018,8 @@ extern "C" int bs_gemm_compressed_b_fp8(const void* A, const float* a_scale, int
     }
     if (A == nullptr || bitmask == nullptr || prefix == nullptr || (vals_numel > 0 && vals == nullptr))
         return set_error(BS_ERR_INVALID, "%s: null pointer", fn);
-    if (((uintptr_t)vals) & 15) return set_error(BS_ERR_INVALID, "%s: vals must be 16-byte aligned", fn);
+    if (((uintptr_t)vals) & (packed ? 3 : 15))
+        return set_error(BS_ERR_INVALID, "%s: vals must be %d-byte aligned", fn, packed ? 4 : 16);
     const Gemm8Plan plan = gemm8_plan(M, N, K);
     const int split = plan.split;
     const int64_t part_bytes = split > 1 ? up256((int64_t)split * M * N * 4) : 0;
@@ -930,13 +1044,27 @@ extern "C" int bs_gemm_compressed_b_fp8(const void* A, const float* a_scale, int
     la.cmax = cmax;
     la.b_scale = sB;
     la.b_scale_out = b_scale_out;
-    // square: the mapped value run after A's packed copy
+    // square / packed: the mapped (or unpacked) value run after A's packed copy
     const int64_t map_cap = map8_cap(K, N);
     uint8_t* map_out = (uint8_t*)workspace + part_bytes + up256(apk8_bytes(M, K));
     int64_t* map_vo = reinterpret_cast<int64_t*>(map_out + up256(map_cap));
-    if (square) {
+    const uint32_t mblk = (uint32_t)std::min<int64_t>((map_cap + 4095) / 4096, 2048);
+    if (packed) {
+        if (square) {
+            hipLaunchKernelGGL(code_max_packed_kernel, dim3(kCodeMaxBlocks), dim3(256), 0, st, la);
+            if (vals_dtype == DT_E4M3FN)
+                hipLaunchKernelGGL((map_packed_kernel<DT_E4M3FN, false>), dim3(mblk), dim3(256), 0, st, la, map_out,
+                                   map_cap, map_vo);
+            else
+                hipLaunchKernelGGL((map_packed_kernel<DT_E5M2, false>), dim3(mblk), dim3(256), 0, st, la, map_out,
+                                   map_cap, map_vo);
+        } else {
+            hipLaunchKernelGGL(copy_scale_kernel, dim3(1), dim3(64), 0, st, b_scale, sB, b_scale_out);
+            hipLaunchKernelGGL((map_packed_kernel<DT_E4M3FN, true>), dim3(mblk), dim3(256), 0, st, la, map_out,
+                               map_cap, map_vo);
+        }
+    } else if (square) {
         hipLaunchKernelGGL(code_max_kernel, dim3(kCodeMaxBlocks), dim3(256), 0, st, la);
-        const uint32_t mblk = (uint32_t)std::min<int64_t>((map_cap + 4095) / 4096, 2048);
         if (vals_dtype == DT_E4M3FN)
             hipLaunchKernelGGL(map_codes_kernel<DT_E4M3FN>, dim3(mblk), dim3(256), 0, st, la, map_out, map_cap, map_vo);
         else
@@ -963,11 +1091,12 @@ extern "C" int bs_gemm_compressed_b_fp8(const void* A, const float* a_scale, int
     g.K = K;
     g.nkb = (uint32_t)nkb;
     g.nrb = (uint32_t)nrb;
-    g.vals = square ? map_out : (const uint8_t*)vals;
-    g.vals_numel = square ? map_cap : vals_numel;
+    const bool mapped = square || packed;
+    g.vals = mapped ? map_out : (const uint8_t*)vals;
+    g.vals_numel = mapped ? map_cap : vals_numel;
     g.bitmask = bitmask;
     g.prefix = prefix;
-    g.vals_offset = square ? map_vo : vals_offset;
+    g.vals_offset = mapped ? map_vo : vals_offset;
     g.N = N;
     g.grid_n = (uint32_t)grid_n;
     const uint32_t nt = (uint32_t)(plan.bn / kTile);
@@ -1005,4 +1134,27 @@ extern "C" int bs_gemm_compressed_b_fp8(const void* A, const float* a_scale, int
     }
     if (e != hipSuccess) return set_error(BS_ERR_HIP, "%s launch: %s", fn, hipGetErrorString(e));
     return BS_OK;
+}
+
+extern "C" int bs_gemm_compressed_b_fp8(const void* A, const float* a_scale, int64_t M, int64_t K, int64_t lda,
+                                        int a_layout, const void* vals, int vals_dtype, int64_t vals_numel,
+                                        const uint8_t* bitmask, const uint32_t* prefix, const int64_t* vals_offset,
+                                        int64_t N, int square, float relu2_scale, const float* b_scale, void* C,
+                                        float* b_scale_out, void* workspace, int64_t workspace_bytes, void* stream)
+{
+    return gemm8_impl(A, a_scale, M, K, lda, a_layout, vals, vals_dtype, vals_numel, bitmask, prefix, vals_offset, N,
+                      square, relu2_scale, b_scale, C, b_scale_out, workspace, workspace_bytes, stream, false,
+                      "bs_gemm_compressed_b_fp8");
+}
+
+extern "C" int bs_gemm_compressed_b_fp8_packed(const void* A, const float* a_scale, int64_t M, int64_t K,
+                                               int64_t lda, int a_layout, const void* stream_bytes, int vals_dtype,
+                                               int64_t stream_nbytes, const uint8_t* bitmask, const uint32_t* prefix,
+                                               const int64_t* vals_offset, int64_t N, int square, float relu2_scale,
+                                               const float* b_scale, void* C, float* b_scale_out, void* workspace,
+                                               int64_t workspace_bytes, void* stream)
+{
+    return gemm8_impl(A, a_scale, M, K, lda, a_layout, stream_bytes, vals_dtype, stream_nbytes, bitmask, prefix,
+                      vals_offset, N, square, relu2_scale, b_scale, C, b_scale_out, workspace, workspace_bytes,
+                      stream, true, "bs_gemm_compressed_b_fp8_packed");
 }

@@ -105,7 +105,7 @@ using namespace bs;
 
 extern "C" const char* bs_last_error(void) { return bs::g_err; }
 
-extern "C" int bs_abi_version(void) { return 12; }
+extern "C" int bs_abi_version(void) { return 13; }
 
 extern "C" int64_t bs_nontemporal_min_bytes(int64_t bytes)
 {

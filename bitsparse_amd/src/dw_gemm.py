@@ -3,7 +3,9 @@
 ``gemm_compressed_b(A, B_sparse, square)`` computes ``A @ B`` (or
 ``A @ (k * B^2)``) with B a BitsparseTensor decoded tile by tile into LDS by
 the kernel; it replaces the decompress-to-HBM + GEMM of reference
-lib_sparse/src/sparse_matmul.py:24-28 / :109-113.
+lib_sparse/src/sparse_matmul.py:24-28 / :109-113.  Packed (pack_sbit) values
+go to the ``*_packed`` entry points, which read the stream itself (reference
+bitpacking.py:37-55 ahead of the same GEMMs).
 """
 from __future__ import annotations
 
@@ -15,16 +17,26 @@ from .._lib import check, ptr, stream_handle
 from ..config import RELU2_SCALE
 
 
+def _stored(B_sparse) -> torch.dtype:
+    """The stored value type (a packed stream's logical dtype)."""
+    return B_sparse.dtype if B_sparse.pack_sbit else B_sparse.vals.dtype
+
+
+def _vals_aligned(B_sparse) -> bool:
+    # raw runs are read as aligned 16-byte slots, packed streams as dwords
+    return B_sparse.vals.data_ptr() % (4 if B_sparse.pack_sbit else 16) == 0
+
+
 def supports(A: Tensor, B_sparse, square: bool) -> bool:
     """Shapes / dtypes the kernel handles: bf16 A on the GPU; B stored as
-    bf16, or fp8 when the operand is the ReLU^2 square."""
-    if not A.is_cuda or A.dim() != 2 or A.dtype != torch.bfloat16 or B_sparse.pack_sbit:
+    bf16 (raw or packed), or raw fp8 when the operand is the ReLU^2 square."""
+    if not A.is_cuda or A.dim() != 2 or A.dtype != torch.bfloat16:
         return False
-    if A.shape[1] != B_sparse.shape[0]:
+    if A.shape[1] != B_sparse.shape[0] or not _vals_aligned(B_sparse):
         return False
-    if B_sparse.vals.data_ptr() % 16 != 0:   # the kernel reads value runs as aligned 16-byte slots
-        return False
-    vdt = B_sparse.vals.dtype
+    vdt = _stored(B_sparse)
+    if B_sparse.pack_sbit:
+        return vdt == torch.bfloat16
     if vdt == torch.bfloat16:
         return True
     return square and vdt in (torch.float8_e4m3fn, torch.float8_e5m2)
@@ -32,14 +44,12 @@ def supports(A: Tensor, B_sparse, square: bool) -> bool:
 
 def supports_fp8(A: Tensor, B_sparse) -> bool:
     """The fp8-operand kernel: e4m3fn A on the GPU (2-D, any strides) and B
-    stored as raw (not pack_sbit) e4m3fn / e5m2 values."""
-    if not A.is_cuda or A.dim() != 2 or A.dtype != torch.float8_e4m3fn or B_sparse.pack_sbit:
+    stored as e4m3fn / e5m2 values, raw or packed."""
+    if not A.is_cuda or A.dim() != 2 or A.dtype != torch.float8_e4m3fn:
         return False
-    if A.shape[1] != B_sparse.shape[0]:
+    if A.shape[1] != B_sparse.shape[0] or not _vals_aligned(B_sparse):
         return False
-    if B_sparse.vals.data_ptr() % 16 != 0:
-        return False
-    return B_sparse.vals.dtype in (torch.float8_e4m3fn, torch.float8_e5m2)
+    return _stored(B_sparse) in (torch.float8_e4m3fn, torch.float8_e5m2)
 
 
 def gemm_compressed_b_fp8(A: Tensor, A_scale: Tensor, B_sparse, square: bool,
@@ -67,11 +77,14 @@ def gemm_compressed_b_fp8(A: Tensor, A_scale: Tensor, B_sparse, square: bool,
         raise ValueError("gemm_compressed_b_fp8: fp8 values without their scale")
     L = _lib.load()
     C = torch.empty((M, N), device=A.device, dtype=torch.bfloat16)
-    need = L.bs_gemm_compressed_b_fp8_workspace_bytes(M, N, K, a_layout, int(square))
+    packed = B_sparse.pack_sbit
+    # a packed stream is unpacked into the room square=1 maps its codes into
+    need = L.bs_gemm_compressed_b_fp8_workspace_bytes(M, N, K, a_layout, int(square or packed))
     ws = torch.empty(need, device=A.device, dtype=torch.uint8)
-    check(L.bs_gemm_compressed_b_fp8(
+    fn = L.bs_gemm_compressed_b_fp8_packed if packed else L.bs_gemm_compressed_b_fp8
+    check(fn(
         a_src.data_ptr(), A_scale.data_ptr(), M, K, lda, a_layout, B_sparse.vals.data_ptr(),
-        dtype_code(B_sparse.vals.dtype), B_sparse.vals.numel(), B_sparse.bitmask.data_ptr(),
+        dtype_code(_stored(B_sparse)), B_sparse.vals.numel(), B_sparse.bitmask.data_ptr(),
         B_sparse.prefix.data_ptr(), B_sparse.vals_offset.data_ptr(), N, int(square), float(RELU2_SCALE),
         ptr(stored_scale), C.data_ptr(), ptr(b_scale_out), ws.data_ptr(), need, stream_handle(A.device)),
         "bs_gemm_compressed_b_fp8")
@@ -101,8 +114,9 @@ def gemm_compressed_b(A: Tensor, B_sparse, square: bool) -> Tensor:
     need = L.bs_gemm_compressed_b_workspace_bytes(M, N, K, a_layout)
     ws = torch.empty(max(need, 0), device=A.device, dtype=torch.uint8) if need > 0 else None
     scale = B_sparse.scale if (square and B_sparse.scale is not None) else None
-    check(L.bs_gemm_compressed_b(
-        a_src.data_ptr(), M, K, lda, a_layout, B_sparse.vals.data_ptr(), dtype_code(B_sparse.vals.dtype),
+    fn = L.bs_gemm_compressed_b_packed if B_sparse.pack_sbit else L.bs_gemm_compressed_b
+    check(fn(
+        a_src.data_ptr(), M, K, lda, a_layout, B_sparse.vals.data_ptr(), dtype_code(_stored(B_sparse)),
         B_sparse.vals.numel(), B_sparse.bitmask.data_ptr(), B_sparse.prefix.data_ptr(),
         B_sparse.vals_offset.data_ptr(), N, int(square), float(RELU2_SCALE), ptr(scale),
         C.data_ptr(), ptr(ws), need, stream_handle(A.device)), "bs_gemm_compressed_b")

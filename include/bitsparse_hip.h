@@ -392,6 +392,36 @@ int bs_gemm_compressed_b_fp8(const void* A, const float* a_scale, int64_t M, int
                              float* b_scale_out, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * The two GEMMs above with B's values in a packed stream (pack_sbit storage,
+ * the format of bs_pack_bits below) of stream_nbytes bytes, 4-byte aligned;
+ * *vals_offset is a value index into the stream.  Everything else as the
+ * unpacked entry points.
+ *   bs_gemm_compressed_b_packed: bf16 values (vals_dtype 0, 15-bit fields);
+ *     each 8-value unit of a tile's run is its 15 stream bytes, widened to
+ *     bf16 (sign 0, and squared when square = 1) as the run is staged in LDS.
+ *     Workspace: bs_gemm_compressed_b_workspace_bytes.
+ *   bs_gemm_compressed_b_fp8_packed: fp8 values (vals_dtype 1 or 2, 7-bit
+ *     fields); the pass that maps the codes for square = 1 reads them from
+ *     the stream, and for square = 0 the same pass copies them unmapped, into
+ *     the workspace run the GEMM stages (the nnz codes, not a dense B).
+ *     Workspace: bs_gemm_compressed_b_fp8_workspace_bytes(M, N, K, a_layout,
+ *     1) whatever `square`.
+ * Replace the pack_sbit branch of the reference's unpack
+ * (lib_sparse/src/triton_kernels.py:186-187, load_packed_at_indices of
+ * bitpacking.py:37-55) ahead of its GEMM (sparse_matmul.py:24-28, :109-113).
+ */
+int bs_gemm_compressed_b_packed(const void* A, int64_t M, int64_t K, int64_t lda, int a_layout,
+                                const void* stream_bytes, int vals_dtype, int64_t stream_nbytes,
+                                const uint8_t* bitmask, const uint32_t* prefix, const int64_t* vals_offset,
+                                int64_t N, int square, float relu2_scale, const float* b_scale, void* C,
+                                void* workspace, int64_t workspace_bytes, void* stream);
+int bs_gemm_compressed_b_fp8_packed(const void* A, const float* a_scale, int64_t M, int64_t K, int64_t lda,
+                                    int a_layout, const void* stream_bytes, int vals_dtype, int64_t stream_nbytes,
+                                    const uint8_t* bitmask, const uint32_t* prefix, const int64_t* vals_offset,
+                                    int64_t N, int square, float relu2_scale, const float* b_scale, void* C,
+                                    float* b_scale_out, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * Packed value stream (pack_sbit storage, reference lib_sparse/src/bitpacking.py).
  * Value i of a stream occupies stream bits [i*PB, (i+1)*PB), least significant
  * bit first (byte i*PB/8 holds the low bits); PB = 15 for bf16 and 7 for fp8
