@@ -1667,7 +1667,11 @@ __global__ __launch_bounds__(kThreads) void relu2_grad_kernel(GatherArgs a)
     const int ntiles = (int)min((uint32_t)U, a.num_tiles - t0);
 
     // mask bytes first: a chunk with no bit set is written without reading
-    // its gradient (at 90% zeros 43% of the chunks); cursor and scale with them
+    // its gradient (at 90% zeros 43% of the chunks); cursor and scale with them.
+    // Memory still moves the 128-byte line of a tile row whenever any of its
+    // eight chunks is read, so the skip saves no HBM traffic below whole
+    // rows, but it keeps the unused chunks out of the CU: reading every chunk
+    // of a live row measured 55.7 against 51.7 us at the configs[3] shape.
     const int64_t vo = a.vals_offset ? *a.vals_offset : 0;
     float sc = 1.0f;
     if constexpr (HAS_SCALE) sc = *a.scale;
