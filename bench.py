@@ -341,8 +341,9 @@ def bench_gemm(steps: int, warmup: int):
     """dW = dY^T @ h with h compressed, at the two MLP configs' dW shapes, as
     the layers call it: configs[1] bf16 (bf16 reconstruct-into-LDS GEMM),
     configs[3] ReLU^2 with e4m3fn storage (fp8 reconstruct-into-LDS GEMM on
-    to_fp8(dY)), each against the decompress + library GEMM path
-    (AspB / AspRelu2B with the LDS GEMMs switched off)."""
+    to_fp8(dY)), each with raw and with packed (pack_sbit) value storage,
+    against the decompress + library GEMM path (AspB / AspRelu2B with the
+    LDS GEMMs switched off)."""
     import torch
     from bitsparse_amd.fp8 import to_fp8
     from bitsparse_amd.src import sparse_matmul
@@ -350,21 +351,23 @@ def bench_gemm(steps: int, warmup: int):
 
     dev = torch.device("cuda", 0)
     out = {}
-    cases = [("configs[1] dW2", 768, 8192, 3072, 0.0, False),
-             ("configs[3] dW2", 4096, 4096, 16384, -1.2816, True)]
-    for name, M, K, N, mu, relu2_fp8 in cases:
+    cases = [("configs[1] dW2", 768, 8192, 3072, 0.0, False, False),
+             ("configs[3] dW2", 4096, 4096, 16384, -1.2816, True, False),
+             ("configs[1] dW2, pack_sbit storage", 768, 8192, 3072, 0.0, False, True),
+             ("configs[3] dW2, pack_sbit storage", 4096, 4096, 16384, -1.2816, True, True)]
+    for name, M, K, N, mu, relu2_fp8, packed in cases:
         g = torch.Generator().manual_seed(0)
         h = (torch.randn((K, N), generator=g) + mu).to(torch.bfloat16).relu_().to(dev)
         dY = torch.randn((K, M), generator=g).to(torch.bfloat16).to(dev)
         if relu2_fp8:
-            _, _, sp = quantize_and_compress(h, None)
+            _, _, sp = quantize_and_compress(h, None, pack_sbit=packed)
             qd, sd = to_fp8(dY)
 
             def call():
                 return sparse_matmul.AspRelu2B(qd.T, sp, A_scale=sd)
             peak, dt = MFMA_FP8_PEAK_TFLOPS, "fp8 e4m3 x e4m3, fp32 accumulate"
         else:
-            sp = dense_to_tilesparse(h, None)
+            sp = dense_to_tilesparse(h, None, pack_sbit=packed)
 
             def call():
                 return sparse_matmul.AspB(dY.T, sp)
@@ -378,7 +381,8 @@ def bench_gemm(steps: int, warmup: int):
         flop = 2.0 * M * N * K
         tf = flop / (t_lds * 1e9)
         out[name] = {"M": M, "K": K, "N": N, "dtype": dt,
-                     "operand": "relu^2 (e4m3fn storage)" if relu2_fp8 else "relu (bf16 storage)",
+                     "operand": ("relu^2 (e4m3fn storage)" if relu2_fp8 else "relu (bf16 storage)") +
+                                (", 7/15-bit packed stream" if packed else ""),
                      "sparsity": round(1 - int(sp.prefix[-1].item()) / (K * N), 4),
                      "lds_gemm_ms": round(t_lds, 4), "lds_gemm_tflops": round(tf, 1),
                      "mfma_frac_of_peak": round(tf / peak, 4), "mfma_peak_tflops": peak,

@@ -65,6 +65,7 @@ _SIGNATURES = {
     "bs_gemm_compressed_b_fp8_workspace_bytes": [_i64, _i64, _i64, _int, _int],
     "bs_gemm_compressed_b_fp8": [_vp, _vp, _i64, _i64, _i64, _int, _vp, _int, _i64, _vp, _vp, _vp, _i64, _int,
                                  _f32, _vp, _vp, _vp, _vp, _i64, _vp],
+    "bs_gemm_compressed_b_packed_workspace_bytes": [_i64, _i64, _i64, _int],
     "bs_gemm_compressed_b_packed": [_vp, _i64, _i64, _i64, _int, _vp, _int, _i64, _vp, _vp, _vp, _i64, _int,
                                     _f32, _vp, _vp, _vp, _i64, _vp],
     "bs_gemm_compressed_b_fp8_packed": [_vp, _vp, _i64, _i64, _i64, _int, _vp, _int, _i64, _vp, _vp, _vp, _i64,
@@ -88,6 +89,7 @@ _RESTYPES = {
     "bs_compress_workspace_bytes": _i64,
     "bs_gemm_compressed_b_workspace_bytes": _i64,
     "bs_gemm_compressed_b_fp8_workspace_bytes": _i64,
+    "bs_gemm_compressed_b_packed_workspace_bytes": _i64,
     "bs_compress_noalloc_max_tiles": _i64,
     "bs_linear_relu_compress_max_n": _i64,
     "bs_nontemporal_min_bytes": _i64,

@@ -191,69 +191,25 @@ __device__ __forceinline__ RunUnit<UB> load_unit_tail(bs_rsrc rs, uint32_t off)
     else return w[0];
 }
 
-// A staging unit of a packed value run: the NWD dwords that hold its PB
-// bytes (8 values of PB bits), read from the dword boundary at or below them.
-template <int NWD>
-struct PkUnit {
-    uint32_t w[NWD];
-};
-
-template <int NWD>
-__device__ __forceinline__ PkUnit<NWD> load_pk(bs_rsrc rs, uint32_t off)
-{
-    PkUnit<NWD> v;
-    if constexpr (NWD == 5) {
-        const uint4 x = load16(rs, off);
-        v.w[0] = x.x, v.w[1] = x.y, v.w[2] = x.z, v.w[3] = x.w;
-        v.w[4] = load4(rs, off + 16u);
-    } else {
-        static_assert(NWD == 3, "packed unit of 15 or 7 bytes");
-        const uint2 x = load8(rs, off);
-        v.w[0] = x.x, v.w[1] = x.y;
-        v.w[2] = load4(rs, off + 8u);
-    }
-    return v;
-}
-
-// The unit's dwords one byte at a time (bytes past the resource read 0): the
-// unit whose dwords reach the stream's last, partial dword.
-template <int NWD>
-__device__ __forceinline__ PkUnit<NWD> load_pk_tail(bs_rsrc rs, uint32_t off)
-{
-    PkUnit<NWD> v;
-#pragma unroll
-    for (int i = 0; i < NWD; i++) v.w[i] = 0u;
-#pragma unroll
-    for (int e = 0; e < 4 * NWD; e++)
-        v.w[e >> 2] |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rs, (int)(off + (uint32_t)e), 0, 0)
-                       << (8 * (e & 3));
-    return v;
-}
-
-// PK: the values come from a packed stream (pack_sbit storage): value i at
-// stream bits [i PB, (i+1) PB), PB = 15 (bf16) / 7 (fp8), sign bit 0.
-template <typename CFG, int V_T, bool SQUARE, bool HAS_SCALE, bool PK = false>
+template <typename CFG, int V_T, bool SQUARE, bool HAS_SCALE>
 __global__ __launch_bounds__(CFG::THREADS, CFG::MINB) void gemm_cb_kernel(GemmArgs a)
 {
     constexpr int NT = CFG::NT, DW = CFG::DW, CH = CFG::CH, BP = CFG::BP, IM = CFG::IM, JN = CFG::JN;
     constexpr int VB = V_T == DT_BF16 ? 2 : 1;                   // stored value bytes
-    constexpr int PB = V_T == DT_BF16 ? 15 : 7;                  // PK: stream bits per value
-    // values per staging unit: a packed unit of 8 values is PB whole bytes
-    constexpr int GV = (SQUARE && !PK) ? 4 : 8;
-    constexpr int UB = GV * VB;                                  // stored bytes per unit (raw runs)
-    constexpr int NWD = PB == 15 ? 5 : 3;                        // PK: dwords read per unit
+    constexpr int GV = SQUARE ? 4 : 8;                           // values per staging unit
+    constexpr int UB = GV * VB;                                  // stored bytes per unit
     constexpr int RX = ((GV - 1 + kTileNumel + GV - 1) / GV + 63) / 64;   // units per lane, worst case
     // units per lane loaded one step ahead (<= 20 registers: 2560 plain bf16
     // values, 1536 bf16 / 1024 fp8 values to square); a denser tile's
     // remaining units are loaded when the run is staged
     // (two workgroups per CU: 2 units, the 50% zeros tile of a plain run,
     // to stay within 256 registers)
-    constexpr int RXP0 = CFG::MINB > 1 ? 2 : (PK ? (NWD == 5 ? 4 : 6) : (UB == 16 ? 5 : (UB == 8 ? 6 : 4)));
+    constexpr int RXP0 = CFG::MINB > 1 ? 2 : (UB == 16 ? 5 : (UB == 8 ? 6 : 4));
     // the DW waves decoding one tile stage its run together: unit u is staged
     // by lane u % 64 of wave (u / 64) % DW, in pass u / (64 DW)
     constexpr int RXD = (RX + DW - 1) / DW;                      // passes per wave, worst case
     constexpr int RXP = RXP0 < RXD ? RXP0 : RXD;
-    typedef typename std::conditional<PK, PkUnit<NWD>, RunUnit<UB>>::type Unit;
+    typedef RunUnit<UB> Unit;
 
     __shared__ __align__(16) uint8_t lds[CFG::LDS];
     uint16_t* B_s = reinterpret_cast<uint16_t*>(lds + CFG::OFF_B);
@@ -367,47 +323,16 @@ __global__ __launch_bounds__(CFG::THREADS, CFG::MINB) void gemm_cb_kernel(GemmAr
     uint32_t rr_avail = 0;
     bool rr_tail = false;
     bs_rsrc rr_rs;
-    uint32_t rr_b0 = 0;                                // PK: byte of the run's first unit in its dword
     auto unit_at = [&](int u) __attribute__((always_inline)) -> Unit {
-        if constexpr (PK) {
-            // unit u: bytes [rr_b0 + u PB, +PB) of the resource, read as the
-            // NWD dwords from the dword boundary at or below them
-            const uint32_t o4 = (rr_b0 + (uint32_t)u * PB) & ~3u;
-            Unit v = load_pk<NWD>(rr_rs, o4);
-            if (rr_tail && o4 + 4u * NWD > rr_avail) v = load_pk_tail<NWD>(rr_rs, o4);
-            return v;
-        } else {
-            Unit v = load_unit<UB>(rr_rs, (uint32_t)u * UB);
-            if (rr_tail && (uint32_t)(u + 1) * GV > rr_avail && (uint32_t)u * GV < rr_avail)
-                v = load_unit_tail<UB, VB>(rr_rs, (uint32_t)u * UB);
-            return v;
-        }
+        Unit v = load_unit<UB>(rr_rs, (uint32_t)u * UB);
+        if (rr_tail && (uint32_t)(u + 1) * GV > rr_avail && (uint32_t)u * GV < rr_avail)
+            v = load_unit_tail<UB, VB>(rr_rs, (uint32_t)u * UB);
+        return v;
     };
     auto load_run = [&](int s) __attribute__((always_inline)) {
         int64_t e0;
         int phase, nunits;
         run_geom(s, e0, phase, nunits);
-        if constexpr (PK) {
-            // unit j = e0/8 + u is stream bytes [j PB, (j+1) PB); the resource
-            // starts at the dword holding byte e0/8 PB and reaches the end of
-            // the last unit's dwords, so that every unit's loads lie wholly
-            // inside it -- unless the stream ends first: the units that reach
-            // its last, partial dword are then read byte by byte
-            const int64_t byte0 = (e0 >> 3) * PB;
-            const int64_t base = byte0 & ~(int64_t)3;
-            const int64_t avail = a.vals_numel - base;  // stream bytes readable from base
-            const bool ok = ((uint64_t)e0 >> 63) == 0 && ((uint64_t)(avail - 1) >> 63) == 0 && nunits > 0;
-            const uint32_t avail32 = ((uint64_t)avail >> 24) != 0 ? (1u << 24) : (uint32_t)avail;
-            rr_b0 = (uint32_t)(byte0 & 3);
-            const uint32_t wend = ((rr_b0 + (uint32_t)(nunits - 1) * PB) & ~3u) + 4u * NWD;
-            rr_nunits = ok ? nunits : 0;
-            rr_avail = avail32 & ~3u;                   // whole dwords readable
-            rr_rs = make_rsrc(ok ? a.vals + base : a.vals, ok ? min(avail32, wend) : 0u);
-            rr_tail = ok && avail32 < wend;
-#pragma unroll
-            for (int x = 0; x < RXP; x++) rr[x] = unit_at((x * DW + tq) * 64 + lane);
-            return;
-        }
         const int64_t avail = a.vals_numel - e0;       // elements readable from e0
         // 64-bit tests by sign and high bits, which stay scalar instructions;
         // avail32 = avail clamped to 2^24 (a run holds at most 4096 elements)
@@ -433,27 +358,7 @@ __global__ __launch_bounds__(CFG::THREADS, CFG::MINB) void gemm_cb_kernel(GemmAr
                 const int u = (x * DW + tq) * 64 + lane;
                 if (x >= RXP) rr[x % RXP] = unit_at(u);
                 if (u < rr_nunits) {
-                    if constexpr (PK) {
-                        // the unit's PB bytes from byte sh of its first dword,
-                        // then value e at bits [PB e, PB e + PB): bf16 bits
-                        // (sign 0), through the transform when SQUARE
-                        const Unit ux = rr[x % RXP];
-                        const uint32_t sh = (rr_b0 + (uint32_t)u * PB) & 3u;
-                        uint32_t q[NWD - 1];
-#pragma unroll
-                        for (int i = 0; i < NWD - 1; i++) q[i] = __builtin_amdgcn_alignbyte(ux.w[i + 1], ux.w[i], sh);
-                        uint32_t y[8];
-#pragma unroll
-                        for (int e = 0; e < 8; e++) {
-                            const int bit = PB * e, wi = bit >> 5, bs = bit & 31;
-                            uint32_t raw = bs + PB <= 32 ? q[wi] >> bs
-                                                         : __builtin_amdgcn_alignbit(q[min(wi + 1, NWD - 2)], q[wi], bs);
-                            raw &= (1u << PB) - 1u;
-                            y[e] = b_elem<V_T, SQUARE, HAS_SCALE>(raw, kr, s2b);
-                        }
-                        *reinterpret_cast<uint4*>(dst + u * 16) =
-                            uint4{y[0] | (y[1] << 16), y[2] | (y[3] << 16), y[4] | (y[5] << 16), y[6] | (y[7] << 16)};
-                    } else if constexpr (!SQUARE) {
+                    if constexpr (!SQUARE) {
                         *reinterpret_cast<uint4*>(dst + u * 16) = rr[x % RXP];
                     } else {
                         uint32_t y[4];
@@ -880,6 +785,67 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* part, i
     }
 }
 
+// Packed bf16 storage (pack_sbit): value i of the stream at bits [15 i,
+// 15 i + 15), least significant first, the value's low 15 bits (sign 0).
+// The run [vo + prefix[0], vo + prefix[T]) is unpacked into out[0, n) as bf16
+// (n = the run's length, within the stream's whole values and cap; cap a
+// multiple of 8, so the 16-byte stores stay inside out), and *out_vo =
+// -prefix[0]: the GEMM then stages tile t's run from out[prefix[t] + *out_vo]
+// as it would stored bf16 values.  8 values per thread and pass: the five
+// dwords from the one holding the group's first bit (whole-dword reads while
+// inside the stream, else byte by byte), funnel-shifted to that bit.
+__global__ __launch_bounds__(256) void unpack15_kernel(const uint8_t* stream, int64_t nbytes, const uint32_t* prefix,
+                                                       int64_t T, const int64_t* vals_offset, uint16_t* out,
+                                                       int64_t cap, int64_t* out_vo)
+{
+    const int64_t vo = vals_offset ? *vals_offset : 0;
+    const int64_t p0 = (int64_t)prefix[0];
+    const int64_t b0 = vo + p0;
+    const int64_t whole = nbytes * 8 / 15;               // values wholly inside the stream
+    int64_t n = (int64_t)prefix[T] - p0;
+    if (b0 < 0 || b0 >= whole) n = 0;
+    else if (n > whole - b0) n = whole - b0;
+    if (n > cap) n = cap;
+    if (blockIdx.x == 0 && threadIdx.x == 0) *out_vo = -p0;
+    if (n <= 0) return;
+    const int64_t base = ((b0 * 15) >> 5) * 4;           // the dword holding the run's first bit
+    const int64_t readable = std::min<int64_t>(nbytes - base, 0xffffffffll);
+    const bs_rsrc rs = make_rsrc(stream + base, (uint32_t)readable);
+    const uint64_t bit0 = (uint64_t)(b0 * 15 - base * 8);
+    const int64_t stride = (int64_t)gridDim.x * 256 * 8;
+    for (int64_t j = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8; j < n; j += stride) {
+        const uint64_t bit = bit0 + (uint64_t)j * 15u;
+        const uint32_t o4 = (uint32_t)(bit >> 5) * 4u, sb = (uint32_t)(bit & 31u);
+        uint32_t w[5];
+        if ((int64_t)o4 + 20 <= readable) {
+            const uint4 v = load16(rs, o4);
+            w[0] = v.x, w[1] = v.y, w[2] = v.z, w[3] = v.w;
+            w[4] = load4(rs, o4 + 16u);
+        } else {
+            w[0] = w[1] = w[2] = w[3] = w[4] = 0u;
+            for (int e = 0; e < 20; e++)
+                w[e >> 2] |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rs, (int)(o4 + (uint32_t)e), 0, 0)
+                             << (8 * (e & 3));
+        }
+        uint32_t q[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) q[i] = __builtin_amdgcn_alignbit(w[i + 1], w[i], sb);
+        uint32_t o[4];
+#pragma unroll
+        for (int d = 0; d < 4; d++) {
+            uint32_t v2[2];
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const int b = 15 * (2 * d + h), wi = b >> 5, bs = b & 31;
+                const uint32_t raw = bs + 15 <= 32 ? q[wi] >> bs : __builtin_amdgcn_alignbit(q[min(wi + 1, 3)], q[wi], bs);
+                v2[h] = raw & 0x7fffu;
+            }
+            o[d] = v2[0] | (v2[1] << 16);
+        }
+        *reinterpret_cast<uint4*>(out + j) = uint4{o[0], o[1], o[2], o[3]};
+    }
+}
+
 // C[0, n) = 0 (bf16 bits), grid-stride
 __global__ __launch_bounds__(256) void zero_fill_u16_kernel(uint16_t* C, int64_t n)
 {
@@ -926,16 +892,14 @@ struct GemmPlan {
     int64_t bm, bn;
     int split;
 };
-// packed: the two default shapes only (the tuning override is not applied)
-static GemmPlan gemm_plan(int64_t M, int64_t N, int64_t K, bool packed = false)
+static GemmPlan gemm_plan(int64_t M, int64_t N, int64_t K)
 {
     GemmPlan p;
     const int64_t pad512 = (M + Cfg512::BM - 1) / Cfg512::BM * Cfg512::BM;
     const int64_t pad256 = (M + Cfg256::BM - 1) / Cfg256::BM * Cfg256::BM;
     if (M >= Cfg512::BM && pad512 <= pad256) p.cfg = CFG_512;
     else p.cfg = CFG_256V;
-    const char* ev = packed ? nullptr : getenv("BITSPARSE_DW_CFG");
-    if (ev) {
+    if (const char* ev = getenv("BITSPARSE_DW_CFG")) {
         const int v = atoi(ev);
         if (v == 256) p.cfg = CFG_256;
         else if (v == 512) p.cfg = CFG_512;
@@ -960,11 +924,21 @@ static int64_t align_up256(int64_t x) { return (x + 255) / 256 * 256; }
 
 using namespace bs;
 
+// packed: the unpacked bf16 value run (room for K N values, whole 16-byte
+// units) and its offset word follow A's packed copy
+static int64_t unpack_run_cap(int64_t K, int64_t N) { return (K * N + 7) / 8 * 8; }
+
+extern "C" int64_t bs_gemm_compressed_b_packed_workspace_bytes(int64_t M, int64_t N, int64_t K, int a_layout)
+{
+    const int64_t base = bs_gemm_compressed_b_workspace_bytes(M, N, K, a_layout);
+    if (M <= 0 || N <= 0 || K <= 0) return base;
+    return align_up256(base) + align_up256(unpack_run_cap(K, N) * 2) + 256;
+}
+
 extern "C" int64_t bs_gemm_compressed_b_workspace_bytes(int64_t M, int64_t N, int64_t K, int a_layout)
 {
     if (M <= 0 || N <= 0 || K <= 0) return 0;
-    // enough for either entry point (the packed one ignores a tuning override)
-    const int split = std::max(gemm_plan(M, N, K).split, gemm_plan(M, N, K, true).split);
+    const int split = gemm_plan(M, N, K).split;
     int64_t bytes = split > 1 ? align_up256((int64_t)split * M * N * 4) : 0;
     (void)a_layout;
     bytes += apk_bytes(M, K);
@@ -1016,12 +990,13 @@ static int gemm_cb_impl(const void* A, int64_t M, int64_t K, int64_t lda, int a_
         return set_error(BS_ERR_INVALID, "%s: vals must be %d-byte aligned", fn, packed ? 4 : 16);
     if (packed && vals_dtype != DT_BF16)
         return set_error(BS_ERR_INVALID, "%s: packed fp8 values go to bs_gemm_compressed_b_fp8_packed", fn);
-    const GemmPlan plan = gemm_plan(M, N, K, packed);
+    const GemmPlan plan = gemm_plan(M, N, K);
     const int split = plan.split;
     const int64_t part_bytes = split > 1 ? align_up256((int64_t)split * M * N * 4) : 0;
     const int64_t nkb = apk_nkb(K), nrb = (M + 31) / 32;
     if (nkb >= (1ll << 20)) return set_error(BS_ERR_INVALID, "%s: K too large", fn);
-    const int64_t need = part_bytes + apk_bytes(M, K);
+    const int64_t need = packed ? bs_gemm_compressed_b_packed_workspace_bytes(M, N, K, a_layout)
+                                : part_bytes + apk_bytes(M, K);
     {
         if (workspace == nullptr || workspace_bytes < need)
             return set_error(BS_ERR_INVALID, "%s: workspace too small (%lld < %lld)", fn,
@@ -1066,6 +1041,20 @@ static int gemm_cb_impl(const void* A, int64_t M, int64_t K, int64_t lda, int a_
     g.Apk = apk;
     g.nkb = (uint32_t)nkb;
     g.nrb = (uint32_t)nrb;
+    if (packed) {
+        // the stream's run unpacked to bf16 after A's packed copy; the GEMM
+        // stages it as stored values
+        const int64_t cap = unpack_run_cap(K, N);
+        uint16_t* run = reinterpret_cast<uint16_t*>((uint8_t*)workspace + align_up256(part_bytes + apk_bytes(M, K)));
+        int64_t* run_vo = reinterpret_cast<int64_t*>((uint8_t*)run + align_up256(cap * 2));
+        const int64_t T = (int64_t)ksteps * g.grid_n;
+        const uint32_t ublk = (uint32_t)std::min<int64_t>((cap + 2047) / 2048, 2048);
+        hipLaunchKernelGGL(unpack15_kernel, dim3(ublk), dim3(256), 0, st, (const uint8_t*)vals, vals_numel, prefix, T,
+                           vals_offset, run, cap, run_vo);
+        g.vals = reinterpret_cast<const uint8_t*>(run);
+        g.vals_numel = cap;
+        g.vals_offset = run_vo;
+    }
 #define BS_GEMM_LAUNCH(VT, SQ, SC)                                                                              \
     do {                                                                                                        \
         if (plan.cfg == CFG_768)                                                                                \
@@ -1084,21 +1073,8 @@ static int gemm_cb_impl(const void* A, int64_t M, int64_t K, int64_t lda, int a_
             hipLaunchKernelGGL((gemm_cb_kernel<Cfg256, VT, SQ, SC>), dim3((uint32_t)blocks), dim3(Cfg256::THREADS), \
                                0, st, g);                                                                       \
     } while (0)
-#define BS_GEMM_LAUNCH_PK(SQ, SC)                                                                        \
-    do {                                                                                                 \
-        if (plan.cfg == CFG_512)                                                                         \
-            hipLaunchKernelGGL((gemm_cb_kernel<Cfg512, DT_BF16, SQ, SC, true>), dim3((uint32_t)blocks),   \
-                               dim3(Cfg512::THREADS), 0, st, g);                                         \
-        else                                                                                             \
-            hipLaunchKernelGGL((gemm_cb_kernel<Cfg256v, DT_BF16, SQ, SC, true>), dim3((uint32_t)blocks),  \
-                               dim3(Cfg256v::THREADS), 0, st, g);                                        \
-    } while (0)
     const bool sc = b_scale != nullptr;
-    if (packed) {
-        if (!square) BS_GEMM_LAUNCH_PK(false, false);
-        else if (!sc) BS_GEMM_LAUNCH_PK(true, false);
-        else BS_GEMM_LAUNCH_PK(true, true);
-    } else switch (vals_dtype) {
+    switch (vals_dtype) {
     case DT_BF16:
         if (!square) BS_GEMM_LAUNCH(DT_BF16, false, false);
         else if (!sc) BS_GEMM_LAUNCH(DT_BF16, true, false);
@@ -1114,7 +1090,6 @@ static int gemm_cb_impl(const void* A, int64_t M, int64_t K, int64_t lda, int a_
         break;
     }
 #undef BS_GEMM_LAUNCH
-#undef BS_GEMM_LAUNCH_PK
     hipError_t e = hipGetLastError();
     if (e == hipSuccess && split > 1) {
         const int64_t n = M * N;

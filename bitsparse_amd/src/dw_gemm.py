@@ -4,7 +4,8 @@
 ``A @ (k * B^2)``) with B a BitsparseTensor decoded tile by tile into LDS by
 the kernel; it replaces the decompress-to-HBM + GEMM of reference
 lib_sparse/src/sparse_matmul.py:24-28 / :109-113.  Packed (pack_sbit) values
-go to the ``*_packed`` entry points, which read the stream itself (reference
+go to the ``*_packed`` entry points, which unpack the tensor's value run (not
+a dense B) in a pre-pass that the GEMM then stages from (reference
 bitpacking.py:37-55 ahead of the same GEMMs).
 """
 from __future__ import annotations
@@ -111,7 +112,9 @@ def gemm_compressed_b(A: Tensor, B_sparse, square: bool) -> Tensor:
         a_layout, a_src, lda = 0, At, At.stride(0)
     L = _lib.load()
     C = torch.empty((M, N), device=A.device, dtype=torch.bfloat16)
-    need = L.bs_gemm_compressed_b_workspace_bytes(M, N, K, a_layout)
+    wsfn = (L.bs_gemm_compressed_b_packed_workspace_bytes if B_sparse.pack_sbit
+            else L.bs_gemm_compressed_b_workspace_bytes)
+    need = wsfn(M, N, K, a_layout)
     ws = torch.empty(max(need, 0), device=A.device, dtype=torch.uint8) if need > 0 else None
     scale = B_sparse.scale if (square and B_sparse.scale is not None) else None
     fn = L.bs_gemm_compressed_b_packed if B_sparse.pack_sbit else L.bs_gemm_compressed_b

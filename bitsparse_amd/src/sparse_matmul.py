@@ -14,9 +14,9 @@ Design.  The compressed operand is consumed where it lies:
   ``row_batch``, which in the reference bounds the size of the dense B it
   decompresses, has nothing to bound for bf16 and the product is computed in
   one launch (one fp32 accumulation over all of K instead of one bf16
-  rounding per batch).  Packed (pack_sbit) storage goes the same way: the
-  bf16 GEMM widens the 15-bit fields as it stages each tile's run, the fp8
-  GEMM unpacks the 7-bit codes in the pass that maps them.
+  rounding per batch).  Packed (pack_sbit) storage goes the same way: a
+  pre-pass of each GEMM call unpacks the tensor's value run (15-bit fields
+  to bf16; 7-bit codes in the pass that maps fp8 codes), never a dense B.
 * Every other case (fp8 row batches -- whose per-batch
   re-quantization is part of their result --, a compressed left operand)
   decodes B to dense -- whole, or ``row_batch`` rows at a time through a

@@ -397,9 +397,11 @@ int bs_gemm_compressed_b_fp8(const void* A, const float* a_scale, int64_t M, int
  * *vals_offset is a value index into the stream.  Everything else as the
  * unpacked entry points.
  *   bs_gemm_compressed_b_packed: bf16 values (vals_dtype 0, 15-bit fields);
- *     each 8-value unit of a tile's run is its 15 stream bytes, widened to
- *     bf16 (sign 0, and squared when square = 1) as the run is staged in LDS.
- *     Workspace: bs_gemm_compressed_b_workspace_bytes.
+ *     a pre-pass unpacks the tensor's run (its nnz values, not a dense B)
+ *     to bf16 in the workspace, which the GEMM then stages as stored
+ *     values (square = 1 squares them there).  Workspace:
+ *     bs_gemm_compressed_b_packed_workspace_bytes (K N bf16 values
+ *     reserved for the run).
  *   bs_gemm_compressed_b_fp8_packed: fp8 values (vals_dtype 1 or 2, 7-bit
  *     fields); the pass that maps the codes for square = 1 reads them from
  *     the stream, and for square = 0 the same pass copies them unmapped, into
@@ -410,6 +412,7 @@ int bs_gemm_compressed_b_fp8(const void* A, const float* a_scale, int64_t M, int
  * (lib_sparse/src/triton_kernels.py:186-187, load_packed_at_indices of
  * bitpacking.py:37-55) ahead of its GEMM (sparse_matmul.py:24-28, :109-113).
  */
+int64_t bs_gemm_compressed_b_packed_workspace_bytes(int64_t M, int64_t N, int64_t K, int a_layout);
 int bs_gemm_compressed_b_packed(const void* A, int64_t M, int64_t K, int64_t lda, int a_layout,
                                 const void* stream_bytes, int vals_dtype, int64_t stream_nbytes,
                                 const uint8_t* bitmask, const uint32_t* prefix, const int64_t* vals_offset,

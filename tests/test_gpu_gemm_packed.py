@@ -1,7 +1,7 @@
 """Reconstruct-into-LDS GEMMs on packed (pack_sbit) storage:
-bs_gemm_compressed_b_packed (bf16 values, 15-bit fields widened as each
-tile's run is staged) and bs_gemm_compressed_b_fp8_packed (7-bit fp8 codes,
-unpacked by the pass that maps them).
+bs_gemm_compressed_b_packed (bf16 values: the run's 15-bit fields unpacked to
+bf16 by a pre-pass the GEMM stages from) and bs_gemm_compressed_b_fp8_packed
+(7-bit fp8 codes, unpacked by the pass that maps them).
 
 The packed and the raw storage of one activation hold the same values, and
 both GEMMs run the same kernels over them (same workgroup shape, split and
