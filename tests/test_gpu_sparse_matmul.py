@@ -64,26 +64,22 @@ def test_aspb_bf16_row_batch_runs_the_lds_gemm(dev, row_batch):
 
 
 @pytest.mark.parametrize("row_batch", [0, 128, 200])
-def test_aspb_packed_row_batches_match_reference_accumulation(dev, row_batch):
-    """Packed storage goes through decompress + library GEMM; with row_batch
-    the blocks accumulate with addmm_ into a bf16 output, which is exactly
-    the reference's computation on the dense operand."""
-    from bitsparse_amd.src.sparse_matmul import AspB, AspRelu2B
+def test_aspb_packed_runs_the_lds_gemm_as_raw_storage(dev, row_batch):
+    """Packed (pack_sbit) bf16 storage takes the LDS GEMM like raw storage:
+    every row_batch is its one launch (no dense B), bit-identical to the
+    raw-storage product of the same activation."""
+    from bitsparse_amd.src.sparse_matmul import AspB, AspRelu2B, decoded
     K, N, M = 320, 256, 128
     h = relu_input((K, N), 0.5, seed=4)
     dY = preact_input((K, M), seed=5).to(dev)
     sp = _compress(h, dev, pack_sbit=True)
-    hd = h.to(dev)
-    for fn, op in ((AspB, lambda t: t), (AspRelu2B, lambda t: t.square())):
+    raw = _compress(h, dev)
+    for fn in (AspB, AspRelu2B):
         got = fn(dY.T, sp, row_batch=row_batch)
-        if row_batch <= 0:
-            ref = dY.T @ op(hd)
-        else:
-            ref = torch.zeros((M, N), device=dev, dtype=torch.bfloat16)
-            step = max(1, row_batch // 64) * 64
-            for r0 in range(0, K, step):
-                ref.addmm_(dY.T[:, r0:r0 + step], op(hd[r0:r0 + step]))
-        assert torch.equal(got, ref)
+        assert torch.equal(got, fn(dY.T, raw, row_batch=row_batch))
+        assert torch.equal(got, fn(dY.T, sp, row_batch=0))
+    _close(AspB(dY.T, sp, row_batch=row_batch), dY.T.float() @ h.to(dev).float())
+    _close(AspRelu2B(dY.T, sp, row_batch=row_batch), dY.T.float() @ decoded(sp, True).float())
 
 
 @pytest.mark.parametrize("row_batch", [0, 128])
