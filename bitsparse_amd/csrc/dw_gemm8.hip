@@ -380,8 +380,11 @@ __global__ __launch_bounds__(CFG::THREADS, CFG::MINB) void gemm_cb8_kernel(Gemm8
     // block's B fragments are read during the current one; one stage of the
     // software-pipelined decode of the next step goes with each MFMA (chunk
     // X/PER: stage_r at X%PER == 0, stage_s half a period later, stage_w at
-    // the next chunk's stage_r).
-    auto step = [&](int s, auto RI) __attribute__((always_inline)) {
+    // the next chunk's stage_r), and `ld` issues the iteration's global loads
+    // behind MFMAs already issued (a burst of them ahead of the first MFMA
+    // stalled the issue while the TA queue drained, with the MFMA pipe idle:
+    // 0.360 -> 0.345 ms at configs[3]).
+    auto step = [&](int s, auto RI, auto&& ld) __attribute__((always_inline)) {
         constexpr int P = decltype(RI)::value;          // s & 1: B_s buffer and A register set
         constexpr int AS = P;
         constexpr int PER = CFG::PER;
@@ -399,6 +402,7 @@ __global__ __launch_bounds__(CFG::THREADS, CFG::MINB) void gemm_cb8_kernel(Gemm8
             // later, and the compiler would otherwise sink all of them past
             // the run staging to the end of the iteration
             asm volatile("" : "+a"(acc[i][jj]));
+            ld(XI);
             if constexpr (X % PER == 0) stage_r(IC<X / PER>{});
             if constexpr (X % PER == PER / 2) stage_s(IC<X / PER>{}, run32);
             if constexpr (X % PER == 0 && X >= PER) stage_w(IC<X / PER - 1>{}, dst);
@@ -410,9 +414,9 @@ __global__ __launch_bounds__(CFG::THREADS, CFG::MINB) void gemm_cb8_kernel(Gemm8
     // Pipeline.  Step j: run(j) staged in run_s[j % 3] through register slot
     // j & 1, bitmask rows in bmq[j & 1], A(j) in areg[j & 1], B(j) decoded
     // into B_s[j & 1].  Iteration s builds the row table of step s+1, then
-    // issues (in this order: loads complete in order, and A is needed an
-    // iteration before the run) A(s+1) and the rows and run of step s+3;
-    // multiplies step s while decoding
+    // multiplies step s while issuing (in this order: loads complete in order,
+    // and A is needed an iteration before the run) A(s+1) and the rows and
+    // run of step s+3 behind its first MFMAs, and while decoding
     // B(s+1) from run_s[(s+1) % 3]; stages run(s+2), loaded an iteration ago,
     // into run_s[(s+2) % 3] (freed by the decode of step s-1) and meets the
     // other waves at the barrier.  Runs thus get two iterations to arrive, A
@@ -446,10 +450,12 @@ __global__ __launch_bounds__(CFG::THREADS, CFG::MINB) void gemm_cb8_kernel(Gemm8
         run_geom(s1, e0a, pha, nua);
         run_geom(s3, e0b, phb, nub);
         decode_rows_at(pha, bmq[P ^ 1]);
-        load_a(s1, IC<P ^ 1>{});
-        bmq[P ^ 1] = load_bm(s3);
-        load_run_at(e0b, nub, IC<P ^ 1>{});
-        step(s, RI);
+        step(s, RI, [&](auto XI) __attribute__((always_inline)) {
+            constexpr int X = decltype(XI)::value;
+            if constexpr (X == 0) load_a(s1, IC<P ^ 1>{});
+            if constexpr (X == CFG::SEG / 4) bmq[P ^ 1] = load_bm(s3);
+            if constexpr (X == CFG::SEG / 2) load_run_at(e0b, nub, IC<P ^ 1>{});
+        });
         store_run((s + 2) % 3, IC<P>{});
         __syncthreads();
     };
