@@ -72,9 +72,10 @@ struct Gemm8Cfg {
     static constexpr int PER = SEG / CH;                         // MFMAs per decoded chunk
     static constexpr int OFF_B = 0;                              // B_s[2][64][BP] bytes
     static constexpr int OFF_RUN = OFF_B + 2 * kBK * BP;         // run_s[3][NT][kRun8Slots] uint4
-    static constexpr int OFF_BM = OFF_RUN + 3 * NT * kRun8Slots * 16;   // bm_s[NWAVES][64] uint64
-    static constexpr int OFF_RP = OFF_BM + NWAVES * 64 * 8;     // rp_s[NWAVES][64] uint32
-    static constexpr int OFF_SEL = OFF_RP + NWAVES * 64 * 4;    // sel_s[256] uint2
+    // row tables of two steps (the one decoded now, the one built for later)
+    static constexpr int OFF_BM = OFF_RUN + 3 * NT * kRun8Slots * 16;   // bm_s[2][NWAVES][64] uint64
+    static constexpr int OFF_RP = OFF_BM + 2 * NWAVES * 64 * 8;     // rp_s[2][NWAVES][64] uint32
+    static constexpr int OFF_SEL = OFF_RP + 2 * NWAVES * 64 * 4;    // sel_s[256] uint2
     static constexpr int OFF_PF = OFF_SEL + 256 * 8;            // pf_s[NT][kMaxSteps] uint2: prefix[t], prefix[t+1]
     static constexpr int ST_P = WAVE_N + 4;                      // epilogue staging pitch (floats)
     static constexpr int LDS_MAIN = OFF_PF + NT * kMaxSteps * 8;
@@ -265,20 +266,22 @@ __global__ __launch_bounds__(CFG::THREADS, CFG::MINB) void gemm_cb8_kernel(Gemm8
     const int dc = lane & 7, dg = lane >> 3;
     const uint64_t below_mask = dc == 0 ? 0ull : (~0ull >> (64 - 8 * dc));
     const int rbase = 8 * CH * tq;
-    auto decode_rows_at = [&](int phase, uint64_t bmr) __attribute__((always_inline)) {
+    // row table tb (step parity): lane r's row word and the run index of its
+    // first value (phase + exclusive prefix of the row popcounts)
+    auto decode_rows_at = [&](int phase, uint64_t bmr, int tb) __attribute__((always_inline)) {
         const uint32_t c = (uint32_t)__popcll(bmr);
         const uint32_t rp = wave_incl_scan(c) - c;
-        bm_s[wave * 64 + lane] = bmr;
-        rp_s[wave * 64 + lane] = rp + (uint32_t)phase;
+        bm_s[(tb * CFG::NWAVES + wave) * 64 + lane] = bmr;
+        rp_s[(tb * CFG::NWAVES + wave) * 64 + lane] = rp + (uint32_t)phase;
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     };
-    auto decode_rows = [&](int s, uint64_t bmr) __attribute__((always_inline)) {
+    auto decode_rows = [&](int s, uint64_t bmr, int tb) __attribute__((always_inline)) {
         int64_t e0;
         int phase, nunits;
         run_geom(s, e0, phase, nunits);
-        decode_rows_at(phase, bmr);
+        decode_rows_at(phase, bmr, tb);
     };
     struct Dec {
         uint64_t mrow;
@@ -287,11 +290,11 @@ __global__ __launch_bounds__(CFG::THREADS, CFG::MINB) void gemm_cb8_kernel(Gemm8
         uint32_t d0, d1, d2, sh;
     };
     Dec dq[2];
-    auto stage_r = [&](auto CI) __attribute__((always_inline)) {
+    auto stage_r = [&](auto CI, int tb) __attribute__((always_inline)) {
         constexpr int C = decltype(CI)::value;
         const int row = rbase + 8 * C + dg;
-        dq[C & 1].mrow = bm_s[wave * 64 + row];
-        dq[C & 1].rpr = rp_s[wave * 64 + row];
+        dq[C & 1].mrow = bm_s[(tb * CFG::NWAVES + wave) * 64 + row];
+        dq[C & 1].rpr = rp_s[(tb * CFG::NWAVES + wave) * 64 + row];
     };
     auto stage_s = [&](auto CI, const uint32_t* run32) __attribute__((always_inline)) {
         constexpr int C = decltype(CI)::value;
@@ -319,11 +322,11 @@ __global__ __launch_bounds__(CFG::THREADS, CFG::MINB) void gemm_cb8_kernel(Gemm8
     auto dst_ptr = [&](int bb) __attribute__((always_inline)) {
         return B_s + bb * (kBK * BP) + tw * 64 + dc * 8;
     };
-    auto decode = [&](int rb, int bb) __attribute__((always_inline)) {
+    auto decode = [&](int rb, int bb, int tb) __attribute__((always_inline)) {
         const uint32_t* run32 = run_ptr(rb);
         uint8_t* dst = dst_ptr(bb);
         static_for<CH>([&](auto CI) __attribute__((always_inline)) {
-            stage_r(CI);
+            stage_r(CI, tb);
             stage_s(CI, run32);
             stage_w(CI, dst);
         });
@@ -403,7 +406,7 @@ __global__ __launch_bounds__(CFG::THREADS, CFG::MINB) void gemm_cb8_kernel(Gemm8
             // the run staging to the end of the iteration
             asm volatile("" : "+a"(acc[i][jj]));
             ld(XI);
-            if constexpr (X % PER == 0) stage_r(IC<X / PER>{});
+            if constexpr (X % PER == 0) stage_r(IC<X / PER>{}, P ^ 1);
             if constexpr (X % PER == PER / 2) stage_s(IC<X / PER>{}, run32);
             if constexpr (X % PER == 0 && X >= PER) stage_w(IC<X / PER - 1>{}, dst);
             __builtin_amdgcn_sched_barrier(0);
@@ -412,15 +415,17 @@ __global__ __launch_bounds__(CFG::THREADS, CFG::MINB) void gemm_cb8_kernel(Gemm8
     };
 
     // Pipeline.  Step j: run(j) staged in run_s[j % 3] through register slot
-    // j & 1, bitmask rows in bmq[j & 1], A(j) in areg[j & 1], B(j) decoded
-    // into B_s[j & 1].  Iteration s builds the row table of step s+1, then
-    // multiplies step s while issuing (in this order: loads complete in order,
-    // and A is needed an iteration before the run) A(s+1) and the rows and
-    // run of step s+3 behind its first MFMAs, and while decoding
-    // B(s+1) from run_s[(s+1) % 3]; stages run(s+2), loaded an iteration ago,
-    // into run_s[(s+2) % 3] (freed by the decode of step s-1) and meets the
-    // other waves at the barrier.  Runs thus get two iterations to arrive, A
-    // one.  Loads past the last step re-read it.
+    // j & 1, bitmask rows in bmq[j & 1], row table j & 1, A(j) in
+    // areg[j & 1], B(j) decoded into B_s[j & 1].  Iteration s multiplies step
+    // s while decoding B(s+1) from run_s[(s+1) % 3] with row table (s+1) & 1,
+    // and issues behind its MFMAs, in this order (loads complete in order,
+    // and A is needed an iteration before the run): A(s+1), the rows and run
+    // of step s+3, the row table of step s+2 (into table s & 1, which the
+    // decode of B(s) last read an iteration ago) and the staging of run(s+2),
+    // loaded an iteration ago, into run_s[(s+2) % 3] (freed by the decode of
+    // step s-1).  It then meets the other waves at the barrier.  Runs thus
+    // get two iterations to arrive, A one.  Loads past the last step re-read
+    // it.
     uint64_t bmq[2] = {0ull, 0ull};
     __syncthreads();                                   // sel_s, pf_s
     if (nsteps > 0) {
@@ -434,29 +439,30 @@ __global__ __launch_bounds__(CFG::THREADS, CFG::MINB) void gemm_cb8_kernel(Gemm8
     }
     __syncthreads();
     if (nsteps > 0) {
-        decode_rows(0, bmq[0]);
-        decode(0, 0);
+        decode_rows(0, bmq[0], 0);
+        decode(0, 0, 0);
+        decode_rows(min(1, last), bmq[1], 1);
         bmq[0] = load_bm(min(2, last));
         load_run(min(2, last), IC<0>{});
     }
     __syncthreads();
     auto iteration = [&](int s, auto RI) __attribute__((always_inline)) {
         constexpr int P = decltype(RI)::value;         // s & 1
-        const int s1 = min(s + 1, last), s3 = min(s + 3, last);
+        const int s1 = min(s + 1, last), s2 = min(s + 2, last), s3 = min(s + 3, last);
         // both steps' run geometry first: the two prefix reads share one
         // LDS round trip (the row-table stores would otherwise order them)
         int64_t e0a, e0b;
         int pha, phb, nua, nub;
-        run_geom(s1, e0a, pha, nua);
+        run_geom(s2, e0a, pha, nua);
         run_geom(s3, e0b, phb, nub);
-        decode_rows_at(pha, bmq[P ^ 1]);
         step(s, RI, [&](auto XI) __attribute__((always_inline)) {
             constexpr int X = decltype(XI)::value;
             if constexpr (X == 0) load_a(s1, IC<P ^ 1>{});
             if constexpr (X == CFG::SEG / 4) bmq[P ^ 1] = load_bm(s3);
             if constexpr (X == CFG::SEG / 2) load_run_at(e0b, nub, IC<P ^ 1>{});
+            if constexpr (X == CFG::SEG / 2 + 1) decode_rows_at(pha, bmq[P], P);
+            if constexpr (X == CFG::SEG * 3 / 4) store_run((s + 2) % 3, IC<P>{});
         });
-        store_run((s + 2) % 3, IC<P>{});
         __syncthreads();
     };
     int s = 0;
