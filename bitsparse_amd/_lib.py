@@ -17,7 +17,7 @@ LIB_NAME = "libbitsparse_hip.so"
 # BITSPARSE_HIP_LIB points at another build of the same sources (tuning sweeps)
 LIB_PATH = os.environ.get("BITSPARSE_HIP_LIB") or os.path.join(
     os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 BS_OK = 0
 BS_ERR_INVALID = 1
@@ -44,6 +44,7 @@ _SIGNATURES = {
     "bs_linear_relu_compress": [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _i64,
                                 _vp, _int, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _u32, _vp],
     "bs_linear_relu_compress_max_n": [_int],
+    "bs_host_device_pointer": [_vp, _vp],
     "bs_compress_packed": [_vp, _int, _i64, _i64, _int, _vp, _u32, _vp, _vp, _vp, _vp, _vp, _i64, _vp,
                            _vp, _vp, _vp, _vp, _i64, _u32, _int, _vp, _vp],
     "bs_amax_relu": [_vp, _i64, _vp, _i64, _u32, _vp],

@@ -18,22 +18,28 @@ __device__ __forceinline__ uint64_t pack_status(uint32_t epoch, uint64_t flag, u
     return ((uint64_t)epoch << 34) | (flag << 32) | v;
 }
 
-// Positive-bit byte of 8 bf16 values with packed 16-bit arithmetic:
-// x > 0  <=>  (bits - 1) mod 2^16 < 0x7f80.
+// Positive-bit byte of 8 bf16 values (x > 0: bits in [1, 0x7f80]) with
+// packed 16-bit arithmetic, 13 VALU ops.  Per half, ((bits + 0x807f) mod 2^16)
+// saturating-minus 0x80 has bit 15 set exactly for those bits: [1, 0x7f80]
+// goes to [0x8080, 0xffff] and then [0x8000, 0xff7f]; 0 and the negative NaNs
+// [0xff81, 0xffff] go to [0x8000, 0x807f] and then below 0x8000; the rest
+// ([0x7f81, 0xff80]) wraps to [0, 0x7fff] and stays below.  v_perm selectors
+// 8-11 replicate bits 15 / 31 of the second and first source into whole
+// bytes, the masks keep bit k of byte k (values 0-3) and bit 4 + k (values
+// 4-7), and a dot product with 0x01010101 adds (ORs) the four bytes.
 __device__ __forceinline__ uint32_t mask_bf16x8_pk(const uint4 v)
 {
     typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-    uint32_t q[4];
+    uint32_t u[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const u16x2 h = __builtin_bit_cast(u16x2, w[i]);
-        const u16x2 t = h - (u16x2)(1);
-        const u16x2 s = __builtin_elementwise_sub_sat((u16x2)(0x7f80), t);
-        q[i] = __builtin_bit_cast(uint32_t, __builtin_elementwise_min(s, (u16x2)(1)));   // bits 0, 16
+        const u16x2 t = __builtin_bit_cast(u16x2, w[i]) + (u16x2)(0x807f);
+        u[i] = __builtin_bit_cast(uint32_t, __builtin_elementwise_sub_sat(t, (u16x2)(0x80)));
     }
-    const uint32_t x = q[0] | (q[1] << 2) | (q[2] << 4) | (q[3] << 6);
-    return (x & 0x55u) | ((x >> 15) & 0xaau);
+    const uint32_t x = __builtin_amdgcn_perm(u[1], u[0], 0x0b0a0908u);   // values 0-3: 0xff / 0 bytes
+    const uint32_t y = __builtin_amdgcn_perm(u[3], u[2], 0x0b0a0908u);   // values 4-7
+    return __builtin_amdgcn_udot4((y & 0x80402010u) | (x & 0x08040201u), 0x01010101u, 0u, false);
 }
 
 // wave total of a per-lane value (every lane)

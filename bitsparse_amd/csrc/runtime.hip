@@ -105,7 +105,23 @@ using namespace bs;
 
 extern "C" const char* bs_last_error(void) { return bs::g_err; }
 
-extern "C" int bs_abi_version(void) { return 13; }
+extern "C" int bs_abi_version(void) { return 14; }
+
+extern "C" int bs_host_device_pointer(void* host_ptr, void** device_ptr)
+{
+    clear_error();
+    if (host_ptr == nullptr || device_ptr == nullptr)
+        return set_error(BS_ERR_INVALID, "bs_host_device_pointer: null pointer");
+    void* d = nullptr;
+    const hipError_t e = hipHostGetDevicePointer(&d, host_ptr, 0);
+    if (e != hipSuccess || d == nullptr) {
+        (void)hipGetLastError();
+        return set_error(BS_ERR_HIP, "bs_host_device_pointer: %s is not mapped pinned host memory (%s)",
+                         "the pointer", hipGetErrorString(e));
+    }
+    *device_ptr = d;
+    return BS_OK;
+}
 
 extern "C" int64_t bs_nontemporal_min_bytes(int64_t bytes)
 {

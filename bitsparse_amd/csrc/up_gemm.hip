@@ -8,30 +8,37 @@
 // output, then the bias add) are the reference's; the fp32 accumulation order
 // is this kernel's own.
 //
-// GEMM: a workgroup is 4 waves (2 x 2, one per SIMD) on a 256 x 192 tile of
-// z; each wave holds 128 x 96 in 4 x 3 v_mfma_f32_32x32x16_bf16 accumulators
-// (192 AGPRs).  x [M, K] and W [N, K] are both k-contiguous, so a K-step (64)
-// stages a 256 x 64 slab of x and a 192 x 64 slab of W in LDS as 16-byte
-// chunks, eight per row.  The chunk index is XOR-swizzled with (row / 2) % 8:
-// 16 lanes storing two rows, or reading one chunk of 16 rows, then touch all
-// 64 banks once.  Slabs are double-buffered (one barrier per step); the next
-// step's slabs are loaded into registers while the current step's MFMAs run.
+// GEMM: a workgroup is 4 waves (2 x 2) on a 128 x 192 tile of z; each wave
+// holds 64 x 96 in 2 x 3 v_mfma_f32_32x32x16_bf16 accumulators (96 VGPRs), so
+// that a wave needs at most 256 VGPRs and the workgroup 80 KiB of LDS: two
+// workgroups share a CU, and one's epilogue (VALU, LDS and memory latency)
+// runs beside the other's MFMAs.  x [M, K] and W [N, K] are both
+// k-contiguous, so a K-step (64) stages a 128 x 64 slab of x and a 192 x 64
+// slab of W in LDS as 16-byte chunks, eight per row.  The chunk index is
+// XOR-swizzled with (row / 2) % 8: 16 lanes storing two rows, or reading one
+// chunk of 16 rows, then touch all 64 banks once.  Slabs are double-buffered
+// (one barrier per step); the next step's slabs are loaded into registers
+// while the current step's MFMAs run.
 //
 // Epilogue: the tile (bias, roundings, torch's GPU relu) is staged in LDS as
-// bf16; elements outside the matrix are staged as 0.  Wave w then owns tile
-// row w of the workgroup: three format tiles, one look-back "unit".  Units
-// are consecutive in tile order (unit (tm, cb) = tiles tm * grid_n + 3 cb ..
-// +2), so the decoupled look-back of the codec applies unchanged.  The wave
-//   * writes its 64 rows of h (16-byte stores) and the tiles' bitmask bytes,
-//   * publishes the unit's count, resolves its offset from the preceding
-//     units' status words and writes the tiles' prefix entries,
-//   * compacts each tile's set elements into a per-wave LDS run (v_perm
-//     selectors per mask byte) and stores the run with 16-byte stores, with
-//     element stores at its two partial ends.
+// bf16 over the slab buffers; elements outside the matrix are staged as 0.
+// Tile row u of the workgroup (three format tiles) is one look-back "unit",
+// shared by waves u and u + 2, each taking half of its 24 chunk rounds in
+// run order.  Units are consecutive in tile order (unit (tm, cb) = tiles
+// tm * grid_n + 3 cb .. +2), so the decoupled look-back of the codec applies
+// unchanged.  The two waves of a unit
+//   * write its 64 rows of h (16-byte stores) and the tiles' bitmask bytes,
+//   * exchange their counts through LDS; one publishes the unit's count,
+//   * compact the tiles' set elements into one LDS run (v_perm selectors per
+//     mask byte), each its half,
+//   * both resolve the unit's offset from the preceding units' status words
+//     (one publishes the inclusive prefix and writes the prefix entries),
+//   * and store the run with 16-byte stores, with element stores at its two
+//     partial ends.
 //
 // Look-back order: unit (tm, cb) waits for every unit before it in tile
 // order, among them (tm - 1, NB - 1), the last workgroup of the same
-// 256-row strip when tm is not the strip's first tile row: a workgroup
+// 128-row strip when tm is not the strip's first tile row: a workgroup
 // dispatched after it.  Every workgroup publishes its counts before it waits
 // for anything, so a strip completes once all of its NB workgroups have been
 // resident.  The host bounds NB by half the workgroups the GPU holds at once
@@ -50,19 +57,28 @@ namespace bs {
 
 typedef __bf16 up_bf16x8_t __attribute__((ext_vector_type(8)));
 
-constexpr int kUpBM = 256, kUpBN = 192;
-constexpr int kUpIM = 4, kUpJN = 3;                     // 32x32 accumulator blocks per wave
+constexpr int kUpBM = 128, kUpBN = 192;
+constexpr int kUpIM = 2, kUpJN = 3;                     // 32x32 accumulator blocks per wave
+constexpr int kUpUnits = kUpBM / kTile;                 // units (tile rows) per workgroup
 constexpr int kUpTiles = kUpBN / kTile;                 // format tiles per unit
-constexpr int kUpAStage = kUpBM * 128;                  // x slab: 256 rows x 64 k bf16
+constexpr int kUpAStage = kUpBM * 128;                  // x slab: 128 rows x 64 k bf16
 constexpr int kUpBStage = kUpBN * 128;                  // W slab: 192 rows x 64 k bf16
 constexpr int kUpMainLds = 2 * (kUpAStage + kUpBStage);
 constexpr int kUpHP = kUpBN * 2 + 16;                   // staged h row pitch, bytes
-constexpr int kUpOffSel = kUpMainLds > kUpBM * kUpHP ? kUpMainLds : kUpBM * kUpHP;
-constexpr int kUpLds = kUpOffSel + 256 * 32;            // + compaction selectors (8 dwords per mask byte)
+// after the main loop: staged h, the compaction selectors (8 dwords per
+// mask byte) and the units' count exchange, all inside the slab buffers
+constexpr int kUpOffSel = kUpBM * kUpHP;
+constexpr int kUpOffCnt = kUpOffSel + 256 * 32;
+constexpr int kUpEpiLds = kUpOffCnt + kUpUnits * 2 * 4 * 4;
+constexpr int kUpLds = kUpMainLds > kUpEpiLds ? kUpMainLds : kUpEpiLds;
+constexpr int kUpHalfRounds = 4 * kUpTiles;             // chunk rounds of half a unit, at most
+// the epilogue: four waves, two per unit; per-tile counts kept for three tiles
+static_assert(kUpUnits == 2 && kUpTiles == 3, "epilogue layout");
 // a unit's compacted run (phase <= 7, three tiles, the 8-element write
 // overrun) fits in the wave's 64 staged rows, where it is built
 static_assert(2 * (7 + kUpTiles * kTileNumel + 8) <= 64 * kUpHP, "unit run");
-static_assert(kUpLds <= 160 * 1024, "LDS budget");
+// two workgroups per CU (160 KiB of LDS)
+static_assert(kUpLds <= 80 * 1024, "LDS budget");
 
 struct UpArgs {
     const uint16_t* x;            // [M, K], row stride ldx
@@ -83,7 +99,7 @@ struct UpArgs {
     int64_t* offset_out;
     int64_t* start_out;
     int32_t* err;
-    int32_t* timeout;             // set to 1 when a look-back wait gave up
+    int32_t* timeout;             // set to 1 when a look-back wait gave up (device or mapped host memory)
     uint64_t* status;             // one word per unit
     uint32_t epoch;
     uint64_t patience;            // ticks a look-back wait may last (0: give up at once)
@@ -107,12 +123,20 @@ constexpr uint64_t kUpLookbackGiveUpTicks = 2000000;
 // walk sums values back to the nearest inclusive prefix; it re-reads while a
 // word it needs is unpublished.
 constexpr int kUpLbWords = 4;
+
+// The time-out flag takes a plain store at system scope (no read-modify-write,
+// so it may live in mapped pinned host memory, where atomics need the bus's
+// support); every writer stores the same 1.
+__device__ __forceinline__ void set_timeout(int32_t* f)
+{
+    __hip_atomic_store(f, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
 __device__ uint32_t up_lookback(const UpArgs& a, uint32_t u, int lane)
 {
     uint32_t excl = 0;
     int64_t pos = (int64_t)u - 1;
     if (a.patience == 0 && pos >= 0) {          // the forced time-out: no wait at all
-        if (lane == 0 && a.timeout) atomicOr(a.timeout, 1);
+        if (lane == 0 && a.timeout) set_timeout(a.timeout);
         return 0u;
     }
     const uint64_t t0 = wall_clock64();
@@ -135,7 +159,7 @@ __device__ uint32_t up_lookback(const UpArgs& a, uint32_t u, int lane)
         const uint64_t need = first == 63 ? ~0ull : ((2ull << first) - 1ull);
         if (__ballot(unpub) & need) {
             if (wall_clock64() - t0 > a.patience) {
-                if (lane == 0 && a.timeout) atomicOr(a.timeout, 1);
+                if (lane == 0 && a.timeout) set_timeout(a.timeout);
                 break;
             }
             __builtin_amdgcn_s_sleep(2);
@@ -148,7 +172,7 @@ __device__ uint32_t up_lookback(const UpArgs& a, uint32_t u, int lane)
     return excl;
 }
 
-__global__ __launch_bounds__(256, 1) void up_relu_compress_kernel(UpArgs a)
+__global__ __launch_bounds__(256, 2) void up_relu_compress_kernel(UpArgs a)
 {
     __shared__ __align__(16) uint8_t lds[kUpLds];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -158,12 +182,6 @@ __global__ __launch_bounds__(256, 1) void up_relu_compress_kernel(UpArgs a)
     const int64_t m0 = (int64_t)strip * kUpBM, n0 = (int64_t)cb * kUpBN;
 
     uint32_t* sel_s = reinterpret_cast<uint32_t*>(lds + kUpOffSel);
-    {
-        uint32_t sel[8];
-        compaction_selectors<2>((uint32_t)tid, sel);
-        *reinterpret_cast<uint4*>(&sel_s[tid * 8]) = uint4{sel[0], sel[1], sel[2], sel[3]};
-        *reinterpret_cast<uint4*>(&sel_s[tid * 8 + 4]) = uint4{sel[4], sel[5], sel[6], sel[7]};
-    }
 
     // ---- slab loads: thread t moves chunk t % 8 of rows t / 8 + 32 i; rows
     // past the matrix read zero through the resources, chunks past K are
@@ -234,7 +252,7 @@ __global__ __launch_bounds__(256, 1) void up_relu_compress_kernel(UpArgs a)
     // chunk 2 ks + l / 32 of its wave's rows
     const int fl = lane & 31;
     const uint32_t fswz = (uint32_t)((fl >> 1) & 7);
-    const int arow = wm * 128 + fl, brow = wn * 96 + fl;
+    const int arow = wm * 64 + fl, brow = wn * 96 + fl;
     up_bf16x8_t fa[2][kUpIM], fb[2][kUpJN];
     auto fread = [&](int buf, int ks, auto SET) __attribute__((always_inline)) {
         constexpr int S = decltype(SET)::value;
@@ -311,131 +329,165 @@ __global__ __launch_bounds__(256, 1) void up_relu_compress_kernel(UpArgs a)
     // Accumulator element r of lane l of a 32x32 block is row 8 (r / 4) +
     // 4 (l / 32) + r % 4, column l % 32; elements r, r + 1 (r even) are two
     // consecutive rows of one column and are converted together.  Without a
-    // bias the add of +0 is exact (it can only turn -0 into +0, which the
-    // relu does anyway), so every element takes the same branch-free path.
+    // bias the add is skipped: adding +0 can only turn -0 into +0, which the
+    // relu does anyway.
     uint8_t* hs = lds;
     {
         const int rq = 4 * (lane >> 5);
         const int rows_in = (int)std::min<int64_t>(kUpBM, a.M - m0);
         typedef float f32x2_t __attribute__((ext_vector_type(2)));
         typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-        typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
-        // relu of two bf16 halves with packed 16-bit arithmetic: a half is
-        // kept iff (bits - 0x8000) mod 2^16 >= 0x7f81 (positive or NaN), i.e.
-        // iff the saturating (bits - 0x8000) - 0x7f80 is nonzero; `in` (1 or
-        // 0 per half) also zeroes elements outside the matrix
-        auto relu2x = [](uint32_t hp, u16x2_t in) __attribute__((always_inline)) {
-            const u16x2_t h = __builtin_bit_cast(u16x2_t, hp);
-            const u16x2_t keep = __builtin_elementwise_min(
-                __builtin_elementwise_sub_sat((u16x2_t)(h - (u16x2_t)(0x8000)), (u16x2_t)(0x7f80)), in);
-            return __builtin_bit_cast(uint32_t, (u16x2_t)(h * keep));
+        typedef short i16x2_t __attribute__((ext_vector_type(2)));
+        // torch's GPU relu of two bf16 halves (x <= 0 -> +0, NaN kept): a half
+        // is kept iff its bits are >= -127 as int16 (+0, positive values, +Inf
+        // and every NaN; -0, negative values and -Inf are below), i.e. iff its
+        // saturating int16 sum with 127 is nonnegative: three packed ops
+        auto relu2x = [](uint32_t hp) __attribute__((always_inline)) {
+            const i16x2_t d = __builtin_elementwise_add_sat(__builtin_bit_cast(i16x2_t, hp), (i16x2_t)(127));
+            return hp & ~__builtin_bit_cast(uint32_t, (i16x2_t)(d >> (i16x2_t)(15)));
         };
-        auto stage = [&](auto BOUNDS) __attribute__((always_inline)) {
-            constexpr bool BD = decltype(BOUNDS)::value;
+        auto stage = [&](auto BOUNDS, auto BIAS) __attribute__((always_inline)) {
+            constexpr bool BD = decltype(BOUNDS)::value, HB = decltype(BIAS)::value;
 #pragma unroll
             for (int j = 0; j < kUpJN; j++) {
                 const int col = wn * 96 + 32 * j + fl;
                 const bool cin = n0 + col < a.N;
-                const float bj = (a.bias != nullptr && cin) ? bf16_to_f32(a.bias[n0 + col]) : 0.0f;
+                float bj = 0.0f;
+                if constexpr (HB) bj = cin ? bf16_to_f32(a.bias[n0 + col]) : 0.0f;
                 uint8_t* cp = hs + col * 2;
 #pragma unroll
                 for (int i = 0; i < kUpIM; i++) {
 #pragma unroll
                     for (int r = 0; r < 16; r += 2) {
-                        const int row = wm * 128 + 32 * i + 8 * (r >> 2) + rq + (r & 3);
-                        const uint32_t zp = __builtin_bit_cast(
+                        const int row = wm * 64 + 32 * i + 8 * (r >> 2) + rq + (r & 3);
+                        uint32_t hp = __builtin_bit_cast(
                             uint32_t, __builtin_convertvector(f32x2_t{acc[i][j][r], acc[i][j][r + 1]}, bf16x2_t));
-                        const f32x2_t zb = {__uint_as_float(zp << 16) + bj, __uint_as_float(zp & 0xffff0000u) + bj};
-                        const uint32_t hp = __builtin_bit_cast(uint32_t, __builtin_convertvector(zb, bf16x2_t));
-                        u16x2_t in = (u16x2_t)(1);
+                        if constexpr (HB) {
+                            const f32x2_t zb = {__uint_as_float(hp << 16) + bj, __uint_as_float(hp & 0xffff0000u) + bj};
+                            hp = __builtin_bit_cast(uint32_t, __builtin_convertvector(zb, bf16x2_t));
+                        }
+                        uint32_t h2 = relu2x(hp);
                         if constexpr (BD)
-                            in = u16x2_t{(unsigned short)(cin && row < rows_in), (unsigned short)(cin && row + 1 < rows_in)};
-                        const uint32_t h2 = relu2x(hp, in);
+                            h2 &= (cin && row < rows_in ? 0x0000ffffu : 0u) | (cin && row + 1 < rows_in ? 0xffff0000u : 0u);
                         *reinterpret_cast<uint16_t*>(cp + row * kUpHP) = (uint16_t)h2;
                         *reinterpret_cast<uint16_t*>(cp + (row + 1) * kUpHP) = (uint16_t)(h2 >> 16);
                     }
                 }
             }
         };
-        if (rows_in == kUpBM && n0 + kUpBN <= a.N) stage(IC<false>{});
-        else stage(IC<true>{});
+        const bool whole = rows_in == kUpBM && n0 + kUpBN <= a.N;
+        if (a.bias == nullptr) {
+            if (whole) stage(IC<false>{}, IC<false>{});
+            else stage(IC<true>{}, IC<false>{});
+        } else {
+            if (whole) stage(IC<false>{}, IC<true>{});
+            else stage(IC<true>{}, IC<true>{});
+        }
+    }
+    {
+        uint32_t sel[8];
+        compaction_selectors<2>((uint32_t)tid, sel);
+        *reinterpret_cast<uint4*>(&sel_s[tid * 8]) = uint4{sel[0], sel[1], sel[2], sel[3]};
+        *reinterpret_cast<uint4*>(&sel_s[tid * 8 + 4]) = uint4{sel[4], sel[5], sel[6], sel[7]};
     }
     __syncthreads();
 
-    // ---- wave w: tile row w of the workgroup (rows 64 w .. +63 of hs)
-    const uint32_t tm = strip * 4u + (uint32_t)wave;
-    if (tm >= a.grid_m) return;                         // past the matrix: no unit
-    const uint8_t* hw = hs + wave * 64 * kUpHP;
-    const int64_t grow0 = m0 + (int64_t)wave * 64;
-
-    // bitmask bytes and counts: tile tt, round k: lane l takes chunk 64 k + l
-    // (tile row 8 k + l / 8, columns 8 (l % 8) .. +7) -- the format's byte order
+    // ---- epilogue.  Unit ui (tile row ui of the workgroup: rows 64 ui .. +63
+    // of hs, three format tiles) is shared by waves ui and ui + kUpUnits.  Its
+    // 8 * ntiles chunk rounds -- tile tt, round k: lane l takes chunk 64 k + l,
+    // tile row 8 k + l / 8, columns 8 (l % 8) .. +7, the format's byte order --
+    // split into two halves in run order: half 0 takes the first 4 * ntiles,
+    // half 1 the rest.  Every wave passes the same barriers; the waves of a
+    // unit past the matrix do no work.
+    const int ui = wave % kUpUnits, half = wave / kUpUnits;
+    const uint32_t tm = strip * (uint32_t)kUpUnits + (uint32_t)ui;
+    const bool active = tm < a.grid_m;
+    const uint8_t* hw = hs + ui * 64 * kUpHP;
+    const int64_t grow0 = m0 + (int64_t)ui * 64;
     const uint32_t t0 = tm * a.grid_n + cb * (uint32_t)kUpTiles;
     const int ntiles = (int)std::min<uint32_t>((uint32_t)kUpTiles, a.grid_n - cb * (uint32_t)kUpTiles);
+    const int nr = 4 * ntiles, r0 = half * nr;          // the half's rounds: r0 .. r0 + nr - 1
     const int lrow = lane >> 3, lcol = (lane & 7) * 16;   // byte offset of the lane's chunk in a tile row
-    uint32_t mk[kUpTiles][2];                           // the 8 mask bytes of each tile, 4 per register
-    uint4 hv[kUpTiles][8];                              // the lane's chunks, reused by the compaction
-    uint32_t tcnt[kUpTiles], toff[kUpTiles + 1];
+    uint32_t* cnt_s = reinterpret_cast<uint32_t*>(lds + kUpOffCnt);   // [unit][half][tile] counts
+
+    // bitmask bytes and the half's per-tile counts
+    uint32_t mk[kUpHalfRounds / 4] = {};                // the half's mask bytes, 4 per register
+    uint4 hv[kUpHalfRounds];                            // the lane's chunks, reused by the compaction
+    uint32_t lc[kUpTiles] = {};                         // the lane's set elements per tile
+    if (active) {
+#pragma unroll
+        for (int i = 0; i < kUpHalfRounds; i++) {
+            if (i >= nr) continue;                      // nr is wave-uniform
+            const int r = r0 + i, tt = r >> 3, k = r & 7;
+            const uint4 v = *reinterpret_cast<const uint4*>(hw + (8 * k + lrow) * kUpHP + tt * 128 + lcol);
+            hv[i] = v;
+            const uint32_t m = mask_bf16x8_pk(v);
+            a.bitmask[(size_t)(t0 + tt) * kTileBytes + 64 * k + lane] = (uint8_t)m;
+            mk[i >> 2] |= m << (8 * (i & 3));
+            const uint32_t c = (uint32_t)__popc(m);
+            if (tt == 0) lc[0] += c;                    // tt is wave-uniform
+            else if (tt == 1) lc[1] += c;
+            else lc[2] += c;
+        }
+#pragma unroll
+        for (int tt = 0; tt < kUpTiles; tt++) {
+            const uint32_t tc = wave_total(lc[tt]);
+            if (lane == 0) cnt_s[(ui * 2 + half) * 4 + tt] = tc;
+        }
+    }
+    __syncthreads();                                    // both halves' counts
+
+    uint32_t toff[kUpTiles + 1], seg0 = 0;             // tile offsets in the unit's run; half 0's length
     toff[0] = 0;
 #pragma unroll
     for (int tt = 0; tt < kUpTiles; tt++) {
-        mk[tt][0] = mk[tt][1] = 0u;
-        uint32_t cl = 0;
-        if (tt < ntiles) {
-#pragma unroll
-            for (int k = 0; k < 8; k++) {
-                const uint4 v = *reinterpret_cast<const uint4*>(hw + (8 * k + lrow) * kUpHP + tt * 128 + lcol);
-                hv[tt][k] = v;
-                const uint32_t m = mask_bf16x8_pk(v);
-                a.bitmask[(size_t)(t0 + tt) * kTileBytes + 64 * k + lane] = (uint8_t)m;
-                mk[tt][k >> 2] |= m << (8 * (k & 3));
-                cl += (uint32_t)__popc(m);
-            }
-        }
-        tcnt[tt] = wave_total(cl);
-        toff[tt + 1] = toff[tt] + tcnt[tt];
+        const uint32_t c0 = cnt_s[(ui * 2) * 4 + tt], c1 = cnt_s[(ui * 2 + 1) * 4 + tt];
+        toff[tt + 1] = toff[tt] + c0 + c1;
+        seg0 += c0;
     }
     const uint32_t unit_total = toff[kUpTiles];
     const uint32_t u = tm * a.nb + cb;
-    if (lane == 0) st_relaxed(&a.status[u], pack_status(a.epoch, u == 0 ? kFlagInc : kFlagAgg, unit_total));
+    if (active && half == 0 && lane == 0)
+        st_relaxed(&a.status[u], pack_status(a.epoch, u == 0 ? kFlagInc : kFlagAgg, unit_total));
 
-    // the dense h stores go out while the preceding units publish
-    // dense h: 64 rows x 24 chunks, 16-byte stores (N % 8 == 0, ldh % 8 == 0)
-    if (a.h != nullptr) {
+    // the dense h stores go out while the preceding units publish: half h
+    // stores rows 32 h .. +31 of the unit, 24 chunks each, 16-byte stores
+    // (N % 8 == 0, ldh % 8 == 0)
+    if (active && a.h != nullptr) {
 #pragma unroll 4
-        for (int q = lane; q < 64 * (kUpBN / 8); q += 64) {
-            const int row = q / (kUpBN / 8), cc = q % (kUpBN / 8);
+        for (int q = lane; q < 32 * (kUpBN / 8); q += 64) {
+            const int row = 32 * half + q / (kUpBN / 8), cc = q % (kUpBN / 8);
             const int64_t grow = grow0 + row, gcol = n0 + cc * 8;
             if (grow < a.M && gcol < a.N)
                 *reinterpret_cast<uint4*>(a.h + grow * a.ldh + gcol) =
                     *reinterpret_cast<const uint4*>(hw + row * kUpHP + cc * 16);
         }
     }
-
+    __syncthreads();                                    // the unit's staged rows are read: the run replaces them
 
     // ---- values, first into LDS: the unit's runs are consecutive in vals,
-    // so the wave compacts all of them into one run at phase 0 -- in its own
-    // 64 staged rows, whose values it holds in registers and whose h stores
-    // have read them.  This needs no offset, so the preceding units have
-    // this long to publish before the look-back below.
-    uint16_t* run = reinterpret_cast<uint16_t*>(hs + wave * 64 * kUpHP);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // so its two halves compact all of them into one run at phase 0 -- in the
+    // unit's 64 staged rows, whose values they hold in registers.  This needs
+    // no offset, so the preceding units have this long to publish before the
+    // look-back below.  A compacted chunk's 8 elements are written in
+    // descending order, its elements past the count landing on the following
+    // chunks' positions, which later writes replace; half 0 writes nothing
+    // past its own run, whose following positions are half 1's (its chunks
+    // near that end store their elements one by one, clipped there).
+    uint16_t* run = reinterpret_cast<uint16_t*>(hs + ui * 64 * kUpHP);
+    if (active) {
+        uint32_t P = half == 0 ? 0u : seg0;            // run offset of the round
 #pragma unroll
-    for (int tt = 0; tt < kUpTiles; tt++) {
-        if (tt >= ntiles) break;
-        uint32_t P = toff[tt];                          // offset of round k in the unit's run
-#pragma unroll
-        for (int k = 0; k < 8; k++) {
-            const uint32_t m = (mk[tt][k >> 2] >> (8 * (k & 3))) & 0xffu;
+        for (int i = 0; i < kUpHalfRounds; i++) {
+            if (i >= nr) continue;
+            const uint32_t m = (mk[i >> 2] >> (8 * (i & 3))) & 0xffu;
             const uint32_t c = (uint32_t)__popc(m);
             const uint32_t incl = wave_incl_scan(c);
             const uint32_t ex = incl - c;
             const uint32_t base = P;
             P += (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
             if (c != 0u) {
-                const uint4 w = hv[tt][k];
+                const uint4 w = hv[i];
                 const uint4 s0 = *reinterpret_cast<const uint4*>(&sel_s[m * 8]);
                 const uint4 s1 = *reinterpret_cast<const uint4*>(&sel_s[m * 8 + 4]);
                 uint4 o;
@@ -443,30 +495,48 @@ __global__ __launch_bounds__(256, 1) void up_relu_compress_kernel(UpArgs a)
                 o.y = __builtin_amdgcn_perm(w.y, w.x, s0.y) | __builtin_amdgcn_perm(w.w, w.z, s1.y);
                 o.z = __builtin_amdgcn_perm(w.y, w.x, s0.z) | __builtin_amdgcn_perm(w.w, w.z, s1.z);
                 o.w = __builtin_amdgcn_perm(w.y, w.x, s0.w) | __builtin_amdgcn_perm(w.w, w.z, s1.w);
-                write_compacted<2>(reinterpret_cast<uint8_t*>(run + (int)base + (int)ex), o);
+                uint8_t* dst = reinterpret_cast<uint8_t*>(run + (int)base + (int)ex);
+                // half 0: elements before half 1's run (at least c)
+                const uint32_t lim = half == 0 ? seg0 - (base + ex) : 8u;
+                if (__ballot(lim < 8u) == 0ull) {
+                    write_compacted<2>(dst, o);
+                } else {                                // the whole wave: same descending order
+                    const uint32_t ow[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+                    for (int e = 7; e >= 0; e--) {
+                        if ((uint32_t)e < lim)
+                            *reinterpret_cast<uint16_t*>(dst + 2 * e) = (uint16_t)(ow[e >> 1] >> (16 * (e & 1)));
+                        asm volatile("" ::: "memory");
+                    }
+                }
             }
         }
     }
+    __syncthreads();                                    // the unit's run is complete
 
-    // ---- offset: look-back, prefix entries, cursor and flags
+    // ---- offset: look-back (both halves, read-only but for half 0's
+    // inclusive status), prefix entries, cursor and flags
+    if (!active) return;
     int64_t start = a.offset_in ? *a.offset_in : 0;
     if (a.align8) start = (start + 7) & ~(int64_t)7;
     uint32_t excl = 0;
     if (u != 0) {
         excl = up_lookback(a, u, lane);
-        if (lane == 0) st_relaxed(&a.status[u], pack_status(a.epoch, kFlagInc, excl + unit_total));
+        if (half == 0 && lane == 0) st_relaxed(&a.status[u], pack_status(a.epoch, kFlagInc, excl + unit_total));
     }
-#pragma unroll
-    for (int tt = 0; tt < kUpTiles; tt++)
-        if (lane == tt && tt < ntiles) a.prefix[t0 + tt] = excl + toff[tt];
     const uint32_t nunits = a.grid_m * a.nb;
-    if (lane == 0 && u == nunits - 1) {
-        a.prefix[a.T] = excl + unit_total;
-        const int64_t end = start + (int64_t)(excl + unit_total);
-        if (a.offset_out) *a.offset_out = end;
-        if (a.start_out) *a.start_out = start;
-        if (a.err && end > a.vals_capacity) atomicOr(a.err, 1);
-        if (a.err && start < 0) atomicOr(a.err, 2);
+    if (half == 0) {
+#pragma unroll
+        for (int tt = 0; tt < kUpTiles; tt++)
+            if (lane == tt && tt < ntiles) a.prefix[t0 + tt] = excl + toff[tt];
+        if (lane == 0 && u == nunits - 1) {
+            a.prefix[a.T] = excl + unit_total;
+            const int64_t end = start + (int64_t)(excl + unit_total);
+            if (a.offset_out) *a.offset_out = end;
+            if (a.start_out) *a.start_out = start;
+            if (a.err && end > a.vals_capacity) atomicOr(a.err, 1);
+            if (a.err && start < 0) atomicOr(a.err, 2);
+        }
     }
     if (start < 0) return;
 
@@ -475,10 +545,8 @@ __global__ __launch_bounds__(256, 1) void up_relu_compress_kernel(UpArgs a)
     // 8 j - a0 .. +7: its 16 bytes start at run byte 16 j - 2 a0, inside the
     // 8-byte-aligned 24 bytes from (16 j - 2 a0) & ~7, at byte offset
     // (-2 a0) mod 8 (the same for every slot).  Partial slots at the two ends
-    // take element stores; elements past the capacity are not written.
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // take element stores; elements past the capacity are not written.  The
+    // two halves take alternate 64-slot groups.
     const int64_t g = start + (int64_t)excl;
     const int a0 = (int)(g & 7);
     const int64_t room = a.vals_capacity - g;
@@ -487,7 +555,7 @@ __global__ __launch_bounds__(256, 1) void up_relu_compress_kernel(UpArgs a)
     uint16_t* const vbase = a.vals + (g - a0);             // 16-byte aligned
     const uint32_t off = (uint32_t)((8 - 2 * a0) & 7);     // byte offset in the window
     const uint8_t* runb = reinterpret_cast<const uint8_t*>(run);
-    for (int j = lane; j < nslots; j += 64) {
+    for (int j = lane + 64 * half; j < nslots; j += 128) {
         const int lo = std::max(8 * j, a0), hi = std::min(8 * j + 8, a0 + endr);
         if (lo == 8 * j && hi == 8 * j + 8) {
             const uint8_t* wp = runb + ((16 * j - 2 * a0) & ~7);

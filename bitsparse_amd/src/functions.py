@@ -108,13 +108,14 @@ def linear_relu_and_compress(x: Tensor, W: Tensor, b: Tensor | None,
     bitmask = torch.empty(num_tiles * TILE_BYTES, device=x.device, dtype=torch.uint8)
     prefix = torch.empty(num_tiles + 1, device=x.device, dtype=torch.uint32)
     vals_offset, new_offset = sparse_data.cursor()
-    timeout = torch.zeros(1, device=x.device, dtype=torch.int32)
+    ring = _flag_ring(x.device)
+    slot, flag_addr = ring.take()
     ops.linear_relu_compress_into(x, W, b, h, bitmask, prefix, sparse_data.vals, vals_offset, new_offset,
-                                  sparse_data.err_flags, timeout)
+                                  sparse_data.err_flags, flag_addr)
     sparse_data.advance(new_offset)
     sp = BitsparseTensor(sparse_data.vals, bitmask, prefix, (M, N), torch.bfloat16, grid_m, grid_n,
                          BLOCK_M, BLOCK_N, scale=None, vals_offset=vals_offset)
-    sp.lookback_check = LookbackCheck(timeout)
+    sp.lookback_check = LookbackCheck(ring, slot)
     return h, sp
 
 
@@ -124,21 +125,63 @@ class LookbackTimeout(RuntimeError):
     produced is wrong."""
 
 
-class LookbackCheck:
-    """The time-out flag of one fused up-projection launch, copied to pinned
-    host memory behind the kernel with an event, so that reading it waits for
-    that kernel only (not for everything queued since)."""
+class _FlagRing:
+    """Time-out flags of fused up-projection launches in pinned host memory
+    that the kernel stores into through its device address, so a launch adds
+    no fill and no copy to the stream: the host clears a slot before the
+    launch and reads it once the launch's event has completed.  Slot i is
+    word 16 i (its own 64 bytes); a slot is reused only after the launch that
+    last held it has ended and its check has taken the flag's value."""
 
-    def __init__(self, flag: Tensor):
-        self.flag = flag
-        self.host = torch.empty(1, dtype=torch.int32, pin_memory=True)
-        self.host.copy_(flag, non_blocking=True)
+    SLOTS = 256
+
+    def __init__(self, device: torch.device):
+        self.host = torch.zeros(self.SLOTS * 16, dtype=torch.int32, pin_memory=True)
+        self.words = self.host.numpy()
+        self.base = ops.host_device_pointer(self.host)
+        self.holders: list = [None] * self.SLOTS      # the LookbackCheck of each slot's last launch
+        self.next = 0
+
+    def take(self) -> tuple[int, int]:
+        """(slot, device address of its word), cleared."""
+        i = self.next
+        self.next = (i + 1) % self.SLOTS
+        if self.holders[i] is not None:
+            self.holders[i].timed_out()                # waits for that launch, keeps its flag
+            self.holders[i] = None
+        self.words[16 * i] = 0
+        return i, self.base + 64 * i
+
+
+_FLAG_RINGS: dict[int, _FlagRing] = {}
+
+
+def _flag_ring(device: torch.device) -> _FlagRing:
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    ring = _FLAG_RINGS.get(idx)
+    if ring is None:
+        ring = _FLAG_RINGS[idx] = _FlagRing(device)
+    return ring
+
+
+class LookbackCheck:
+    """The time-out flag of one fused up-projection launch (a slot of the
+    device's pinned flag ring) and an event recorded behind the launch, so
+    that reading the flag waits for that kernel only (not for everything
+    queued since)."""
+
+    def __init__(self, ring: _FlagRing, slot: int):
+        self.ring, self.slot = ring, slot
         self.event = torch.cuda.Event()
         self.event.record()
+        self.result = None
+        ring.holders[slot] = self
 
     def timed_out(self) -> bool:
-        self.event.synchronize()
-        return int(self.host[0]) != 0
+        if self.result is None:
+            self.event.synchronize()
+            self.result = int(self.ring.words[16 * self.slot]) != 0
+        return self.result
 
     def raise_if_timed_out(self) -> None:
         if self.timed_out():

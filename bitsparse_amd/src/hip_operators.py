@@ -7,6 +7,8 @@ stream of the tensors' device and raises on CPU tensors (no CPU path).
 """
 from __future__ import annotations
 
+import ctypes
+
 import torch
 from torch import Tensor
 
@@ -162,13 +164,14 @@ UP_LOOKBACK_PATIENCE_TICKS = -1
 def linear_relu_compress_into(x: Tensor, W: Tensor, bias: Tensor | None, h_out: Tensor | None,
                               bitmask: Tensor, prefix: Tensor, vals: Tensor,
                               vals_offset_in: Tensor | None, vals_offset_out: Tensor | None,
-                              err_flags: Tensor | None, timeout_flag: Tensor | None = None) -> None:
+                              err_flags: Tensor | None, timeout_flag: Tensor | int | None = None) -> None:
     """h = relu(x @ W.T + bias) with its compressed form, in one kernel
     (bs_linear_relu_compress): x [M, K], W [N, K], bias [N] (or None), bf16,
     rows contiguous; h_out (or None) [M, N] bf16 receives h; bitmask / prefix /
     vals / cursors as for ``compress_into`` (bf16 values); ``timeout_flag``
-    (int32 [1], zeroed, or None) is set to 1 if a look-back wait gave up, in
-    which case the compressed form is wrong."""
+    (a zeroed int32 device tensor, the device address of a zeroed pinned host
+    word from ``host_device_pointer``, or None) is set to 1 if a look-back
+    wait gave up, in which case the compressed form is wrong."""
     require_device(x, "linear_relu_compress")
     for t, what in ((x, "x"), (W, "W")):
         if t.dtype != torch.bfloat16 or t.dim() != 2 or t.stride(1) != 1:
@@ -191,9 +194,21 @@ def linear_relu_compress_into(x: Tensor, W: Tensor, bias: Tensor | None, h_out: 
                                     ptr(h_out), h_out.stride(0) if h_out is not None else N,
                                     bitmask.data_ptr(), prefix.data_ptr(), vals.data_ptr(), vals.numel(),
                                     ptr(vals_offset_in), 0, ptr(vals_offset_out), None, ptr(err_flags),
-                                    ptr(timeout_flag), int(UP_LOOKBACK_PATIENCE_TICKS),
+                                    timeout_flag if isinstance(timeout_flag, int) else ptr(timeout_flag),
+                                    int(UP_LOOKBACK_PATIENCE_TICKS),
                                     ws.buf.data_ptr(), ws.nbytes, epoch, stream_handle(x.device)),
           "bs_linear_relu_compress")
+
+
+def host_device_pointer(t: Tensor) -> int:
+    """Device address of a pinned host tensor's storage (bs_host_device_pointer),
+    for flags a kernel stores into directly; raises if the memory is not
+    mapped for the device."""
+    if not t.is_pinned():
+        raise ValueError("host_device_pointer: the tensor must be in pinned host memory")
+    out = ctypes.c_void_p()
+    check(_lib.load().bs_host_device_pointer(t.data_ptr(), ctypes.byref(out)), "bs_host_device_pointer")
+    return int(out.value)
 
 
 _UP_MAX_N: dict[int, int] = {}

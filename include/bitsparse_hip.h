@@ -169,8 +169,12 @@ int bs_compress_relu(const void* preact, int in_dtype, int64_t M, int64_t N, int
  * always exactly that of the h it writes.
  *   timeout_flag    nullable int32 the kernel sets to 1 when a look-back wait
  *                   gave up (the compressed form is then wrong and must be
- *                   discarded).  A unit can wait for a workgroup dispatched
- *                   after it in the same 256-row strip, so the strip's
+ *                   discarded), with a plain store: device memory, or pinned
+ *                   host memory through its device address
+ *                   (bs_host_device_pointer), which the host can read once
+ *                   the kernel has ended without a copy on the stream.  A
+ *                   unit can wait for a workgroup dispatched
+ *                   after it in the same 128-row strip, so the strip's
  *                   workgroups must be co-resident: the N bound keeps them to
  *                   half of what the device holds, but other streams' work
  *                   can still crowd them out.
@@ -190,6 +194,10 @@ int bs_linear_relu_compress(const void* x, int64_t M, int64_t K, int64_t ldx, co
 /* Largest N bs_linear_relu_compress accepts on `device` (-1 if the occupancy
  * query fails).  No counterpart in the reference. */
 int64_t bs_linear_relu_compress_max_n(int device);
+/* Device address of pinned (hipHostMalloc) host memory, for flags a kernel
+ * stores into directly (bs_linear_relu_compress's timeout_flag); BS_ERR_HIP if
+ * host_ptr is not mapped for the device.  No counterpart in the reference. */
+int bs_host_device_pointer(void* host_ptr, void** device_ptr);
 
 /*
  * bs_compress with pack_sbit storage: the values are written straight into

@@ -146,6 +146,8 @@ def test_invalid_arguments_rejected_on_host():
     assert rc == _lib.BS_ERR_INVALID
     rc = L.bs_amax(fake, -1, fake, 1 << 20, 1, None)
     assert rc == _lib.BS_ERR_INVALID
+    rc = L.bs_host_device_pointer(None, None)
+    assert rc == _lib.BS_ERR_INVALID and "null" in _err()
 
 
 def test_python_api_rejects_cpu_tensors_and_bad_dtypes():

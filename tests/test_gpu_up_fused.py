@@ -72,7 +72,7 @@ def _check_h(h, x, W, b):
     torch.testing.assert_close(h.float(), ref, rtol=2 ** -7, atol=atol, equal_nan=True)
 
 
-# (M, N, K): whole and partial 256 x 192 workgroup tiles, partial 64 x 64
+# (M, N, K): whole and partial 128 x 192 workgroup tiles, partial 64 x 64
 # format tiles, K not a multiple of the 64-deep step, one-tile matrices
 SHAPES = [(256, 192, 64), (300, 200, 72), (64, 8, 8), (1000, 768, 256), (513, 392, 40), (40, 1000, 128),
           (2048, 3072, 96)]
@@ -199,7 +199,7 @@ def test_forced_lookback_timeout_sets_its_own_flag(dev, monkeypatch):
     word is set and the capacity flags stay clear."""
     H = _ops()
     monkeypatch.setattr(H, "UP_LOOKBACK_PATIENCE_TICKS", 0)
-    x, W, b = _operands(512, 768, 64, 21, dev)          # 2 strips x 4 workgroups x 4 units
+    x, W, b = _operands(512, 768, 64, 21, dev)          # 4 strips x 4 workgroups x 2 units
     M, N = x.shape[0], W.shape[0]
     T = (M // 64) * (N // 64)
     h = torch.empty((M, N), device=dev, dtype=torch.bfloat16)
@@ -246,6 +246,31 @@ def test_layer_raises_on_lookback_timeout(dev, monkeypatch, relu2):
     assert not buf.overflowed()
 
 
+def test_flag_ring_keeps_a_timeout_across_slot_reuse(dev, monkeypatch):
+    """The layers' time-out flags are slots of a pinned host ring that the
+    kernel stores into through its device address (no copy on the stream).
+    A slot is reused after SLOTS launches: a check taken before that still
+    reports its own launch's (forced) time-out, and the later launches'
+    checks report none."""
+    from bitsparse_amd.bitsparse import TensorBuffer
+    from bitsparse_amd.src import functions as F
+    H = _ops()
+    x, W, _ = _operands(256, 192, 64, 24, dev, bias=False)   # 4 units: every unit but the first gives up
+    buf = TensorBuffer(2 * 256 * 192 + 64, device=dev)
+    monkeypatch.setattr(H, "UP_LOOKBACK_PATIENCE_TICKS", 0)
+    buf.reset_buffer()
+    _, sp0 = F.linear_relu_and_compress(x, W, None, buf)
+    monkeypatch.setattr(H, "UP_LOOKBACK_PATIENCE_TICKS", -1)
+    checks = []
+    for _ in range(F._FlagRing.SLOTS + 3):
+        buf.reset_buffer()
+        h, sp = F.linear_relu_and_compress(x, W, None, buf)
+        checks.append(sp.lookback_check)
+    assert sp0.lookback_check.timed_out()
+    assert not any(c.timed_out() for c in checks)
+    _check_compressed(h, sp.bitmask, sp.prefix, buf.vals, buf.offset)
+
+
 def test_width_bound_from_occupancy(dev):
     """The widest N the fused kernel takes comes from the occupancy API (half
     of the workgroups the device holds, 192 columns each); wider is refused by
@@ -257,7 +282,7 @@ def test_width_bound_from_occupancy(dev):
     max_n = H.linear_relu_compress_max_n(dev)
     props = torch.cuda.get_device_properties(dev)
     assert max_n > 0 and max_n % 192 == 0
-    assert max_n <= 192 * props.multi_processor_count      # at most one workgroup per CU here
+    assert max_n <= 192 * props.multi_processor_count      # half of two workgroups per CU
     assert int(_lib.load().bs_linear_relu_compress_max_n(dev.index or 0)) == max_n
     x, W, b = _operands(64, max_n + 192, 16, 24, dev, bias=False)
     assert not H.linear_relu_compress_supported(x, W, b)
