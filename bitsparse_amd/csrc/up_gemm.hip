@@ -143,10 +143,18 @@ __device__ uint32_t up_lookback(const UpArgs& a, uint32_t u, int lane)
     while (pos >= 0) {
         uint32_t sum = 0;
         bool unpub = false, inc = false;
+        // all of the lane's words in flight at once: unconditional loads (a
+        // word before unit 0 reads unit 0 and is replaced by an inclusive 0)
+        uint64_t w[kUpLbWords];
 #pragma unroll
         for (int i = 0; i < kUpLbWords; i++) {
             const int64_t q = pos - kUpLbWords * lane - i;
-            const uint64_t s = q >= 0 ? ld_relaxed(&a.status[q]) : pack_status(a.epoch, kFlagInc, 0u);
+            w[i] = ld_relaxed(&a.status[q >= 0 ? q : 0]);
+        }
+#pragma unroll
+        for (int i = 0; i < kUpLbWords; i++) {
+            const int64_t q = pos - kUpLbWords * lane - i;
+            const uint64_t s = q >= 0 ? w[i] : pack_status(a.epoch, kFlagInc, 0u);
             const uint32_t flag = (uint32_t)(s >> 34) == a.epoch ? (uint32_t)(s >> 32) & 3u : 0u;
             if (!inc) {                  // words up to the lane's nearest inclusive prefix
                 unpub |= flag == 0u;
@@ -182,6 +190,10 @@ __global__ __launch_bounds__(256, 2) void up_relu_compress_kernel(UpArgs a)
     const int64_t m0 = (int64_t)strip * kUpBM, n0 = (int64_t)cb * kUpBN;
 
     uint32_t* sel_s = reinterpret_cast<uint32_t*>(lds + kUpOffSel);
+    // the cursor, read at the start: a load issued in the epilogue waits for
+    // every earlier h / bitmask store as well (one vmcnt counts both)
+    int64_t start = a.offset_in ? *a.offset_in : 0;
+    if (a.align8) start = (start + 7) & ~(int64_t)7;
 
     // ---- slab loads: thread t moves chunk t % 8 of rows t / 8 + 32 i; rows
     // past the matrix read zero through the resources, chunks past K are
@@ -410,30 +422,37 @@ __global__ __launch_bounds__(256, 2) void up_relu_compress_kernel(UpArgs a)
     const int lrow = lane >> 3, lcol = (lane & 7) * 16;   // byte offset of the lane's chunk in a tile row
     uint32_t* cnt_s = reinterpret_cast<uint32_t*>(lds + kUpOffCnt);   // [unit][half][tile] counts
 
-    // bitmask bytes and the half's per-tile counts
+    // bitmask bytes and the half's per-tile counts.  Every round's chunk is
+    // read first (rounds past nr read staged rows of the same tile row: in
+    // bounds, their masks are dropped); a half spans at most two tiles, ta
+    // for its rounds i < bnd and ta + 1 after, so two lane counts packed in
+    // one word take one wave sum.
     uint32_t mk[kUpHalfRounds / 4] = {};                // the half's mask bytes, 4 per register
     uint4 hv[kUpHalfRounds];                            // the lane's chunks, reused by the compaction
-    uint32_t lc[kUpTiles] = {};                         // the lane's set elements per tile
+    const int ta = r0 >> 3, bnd = 8 - (r0 & 7);
     if (active) {
 #pragma unroll
         for (int i = 0; i < kUpHalfRounds; i++) {
-            if (i >= nr) continue;                      // nr is wave-uniform
             const int r = r0 + i, tt = r >> 3, k = r & 7;
-            const uint4 v = *reinterpret_cast<const uint4*>(hw + (8 * k + lrow) * kUpHP + tt * 128 + lcol);
-            hv[i] = v;
-            const uint32_t m = mask_bf16x8_pk(v);
-            a.bitmask[(size_t)(t0 + tt) * kTileBytes + 64 * k + lane] = (uint8_t)m;
+            hv[i] = *reinterpret_cast<const uint4*>(hw + (8 * k + lrow) * kUpHP + tt * 128 + lcol);
+        }
+        uint32_t cab = 0;                               // lane counts: tile ta in bits 0-15, ta + 1 above
+#pragma unroll
+        for (int i = 0; i < kUpHalfRounds; i++) {
+            const uint32_t m = mask_bf16x8_pk(hv[i]) & (0u - (uint32_t)(i < nr));
             mk[i >> 2] |= m << (8 * (i & 3));
-            const uint32_t c = (uint32_t)__popc(m);
-            if (tt == 0) lc[0] += c;                    // tt is wave-uniform
-            else if (tt == 1) lc[1] += c;
-            else lc[2] += c;
+            cab += (uint32_t)__popc(m) << (i < bnd ? 0 : 16);
         }
 #pragma unroll
-        for (int tt = 0; tt < kUpTiles; tt++) {
-            const uint32_t tc = wave_total(lc[tt]);
-            if (lane == 0) cnt_s[(ui * 2 + half) * 4 + tt] = tc;
+        for (int i = 0; i < kUpHalfRounds; i++) {
+            if (i < nr) {
+                const int r = r0 + i, tt = r >> 3, k = r & 7;
+                a.bitmask[(size_t)(t0 + tt) * kTileBytes + 64 * k + lane] = (uint8_t)(mk[i >> 2] >> (8 * (i & 3)));
+            }
         }
+        const uint32_t tot = wave_total(cab);           // a tile's count is at most 4096
+        if (lane < kUpTiles)
+            cnt_s[(ui * 2 + half) * 4 + lane] = lane == ta ? (tot & 0xffffu) : lane == ta + 1 ? (tot >> 16) : 0u;
     }
     __syncthreads();                                    // both halves' counts
 
@@ -476,28 +495,46 @@ __global__ __launch_bounds__(256, 2) void up_relu_compress_kernel(UpArgs a)
     // near that end store their elements one by one, clipped there).
     uint16_t* run = reinterpret_cast<uint16_t*>(hs + ui * 64 * kUpHP);
     if (active) {
+        // every round's selector rows first; rounds past nr have empty masks
+        uint4 s0[kUpHalfRounds], s1[kUpHalfRounds];
+#pragma unroll
+        for (int i = 0; i < kUpHalfRounds; i++) {
+            const uint32_t m = (mk[i >> 2] >> (8 * (i & 3))) & 0xffu;
+            s0[i] = *reinterpret_cast<const uint4*>(&sel_s[m * 8]);
+            s1[i] = *reinterpret_cast<const uint4*>(&sel_s[m * 8 + 4]);
+        }
+        // each round's lane offsets and total: three rounds per wave scan, in
+        // 10-bit fields (a round's total is at most 512)
+        uint32_t ex[kUpHalfRounds], rt[kUpHalfRounds];
+#pragma unroll
+        for (int g = 0; g < kUpHalfRounds / 3; g++) {
+            uint32_t cp = 0;
+#pragma unroll
+            for (int j = 0; j < 3; j++) cp |= (uint32_t)__popc((mk[(3 * g + j) >> 2] >> (8 * ((3 * g + j) & 3))) & 0xffu) << (10 * j);
+            const uint32_t incl = wave_incl_scan(cp);
+            const uint32_t last = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+#pragma unroll
+            for (int j = 0; j < 3; j++) {
+                ex[3 * g + j] = ((incl - cp) >> (10 * j)) & 1023u;
+                rt[3 * g + j] = (last >> (10 * j)) & 1023u;
+            }
+        }
         uint32_t P = half == 0 ? 0u : seg0;            // run offset of the round
 #pragma unroll
         for (int i = 0; i < kUpHalfRounds; i++) {
-            if (i >= nr) continue;
             const uint32_t m = (mk[i >> 2] >> (8 * (i & 3))) & 0xffu;
-            const uint32_t c = (uint32_t)__popc(m);
-            const uint32_t incl = wave_incl_scan(c);
-            const uint32_t ex = incl - c;
             const uint32_t base = P;
-            P += (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
-            if (c != 0u) {
+            P += rt[i];
+            if (m != 0u) {
                 const uint4 w = hv[i];
-                const uint4 s0 = *reinterpret_cast<const uint4*>(&sel_s[m * 8]);
-                const uint4 s1 = *reinterpret_cast<const uint4*>(&sel_s[m * 8 + 4]);
                 uint4 o;
-                o.x = __builtin_amdgcn_perm(w.y, w.x, s0.x) | __builtin_amdgcn_perm(w.w, w.z, s1.x);
-                o.y = __builtin_amdgcn_perm(w.y, w.x, s0.y) | __builtin_amdgcn_perm(w.w, w.z, s1.y);
-                o.z = __builtin_amdgcn_perm(w.y, w.x, s0.z) | __builtin_amdgcn_perm(w.w, w.z, s1.z);
-                o.w = __builtin_amdgcn_perm(w.y, w.x, s0.w) | __builtin_amdgcn_perm(w.w, w.z, s1.w);
-                uint8_t* dst = reinterpret_cast<uint8_t*>(run + (int)base + (int)ex);
-                // half 0: elements before half 1's run (at least c)
-                const uint32_t lim = half == 0 ? seg0 - (base + ex) : 8u;
+                o.x = __builtin_amdgcn_perm(w.y, w.x, s0[i].x) | __builtin_amdgcn_perm(w.w, w.z, s1[i].x);
+                o.y = __builtin_amdgcn_perm(w.y, w.x, s0[i].y) | __builtin_amdgcn_perm(w.w, w.z, s1[i].y);
+                o.z = __builtin_amdgcn_perm(w.y, w.x, s0[i].z) | __builtin_amdgcn_perm(w.w, w.z, s1[i].z);
+                o.w = __builtin_amdgcn_perm(w.y, w.x, s0[i].w) | __builtin_amdgcn_perm(w.w, w.z, s1[i].w);
+                uint8_t* dst = reinterpret_cast<uint8_t*>(run + (int)base + (int)ex[i]);
+                // half 0: elements before half 1's run (at least the chunk's count)
+                const uint32_t lim = half == 0 ? seg0 - (base + ex[i]) : 8u;
                 if (__ballot(lim < 8u) == 0ull) {
                     write_compacted<2>(dst, o);
                 } else {                                // the whole wave: same descending order
@@ -517,8 +554,6 @@ __global__ __launch_bounds__(256, 2) void up_relu_compress_kernel(UpArgs a)
     // ---- offset: look-back (both halves, read-only but for half 0's
     // inclusive status), prefix entries, cursor and flags
     if (!active) return;
-    int64_t start = a.offset_in ? *a.offset_in : 0;
-    if (a.align8) start = (start + 7) & ~(int64_t)7;
     uint32_t excl = 0;
     if (u != 0) {
         excl = up_lookback(a, u, lane);
@@ -555,27 +590,40 @@ __global__ __launch_bounds__(256, 2) void up_relu_compress_kernel(UpArgs a)
     uint16_t* const vbase = a.vals + (g - a0);             // 16-byte aligned
     const uint32_t off = (uint32_t)((8 - 2 * a0) & 7);     // byte offset in the window
     const uint8_t* runb = reinterpret_cast<const uint8_t*>(run);
-    for (int j = lane + 64 * half; j < nslots; j += 128) {
-        const int lo = std::max(8 * j, a0), hi = std::min(8 * j + 8, a0 + endr);
-        if (lo == 8 * j && hi == 8 * j + 8) {
-            const uint8_t* wp = runb + ((16 * j - 2 * a0) & ~7);
-            const uint2 q0 = *reinterpret_cast<const uint2*>(wp);
-            const uint2 q1 = *reinterpret_cast<const uint2*>(wp + 8);
-            const uint2 q2 = *reinterpret_cast<const uint2*>(wp + 16);
-            const uint32_t d[6] = {q0.x, q0.y, q1.x, q1.y, q2.x, q2.y};
-            uint32_t o[4];
-            if (off >= 4) {
+    // three slots per pass, all their windows read before any is stored;
+    // windows of partial slots and of slots past the end read clamped
+    // addresses inside the workgroup's LDS and go unused
+    auto store_slots = [&](auto SHIFT) __attribute__((always_inline)) {
+        constexpr int S = decltype(SHIFT)::value;           // off >= 4: the window's first dword is skipped
+        const uint32_t ob = off & 3u;
+        for (int j = lane + 64 * half; j < nslots; j += 3 * 128) {
+            uint32_t d[3][6];
 #pragma unroll
-                for (int i = 0; i < 4; i++) o[i] = __builtin_amdgcn_alignbyte(d[i + 2], d[i + 1], off - 4);
-            } else {
-#pragma unroll
-                for (int i = 0; i < 4; i++) o[i] = __builtin_amdgcn_alignbyte(d[i + 1], d[i], off);
+            for (int v = 0; v < 3; v++) {
+                const uint8_t* wp = runb + std::max(0, (16 * (j + 128 * v) - 2 * a0) & ~7);
+                const uint2 q0 = *reinterpret_cast<const uint2*>(wp);
+                const uint2 q1 = *reinterpret_cast<const uint2*>(wp + 8);
+                const uint2 q2 = *reinterpret_cast<const uint2*>(wp + 16);
+                d[v][0] = q0.x; d[v][1] = q0.y; d[v][2] = q1.x; d[v][3] = q1.y; d[v][4] = q2.x; d[v][5] = q2.y;
             }
-            *reinterpret_cast<uint4*>(vbase + 8 * j) = uint4{o[0], o[1], o[2], o[3]};
-        } else {
-            for (int e = lo; e < hi; e++) vbase[e] = run[e - a0];
+#pragma unroll
+            for (int v = 0; v < 3; v++) {
+                const int jj = j + 128 * v;
+                if (jj >= nslots) break;
+                const int lo = std::max(8 * jj, a0), hi = std::min(8 * jj + 8, a0 + endr);
+                if (lo == 8 * jj && hi == 8 * jj + 8) {
+                    uint32_t o[4];
+#pragma unroll
+                    for (int i = 0; i < 4; i++) o[i] = __builtin_amdgcn_alignbyte(d[v][i + 1 + S], d[v][i + S], ob);
+                    *reinterpret_cast<uint4*>(vbase + 8 * jj) = uint4{o[0], o[1], o[2], o[3]};
+                } else {
+                    for (int e = lo; e < hi; e++) vbase[e] = run[e - a0];
+                }
+            }
         }
-    }
+    };
+    if (off >= 4) store_slots(IC<1>{});
+    else store_slots(IC<0>{});
 }
 
 // Workgroups per tile row the launch accepts on device `dev`: half of what
