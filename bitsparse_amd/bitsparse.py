@@ -73,7 +73,7 @@ class BitsparseTensor:
         self.BLOCK_N = BLOCK_N
         self.shape = shape
         # produced by the fused up-projection: its look-back time-out flag
-        # (functions.LookbackCheck), checked before the values are first read
+        # (functions.LookbackCheck), checked by the backward that reads it
         self.lookback_check = None
 
     @property

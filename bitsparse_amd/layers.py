@@ -208,9 +208,6 @@ class _UpReluLinear(Function):
         x, W1, W2 = ctx.saved_tensors
         h: BitsparseTensor = ctx.h_sparse
         ctx.h_sparse = None
-        # the forward kernel's look-back must not have given up (checked here,
-        # where the compressed form is first read; waits for that kernel only)
-        h.lookback_check.raise_if_timed_out()
         if ctx.square:
             grad_W2 = AspRelu2B(grad_output.T, h)
         else:
@@ -223,7 +220,12 @@ class _UpReluLinear(Function):
             if ctx.needs_input_grad[0]:
                 grad_x = grad_z.mm(W1)
             if ctx.needs_input_grad[1]:
-                grad_W1 = x.t().mm(grad_z).t()
+                grad_W1 = grad_z.t().mm(x)          # W1's own layout, as autograd forms it for x @ W1.T
             if ctx.has_b1 and ctx.needs_input_grad[2]:
                 grad_b1 = grad_z.sum(0)
+        # the forward kernel's look-back must not have given up: checked once
+        # this node's kernels are queued (the check waits for that forward
+        # kernel, so checking first would leave the GPU idle while the host
+        # queues them); gradients from a misplaced value run are never returned
+        h.lookback_check.raise_if_timed_out()
         return grad_x, grad_W1, grad_b1, grad_W2, None, None
