@@ -515,7 +515,9 @@ __global__ __launch_bounds__(CFG::THREADS, CFG::MINB) void gemm_cb8_kernel(Gemm8
                     const uint32_t b0 = f32_to_bf16(v.x * sc), b1 = f32_to_bf16(v.y * sc);
                     const uint32_t b2 = f32_to_bf16(v.z * sc), b3 = f32_to_bf16(v.w * sc);
                     if (cvec) {
-                        *reinterpret_cast<uint2*>(dst) = uint2{b0 | (b1 << 16), b2 | (b3 << 16)};
+                        // nontemporal: C is written once and larger than the caches
+                        // at the shapes this kernel serves (configs[3]: 128 MiB)
+                        st8<true>(dst, uint2{b0 | (b1 << 16), b2 | (b3 << 16)});
                     } else {
                         const uint32_t e[4] = {b0, b1, b2, b3};
                         for (int x = 0; x < 4 && c4 + x < a.N; x++) dst[x] = (uint16_t)e[x];
