@@ -673,8 +673,9 @@ extern "C" int bs_linear_relu_compress(const void* x, int64_t M, int64_t K, int6
         return set_error(BS_ERR_INVALID, "%s: null pointer", fn);
     if (ldx < K || ldw < K || ldx % 8 || ldw % 8)
         return set_error(BS_ERR_INVALID, "%s: row strides must be >= K and multiples of 8", fn);
-    // 32-bit buffer offsets: a slab's rows stay below 2^31 bytes from its base
-    if ((int64_t)kUpBM * std::max(ldx, ldw) * 2 >= (1ll << 31))
+    // 32-bit buffer offsets: the rows of an x slab (128) and of a W slab
+    // (192) stay below 2^31 bytes from their base
+    if ((int64_t)std::max(kUpBM, kUpBN) * std::max(ldx, ldw) * 2 >= (1ll << 31))
         return set_error(BS_ERR_INVALID, "%s: row stride too large", fn);
     if ((((uintptr_t)x) & 15) || (((uintptr_t)w) & 15))
         return set_error(BS_ERR_INVALID, "%s: x and W must be 16-byte aligned", fn);

@@ -148,6 +148,12 @@ def test_invalid_arguments_rejected_on_host():
     assert rc == _lib.BS_ERR_INVALID
     rc = L.bs_host_device_pointer(None, None)
     assert rc == _lib.BS_ERR_INVALID and "null" in _err()
+    # fused up-projection: a W row stride whose 192-row slab passes 2^31 bytes
+    # (the 128-row x block alone would not) is refused before any launch
+    ld = 5592408                                   # 128 * ld * 2 < 2^31 <= 192 * ld * 2
+    rc = L.bs_linear_relu_compress(fake, 64, 64, 64, fake, 64, ld, None, None, 64, fake, fake, fake, 4096,
+                                   None, 0, None, None, None, None, -1, fake, 1 << 20, 1, None)
+    assert rc == _lib.BS_ERR_INVALID and "row stride" in _err()
 
 
 def test_python_api_rejects_cpu_tensors_and_bad_dtypes():
