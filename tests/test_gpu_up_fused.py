@@ -73,9 +73,11 @@ def _check_h(h, x, W, b):
 
 
 # (M, N, K): whole and partial 128 x 192 workgroup tiles, partial 64 x 64
-# format tiles, K not a multiple of the 64-deep step, one-tile matrices
+# format tiles, K not a multiple of the 64-deep step, one-tile matrices, and
+# right-edge units of one, two (N = 320, 128) or three format tiles (each
+# unit's rounds split between two waves)
 SHAPES = [(256, 192, 64), (300, 200, 72), (64, 8, 8), (1000, 768, 256), (513, 392, 40), (40, 1000, 128),
-          (2048, 3072, 96)]
+          (2048, 3072, 96), (200, 320, 48), (130, 128, 64)]
 
 
 @pytest.mark.parametrize("shape", SHAPES)
