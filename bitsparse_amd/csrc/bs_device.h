@@ -218,15 +218,23 @@ __device__ __forceinline__ uint32_t mask_bf16x8(const uint4 v)
            (pos_bf16(v.w & 0xffffu) << 6) | (pos_bf16(v.w >> 16) << 7);
 }
 
+// Positive-bit byte of 8 fp8 codes, byte-parallel (13 VALU ops): a code is
+// positive iff its sign bit is clear and its low 7 bits l satisfy
+// 1 <= l <= MAXP (0x7e e4m3fn, 0x7c e5m2: above are NaN / Inf).  Per byte,
+// l + 0x7f has bit 7 set iff l != 0 and l + (0x7f - MAXP) has it set iff
+// l > MAXP; neither sum carries out of its byte.  Two byte dot products with
+// 0x08040201 / 0x80402010 gather the eight bit-7 flags.
 template <int DT>
 __device__ __forceinline__ uint32_t mask_fp8x8(const uint2 v)
 {
-    uint32_t m = 0;
-#pragma unroll
-    for (int i = 0; i < 4; i++) m |= pos8<DT>((v.x >> (8 * i)) & 0xffu) << i;
-#pragma unroll
-    for (int i = 0; i < 4; i++) m |= pos8<DT>((v.y >> (8 * i)) & 0xffu) << (4 + i);
-    return m;
+    constexpr uint32_t MAXP = DT == DT_E4M3FN ? 0x7eu : 0x7cu;
+    auto flags = [](uint32_t w) __attribute__((always_inline)) {
+        const uint32_t l = w & 0x7f7f7f7fu;
+        return (l + 0x7f7f7f7fu) & ~(l + (0x7fu - MAXP) * 0x01010101u) & ~w & 0x80808080u;
+    };
+    const uint32_t d = __builtin_amdgcn_udot4(flags(v.y), 0x80402010u,
+                                              __builtin_amdgcn_udot4(flags(v.x), 0x08040201u, 0u, false), false);
+    return d >> 7;
 }
 
 __device__ __forceinline__ uint32_t get16(const uint4 v, int e)

@@ -1,4 +1,4 @@
-"""CPU check of two packed 16-bit identities in the bf16 kernels (no GPU).
+"""CPU check of the packed bit identities in the codec kernels (no GPU).
 
 * ``mask_bf16x8_pk`` (bitsparse_amd/csrc/compact.h), the bitmask byte of 8
   bf16 values in the streaming compress and the fused up-projection: per
@@ -11,6 +11,11 @@
 * ``relu2x`` (bitsparse_amd/csrc/up_gemm.hip), torch's GPU relu on two bf16
   halves (x <= 0 -> +0, NaN kept): a half is kept iff its saturating int16
   sum with 127 is nonnegative.  Compared with that rule over every pattern.
+* ``mask_fp8x8`` (bitsparse_amd/csrc/bs_device.h), the bitmask byte of 8 fp8
+  codes in the quantizing and fp8 compress: per byte, bit 7 of
+  (l + 0x7f) & ~(l + 0x7f - MAXP) & ~code, l = code & 0x7f; two byte dot
+  products gather the 8 flags.  Compared with the format's x > 0 over every
+  code in every byte position.
 """
 import numpy as np
 import torch
@@ -65,3 +70,32 @@ def test_relu_of_every_pattern():
     x = torch.from_numpy(ALL.astype(np.uint16).view(np.int16)).view(torch.bfloat16).float().numpy()
     want = np.where(np.isnan(x) | (x > 0), ALL, 0)           # x <= 0 -> +0, NaN and positives keep their bits
     assert (got == want).all()
+
+
+def _fp8_flags(w, maxp):
+    lo = w & 0x7F7F7F7F
+    return (lo + 0x7F7F7F7F) & ~(lo + (0x7F - maxp) * 0x01010101) & ~w & 0x80808080 & 0xFFFFFFFF
+
+
+def _dot4(a, wts):
+    return sum(((a >> (8 * k)) & 0xFF) * ((wts >> (8 * k)) & 0xFF) for k in range(4))
+
+
+def test_fp8_mask_byte():
+    """``mask_fp8x8`` (bitsparse_amd/csrc/bs_device.h): the byte-parallel
+    positive flags of 8 fp8 codes against the format's definition (x > 0:
+    codes 0x01..0x7e for e4m3fn, 0x01..0x7c for e5m2), every code in every
+    byte position and random chunks."""
+    b = np.arange(256, dtype=np.int64)
+    rng = np.random.default_rng(1)
+    v = rng.integers(0, 256, (100000, 8))
+    for maxp in (0x7E, 0x7C):
+        want_b = ((b >= 1) & (b <= maxp)).astype(np.int64)
+        for k in range(4):
+            w = (b << (8 * k)) | (0xA5 << (8 * ((k + 1) % 4)))
+            assert ((_fp8_flags(w, maxp) >> (8 * k + 7)) & 1 == want_b).all()
+        x0 = sum(v[:, k] << (8 * k) for k in range(4))
+        x1 = sum(v[:, 4 + k] << (8 * k) for k in range(4))
+        got = (_dot4(_fp8_flags(x1, maxp), 0x80402010) + _dot4(_fp8_flags(x0, maxp), 0x08040201)) >> 7
+        want = sum((((v[:, e] >= 1) & (v[:, e] <= maxp)).astype(np.int64)) << e for e in range(8))
+        assert (got == want).all()
