@@ -47,6 +47,7 @@
 // patience with the time-out flag set (its own word, never the capacity
 // flags), the unit's offset is wrong, and the caller must discard the result.
 #include <algorithm>
+#include <atomic>
 
 #include "bs_device.h"
 #include "bs_host.h"
@@ -641,6 +642,20 @@ static int64_t up_max_nb(int dev)
     return (int64_t)cus * per_cu / 2;
 }
 
+// up_max_nb per device, queried once (the occupancy query costs host time
+// on every launch otherwise); 0 until known
+static int64_t up_max_nb_cached(int dev)
+{
+    static std::atomic<int64_t> known[64];
+    if (dev < 0 || dev >= 64) return up_max_nb(dev);
+    int64_t v = known[dev].load(std::memory_order_relaxed);
+    if (v <= 0) {
+        v = up_max_nb(dev);
+        if (v > 0) known[dev].store(v, std::memory_order_relaxed);
+    }
+    return v;
+}
+
 }  // namespace bs
 
 using namespace bs;
@@ -648,7 +663,7 @@ using namespace bs;
 extern "C" int64_t bs_linear_relu_compress_max_n(int device)
 {
     clear_error();
-    const int64_t nb = up_max_nb(device);
+    const int64_t nb = up_max_nb_cached(device);
     if (nb <= 0) {
         set_error(BS_ERR_HIP, "bs_linear_relu_compress_max_n: occupancy query failed");
         return -1;
@@ -693,7 +708,7 @@ extern "C" int bs_linear_relu_compress(const void* x, int64_t M, int64_t K, int6
     int dev = 0;
     if (stream_device((hipStream_t)stream, &dev) != hipSuccess)
         return set_error(BS_ERR_HIP, "%s: cannot resolve the stream's device", fn);
-    const int64_t max_nb = up_max_nb(dev);
+    const int64_t max_nb = up_max_nb_cached(dev);
     if (max_nb <= 0) return set_error(BS_ERR_HIP, "%s: occupancy query failed", fn);
     if (nb > max_nb)
         return set_error(BS_ERR_INVALID, "%s: N must be at most %lld on this device", fn,

@@ -140,6 +140,9 @@ class _FlagRing:
         self.words = self.host.numpy()
         self.base = ops.host_device_pointer(self.host)
         self.holders: list = [None] * self.SLOTS      # the LookbackCheck of each slot's last launch
+        # one event per slot, recorded behind each launch that takes the slot
+        # (re-recorded only after the previous holder has read its flag)
+        self.events: list = [None] * self.SLOTS
         self.next = 0
 
     def take(self) -> tuple[int, int]:
@@ -172,7 +175,9 @@ class LookbackCheck:
 
     def __init__(self, ring: _FlagRing, slot: int):
         self.ring, self.slot = ring, slot
-        self.event = torch.cuda.Event()
+        if ring.events[slot] is None:
+            ring.events[slot] = torch.cuda.Event()
+        self.event = ring.events[slot]
         self.event.record()
         self.result = None
         ring.holders[slot] = self
