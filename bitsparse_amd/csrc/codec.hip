@@ -111,65 +111,6 @@ __device__ __forceinline__ uint2 quant_chunk(const uint4 v, float scale, float r
     return uint2{p[0] | (p[1] << 16), p[2] | (p[3] << 16)};
 }
 
-// The quantizer through a code table.  For a fixed scale s, f32_to_e4m3(x / s)
-// of a bf16 x depends only on x's 15 magnitude bits m (RNE and the NaN rule
-// are symmetric, so the sign bit is x's), and only a window of 24 exponents
-// around s's gives codes other than 0 and 0x7f.  With Es the biased exponent
-// of s (s < 2^(Es-126)):
-//   * m below (Es - 12) * 128 is x < 2^(Es-139) <= s * 2^-12: the quotient
-//     rounds below 2^-12 and converts to 0;
-//   * m at or above (Es + 12) * 128 is x >= 2^(Es-115) > s * 2^11: the
-//     quotient is above 464 (or Inf / NaN for the Inf and NaN magnitudes)
-//     and converts to 0x7f.
-// A NaN scale makes every code NaN: the scale's own (positive, 0x7f) for a
-// non-NaN x, x's for a NaN x (a quotient with one NaN operand is that NaN).
-// An infinite scale puts the window past the Inf/NaN exponent, whose entries
-// are then computed like the others.
-// Table, one half per sign of x (kQtabEntries each, negative half second):
-// [0] the code of every magnitude below the window, [1 + i] the code of
-// magnitude base + i (i < 3072), [3073] the code of every magnitude above it,
-// each from one correctly rounded division (the quantizer's own rule); a
-// lookup is qtab[clamp(m - base + 1, 0, 3073) + sign * kQtabEntries].
-constexpr int kQwinExps = 24;
-constexpr int kQtabEntries = kQwinExps * 128 + 2;
-constexpr int kQtabBytes = (2 * kQtabEntries + 15) / 16 * 16;     // the table's space (16-byte copies)
-
-// window base (a magnitude) of a scale, minus 1: the lookup's offset
-__device__ __forceinline__ int qtab_offset(float scale)
-{
-    return ((int)((__float_as_uint(scale) >> 23) & 0xffu) - kQwinExps / 2) * 128 - 1;
-}
-
-__device__ __forceinline__ uint32_t qtab_code(const uint8_t* qtab, uint32_t m, uint32_t sign, int qoff)
-{
-    const int i = min(max((int)m - qoff, 0), kQtabEntries - 1);
-    return (uint32_t)qtab[i + (int)sign * kQtabEntries];
-}
-
-// qtab_code of 8 bf16 values, the table indices formed two at a time with
-// packed 16-bit arithmetic: clamp(m - qoff, 0, E - 1) = clamp(m, L, L') - qoff
-// with L = max(qoff, 0), L' = qoff + E - 1 (qoff >= -1537, so L <= L' < 2^16),
-// the subtraction taken mod 2^16 (its result is in [0, E - 1]); + E for x < 0.
-__device__ __forceinline__ uint2 quant_chunk_tab(const uint4 v, const uint8_t* qtab, int qoff)
-{
-    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
-    const u16x2 lo = (u16x2)(unsigned short)(qoff > 0 ? qoff : 0);
-    const u16x2 hi = (u16x2)(unsigned short)(qoff + kQtabEntries - 1);
-    const u16x2 off = (u16x2)(unsigned short)(uint32_t)qoff;
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-    uint32_t p[4];
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const u16x2 h = __builtin_bit_cast(u16x2, w[k]);
-        const u16x2 m = h & (u16x2)(unsigned short)0x7fff;
-        const u16x2 i = __builtin_elementwise_min(__builtin_elementwise_max(m, lo), hi) - off +
-                        (h >> (u16x2)(unsigned short)15) * (u16x2)(unsigned short)kQtabEntries;
-        const uint32_t ii = __builtin_bit_cast(uint32_t, i);
-        p[k] = (uint32_t)qtab[ii & 0xffffu] | ((uint32_t)qtab[ii >> 16] << 8);
-    }
-    return uint2{p[0] | (p[1] << 16), p[2] | (p[3] << 16)};
-}
-
 // entry i of each half stands for magnitude base + i - 1 (the end entries
 // for every magnitude past them); scale from the amax slot
 __global__ __launch_bounds__(256) void qtab_build_kernel(const uint64_t* slot, uint32_t epoch, uint8_t* qtab)

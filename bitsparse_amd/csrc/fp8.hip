@@ -2,8 +2,9 @@
 // together replace lib_sparse/fp8.py:123-129 (to_fp8).
 //
 // scale = max(fp32(amax|x|) / 448, 1e-9); q = e4m3fn_RNE(fp32(x) / scale)
-// with one correctly rounded fp32 division per element (computed as a
-// reciprocal product converted in hardware, exact division near ties).
+// with one correctly rounded fp32 division per value: the quantize pass reads
+// each code from a table of the scale's 24-exponent window (quant_chunk_tab),
+// which every workgroup builds in LDS from exact divisions.
 #include "bs_device.h"
 #include "bs_host.h"
 
@@ -81,13 +82,40 @@ __device__ __forceinline__ float fp8_scale_from_slot(const uint64_t* slot, uint3
     return (sc < 1e-9f) ? 1e-9f : sc;
 }
 
-// NT: nontemporal loads of x and stores of q.
+// The code table of `scale` (qtab_build_kernel's layout) built in LDS by the
+// workgroup: the positive half from div2_to_e4m3 on pairs of magnitudes
+// (exact: f32_to_e4m3 of the correctly rounded quotient), the negative half
+// with the sign bit set; a NaN scale gives the scale's NaN for every non-NaN
+// magnitude and x's own NaN otherwise, as the division does.
+__device__ __forceinline__ void qtab_build_lds(uint8_t* tab, float scale, float rcp, int tid)
+{
+    const int qoff = qtab_offset(scale);
+    const bool nan_s = scale != scale;
+    static_assert(kQtabEntries % 2 == 0, "entries come in pairs");
+    for (int p = tid; p < kQtabEntries / 2; p += kFp8Threads) {
+        const int m0 = min(max(qoff + 2 * p, 0), 0x7fff), m1 = min(max(qoff + 2 * p + 1, 0), 0x7fff);
+        uint32_t pos, neg;
+        if (nan_s) {
+            pos = 0x7f7fu;
+            neg = (m0 > 0x7f80 ? 0xffu : 0x7fu) | ((m1 > 0x7f80 ? 0xffu : 0x7fu) << 8);
+        } else {
+            pos = div2_to_e4m3(bf16_to_f32((uint32_t)m0), bf16_to_f32((uint32_t)m1), scale, rcp);
+            neg = pos | 0x8080u;
+        }
+        *reinterpret_cast<uint16_t*>(tab + 2 * p) = (uint16_t)pos;
+        *reinterpret_cast<uint16_t*>(tab + kQtabEntries + 2 * p) = (uint16_t)neg;
+    }
+}
+
+// NT: nontemporal loads of x and stores of q.  Each thread's first chunk is
+// loaded before the table is built.
 template <bool NT>
 __global__ __launch_bounds__(kFp8Threads) void quantize_e4m3_kernel(const uint16_t* x, int64_t n,
                                                                     uint8_t* q, float* scale_out,
                                                                     const uint64_t* slot,
                                                                     uint32_t epoch)
 {
+    __shared__ __align__(16) uint8_t s_tab[kQtabBytes];
     const float scale = fp8_scale_from_slot(slot, epoch);
     const float rcp = 1.0f / scale;
     const int tid = threadIdx.x;
@@ -95,18 +123,21 @@ __global__ __launch_bounds__(kFp8Threads) void quantize_e4m3_kernel(const uint16
     const bool vec = ((((uintptr_t)x) & 15u) == 0) && ((((uintptr_t)q) & 7u) == 0);
     const int64_t nvec = vec ? n / 8 : 0;
     const int64_t stride = (int64_t)gridDim.x * kFp8Threads;
-    for (int64_t i = (int64_t)blockIdx.x * kFp8Threads + tid; i < nvec; i += stride) {
-        const uint4 v = ld16<NT>(reinterpret_cast<const uint4*>(x) + i);
-        uint32_t w[4] = {v.x, v.y, v.z, v.w};
-        uint32_t o[2] = {0u, 0u};
-#pragma unroll
-        for (int k = 0; k < 4; k++)
-            o[k >> 1] |= div2_to_e4m3(bf16_to_f32(w[k] & 0xffffu), bf16_to_f32(w[k] >> 16), scale, rcp)
-                         << (16 * (k & 1));
-        st8<NT>(reinterpret_cast<uint2*>(q) + i, uint2{o[0], o[1]});
+    int64_t i = (int64_t)blockIdx.x * kFp8Threads + tid;
+    uint4 v = i < nvec ? ld16<NT>(reinterpret_cast<const uint4*>(x) + i) : uint4{0u, 0u, 0u, 0u};
+    qtab_build_lds(s_tab, scale, rcp, tid);
+    __syncthreads();
+    const int qoff = qtab_offset(scale);
+    for (; i < nvec; i += stride) {
+        const int64_t inext = i + stride;
+        const uint4 vn = inext < nvec ? ld16<NT>(reinterpret_cast<const uint4*>(x) + inext) : uint4{0u, 0u, 0u, 0u};
+        st8<NT>(reinterpret_cast<uint2*>(q) + i, quant_chunk_tab(v, s_tab, qoff));
+        v = vn;
     }
-    for (int64_t i = nvec * 8 + (int64_t)blockIdx.x * kFp8Threads + tid; i < n; i += stride)
-        q[i] = (uint8_t)div_to_e4m3(bf16_to_f32(x[i]), scale, rcp);
+    for (int64_t j = nvec * 8 + (int64_t)blockIdx.x * kFp8Threads + tid; j < n; j += stride) {
+        const uint32_t b = x[j];
+        q[j] = (uint8_t)qtab_code(s_tab, b & 0x7fffu, b >> 15, qoff);
+    }
 }
 
 static uint32_t grid_for(int64_t n)
@@ -114,6 +145,16 @@ static uint32_t grid_for(int64_t n)
     int64_t g = (n / 8 + kFp8Threads - 1) / kFp8Threads;
     if (g < 1) g = 1;
     if (g > 4096) g = 4096;
+    return (uint32_t)g;
+}
+
+// the quantize pass: at least 8 chunks per thread where n allows (each
+// workgroup builds the 6 KiB code table first), at most 2048 workgroups
+static uint32_t quantize_grid(int64_t n)
+{
+    int64_t g = (n / 8 + 8 * kFp8Threads - 1) / (8 * kFp8Threads);
+    if (g < 1) g = 1;
+    if (g > 2048) g = 2048;
     return (uint32_t)g;
 }
 
@@ -328,7 +369,7 @@ extern "C" int bs_quantize_e4m3fn(const void* x, int64_t n, void* q_out, float* 
     if (((uintptr_t)x) & 1u) return set_error(BS_ERR_INVALID, "bs_quantize_e4m3fn: input misaligned");
     const uint64_t* slot = reinterpret_cast<const uint64_t*>((const uint8_t*)workspace + kWsAmaxOffset);
     auto kernel = use_nontemporal(2 * n) ? quantize_e4m3_kernel<true> : quantize_e4m3_kernel<false>;
-    hipLaunchKernelGGL(kernel, dim3(grid_for(n)), dim3(kFp8Threads), 0, (hipStream_t)stream,
+    hipLaunchKernelGGL(kernel, dim3(quantize_grid(n)), dim3(kFp8Threads), 0, (hipStream_t)stream,
                        (const uint16_t*)x, n, (uint8_t*)q_out, scale_out, slot, epoch);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(BS_ERR_HIP, "bs_quantize_e4m3fn launch: %s", hipGetErrorString(e));

@@ -136,6 +136,7 @@ class _FlagRing:
     SLOTS = 256
 
     def __init__(self, device: torch.device):
+        self.device = device
         self.host = torch.zeros(self.SLOTS * 16, dtype=torch.int32, pin_memory=True)
         self.words = self.host.numpy()
         self.base = ops.host_device_pointer(self.host)
@@ -163,7 +164,7 @@ def _flag_ring(device: torch.device) -> _FlagRing:
     idx = device.index if device.index is not None else torch.cuda.current_device()
     ring = _FLAG_RINGS.get(idx)
     if ring is None:
-        ring = _FLAG_RINGS[idx] = _FlagRing(device)
+        ring = _FLAG_RINGS[idx] = _FlagRing(torch.device("cuda", idx))
     return ring
 
 
@@ -178,7 +179,8 @@ class LookbackCheck:
         if ring.events[slot] is None:
             ring.events[slot] = torch.cuda.Event()
         self.event = ring.events[slot]
-        self.event.record()
+        # on the stream the kernel went to (the ring's device, whichever is current)
+        self.event.record(torch.cuda.current_stream(ring.device))
         self.result = None
         ring.holders[slot] = self
 
