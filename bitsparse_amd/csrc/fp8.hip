@@ -234,6 +234,25 @@ __device__ __forceinline__ uint32_t e4m3_to_bf16_bits(uint32_t c)
     return s | ((p + 118u) << 7) | ((m << (7u - p)) & 0x7fu);
 }
 
+// bf16 bits of the four e4m3fn codes of w, two per dword: the hardware
+// conversion to fp32 (v_cvt_pk_f32_fp8: every e4m3fn value is a bf16 value,
+// so the fp32's high half is exact), NaN codes (0x7f / 0xff) as 0x7fc0
+__device__ __forceinline__ void widen4_e4m3(uint32_t w, uint32_t& lo, uint32_t& hi)
+{
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    const f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+    const f32x2 b = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+    lo = __builtin_amdgcn_perm(__float_as_uint(a.y), __float_as_uint(a.x), 0x07060302u);
+    hi = __builtin_amdgcn_perm(__float_as_uint(b.y), __float_as_uint(b.x), 0x07060302u);
+    const uint32_t nan = ((w & 0x7f7f7f7fu) + 0x01010101u) & 0x80808080u;   // bit 7 of each NaN byte
+    if (nan) {
+        if (nan & 0x00000080u) lo = (lo & 0xffff0000u) | 0x7fc0u;
+        if (nan & 0x00008000u) lo = (lo & 0x0000ffffu) | 0x7fc00000u;
+        if (nan & 0x00800000u) hi = (hi & 0xffff0000u) | 0x7fc0u;
+        if (nan & 0x80000000u) hi = (hi & 0x0000ffffu) | 0x7fc00000u;
+    }
+}
+
 // out[i] = bf16(in[i]) for e4m3fn codes: 16 codes per lane (one 16-byte load,
 // two 16-byte stores), grid-stride; a tail of n % 16 codes element by element
 __global__ __launch_bounds__(256) void widen_e4m3_kernel(const uint8_t* in, int64_t n, uint16_t* out)
@@ -245,10 +264,7 @@ __global__ __launch_bounds__(256) void widen_e4m3_kernel(const uint8_t* in, int6
         const uint32_t w[4] = {v.x, v.y, v.z, v.w};
         uint32_t o[8];
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            o[2 * k] = e4m3_to_bf16_bits(w[k] & 0xffu) | (e4m3_to_bf16_bits((w[k] >> 8) & 0xffu) << 16);
-            o[2 * k + 1] = e4m3_to_bf16_bits((w[k] >> 16) & 0xffu) | (e4m3_to_bf16_bits(w[k] >> 24) << 16);
-        }
+        for (int k = 0; k < 4; k++) widen4_e4m3(w[k], o[2 * k], o[2 * k + 1]);
         uint4* dst = reinterpret_cast<uint4*>(out + g * 16);
         dst[0] = uint4{o[0], o[1], o[2], o[3]};
         dst[1] = uint4{o[4], o[5], o[6], o[7]};
