@@ -88,14 +88,6 @@ __device__ __forceinline__ void st_chunk(void* p, const T& v)
 // positive tests on raw bits: x > 0 <=> bits in (0, +Inf]
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ uint32_t pos_bf16(uint32_t b) { return (b - 1u) < 0x7f80u; }
-__device__ __forceinline__ uint32_t pos_e4m3(uint32_t b) { return ((b - 1u) & 0xffu) < 0x7eu; }
-__device__ __forceinline__ uint32_t pos_e5m2(uint32_t b) { return ((b - 1u) & 0xffu) < 0x7cu; }
-
-template <int DT>
-__device__ __forceinline__ uint32_t pos8(uint32_t b)
-{
-    return DT == DT_E4M3FN ? pos_e4m3(b) : pos_e5m2(b);
-}
 
 // ---------------------------------------------------------------------------
 // scalar conversions
@@ -152,33 +144,6 @@ __device__ __forceinline__ uint32_t f32_to_e4m3(float f)
     }
     a += 0x7ffffu + ((a >> 20) & 1u);                                // RNE at mantissa bit 20
     return sign | ((((a >> 23) - 120u) << 3) | ((a >> 20) & 7u));
-}
-
-// fp32 -> e4m3fn bits with the hardware conversion (v_cvt_pk_fp8_f32, RNE, no
-// saturation).  It matches f32_to_e4m3 on every fp32 input except positive
-// NaN, which it encodes as 0xff: callers route NaN elsewhere.
-__device__ __forceinline__ uint32_t hw_e4m3(float f)
-{
-    return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(f, f, 0, false) & 0xffu;
-}
-
-// f32_to_e4m3(x / s) with r = 1/s: q = x*r plus one FMA residual step is
-// within 2 ulp of the correctly rounded quotient, so when q - 2 ulp and
-// q + 2 ulp convert to the same byte as q, the correctly rounded quotient
-// does too; a zero x gives a zero of x's sign.  Otherwise (a rounding tie nearby,
-// tiny or overflowing quotients, NaN) the exact division decides.
-__device__ __forceinline__ uint32_t div_to_e4m3(float x, float s, float r)
-{
-    const float y = x * r;
-    const float q = __builtin_fmaf(__builtin_fmaf(-y, s, x), r, y);
-    const uint32_t qb = __float_as_uint(q);
-    const uint32_t out = hw_e4m3(q);
-    const uint32_t nb = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(__uint_as_float(qb - 2u),
-                                                                 __uint_as_float(qb + 2u), 0, false);
-    if (x == 0.0f && s == s) return (__float_as_uint(x) >> 24) & 0x80u;   // +-0 / s = +-0
-    const bool ok = (qb & 0x7fffffffu) - 2u < 0x7f7ffffdu && (nb & 0xffu) == out && ((nb >> 8) & 0xffu) == out;
-    if (ok) return out;
-    return f32_to_e4m3(x / s);
 }
 
 // The plain product y = x * r (r = 1/s rounded, one more rounding in the
