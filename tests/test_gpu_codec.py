@@ -353,6 +353,20 @@ def test_to_fp8(dev, shape):
     assert qt.shape == x.T.shape and (bits(qt.contiguous()) == qo.T).all()
 
 
+def test_to_fp8_misaligned_input(dev):
+    """A contiguous view starting 2 bytes into its storage, of odd length: the
+    amax and the quantizer take their per-element paths (no 16-byte vectors),
+    the quantizer reading each code from its LDS table."""
+    from bitsparse_amd.fp8 import to_fp8
+    x = preact_input((1000, 4097), seed=75) * 5
+    flat = x.to(dev).reshape(-1)[1:]
+    assert flat.data_ptr() % 16 != 0 and flat.numel() % 8 != 0
+    q, s = to_fp8(flat)
+    qo, so = O.to_fp8(bits(x).reshape(-1)[1:])
+    assert float(s.item()) == so
+    assert (bits(q) == qo).all()
+
+
 @pytest.mark.parametrize("shape", [(129, 131), (512, 1024)])
 def test_quantize_and_compress(dev, shape):
     F, _, TB = _bs()
