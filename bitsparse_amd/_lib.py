@@ -17,7 +17,7 @@ LIB_NAME = "libbitsparse_hip.so"
 # BITSPARSE_HIP_LIB points at another build of the same sources (tuning sweeps)
 LIB_PATH = os.environ.get("BITSPARSE_HIP_LIB") or os.path.join(
     os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 14
+ABI_VERSION = 15
 
 BS_OK = 0
 BS_ERR_INVALID = 1
@@ -60,6 +60,9 @@ _SIGNATURES = {
     "bs_transpose_u8": [_vp, _i64, _i64, _i64, _vp, _i64, _vp],
     "bs_widen_e4m3fn": [_vp, _i64, _vp, _vp],
     "bs_relu2_square_amax": [_vp, _i64, ctypes.c_float, _vp, _i64, _u32, _vp],
+    "bs_compress_relu2": [_vp, _int, _i64, _i64, _vp, _u32, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp,
+                          _vp, _i64, _u32, _vp, ctypes.c_float, _vp],
+    "bs_amax_relu2_from": [_vp, _i64, _u32, _u32, ctypes.c_float, _vp],
     "bs_gemm_compressed_b_workspace_bytes": [_i64, _i64, _i64, _int],
     "bs_gemm_compressed_b": [_vp, _i64, _i64, _i64, _int, _vp, _int, _i64, _vp, _vp, _vp, _i64, _int, _f32,
                              _vp, _vp, _vp, _i64, _vp],

@@ -172,6 +172,28 @@ __device__ __forceinline__ uint32_t div2_to_e4m3(float x0, float x1, float s, fl
     return out;
 }
 
+// The ReLU^2 layer's h = k * r^2 as torch forms it in place (h.square_()
+// then h.mul_(k)): bf16(bf16(r * r) * k), a NaN as torch's 0x7fc0.  For
+// r >= 0 (or NaN) and a finite k, |h| is non-decreasing in r (the square is
+// exact in fp32, each rounding is monotonic), so max |h| = |h(max r)|.
+__device__ __forceinline__ uint32_t relu2_sq_bits(uint32_t b, float k)
+{
+    const float r = bf16_to_f32(b);
+    const uint32_t sq = f32_to_bf16(r * r);
+    const uint32_t h = f32_to_bf16(bf16_to_f32(sq) * k);
+    return (h & 0x7fffu) > 0x7f80u ? 0x7fc0u : h;
+}
+
+// relu2_sq_bits of the 8 bf16 values of a chunk
+__device__ __forceinline__ uint4 relu2_sq_chunk(const uint4 v, float k)
+{
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) o[i] = relu2_sq_bits(w[i] & 0xffffu, k) | (relu2_sq_bits(w[i] >> 16, k) << 16);
+    return uint4{o[0], o[1], o[2], o[3]};
+}
+
 // ---------------------------------------------------------------------------
 // 8-element chunks: bitmask byte of 8 values held in registers
 // ---------------------------------------------------------------------------

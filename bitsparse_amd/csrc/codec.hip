@@ -14,6 +14,7 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <cmath>
 #include <functional>
 #include <mutex>
 
@@ -171,6 +172,7 @@ struct CompressArgs {
     uint32_t* fallbacks;
     uint64_t patience;          // look-back wait (s_memrealtime ticks) before counting a unit itself
     const uint8_t* qtab;        // quantize: the code table (kQtabBytes), copied into LDS
+    float relu_k;               // RSQ: relu_out receives bf16(bf16(r * r) * relu_k), r = relu(dense)
 };
 
 // 200 us at the 100 MHz s_memrealtime clock: waiting longer than this for a
@@ -589,13 +591,16 @@ __device__ __forceinline__ void packed_unit_edges(const CompressArgs& a, int64_t
 #endif
 
 // NT: nontemporal loads of the dense input and stores of the value slots.
-template <int IN_T, bool QUANT, bool VEC, int MODE, int U, bool PACKED, bool NT>
+// RSQ: the fused ReLU's write-back is the ReLU^2 layer's in-place square
+// (relu2_sq_bits of relu(dense)); the compressed form is that of relu(dense).
+template <int IN_T, bool QUANT, bool VEC, int MODE, int U, bool PACKED, bool NT, bool RSQ = false>
 __global__ __launch_bounds__(64 * U) __attribute__((amdgpu_waves_per_eu(
     QUANT ? BS_QUANT_WAVES_PER_EU : (PACKED ? BS_PACKED_WAVES_PER_EU : BS_STREAM_WAVES_PER_EU))))
 void compress_stream_kernel(CompressArgs a)
 {
     static_assert(!(QUANT && MODE == MODE_VALS), "the values pass copies stored values");
     static_assert(!PACKED || MODE == MODE_FUSED, "the packed stream is written by the fused pass");
+    static_assert(!RSQ || (IN_T == DT_BF16 && MODE == MODE_FUSED && !PACKED), "the ReLU^2 write-back");
     constexpr bool WRITE_VALS = MODE != MODE_COUNT;
     using TR = CompressTraits<IN_T, QUANT>;
     constexpr int INB = TR::INB, OUTB = TR::OUTB;
@@ -721,15 +726,25 @@ void compress_stream_kernel(CompressArgs a)
                         // in range, the lane's unclamped place in the tile
                         const uint64_t ko = t_org + (uint64_t)(8 * k) * (uint64_t)a.N;
                         const uint32_t lo = r_in + c_in;
-                        if (a.relu_out != nullptr && 8 * k < rows_in)
-                            st_chunk<false, RawIn>(a.relu_out + ko * INB + (uint64_t)(lo * (uint32_t)INB), d[k]);
+                        if (a.relu_out != nullptr && 8 * k < rows_in) {
+                            if constexpr (RSQ)
+                                st_chunk<false, RawIn>(a.relu_out + ko * INB + (uint64_t)(lo * (uint32_t)INB),
+                                                       relu2_sq_chunk(d[k], a.relu_k));
+                            else
+                                st_chunk<false, RawIn>(a.relu_out + ko * INB + (uint64_t)(lo * (uint32_t)INB), d[k]);
+                        }
                         if constexpr (QUANT) {
                             if (a.dense_q_out != nullptr && 8 * k < rows_in)
                                 st_chunk<false, RawOut>(a.dense_q_out + ko + (uint64_t)lo, o[k]);
                         }
                     } else {
-                        if (a.relu_out != nullptr)
-                            store_chunk<INB, VEC>(a.relu_out, a.M, a.N, row0 + 8 * k, col0, d[k]);
+                        if (a.relu_out != nullptr) {
+                            if constexpr (RSQ)
+                                store_chunk<INB, VEC>(a.relu_out, a.M, a.N, row0 + 8 * k, col0,
+                                                      relu2_sq_chunk(d[k], a.relu_k));
+                            else
+                                store_chunk<INB, VEC>(a.relu_out, a.M, a.N, row0 + 8 * k, col0, d[k]);
+                        }
                         if constexpr (QUANT) {
                             if (a.dense_q_out != nullptr)
                                 store_chunk<1, VEC>(a.dense_q_out, a.M, a.N, row0 + 8 * k, col0, o[k]);
@@ -1768,11 +1783,25 @@ constexpr int kStreamU = BS_STREAM_U;
 static bool vec_rows_fit(int64_t N, int eb) { return 8 * N * (int64_t)eb < (int64_t(1) << 32); }
 
 template <int IN_T, bool QUANT, int MODE, bool PACKED>
-static hipError_t launch_compress_mode(const CompressArgs& a, bool vec, bool nt, hipStream_t st)
+static hipError_t launch_compress_mode(const CompressArgs& a, bool vec, bool nt, hipStream_t st, bool rsq = false)
 {
     const uint32_t units = (a.tend - a.tile0 + kStreamU - 1) / kStreamU;
     // the streaming hint is built for the fused pass over a vector-loadable input
     constexpr bool kHasNt = MODE == MODE_FUSED;
+    if constexpr (IN_T == DT_BF16 && MODE == MODE_FUSED && !PACKED) {
+        if (rsq) {
+            if (vec && nt)
+                launch_timed(0, compress_stream_kernel<IN_T, QUANT, true, MODE, kStreamU, PACKED, true, true>,
+                             dim3(units), dim3(64 * kStreamU), 0, st, a);
+            else if (vec)
+                launch_timed(0, compress_stream_kernel<IN_T, QUANT, true, MODE, kStreamU, PACKED, false, true>,
+                             dim3(units), dim3(64 * kStreamU), 0, st, a);
+            else
+                launch_timed(0, compress_stream_kernel<IN_T, QUANT, false, MODE, kStreamU, PACKED, false, true>,
+                             dim3(units), dim3(64 * kStreamU), 0, st, a);
+            return hipGetLastError();
+        }
+    }
     if (vec && nt && kHasNt)
         launch_timed(0, compress_stream_kernel<IN_T, QUANT, true, MODE, kStreamU, PACKED, kHasNt>, dim3(units),
                      dim3(64 * kStreamU), 0, st, a);
@@ -1787,13 +1816,13 @@ static hipError_t launch_compress_mode(const CompressArgs& a, bool vec, bool nt,
 
 template <int MODE, bool PACKED = false>
 static hipError_t launch_compress(const CompressArgs& a, int in_dtype, bool quant, bool vec, bool nt,
-                                  hipStream_t st)
+                                  hipStream_t st, bool rsq = false)
 {
     if constexpr (MODE != MODE_VALS) {
-        if (quant) return launch_compress_mode<DT_BF16, true, MODE, PACKED>(a, vec, nt, st);
+        if (quant) return launch_compress_mode<DT_BF16, true, MODE, PACKED>(a, vec, nt, st, rsq);
     }
     switch (in_dtype) {
-    case DT_BF16: return launch_compress_mode<DT_BF16, false, MODE, PACKED>(a, vec, nt, st);
+    case DT_BF16: return launch_compress_mode<DT_BF16, false, MODE, PACKED>(a, vec, nt, st, rsq);
     case DT_E4M3FN: return launch_compress_mode<DT_E4M3FN, false, MODE, PACKED>(a, vec, nt, st);
     default: return launch_compress_mode<DT_E5M2, false, MODE, PACKED>(a, vec, nt, st);
     }
@@ -1848,8 +1877,16 @@ static int compress_impl(const void* dense, int in_dtype, int64_t M, int64_t N, 
                          int64_t* vals_offset_out, int64_t* vals_start_out, int write_vals,
                          int32_t* err_flags, void* workspace, int64_t workspace_bytes,
                          uint32_t epoch, void* stream, bool relu, void* relu_out, bool packed = false,
-                         bool check_capture = true, const std::function<int()>& before_launch = nullptr)
+                         bool check_capture = true, const std::function<int()>& before_launch = nullptr,
+                         bool relu_sq = false, float relu_k = 1.0f)
 {
+    if (relu_sq) {
+        // the ReLU^2 write-back: bf16 pre-activation, values into a buffer
+        if (!relu || relu_out == nullptr || in_dtype != DT_BF16 || packed || !write_vals)
+            return set_error(BS_ERR_INVALID, "bs_compress_relu2: needs a bf16 pre-activation, relu_out and "
+                                             "write_vals = 1");
+        if (!std::isfinite(relu_k)) return set_error(BS_ERR_INVALID, "bs_compress_relu2: k must be finite");
+    }
     if (packed) {
         // vals is the packed stream and vals_capacity its size in bytes
         if (!write_vals) return set_error(BS_ERR_INVALID, "bs_compress_packed: write_vals must be 1");
@@ -1928,6 +1965,7 @@ static int compress_impl(const void* dense, int in_dtype, int64_t M, int64_t N, 
     a.tend = (uint32_t)T;
     a.relu = relu ? 1 : 0;
     a.relu_out = (uint8_t*)relu_out;
+    a.relu_k = relu_k;
     a.status = reinterpret_cast<uint64_t*>((uint8_t*)workspace + kWsHeaderBytes);
     a.epoch = epoch;
     a.err = err_flags;
@@ -1952,7 +1990,7 @@ static int compress_impl(const void* dense, int in_dtype, int64_t M, int64_t N, 
                (relu_out == nullptr || ((uintptr_t)relu_out) % (8 * inb) == 0);
     const bool nt = use_nontemporal(M * N * inb);
     hipError_t e = packed     ? launch_compress<MODE_FUSED, true>(a, in_dtype, quantize != 0, vec, nt, st)
-                 : write_vals ? launch_compress<MODE_FUSED>(a, in_dtype, quantize != 0, vec, nt, st)
+                 : write_vals ? launch_compress<MODE_FUSED>(a, in_dtype, quantize != 0, vec, nt, st, relu_sq)
                               : launch_compress<MODE_COUNT>(a, in_dtype, quantize != 0, vec, nt, st);
     if (e != hipSuccess) return set_error(BS_ERR_HIP, "bs_compress launch: %s", hipGetErrorString(e));
     return BS_OK;
@@ -1986,6 +2024,20 @@ extern "C" int bs_compress_relu(const void* preact, int in_dtype, int64_t M, int
                          bitmask, prefix, vals, vals_capacity, vals_offset_in, align8, vals_offset_out,
                          vals_start_out, write_vals, err_flags, workspace, workspace_bytes, epoch, stream,
                          true, relu_out);
+}
+
+extern "C" int bs_compress_relu2(const void* preact, int quantize, int64_t M, int64_t N,
+                                 const uint64_t* amax_slot, uint32_t amax_epoch, float* scale_out,
+                                 void* dense_q_out, uint8_t* bitmask, uint32_t* prefix, void* vals,
+                                 int64_t vals_capacity, const int64_t* vals_offset_in, int64_t* vals_offset_out,
+                                 int32_t* err_flags, void* workspace, int64_t workspace_bytes, uint32_t epoch,
+                                 void* relu_out, float k, void* stream)
+{
+    clear_error();
+    return compress_impl(preact, DT_BF16, M, N, quantize, amax_slot, amax_epoch, scale_out, dense_q_out,
+                         bitmask, prefix, vals, vals_capacity, vals_offset_in, 0, vals_offset_out, nullptr, 1,
+                         err_flags, workspace, workspace_bytes, epoch, stream, true, relu_out, false, true, nullptr,
+                         true, k);
 }
 
 extern "C" int bs_compress_packed(const void* dense, int in_dtype, int64_t M, int64_t N, int quantize,

@@ -5,6 +5,8 @@
 // with one correctly rounded fp32 division per value: the quantize pass reads
 // each code from a table of the scale's 24-exponent window (quant_chunk_tab),
 // which every workgroup builds in LDS from exact divisions.
+#include <cmath>
+
 #include "bs_device.h"
 #include "bs_host.h"
 
@@ -276,17 +278,9 @@ __global__ __launch_bounds__(256) void widen_e4m3_kernel(const uint8_t* in, int6
 }
 
 
-// The ReLU^2 forward's h = k * r^2 as torch forms it (h.square_() then
-// h.mul_(k): bf16(bf16(r * r) * k), a NaN as torch's 0x7fc0), written back in
-// place, with amax|h| into the slot: the square and scale passes and the
-// amax pass of to_fp8(h) in one read and one write of r.
-__device__ __forceinline__ uint32_t relu2_sq_bits(uint32_t b, float k)
-{
-    const float r = bf16_to_f32(b);
-    const uint32_t sq = f32_to_bf16(r * r);
-    const uint32_t h = f32_to_bf16(bf16_to_f32(sq) * k);
-    return (h & 0x7fffu) > 0x7f80u ? 0x7fc0u : h;
-}
+// The ReLU^2 forward's h = k * r^2 (relu2_sq_bits) written back in place,
+// with amax|h| into the slot: the square and scale passes and the amax pass
+// of to_fp8(h) in one read and one write of r.
 
 template <bool NT>
 __global__ __launch_bounds__(kFp8Threads) void relu2_square_amax_kernel(uint16_t* x, int64_t n, float k,
@@ -324,9 +318,39 @@ __global__ __launch_bounds__(kFp8Threads) void relu2_square_amax_kernel(uint16_t
     }
 }
 
+// amax|k r^2| (relu2_sq_bits) from the amax of r = relu(z) in the slot, for
+// a finite k: the map is non-decreasing on r >= 0 and NaN, so the amax of the
+// squared tensor is that of its largest element; written under epoch_out
+// (slot = amax 0 when the slot does not hold epoch_in).
+__global__ void amax_relu2_from_kernel(uint64_t* slot, uint32_t epoch_in, uint32_t epoch_out, float k)
+{
+    if (threadIdx.x != 0) return;
+    const uint64_t s = *slot;
+    const uint32_t m = (uint32_t)(s >> 32) == epoch_in ? (uint32_t)s & 0x7fffu : 0u;
+    *slot = ((uint64_t)epoch_out << 32) | (relu2_sq_bits(m, k) & 0x7fffu);
+}
+
 }  // namespace bs
 
 using namespace bs;
+
+extern "C" int bs_amax_relu2_from(void* workspace, int64_t workspace_bytes, uint32_t epoch_in, uint32_t epoch_out,
+                                  float k, void* stream)
+{
+    clear_error();
+    if (workspace == nullptr || workspace_bytes < kWsHeaderBytes)
+        return set_error(BS_ERR_INVALID, "bs_amax_relu2_from: workspace too small");
+    if (epoch_in == 0 || epoch_in >= (1u << 30) || epoch_out == 0 || epoch_out >= (1u << 30))
+        return set_error(BS_ERR_INVALID, "bs_amax_relu2_from: epoch out of range");
+    if (!std::isfinite(k)) return set_error(BS_ERR_INVALID, "bs_amax_relu2_from: k must be finite");
+    if (int rc = refuse_capture((hipStream_t)stream, "bs_amax_relu2_from")) return rc;
+    uint64_t* slot = reinterpret_cast<uint64_t*>((uint8_t*)workspace + kWsAmaxOffset);
+    hipLaunchKernelGGL(amax_relu2_from_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, slot, epoch_in, epoch_out,
+                       k);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(BS_ERR_HIP, "bs_amax_relu2_from launch: %s", hipGetErrorString(e));
+    return BS_OK;
+}
 
 int bs::amax_launch(const void* x, int64_t n, void* workspace, int64_t workspace_bytes, uint32_t epoch,
                     void* stream, bool relu, bool check_capture)

@@ -105,7 +105,7 @@ using namespace bs;
 
 extern "C" const char* bs_last_error(void) { return bs::g_err; }
 
-extern "C" int bs_abi_version(void) { return 14; }
+extern "C" int bs_abi_version(void) { return 15; }
 
 extern "C" int bs_host_device_pointer(void* host_ptr, void** device_ptr)
 {

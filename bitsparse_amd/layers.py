@@ -17,7 +17,8 @@ from torch.autograd import Function
 from .bitsparse import BitsparseTensor, TensorBuffer
 from .config import RELU2_SCALE
 from .fp8 import is_fp8, matmul, to_fp8
-from .src.functions import (fused_linear_relu_ok, linear_relu_and_compress, relu_and_compress,
+from .src.functions import (fused_linear_relu_ok, linear_relu_and_compress, relu2_and_compress,
+                            relu2_fused_ok, relu2_quantize_and_compress, relu_and_compress,
                             relu_quantize_and_compress)
 from .src.hip_operators import mask_with_bitmask_, quantize_e4m3fn, relu2_grad_sparse_, relu2_square_amax_
 from .src.sparse_matmul import AspB, AspRelu2B
@@ -114,23 +115,30 @@ class Relu2Linear(Function):
         ctx.dtype = storage_dtype
         ctx.save_for_backward(W)
         # h = z.relu_() fused into the compress pass (z is still updated in place)
+        fused_sq = relu2_fused_ok(z, sparse_data, pack_sbit, RELU2_SCALE)
         if is_fp8(storage_dtype):
             # e4m3fn codes for every fp8 storage dtype, as to_fp8 makes them;
             # the forward multiplies the bf16 square, so no dense e4m3fn copy
-            _, scale, h_sparse = relu_quantize_and_compress(z, sparse_data, pack_sbit, dense_out=False)
+            if fused_sq:
+                # the compress also writes h = k r^2 into z; amax|h| follows
+                # from the amax of r
+                _, h_sparse, epoch = relu2_quantize_and_compress(z, sparse_data, RELU2_SCALE)
+            else:
+                _, _, h_sparse = relu_quantize_and_compress(z, sparse_data, pack_sbit, dense_out=False)
+                # h.square_(); h.mul_(k) and the amax of to_fp8(h) in one pass
+                epoch = relu2_square_amax_(z, RELU2_SCALE)
+            ctx.h_sparse = h_sparse
+            # h ends up in z, as the reference's in-place ops leave it
+            h8, h_scale = quantize_e4m3fn(z, epoch)
+            return matmul(h8, W.T, True, a_scale=h_scale)
+        if fused_sq:
+            h_sparse = relu2_and_compress(z, sparse_data, RELU2_SCALE)
             h = z
         else:
             h, h_sparse = relu_and_compress(z, sparse_data, pack_sbit)
+            h.square_()
+            h.mul_(RELU2_SCALE)
         ctx.h_sparse = h_sparse
-
-        if is_fp8(storage_dtype):
-            # h.square_(); h.mul_(k) and the amax of to_fp8(h) in one pass
-            # (h still ends up in z, as the in-place ops leave it)
-            epoch = relu2_square_amax_(h, RELU2_SCALE)
-            h8, h_scale = quantize_e4m3fn(h, epoch)
-            return matmul(h8, W.T, True, a_scale=h_scale)
-        h.square_()
-        h.mul_(RELU2_SCALE)
         return matmul(h, W.T, False)
 
     @staticmethod

@@ -19,6 +19,7 @@ first and pack them with ``bitpacking.pack_bits``.
 """
 from __future__ import annotations
 
+import math
 from typing import NamedTuple
 
 import torch
@@ -281,6 +282,70 @@ def _compress_packed_staged(dense: Tensor, scale: Tensor | None, buf: TensorBuff
     return BitsparseTensor(buf.vals, bitmask, prefix, dense.shape, stored,
                            grid_m, grid_n, BLOCK_M, BLOCK_N, scale=scale,
                            vals_offset=vals_offset, pack_sbit=True)
+
+
+def relu2_fused_ok(z: Tensor, sparse_data: TensorBuffer | None, pack_sbit: bool, k: float) -> bool:
+    """The ReLU^2 layer's square can ride on the compress pass
+    (``relu2_and_compress`` / ``relu2_quantize_and_compress``): a contiguous
+    bf16 GPU z, a raw (not pack_sbit) TensorBuffer and a finite k."""
+    return (sparse_data is not None and not pack_sbit and not sparse_data.pack_sbit and z.is_cuda
+            and z.dtype == torch.bfloat16 and z.dim() == 2 and z.is_contiguous() and math.isfinite(k))
+
+
+def relu2_and_compress(z: Tensor, sparse_data: TensorBuffer, k: float) -> BitsparseTensor:
+    """``h = z.relu_(); sp = dense_to_tilesparse(h, None, sparse_data);
+    h.square_(); h.mul_(k)`` (reference layers.py:107-119, bf16 storage) in
+    one pass: the compress of relu(z) writes bf16(bf16(r * r) * k) back into z
+    (bs_compress_relu2).  Needs ``relu2_fused_ok``; returns the compressed r."""
+    if not relu2_fused_ok(z, sparse_data, False, k):
+        raise ValueError("relu2_and_compress: operands do not qualify (relu2_fused_ok)")
+    _check_input(z)
+    _check_buffer(sparse_data, z.dtype, False)
+    if sparse_data.vals.dtype != z.dtype:
+        raise TypeError(f"TensorBuffer stores {sparse_data.vals.dtype} but the input is {z.dtype}")
+    M, N = z.shape
+    grid_m, grid_n, num_tiles, TILE_NUMEL, TILE_BYTES = tile_grid(M, N, BLOCK_M, BLOCK_N)
+    bitmask = torch.empty(num_tiles * TILE_BYTES, device=z.device, dtype=torch.uint8)
+    prefix = torch.empty(num_tiles + 1, device=z.device, dtype=torch.uint32)
+    vals_offset, new_offset = sparse_data.cursor()
+    ops.compress_into(z, bitmask, prefix, sparse_data.vals, vals_offset, new_offset, sparse_data.err_flags,
+                      write_vals=True, relu=True, relu_out=z, relu_square_k=k)
+    sparse_data.advance(new_offset)
+    return BitsparseTensor(sparse_data.vals, bitmask, prefix, z.shape, z.dtype, grid_m, grid_n, BLOCK_M, BLOCK_N,
+                           scale=None, vals_offset=vals_offset)
+
+
+def relu2_quantize_and_compress(z: Tensor, sparse_data: TensorBuffer,
+                                k: float) -> tuple[Tensor, BitsparseTensor, int]:
+    """The fp8 ReLU^2 forward's ``h = z.relu_(); (h8, s) = to_fp8(h);
+    sp = dense_to_tilesparse(h8, s, sparse_data); h.square_(); h.mul_(k)``
+    and the amax of ``to_fp8(h)`` (reference layers.py:107-119 with
+    fp8.py:123-129): one amax pass over relu(z), one compress pass that also
+    writes bf16(bf16(r * r) * k) back into z, and the amax of that square
+    taken from the amax of r (the map is non-decreasing for a finite k, so its
+    maximum is the image of r's: bs_amax_relu2_from).  Needs
+    ``relu2_fused_ok``; returns (scale of the stored codes, compressed r, the
+    workspace epoch of amax|h| for ``quantize_e4m3fn(z, epoch)``)."""
+    if not relu2_fused_ok(z, sparse_data, False, k):
+        raise ValueError("relu2_quantize_and_compress: operands do not qualify (relu2_fused_ok)")
+    _check_buffer(sparse_data, torch.float8_e4m3fn, False)
+    if sparse_data.vals.dtype != torch.float8_e4m3fn:
+        raise TypeError(f"TensorBuffer stores {sparse_data.vals.dtype}, need float8_e4m3fn")
+    ops.require_device(z, "relu2_quantize_and_compress")
+    M, N = z.shape
+    grid_m, grid_n, num_tiles, TILE_NUMEL, TILE_BYTES = tile_grid(M, N, BLOCK_M, BLOCK_N)
+    amax_epoch = ops.amax_into_workspace(z, relu=True, reserve=3)   # + the compress and the derived amax
+    scale = torch.empty((), device=z.device, dtype=torch.float32)
+    bitmask = torch.empty(num_tiles * TILE_BYTES, device=z.device, dtype=torch.uint8)
+    prefix = torch.empty(num_tiles + 1, device=z.device, dtype=torch.uint32)
+    vals_offset, new_offset = sparse_data.cursor()
+    ops.compress_into(z, bitmask, prefix, sparse_data.vals, vals_offset, new_offset, sparse_data.err_flags,
+                      write_vals=True, quantize=True, scale_out=scale, amax_epoch=amax_epoch,
+                      relu=True, relu_out=z, relu_square_k=k)
+    sparse_data.advance(new_offset)
+    sp = BitsparseTensor(sparse_data.vals, bitmask, prefix, z.shape, torch.float8_e4m3fn, grid_m, grid_n,
+                         BLOCK_M, BLOCK_N, scale=scale, vals_offset=vals_offset)
+    return scale, sp, ops.amax_relu2_from(z.device, amax_epoch, k)
 
 
 def relu_quantize_and_compress(

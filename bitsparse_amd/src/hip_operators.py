@@ -125,13 +125,16 @@ def compress_into(dense: Tensor, bitmask: Tensor, prefix: Tensor, vals: Tensor |
                   err_flags: Tensor | None, write_vals: bool = True,
                   quantize: bool = False, scale_out: Tensor | None = None,
                   dense_q_out: Tensor | None = None, amax_epoch: int = 0,
-                  relu: bool = False, relu_out: Tensor | None = None) -> None:
+                  relu: bool = False, relu_out: Tensor | None = None,
+                  relu_square_k: float | None = None) -> None:
     """Single-pass compress (bitmask + prefix + values in one read of dense).
 
     ``quantize``: dense is bf16 and is quantized to e4m3fn with the scale of
     the amax computed by ``amax_into_workspace`` under ``amax_epoch``.
     ``relu``: dense is a pre-activation z and relu(z) is compressed (fused
-    ReLU); ``relu_out`` (may be ``dense`` itself) receives relu(z)."""
+    ReLU); ``relu_out`` (may be ``dense`` itself) receives relu(z), or with
+    ``relu_square_k`` = k (bs_compress_relu2: bf16 z, values into a buffer,
+    relu_out required) the ReLU^2 layer's bf16(bf16(r * r) * k), r = relu(z)."""
     require_device(dense, "compress")
     _contig(dense, "dense")
     M, N = dense.shape
@@ -150,6 +153,16 @@ def compress_into(dense: Tensor, bitmask: Tensor, prefix: Tensor, vals: Tensor |
         if relu_out is not None and (relu_out.shape != dense.shape or relu_out.dtype != dense.dtype
                                      or not relu_out.is_contiguous()):
             raise ValueError("compress: relu_out must be a contiguous tensor like dense")
+        if relu_square_k is not None:
+            if relu_out is None or not write_vals:
+                raise ValueError("compress: the ReLU^2 write-back needs relu_out and a value buffer")
+            check(L.bs_compress_relu2(dense.data_ptr(), int(quantize), M, N,
+                                      ws.amax_slot_ptr() if quantize else None, amax_epoch, ptr(scale_out),
+                                      ptr(dense_q_out), bitmask.data_ptr(), prefix.data_ptr(), ptr(vals), cap,
+                                      ptr(vals_offset_in), ptr(vals_offset_out), ptr(err_flags),
+                                      ws.buf.data_ptr(), ws.nbytes, epoch, ptr(relu_out), float(relu_square_k),
+                                      stream_handle(dense.device)), "bs_compress_relu2")
+            return
         check(L.bs_compress_relu(*args, ptr(relu_out), stream_handle(dense.device)), "bs_compress_relu")
     else:
         check(L.bs_compress(*args, stream_handle(dense.device)), "bs_compress")
@@ -270,9 +283,10 @@ def compress_packed_into(dense: Tensor, bitmask: Tensor, prefix: Tensor, stream:
                                stream_handle(dense.device)), "bs_compress_packed")
 
 
-def amax_into_workspace(x: Tensor, relu: bool = False) -> int:
+def amax_into_workspace(x: Tensor, relu: bool = False, reserve: int = 2) -> int:
     """amax(|x|) (``relu``: amax of relu(x)) of a bf16 tensor into the
-    stream's workspace; returns the epoch that tags it."""
+    stream's workspace; returns the epoch that tags it.  ``reserve``: the
+    epochs the caller's sequence takes from here (this one included)."""
     require_device(x, "amax")
     _contig(x, "x")
     if x.dtype != torch.bfloat16:
@@ -280,10 +294,22 @@ def amax_into_workspace(x: Tensor, relu: bool = False) -> int:
     L = _lib.load()
     ws = _lib.workspace_for(x.device)
     ws.ensure(256)
-    epoch = ws.next_epoch(reserve=2)     # the compress that reads this amax takes the next one
+    epoch = ws.next_epoch(reserve=reserve)   # the compress that reads this amax takes the next one
     fn = L.bs_amax_relu if relu else L.bs_amax
     check(fn(x.data_ptr(), x.numel(), ws.buf.data_ptr(), ws.nbytes, epoch,
              stream_handle(x.device)), "bs_amax")
+    return epoch
+
+
+def amax_relu2_from(device: torch.device, epoch_in: int, k: float) -> int:
+    """amax|bf16(bf16(r * r) * k)| from the amax|r| of ``epoch_in`` (r = relu(z),
+    bs_amax_relu2_from) into the stream's workspace; returns the epoch that
+    tags it.  k must be finite."""
+    L = _lib.load()
+    ws = _lib.workspace_for(device)
+    epoch = ws.next_epoch()
+    check(L.bs_amax_relu2_from(ws.buf.data_ptr(), ws.nbytes, epoch_in, epoch, float(k), stream_handle(device)),
+          "bs_amax_relu2_from")
     return epoch
 
 

@@ -323,6 +323,39 @@ int bs_relu2_square_amax(void* r, int64_t n, float k, void* workspace, int64_t w
                          uint32_t epoch, void* stream);
 
 /*
+ * The ReLU^2 layer's compress with its in-place square fused into the ReLU
+ * write-back: `preact` (bf16 z) is compressed as bs_compress_relu compresses
+ * it (the bitmask, prefix and values of r = relu(z): bf16 values, or e4m3fn
+ * codes with quantize = 1 and the amax of r in amax_slot under amax_epoch),
+ * and `relu_out` (required, may alias preact) receives bf16(bf16(r*r) * k)
+ * (NaN -> 0x7fc0), what h = z.relu_(); h.square_(); h.mul_(k) leaves in z.
+ * k must be finite; values go into a buffer (vals, vals_capacity, the
+ * cursor as for bs_compress with align8 = 0).  Replaces lib_sparse/
+ * layers.py:107-119 (the relu, the compress and the two in-place passes) for
+ * raw storage.  Refuses graph capture.
+ */
+int bs_compress_relu2(const void* preact, int quantize, int64_t M, int64_t N, const uint64_t* amax_slot,
+                      uint32_t amax_epoch, float* scale_out, void* dense_q_out, uint8_t* bitmask,
+                      uint32_t* prefix, void* vals, int64_t vals_capacity, const int64_t* vals_offset_in,
+                      int64_t* vals_offset_out, int32_t* err_flags, void* workspace, int64_t workspace_bytes,
+                      uint32_t epoch, void* relu_out, float k, void* stream);
+
+/*
+ * amax|bf16(bf16(r*r) * k)| of a tensor r = relu(z) from its amax|r| (the
+ * workspace's amax slot under epoch_in, as bs_amax_relu leaves it), written
+ * into the slot under epoch_out: for a finite k that map is non-decreasing
+ * in r (the square of a bf16 is exact in fp32 and each rounding is
+ * monotonic; NaN stays NaN), so the amax of the squared tensor is the image
+ * of the amax.  With bs_compress_relu2 it replaces the separate square-and-
+ * amax pass (bs_relu2_square_amax) of the fp8 ReLU^2 forward; then
+ * bs_quantize_e4m3fn(relu_out, epoch_out) gives to_fp8(h).  One thread,
+ * stream-ordered after the compress that reads the slot.  Refuses graph
+ * capture.
+ */
+int bs_amax_relu2_from(void* workspace, int64_t workspace_bytes, uint32_t epoch_in, uint32_t epoch_out,
+                       float k, void* stream);
+
+/*
  * out[c * ld_out + r] = in[r * ld_in + c] for an [R, C] byte matrix: the
  * fp8 operand layout change in front of the fp8 GEMM.  Replaces the
  * a.contiguous() / b.T.contiguous().T / a_fp8.T.contiguous() copies of

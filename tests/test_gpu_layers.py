@@ -155,3 +155,81 @@ def test_ffn_relu2_fp8_forward_bit_identical_to_dense(dev):
     want.mul_(RELU2_SCALE)
     Relu2Linear.apply(z, W2s, None, False, torch.float8_e4m3fn)
     assert torch.equal(z.view(torch.int16), want.view(torch.int16))
+
+
+def _relu2_special_inputs(dev, B=304, D=192, H=528, seed=9):
+    """MLP operands for the ReLU^2 layer (B and H not multiples of 64, but
+    multiples of 16 as the fp8 library GEMMs need); the test writes -0,
+    +-Inf, +-NaN and values whose square overflows bf16 into z."""
+    x, W1, W2, dY = _mlp_inputs(B, D, H, seed=seed, shift=0.01)
+    return [t.to(dev) for t in (x, W1, W2, dY)]
+
+
+@pytest.mark.parametrize("storage", ["bf16", "e4m3fn"])
+def test_relu2_square_fused_into_compress(dev, monkeypatch, storage):
+    """Relu2Linear with the square written back by the compress pass (and,
+    for fp8 storage, amax|k r^2| derived from amax|r|) against the same layer
+    with the separate in-place square / square-and-amax pass: the output, z
+    after the forward (k r^2, as the reference's in-place ops leave it), the
+    compressed r and every gradient are bit-identical, on ordinary and on
+    special pre-activations (-0, +-Inf, +-NaN, squares past bf16's range)."""
+    from bitsparse_amd import layers
+    from bitsparse_amd.bitsparse import TensorBuffer
+    from bitsparse_amd.src import functions as F
+    dt = torch.bfloat16 if storage == "bf16" else torch.float8_e4m3fn
+    x, W1, W2, dY = _relu2_special_inputs(dev)
+    z0 = (x @ W1.T).contiguous()
+    zb = z0.view(torch.int16).view(-1)
+    zb[[0, 7, 64, 200, 333, 4099, 7000, 9001]] = torch.tensor(
+        [-32768, 0x7f80, -128, 0x7fc0, -64, 0x7f7f, 0x5f00, -0x1f00], dtype=torch.int16, device=dev)
+    for special in (False, True):
+        z_in = z0 if special else (x @ W1.T).contiguous()
+        if special and storage == "e4m3fn":
+            z_in = z_in.clone()
+            z_in.view(-1)[[200, 4099]] = 1.0        # no NaN / Inf: a finite scale for the codes
+        outs = []
+        for fused in (True, False):
+            if not fused:
+                monkeypatch.setattr(F, "relu2_fused_ok", lambda *a: False)
+                monkeypatch.setattr(layers, "relu2_fused_ok", lambda *a: False)
+            buf = TensorBuffer(z_in.numel() * (2 if storage == "bf16" else 1), device=dev, dtype=dt)
+            z = z_in.clone().requires_grad_()
+            Wq = W2.clone().requires_grad_()
+            y = layers.Relu2Linear.apply(z, Wq, buf, False, dt)
+            zf = z.detach().clone()
+            y.backward(dY)
+            nbytes = int(buf.offset.item()) * buf.vals.element_size()
+            outs.append((y.detach(), zf, z.grad, Wq.grad, buf.vals.view(torch.uint8)[:nbytes].clone()))
+            monkeypatch.undo()
+        for a, b, name in zip(outs[0], outs[1], ("y", "z after forward", "dz", "dW2", "stored values")):
+            assert a.shape == b.shape, name
+            assert torch.equal(a.view(torch.uint8), b.view(torch.uint8)), (name, special)
+
+
+@pytest.mark.parametrize("k", [1.0, 0.5, 3.0, -2.0, 0.0])
+def test_relu2_amax_derived_from_relu_amax(dev, k):
+    """amax|bf16(bf16(r*r) * k)| from amax|relu(z)| (bs_amax_relu2_from)
+    equals the amax the square-and-amax pass takes of the squared tensor,
+    through the quantizer's output, for ordinary, huge and NaN inputs."""
+    from bitsparse_amd.src import hip_operators as H
+    g = torch.Generator().manual_seed(int(abs(k) * 10) + 3)
+    for kind in ("normal", "huge", "nan", "all_negative"):
+        z = torch.randn((257, 333), generator=g).to(torch.bfloat16)
+        if kind == "huge":
+            z[5, 7] = 3.0e19
+        elif kind == "nan":
+            z[100, 3] = float("nan")
+        elif kind == "all_negative":
+            z = -z.abs() - 1
+        z = z.to(dev)
+        r = z.relu()
+        e1 = H.amax_into_workspace(z, relu=True, reserve=2)
+        e2 = H.amax_relu2_from(z.device, e1, k)
+        q_derived, s_derived = H.quantize_e4m3fn(r.clone(), e2)    # a quantizer over any tensor with that amax
+        h = r.clone()
+        e3 = H.relu2_square_amax_(h, k)
+        q_pass, s_pass = H.quantize_e4m3fn(r.clone(), e3)
+        sd, sp = float(s_derived.item()), float(s_pass.item())
+        assert (sd == sp) or (sd != sd and sp != sp), (kind, sd, sp)
+        if sd == sd:
+            assert torch.equal(q_derived.view(torch.uint8), q_pass.view(torch.uint8)), kind
