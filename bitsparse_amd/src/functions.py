@@ -284,11 +284,20 @@ def _compress_packed_staged(dense: Tensor, scale: Tensor | None, buf: TensorBuff
                            vals_offset=vals_offset, pack_sbit=True)
 
 
+# The ReLU^2 layer's square on the compress pass (bs_compress_relu2 +
+# bs_amax_relu2_from) is switched off: a GPU memory fault ended a full GPU
+# test run after it was added, and no out-of-bounds access has been found in
+# it yet; the layer keeps its separate square / square-and-amax pass.
+USE_FUSED_RELU2_SQUARE = False
+
+
 def relu2_fused_ok(z: Tensor, sparse_data: TensorBuffer | None, pack_sbit: bool, k: float) -> bool:
     """The ReLU^2 layer's square can ride on the compress pass
-    (``relu2_and_compress`` / ``relu2_quantize_and_compress``): a contiguous
-    bf16 GPU z, a raw (not pack_sbit) TensorBuffer and a finite k."""
-    return (sparse_data is not None and not pack_sbit and not sparse_data.pack_sbit and z.is_cuda
+    (``relu2_and_compress`` / ``relu2_quantize_and_compress``): the path is
+    switched on (USE_FUSED_RELU2_SQUARE), a contiguous bf16 GPU z, a raw (not
+    pack_sbit) TensorBuffer and a finite k."""
+    return (USE_FUSED_RELU2_SQUARE and sparse_data is not None and not pack_sbit and not sparse_data.pack_sbit
+            and z.is_cuda
             and z.dtype == torch.bfloat16 and z.dim() == 2 and z.is_contiguous() and math.isfinite(k))
 
 
