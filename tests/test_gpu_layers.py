@@ -56,9 +56,12 @@ def test_ffn_relu2_matches_dense(dev):
     from bitsparse_amd.layers import FFNRelu2
     x, W1, W2, dY = _mlp_inputs(512, 256, 768, seed=2)
     xs, W1s, W2s = (t.to(dev).requires_grad_() for t in (x, W1, W2))
-    FFNRelu2.apply(xs, W1s, W2s).backward(dY.to(dev))
+    ys = FFNRelu2.apply(xs, W1s, W2s)
+    ys.backward(dY.to(dev))
     xd, W1d, W2d = (t.to(dev).requires_grad_() for t in (x, W1, W2))
-    DenseFFNRelu2.apply(xd, W1d, W2d).backward(dY.to(dev))
+    yd = DenseFFNRelu2.apply(xd, W1d, W2d)
+    yd.backward(dY.to(dev))
+    assert torch.equal(ys, yd)                        # the one-pass square and scale == square(); mul_(k)
     assert torch.equal(xs.grad, xd.grad)              # relu2 grad == grad_z * (2 k r)
     assert torch.equal(W1s.grad, W1d.grad)
     xf, W1f, W2f = (t.float().requires_grad_() for t in (x, W1, W2))
